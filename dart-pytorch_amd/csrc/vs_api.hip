@@ -1,0 +1,1131 @@
+// vs_api.hip -- the extern "C" ABI of libvs_hip.so (declared in
+// include/vs_hip.h): index lifecycle, planning, host<->device staging,
+// error reporting.  All device work of a handle runs on its own stream.
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <numeric>
+#include <string>
+#include <vector>
+
+#include "../../include/vs_hip.h"
+#include "vs_internal.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int set_err(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_err(hipError_t e, const char *what) {
+    if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation)
+        return set_err(VS_ERR_OOM, "%s: out of device memory (%s)", what, hipGetErrorString(e));
+    return set_err(VS_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define VS_HIP(call, what)                            \
+    do {                                              \
+        hipError_t e_ = (call);                       \
+        if (e_ != hipSuccess) return hip_err(e_, what); \
+    } while (0)
+
+// Restores the caller's current device on scope exit.
+struct DeviceGuard {
+    int prev = -1;
+    hipError_t err = hipSuccess;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        err = hipSetDevice(dev);
+    }
+    ~DeviceGuard() {
+        if (prev >= 0) (void)hipSetDevice(prev);
+    }
+};
+
+// Device buffer that only grows.
+struct DevBuf {
+    void *p = nullptr;
+    size_t bytes = 0;
+    hipError_t ensure(size_t need) {
+        if (need <= bytes) return hipSuccess;
+        if (p) {
+            hipError_t e = hipFree(p);
+            if (e != hipSuccess) return e;
+            p = nullptr;
+            bytes = 0;
+        }
+        size_t nb = std::max(need, (size_t)4096);
+        hipError_t e = hipMalloc(&p, nb);
+        if (e != hipSuccess) {
+            p = nullptr;
+            return e;
+        }
+        bytes = nb;
+        return hipSuccess;
+    }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        bytes = 0;
+    }
+    template <typename T>
+    T *as() const {
+        return (T *)p;
+    }
+};
+
+struct ProfEntry {
+    int64_t launches = 0;
+    double total_ms = 0.0;
+};
+
+struct PendingEvent {
+    std::string family;
+    hipEvent_t a, b;
+};
+
+int64_t next_pow2(int64_t v) {
+    int64_t p = 1;
+    while (p < v) p <<= 1;
+    return p;
+}
+
+int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+
+}  // namespace
+
+struct vs_index {
+    int device = 0;
+    int64_t d = 0;
+    int metric = 0;
+    int mode = VS_STORAGE_F32;  // requested
+    int storage = 0;            // current: 0 fp32, 1 bf16
+    int64_t ld = 0;
+    int64_t ntotal = 0, cap = 0;
+    void *xb = nullptr;
+    float *xn = nullptr;
+    hipStream_t st = nullptr;
+    int num_cu = 256;
+    size_t lds_max = 64 * 1024;
+    // scratch (grown on demand, reused across calls)
+    DevBuf stage, qp, qf, qnorm, flags, cand_v, cand_i, outD, outI, athr, rq, ri, rs, rkeep, rcount,
+        misc;
+    DevBuf km_cen, km_cxn, km_assign, km_best, km_fb, km_keys, km_order, km_tmp, km_counts,
+        km_offsets, km_out, km_iota;
+    bool prof_on = false;
+    std::map<std::string, ProfEntry> prof;
+    std::vector<PendingEvent> pending;
+};
+
+namespace {
+
+int64_t elem_size(int storage) { return storage == 1 ? 2 : 4; }
+
+int64_t row_bytes(const vs_index *x) { return x->ld * elem_size(x->storage); }
+
+// Brackets a launch with events on the handle's stream when profiling is on.
+struct ProfScope {
+    vs_index *x;
+    const char *fam;
+    hipEvent_t a = nullptr, b = nullptr;
+    ProfScope(vs_index *x_, const char *fam_) : x(x_), fam(fam_) {
+        if (!x->prof_on) return;
+        if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) {
+            a = b = nullptr;
+            return;
+        }
+        (void)hipEventRecord(a, x->st);
+    }
+    ~ProfScope() {
+        if (!a) return;
+        (void)hipEventRecord(b, x->st);
+        x->pending.push_back({fam, a, b});
+    }
+};
+
+void prof_collect(vs_index *x) {
+    if (x->pending.empty()) return;
+    (void)hipStreamSynchronize(x->st);
+    for (auto &p : x->pending) {
+        float ms = 0.f;
+        if (hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
+            auto &e = x->prof[p.family];
+            e.launches++;
+            e.total_ms += ms;
+        }
+        (void)hipEventDestroy(p.a);
+        (void)hipEventDestroy(p.b);
+    }
+    x->pending.clear();
+}
+
+int check_index(const vs_index *x) {
+    if (!x) return set_err(VS_ERR_INVALID, "null index handle");
+    return VS_OK;
+}
+
+// Grows device storage to hold `need` rows; rows past ntotal stay zero and
+// kRowCapAlign slack rows follow the capacity so whole-tile reads of the
+// last rows stay inside the allocation.
+int ensure_capacity(vs_index *x, int64_t need) {
+    if (need <= x->cap) return VS_OK;
+    int64_t nc = std::max<int64_t>(need, x->cap * 2);
+    nc = std::max<int64_t>(nc, 1024);
+    nc = round_up(nc, kRowCapAlign);
+    const int64_t rb = row_bytes(x);
+    void *nxb = nullptr;
+    float *nxn = nullptr;
+    const size_t xbytes = (size_t)(nc + kRowCapAlign) * rb;
+    const size_t nbytes = (size_t)(nc + kRowCapAlign) * sizeof(float);
+    VS_HIP(hipMalloc(&nxb, xbytes), "allocating vector storage");
+    if (hipMalloc((void **)&nxn, nbytes) != hipSuccess) {
+        (void)hipFree(nxb);
+        return set_err(VS_ERR_OOM, "allocating norm storage (%zu bytes)", nbytes);
+    }
+    VS_HIP(hipMemsetAsync(nxb, 0, xbytes, x->st), "clearing storage");
+    VS_HIP(hipMemsetAsync(nxn, 0, nbytes, x->st), "clearing norms");
+    if (x->ntotal > 0) {
+        VS_HIP(hipMemcpyAsync(nxb, x->xb, (size_t)x->ntotal * rb, hipMemcpyDeviceToDevice, x->st),
+               "copying storage");
+        VS_HIP(hipMemcpyAsync(nxn, x->xn, (size_t)x->ntotal * sizeof(float),
+                              hipMemcpyDeviceToDevice, x->st),
+               "copying norms");
+    }
+    VS_HIP(hipStreamSynchronize(x->st), "growing storage");
+    if (x->xb) (void)hipFree(x->xb);
+    if (x->xn) (void)hipFree(x->xn);
+    x->xb = nxb;
+    x->xn = nxn;
+    x->cap = nc;
+    return VS_OK;
+}
+
+// Validation of n rows already on the device: returns flags.
+int device_flags(vs_index *x, const void *src, int dtype, int64_t stride, int64_t n, uint32_t *out) {
+    VS_HIP(x->flags.ensure(sizeof(uint32_t)), "flags buffer");
+    VS_HIP(hipMemsetAsync(x->flags.p, 0, sizeof(uint32_t), x->st), "clearing flags");
+    // store_rows with a throw-away destination computes the flags: use the
+    // misc buffer sized for one chunk of rows.
+    const int64_t chunk = 1 << 16;
+    for (int64_t r = 0; r < n; r += chunk) {
+        const int64_t m = std::min(chunk, n - r);
+        const int64_t dst_ld = vs::storage_ld(x->d, 0);
+        VS_HIP(x->misc.ensure((size_t)m * dst_ld * 4 + (size_t)m * 4), "validation scratch");
+        const char *s = (const char *)src + (size_t)r * stride * (dtype == 1 ? 2 : 4);
+        VS_HIP(vs::launch_store_rows(s, dtype, stride, m, x->d, x->misc.p, 0, dst_ld,
+                                     (float *)((char *)x->misc.p + (size_t)m * dst_ld * 4),
+                                     x->flags.as<uint32_t>(), x->st),
+               "validating rows");
+    }
+    VS_HIP(hipMemcpyAsync(out, x->flags.p, sizeof(uint32_t), hipMemcpyDeviceToHost, x->st),
+           "reading flags");
+    VS_HIP(hipStreamSynchronize(x->st), "validating rows");
+    return VS_OK;
+}
+
+// Switch bf16 storage to fp32 (AUTO storage meeting a non-bf16 value).
+int widen_storage(vs_index *x) {
+    const int64_t new_ld = vs::storage_ld(x->d, 0);
+    const int64_t nc = std::max<int64_t>(x->cap, 1024);
+    void *nxb = nullptr;
+    float *nxn = nullptr;
+    const size_t xbytes = (size_t)(nc + kRowCapAlign) * new_ld * 4;
+    const size_t nbytes = (size_t)(nc + kRowCapAlign) * sizeof(float);
+    VS_HIP(hipMalloc(&nxb, xbytes), "allocating fp32 storage");
+    if (hipMalloc((void **)&nxn, nbytes) != hipSuccess) {
+        (void)hipFree(nxb);
+        return set_err(VS_ERR_OOM, "allocating norm storage");
+    }
+    VS_HIP(hipMemsetAsync(nxb, 0, xbytes, x->st), "clearing storage");
+    VS_HIP(hipMemsetAsync(nxn, 0, nbytes, x->st), "clearing norms");
+    VS_HIP(x->flags.ensure(sizeof(uint32_t)), "flags buffer");
+    if (x->ntotal > 0)
+        VS_HIP(vs::launch_store_rows(x->xb, 1, x->ld, x->ntotal, x->d, nxb, 0, new_ld, nxn,
+                                     x->flags.as<uint32_t>(), x->st),
+               "widening storage");
+    VS_HIP(hipStreamSynchronize(x->st), "widening storage");
+    if (x->xb) (void)hipFree(x->xb);
+    if (x->xn) (void)hipFree(x->xn);
+    x->xb = nxb;
+    x->xn = nxn;
+    x->cap = nc;
+    x->ld = new_ld;
+    x->storage = 0;
+    return VS_OK;
+}
+
+int add_device_rows(vs_index *x, const void *src, int dtype, int64_t n) {
+    uint32_t f = 0;
+    int rc = device_flags(x, src, dtype, x->d, n, &f);
+    if (rc) return rc;
+    if (f & vs::kFlagNonFinite)
+        return set_err(VS_ERR_NONFINITE, "vectors contain NaN or infinity");
+    if (x->mode == VS_STORAGE_AUTO && x->storage == 1 && (f & vs::kFlagNotBf16)) {
+        rc = widen_storage(x);
+        if (rc) return rc;
+    }
+    rc = ensure_capacity(x, x->ntotal + n);
+    if (rc) return rc;
+    VS_HIP(x->flags.ensure(sizeof(uint32_t)), "flags buffer");
+    char *dst = (char *)x->xb + (size_t)x->ntotal * row_bytes(x);
+    VS_HIP(vs::launch_store_rows(src, dtype, x->d, n, x->d, dst, x->storage, x->ld,
+                                 x->xn + x->ntotal, x->flags.as<uint32_t>(), x->st),
+           "storing rows");
+    VS_HIP(hipStreamSynchronize(x->st), "storing rows");
+    x->ntotal += n;
+    return VS_OK;
+}
+
+int check_dtype(int dt) {
+    if (dt != VS_DTYPE_F32 && dt != VS_DTYPE_BF16)
+        return set_err(VS_ERR_INVALID, "dtype must be VS_DTYPE_F32 or VS_DTYPE_BF16 (got %d)", dt);
+    return VS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Planning
+// ---------------------------------------------------------------------------
+int plan_scan(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t kk,
+              vs::ScanPlan *p) {
+    p->kk = (int)kk;
+    p->cap = (int)next_pow2(kk + 48);
+    p->tm = 2;
+    const int cands[3] = {64, 32, 16};
+    p->bn = 0;
+    for (int bn : cands) {
+        if (bn > 16 && round_up(nq, 16) < bn) continue;
+        if (vs::scan_lds_bytes(bn, planes, x->ld, p->cap) <= x->lds_max) {
+            p->bn = bn;
+            break;
+        }
+    }
+    if (!p->bn)
+        return set_err(VS_ERR_UNSUPPORTED,
+                       "d=%lld is too large for the LDS-resident query block of this build",
+                       (long long)x->d);
+    p->lds_bytes = vs::scan_lds_bytes(p->bn, planes, x->ld, p->cap);
+    p->nqblk = (nq + p->bn - 1) / p->bn;
+    const int64_t tile_rows = 64 * p->tm;  // rows per block per round
+    const int64_t target = (int64_t)x->num_cu * 4;
+    int64_t nsplit = std::max<int64_t>(1, (target + p->nqblk - 1) / p->nqblk);
+    const int64_t min_rows = tile_rows * 8;
+    nsplit = std::min<int64_t>(nsplit, std::max<int64_t>(1, (nrows + min_rows - 1) / min_rows));
+    int64_t rps = round_up((nrows + nsplit - 1) / nsplit, tile_rows);
+    if (rps <= 0) rps = tile_rows;
+    p->rows_per_split = rps;
+    p->nsplit = std::max<int64_t>(1, (nrows + rps - 1) / rps);
+    return VS_OK;
+}
+
+int prepare_queries(vs_index *x, const void *q_dev, int q_dtype, int64_t stride, int64_t nq,
+                    vs::PreparedQueries *pq, uint32_t *flags_out) {
+    pq->nq = nq;
+    pq->nq_pad = round_up(std::max<int64_t>(nq, 1), 64);
+    VS_HIP(x->qp.ensure((size_t)pq->nq_pad * 2 * x->ld * 2), "query planes");
+    VS_HIP(x->qf.ensure((size_t)std::max<int64_t>(nq, 1) * x->d * 4), "query copy");
+    VS_HIP(x->qnorm.ensure((size_t)pq->nq_pad * 4), "query norms");
+    VS_HIP(x->flags.ensure(sizeof(uint32_t)), "flags buffer");
+    pq->qp = x->qp.as<uint16_t>();
+    pq->qf = x->qf.as<float>();
+    pq->qnorm = x->qnorm.as<float>();
+    VS_HIP(hipMemsetAsync(x->flags.p, 0, sizeof(uint32_t), x->st), "clearing flags");
+    VS_HIP(vs::launch_prepare_queries(q_dev, q_dtype, stride, nq, x->d, x->ld, x->metric, *pq,
+                                      x->flags.as<uint32_t>(), x->st),
+           "preparing queries");
+    uint32_t f = 0;
+    VS_HIP(hipMemcpyAsync(&f, x->flags.p, sizeof f, hipMemcpyDeviceToHost, x->st), "query flags");
+    VS_HIP(hipStreamSynchronize(x->st), "preparing queries");
+    if (f & vs::kFlagNonFinite) return set_err(VS_ERR_NONFINITE, "queries contain NaN or infinity");
+    pq->planes = (f & vs::kFlagNotBf16) ? 2 : 1;
+    if (flags_out) *flags_out = f;
+    return VS_OK;
+}
+
+__global__ void fill_sentinels_kernel(float *D, int32_t *I, int64_t m, float v) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t < m) {
+        D[t] = v;
+        I[t] = -1;
+    }
+}
+
+int search_device(vs_index *x, const void *q_dev, int q_dtype, int64_t nq, int64_t k, float *D,
+                  int32_t *I) {
+    if (nq < 0 || k < 0) return set_err(VS_ERR_INVALID, "nq and k must be >= 0");
+    if (nq == 0) return VS_OK;
+    if (k == 0) {
+        if (x->ntotal == 0) return VS_OK;
+        // TopK(0).push reads _score[0] of an empty list (index.dart:248-260)
+        return set_err(VS_ERR_INVALID, "k must be >= 1 for a non-empty index");
+    }
+    if (x->ntotal == 0) {
+        const int64_t m = nq * k;
+        fill_sentinels_kernel<<<dim3((unsigned)((m + 255) / 256)), dim3(256), 0, x->st>>>(
+            D, I, m, x->metric == 0 ? __builtin_huge_valf() : -__builtin_huge_valf());
+        VS_HIP(hipGetLastError(), "filling sentinels");
+        VS_HIP(hipStreamSynchronize(x->st), "search");
+        return VS_OK;
+    }
+    const int64_t kk = std::max<int64_t>(8, next_pow2(k + std::max<int64_t>(4, k / 4)));
+    if (kk > 512)
+        return set_err(VS_ERR_UNSUPPORTED, "k=%lld exceeds the fused top-k limit of this build (400)",
+                       (long long)k);
+    vs::PreparedQueries pq;
+    int rc = prepare_queries(x, q_dev, q_dtype, x->d, nq, &pq, nullptr);
+    if (rc) return rc;
+    vs::ScanPlan plan;
+    rc = plan_scan(x, nq, x->ntotal, pq.planes, kk, &plan);
+    if (rc) return rc;
+    const size_t nlist = (size_t)plan.nqblk * plan.nsplit * 4 * plan.bn * plan.cap;
+    VS_HIP(x->cand_v.ensure(nlist * 4), "candidate lists");
+    VS_HIP(x->cand_i.ensure(nlist * 4), "candidate lists");
+    {
+        ProfScope ps(x, "scan");
+        VS_HIP(vs::launch_scan_topk(x->xb, x->storage, x->ld, x->xn, x->ntotal, x->metric, pq, plan,
+                                    x->cand_v.as<float>(), x->cand_i.as<int32_t>(), x->st),
+               "scan kernel");
+    }
+    {
+        ProfScope ps(x, "merge");
+        VS_HIP(vs::launch_merge_refine(x->xb, x->storage, x->ld, x->d, x->metric, pq, plan,
+                                       x->cand_v.as<float>(), x->cand_i.as<int32_t>(), k, D, I,
+                                       x->st),
+               "merge kernel");
+    }
+    VS_HIP(hipStreamSynchronize(x->st), "search");
+    return VS_OK;
+}
+
+float xnorm_max(vs_index *x) {
+    if (x->ntotal == 0) return 0.f;
+    if (x->misc.ensure(sizeof(float)) != hipSuccess) return INFINITY;
+    if (vs::launch_max_reduce(x->xn, x->ntotal, x->misc.as<float>(), x->st) != hipSuccess)
+        return INFINITY;
+    float m = 0.f;
+    if (hipMemcpyAsync(&m, x->misc.p, sizeof m, hipMemcpyDeviceToHost, x->st) != hipSuccess)
+        return INFINITY;
+    if (hipStreamSynchronize(x->st) != hipSuccess) return INFINITY;
+    return std::sqrt(m) * (1.0f + 1e-6f);
+}
+
+struct RangeHits {
+    std::vector<int32_t> q, id;
+    std::vector<float> s;
+};
+
+// Candidate scan + exact re-test; hits sorted by (query, id).
+int range_core(vs_index *x, const vs::PreparedQueries &pq, double radius, int self_join,
+               uint32_t qflags, RangeHits *out) {
+    out->q.clear();
+    out->id.clear();
+    out->s.clear();
+    if (pq.nq == 0 || x->ntotal == 0) return VS_OK;
+    vs::ScanPlan plan;
+    int rc = plan_scan(x, pq.nq, x->ntotal, pq.planes, 8, &plan);
+    if (rc) return rc;
+    const float xmax = xnorm_max(x);
+    VS_HIP(x->athr.ensure((size_t)pq.nq * 4), "range bounds");
+    const int exact_q = (qflags & vs::kFlagNotBf16) ? 0 : 1;
+    const int exact_x = x->storage == 1 ? 1 : 0;
+    VS_HIP(vs::launch_range_bounds(pq, x->d, x->metric, radius, xmax, exact_q, exact_x,
+                                   x->athr.as<float>(), x->st),
+           "range bounds");
+    VS_HIP(x->rcount.ensure(sizeof(unsigned long long)), "range counter");
+    int64_t cap = std::max<int64_t>(1 << 20, pq.nq * 4);
+    unsigned long long found = 0;
+    for (int attempt = 0; attempt < 2; ++attempt) {
+        VS_HIP(x->rq.ensure((size_t)cap * 4), "range candidates");
+        VS_HIP(x->ri.ensure((size_t)cap * 4), "range candidates");
+        VS_HIP(hipMemsetAsync(x->rcount.p, 0, sizeof(unsigned long long), x->st), "range counter");
+        {
+            ProfScope ps(x, self_join ? "join" : "range");
+            VS_HIP(vs::launch_scan_range(x->xb, x->storage, x->ld, x->xn, x->ntotal, pq, plan,
+                                         x->athr.as<float>(), self_join, x->metric,
+                                         x->rq.as<int32_t>(), x->ri.as<int32_t>(),
+                                         x->rcount.as<unsigned long long>(), cap, x->st),
+                   "range scan");
+        }
+        VS_HIP(hipMemcpyAsync(&found, x->rcount.p, sizeof found, hipMemcpyDeviceToHost, x->st),
+               "range count");
+        VS_HIP(hipStreamSynchronize(x->st), "range scan");
+        if ((int64_t)found <= cap) break;
+        cap = (int64_t)found;  // second pass stores everything
+    }
+    const int64_t m = (int64_t)found;
+    if (m == 0) return VS_OK;
+    VS_HIP(x->rs.ensure((size_t)m * 4), "range scores");
+    VS_HIP(x->rkeep.ensure((size_t)m), "range flags");
+    {
+        ProfScope ps(x, "refine");
+        VS_HIP(vs::launch_range_refine(x->xb, x->storage, x->ld, x->d, x->metric, pq.qf,
+                                       x->rq.as<int32_t>(), x->ri.as<int32_t>(), m, radius,
+                                       x->rs.as<float>(), x->rkeep.as<uint8_t>(), x->st),
+               "range refine");
+    }
+    std::vector<int32_t> cq(m), ci(m);
+    std::vector<float> cs(m);
+    std::vector<uint8_t> keep(m);
+    VS_HIP(hipMemcpyAsync(cq.data(), x->rq.p, (size_t)m * 4, hipMemcpyDeviceToHost, x->st), "D2H");
+    VS_HIP(hipMemcpyAsync(ci.data(), x->ri.p, (size_t)m * 4, hipMemcpyDeviceToHost, x->st), "D2H");
+    VS_HIP(hipMemcpyAsync(cs.data(), x->rs.p, (size_t)m * 4, hipMemcpyDeviceToHost, x->st), "D2H");
+    VS_HIP(hipMemcpyAsync(keep.data(), x->rkeep.p, (size_t)m, hipMemcpyDeviceToHost, x->st), "D2H");
+    VS_HIP(hipStreamSynchronize(x->st), "range results");
+    std::vector<int64_t> idx;
+    idx.reserve(m);
+    for (int64_t t = 0; t < m; ++t)
+        if (keep[t]) idx.push_back(t);
+    std::sort(idx.begin(), idx.end(), [&](int64_t a, int64_t b) {
+        return cq[a] != cq[b] ? cq[a] < cq[b] : ci[a] < ci[b];
+    });
+    out->q.resize(idx.size());
+    out->id.resize(idx.size());
+    out->s.resize(idx.size());
+    for (size_t t = 0; t < idx.size(); ++t) {
+        out->q[t] = cq[idx[t]];
+        out->id[t] = ci[idx[t]];
+        out->s[t] = cs[idx[t]];
+    }
+    return VS_OK;
+}
+
+}  // namespace
+
+// ===========================================================================
+// ABI
+// ===========================================================================
+extern "C" {
+
+const char *vs_last_error(void) { return g_err.c_str(); }
+
+int vs_device_count(int *count) {
+    if (!count) return set_err(VS_ERR_INVALID, "null count");
+    int c = 0;
+    hipError_t e = hipGetDeviceCount(&c);
+    if (e != hipSuccess) {
+        *count = 0;
+        return set_err(VS_ERR_NO_DEVICE, "hipGetDeviceCount: %s", hipGetErrorString(e));
+    }
+    *count = c;
+    return VS_OK;
+}
+
+int vs_device_name(int device, char *buf, int64_t len) {
+    hipDeviceProp_t p;
+    hipError_t e = hipGetDeviceProperties(&p, device);
+    if (e != hipSuccess) return hip_err(e, "hipGetDeviceProperties");
+    snprintf(buf, (size_t)len, "%s (%s, %d CUs)", p.name, p.gcnArchName, p.multiProcessorCount);
+    return VS_OK;
+}
+
+int vs_index_create(int device, int64_t d, int metric, int storage, vs_index **out) {
+    if (!out) return set_err(VS_ERR_INVALID, "null output handle");
+    *out = nullptr;
+    if (d <= 0) return set_err(VS_ERR_INVALID, "d must be > 0 (got %lld)", (long long)d);
+    if (metric != VS_METRIC_L2 && metric != VS_METRIC_IP)
+        return set_err(VS_ERR_INVALID, "unknown metric code %d", metric);
+    if (storage != VS_STORAGE_F32 && storage != VS_STORAGE_BF16 && storage != VS_STORAGE_AUTO)
+        return set_err(VS_ERR_INVALID, "unknown storage code %d", storage);
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0)
+        return set_err(VS_ERR_NO_DEVICE, "no HIP device visible");
+    if (device < 0 || device >= count)
+        return set_err(VS_ERR_INVALID, "device %d out of range [0, %d)", device, count);
+    DeviceGuard g(device);
+    if (g.err != hipSuccess) return hip_err(g.err, "hipSetDevice");
+    vs_index *x = new (std::nothrow) vs_index();
+    if (!x) return set_err(VS_ERR_OOM, "host allocation");
+    x->device = device;
+    x->d = d;
+    x->metric = metric;
+    x->mode = storage;
+    x->storage = storage == VS_STORAGE_F32 ? 0 : 1;
+    x->ld = vs::storage_ld(d, x->storage);
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, device) == hipSuccess) {
+        x->num_cu = p.multiProcessorCount;
+        x->lds_max = p.sharedMemPerBlock;
+    }
+    hipError_t e = hipStreamCreateWithFlags(&x->st, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete x;
+        return hip_err(e, "hipStreamCreate");
+    }
+    *out = x;
+    return VS_OK;
+}
+
+void vs_index_destroy(vs_index *x) {
+    if (!x) return;
+    DeviceGuard g(x->device);
+    if (x->st) (void)hipStreamSynchronize(x->st);
+    for (auto &p : x->pending) {
+        (void)hipEventDestroy(p.a);
+        (void)hipEventDestroy(p.b);
+    }
+    if (x->xb) (void)hipFree(x->xb);
+    if (x->xn) (void)hipFree(x->xn);
+    DevBuf *bufs[] = {&x->stage,   &x->qp,        &x->qf,       &x->qnorm,    &x->flags,
+                      &x->cand_v,  &x->cand_i,    &x->outD,     &x->outI,     &x->athr,
+                      &x->rq,      &x->ri,        &x->rs,       &x->rkeep,    &x->rcount,
+                      &x->misc,    &x->km_cen,    &x->km_cxn,   &x->km_assign, &x->km_best,
+                      &x->km_fb,   &x->km_keys,   &x->km_order, &x->km_tmp,   &x->km_counts,
+                      &x->km_offsets, &x->km_out, &x->km_iota};
+    for (DevBuf *b : bufs) b->release();
+    if (x->st) (void)hipStreamDestroy(x->st);
+    delete x;
+}
+
+int vs_index_reserve(vs_index *x, int64_t n) {
+    if (int rc = check_index(x)) return rc;
+    if (n < 0) return set_err(VS_ERR_INVALID, "n must be >= 0");
+    DeviceGuard g(x->device);
+    return ensure_capacity(x, n);
+}
+
+int vs_index_reset(vs_index *x) {
+    if (int rc = check_index(x)) return rc;
+    DeviceGuard g(x->device);
+    if (x->ntotal > 0) {
+        VS_HIP(hipMemsetAsync(x->xb, 0, (size_t)x->ntotal * row_bytes(x), x->st), "reset");
+        VS_HIP(hipMemsetAsync(x->xn, 0, (size_t)x->ntotal * 4, x->st), "reset");
+        VS_HIP(hipStreamSynchronize(x->st), "reset");
+    }
+    x->ntotal = 0;
+    return VS_OK;
+}
+
+int64_t vs_index_ntotal(const vs_index *x) { return x ? x->ntotal : -1; }
+int64_t vs_index_d(const vs_index *x) { return x ? x->d : -1; }
+int vs_index_metric(const vs_index *x) { return x ? x->metric : -1; }
+int vs_index_storage(const vs_index *x) { return x ? x->storage : -1; }
+
+int vs_index_add(vs_index *x, const void *xs, int src_dtype, int64_t n) {
+    if (int rc = check_index(x)) return rc;
+    if (int rc = check_dtype(src_dtype)) return rc;
+    if (n < 0) return set_err(VS_ERR_INVALID, "n must be >= 0");
+    if (n == 0) return VS_OK;
+    if (!xs) return set_err(VS_ERR_INVALID, "null vectors");
+    if (x->ntotal + n > (int64_t)INT32_MAX)
+        return set_err(VS_ERR_INVALID, "ids are int32: ntotal + n must stay below 2^31");
+    DeviceGuard g(x->device);
+    const int64_t es = src_dtype == 1 ? 2 : 4;
+    const int64_t rowb = x->d * es;
+    // validate everything before storing anything (add is all-or-nothing)
+    const int64_t chunk = std::max<int64_t>(1, (int64_t)(256 << 20) / rowb);
+    bool any_not_bf16 = false;
+    for (int64_t r = 0; r < n; r += chunk) {
+        const int64_t m = std::min(chunk, n - r);
+        VS_HIP(x->stage.ensure((size_t)m * rowb), "staging buffer");
+        VS_HIP(hipMemcpyAsync(x->stage.p, (const char *)xs + (size_t)r * rowb, (size_t)m * rowb,
+                              hipMemcpyHostToDevice, x->st),
+               "uploading vectors");
+        uint32_t f = 0;
+        int rc = device_flags(x, x->stage.p, src_dtype, x->d, m, &f);
+        if (rc) return rc;
+        if (f & vs::kFlagNonFinite)
+            return set_err(VS_ERR_NONFINITE, "vectors contain NaN or infinity");
+        any_not_bf16 |= (f & vs::kFlagNotBf16) != 0;
+    }
+    if (x->mode == VS_STORAGE_AUTO && x->storage == 1 && any_not_bf16) {
+        int rc = widen_storage(x);
+        if (rc) return rc;
+    }
+    int rc = ensure_capacity(x, x->ntotal + n);
+    if (rc) return rc;
+    VS_HIP(x->flags.ensure(sizeof(uint32_t)), "flags buffer");
+    for (int64_t r = 0; r < n; r += chunk) {
+        const int64_t m = std::min(chunk, n - r);
+        VS_HIP(hipMemcpyAsync(x->stage.p, (const char *)xs + (size_t)r * rowb, (size_t)m * rowb,
+                              hipMemcpyHostToDevice, x->st),
+               "uploading vectors");
+        char *dst = (char *)x->xb + (size_t)(x->ntotal + r) * row_bytes(x);
+        VS_HIP(vs::launch_store_rows(x->stage.p, src_dtype, x->d, m, x->d, dst, x->storage, x->ld,
+                                     x->xn + x->ntotal + r, x->flags.as<uint32_t>(), x->st),
+               "storing rows");
+        VS_HIP(hipStreamSynchronize(x->st), "storing rows");
+    }
+    x->ntotal += n;
+    return VS_OK;
+}
+
+int vs_index_add_device(vs_index *x, const void *xs_dev, int src_dtype, int64_t n) {
+    if (int rc = check_index(x)) return rc;
+    if (int rc = check_dtype(src_dtype)) return rc;
+    if (n < 0) return set_err(VS_ERR_INVALID, "n must be >= 0");
+    if (n == 0) return VS_OK;
+    if (!xs_dev) return set_err(VS_ERR_INVALID, "null vectors");
+    if (x->ntotal + n > (int64_t)INT32_MAX)
+        return set_err(VS_ERR_INVALID, "ids are int32: ntotal + n must stay below 2^31");
+    DeviceGuard g(x->device);
+    return add_device_rows(x, xs_dev, src_dtype, n);
+}
+
+int vs_index_reconstruct(vs_index *x, int64_t i0, int64_t n, float *out) {
+    if (int rc = check_index(x)) return rc;
+    if (i0 < 0 || n < 0 || i0 + n > x->ntotal)
+        return set_err(VS_ERR_INVALID, "rows [%lld, %lld) out of range [0, %lld)", (long long)i0,
+                       (long long)(i0 + n), (long long)x->ntotal);
+    if (n == 0) return VS_OK;
+    if (!out) return set_err(VS_ERR_INVALID, "null output");
+    DeviceGuard g(x->device);
+    const int64_t rb = row_bytes(x);
+    std::vector<char> tmp((size_t)n * rb);
+    VS_HIP(hipMemcpyAsync(tmp.data(), (const char *)x->xb + (size_t)i0 * rb, (size_t)n * rb,
+                          hipMemcpyDeviceToHost, x->st),
+           "reading rows");
+    VS_HIP(hipStreamSynchronize(x->st), "reading rows");
+    for (int64_t r = 0; r < n; ++r)
+        for (int64_t j = 0; j < x->d; ++j)
+            out[r * x->d + j] = x->storage == 1
+                                    ? bf16_to_f32(((const uint16_t *)(tmp.data() + r * rb))[j])
+                                    : ((const float *)(tmp.data() + r * rb))[j];
+    return VS_OK;
+}
+
+int vs_index_remove_ids(vs_index *x, const int64_t *ids, int64_t n, int64_t *nremoved) {
+    if (int rc = check_index(x)) return rc;
+    if (n < 0) return set_err(VS_ERR_INVALID, "n must be >= 0");
+    if (nremoved) *nremoved = 0;
+    if (n == 0 || x->ntotal == 0) return VS_OK;
+    if (!ids) return set_err(VS_ERR_INVALID, "null ids");
+    DeviceGuard g(x->device);
+    std::vector<uint8_t> drop((size_t)x->ntotal, 0);
+    for (int64_t t = 0; t < n; ++t)
+        if (ids[t] >= 0 && ids[t] < x->ntotal) drop[(size_t)ids[t]] = 1;
+    std::vector<int32_t> dst((size_t)x->ntotal);
+    int64_t w = 0;
+    for (int64_t r = 0; r < x->ntotal; ++r) dst[(size_t)r] = drop[(size_t)r] ? -1 : (int32_t)w++;
+    const int64_t removed = x->ntotal - w;
+    if (removed == 0) return VS_OK;
+    const int64_t rb = row_bytes(x);
+    void *nxb = nullptr;
+    float *nxn = nullptr;
+    const size_t xbytes = (size_t)(x->cap + kRowCapAlign) * rb;
+    const size_t nbytes = (size_t)(x->cap + kRowCapAlign) * 4;
+    VS_HIP(hipMalloc(&nxb, xbytes), "removeIds storage");
+    if (hipMalloc((void **)&nxn, nbytes) != hipSuccess) {
+        (void)hipFree(nxb);
+        return set_err(VS_ERR_OOM, "removeIds norms");
+    }
+    VS_HIP(hipMemsetAsync(nxb, 0, xbytes, x->st), "removeIds");
+    VS_HIP(hipMemsetAsync(nxn, 0, nbytes, x->st), "removeIds");
+    VS_HIP(x->misc.ensure((size_t)x->ntotal * 4), "removeIds map");
+    VS_HIP(hipMemcpyAsync(x->misc.p, dst.data(), (size_t)x->ntotal * 4, hipMemcpyHostToDevice,
+                          x->st),
+           "removeIds map");
+    VS_HIP(vs::launch_compact_rows(x->xb, nxb, x->xn, nxn, x->misc.as<int32_t>(), x->ntotal, rb,
+                                   x->st),
+           "removeIds compaction");
+    VS_HIP(hipStreamSynchronize(x->st), "removeIds");
+    (void)hipFree(x->xb);
+    (void)hipFree(x->xn);
+    x->xb = nxb;
+    x->xn = nxn;
+    x->ntotal = w;
+    if (nremoved) *nremoved = removed;
+    return VS_OK;
+}
+
+int vs_index_search_device(vs_index *x, const void *q_dev, int q_dtype, int64_t nq, int64_t k,
+                           float *D_dev, int32_t *I_dev) {
+    if (int rc = check_index(x)) return rc;
+    if (int rc = check_dtype(q_dtype)) return rc;
+    if (nq > 0 && k > 0 && (!q_dev || !D_dev || !I_dev))
+        return set_err(VS_ERR_INVALID, "null query or output buffer");
+    DeviceGuard g(x->device);
+    return search_device(x, q_dev, q_dtype, nq, k, D_dev, I_dev);
+}
+
+int vs_index_search(vs_index *x, const void *q, int q_dtype, int64_t nq, int64_t k, float *D,
+                    int32_t *I) {
+    if (int rc = check_index(x)) return rc;
+    if (int rc = check_dtype(q_dtype)) return rc;
+    if (nq < 0 || k < 0) return set_err(VS_ERR_INVALID, "nq and k must be >= 0");
+    if (nq == 0) return VS_OK;
+    if (k > 0 && (!q || !D || !I)) return set_err(VS_ERR_INVALID, "null query or output buffer");
+    DeviceGuard g(x->device);
+    const size_t qbytes = (size_t)nq * x->d * (q_dtype == 1 ? 2 : 4);
+    VS_HIP(x->stage.ensure(qbytes), "query staging");
+    VS_HIP(hipMemcpyAsync(x->stage.p, q, qbytes, hipMemcpyHostToDevice, x->st), "uploading queries");
+    if (k == 0) return search_device(x, x->stage.p, q_dtype, nq, k, nullptr, nullptr);
+    VS_HIP(x->outD.ensure((size_t)nq * k * 4), "result buffer");
+    VS_HIP(x->outI.ensure((size_t)nq * k * 4), "result buffer");
+    int rc = search_device(x, x->stage.p, q_dtype, nq, k, x->outD.as<float>(), x->outI.as<int32_t>());
+    if (rc) return rc;
+    VS_HIP(hipMemcpyAsync(D, x->outD.p, (size_t)nq * k * 4, hipMemcpyDeviceToHost, x->st),
+           "reading distances");
+    VS_HIP(hipMemcpyAsync(I, x->outI.p, (size_t)nq * k * 4, hipMemcpyDeviceToHost, x->st),
+           "reading ids");
+    VS_HIP(hipStreamSynchronize(x->st), "search");
+    return VS_OK;
+}
+
+int vs_index_range_search(vs_index *x, const void *q, int q_dtype, int64_t nq, double radius,
+                          vs_range_result **out) {
+    if (int rc = check_index(x)) return rc;
+    if (int rc = check_dtype(q_dtype)) return rc;
+    if (!out) return set_err(VS_ERR_INVALID, "null output");
+    *out = nullptr;
+    if (nq < 0) return set_err(VS_ERR_INVALID, "nq must be >= 0");
+    if (nq > 0 && !q) return set_err(VS_ERR_INVALID, "null queries");
+    if (!std::isfinite(radius)) return set_err(VS_ERR_INVALID, "radius must be finite");
+    DeviceGuard g(x->device);
+    RangeHits hits;
+    if (nq > 0 && x->ntotal > 0) {
+        const size_t qbytes = (size_t)nq * x->d * (q_dtype == 1 ? 2 : 4);
+        VS_HIP(x->stage.ensure(qbytes), "query staging");
+        VS_HIP(hipMemcpyAsync(x->stage.p, q, qbytes, hipMemcpyHostToDevice, x->st),
+               "uploading queries");
+        vs::PreparedQueries pq;
+        uint32_t f = 0;
+        int rc = prepare_queries(x, x->stage.p, q_dtype, x->d, nq, &pq, &f);
+        if (rc) return rc;
+        rc = range_core(x, pq, radius, 0, f, &hits);
+        if (rc) return rc;
+    }
+    vs_range_result *r = (vs_range_result *)calloc(1, sizeof(vs_range_result));
+    if (!r) return set_err(VS_ERR_OOM, "host allocation");
+    const size_t m = hits.q.size();
+    r->nq = nq;
+    r->lims = (int64_t *)calloc((size_t)nq + 1, sizeof(int64_t));
+    r->D = (float *)malloc(std::max<size_t>(m, 1) * sizeof(float));
+    r->I = (int32_t *)malloc(std::max<size_t>(m, 1) * sizeof(int32_t));
+    if (!r->lims || !r->D || !r->I) {
+        vs_range_result_free(r);
+        return set_err(VS_ERR_OOM, "host allocation");
+    }
+    for (size_t t = 0; t < m; ++t) r->lims[hits.q[t] + 1]++;
+    for (int64_t qi = 0; qi < nq; ++qi) r->lims[qi + 1] += r->lims[qi];
+    if (m) {
+        memcpy(r->D, hits.s.data(), m * sizeof(float));
+        memcpy(r->I, hits.id.data(), m * sizeof(int32_t));
+    }
+    *out = r;
+    return VS_OK;
+}
+
+void vs_range_result_free(vs_range_result *r) {
+    if (!r) return;
+    free(r->lims);
+    free(r->D);
+    free(r->I);
+    free(r);
+}
+
+int vs_index_self_join(vs_index *x, double threshold, vs_pairs **out) {
+    if (int rc = check_index(x)) return rc;
+    if (!out) return set_err(VS_ERR_INVALID, "null output");
+    *out = nullptr;
+    if (!std::isfinite(threshold)) return set_err(VS_ERR_INVALID, "threshold must be finite");
+    DeviceGuard g(x->device);
+    RangeHits hits;
+    if (x->ntotal > 1) {
+        vs::PreparedQueries pq;
+        uint32_t f = 0;
+        int rc = prepare_queries(x, x->xb, x->storage, x->ld, x->ntotal, &pq, &f);
+        if (rc) return rc;
+        rc = range_core(x, pq, threshold, 1, f, &hits);
+        if (rc) return rc;
+    }
+    vs_pairs *p = (vs_pairs *)calloc(1, sizeof(vs_pairs));
+    if (!p) return set_err(VS_ERR_OOM, "host allocation");
+    const size_t m = hits.q.size();
+    p->npairs = (int64_t)m;
+    p->i = (int32_t *)malloc(std::max<size_t>(m, 1) * 4);
+    p->j = (int32_t *)malloc(std::max<size_t>(m, 1) * 4);
+    p->s = (float *)malloc(std::max<size_t>(m, 1) * 4);
+    if (!p->i || !p->j || !p->s) {
+        vs_pairs_free(p);
+        return set_err(VS_ERR_OOM, "host allocation");
+    }
+    if (m) {
+        memcpy(p->i, hits.q.data(), m * 4);
+        memcpy(p->j, hits.id.data(), m * 4);
+        memcpy(p->s, hits.s.data(), m * 4);
+    }
+    *out = p;
+    return VS_OK;
+}
+
+void vs_pairs_free(vs_pairs *p) {
+    if (!p) return;
+    free(p->i);
+    free(p->j);
+    free(p->s);
+    free(p);
+}
+
+int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t min_points,
+                   const double *jitter_u, int64_t njitter, int32_t *assign, float *centroids_out,
+                   int32_t *counts, double *obj) {
+    if (int rc = check_index(x)) return rc;
+    if (K <= 0) return set_err(VS_ERR_INVALID, "K must be > 0");
+    if (!centroids_in || !assign || !centroids_out || !counts)
+        return set_err(VS_ERR_INVALID, "null buffer");
+    if (njitter < 0 || (njitter > 0 && !jitter_u))
+        return set_err(VS_ERR_INVALID, "bad jitter buffer");
+    if (x->storage != 0)
+        return set_err(VS_ERR_UNSUPPORTED, "k-means points must use fp32 storage");
+    if (x->ntotal < K)
+        return set_err(VS_ERR_INVALID, "k-means: need at least k=%lld vectors, got %lld",
+                       (long long)K, (long long)x->ntotal);
+    if (K > (int64_t)INT32_MAX) return set_err(VS_ERR_INVALID, "K too large");
+    DeviceGuard g(x->device);
+    const int64_t n = x->ntotal, d = x->d, ld = x->ld;
+    std::vector<float> cen_in(centroids_in, centroids_in + K * d);  // centroids_out may alias
+
+    // centroid storage: fp32 rows of ld, slack rows zero, plus norms
+    VS_HIP(x->km_cen.ensure((size_t)(K + kRowCapAlign) * ld * 4), "centroid storage");
+    VS_HIP(x->km_cxn.ensure((size_t)(K + kRowCapAlign) * 4), "centroid norms");
+    VS_HIP(hipMemsetAsync(x->km_cen.p, 0, (size_t)(K + kRowCapAlign) * ld * 4, x->st), "clear");
+    VS_HIP(hipMemsetAsync(x->km_cxn.p, 0, (size_t)(K + kRowCapAlign) * 4, x->st), "clear");
+    VS_HIP(x->stage.ensure((size_t)K * d * 4), "centroid staging");
+    VS_HIP(hipMemcpyAsync(x->stage.p, cen_in.data(), (size_t)K * d * 4, hipMemcpyHostToDevice,
+                          x->st),
+           "uploading centroids");
+    VS_HIP(x->flags.ensure(4), "flags");
+    VS_HIP(hipMemsetAsync(x->flags.p, 0, 4, x->st), "flags");
+    VS_HIP(vs::launch_store_rows(x->stage.p, 0, d, K, d, x->km_cen.p, 0, ld,
+                                 x->km_cxn.as<float>(), x->flags.as<uint32_t>(), x->st),
+           "storing centroids");
+    uint32_t cf = 0;
+    VS_HIP(hipMemcpyAsync(&cf, x->flags.p, 4, hipMemcpyDeviceToHost, x->st), "flags");
+    VS_HIP(hipStreamSynchronize(x->st), "centroids");
+    if (cf & vs::kFlagNonFinite) return set_err(VS_ERR_NONFINITE, "centroids contain NaN or infinity");
+
+    // points as prepared queries against the centroid "database"
+    vs::PreparedQueries pq;
+    uint32_t pf = 0;
+    int rc = prepare_queries(x, x->xb, 0, ld, n, &pq, &pf);
+    if (rc) return rc;
+    // the distance kernels index the centroid rows with the points' ld
+    vs_index cview;
+    cview.ld = ld;
+    cview.d = d;
+    cview.lds_max = x->lds_max;
+    cview.num_cu = x->num_cu;
+    vs::ScanPlan plan;
+    rc = plan_scan(&cview, n, K, pq.planes, 16, &plan);
+    if (rc) return rc;
+    const size_t nlist = (size_t)plan.nqblk * plan.nsplit * 4 * plan.bn * plan.cap;
+    VS_HIP(x->cand_v.ensure(nlist * 4), "candidate lists");
+    VS_HIP(x->cand_i.ensure(nlist * 4), "candidate lists");
+    {
+        ProfScope ps(x, "assign");
+        VS_HIP(vs::launch_scan_topk(x->km_cen.p, 0, ld, x->km_cxn.as<float>(), K, 0, pq, plan,
+                                    x->cand_v.as<float>(), x->cand_i.as<int32_t>(), x->st),
+               "assign scan");
+    }
+    // error bound of the accumulator (split-bf16 products + fp32 sums)
+    float cmax = 0.f;
+    {
+        VS_HIP(x->misc.ensure(4), "misc");
+        VS_HIP(vs::launch_max_reduce(x->km_cxn.as<float>(), K, x->misc.as<float>(), x->st), "max");
+        VS_HIP(hipMemcpyAsync(&cmax, x->misc.p, 4, hipMemcpyDeviceToHost, x->st), "max");
+        VS_HIP(hipStreamSynchronize(x->st), "max");
+    }
+    const float pmax = xnorm_max(x);
+    const double u = 1.0 / 16777216.0;
+    const double rel = 4.0 * (d + 4) * u + 8.0 / 65536.0;
+    const float bound = (float)(rel * (2.0 * pmax * std::sqrt((double)cmax) + cmax) * 2.0 + 1e-6);
+
+    VS_HIP(x->km_assign.ensure((size_t)n * 4), "assignments");
+    VS_HIP(x->km_best.ensure((size_t)n * 8), "distances");
+    VS_HIP(x->km_fb.ensure((size_t)(n + 1) * 4), "fallback list");
+    VS_HIP(hipMemsetAsync(x->km_fb.p, 0, 4, x->st), "fallback count");
+    int32_t *fb_count = x->km_fb.as<int32_t>();
+    int32_t *fb_list = fb_count + 1;
+    {
+        ProfScope ps(x, "pick");
+        VS_HIP(vs::launch_kmeans_pick(x->km_cen.as<float>(), ld, d, n, x->km_cen.as<float>(), K,
+                                      x->cand_v.as<float>(), x->cand_i.as<int32_t>(), plan, bound,
+                                      pq.qf, x->km_assign.as<int32_t>(), x->km_best.as<double>(),
+                                      fb_count, fb_list, x->st),
+               "assign pick");
+    }
+    int32_t nfb = 0;
+    VS_HIP(hipMemcpyAsync(&nfb, fb_count, 4, hipMemcpyDeviceToHost, x->st), "fallbacks");
+    VS_HIP(hipStreamSynchronize(x->st), "assign");
+    if (nfb > 0) {
+        ProfScope ps(x, "exhaustive");
+        VS_HIP(vs::launch_kmeans_exhaustive((const float *)x->xb, ld, d, x->km_cen.as<float>(), K,
+                                            fb_list, nfb, x->km_assign.as<int32_t>(),
+                                            x->km_best.as<double>(), x->st),
+               "exhaustive assign");
+    }
+    // objective: fp64 sum in point order (kmeans.dart:104)
+    std::vector<double> best((size_t)n);
+    VS_HIP(hipMemcpyAsync(best.data(), x->km_best.p, (size_t)n * 8, hipMemcpyDeviceToHost, x->st),
+           "reading distances");
+    VS_HIP(hipMemcpyAsync(assign, x->km_assign.p, (size_t)n * 4, hipMemcpyDeviceToHost, x->st),
+           "reading assignments");
+
+    // update: counts, stable grouping by cluster, ordered fp32 sums
+    VS_HIP(x->km_counts.ensure((size_t)K * 4), "counts");
+    VS_HIP(hipMemsetAsync(x->km_counts.p, 0, (size_t)K * 4, x->st), "counts");
+    VS_HIP(vs::launch_kmeans_count(x->km_assign.as<int32_t>(), n, x->km_counts.as<int32_t>(),
+                                   x->st),
+           "counts");
+    VS_HIP(x->km_iota.ensure((size_t)n * 4), "iota");
+    {
+        std::vector<int32_t> iota((size_t)n);
+        std::iota(iota.begin(), iota.end(), 0);
+        VS_HIP(hipMemcpyAsync(x->km_iota.p, iota.data(), (size_t)n * 4, hipMemcpyHostToDevice,
+                              x->st),
+               "iota");
+        VS_HIP(hipStreamSynchronize(x->st), "iota");
+    }
+    VS_HIP(x->km_keys.ensure((size_t)n * 4), "sort keys");
+    VS_HIP(x->km_order.ensure((size_t)n * 4), "sort values");
+    int key_bits = 1;
+    while ((int64_t(1) << key_bits) < K) ++key_bits;
+    size_t tmp_bytes = 0;
+    VS_HIP(vs::sort_pairs_by_key(nullptr, tmp_bytes, x->km_assign.as<int32_t>(),
+                                 x->km_keys.as<int32_t>(), x->km_iota.as<int32_t>(),
+                                 x->km_order.as<int32_t>(), n, key_bits, x->st),
+           "sort size");
+    VS_HIP(x->km_tmp.ensure(tmp_bytes + 16), "sort scratch");
+    VS_HIP(vs::sort_pairs_by_key(x->km_tmp.p, tmp_bytes, x->km_assign.as<int32_t>(),
+                                 x->km_keys.as<int32_t>(), x->km_iota.as<int32_t>(),
+                                 x->km_order.as<int32_t>(), n, key_bits, x->st),
+           "grouping points");
+    VS_HIP(hipMemcpyAsync(counts, x->km_counts.p, (size_t)K * 4, hipMemcpyDeviceToHost, x->st),
+           "reading counts");
+    VS_HIP(hipStreamSynchronize(x->st), "counts");
+    std::vector<int32_t> offs((size_t)K);
+    {
+        int64_t acc = 0;
+        for (int64_t c = 0; c < K; ++c) {
+            offs[(size_t)c] = (int32_t)acc;
+            acc += counts[c];
+        }
+    }
+    VS_HIP(x->km_offsets.ensure((size_t)K * 4), "offsets");
+    VS_HIP(hipMemcpyAsync(x->km_offsets.p, offs.data(), (size_t)K * 4, hipMemcpyHostToDevice,
+                          x->st),
+           "offsets");
+    VS_HIP(x->km_out.ensure((size_t)K * d * 4), "new centroids");
+    VS_HIP(hipMemcpyAsync(x->km_out.p, cen_in.data(), (size_t)K * d * 4, hipMemcpyHostToDevice,
+                          x->st),
+           "new centroids");
+    {
+        ProfScope ps(x, "update");
+        VS_HIP(vs::launch_kmeans_update((const float *)x->xb, ld, d, n, x->km_order.as<int32_t>(),
+                                        x->km_offsets.as<int32_t>(), K,
+                                        x->km_counts.as<int32_t>(), min_points,
+                                        x->km_out.as<float>(), x->st),
+               "update");
+    }
+    std::vector<float> cen_new((size_t)K * d);
+    VS_HIP(hipMemcpyAsync(cen_new.data(), x->km_out.p, (size_t)K * d * 4, hipMemcpyDeviceToHost,
+                          x->st),
+           "reading centroids");
+    VS_HIP(hipStreamSynchronize(x->st), "update");
+    double o = 0.0;
+    for (int64_t i = 0; i < n; ++i) o += best[(size_t)i];
+    if (obj) *obj = o;
+    // empty clusters, in centroid order, in place (kmeans.dart:127-139): the
+    // largest cluster's centroid is already updated when it precedes c
+    int64_t used = 0;
+    for (int64_t c = 0; c < K; ++c) {
+        if (counts[c] >= min_points) continue;
+        int64_t big = 0;
+        for (int64_t cc = 1; cc < K; ++cc)
+            if (counts[cc] > counts[big]) big = cc;
+        for (int64_t j = 0; j < d; ++j) {
+            if (used >= njitter)
+                return set_err(VS_ERR_INVALID,
+                               "empty cluster needs more jitter values than the %lld given",
+                               (long long)njitter);
+            const double jit = (jitter_u[used++] - 0.5) * 1e-4;
+            cen_new[(size_t)(c * d + j)] = (float)((double)cen_new[(size_t)(big * d + j)] + jit);
+        }
+    }
+    memcpy(centroids_out, cen_new.data(), (size_t)K * d * 4);
+    return VS_OK;
+}
+
+// ---- bench / test support ----
+
+int vs_dev_alloc(int device, int64_t bytes, void **out) {
+    if (!out || bytes < 0) return set_err(VS_ERR_INVALID, "bad arguments");
+    DeviceGuard g(device);
+    if (g.err != hipSuccess) return hip_err(g.err, "hipSetDevice");
+    VS_HIP(hipMalloc(out, (size_t)std::max<int64_t>(bytes, 1)), "hipMalloc");
+    return VS_OK;
+}
+
+int vs_dev_free(int device, void *p) {
+    DeviceGuard g(device);
+    if (p) VS_HIP(hipFree(p), "hipFree");
+    return VS_OK;
+}
+
+int vs_dev_upload(int device, void *dst, const void *src, int64_t bytes) {
+    DeviceGuard g(device);
+    VS_HIP(hipMemcpy(dst, src, (size_t)bytes, hipMemcpyHostToDevice), "upload");
+    return VS_OK;
+}
+
+int vs_dev_download(int device, void *dst, const void *src, int64_t bytes) {
+    DeviceGuard g(device);
+    VS_HIP(hipMemcpy(dst, src, (size_t)bytes, hipMemcpyDeviceToHost), "download");
+    return VS_OK;
+}
+
+int vs_gen_normal(int device, void *dst, int out_dtype, int64_t n, int64_t d, uint64_t seed,
+                  uint64_t stream, int normalize) {
+    if (int rc = check_dtype(out_dtype)) return rc;
+    if (n < 0 || d <= 0 || (n > 0 && !dst)) return set_err(VS_ERR_INVALID, "bad arguments");
+    DeviceGuard g(device);
+    if (g.err != hipSuccess) return hip_err(g.err, "hipSetDevice");
+    VS_HIP(vs::launch_gen_normal(dst, out_dtype, n, d, seed, stream, normalize, nullptr),
+           "generator");
+    VS_HIP(hipDeviceSynchronize(), "generator");
+    return VS_OK;
+}
+
+int vs_prof_enable(vs_index *x, int on) {
+    if (int rc = check_index(x)) return rc;
+    x->prof_on = on != 0;
+    return VS_OK;
+}
+
+int vs_prof_get(vs_index *x, const char *family, int64_t *launches, double *total_ms) {
+    if (int rc = check_index(x)) return rc;
+    if (!family) return set_err(VS_ERR_INVALID, "null family");
+    DeviceGuard g(x->device);
+    prof_collect(x);
+    auto it = x->prof.find(family);
+    if (launches) *launches = it == x->prof.end() ? 0 : it->second.launches;
+    if (total_ms) *total_ms = it == x->prof.end() ? 0.0 : it->second.total_ms;
+    return VS_OK;
+}
+
+int vs_prof_reset(vs_index *x) {
+    if (int rc = check_index(x)) return rc;
+    DeviceGuard g(x->device);
+    prof_collect(x);
+    x->prof.clear();
+    return VS_OK;
+}
+
+int vs_index_sync(vs_index *x) {
+    if (int rc = check_index(x)) return rc;
+    DeviceGuard g(x->device);
+    VS_HIP(hipStreamSynchronize(x->st), "sync");
+    return VS_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,157 @@
+// vs_internal.h -- shared definitions of libvs_hip.so (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// Row storage is padded so that one row is a whole number of 256-byte
+// segments: the scan kernels consume rows in 64-byte K-steps, four at a time,
+// without tail handling.
+constexpr int64_t kRowAlignBytes = 256;
+// Device row capacity is a multiple of this, and rows past ntotal are zero,
+// so the last tile of a scan may read whole tiles without bounds checks.
+constexpr int64_t kRowCapAlign = 256;
+
+// ---------------------------------------------------------------------------
+// bf16 helpers (round to nearest even; inputs are finite)
+// ---------------------------------------------------------------------------
+__host__ __device__ inline uint16_t f32_to_bf16_rne(float f) {
+    uint32_t u = __builtin_bit_cast(uint32_t, f);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+__host__ __device__ inline float bf16_to_f32(uint16_t h) {
+    return __builtin_bit_cast(float, (uint32_t)h << 16);
+}
+
+namespace vs {
+
+// ---------------------------------------------------------------------------
+// Kernel-side argument blocks
+// ---------------------------------------------------------------------------
+
+// Prepared queries: the B operand of the distance MFMA.  For query q, plane p
+// (p < planes) holds ld bf16 values at qp + (q * planes + p) * ld.  Plane 0 is
+// bf16(s * q), plane 1 is bf16(s * q - plane0) with s = -2 (L2) or -1 (IP),
+// so the accumulator xn - 2 q.x (L2) or -q.x (IP) is "smaller is better"
+// for both metrics.  Rows beyond d and queries beyond nq are zero.
+struct PreparedQueries {
+    uint16_t *qp = nullptr;  // [nq_pad][planes][ld] bf16
+    float *qf = nullptr;     // [nq][d] fp32 copy of the queries as given
+    float *qnorm = nullptr;  // [nq] sqrt of the fp64 sum of squares
+    int planes = 1;
+    int64_t nq = 0, nq_pad = 0;
+};
+
+// Status flags written by the query-preparation kernel.
+enum : uint32_t { kFlagNonFinite = 1u, kFlagNotBf16 = 2u };
+
+// ---------------------------------------------------------------------------
+// Launchers (vs_kernels.hip).  All enqueue on `st`; none synchronises.
+// ---------------------------------------------------------------------------
+
+// x (n rows, d elems, src dtype, src row stride in elements) -> storage rows
+// (dst dtype, ld) plus xn[i] = fp32(fp64 sum of squares of the stored values).
+// flags |= kFlagNonFinite / kFlagNotBf16 as found in the source values.
+hipError_t launch_store_rows(const void *src, int src_dtype, int64_t src_stride, int64_t n,
+                             int64_t d, void *dst, int dst_dtype, int64_t ld, float *xn,
+                             uint32_t *flags, hipStream_t st);
+
+// Build PreparedQueries from n query rows (src dtype / stride).
+hipError_t launch_prepare_queries(const void *src, int src_dtype, int64_t src_stride, int64_t nq,
+                                  int64_t d, int64_t ld, int metric, const PreparedQueries &pq,
+                                  uint32_t *flags, hipStream_t st);
+
+struct ScanPlan {
+    int bn = 64;          // queries per block (16 * nqb)
+    int tm = 2;           // 16-row blocks per wave tile
+    int kk = 16;          // per-list kept candidates (power of two)
+    int cap = 64;         // per-list buffer capacity (power of two)
+    int64_t nqblk = 0;    // query blocks
+    int64_t nsplit = 0;   // database splits
+    int64_t rows_per_split = 0;
+    size_t lds_bytes = 0;
+};
+
+// Top-k scan: per (query block, split, wave) lists of the kk best approximate
+// candidates, written to cand_v / cand_i ([nqblk][nsplit][4][bn][cap]).
+hipError_t launch_scan_topk(const void *xb, int storage, int64_t ld, const float *xn, int64_t n,
+                            int metric, const PreparedQueries &pq, const ScanPlan &plan,
+                            float *cand_v, int32_t *cand_i, hipStream_t st);
+
+// Merge the per-wave lists of each query, re-rank the kk survivors with the
+// exact fp64 distance and write the k best (sentinel-filled) to D / I.
+hipError_t launch_merge_refine(const void *xb, int storage, int64_t ld, int64_t d, int metric,
+                               const PreparedQueries &pq, const ScanPlan &plan,
+                               const float *cand_v, const int32_t *cand_i, int64_t k, float *D,
+                               int32_t *I, hipStream_t st);
+
+// Range scan: appends (query, id) of every approximate score within the
+// per-query acceptance bound athr (accumulator space) to out_q / out_i
+// (capacity cap); *count receives the total number found (may exceed cap).
+// If self_join, only ids > query index are considered and query q is row
+// q of the database.
+hipError_t launch_scan_range(const void *xb, int storage, int64_t ld, const float *xn, int64_t n,
+                             const PreparedQueries &pq, const ScanPlan &plan, const float *athr,
+                             int self_join, int metric, int32_t *out_q, int32_t *out_i,
+                             unsigned long long *count, int64_t cap, hipStream_t st);
+
+// Exact fp64 re-test of range candidates: s = fp64 score of (q, id); keep[j]
+// = s <= radius (L2) or s >= radius (IP); out_s[j] = fp32(s).
+hipError_t launch_range_refine(const void *xb, int storage, int64_t ld, int64_t d, int metric,
+                               const float *qf, const int32_t *cq, const int32_t *ci, int64_t m,
+                               double radius, float *out_s, uint8_t *keep, hipStream_t st);
+
+// Per-query acceptance bounds for the range scan (accumulator space).
+hipError_t launch_range_bounds(const PreparedQueries &pq, int64_t d, int metric, double radius,
+                               float xnorm_max, int exact_q, int exact_x, float *athr,
+                               hipStream_t st);
+
+// max over rows of xn (for margins)
+hipError_t launch_max_reduce(const float *x, int64_t n, float *out, hipStream_t st);
+
+// Compact database rows: keep rows whose flag is 0, in order.
+hipError_t launch_compact_rows(const void *src, void *dst, const float *xn_src, float *xn_dst,
+                               const int32_t *dst_index, int64_t n, int64_t row_bytes,
+                               hipStream_t st);
+
+// k-means update helpers
+hipError_t launch_kmeans_update(const float *x, int64_t ld, int64_t d, int64_t n,
+                                const int32_t *order, const int32_t *offsets, int64_t K,
+                                const int32_t *counts, int64_t min_points, float *cen_out,
+                                hipStream_t st);
+
+// Exact fp64 argmin over a shortlist; flags points whose shortlist cannot be
+// proven to contain the argmin (then the caller runs the exhaustive path).
+hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, const float *cen,
+                              int64_t K, const float *cand_v, const int32_t *cand_i,
+                              const ScanPlan &plan, float bound, const float *qf, int32_t *assign,
+                              double *best_sq, int32_t *fallback_count, int32_t *fallback_list,
+                              hipStream_t st);
+
+hipError_t launch_kmeans_count(const int32_t *assign, int64_t n, int32_t *counts, hipStream_t st);
+
+// Stable sort of (key, value) int32 pairs by key (rocPRIM radix sort).
+// Call with tmp == nullptr to query tmp_bytes.
+hipError_t sort_pairs_by_key(void *tmp, size_t &tmp_bytes, const int32_t *kin, int32_t *kout,
+                             const int32_t *vin, int32_t *vout, int64_t n, int key_bits,
+                             hipStream_t st);
+
+hipError_t launch_kmeans_exhaustive(const float *x, int64_t ld, int64_t d, const float *cen,
+                                    int64_t K, const int32_t *list, int64_t m, int32_t *assign,
+                                    double *best_sq, hipStream_t st);
+
+hipError_t launch_gen_normal(void *dst, int out_dtype, int64_t n, int64_t d, uint64_t seed,
+                             uint64_t stream, int normalize, hipStream_t st);
+
+// Shape rules shared by the host planner and the kernels.
+int64_t storage_ld(int64_t d, int storage);  // elements per stored row
+size_t scan_lds_bytes(int bn, int planes, int64_t ld, int cap);
+
+}  // namespace vs

@@ -1,0 +1,1241 @@
+// vs_kernels.hip -- gfx950 kernels of libvs_hip.so.
+//
+// Build with -ffp-contract=off: the exact re-rank kernels reproduce the
+// reference's separate fp64 multiply and add (index_flat.dart:78-88); a
+// fused multiply-add would change the L2 sums.
+//
+// Data layout in HBM (one index):
+//   xb  [cap][ld]  storage rows (fp32 or bf16), row bytes a multiple of 256,
+//                  rows past ntotal zero, cap a multiple of 256;
+//   xn  [cap]      fp32 of the fp64 sum of squares of each stored row.
+// Distance accumulator ("acc space", smaller is better for both metrics):
+//   L2: xn[r] - 2 q.x[r]      (the query's own |q|^2 is a per-query constant)
+//   IP: -q.x[r]
+// The MFMA B operand holds bf16 planes of s*q with s = -2 (L2) or -1 (IP);
+// fp32 rows are split in registers into bf16 hi + lo, so an fp32 dot is
+// hi*q0 + lo*q0 (+ hi*q1 when the query needs a second plane).
+#include <float.h>
+#include <limits.h>
+#include <math.h>
+
+#include "vs_internal.h"
+
+namespace vs {
+
+#define VS_INF __builtin_huge_valf()
+
+// Lane-group synchronisation for data exchanged through LDS or global
+// memory between lanes of one wave (all waves of a workgroup share the CU's
+// L1, so workgroup-scope fences order both).
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+template <typename T>
+__device__ __forceinline__ float load_f32(const T *p, int64_t i);
+template <>
+__device__ __forceinline__ float load_f32<float>(const float *p, int64_t i) {
+    return p[i];
+}
+template <>
+__device__ __forceinline__ float load_f32<uint16_t>(const uint16_t *p, int64_t i) {
+    return bf16_to_f32(p[i]);
+}
+
+int64_t storage_ld(int64_t d, int storage) {
+    const int64_t es = storage == 1 ? 2 : 4;
+    const int64_t bytes = ((d * es + kRowAlignBytes - 1) / kRowAlignBytes) * kRowAlignBytes;
+    return bytes / es;
+}
+
+// ---------------------------------------------------------------------------
+// Row storage: convert / pad / norms / flags.  One wave per row.
+// ---------------------------------------------------------------------------
+template <typename TS, typename TD>
+__global__ __launch_bounds__(256) void store_rows_kernel(const TS *__restrict__ src,
+                                                         int64_t src_stride, int64_t n, int64_t d,
+                                                         TD *__restrict__ dst, int64_t ld,
+                                                         float *__restrict__ xn, uint32_t *flags) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= n) return;
+    double ss = 0.0;
+    uint32_t f = 0;
+    for (int64_t j = lane; j < ld; j += 64) {
+        const float v = j < d ? load_f32(src, row * src_stride + j) : 0.0f;
+        if (!__builtin_isfinite(v)) f |= kFlagNonFinite;
+        const uint16_t h = f32_to_bf16_rne(v);
+        if (bf16_to_f32(h) != v) f |= kFlagNotBf16;
+        float stored;
+        if constexpr (sizeof(TD) == 2) {
+            dst[row * ld + j] = h;
+            stored = bf16_to_f32(h);
+        } else {
+            dst[row * ld + j] = v;
+            stored = v;
+        }
+        ss += (double)stored * (double)stored;
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        ss += __shfl_xor(ss, o);
+        f |= __shfl_xor(f, o);
+    }
+    if (lane == 0) {
+        xn[row] = (float)ss;
+        if (f) atomicOr(flags, f);
+    }
+}
+
+hipError_t launch_store_rows(const void *src, int src_dtype, int64_t src_stride, int64_t n,
+                             int64_t d, void *dst, int dst_dtype, int64_t ld, float *xn,
+                             uint32_t *flags, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    const dim3 grid((unsigned)((n + 3) / 4)), block(256);
+    if (src_dtype == 0 && dst_dtype == 0)
+        store_rows_kernel<float, float><<<grid, block, 0, st>>>((const float *)src, src_stride, n,
+                                                                d, (float *)dst, ld, xn, flags);
+    else if (src_dtype == 0 && dst_dtype == 1)
+        store_rows_kernel<float, uint16_t><<<grid, block, 0, st>>>(
+            (const float *)src, src_stride, n, d, (uint16_t *)dst, ld, xn, flags);
+    else if (src_dtype == 1 && dst_dtype == 0)
+        store_rows_kernel<uint16_t, float><<<grid, block, 0, st>>>(
+            (const uint16_t *)src, src_stride, n, d, (float *)dst, ld, xn, flags);
+    else
+        store_rows_kernel<uint16_t, uint16_t><<<grid, block, 0, st>>>(
+            (const uint16_t *)src, src_stride, n, d, (uint16_t *)dst, ld, xn, flags);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Query preparation.  One wave per (padded) query row.
+// ---------------------------------------------------------------------------
+template <typename TS>
+__global__ __launch_bounds__(256) void prep_queries_kernel(const TS *__restrict__ src,
+                                                           int64_t src_stride, int64_t nq,
+                                                           int64_t nq_pad, int64_t d, int64_t ld,
+                                                           float scale, uint16_t *__restrict__ qp,
+                                                           float *__restrict__ qf,
+                                                           float *__restrict__ qnorm,
+                                                           uint32_t *flags) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= nq_pad) return;
+    const bool valid = row < nq;
+    double ss = 0.0;
+    uint32_t f = 0;
+    for (int64_t j = lane; j < ld; j += 64) {
+        const bool in = valid && j < d;
+        const float v = in ? load_f32(src, row * src_stride + j) : 0.0f;
+        if (in) {
+            qf[row * d + j] = v;
+            if (!__builtin_isfinite(v)) f |= kFlagNonFinite;
+        }
+        ss += (double)v * (double)v;
+        const float s = v * scale;  // scale is -1 or -2: exact
+        const uint16_t h0 = f32_to_bf16_rne(s);
+        const uint16_t h1 = f32_to_bf16_rne(s - bf16_to_f32(h0));
+        if (h1 & 0x7FFFu) f |= kFlagNotBf16;
+        qp[(row * 2 + 0) * ld + j] = h0;
+        qp[(row * 2 + 1) * ld + j] = h1;
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        ss += __shfl_xor(ss, o);
+        f |= __shfl_xor(f, o);
+    }
+    if (lane == 0) {
+        if (valid) qnorm[row] = (float)sqrt(ss);
+        if (f) atomicOr(flags, f);
+    }
+}
+
+hipError_t launch_prepare_queries(const void *src, int src_dtype, int64_t src_stride, int64_t nq,
+                                  int64_t d, int64_t ld, int metric, const PreparedQueries &pq,
+                                  uint32_t *flags, hipStream_t st) {
+    if (pq.nq_pad <= 0) return hipSuccess;
+    const float scale = metric == 0 ? -2.0f : -1.0f;
+    const dim3 grid((unsigned)((pq.nq_pad + 3) / 4)), block(256);
+    if (src_dtype == 0)
+        prep_queries_kernel<float><<<grid, block, 0, st>>>((const float *)src, src_stride, nq,
+                                                           pq.nq_pad, d, ld, scale, pq.qp, pq.qf,
+                                                           pq.qnorm, flags);
+    else
+        prep_queries_kernel<uint16_t><<<grid, block, 0, st>>>((const uint16_t *)src, src_stride,
+                                                              nq, pq.nq_pad, d, ld, scale, pq.qp,
+                                                              pq.qf, pq.qnorm, flags);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Wave-level bitonic sort of (v, i) pairs in LDS, ascending by (v, i).
+// ---------------------------------------------------------------------------
+__device__ void bitonic_sort_wave(float *sv, int *si, int n, int lane) {
+    for (int size = 2; size <= n; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int t = lane; t < (n >> 1); t += 64) {
+                const int i = 2 * t - (t & (stride - 1));
+                const int j = i + stride;
+                const bool asc = (i & size) == 0;
+                const float vi = sv[i], vj = sv[j];
+                const int ii = si[i], ij = si[j];
+                const bool gt = vi > vj || (vi == vj && ii > ij);
+                if (gt == asc) {
+                    sv[i] = vj;
+                    sv[j] = vi;
+                    si[i] = ij;
+                    si[j] = ii;
+                }
+            }
+            wave_sync();
+        }
+    }
+}
+
+// Block-level bitonic sort (blockDim.x threads) of n (power of two) pairs.
+__device__ void bitonic_sort_block(float *sv, int *si, int n) {
+    for (int size = 2; size <= n; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int t = threadIdx.x; t < (n >> 1); t += blockDim.x) {
+                const int i = 2 * t - (t & (stride - 1));
+                const int j = i + stride;
+                const bool asc = (i & size) == 0;
+                const float vi = sv[i], vj = sv[j];
+                const int ii = si[i], ij = si[j];
+                const bool gt = vi > vj || (vi == vj && ii > ij);
+                if (gt == asc) {
+                    sv[i] = vj;
+                    sv[j] = vi;
+                    si[i] = ij;
+                    si[j] = ii;
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// The fused distance scan.
+//
+// Grid: one workgroup per (query block, database split), 4 waves.  The
+// block's bn queries sit in LDS as bf16 planes; each wave streams its own
+// tiles of 16*TM database rows straight from HBM into MFMA A operands
+// (16-byte loads; for bf16 rows, 4 lanes x 16 B = 64 contiguous bytes of a
+// row per K-step) and multiplies them by all bn queries with
+// v_mfma_f32_16x16x32_bf16.
+//
+// Operand layout of v_mfma_f32_16x16x32_bf16 as used here (lane l, r = l%16,
+// g = l/16): A lane holds row r, K elements 8g..8g+7; B lane holds query r,
+// the same K elements; D lane holds rows 4g..4g+3 of query r.  A and B use
+// the same K assignment, so the dot product does not depend on how the
+// hardware orders K inside the instruction.
+//
+// MODE 0 (top-k): every accumulator below the wave's per-query threshold is
+// appended to a per-(wave, query) list in global memory; a list nearing its
+// capacity is sorted by the wave and cut to its kk best, which also tightens
+// the threshold.  Nothing else of the distance matrix is written.
+// MODE 1 (range): accumulators within the per-query bound are appended to a
+// global (query, id) candidate list for exact re-testing.
+// ---------------------------------------------------------------------------
+struct ScanKArgs {
+    const void *xb;
+    int64_t ld;
+    const float *xn;
+    int64_t n;
+    const uint16_t *qp;
+    int64_t nq;
+    int64_t nqblk, nsplit, rows_per_split;
+    int kk, cap, metric;
+    float *cand_v;
+    int32_t *cand_i;
+    const float *athr;
+    int self_join;
+    int32_t *out_q, *out_i;
+    unsigned long long *count;
+    int64_t out_cap;
+};
+
+size_t scan_lds_bytes(int bn, int planes, int64_t ld, int cap) {
+    return (size_t)bn * planes * (size_t)(ld + 8) * 2 + (size_t)4 * bn * 8 + (size_t)4 * cap * 8;
+}
+
+// Flush one (wave, query) list: sort, keep the kk best, set count/threshold.
+__device__ void flush_list(float *cvq, int32_t *ciq, int *cnt_q, float *thr_q, float *sv, int *si,
+                           int cap, int kk, int lane) {
+    const int c = *cnt_q;
+    for (int j = lane; j < cap; j += 64) {
+        const bool in = j < c;
+        sv[j] = in ? cvq[j] : VS_INF;
+        si[j] = in ? ciq[j] : INT_MAX;
+    }
+    wave_sync();
+    bitonic_sort_wave(sv, si, cap, lane);
+    const int keep = c < kk ? c : kk;
+    for (int j = lane; j < kk; j += 64) {
+        cvq[j] = j < keep ? sv[j] : VS_INF;
+        ciq[j] = j < keep ? si[j] : -1;
+    }
+    wave_sync();
+    if (lane == 0) {
+        *cnt_q = keep;
+        *thr_q = c >= kk ? sv[kk - 1] : VS_INF;
+    }
+    wave_sync();
+}
+
+typedef float f32x8_t __attribute__((ext_vector_type(8)));
+struct U8x2 {
+    uint4 a, b;
+};
+
+__device__ __forceinline__ f32x4_t mfma_bf16(bf16x8_t a, bf16x8_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Maps a flat block index to (split, query block) so that the query blocks
+// of one split land on the same XCD (blocks are dealt to the 8 XCDs round-
+// robin) back to back: they read the same database rows at about the same
+// time and share that XCD's L2.
+__device__ __forceinline__ bool map_block(int64_t nqblk, int64_t nsplit, int64_t *split,
+                                          int64_t *qblk) {
+    const int64_t total = nqblk * nsplit;
+    const int64_t per_xcd = (total + 7) / 8;
+    const int64_t w = (int64_t)(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (w >= total) return false;
+    *split = w / nqblk;
+    *qblk = w % nqblk;
+    return true;
+}
+
+template <int ST, int PQ, int NQB, int TM, int MODE>
+__global__ __launch_bounds__(256) void scan_kernel(ScanKArgs a) {
+    extern __shared__ __align__(16) char smem[];
+    constexpr int BN = 16 * NQB;
+    constexpr int UK = ST == 1 ? 4 : 2;  // K-steps per load batch
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r16 = lane & 15, g = lane >> 4;
+
+    int64_t split, qblk;
+    if (!map_block(a.nqblk, a.nsplit, &split, &qblk)) return;
+    int64_t r0 = split * a.rows_per_split;
+    const int64_t r1 = min(a.n, r0 + a.rows_per_split);
+    if (MODE == 1 && a.self_join) r0 = max(r0, qblk * BN);  // only ids > query
+    if (r0 >= r1) return;
+
+    const int64_t ldp = a.ld + 8;
+    uint16_t *qs = (uint16_t *)smem;  // [BN][PQ][ldp]
+    int *cnt = (int *)(smem + (size_t)BN * PQ * ldp * 2);
+    float *thr = (float *)(cnt + 4 * BN);
+    float *sv = thr + 4 * BN;
+    int *si = (int *)(sv + 4 * a.cap);
+
+    const int64_t q0 = qblk * BN;
+    {
+        const int64_t cpr = a.ld / 8;  // 16-byte chunks per plane row
+        const int64_t nch = (int64_t)BN * PQ * cpr;
+        for (int64_t c = threadIdx.x; c < nch; c += 256) {
+            const int64_t row = c / cpr, ch = c % cpr;
+            const int64_t q = row / PQ, p = row % PQ;
+            const uint4 v = *(const uint4 *)(a.qp + ((q0 + q) * 2 + p) * a.ld + ch * 8);
+            *(uint4 *)(qs + row * ldp + ch * 8) = v;
+        }
+        for (int t = threadIdx.x; t < 4 * BN; t += 256) {
+            cnt[t] = 0;
+            thr[t] = q0 + (t % BN) < a.nq ? VS_INF : -VS_INF;
+        }
+    }
+    __syncthreads();
+
+    int *cnt_w = cnt + wave * BN;
+    float *thr_w = thr + wave * BN;
+    float *sv_w = sv + wave * a.cap;
+    int *si_w = si + wave * a.cap;
+    const int64_t list_base = ((qblk * a.nsplit + split) * 4 + wave) * (int64_t)BN * a.cap;
+    float *cv = MODE == 0 ? a.cand_v + list_base : nullptr;
+    int32_t *ci = MODE == 0 ? a.cand_i + list_base : nullptr;
+
+    float thr_r[NQB];
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) {
+        const int64_t qg = q0 + qb * 16 + r16;
+        if (MODE == 0)
+            thr_r[qb] = thr_w[qb * 16 + r16];
+        else
+            thr_r[qb] = qg < a.nq ? a.athr[qg] : -VS_INF;
+    }
+
+    const int nks = (int)(a.ld / 32);
+    const int64_t row_bytes = a.ld * (ST == 1 ? 2 : 4);
+    const char *xbase = (const char *)a.xb + (ST == 1 ? g * 16 : g * 32);
+    const uint16_t *qlane = qs + (int64_t)r16 * PQ * ldp + 8 * g;
+
+    for (int64_t t0 = r0 + wave * 16 * TM; t0 < r1; t0 += 64 * TM) {
+        f32x4_t acc[TM][NQB];
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) {
+            f32x4_t init = {0.f, 0.f, 0.f, 0.f};
+            if (a.metric == 0) init = *(const f32x4_t *)(a.xn + t0 + tm * 16 + 4 * g);
+#pragma unroll
+            for (int qb = 0; qb < NQB; ++qb) acc[tm][qb] = init;
+        }
+        const char *rowp[TM];
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) rowp[tm] = xbase + (t0 + tm * 16 + r16) * row_bytes;
+
+        if constexpr (ST == 1) {
+            uint4 cur[UK][TM], nxt[UK][TM];
+#pragma unroll
+            for (int u = 0; u < UK; ++u)
+#pragma unroll
+                for (int tm = 0; tm < TM; ++tm) cur[u][tm] = *(const uint4 *)(rowp[tm] + u * 64);
+            for (int ks = 0; ks < nks; ks += UK) {
+                if (ks + UK < nks) {
+#pragma unroll
+                    for (int u = 0; u < UK; ++u)
+#pragma unroll
+                        for (int tm = 0; tm < TM; ++tm)
+                            nxt[u][tm] = *(const uint4 *)(rowp[tm] + (int64_t)(ks + UK + u) * 64);
+                }
+#pragma unroll
+                for (int u = 0; u < UK; ++u) {
+#pragma unroll
+                    for (int qb = 0; qb < NQB; ++qb) {
+                        const uint16_t *qrow = qlane + (int64_t)qb * 16 * PQ * ldp + (ks + u) * 32;
+                        const bf16x8_t b0 = __builtin_bit_cast(bf16x8_t, *(const uint4 *)qrow);
+#pragma unroll
+                        for (int tm = 0; tm < TM; ++tm)
+                            acc[tm][qb] =
+                                mfma_bf16(__builtin_bit_cast(bf16x8_t, cur[u][tm]), b0, acc[tm][qb]);
+                        if constexpr (PQ == 2) {
+                            const bf16x8_t b1 =
+                                __builtin_bit_cast(bf16x8_t, *(const uint4 *)(qrow + ldp));
+#pragma unroll
+                            for (int tm = 0; tm < TM; ++tm)
+                                acc[tm][qb] = mfma_bf16(__builtin_bit_cast(bf16x8_t, cur[u][tm]),
+                                                        b1, acc[tm][qb]);
+                        }
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < UK; ++u)
+#pragma unroll
+                    for (int tm = 0; tm < TM; ++tm) cur[u][tm] = nxt[u][tm];
+            }
+        } else {
+            U8x2 cur[UK][TM], nxt[UK][TM];
+#pragma unroll
+            for (int u = 0; u < UK; ++u)
+#pragma unroll
+                for (int tm = 0; tm < TM; ++tm) {
+                    cur[u][tm].a = *(const uint4 *)(rowp[tm] + u * 128);
+                    cur[u][tm].b = *(const uint4 *)(rowp[tm] + u * 128 + 16);
+                }
+            for (int ks = 0; ks < nks; ks += UK) {
+                if (ks + UK < nks) {
+#pragma unroll
+                    for (int u = 0; u < UK; ++u)
+#pragma unroll
+                        for (int tm = 0; tm < TM; ++tm) {
+                            const char *p = rowp[tm] + (int64_t)(ks + UK + u) * 128;
+                            nxt[u][tm].a = *(const uint4 *)p;
+                            nxt[u][tm].b = *(const uint4 *)(p + 16);
+                        }
+                }
+#pragma unroll
+                for (int u = 0; u < UK; ++u) {
+                    bf16x8_t hi[TM], lo[TM];
+#pragma unroll
+                    for (int tm = 0; tm < TM; ++tm) {
+                        const f32x8_t v = __builtin_bit_cast(f32x8_t, cur[u][tm]);
+                        hi[tm] = __builtin_convertvector(v, bf16x8_t);
+                        lo[tm] = __builtin_convertvector(v - __builtin_convertvector(hi[tm], f32x8_t),
+                                                         bf16x8_t);
+                    }
+#pragma unroll
+                    for (int qb = 0; qb < NQB; ++qb) {
+                        const uint16_t *qrow = qlane + (int64_t)qb * 16 * PQ * ldp + (ks + u) * 32;
+                        const bf16x8_t b0 = __builtin_bit_cast(bf16x8_t, *(const uint4 *)qrow);
+#pragma unroll
+                        for (int tm = 0; tm < TM; ++tm) {
+                            acc[tm][qb] = mfma_bf16(hi[tm], b0, acc[tm][qb]);
+                            acc[tm][qb] = mfma_bf16(lo[tm], b0, acc[tm][qb]);
+                        }
+                        if constexpr (PQ == 2) {
+                            const bf16x8_t b1 =
+                                __builtin_bit_cast(bf16x8_t, *(const uint4 *)(qrow + ldp));
+#pragma unroll
+                            for (int tm = 0; tm < TM; ++tm)
+                                acc[tm][qb] = mfma_bf16(hi[tm], b1, acc[tm][qb]);
+                        }
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < UK; ++u)
+#pragma unroll
+                    for (int tm = 0; tm < TM; ++tm) cur[u][tm] = nxt[u][tm];
+            }
+        }
+
+        // ---- epilogue ----
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) {
+            const int64_t rbase = t0 + tm * 16 + 4 * g;
+            if constexpr (MODE == 0) {
+                // make room: any list of this wave that a 16-row block could
+                // overflow is cut back to its kk best first
+                bool need = false;
+                if (g == 0) {
+#pragma unroll
+                    for (int qb = 0; qb < NQB; ++qb) need |= cnt_w[qb * 16 + r16] > a.cap - 16;
+                }
+                if (__ballot(need)) {
+                    for (int q = 0; q < BN; ++q) {
+                        if (cnt_w[q] > a.cap - 16)
+                            flush_list(cv + (int64_t)q * a.cap, ci + (int64_t)q * a.cap, &cnt_w[q],
+                                       &thr_w[q], sv_w, si_w, a.cap, a.kk, lane);
+                    }
+#pragma unroll
+                    for (int qb = 0; qb < NQB; ++qb) thr_r[qb] = thr_w[qb * 16 + r16];
+                }
+#pragma unroll
+                for (int qb = 0; qb < NQB; ++qb) {
+                    const int q = qb * 16 + r16;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int64_t row = rbase + i;
+                        const float v = acc[tm][qb][i];
+                        if (row < r1 && v < thr_r[qb]) {
+                            const int pos = atomicAdd(&cnt_w[q], 1);
+                            cv[(int64_t)q * a.cap + pos] = v;
+                            ci[(int64_t)q * a.cap + pos] = (int32_t)row;
+                        }
+                    }
+                }
+                wave_sync();
+            } else {
+#pragma unroll
+                for (int qb = 0; qb < NQB; ++qb) {
+                    const int64_t qg = q0 + qb * 16 + r16;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int64_t row = rbase + i;
+                        const float v = acc[tm][qb][i];
+                        if (row < r1 && v <= thr_r[qb] && (!a.self_join || row > qg)) {
+                            const unsigned long long pos = atomicAdd(a.count, 1ull);
+                            if (pos < (unsigned long long)a.out_cap) {
+                                a.out_q[pos] = (int32_t)qg;
+                                a.out_i[pos] = (int32_t)row;
+                            }
+                        }
+                    }
+                }
+            }
+        }
+    }
+
+    if constexpr (MODE == 0) {
+        // final: every list holds its kk best in slots [0, kk), padded
+        wave_sync();
+        for (int q = 0; q < BN; ++q) {
+            const int c = cnt_w[q];
+            if (c > a.kk) {
+                flush_list(cv + (int64_t)q * a.cap, ci + (int64_t)q * a.cap, &cnt_w[q], &thr_w[q],
+                           sv_w, si_w, a.cap, a.kk, lane);
+            } else {
+                for (int j = c + lane; j < a.kk; j += 64) {
+                    cv[(int64_t)q * a.cap + j] = VS_INF;
+                    ci[(int64_t)q * a.cap + j] = -1;
+                }
+            }
+        }
+    }
+}
+
+template <int MODE>
+static hipError_t launch_scan_mode(const void *xb, int storage, int64_t ld, const float *xn,
+                                   int64_t n, const PreparedQueries &pq, const ScanPlan &plan,
+                                   const ScanKArgs &args, hipStream_t st) {
+    (void)xb;
+    (void)ld;
+    (void)xn;
+    (void)n;
+    const int64_t total = plan.nqblk * plan.nsplit;
+    const int64_t grid = ((total + 7) / 8) * 8;
+    const size_t lds = plan.lds_bytes;
+    void (*fn)(ScanKArgs) = nullptr;
+    const int nqb = plan.bn / 16;
+#define VS_PICK(ST_, PQ_, NQB_, TM_)                                                     \
+    if (storage == ST_ && pq.planes == PQ_ && nqb == NQB_ && plan.tm == TM_) \
+        fn = scan_kernel<ST_, PQ_, NQB_, TM_, MODE>;
+#define VS_PICK_TM(ST_, PQ_, NQB_) \
+    VS_PICK(ST_, PQ_, NQB_, 1) VS_PICK(ST_, PQ_, NQB_, 2) VS_PICK(ST_, PQ_, NQB_, 4)
+#define VS_PICK_NQB(ST_, PQ_) VS_PICK_TM(ST_, PQ_, 1) VS_PICK_TM(ST_, PQ_, 2) VS_PICK_TM(ST_, PQ_, 4)
+    VS_PICK_NQB(0, 1)
+    VS_PICK_NQB(0, 2)
+    VS_PICK_NQB(1, 1)
+    VS_PICK_NQB(1, 2)
+#undef VS_PICK_NQB
+#undef VS_PICK_TM
+#undef VS_PICK
+    if (!fn) return hipErrorInvalidValue;
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute((const void *)fn,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(256), lds, st, args);
+    return hipGetLastError();
+}
+
+hipError_t launch_scan_topk(const void *xb, int storage, int64_t ld, const float *xn, int64_t n,
+                            int metric, const PreparedQueries &pq, const ScanPlan &plan,
+                            float *cand_v, int32_t *cand_i, hipStream_t st) {
+    ScanKArgs a{};
+    a.xb = xb;
+    a.ld = ld;
+    a.xn = xn;
+    a.n = n;
+    a.qp = pq.qp;
+    a.nq = pq.nq;
+    a.nqblk = plan.nqblk;
+    a.nsplit = plan.nsplit;
+    a.rows_per_split = plan.rows_per_split;
+    a.kk = plan.kk;
+    a.cap = plan.cap;
+    a.metric = metric;
+    a.cand_v = cand_v;
+    a.cand_i = cand_i;
+    return launch_scan_mode<0>(xb, storage, ld, xn, n, pq, plan, a, st);
+}
+
+hipError_t launch_scan_range(const void *xb, int storage, int64_t ld, const float *xn, int64_t n,
+                             const PreparedQueries &pq, const ScanPlan &plan, const float *athr,
+                             int self_join, int metric, int32_t *out_q, int32_t *out_i,
+                             unsigned long long *count, int64_t cap, hipStream_t st) {
+    ScanKArgs a{};
+    a.xb = xb;
+    a.ld = ld;
+    a.xn = xn;
+    a.n = n;
+    a.qp = pq.qp;
+    a.nq = pq.nq;
+    a.nqblk = plan.nqblk;
+    a.nsplit = plan.nsplit;
+    a.rows_per_split = plan.rows_per_split;
+    a.kk = plan.kk;
+    a.cap = plan.cap;
+    a.metric = metric;
+    a.athr = athr;
+    a.self_join = self_join;
+    a.out_q = out_q;
+    a.out_i = out_i;
+    a.count = count;
+    a.out_cap = cap;
+    return launch_scan_mode<1>(xb, storage, ld, xn, n, pq, plan, a, st);
+}
+
+// ---------------------------------------------------------------------------
+// Exact score of (query, row) in the reference's arithmetic: fp64 sum over
+// j = 0..d-1 in order of q[j]*x[j] (IP) or (q[j]-x[j])^2 (L2), with the fp32
+// values promoted to fp64 (index_flat.dart:78-88; index.dart:181-200).
+// Rows are zero past d and so is q (qrow must hold ld values, zero past d):
+// the extra terms add +0.0 to the sum.
+// ---------------------------------------------------------------------------
+template <int ST>
+__device__ double exact_score(const float *qrow, const void *xb, int64_t ld, int64_t id,
+                              int64_t d, int metric) {
+    double s = 0.0;
+    const int64_t dend = (d + 7) & ~(int64_t)7;
+    if constexpr (ST == 1) {
+        const uint16_t *x = (const uint16_t *)xb + id * ld;
+        for (int64_t j = 0; j < dend; j += 8) {
+            const uint4 raw = *(const uint4 *)(x + j);
+            const uint16_t *h = (const uint16_t *)&raw;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const double xv = (double)bf16_to_f32(h[u]);
+                const double qv = (double)qrow[j + u];
+                if (metric == 0) {
+                    const double diff = qv - xv;
+                    s = s + diff * diff;
+                } else {
+                    s = s + qv * xv;
+                }
+            }
+        }
+    } else {
+        const float *x = (const float *)xb + id * ld;
+        for (int64_t j = 0; j < dend; j += 4) {
+            const float4 raw = *(const float4 *)(x + j);
+            const float xs[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const double xv = (double)xs[u];
+                const double qv = (double)qrow[j + u];
+                if (metric == 0) {
+                    const double diff = qv - xv;
+                    s = s + diff * diff;
+                } else {
+                    s = s + qv * xv;
+                }
+            }
+        }
+    }
+    return s;
+}
+
+// ---------------------------------------------------------------------------
+// Merge + exact re-rank.  One workgroup (256 threads) per query.
+//   1. stream the query's per-wave lists, keeping entries that beat the
+//      current kk-th best, sorting when the LDS buffer fills;
+//   2. score the kk survivors exactly in fp64;
+//   3. MODE 0: sort by (fp32 score, id), write the k best with sentinels
+//      (index.dart:306-313).  MODE 1 (k-means argmin): strict-'<' argmin in
+//      id order over the exact scores (kmeans.dart:93-101) plus the proof
+//      that no centroid outside the shortlist can beat it.
+// ---------------------------------------------------------------------------
+struct MergeKArgs {
+    const void *xb;
+    int64_t ld, d;
+    int metric;
+    const float *qf;
+    int64_t nq;
+    int bn, kk, cap;
+    int64_t nsplit;
+    const float *cand_v;
+    const int32_t *cand_i;
+    int64_t k;
+    float *D;
+    int32_t *I;
+    // k-means argmin mode
+    float bound;
+    int32_t *assign;
+    double *best_sq;
+    int32_t *fb_count;
+    int32_t *fb_list;
+};
+
+constexpr int kMergeBuf = 2048;
+
+template <int ST, int MODE>
+__global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
+    extern __shared__ __align__(16) char smem[];
+    float *bv = (float *)smem;                  // [kMergeBuf]
+    int *bi = (int *)(bv + kMergeBuf);          // [kMergeBuf]
+    float *qsh = (float *)(bi + kMergeBuf);     // [ld]
+    __shared__ int s_cnt;
+    __shared__ float s_thr;
+    __shared__ int s_thr_id;
+
+    const int64_t qg = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int kk = a.kk;
+    const int64_t qblk = qg / a.bn, q = qg % a.bn;
+    const int64_t nlists = a.nsplit * 4;
+    const int64_t total = nlists * kk;
+
+    for (int t = tid; t < kk; t += 256) {
+        bv[t] = VS_INF;
+        bi[t] = INT_MAX;
+    }
+    if (tid == 0) {
+        s_cnt = 0;
+        s_thr = VS_INF;
+        s_thr_id = INT_MAX;
+    }
+    for (int64_t j = tid; j < a.ld; j += 256) qsh[j] = j < a.d ? a.qf[qg * a.d + j] : 0.0f;
+    __syncthreads();
+
+    for (int64_t base = 0; base < total; base += 256) {
+        const int64_t e = base + tid;
+        if (e < total) {
+            const int64_t list = e / kk, j = e % kk;
+            const int64_t split = list >> 2, w = list & 3;
+            const int64_t off = (((qblk * a.nsplit + split) * 4 + w) * a.bn + q) * a.cap + j;
+            const float v = a.cand_v[off];
+            const int id = a.cand_i[off];
+            if (id >= 0 && (v < s_thr || (v == s_thr && id < s_thr_id))) {
+                const int pos = atomicAdd(&s_cnt, 1);
+                bv[kk + pos] = v;
+                bi[kk + pos] = id;
+            }
+        }
+        __syncthreads();
+        const int c = s_cnt;
+        if (c > kMergeBuf - kk - 256 || (base + 256 >= total && c > 0)) {
+            int sz = 1;
+            while (sz < kk + c) sz <<= 1;
+            for (int t = kk + c + tid; t < sz; t += 256) {
+                bv[t] = VS_INF;
+                bi[t] = INT_MAX;
+            }
+            __syncthreads();
+            bitonic_sort_block(bv, bi, sz);
+            if (tid == 0) {
+                s_cnt = 0;
+                s_thr = bv[kk - 1];
+                s_thr_id = bi[kk - 1];
+            }
+            __syncthreads();
+        }
+    }
+
+    // exact re-rank of the kk survivors (slots [0, kk), sentinel id INT_MAX);
+    // each thread rewrites only its own slots: (key, id) with key = score
+    // (L2) or -score (IP), so ascending order is best-first
+    double best_ex = __builtin_huge_val();
+    int best_id = INT_MAX;
+    float a_last = 0.f;
+    if constexpr (MODE == 1) a_last = bv[kk - 1];
+    __syncthreads();
+    for (int t = tid; t < kk; t += 256) {
+        const int id = bi[t];
+        float key = VS_INF;
+        if (id != INT_MAX) {
+            const double ex = exact_score<ST>(qsh, a.xb, a.ld, id, a.d, a.metric);
+            key = a.metric == 0 ? (float)ex : -(float)ex;
+            if (MODE == 1 && (ex < best_ex || (ex == best_ex && id < best_id))) {
+                best_ex = ex;
+                best_id = id;
+            }
+        }
+        bv[t] = key;
+    }
+    __syncthreads();
+
+    if constexpr (MODE == 0) {
+        bitonic_sort_block(bv, bi, kk);
+        for (int64_t t = tid; t < a.k; t += 256) {
+            const bool ok = t < kk && bi[t] != INT_MAX;
+            a.D[qg * a.k + t] = ok ? (a.metric == 0 ? bv[t] : -bv[t])
+                                   : (a.metric == 0 ? VS_INF : -VS_INF);
+            a.I[qg * a.k + t] = ok ? bi[t] : -1;
+        }
+    } else {
+        // argmin over (exact score, id): smallest score, lowest id among
+        // equals -- the strict '<' scan in centroid order (kmeans.dart:96-101)
+        double *dsh = (double *)bv;  // bv is free again: 256 doubles fit
+        int *ish = bi;
+        __syncthreads();
+        dsh[tid] = best_ex;
+        ish[tid] = best_id;
+        __syncthreads();
+        for (int s = 128; s > 0; s >>= 1) {
+            if (tid < s) {
+                const double v1 = dsh[tid + s];
+                const int i1 = ish[tid + s];
+                if (v1 < dsh[tid] || (v1 == dsh[tid] && i1 < ish[tid])) {
+                    dsh[tid] = v1;
+                    ish[tid] = i1;
+                }
+            }
+            __syncthreads();
+        }
+        if (tid == 0) {
+            const double best = dsh[0];
+            const int bid = ish[0];
+            // the shortlist holds the argmin if every centroid outside it is
+            // provably worse: its accumulator is >= a_last, and accumulators
+            // are within `bound` of xn[c] - 2 x.c = score - |x|^2
+            double xx = 0.0;
+            for (int64_t j = 0; j < a.d; ++j) xx = xx + (double)qsh[j] * (double)qsh[j];
+            const double acc_best = best - xx;
+            const bool safe = a_last == VS_INF ||
+                              (double)a_last - (double)a.bound > acc_best + 1e-9 * (fabs(xx) + 1.0);
+            a.assign[qg] = bid;
+            a.best_sq[qg] = best;
+            if (!safe) {
+                const int pos = atomicAdd(a.fb_count, 1);
+                a.fb_list[pos] = (int32_t)qg;
+            }
+        }
+    }
+}
+
+static size_t merge_lds(int64_t ld) { return (size_t)kMergeBuf * 8 + (size_t)ld * 4; }
+
+hipError_t launch_merge_refine(const void *xb, int storage, int64_t ld, int64_t d, int metric,
+                               const PreparedQueries &pq, const ScanPlan &plan,
+                               const float *cand_v, const int32_t *cand_i, int64_t k, float *D,
+                               int32_t *I, hipStream_t st) {
+    if (pq.nq <= 0) return hipSuccess;
+    MergeKArgs a{};
+    a.xb = xb;
+    a.ld = ld;
+    a.d = d;
+    a.metric = metric;
+    a.qf = pq.qf;
+    a.nq = pq.nq;
+    a.bn = plan.bn;
+    a.kk = plan.kk;
+    a.cap = plan.cap;
+    a.nsplit = plan.nsplit;
+    a.cand_v = cand_v;
+    a.cand_i = cand_i;
+    a.k = k;
+    a.D = D;
+    a.I = I;
+    const size_t lds = merge_lds(ld);
+    void (*fn)(MergeKArgs) = storage == 1 ? merge_refine_kernel<1, 0> : merge_refine_kernel<0, 0>;
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute((const void *)fn,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(fn, dim3((unsigned)pq.nq), dim3(256), lds, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, const float *cen,
+                              int64_t K, const float *cand_v, const int32_t *cand_i,
+                              const ScanPlan &plan, float bound, const float *qf, int32_t *assign,
+                              double *best_sq, int32_t *fallback_count, int32_t *fallback_list,
+                              hipStream_t st) {
+    (void)x;
+    (void)K;
+    if (n <= 0) return hipSuccess;
+    MergeKArgs a{};
+    a.xb = cen;
+    a.ld = ld;
+    a.d = d;
+    a.metric = 0;
+    a.qf = qf;
+    a.nq = n;
+    a.bn = plan.bn;
+    a.kk = plan.kk;
+    a.cap = plan.cap;
+    a.nsplit = plan.nsplit;
+    a.cand_v = cand_v;
+    a.cand_i = cand_i;
+    a.bound = bound;
+    a.assign = assign;
+    a.best_sq = best_sq;
+    a.fb_count = fallback_count;
+    a.fb_list = fallback_list;
+    const size_t lds = merge_lds(ld);
+    void (*fn)(MergeKArgs) = merge_refine_kernel<0, 1>;
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute((const void *)fn,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(fn, dim3((unsigned)n), dim3(256), lds, st, a);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// k-means exhaustive exact argmin for points whose shortlist was not proven:
+// one workgroup per point; strict '<' in centroid order (kmeans.dart:93-101).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void kmeans_exhaustive_kernel(const float *__restrict__ x,
+                                                                int64_t ld, int64_t d,
+                                                                const float *__restrict__ cen,
+                                                                int64_t K,
+                                                                const int32_t *__restrict__ list,
+                                                                int32_t *assign,
+                                                                double *best_sq) {
+    __shared__ double dsh[256];
+    __shared__ int ish[256];
+    const int64_t p = list[blockIdx.x];
+    const float *xp = x + p * ld;
+    double best = __builtin_huge_val();
+    int bid = INT_MAX;
+    for (int64_t c = threadIdx.x; c < K; c += 256) {
+        const float *cc = cen + c * ld;
+        double s = 0.0;
+        for (int64_t j = 0; j < d; ++j) {
+            const double diff = (double)xp[j] - (double)cc[j];
+            s = s + diff * diff;
+        }
+        if (s < best) {  // c increases: keeps the lowest id among equals
+            best = s;
+            bid = (int)c;
+        }
+    }
+    dsh[threadIdx.x] = best;
+    ish[threadIdx.x] = bid;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) {
+            const double v1 = dsh[threadIdx.x + s];
+            const int i1 = ish[threadIdx.x + s];
+            if (v1 < dsh[threadIdx.x] || (v1 == dsh[threadIdx.x] && i1 < ish[threadIdx.x])) {
+                dsh[threadIdx.x] = v1;
+                ish[threadIdx.x] = i1;
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        assign[p] = ish[0];
+        best_sq[p] = dsh[0];
+    }
+}
+
+hipError_t launch_kmeans_exhaustive(const float *x, int64_t ld, int64_t d, const float *cen,
+                                    int64_t K, const int32_t *list, int64_t m, int32_t *assign,
+                                    double *best_sq, hipStream_t st) {
+    if (m <= 0) return hipSuccess;
+    kmeans_exhaustive_kernel<<<dim3((unsigned)m), dim3(256), 0, st>>>(x, ld, d, cen, K, list,
+                                                                      assign, best_sq);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// k-means update: per centroid c and dimension j, the fp32 running sum over
+// the cluster's points in increasing point order, then fp32(sum * fp64
+// 1/count) (kmeans.dart:107-126).  `order` lists point ids grouped by
+// cluster, ascending within a cluster.  One workgroup per centroid.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void kmeans_update_kernel(const float *__restrict__ x,
+                                                            int64_t ld, int64_t d,
+                                                            const int32_t *__restrict__ order,
+                                                            const int32_t *__restrict__ offsets,
+                                                            const int32_t *__restrict__ counts,
+                                                            int64_t min_points,
+                                                            float *__restrict__ cen_out) {
+    const int64_t c = blockIdx.x;
+    const int cnt = counts[c];
+    if (cnt < min_points) return;
+    const int off = offsets[c];
+    const double inv = 1.0 / (double)cnt;
+    for (int64_t j = threadIdx.x; j < d; j += blockDim.x) {
+        float s = 0.0f;
+        for (int t = 0; t < cnt; ++t) s = s + x[(int64_t)order[off + t] * ld + j];
+        cen_out[c * d + j] = (float)((double)s * inv);
+    }
+}
+
+hipError_t launch_kmeans_update(const float *x, int64_t ld, int64_t d, int64_t n,
+                                const int32_t *order, const int32_t *offsets, int64_t K,
+                                const int32_t *counts, int64_t min_points, float *cen_out,
+                                hipStream_t st) {
+    (void)n;
+    if (K <= 0) return hipSuccess;
+    kmeans_update_kernel<<<dim3((unsigned)K), dim3(256), 0, st>>>(x, ld, d, order, offsets, counts,
+                                                                  min_points, cen_out);
+    return hipGetLastError();
+}
+
+// cluster sizes (integer atomics: order-independent)
+__global__ void kmeans_count_kernel(const int32_t *__restrict__ assign, int64_t n,
+                                    int32_t *counts) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) atomicAdd(&counts[assign[i]], 1);
+}
+
+hipError_t launch_kmeans_count(const int32_t *assign, int64_t n, int32_t *counts, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    kmeans_count_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(assign, n,
+                                                                                 counts);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Range search support
+// ---------------------------------------------------------------------------
+// Acceptance bounds in accumulator space.  acc approximates
+//   L2: xn - 2 q.x = score - |q|^2      IP: -q.x = -score
+// with |acc - exact| <= err(q) = c * |q| * max|x| (+ the norm rounding for
+// L2).  The scan keeps acc <= athr, athr = exact bound + err, and the exact
+// fp64 re-test decides.
+__global__ void range_bounds_kernel(const float *__restrict__ qnorm, int64_t nq, int metric,
+                                    double radius, float xmax, float rel, float *athr) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nq) return;
+    const double qn = qnorm[i];
+    const double xm = xmax;
+    const double err =
+        metric == 0 ? (double)rel * (2.0 * qn * xm + qn * qn + xm * xm) : (double)rel * qn * xm;
+    double t;
+    if (metric == 0)
+        t = radius - qn * qn + err;
+    else
+        t = -radius + err;
+    athr[i] = (float)t + fabsf((float)t) * 1e-6f + 1e-30f;
+}
+
+hipError_t launch_range_bounds(const PreparedQueries &pq, int64_t d, int metric, double radius,
+                               float xnorm_max, int exact_q, int exact_x, float *athr,
+                               hipStream_t st) {
+    if (pq.nq <= 0) return hipSuccess;
+    // relative error of the split-bf16 dot product with fp32 accumulation:
+    // products: each operand within 2^-16 relative of its value (hi + lo),
+    // 2^-8 when a query is rounded to one bf16 plane; accumulation gamma_d.
+    const double u = 1.0 / 16777216.0;
+    double rel = 4.0 * (double)(d + 4) * u + 1.0 / 1048576.0;
+    if (!exact_x) rel += 4.0 / 65536.0;
+    if (!exact_q) rel += 4.0 / 65536.0;
+    range_bounds_kernel<<<dim3((unsigned)((pq.nq + 255) / 256)), dim3(256), 0, st>>>(
+        pq.qnorm, pq.nq, metric, radius, xnorm_max, (float)rel, athr);
+    return hipGetLastError();
+}
+
+template <int ST>
+__global__ void range_refine_kernel(const void *xb, int64_t ld, int64_t d, int metric,
+                                    const float *__restrict__ qf, const int32_t *__restrict__ cq,
+                                    const int32_t *__restrict__ ci, int64_t m, double radius,
+                                    float *__restrict__ out_s, uint8_t *__restrict__ keep) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= m) return;
+    const int64_t q = cq[t], id = ci[t];
+    const float *qrow = qf + q * d;
+    double s = 0.0;
+    for (int64_t j = 0; j < d; ++j) {
+        const double xv = ST == 1 ? (double)bf16_to_f32(((const uint16_t *)xb)[id * ld + j])
+                                  : (double)((const float *)xb)[id * ld + j];
+        const double qv = (double)qrow[j];
+        if (metric == 0) {
+            const double diff = qv - xv;
+            s = s + diff * diff;
+        } else {
+            s = s + qv * xv;
+        }
+    }
+    out_s[t] = (float)s;
+    keep[t] = metric == 0 ? (s <= radius) : (s >= radius);
+}
+
+hipError_t launch_range_refine(const void *xb, int storage, int64_t ld, int64_t d, int metric,
+                               const float *qf, const int32_t *cq, const int32_t *ci, int64_t m,
+                               double radius, float *out_s, uint8_t *keep, hipStream_t st) {
+    if (m <= 0) return hipSuccess;
+    const dim3 grid((unsigned)((m + 255) / 256)), block(256);
+    if (storage == 1)
+        range_refine_kernel<1><<<grid, block, 0, st>>>(xb, ld, d, metric, qf, cq, ci, m, radius,
+                                                       out_s, keep);
+    else
+        range_refine_kernel<0><<<grid, block, 0, st>>>(xb, ld, d, metric, qf, cq, ci, m, radius,
+                                                       out_s, keep);
+    return hipGetLastError();
+}
+
+__global__ void max_reduce_kernel(const float *__restrict__ x, int64_t n, float *out) {
+    float m = 0.0f;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        m = fmaxf(m, x[i]);
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((threadIdx.x & 63) == 0) atomicMax((unsigned int *)out, __float_as_uint(m));
+}
+
+hipError_t launch_max_reduce(const float *x, int64_t n, float *out, hipStream_t st) {
+    hipError_t e = hipMemsetAsync(out, 0, sizeof(float), st);
+    if (e != hipSuccess || n <= 0) return e;
+    max_reduce_kernel<<<dim3(1024), dim3(256), 0, st>>>(x, n, out);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// removeIds compaction (index_flat.dart:139-160): row r moves to
+// dst_index[r] (or is dropped when -1).  One wave per row.
+// ---------------------------------------------------------------------------
+__global__ void compact_rows_kernel(const char *__restrict__ src, char *__restrict__ dst,
+                                    const float *__restrict__ xn_src, float *__restrict__ xn_dst,
+                                    const int32_t *__restrict__ dst_index, int64_t n,
+                                    int64_t row_bytes) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= n) return;
+    const int64_t t = dst_index[r];
+    if (t < 0) return;
+    for (int64_t b = (int64_t)lane * 16; b < row_bytes; b += 64 * 16)
+        *(uint4 *)(dst + t * row_bytes + b) = *(const uint4 *)(src + r * row_bytes + b);
+    if (lane == 0) xn_dst[t] = xn_src[r];
+}
+
+hipError_t launch_compact_rows(const void *src, void *dst, const float *xn_src, float *xn_dst,
+                               const int32_t *dst_index, int64_t n, int64_t row_bytes,
+                               hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    compact_rows_kernel<<<dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st>>>(
+        (const char *)src, (char *)dst, xn_src, xn_dst, dst_index, n, row_bytes);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Synthetic data: Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random
+// numbers: as easy as 1, 2, 3", SC'11) keyed by the seed, counter = (element
+// group, row-major position / 4, stream); Box-Muller on pairs of uniforms.
+// One wave per row; with normalize the row is scaled by 1/sqrt(fp64 sum of
+// squares), the L2NormTransform convention (l2_norm_transform.dart:23-46).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint4 philox4x32_10(uint4 c, uint2 k) {
+    const uint32_t M0 = 0xD2511F53u, M1 = 0xCD9E8D57u, W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
+#pragma unroll
+    for (int r = 0; r < 10; ++r) {
+        const uint32_t hi0 = __umulhi(M0, c.x), lo0 = M0 * c.x;
+        const uint32_t hi1 = __umulhi(M1, c.z), lo1 = M1 * c.z;
+        c = make_uint4(hi1 ^ c.y ^ k.x, lo1, hi0 ^ c.w ^ k.y, lo0);
+        k.x += W0;
+        k.y += W1;
+    }
+    return c;
+}
+
+__device__ __forceinline__ void box_muller(uint32_t a, uint32_t b, float &z0, float &z1) {
+    const float u1 = ((float)(a >> 8) + 1.0f) * (1.0f / 16777216.0f);  // (0, 1]
+    const float u2 = (float)(b >> 8) * (1.0f / 16777216.0f);           // [0, 1)
+    const float r = sqrtf(-2.0f * logf(u1));
+    float sn, cs;
+    sincosf(6.283185307179586f * u2, &sn, &cs);
+    z0 = r * cs;
+    z1 = r * sn;
+}
+
+template <int OUT_BF16>
+__global__ __launch_bounds__(256) void gen_normal_kernel(void *dst, int64_t n, int64_t d,
+                                                         uint64_t seed, uint64_t stream,
+                                                         int normalize) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= n) return;
+    const uint2 key = make_uint2((uint32_t)seed, (uint32_t)(seed >> 32));
+    const int64_t groups = (d + 3) / 4;
+    double ss = 0.0;
+    // first pass: sum of squares (values regenerated in the second pass)
+    for (int pass = 0; pass < 2; ++pass) {
+        double inv = 1.0;
+        if (pass == 1 && normalize) inv = ss > 0.0 ? 1.0 / sqrt(ss) : 0.0;
+        if (pass == 0 && !normalize) continue;
+        for (int64_t gi = lane; gi < groups; gi += 64) {
+            const uint64_t ctr = (uint64_t)row * (uint64_t)groups + (uint64_t)gi;
+            const uint4 r = philox4x32_10(
+                make_uint4((uint32_t)ctr, (uint32_t)(ctr >> 32), (uint32_t)stream,
+                           (uint32_t)(stream >> 32)),
+                key);
+            float z[4];
+            box_muller(r.x, r.y, z[0], z[1]);
+            box_muller(r.z, r.w, z[2], z[3]);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int64_t j = gi * 4 + u;
+                if (j >= d) break;
+                if (pass == 0) {
+                    ss += (double)z[u] * (double)z[u];
+                } else {
+                    const float o = normalize ? (float)((double)z[u] * inv) : z[u];
+                    if (OUT_BF16)
+                        ((uint16_t *)dst)[row * d + j] = f32_to_bf16_rne(o);
+                    else
+                        ((float *)dst)[row * d + j] = o;
+                }
+            }
+        }
+        if (pass == 0)
+            for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+    }
+}
+
+hipError_t launch_gen_normal(void *dst, int out_dtype, int64_t n, int64_t d, uint64_t seed,
+                             uint64_t stream, int normalize, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    const dim3 grid((unsigned)((n + 3) / 4)), block(256);
+    if (out_dtype == 1)
+        gen_normal_kernel<1><<<grid, block, 0, st>>>(dst, n, d, seed, stream, normalize);
+    else
+        gen_normal_kernel<0><<<grid, block, 0, st>>>(dst, n, d, seed, stream, normalize);
+    return hipGetLastError();
+}
+
+}  // namespace vs

@@ -1,0 +1,87 @@
+"""Lloyd k-means on the GPU flat path (lib/core/vector_store/kmeans.dart).
+
+Each iteration is one library call (vs_kmeans_step) doing the reference's
+assignment step (strict-'<' argmin over fp64 squared distances, fp64
+objective in point order; kmeans.dart:91-105) and update step (fp32 running
+sums in point order scaled by fp64 1/count, empty clusters copied from the
+largest one plus jitter; kmeans.dart:107-140).
+
+Initialisation differs by necessity: the reference's k-means++ draws from
+dart:math Random (kmeans.dart:48-85), whose stream cannot be reproduced
+outside the Dart VM.  Kmeans here seeds with a uniform random subset of the
+points (Philox-seeded numpy generator) unless init_centroids is given; the
+jitter of empty clusters uses the same generator.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _native as N
+from .gpu_index_flat import GpuIndexFlat
+from .index import Metric
+
+
+@dataclass
+class KmeansResult:
+    """kmeans.dart:12-23."""
+
+    centroids: np.ndarray  # (k, d) float32
+    assignments: np.ndarray  # (n,) int32
+    objective: float
+
+
+def kmeans_step(points: GpuIndexFlat, centroids: np.ndarray, min_points: int = 1,
+                jitter_u: np.ndarray | None = None):
+    """One Lloyd iteration.  Returns (assign, new_centroids, counts, objective)."""
+    cen = np.ascontiguousarray(centroids, dtype=np.float32)
+    K, d = cen.shape
+    n = points.ntotal
+    assign = np.empty(n, np.int32)
+    out = np.empty((K, d), np.float32)
+    counts = np.empty(K, np.int32)
+    obj = ctypes.c_double(0.0)
+    ju = np.ascontiguousarray(jitter_u if jitter_u is not None else np.zeros(0), dtype=np.float64)
+    N.check(points._lib.vs_kmeans_step(points.handle, cen.ctypes.data_as(ctypes.c_void_p), K,
+                                       int(min_points), ju.ctypes.data_as(ctypes.c_void_p), ju.size,
+                                       assign.ctypes.data_as(ctypes.c_void_p),
+                                       out.ctypes.data_as(ctypes.c_void_p),
+                                       counts.ctypes.data_as(ctypes.c_void_p), ctypes.byref(obj)))
+    return assign, out, counts, float(obj.value)
+
+
+class Kmeans:
+    """kmeans.dart:26-41: Kmeans(d, k, niter=20, seed=1234, minPointsPerCentroid=1)."""
+
+    def __init__(self, d: int, k: int, niter: int = 20, seed: int = 1234,
+                 min_points_per_centroid: int = 1, verbose: bool = False, device: int = 0):
+        self.d, self.k, self.niter, self.seed = int(d), int(k), int(niter), int(seed)
+        self.min_points_per_centroid = int(min_points_per_centroid)
+        self.verbose = verbose
+        self.device = device
+
+    def train(self, xs, init_centroids: np.ndarray | None = None) -> KmeansResult:
+        x = np.ascontiguousarray(xs, dtype=np.float32)
+        n = x.shape[0]
+        if n < self.k:
+            raise ValueError(f"k-means: need at least k={self.k} vectors, got {n}")
+        rng = np.random.Generator(np.random.Philox(self.seed))
+        if init_centroids is None:
+            cen = x[rng.choice(n, size=self.k, replace=False)].copy()
+        else:
+            cen = np.ascontiguousarray(init_centroids, dtype=np.float32).copy()
+        pts = GpuIndexFlat(self.d, Metric.l2, storage="f32", device=self.device)
+        try:
+            pts.add(x)
+            assign = np.zeros(n, np.int32)
+            obj = 0.0
+            for it in range(self.niter):
+                jitter = rng.random(self.k * self.d)
+                assign, cen, _counts, obj = kmeans_step(pts, cen, self.min_points_per_centroid, jitter)
+                if self.verbose:
+                    print(f"  k-means iter {it} obj={obj:.4f}")
+        finally:
+            pts.close()
+        return KmeansResult(cen, assign, obj)

@@ -1,0 +1,73 @@
+"""Seeded synthetic inputs for the benchmark configurations.
+
+Host generation uses numpy's Philox bit generator; one host buffer is fed to
+both the GPU library and the CPU checker in the same run, so the two sides
+always see identical bytes.  The 20M x 768 configuration is generated on the
+device instead (vs_gen_normal) and checked on rows read back.
+
+Normalisation follows L2NormTransform (l2_norm_transform.dart:23-46): fp64
+sum of squares, inv = 1/sqrt, o = v * inv rounded to fp32 (zero rows stay
+zero).  bf16 values are carried as uint16 bit patterns (round to nearest even).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+
+def rng(seed: int, stream: int = 0) -> np.random.Generator:
+    return np.random.Generator(np.random.Philox(key=seed, counter=[0, 0, 0, stream]))
+
+
+def l2_normalize(x: np.ndarray) -> np.ndarray:
+    x64 = x.astype(np.float64)
+    ss = np.einsum("ij,ij->i", x64, x64)
+    inv = np.where(ss > 0, 1.0 / np.sqrt(np.where(ss > 0, ss, 1.0)), 0.0)
+    return (x64 * inv[:, None]).astype(np.float32)
+
+
+def to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bit patterns, round to nearest even."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return u.astype(np.uint16)
+
+
+def bf16_bits_to_f32(h: np.ndarray) -> np.ndarray:
+    return (h.astype(np.uint32) << 16).view(np.float32)
+
+
+def normal_unit(n: int, d: int, seed: int, stream: int) -> np.ndarray:
+    """N(0,1) rows, L2-normalised (configs 1, 3, 5)."""
+    return l2_normalize(rng(seed, stream).standard_normal((n, d), dtype=np.float32))
+
+
+def int_grid(n: int, d: int, seed: int, stream: int) -> np.ndarray:
+    """Uniform integers 0..255 stored as fp32 (config 2)."""
+    return rng(seed, stream).integers(0, 256, size=(n, d), dtype=np.int32).astype(np.float32)
+
+
+def gaussian_mixture(n: int, d: int, ncomp: int, sigma: float, seed: int):
+    """Config 4: centres N(0,1); point = centre[uniform component] + N(0, sigma^2)."""
+    g = rng(seed, 0)
+    centres = g.standard_normal((ncomp, d), dtype=np.float32)
+    comp = rng(seed, 1).integers(0, ncomp, size=n)
+    noise = rng(seed, 2).standard_normal((n, d), dtype=np.float32) * np.float32(sigma)
+    return (centres[comp] + noise).astype(np.float32), comp
+
+
+def seeded_subset(n: int, k: int, seed: int) -> np.ndarray:
+    """k distinct indices of [0, n) (partial Fisher-Yates via Generator.choice)."""
+    return rng(seed, 3).choice(n, size=k, replace=False)
+
+
+def dedup_set(n: int, d: int, dup_frac: float, noise: float, seed: int) -> np.ndarray:
+    """Config 5: (1 - dup_frac) n unit base vectors, dup_frac n copies of random
+    bases + N(0, noise^2) renormalised, rows shuffled by a seeded permutation."""
+    ndup = int(round(n * dup_frac))
+    nbase = n - ndup
+    base = normal_unit(nbase, d, seed, 0)
+    src = rng(seed, 1).integers(0, nbase, size=ndup)
+    cop = base[src] + rng(seed, 2).standard_normal((ndup, d), dtype=np.float32) * np.float32(noise)
+    allv = np.concatenate([base, l2_normalize(cop)], axis=0)
+    perm = rng(seed, 3).permutation(n)
+    return np.ascontiguousarray(allv[perm])

@@ -1,0 +1,188 @@
+/*
+ * vs_hip.h -- C ABI of libvs_hip.so, the MI355X (gfx950) flat exact
+ * nearest-neighbour library.
+ *
+ * This ABI replaces, for the vector-store search path, the CUDA
+ * libmat_mul.so bindings that the reference opens through dart:ffi
+ * (lib/core/tensor/cuda_engine.dart:241-413, path resolution :428-455) and
+ * the GpuIndexFlat slot built on them (lib/core/vector_store/gpu_index_flat.dart:40-194).
+ * The reference's per-search sequence create_tensor / transpose_tensor /
+ * matmul_tensors / get_tensor_data / destroy_tensor (engine.cu:94-132,328-338)
+ * becomes one vs_index_search call on an HBM-resident index.
+ *
+ * Rules:
+ *   - every size and count is int64_t; ids are int32_t because the
+ *     reference's result containers are Int32List (index.dart:28-35);
+ *   - every entry point returns a status (VS_OK = 0) and never fails
+ *     silently; vs_last_error() returns a thread-local message for the last
+ *     failing call on the calling thread;
+ *   - the library owns all device memory; the caller owns host buffers
+ *     except the result objects, which have their own free functions;
+ *   - an index handle is single-threaded (one internal HIP stream);
+ *     separate handles may be used from separate threads.
+ */
+#ifndef VS_HIP_H
+#define VS_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VS_API __attribute__((visibility("default")))
+
+/* status codes */
+enum {
+    VS_OK = 0,
+    VS_ERR_INVALID = 1,     /* bad argument: d <= 0, bad metric, k < 0, ... */
+    VS_ERR_OOM = 2,         /* device or host allocation failed */
+    VS_ERR_HIP = 3,         /* HIP runtime error (message holds the HIP string) */
+    VS_ERR_UNSUPPORTED = 4, /* valid request outside what this build implements */
+    VS_ERR_NONFINITE = 5,   /* NaN or infinity in vectors or queries */
+    VS_ERR_NO_DEVICE = 6    /* no HIP device visible */
+};
+
+/* Metric codes follow the FAISDART on-disk encoding, 0 = L2, 1 = IP
+ * (index_io.dart:233-243).  L2 is the squared Euclidean distance, smaller is
+ * better; IP is the raw dot product, larger is better (index.dart:11-16). */
+enum { VS_METRIC_L2 = 0, VS_METRIC_IP = 1 };
+
+/* element types of caller buffers */
+enum { VS_DTYPE_F32 = 0, VS_DTYPE_BF16 = 1 };
+
+/* Storage of the database rows in HBM.
+ *   F32  -- fp32, as IndexFlat's Float32List storage (index_flat.dart:20);
+ *   BF16 -- bf16; fp32 input rows are rounded to nearest-even once at add;
+ *   AUTO -- bf16 while every stored value is exactly a bf16 value (then
+ *           results are those of fp32 storage), fp32 otherwise; the switch
+ *           to fp32 happens at the first add that needs it. */
+enum { VS_STORAGE_F32 = 0, VS_STORAGE_BF16 = 1, VS_STORAGE_AUTO = 2 };
+
+typedef struct vs_index vs_index;
+
+/* CSR range-search result, the layout of RangeSearchResult (index.dart:37-85):
+ * hits of query q are [lims[q], lims[q+1]) in ascending id order. */
+typedef struct vs_range_result {
+    int64_t nq;
+    int64_t *lims; /* nq + 1 */
+    float *D;      /* lims[nq] distances (fp32 of the fp64 score) */
+    int32_t *I;    /* lims[nq] ids */
+} vs_range_result;
+
+/* Pair list of a self-join, sorted by (i, j), i < j. */
+typedef struct vs_pairs {
+    int64_t npairs;
+    int32_t *i;
+    int32_t *j;
+    float *s;
+} vs_pairs;
+
+/* ---- lifecycle (replaces create_tensor/destroy_tensor, engine.cu:94-107) ---- */
+
+/* IndexFlat(d, metric) (index_flat.dart:17-18; IndexFlatL2/IP :192,196);
+ * GpuIndexFlat.l2/.ip (gpu_index_flat.dart:47-51). */
+VS_API int vs_index_create(int device, int64_t d, int metric, int storage, vs_index **out);
+VS_API void vs_index_destroy(vs_index *idx);
+/* Pre-size device storage for n vectors (avoids regrowth copies). */
+VS_API int vs_index_reserve(vs_index *idx, int64_t n);
+/* Drop all vectors (ntotal = 0), keep the allocation. */
+VS_API int vs_index_reset(vs_index *idx);
+
+VS_API int64_t vs_index_ntotal(const vs_index *idx);
+VS_API int64_t vs_index_d(const vs_index *idx);
+VS_API int vs_index_metric(const vs_index *idx);
+/* Current storage (VS_STORAGE_F32 or VS_STORAGE_BF16). */
+VS_API int vs_index_storage(const vs_index *idx);
+
+/* ---- data in ---- */
+
+/* IndexFlat.add (index_flat.dart:23-51): append n row-major host rows of d
+ * elements; ids are assigned sequentially from ntotal. */
+VS_API int vs_index_add(vs_index *idx, const void *xs, int src_dtype, int64_t n);
+/* Same, rows already in device memory on the index's device. */
+VS_API int vs_index_add_device(vs_index *idx, const void *xs_dev, int src_dtype, int64_t n);
+/* IndexFlat.reconstruct (index_flat.dart:55-60) for rows [i0, i0+n) as fp32. */
+VS_API int vs_index_reconstruct(vs_index *idx, int64_t i0, int64_t n, float *out);
+/* IndexFlat.removeIds (index_flat.dart:139-160): drop the listed ids, compact
+ * the remaining rows in order and renumber them from 0.  Ids outside
+ * [0, ntotal) and duplicates are ignored, as a Set<int> lookup does. */
+VS_API int vs_index_remove_ids(vs_index *idx, const int64_t *ids, int64_t n, int64_t *nremoved);
+
+/* ---- search ---- */
+
+/* IndexFlat.search (index_flat.dart:62-97) / GpuIndexFlat.search
+ * (gpu_index_flat.dart:119-193).  Host queries nq x d, host outputs nq x k
+ * (caller-allocated).  Rows are best-first; slots beyond ntotal hold +inf
+ * (L2) or -inf (IP) with id -1 (index.dart:306-313).  Distances are the
+ * fp64 sum in dimension order rounded to fp32, as the reference reports. */
+VS_API int vs_index_search(vs_index *idx, const void *q, int q_dtype, int64_t nq, int64_t k,
+                           float *D, int32_t *I);
+/* Same with q, D and I in device memory (inputs resident in HBM). */
+VS_API int vs_index_search_device(vs_index *idx, const void *q_dev, int q_dtype, int64_t nq,
+                                  int64_t k, float *D_dev, int32_t *I_dev);
+
+/* IndexFlat.rangeSearch (index_flat.dart:99-137): every stored vector with
+ * dist <= radius (L2) or dot >= radius (IP), tested on the fp64 score.
+ * *out is library-allocated; free it with vs_range_result_free. */
+VS_API int vs_index_range_search(vs_index *idx, const void *q, int q_dtype, int64_t nq,
+                                 double radius, vs_range_result **out);
+VS_API void vs_range_result_free(vs_range_result *r);
+
+/* Near-duplicate self-join over the index's own vectors: all pairs i < j
+ * with dot(x_i, x_j) >= threshold (IP) or |x_i - x_j|^2 <= threshold (L2),
+ * sorted by (i, j) -- the pair list bin/vector_dedup_demo.dart:115-128
+ * builds from rangeSearch(all, threshold). */
+VS_API int vs_index_self_join(vs_index *idx, double threshold, vs_pairs **out);
+VS_API void vs_pairs_free(vs_pairs *p);
+
+/* One Lloyd iteration of Kmeans.train (kmeans.dart:91-140) with the index's
+ * vectors as the training points (metric ignored; storage must be F32):
+ * assign[i] = strict-'<' argmin over centroids_in of the fp64 squared
+ * distance; *obj = their fp64 sum in point order; counts[c]; centroids_out
+ * = fp32 running sums in point order times fp64 1/count.  A centroid with
+ * count < min_points copies the largest cluster plus (u - 0.5) * 1e-4 with
+ * u taken in order from jitter_u (njitter values; the reference draws them
+ * from dart:math Random).  Host buffers; centroids_out may equal centroids_in. */
+VS_API int vs_kmeans_step(vs_index *points, const float *centroids_in, int64_t K,
+                          int64_t min_points, const double *jitter_u, int64_t njitter,
+                          int32_t *assign, float *centroids_out, int32_t *counts, double *obj);
+
+/* ---- errors ---- */
+VS_API const char *vs_last_error(void);
+
+/* ---- bench / test support (no reference counterpart) ---- */
+
+/* Device buffers on `device` for inputs that must be resident in HBM. */
+VS_API int vs_dev_alloc(int device, int64_t bytes, void **out);
+VS_API int vs_dev_free(int device, void *p);
+VS_API int vs_dev_upload(int device, void *dst_dev, const void *src_host, int64_t bytes);
+VS_API int vs_dev_download(int device, void *dst_host, const void *src_dev, int64_t bytes);
+VS_API int vs_device_count(int *count);
+VS_API int vs_device_name(int device, char *buf, int64_t len);
+
+/* Fill n x d rows at dst_dev with N(0,1) values from Philox4x32-10
+ * (Salmon et al., SC'11) keyed by (seed, stream) and Box-Muller; if
+ * normalize != 0 each row is then scaled by 1/sqrt(sum of squares)
+ * (computed in fp64, the L2NormTransform convention,
+ * l2_norm_transform.dart:23-46); out_dtype F32 or BF16 (round to nearest
+ * even after normalisation). */
+VS_API int vs_gen_normal(int device, void *dst_dev, int out_dtype, int64_t n, int64_t d,
+                         uint64_t seed, uint64_t stream, int normalize);
+
+/* Per-kernel timing on the index's stream with HIP events: when enabled,
+ * every launch of the named kernel family is bracketed by events and its
+ * duration accumulated.  Families: "scan", "merge", "range", "assign",
+ * "update", "join". */
+VS_API int vs_prof_enable(vs_index *idx, int on);
+VS_API int vs_prof_get(vs_index *idx, const char *family, int64_t *launches, double *total_ms);
+VS_API int vs_prof_reset(vs_index *idx);
+
+/* Synchronise the index's stream. */
+VS_API int vs_index_sync(vs_index *idx);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VS_HIP_H */

@@ -1,0 +1,52 @@
+"""k-means step parity (kmeans.dart:91-140) against the oracle with identical
+input centroids: assignments equal (strict '<', lowest index on ties),
+objective and updated centroids bit-identical (same fp64 scores, same fp32
+running sums in point order)."""
+import numpy as np
+import pytest
+
+import oracle
+from vector_store import synthetic as syn
+
+pytestmark = pytest.mark.gpu
+NT = oracle.default_threads()
+
+
+def test_kmeans_step_parity(vs):
+    x, _ = syn.gaussian_mixture(20_000, 256, 64, 0.1, 1234)
+    cen = x[syn.seeded_subset(len(x), 256, 1234)].copy()
+    pts = vs.GpuIndexFlat.l2(256, storage="f32")
+    pts.add(x)
+    for it in range(3):
+        a, newc, cnt, obj = vs.kmeans_step(pts, cen)
+        ar, br, objr = oracle.kmeans_assign(x, cen, NT)
+        assert np.array_equal(a, ar), f"iteration {it}: {np.sum(a != ar)} assignments differ"
+        assert obj == objr
+        cr, cntr, _ = oracle.kmeans_update(x, ar, cen)
+        assert np.array_equal(cnt, cntr)
+        assert np.array_equal(newc.view(np.uint32), cr.view(np.uint32))
+        cen = newc
+
+
+def test_kmeans_empty_cluster_jitter(vs):
+    """Centroids far from every point get no points: they copy the largest
+    cluster plus (u - 0.5) * 1e-4 with u taken in order (kmeans.dart:127-139)."""
+    x, _ = syn.gaussian_mixture(3000, 32, 4, 0.1, 7)
+    cen = np.concatenate([x[:6], np.full((2, 32), 1e3, np.float32)]).astype(np.float32)
+    u = syn.rng(1, 0).random(2 * 32)
+    pts = vs.GpuIndexFlat.l2(32, storage="f32")
+    pts.add(x)
+    a, newc, cnt, obj = vs.kmeans_step(pts, cen, 1, u)
+    ar, _, objr = oracle.kmeans_assign(x, cen, NT)
+    cr, cntr, used = oracle.kmeans_update(x, ar, cen, 1, u)
+    assert used == 64 and np.array_equal(a, ar) and obj == objr
+    assert np.array_equal(newc.view(np.uint32), cr.view(np.uint32))
+
+
+def test_kmeans_train_monotone(vs):
+    """vector_store_test.dart:91-111: re-assignment objective <= 1.05 x training objective."""
+    x, _ = syn.gaussian_mixture(400, 16, 8, 0.05, 1)
+    res = vs.Kmeans(16, 8, niter=30).train(x)
+    assert res.centroids.shape == (8, 16) and res.assignments.shape == (400,)
+    _, _, reobj = oracle.kmeans_assign(x, res.centroids, 1)
+    assert reobj <= res.objective * 1.05 + 1e-6
