@@ -1,0 +1,204 @@
+"""Benchmark of the MI355X flat k-NN path (one JSON line on stdout).
+
+Default workload = BASELINE.json configs[1]: exact L2 top-100 over a
+1,000,000 x 128 database of integers 0..255 stored as fp32, 10,000 queries of
+the same distribution.  One step = one search of the whole query batch with
+the database, the queries and the result buffers resident in HBM.
+
+value = queries per second over the K timed steps.  roofline = the scan
+kernel (the dominant launch) timed with HIP events on the index's stream:
+algorithmic flops per launch (2 * nq * N * d) over its mean duration, against
+the peak of the MFMA instruction it runs (bf16 for lossless-bf16 storage).
+cpu_baseline = the CPU oracle (a restatement of IndexFlat.search,
+index_flat.dart:62-97) on this host's cores over a bounded query sample of
+the same database, scaled to queries per second.
+
+Other workloads (--workload c1|c3|c4|c5) exist for exploration and profiling.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "dart-pytorch_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "QPS, flat top-k k-NN (1M×128 fp32, 20M×768 bf16); % HBM / MFMA roofline"
+PEAK = {"bf16_mfma_tflops": 2500.0, "fp32_mfma_tflops": 157.3, "hbm_gbs": 8000.0}
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def host_info():
+    cpu = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    return cpu, cores
+
+
+def cpu_baseline(xb, xq, k, metric, target_s, threads):
+    """Times the oracle on a bounded sample of the batch; returns (qps, sample, results)."""
+    import oracle
+
+    n0 = min(len(xq), max(threads, 4))
+    t = time.perf_counter()
+    oracle.flat_search(xb, xq[:n0], k, metric, threads)
+    per_q = (time.perf_counter() - t) / n0
+    ns = int(min(len(xq), max(n0, target_s / max(per_q, 1e-9))))
+    ns = max(threads, (ns // threads) * threads) if ns >= threads else ns
+    t = time.perf_counter()
+    D, I = oracle.flat_search(xb, xq[:ns], k, metric, threads)
+    dt = time.perf_counter() - t
+    return ns / dt, ns, dt, (D, I)
+
+
+def run_search_workload(args, vs, syn, N):
+    from vector_store import _native as NN
+
+    if args.workload == "c2":
+        n, d, nq, k, metric = args.n or 1_000_000, 128, args.nq or 10_000, 100, 0
+        xb = syn.int_grid(n, d, args.seed, 0)
+        xq = syn.int_grid(nq, d, args.seed, 1)
+        storage, qdt = "auto", NN.VS_DTYPE_F32
+        desc = f"c2: exact L2 top-{k}, {n} x {d} fp32 integers 0..255, {nq} queries"
+    elif args.workload == "c1":
+        n, d, nq, k, metric = args.n or 10_000, 384, args.nq or 100, 10, 1
+        xb = syn.normal_unit(n, d, args.seed, 0)
+        xq = syn.normal_unit(nq, d, args.seed, 1)
+        storage, qdt = "f32", NN.VS_DTYPE_F32
+        desc = f"c1: exact IP top-{k}, {n} x {d} fp32 unit N(0,1), {nq} queries"
+    elif args.workload == "c3":
+        n, d, nq, k, metric = args.n or 20_000_000, 768, args.nq or args.batch, 10, 1
+        xb = None
+        xq = syn.to_bf16_bits(syn.normal_unit(nq, d, args.seed, 1))
+        storage, qdt = "bf16", NN.VS_DTYPE_BF16
+        desc = f"c3: exact IP top-{k}, {n} x {d} bf16 unit N(0,1) (device-generated), batch {nq}"
+    else:
+        raise SystemExit(f"unknown search workload {args.workload}")
+
+    idx = vs.GpuIndexFlat(d, vs.Metric(metric), storage=storage)
+    t0 = time.perf_counter()
+    if xb is not None:
+        idx.add(xb)
+    else:
+        idx.reserve(n)
+        chunk = 1 << 20
+        buf = NN.DeviceBuffer(chunk * d * 2)
+        for r in range(0, n, chunk):
+            m = min(chunk, n - r)
+            NN.check(NN.load().vs_gen_normal(0, buf.ptr, NN.VS_DTYPE_BF16, m, d, args.seed,
+                                             (1 << 32) + r, 1))
+            idx.add_device(buf, m, NN.VS_DTYPE_BF16)
+        buf.free()
+    log(f"[bench] {desc}: add {time.perf_counter() - t0:.1f}s, storage={idx.storage}")
+
+    esz = 2 if qdt == NN.VS_DTYPE_BF16 else 4
+    qbuf = NN.DeviceBuffer(nq * d * esz)
+    qbuf.upload(xq)
+    Dbuf = NN.DeviceBuffer(nq * k * 4)
+    Ibuf = NN.DeviceBuffer(nq * k * 4)
+
+    for _ in range(args.warmup):
+        idx.search_device(qbuf, nq, k, Dbuf, Ibuf, qdt)
+    idx.prof_enable(True)
+    idx.prof_reset()
+    t = time.perf_counter()
+    for i in range(args.steps):
+        idx.search_device(qbuf, nq, k, Dbuf, Ibuf, qdt)
+        log(f"[bench] step {i + 1}/{args.steps} done")
+    wall = time.perf_counter() - t
+    idx.prof_enable(False)
+    nscan, scan_ms = idx.prof_get("scan")
+    nmerge, merge_ms = idx.prof_get("merge")
+
+    D = np.empty((nq, k), np.float32)
+    I = np.empty((nq, k), np.int32)
+    Dbuf.download(D)
+    Ibuf.download(I)
+
+    flops = 2.0 * nq * n * d
+    scan_avg_s = scan_ms / max(nscan, 1) / 1e3
+    bf16 = idx.storage == "bf16"
+    peak = PEAK["bf16_mfma_tflops"] if bf16 else PEAK["bf16_mfma_tflops"]
+    achieved = flops / scan_avg_s / 1e12
+    roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
+            "frac": round(achieved / peak, 4), "traffic": None,
+            "kernel": "scan_kernel", "launches": nscan, "avg_ms": round(scan_avg_s * 1e3, 4),
+            "algorithmic_flops_per_launch": flops, "merge_avg_ms": round(merge_ms / max(nmerge, 1), 4)}
+    if nq <= 64:  # streaming regime: the database bytes bound the kernel
+        db_bytes = n * d * (2 if bf16 else 4)
+        gbs = db_bytes / scan_avg_s / 1e9
+        roof.update({"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK["hbm_gbs"],
+                     "unit": "GB/s", "frac": round(gbs / PEAK["hbm_gbs"], 4),
+                     "algorithmic_bytes_per_launch": db_bytes})
+
+    out = {"metric": METRIC, "value": round(nq * args.steps / wall, 1), "unit": "queries/s",
+           "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": round(wall / args.steps * 1e3, 3), "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None,
+           "dtype": "bf16" if bf16 else "fp32", "data": "synthetic",
+           "config": {"workload": desc, "n": n, "d": d, "nq": nq, "k": k,
+                      "metric": "L2" if metric == 0 else "IP", "storage": idx.storage},
+           "roofline": roof}
+
+    if not args.no_cpu and xb is not None:
+        cpu, cores = host_info()
+        threads = min(cores, 16)
+        qps, ns, dt, (Dc, Ic) = cpu_baseline(xb, xq, k, metric, args.cpu_seconds, threads)
+        rec = float(np.mean([len(set(I[i]) & set(Ic[i])) / k for i in range(ns)]))
+        out["cpu_baseline"] = {"value": round(qps, 3), "unit": "queries/s", "cores": threads,
+                               "kind": "port",
+                               "sample": f"first {ns} of the {nq} queries against the full "
+                                         f"{n}-row database ({dt:.1f} s), fp64 oracle",
+                               "cpu": cpu}
+        out["recall_vs_cpu_sample"] = round(rec, 6)
+    idx.close()
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--workload", default="c2")
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--n", type=int, default=0)
+    ap.add_argument("--nq", type=int, default=0)
+    ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the multi-GPU "
+              "sharding of this path is a design note, not built.", file=sys.stderr)
+        sys.exit(2)
+    import vector_store as vs
+    from vector_store import synthetic as syn
+
+    if vs.device_count() < 1:
+        raise SystemExit("no HIP device visible")
+    out = run_search_workload(args, vs, syn, None)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

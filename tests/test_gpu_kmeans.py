@@ -18,11 +18,12 @@ def test_kmeans_step_parity(vs):
     pts = vs.GpuIndexFlat.l2(256, storage="f32")
     pts.add(x)
     for it in range(3):
-        a, newc, cnt, obj = vs.kmeans_step(pts, cen)
+        u = syn.rng(77, it).random(256 * 256)  # jitter draws (an empty cluster appears at it = 1)
+        a, newc, cnt, obj = vs.kmeans_step(pts, cen, 1, u)
         ar, br, objr = oracle.kmeans_assign(x, cen, NT)
         assert np.array_equal(a, ar), f"iteration {it}: {np.sum(a != ar)} assignments differ"
         assert obj == objr
-        cr, cntr, _ = oracle.kmeans_update(x, ar, cen)
+        cr, cntr, _ = oracle.kmeans_update(x, ar, cen, 1, u)
         assert np.array_equal(cnt, cntr)
         assert np.array_equal(newc.view(np.uint32), cr.view(np.uint32))
         cen = newc

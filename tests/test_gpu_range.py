@@ -29,9 +29,14 @@ def test_range_matches_filtered_knn(vs):
         assert set(rr.ids[rr.limits[q]:rr.limits[q + 1]].tolist()) == exp
 
 
-@pytest.mark.parametrize("metric,radius", [(0, 0.5), (0, 0.05), (1, 0.9), (1, 0.3)])
-def test_range_parity(vs, metric, radius):
-    xb, xq = blobs(5000, 24, seed=3), blobs(50, 24, seed=4)
+@pytest.mark.parametrize("metric,rank", [(0, 3), (0, 60), (1, 5), (1, 200)])
+def test_range_parity(vs, metric, rank):
+    """radius = the oracle's rank-th score of query 0, so hits exist and one
+    query sits exactly on its boundary."""
+    xb = blobs(5000, 24, seed=3)
+    xq = np.concatenate([xb[:25] + 0.01, blobs(25, 24, seed=4)]).astype(np.float32)
+    Dk, _ = oracle.flat_search(xb, xq[:1], rank, metric, 1)
+    radius = float(Dk[0, -1])
     g = vs.GpuIndexFlat(24, vs.Metric(metric))
     g.add(xb)
     rr = g.range_search(xq, radius)
