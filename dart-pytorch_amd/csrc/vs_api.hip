@@ -119,8 +119,8 @@ struct vs_index {
     int num_cu = 256;
     size_t lds_max = 64 * 1024;
     // scratch (grown on demand, reused across calls)
-    DevBuf stage, qp, qf, qnorm, flags, cand_v, cand_i, outD, outI, athr, rq, ri, rs, rkeep, rcount,
-        misc;
+    DevBuf stage, qp, qf, qnorm, flags, cand_v, cand_i, gthr, lbound, vf, fbq, fbD, fbI, outD, outI,
+        athr, rq, ri, rs, rkeep, rcount, misc;
     DevBuf km_cen, km_cxn, km_assign, km_best, km_fb, km_keys, km_order, km_tmp, km_counts,
         km_offsets, km_out, km_iota;
     bool prof_on = false;
@@ -296,17 +296,44 @@ int check_dtype(int dt) {
 // ---------------------------------------------------------------------------
 // Planning
 // ---------------------------------------------------------------------------
-int plan_scan(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t kk,
-              vs::ScanPlan *p) {
+int env_int(const char *name, int dflt) {
+    const char *v = getenv(name);
+    return v && *v ? atoi(v) : dflt;
+}
+
+// Scan planning.  kk_final candidates per query survive the merge; each
+// wave's list keeps kk of them: kk_final itself up to 32, else kk_final / 4
+// (then four lists of a block together bound the kk_final-th value, and the
+// merge verifies that no list dropped a winner; safe forces kk = kk_final).
+// Tuning knobs (for sweeps; defaults are the tuned values): VS_SCAN_TM
+// (16-row blocks per wave tile), VS_SCAN_BN (queries per block),
+// VS_SCAN_BLOCKS_PER_CU (target workgroups per CU), VS_SCAN_QREG (0 disables
+// register-resident queries), VS_SCAN_KKW (per-list keep, for tests of the
+// verification path).
+int plan_scan(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t kk_final,
+              int storage, vs::ScanPlan *p, bool safe = false) {
+    int64_t kk = kk_final <= 32 ? kk_final : kk_final / 4;
+    const int kkw = env_int("VS_SCAN_KKW", 0);
+    if (kkw > 0) kk = std::min<int64_t>(kk_final, std::max<int64_t>(4, next_pow2(kkw)));
+    if (safe) kk = kk_final;
+    p->kk_final = (int)kk_final;
     p->kk = (int)kk;
     p->cap = (int)next_pow2(kk + 48);
-    p->tm = 2;
+    p->tm = env_int("VS_SCAN_TM", 2);
+    if (p->tm != 1 && p->tm != 2 && p->tm != 4) p->tm = 2;
+    const int nks = (int)(x->ld / 32);
+    const int force_bn = env_int("VS_SCAN_BN", 0);
     const int cands[3] = {64, 32, 16};
     p->bn = 0;
+    p->nks = 0;
     for (int bn : cands) {
-        if (bn > 16 && round_up(nq, 16) < bn) continue;
-        if (vs::scan_lds_bytes(bn, planes, x->ld, p->cap) <= x->lds_max) {
+        if (force_bn && bn != force_bn) continue;
+        if (!force_bn && bn > 16 && round_up(nq, 16) < bn) continue;
+        const bool qreg = env_int("VS_SCAN_QREG", 1) && storage == 1 && planes == 1 &&
+                          (nks == 4 || nks == 8) && nks * (bn / 16) <= 16;
+        if (vs::scan_lds_bytes(bn, qreg ? 0 : planes, x->ld, p->cap) <= x->lds_max) {
             p->bn = bn;
+            p->nks = qreg ? nks : 0;
             break;
         }
     }
@@ -314,10 +341,10 @@ int plan_scan(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t 
         return set_err(VS_ERR_UNSUPPORTED,
                        "d=%lld is too large for the LDS-resident query block of this build",
                        (long long)x->d);
-    p->lds_bytes = vs::scan_lds_bytes(p->bn, planes, x->ld, p->cap);
+    p->lds_bytes = vs::scan_lds_bytes(p->bn, p->nks ? 0 : planes, x->ld, p->cap);
     p->nqblk = (nq + p->bn - 1) / p->bn;
     const int64_t tile_rows = 64 * p->tm;  // rows per block per round
-    const int64_t target = (int64_t)x->num_cu * 4;
+    const int64_t target = (int64_t)x->num_cu * env_int("VS_SCAN_BLOCKS_PER_CU", 8);
     int64_t nsplit = std::max<int64_t>(1, (target + p->nqblk - 1) / p->nqblk);
     const int64_t min_rows = tile_rows * 8;
     nsplit = std::min<int64_t>(nsplit, std::max<int64_t>(1, (nrows + min_rows - 1) / min_rows));
@@ -361,7 +388,7 @@ __global__ void fill_sentinels_kernel(float *D, int32_t *I, int64_t m, float v) 
 }
 
 int search_device(vs_index *x, const void *q_dev, int q_dtype, int64_t nq, int64_t k, float *D,
-                  int32_t *I) {
+                  int32_t *I, bool safe = false) {
     if (nq < 0 || k < 0) return set_err(VS_ERR_INVALID, "nq and k must be >= 0");
     if (nq == 0) return VS_OK;
     if (k == 0) {
@@ -385,23 +412,71 @@ int search_device(vs_index *x, const void *q_dev, int q_dtype, int64_t nq, int64
     int rc = prepare_queries(x, q_dev, q_dtype, x->d, nq, &pq, nullptr);
     if (rc) return rc;
     vs::ScanPlan plan;
-    rc = plan_scan(x, nq, x->ntotal, pq.planes, kk, &plan);
+    rc = plan_scan(x, nq, x->ntotal, pq.planes, kk, x->storage, &plan, safe);
     if (rc) return rc;
-    const size_t nlist = (size_t)plan.nqblk * plan.nsplit * 4 * plan.bn * plan.cap;
+    const size_t nlists = (size_t)plan.nqblk * plan.nsplit * 4 * plan.bn;
+    const size_t nlist = nlists * plan.cap;
     VS_HIP(x->cand_v.ensure(nlist * 4), "candidate lists");
     VS_HIP(x->cand_i.ensure(nlist * 4), "candidate lists");
+    VS_HIP(x->gthr.ensure((size_t)pq.nq_pad * 4), "shared thresholds");
+    VS_HIP(hipMemsetD32Async((hipDeviceptr_t)x->gthr.p, (int)vs::kGthrInit, (size_t)pq.nq_pad, x->st),
+           "shared thresholds");
+    const bool verify = plan.kk < plan.kk_final;
+    if (verify) {
+        VS_HIP(x->lbound.ensure(nlists * 4), "list bounds");
+        VS_HIP(x->vf.ensure((size_t)(nq + 1) * 4), "verification list");
+        VS_HIP(hipMemsetAsync(x->vf.p, 0, 4, x->st), "verification count");
+    }
     {
         ProfScope ps(x, "scan");
         VS_HIP(vs::launch_scan_topk(x->xb, x->storage, x->ld, x->xn, x->ntotal, x->metric, pq, plan,
-                                    x->cand_v.as<float>(), x->cand_i.as<int32_t>(), x->st),
+                                    x->cand_v.as<float>(), x->cand_i.as<int32_t>(),
+                                    x->gthr.as<uint32_t>(), x->lbound.as<float>(), x->st),
                "scan kernel");
     }
     {
         ProfScope ps(x, "merge");
         VS_HIP(vs::launch_merge_refine(x->xb, x->storage, x->ld, x->d, x->metric, pq, plan,
-                                       x->cand_v.as<float>(), x->cand_i.as<int32_t>(), k, D, I,
+                                       x->cand_v.as<float>(), x->cand_i.as<int32_t>(),
+                                       x->gthr.as<uint32_t>(), x->lbound.as<float>(),
+                                       x->vf.as<int32_t>(), x->vf.as<int32_t>() + 1, k, D, I,
                                        x->st),
                "merge kernel");
+    }
+    if (verify) {
+        // queries whose shortened lists may have dropped a winner are searched
+        // again with full-length lists (exact; rare for unordered data)
+        int32_t nvf = 0;
+        VS_HIP(hipMemcpyAsync(&nvf, x->vf.p, 4, hipMemcpyDeviceToHost, x->st), "verification");
+        VS_HIP(hipStreamSynchronize(x->st), "search");
+        if (nvf > 0) {
+            std::vector<int32_t> lst((size_t)nvf);
+            VS_HIP(hipMemcpy(lst.data(), x->vf.as<int32_t>() + 1, (size_t)nvf * 4,
+                             hipMemcpyDeviceToHost),
+                   "verification list");
+            std::sort(lst.begin(), lst.end());
+            VS_HIP(x->fbq.ensure((size_t)nvf * x->d * 4), "fallback queries");
+            for (int32_t i = 0; i < nvf; ++i)
+                VS_HIP(hipMemcpyAsync(x->fbq.as<float>() + (size_t)i * x->d,
+                                      pq.qf + (size_t)lst[(size_t)i] * x->d, (size_t)x->d * 4,
+                                      hipMemcpyDeviceToDevice, x->st),
+                       "fallback gather");
+            VS_HIP(x->fbD.ensure((size_t)nvf * k * 4), "fallback results");
+            VS_HIP(x->fbI.ensure((size_t)nvf * k * 4), "fallback results");
+            rc = search_device(x, x->fbq.p, VS_DTYPE_F32, nvf, k, x->fbD.as<float>(),
+                               x->fbI.as<int32_t>(), true);
+            if (rc) return rc;
+            for (int32_t i = 0; i < nvf; ++i) {
+                VS_HIP(hipMemcpyAsync(D + (size_t)lst[(size_t)i] * k, x->fbD.as<float>() + (size_t)i * k,
+                                      (size_t)k * 4, hipMemcpyDeviceToDevice, x->st),
+                       "fallback scatter");
+                VS_HIP(hipMemcpyAsync(I + (size_t)lst[(size_t)i] * k, x->fbI.as<int32_t>() + (size_t)i * k,
+                                      (size_t)k * 4, hipMemcpyDeviceToDevice, x->st),
+                       "fallback scatter");
+            }
+            auto &e = x->prof["fallback"];
+            e.launches += nvf;
+        }
     }
     VS_HIP(hipStreamSynchronize(x->st), "search");
     return VS_OK;
@@ -432,7 +507,7 @@ int range_core(vs_index *x, const vs::PreparedQueries &pq, double radius, int se
     out->s.clear();
     if (pq.nq == 0 || x->ntotal == 0) return VS_OK;
     vs::ScanPlan plan;
-    int rc = plan_scan(x, pq.nq, x->ntotal, pq.planes, 8, &plan);
+    int rc = plan_scan(x, pq.nq, x->ntotal, pq.planes, 8, x->storage, &plan);
     if (rc) return rc;
     const float xmax = xnorm_max(x);
     VS_HIP(x->athr.ensure((size_t)pq.nq * 4), "range bounds");
@@ -575,7 +650,8 @@ void vs_index_destroy(vs_index *x) {
     }
     if (x->xb) (void)hipFree(x->xb);
     if (x->xn) (void)hipFree(x->xn);
-    DevBuf *bufs[] = {&x->stage,   &x->qp,        &x->qf,       &x->qnorm,    &x->flags,
+    DevBuf *bufs[] = {&x->stage,   &x->qp,        &x->qf,       &x->qnorm,    &x->flags, &x->gthr,
+                      &x->lbound,  &x->vf,        &x->fbq,      &x->fbD,      &x->fbI,
                       &x->cand_v,  &x->cand_i,    &x->outD,     &x->outI,     &x->athr,
                       &x->rq,      &x->ri,        &x->rs,       &x->rkeep,    &x->rcount,
                       &x->misc,    &x->km_cen,    &x->km_cxn,   &x->km_assign, &x->km_best,
@@ -916,15 +992,19 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     cview.lds_max = x->lds_max;
     cview.num_cu = x->num_cu;
     vs::ScanPlan plan;
-    rc = plan_scan(&cview, n, K, pq.planes, 16, &plan);
+    rc = plan_scan(&cview, n, K, pq.planes, 16, 0, &plan);
     if (rc) return rc;
     const size_t nlist = (size_t)plan.nqblk * plan.nsplit * 4 * plan.bn * plan.cap;
     VS_HIP(x->cand_v.ensure(nlist * 4), "candidate lists");
     VS_HIP(x->cand_i.ensure(nlist * 4), "candidate lists");
+    VS_HIP(x->gthr.ensure((size_t)pq.nq_pad * 4), "shared thresholds");
+    VS_HIP(hipMemsetD32Async((hipDeviceptr_t)x->gthr.p, (int)vs::kGthrInit, (size_t)pq.nq_pad, x->st),
+           "shared thresholds");
     {
         ProfScope ps(x, "assign");
         VS_HIP(vs::launch_scan_topk(x->km_cen.p, 0, ld, x->km_cxn.as<float>(), K, 0, pq, plan,
-                                    x->cand_v.as<float>(), x->cand_i.as<int32_t>(), x->st),
+                                    x->cand_v.as<float>(), x->cand_i.as<int32_t>(),
+                                    x->gthr.as<uint32_t>(), nullptr, x->st),
                "assign scan");
     }
     // error bound of the accumulator (split-bf16 products + fp32 sums)
@@ -949,7 +1029,8 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     {
         ProfScope ps(x, "pick");
         VS_HIP(vs::launch_kmeans_pick(x->km_cen.as<float>(), ld, d, n, x->km_cen.as<float>(), K,
-                                      x->cand_v.as<float>(), x->cand_i.as<int32_t>(), plan, bound,
+                                      x->cand_v.as<float>(), x->cand_i.as<int32_t>(),
+                                      x->gthr.as<uint32_t>(), plan, bound,
                                       pq.qf, x->km_assign.as<int32_t>(), x->km_best.as<double>(),
                                       fb_count, fb_list, x->st),
                "assign pick");

@@ -52,6 +52,9 @@ struct PreparedQueries {
 // Status flags written by the query-preparation kernel.
 enum : uint32_t { kFlagNonFinite = 1u, kFlagNotBf16 = 2u };
 
+// order-preserving code of +inf (see enc_order in vs_kernels.hip)
+constexpr uint32_t kGthrInit = 0xFF800000u;
+
 // ---------------------------------------------------------------------------
 // Launchers (vs_kernels.hip).  All enqueue on `st`; none synchronises.
 // ---------------------------------------------------------------------------
@@ -72,7 +75,9 @@ struct ScanPlan {
     int bn = 64;          // queries per block (16 * nqb)
     int tm = 2;           // 16-row blocks per wave tile
     int kk = 16;          // per-list kept candidates (power of two)
+    int kk_final = 16;    // candidates kept per query by the merge (power of two, >= kk)
     int cap = 64;         // per-list buffer capacity (power of two)
+    int nks = 0;          // >0: queries held in registers for this many K-steps
     int64_t nqblk = 0;    // query blocks
     int64_t nsplit = 0;   // database splits
     int64_t rows_per_split = 0;
@@ -81,16 +86,20 @@ struct ScanPlan {
 
 // Top-k scan: per (query block, split, wave) lists of the kk best approximate
 // candidates, written to cand_v / cand_i ([nqblk][nsplit][4][bn][cap]).
+// gthr [nq_pad] holds each query's shared threshold in an order-preserving
+// uint32 code; it must start at the code of +inf (kGthrInit).
 hipError_t launch_scan_topk(const void *xb, int storage, int64_t ld, const float *xn, int64_t n,
                             int metric, const PreparedQueries &pq, const ScanPlan &plan,
-                            float *cand_v, int32_t *cand_i, hipStream_t st);
+                            float *cand_v, int32_t *cand_i, uint32_t *gthr, float *lbound,
+                            hipStream_t st);
 
 // Merge the per-wave lists of each query, re-rank the kk survivors with the
 // exact fp64 distance and write the k best (sentinel-filled) to D / I.
 hipError_t launch_merge_refine(const void *xb, int storage, int64_t ld, int64_t d, int metric,
                                const PreparedQueries &pq, const ScanPlan &plan,
-                               const float *cand_v, const int32_t *cand_i, int64_t k, float *D,
-                               int32_t *I, hipStream_t st);
+                               const float *cand_v, const int32_t *cand_i, const uint32_t *gthr,
+                               const float *lbound, int32_t *vf_count, int32_t *vf_list,
+                               int64_t k, float *D, int32_t *I, hipStream_t st);
 
 // Range scan: appends (query, id) of every approximate score within the
 // per-query acceptance bound athr (accumulator space) to out_q / out_i
@@ -131,7 +140,8 @@ hipError_t launch_kmeans_update(const float *x, int64_t ld, int64_t d, int64_t n
 // proven to contain the argmin (then the caller runs the exhaustive path).
 hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, const float *cen,
                               int64_t K, const float *cand_v, const int32_t *cand_i,
-                              const ScanPlan &plan, float bound, const float *qf, int32_t *assign,
+                              const uint32_t *gthr, const ScanPlan &plan, float bound,
+                              const float *qf, int32_t *assign,
                               double *best_sq, int32_t *fallback_count, int32_t *fallback_list,
                               hipStream_t st);
 

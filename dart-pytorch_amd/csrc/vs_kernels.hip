@@ -33,6 +33,13 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
+// Orders LDS accesses between lanes of one wave: LDS instructions of a wave
+// execute in order, so only the compiler must not move them across.
+__device__ __forceinline__ void lds_wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
 template <typename T>
 __device__ __forceinline__ float load_f32(const T *p, int64_t i);
 template <>
@@ -187,7 +194,7 @@ __device__ void bitonic_sort_wave(float *sv, int *si, int n, int lane) {
                     si[j] = ii;
                 }
             }
-            wave_sync();
+            lds_wave_sync();
         }
     }
 }
@@ -247,8 +254,12 @@ struct ScanKArgs {
     int64_t nq;
     int64_t nqblk, nsplit, rows_per_split;
     int kk, cap, metric;
+    int kk_final;        // candidates the merge keeps per query
+    int publish_block;   // 4 * kk >= kk_final: a block's four lists bound the kk_final-th value
+    float *lbound;       // per list: its own final threshold (verification of kk < kk_final)
     float *cand_v;
     int32_t *cand_i;
+    uint32_t *gthr;  // per-query threshold shared by every list (order-preserving code)
     const float *athr;
     int self_join;
     int32_t *out_q, *out_i;
@@ -256,30 +267,56 @@ struct ScanKArgs {
     int64_t out_cap;
 };
 
+// planes == 0: the queries live in registers and need no LDS copy.
 size_t scan_lds_bytes(int bn, int planes, int64_t ld, int cap) {
     return (size_t)bn * planes * (size_t)(ld + 8) * 2 + (size_t)4 * bn * 8 + (size_t)4 * cap * 8;
 }
 
-// Flush one (wave, query) list: sort, keep the kk best, set count/threshold.
-__device__ void flush_list(float *cvq, int32_t *ciq, int *cnt_q, float *thr_q, float *sv, int *si,
-                           int cap, int kk, int lane) {
+// Order-preserving map of finite floats to uint32 (a < b  <=>  enc(a) < enc(b)),
+// so a shared threshold can be tightened with an integer atomicMin.
+__device__ __forceinline__ uint32_t enc_order(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float dec_order(uint32_t u) {
+    return __uint_as_float((u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u);
+}
+
+// Flush one (wave, query) list: sort, keep its kk best, set count and the
+// list's own threshold, and tighten the query's shared threshold with a
+// value that provably has kk_final candidates at or below it: the list's own
+// kk-th value when kk == kk_final, otherwise (4 * kk >= kk_final) the largest
+// of the four waves' thresholds of this block.  thr_q0 points at wave 0's
+// threshold of the query; waves are bn apart.
+__device__ void flush_list(float *cvq, int32_t *ciq, int *cnt_q, float *thr_q, const float *thr_q0,
+                           int bn, uint32_t *gthr_q, float *sv, int *si, int cap, int kk,
+                           int kk_final, int publish_block, int lane) {
+    wave_sync();  // the list's global entries were appended by other lanes
     const int c = *cnt_q;
     for (int j = lane; j < cap; j += 64) {
         const bool in = j < c;
         sv[j] = in ? cvq[j] : VS_INF;
         si[j] = in ? ciq[j] : INT_MAX;
     }
-    wave_sync();
+    lds_wave_sync();
     bitonic_sort_wave(sv, si, cap, lane);
     const int keep = c < kk ? c : kk;
     for (int j = lane; j < kk; j += 64) {
         cvq[j] = j < keep ? sv[j] : VS_INF;
         ciq[j] = j < keep ? si[j] : -1;
     }
-    wave_sync();
     if (lane == 0) {
         *cnt_q = keep;
-        *thr_q = c >= kk ? sv[kk - 1] : VS_INF;
+        if (c >= kk) {
+            const float kth = fminf(*thr_q, sv[kk - 1]);
+            *thr_q = kth;
+            if (kk >= kk_final) {
+                atomicMin(gthr_q, enc_order(kth));
+            } else if (publish_block) {
+                const float b = fmaxf(fmaxf(thr_q0[0], thr_q0[bn]), fmaxf(thr_q0[2 * bn], thr_q0[3 * bn]));
+                if (b < VS_INF) atomicMin(gthr_q, enc_order(b));
+            }
+        }
     }
     wave_sync();
 }
@@ -308,11 +345,36 @@ __device__ __forceinline__ bool map_block(int64_t nqblk, int64_t nsplit, int64_t
     return true;
 }
 
-template <int ST, int PQ, int NQB, int TM, int MODE>
+template <int ST>
+struct AFrag;
+template <>
+struct AFrag<1> {  // bf16 row: 8 values (16 B) per lane and K-step
+    uint4 v;
+    __device__ __forceinline__ void load(const char *p) { v = *(const uint4 *)p; }
+};
+template <>
+struct AFrag<0> {  // fp32 row: 8 values (32 B) per lane and K-step
+    U8x2 v;
+    __device__ __forceinline__ void load(const char *p) {
+        v.a = *(const uint4 *)p;
+        v.b = *(const uint4 *)(p + 16);
+    }
+};
+
+// NKS > 0: bf16 rows, one query plane, NKS K-steps known at compile time; the
+// queries' B fragments stay in registers for the whole kernel and each wave
+// prefetches its next tile whole while computing the current one.
+// NKS == 0: queries in LDS; rows are consumed in chunks of UK K-steps with the
+// next chunk (or the next tile's first chunk) in flight.
+template <int ST, int PQ, int NQB, int TM, int MODE, int NKS>
 __global__ __launch_bounds__(256) void scan_kernel(ScanKArgs a) {
     extern __shared__ __align__(16) char smem[];
     constexpr int BN = 16 * NQB;
-    constexpr int UK = ST == 1 ? 4 : 2;  // K-steps per load batch
+    constexpr bool QREG = NKS > 0;
+    static_assert(!QREG || (ST == 1 && PQ == 1), "register queries need bf16 rows, one plane");
+    constexpr int UK = QREG ? NKS : (ST == 1 ? 4 : 2);
+    constexpr int QPL = QREG ? 0 : PQ;  // query planes held in LDS
+    constexpr int64_t KSTEP_BYTES = ST == 1 ? 64 : 128;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r16 = lane & 15, g = lane >> 4;
 
     int64_t split, qblk;
@@ -323,26 +385,26 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanKArgs a) {
     if (r0 >= r1) return;
 
     const int64_t ldp = a.ld + 8;
-    uint16_t *qs = (uint16_t *)smem;  // [BN][PQ][ldp]
-    int *cnt = (int *)(smem + (size_t)BN * PQ * ldp * 2);
+    uint16_t *qs = (uint16_t *)smem;  // [BN][QPL][ldp]
+    int *cnt = (int *)(smem + (size_t)BN * QPL * ldp * 2);
     float *thr = (float *)(cnt + 4 * BN);
     float *sv = thr + 4 * BN;
     int *si = (int *)(sv + 4 * a.cap);
 
     const int64_t q0 = qblk * BN;
-    {
+    if constexpr (QPL > 0) {
         const int64_t cpr = a.ld / 8;  // 16-byte chunks per plane row
-        const int64_t nch = (int64_t)BN * PQ * cpr;
+        const int64_t nch = (int64_t)BN * QPL * cpr;
         for (int64_t c = threadIdx.x; c < nch; c += 256) {
             const int64_t row = c / cpr, ch = c % cpr;
-            const int64_t q = row / PQ, p = row % PQ;
+            const int64_t q = row / QPL, p = row % QPL;
             const uint4 v = *(const uint4 *)(a.qp + ((q0 + q) * 2 + p) * a.ld + ch * 8);
             *(uint4 *)(qs + row * ldp + ch * 8) = v;
         }
-        for (int t = threadIdx.x; t < 4 * BN; t += 256) {
-            cnt[t] = 0;
-            thr[t] = q0 + (t % BN) < a.nq ? VS_INF : -VS_INF;
-        }
+    }
+    for (int t = threadIdx.x; t < 4 * BN; t += 256) {
+        cnt[t] = 0;
+        thr[t] = q0 + (t % BN) < a.nq ? VS_INF : -VS_INF;
     }
     __syncthreads();
 
@@ -364,125 +426,157 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanKArgs a) {
             thr_r[qb] = qg < a.nq ? a.athr[qg] : -VS_INF;
     }
 
-    const int nks = (int)(a.ld / 32);
+    const int nks = QREG ? NKS : (int)(a.ld / 32);
     const int64_t row_bytes = a.ld * (ST == 1 ? 2 : 4);
     const char *xbase = (const char *)a.xb + (ST == 1 ? g * 16 : g * 32);
-    const uint16_t *qlane = qs + (int64_t)r16 * PQ * ldp + 8 * g;
+    const uint16_t *qlane = qs + (int64_t)r16 * QPL * ldp + 8 * g;
 
-    for (int64_t t0 = r0 + wave * 16 * TM; t0 < r1; t0 += 64 * TM) {
+    uint4 bq[QREG ? NKS : 1][NQB];
+    if constexpr (QREG) {
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+            for (int qb = 0; qb < NQB; ++qb)
+                bq[ks][qb] =
+                    *(const uint4 *)(a.qp + ((q0 + qb * 16 + r16) * 2) * a.ld + ks * 32 + 8 * g);
+    }
+
+    AFrag<ST> cur[UK][TM], nxt[UK][TM];
+    f32x4_t xn_cur[TM], xn_nxt[TM];
+    const f32x4_t zero4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+        xn_cur[tm] = zero4;
+        xn_nxt[tm] = zero4;
+    }
+
+    int64_t t0 = r0 + wave * 16 * TM;
+    if (t0 < r1) {
+#pragma unroll
+        for (int u = 0; u < UK; ++u)
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm)
+                cur[u][tm].load(xbase + (t0 + tm * 16 + r16) * row_bytes + u * KSTEP_BYTES);
+        if (a.metric == 0) {
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm)
+                xn_cur[tm] = *(const f32x4_t *)(a.xn + t0 + tm * 16 + 4 * g);
+        }
+    }
+
+    for (; t0 < r1; t0 += 64 * TM) {
+        uint32_t gt[NQB];
+        if constexpr (MODE == 0) {
+#pragma unroll
+            for (int qb = 0; qb < NQB; ++qb)
+                gt[qb] = __hip_atomic_load(&a.gthr[q0 + qb * 16 + r16], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+        }
         f32x4_t acc[TM][NQB];
 #pragma unroll
-        for (int tm = 0; tm < TM; ++tm) {
-            f32x4_t init = {0.f, 0.f, 0.f, 0.f};
-            if (a.metric == 0) init = *(const f32x4_t *)(a.xn + t0 + tm * 16 + 4 * g);
+        for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-            for (int qb = 0; qb < NQB; ++qb) acc[tm][qb] = init;
-        }
-        const char *rowp[TM];
-#pragma unroll
-        for (int tm = 0; tm < TM; ++tm) rowp[tm] = xbase + (t0 + tm * 16 + r16) * row_bytes;
+            for (int qb = 0; qb < NQB; ++qb) acc[tm][qb] = xn_cur[tm];
 
-        if constexpr (ST == 1) {
-            uint4 cur[UK][TM], nxt[UK][TM];
-#pragma unroll
-            for (int u = 0; u < UK; ++u)
-#pragma unroll
-                for (int tm = 0; tm < TM; ++tm) cur[u][tm] = *(const uint4 *)(rowp[tm] + u * 64);
-            for (int ks = 0; ks < nks; ks += UK) {
-                if (ks + UK < nks) {
-#pragma unroll
-                    for (int u = 0; u < UK; ++u)
-#pragma unroll
-                        for (int tm = 0; tm < TM; ++tm)
-                            nxt[u][tm] = *(const uint4 *)(rowp[tm] + (int64_t)(ks + UK + u) * 64);
-                }
-#pragma unroll
-                for (int u = 0; u < UK; ++u) {
-#pragma unroll
-                    for (int qb = 0; qb < NQB; ++qb) {
-                        const uint16_t *qrow = qlane + (int64_t)qb * 16 * PQ * ldp + (ks + u) * 32;
-                        const bf16x8_t b0 = __builtin_bit_cast(bf16x8_t, *(const uint4 *)qrow);
-#pragma unroll
-                        for (int tm = 0; tm < TM; ++tm)
-                            acc[tm][qb] =
-                                mfma_bf16(__builtin_bit_cast(bf16x8_t, cur[u][tm]), b0, acc[tm][qb]);
-                        if constexpr (PQ == 2) {
-                            const bf16x8_t b1 =
-                                __builtin_bit_cast(bf16x8_t, *(const uint4 *)(qrow + ldp));
-#pragma unroll
-                            for (int tm = 0; tm < TM; ++tm)
-                                acc[tm][qb] = mfma_bf16(__builtin_bit_cast(bf16x8_t, cur[u][tm]),
-                                                        b1, acc[tm][qb]);
-                        }
-                    }
-                }
+        const int64_t tn = t0 + 64 * TM;
+        for (int ks = 0; ks < nks; ks += UK) {
+            // prefetch: the next chunk of this tile, else the next tile's first
+            if (ks + UK < nks) {
 #pragma unroll
                 for (int u = 0; u < UK; ++u)
 #pragma unroll
-                    for (int tm = 0; tm < TM; ++tm) cur[u][tm] = nxt[u][tm];
+                    for (int tm = 0; tm < TM; ++tm)
+                        nxt[u][tm].load(xbase + (t0 + tm * 16 + r16) * row_bytes +
+                                        (int64_t)(ks + UK + u) * KSTEP_BYTES);
+            } else if (tn < r1) {
+#pragma unroll
+                for (int u = 0; u < UK; ++u)
+#pragma unroll
+                    for (int tm = 0; tm < TM; ++tm)
+                        nxt[u][tm].load(xbase + (tn + tm * 16 + r16) * row_bytes + u * KSTEP_BYTES);
+                if (a.metric == 0) {
+#pragma unroll
+                    for (int tm = 0; tm < TM; ++tm)
+                        xn_nxt[tm] = *(const f32x4_t *)(a.xn + tn + tm * 16 + 4 * g);
+                }
             }
-        } else {
-            U8x2 cur[UK][TM], nxt[UK][TM];
 #pragma unroll
-            for (int u = 0; u < UK; ++u)
-#pragma unroll
-                for (int tm = 0; tm < TM; ++tm) {
-                    cur[u][tm].a = *(const uint4 *)(rowp[tm] + u * 128);
-                    cur[u][tm].b = *(const uint4 *)(rowp[tm] + u * 128 + 16);
-                }
-            for (int ks = 0; ks < nks; ks += UK) {
-                if (ks + UK < nks) {
-#pragma unroll
-                    for (int u = 0; u < UK; ++u)
-#pragma unroll
-                        for (int tm = 0; tm < TM; ++tm) {
-                            const char *p = rowp[tm] + (int64_t)(ks + UK + u) * 128;
-                            nxt[u][tm].a = *(const uint4 *)p;
-                            nxt[u][tm].b = *(const uint4 *)(p + 16);
-                        }
-                }
-#pragma unroll
-                for (int u = 0; u < UK; ++u) {
-                    bf16x8_t hi[TM], lo[TM];
+            for (int u = 0; u < UK; ++u) {
+                bf16x8_t hi[TM], lo[TM];
+                if constexpr (ST == 0) {
 #pragma unroll
                     for (int tm = 0; tm < TM; ++tm) {
-                        const f32x8_t v = __builtin_bit_cast(f32x8_t, cur[u][tm]);
+                        const f32x8_t v = __builtin_bit_cast(f32x8_t, cur[u][tm].v);
                         hi[tm] = __builtin_convertvector(v, bf16x8_t);
-                        lo[tm] = __builtin_convertvector(v - __builtin_convertvector(hi[tm], f32x8_t),
-                                                         bf16x8_t);
+                        lo[tm] = __builtin_convertvector(
+                            v - __builtin_convertvector(hi[tm], f32x8_t), bf16x8_t);
                     }
+                } else {
 #pragma unroll
-                    for (int qb = 0; qb < NQB; ++qb) {
-                        const uint16_t *qrow = qlane + (int64_t)qb * 16 * PQ * ldp + (ks + u) * 32;
-                        const bf16x8_t b0 = __builtin_bit_cast(bf16x8_t, *(const uint4 *)qrow);
-#pragma unroll
-                        for (int tm = 0; tm < TM; ++tm) {
-                            acc[tm][qb] = mfma_bf16(hi[tm], b0, acc[tm][qb]);
-                            acc[tm][qb] = mfma_bf16(lo[tm], b0, acc[tm][qb]);
-                        }
-                        if constexpr (PQ == 2) {
-                            const bf16x8_t b1 =
-                                __builtin_bit_cast(bf16x8_t, *(const uint4 *)(qrow + ldp));
-#pragma unroll
-                            for (int tm = 0; tm < TM; ++tm)
-                                acc[tm][qb] = mfma_bf16(hi[tm], b1, acc[tm][qb]);
-                        }
-                    }
+                    for (int tm = 0; tm < TM; ++tm) hi[tm] = __builtin_bit_cast(bf16x8_t, cur[u][tm].v);
                 }
 #pragma unroll
-                for (int u = 0; u < UK; ++u)
+                for (int qb = 0; qb < NQB; ++qb) {
+                    bf16x8_t b0, b1;
+                    if constexpr (QREG) {
+                        b0 = __builtin_bit_cast(bf16x8_t, bq[u][qb]);
+                    } else {
+                        const uint16_t *qrow =
+                            qlane + (int64_t)qb * 16 * QPL * ldp + (int64_t)(ks + u) * 32;
+                        b0 = __builtin_bit_cast(bf16x8_t, *(const uint4 *)qrow);
+                        if constexpr (PQ == 2)
+                            b1 = __builtin_bit_cast(bf16x8_t, *(const uint4 *)(qrow + ldp));
+                    }
 #pragma unroll
-                    for (int tm = 0; tm < TM; ++tm) cur[u][tm] = nxt[u][tm];
+                    for (int tm = 0; tm < TM; ++tm) {
+                        acc[tm][qb] = mfma_bf16(hi[tm], b0, acc[tm][qb]);
+                        if constexpr (ST == 0) acc[tm][qb] = mfma_bf16(lo[tm], b0, acc[tm][qb]);
+                        if constexpr (PQ == 2) acc[tm][qb] = mfma_bf16(hi[tm], b1, acc[tm][qb]);
+                    }
+                }
             }
+#pragma unroll
+            for (int u = 0; u < UK; ++u)
+#pragma unroll
+                for (int tm = 0; tm < TM; ++tm) cur[u][tm] = nxt[u][tm];
         }
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) xn_cur[tm] = xn_nxt[tm];
 
         // ---- epilogue ----
+        if (t0 + 16 * TM > r1) {  // rows past the split end never qualify
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (t0 + tm * 16 + 4 * g + i >= r1) {
+#pragma unroll
+                        for (int qb = 0; qb < NQB; ++qb) acc[tm][qb][i] = VS_INF;
+                    }
+        }
+        if constexpr (MODE == 0) {
+#pragma unroll
+            for (int qb = 0; qb < NQB; ++qb) thr_r[qb] = fminf(thr_r[qb], dec_order(gt[qb]));
+        }
+        // one compare per lane and query block decides whether anything passes
+        bool pass = false;
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) {
+            float m = VS_INF;
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) m = fminf(m, acc[tm][qb][i]);
+            pass |= MODE == 0 ? (m < thr_r[qb]) : (m <= thr_r[qb]);
+        }
+        if (!__ballot(pass)) continue;
+
 #pragma unroll
         for (int tm = 0; tm < TM; ++tm) {
             const int64_t rbase = t0 + tm * 16 + 4 * g;
             if constexpr (MODE == 0) {
-                // make room: any list of this wave that a 16-row block could
-                // overflow is cut back to its kk best first
+                // make room: a list a 16-row block could overflow is cut back
+                // to its kk best first
                 bool need = false;
                 if (g == 0) {
 #pragma unroll
@@ -492,26 +586,27 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanKArgs a) {
                     for (int q = 0; q < BN; ++q) {
                         if (cnt_w[q] > a.cap - 16)
                             flush_list(cv + (int64_t)q * a.cap, ci + (int64_t)q * a.cap, &cnt_w[q],
-                                       &thr_w[q], sv_w, si_w, a.cap, a.kk, lane);
+                                       &thr_w[q], &thr[q], BN, &a.gthr[q0 + q], sv_w, si_w, a.cap,
+                                       a.kk, a.kk_final, a.publish_block, lane);
                     }
 #pragma unroll
-                    for (int qb = 0; qb < NQB; ++qb) thr_r[qb] = thr_w[qb * 16 + r16];
+                    for (int qb = 0; qb < NQB; ++qb)
+                        thr_r[qb] = fminf(thr_r[qb], thr_w[qb * 16 + r16]);
                 }
 #pragma unroll
                 for (int qb = 0; qb < NQB; ++qb) {
                     const int q = qb * 16 + r16;
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const int64_t row = rbase + i;
                         const float v = acc[tm][qb][i];
-                        if (row < r1 && v < thr_r[qb]) {
+                        if (v < thr_r[qb]) {
                             const int pos = atomicAdd(&cnt_w[q], 1);
                             cv[(int64_t)q * a.cap + pos] = v;
-                            ci[(int64_t)q * a.cap + pos] = (int32_t)row;
+                            ci[(int64_t)q * a.cap + pos] = (int32_t)(rbase + i);
                         }
                     }
                 }
-                wave_sync();
+                lds_wave_sync();
             } else {
 #pragma unroll
                 for (int qb = 0; qb < NQB; ++qb) {
@@ -519,8 +614,7 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanKArgs a) {
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int64_t row = rbase + i;
-                        const float v = acc[tm][qb][i];
-                        if (row < r1 && v <= thr_r[qb] && (!a.self_join || row > qg)) {
+                        if (acc[tm][qb][i] <= thr_r[qb] && (!a.self_join || row > qg)) {
                             const unsigned long long pos = atomicAdd(a.count, 1ull);
                             if (pos < (unsigned long long)a.out_cap) {
                                 a.out_q[pos] = (int32_t)qg;
@@ -540,7 +634,8 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanKArgs a) {
             const int c = cnt_w[q];
             if (c > a.kk) {
                 flush_list(cv + (int64_t)q * a.cap, ci + (int64_t)q * a.cap, &cnt_w[q], &thr_w[q],
-                           sv_w, si_w, a.cap, a.kk, lane);
+                           &thr[q], BN, &a.gthr[q0 + q], sv_w, si_w, a.cap, a.kk, a.kk_final,
+                           a.publish_block, lane);
             } else {
                 for (int j = c + lane; j < a.kk; j += 64) {
                     cv[(int64_t)q * a.cap + j] = VS_INF;
@@ -548,32 +643,38 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanKArgs a) {
                 }
             }
         }
+        // a list that cut itself to kk < kk_final entries may have dropped
+        // rows at or above its own final threshold: the merge checks that
+        // value against the query's final kk_final-th value
+        if (a.lbound) {
+            wave_sync();
+            const int64_t lb = ((qblk * a.nsplit + split) * 4 + wave) * (int64_t)BN;
+            for (int q = lane; q < BN; q += 64) a.lbound[lb + q] = thr_w[q];
+        }
     }
 }
 
 template <int MODE>
-static hipError_t launch_scan_mode(const void *xb, int storage, int64_t ld, const float *xn,
-                                   int64_t n, const PreparedQueries &pq, const ScanPlan &plan,
+static hipError_t launch_scan_mode(int storage, const PreparedQueries &pq, const ScanPlan &plan,
                                    const ScanKArgs &args, hipStream_t st) {
-    (void)xb;
-    (void)ld;
-    (void)xn;
-    (void)n;
     const int64_t total = plan.nqblk * plan.nsplit;
     const int64_t grid = ((total + 7) / 8) * 8;
     const size_t lds = plan.lds_bytes;
     void (*fn)(ScanKArgs) = nullptr;
     const int nqb = plan.bn / 16;
-#define VS_PICK(ST_, PQ_, NQB_, TM_)                                                     \
-    if (storage == ST_ && pq.planes == PQ_ && nqb == NQB_ && plan.tm == TM_) \
-        fn = scan_kernel<ST_, PQ_, NQB_, TM_, MODE>;
-#define VS_PICK_TM(ST_, PQ_, NQB_) \
-    VS_PICK(ST_, PQ_, NQB_, 1) VS_PICK(ST_, PQ_, NQB_, 2) VS_PICK(ST_, PQ_, NQB_, 4)
-#define VS_PICK_NQB(ST_, PQ_) VS_PICK_TM(ST_, PQ_, 1) VS_PICK_TM(ST_, PQ_, 2) VS_PICK_TM(ST_, PQ_, 4)
-    VS_PICK_NQB(0, 1)
-    VS_PICK_NQB(0, 2)
-    VS_PICK_NQB(1, 1)
-    VS_PICK_NQB(1, 2)
+#define VS_PICK(ST_, PQ_, NQB_, TM_, NKS_)                                                  \
+    if (storage == ST_ && pq.planes == PQ_ && nqb == NQB_ && plan.tm == TM_ && plan.nks == NKS_) \
+        fn = scan_kernel<ST_, PQ_, NQB_, TM_, MODE, NKS_>;
+#define VS_PICK_TM(ST_, PQ_, NQB_, NKS_) \
+    VS_PICK(ST_, PQ_, NQB_, 1, NKS_) VS_PICK(ST_, PQ_, NQB_, 2, NKS_) VS_PICK(ST_, PQ_, NQB_, 4, NKS_)
+#define VS_PICK_NQB(ST_, PQ_, NKS_) \
+    VS_PICK_TM(ST_, PQ_, 1, NKS_) VS_PICK_TM(ST_, PQ_, 2, NKS_) VS_PICK_TM(ST_, PQ_, 4, NKS_)
+    VS_PICK_NQB(0, 1, 0)
+    VS_PICK_NQB(0, 2, 0)
+    VS_PICK_NQB(1, 1, 0)
+    VS_PICK_NQB(1, 2, 0)
+    VS_PICK_NQB(1, 1, 4)
+    VS_PICK_NQB(1, 1, 8)
 #undef VS_PICK_NQB
 #undef VS_PICK_TM
 #undef VS_PICK
@@ -589,7 +690,8 @@ static hipError_t launch_scan_mode(const void *xb, int storage, int64_t ld, cons
 
 hipError_t launch_scan_topk(const void *xb, int storage, int64_t ld, const float *xn, int64_t n,
                             int metric, const PreparedQueries &pq, const ScanPlan &plan,
-                            float *cand_v, int32_t *cand_i, hipStream_t st) {
+                            float *cand_v, int32_t *cand_i, uint32_t *gthr, float *lbound,
+                            hipStream_t st) {
     ScanKArgs a{};
     a.xb = xb;
     a.ld = ld;
@@ -605,7 +707,11 @@ hipError_t launch_scan_topk(const void *xb, int storage, int64_t ld, const float
     a.metric = metric;
     a.cand_v = cand_v;
     a.cand_i = cand_i;
-    return launch_scan_mode<0>(xb, storage, ld, xn, n, pq, plan, a, st);
+    a.gthr = gthr;
+    a.kk_final = plan.kk_final;
+    a.publish_block = 4 * plan.kk >= plan.kk_final;
+    a.lbound = plan.kk < plan.kk_final ? lbound : nullptr;
+    return launch_scan_mode<0>(storage, pq, plan, a, st);
 }
 
 hipError_t launch_scan_range(const void *xb, int storage, int64_t ld, const float *xn, int64_t n,
@@ -625,13 +731,14 @@ hipError_t launch_scan_range(const void *xb, int storage, int64_t ld, const floa
     a.kk = plan.kk;
     a.cap = plan.cap;
     a.metric = metric;
+    a.kk_final = plan.kk;
     a.athr = athr;
     a.self_join = self_join;
     a.out_q = out_q;
     a.out_i = out_i;
     a.count = count;
     a.out_cap = cap;
-    return launch_scan_mode<1>(xb, storage, ld, xn, n, pq, plan, a, st);
+    return launch_scan_mode<1>(storage, pq, plan, a, st);
 }
 
 // ---------------------------------------------------------------------------
@@ -704,6 +811,11 @@ struct MergeKArgs {
     int64_t nsplit;
     const float *cand_v;
     const int32_t *cand_i;
+    const uint32_t *gthr;
+    int kl;               // entries per list (<= kk)
+    const float *lbound;  // per-list own thresholds, or null
+    int32_t *vf_count;    // queries whose lists may have dropped a winner
+    int32_t *vf_list;
     int64_t k;
     float *D;
     int32_t *I;
@@ -715,7 +827,7 @@ struct MergeKArgs {
     int32_t *fb_list;
 };
 
-constexpr int kMergeBuf = 2048;
+constexpr int kMergeBuf = 4096;
 
 template <int ST, int MODE>
 __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
@@ -730,9 +842,10 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
     const int64_t qg = blockIdx.x;
     const int tid = threadIdx.x;
     const int kk = a.kk;
+    const int kl = a.kl;
     const int64_t qblk = qg / a.bn, q = qg % a.bn;
     const int64_t nlists = a.nsplit * 4;
-    const int64_t total = nlists * kk;
+    const int64_t total = nlists * kl;
 
     for (int t = tid; t < kk; t += 256) {
         bv[t] = VS_INF;
@@ -746,23 +859,36 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
     for (int64_t j = tid; j < a.ld; j += 256) qsh[j] = j < a.d ? a.qf[qg * a.d + j] : 0.0f;
     __syncthreads();
 
-    for (int64_t base = 0; base < total; base += 256) {
-        const int64_t e = base + tid;
+    // entries above the query's final shared threshold cannot be among the
+    // kk best (at least kk candidates lie at or below it); each thread reads
+    // 4 adjacent entries of one list per step (kl is a multiple of 4)
+    const float tfinal = a.gthr ? dec_order(a.gthr[qg]) : VS_INF;
+    for (int64_t base = 0; base < total; base += 1024) {
+        const int64_t e = base + 4 * tid;
         if (e < total) {
-            const int64_t list = e / kk, j = e % kk;
+            const int64_t list = e / kl, j = e % kl;
             const int64_t split = list >> 2, w = list & 3;
             const int64_t off = (((qblk * a.nsplit + split) * 4 + w) * a.bn + q) * a.cap + j;
-            const float v = a.cand_v[off];
-            const int id = a.cand_i[off];
-            if (id >= 0 && (v < s_thr || (v == s_thr && id < s_thr_id))) {
-                const int pos = atomicAdd(&s_cnt, 1);
-                bv[kk + pos] = v;
-                bi[kk + pos] = id;
+            const float4 v4 = *(const float4 *)(a.cand_v + off);
+            const int4 i4 = *(const int4 *)(a.cand_i + off);
+            const float vs4[4] = {v4.x, v4.y, v4.z, v4.w};
+            const int is4[4] = {i4.x, i4.y, i4.z, i4.w};
+            const float th = s_thr;
+            const int thi = s_thr_id;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float v = vs4[u];
+                const int id = is4[u];
+                if (id >= 0 && v <= tfinal && (v < th || (v == th && id < thi))) {
+                    const int pos = atomicAdd(&s_cnt, 1);
+                    bv[kk + pos] = v;
+                    bi[kk + pos] = id;
+                }
             }
         }
         __syncthreads();
         const int c = s_cnt;
-        if (c > kMergeBuf - kk - 256 || (base + 256 >= total && c > 0)) {
+        if (c > kMergeBuf - kk - 1024 || (base + 1024 >= total && c > 0)) {
             int sz = 1;
             while (sz < kk + c) sz <<= 1;
             for (int t = kk + c + tid; t < sz; t += 256) {
@@ -776,7 +902,26 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
                 s_thr = bv[kk - 1];
                 s_thr_id = bi[kk - 1];
             }
-            __syncthreads();
+        }
+        __syncthreads();
+    }
+
+    // Lists that kept only kl < kk entries dropped rows at or above their own
+    // final threshold; the merged result is exact when none of those
+    // thresholds is below the kk-th kept value.  Otherwise flag the query.
+    if (MODE == 0 && a.lbound) {
+        __shared__ float s_lmin[4];
+        float lmin = VS_INF;
+        for (int64_t l = tid; l < nlists; l += 256) {
+            const int64_t split = l >> 2, w = l & 3;
+            lmin = fminf(lmin, a.lbound[((qblk * a.nsplit + split) * 4 + w) * a.bn + q]);
+        }
+        for (int o = 32; o > 0; o >>= 1) lmin = fminf(lmin, __shfl_xor(lmin, o));
+        if ((tid & 63) == 0) s_lmin[tid >> 6] = lmin;
+        __syncthreads();
+        if (tid == 0) {
+            const float m = fminf(fminf(s_lmin[0], s_lmin[1]), fminf(s_lmin[2], s_lmin[3]));
+            if (m < bv[kk - 1]) a.vf_list[atomicAdd(a.vf_count, 1)] = (int32_t)qg;
         }
     }
 
@@ -856,8 +1001,9 @@ static size_t merge_lds(int64_t ld) { return (size_t)kMergeBuf * 8 + (size_t)ld 
 
 hipError_t launch_merge_refine(const void *xb, int storage, int64_t ld, int64_t d, int metric,
                                const PreparedQueries &pq, const ScanPlan &plan,
-                               const float *cand_v, const int32_t *cand_i, int64_t k, float *D,
-                               int32_t *I, hipStream_t st) {
+                               const float *cand_v, const int32_t *cand_i, const uint32_t *gthr,
+                               const float *lbound, int32_t *vf_count, int32_t *vf_list,
+                               int64_t k, float *D, int32_t *I, hipStream_t st) {
     if (pq.nq <= 0) return hipSuccess;
     MergeKArgs a{};
     a.xb = xb;
@@ -867,11 +1013,16 @@ hipError_t launch_merge_refine(const void *xb, int storage, int64_t ld, int64_t 
     a.qf = pq.qf;
     a.nq = pq.nq;
     a.bn = plan.bn;
-    a.kk = plan.kk;
+    a.kk = plan.kk_final;
+    a.kl = plan.kk;
     a.cap = plan.cap;
     a.nsplit = plan.nsplit;
     a.cand_v = cand_v;
     a.cand_i = cand_i;
+    a.gthr = gthr;
+    a.lbound = plan.kk < plan.kk_final ? lbound : nullptr;
+    a.vf_count = vf_count;
+    a.vf_list = vf_list;
     a.k = k;
     a.D = D;
     a.I = I;
@@ -888,7 +1039,8 @@ hipError_t launch_merge_refine(const void *xb, int storage, int64_t ld, int64_t 
 
 hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, const float *cen,
                               int64_t K, const float *cand_v, const int32_t *cand_i,
-                              const ScanPlan &plan, float bound, const float *qf, int32_t *assign,
+                              const uint32_t *gthr, const ScanPlan &plan, float bound,
+                              const float *qf, int32_t *assign,
                               double *best_sq, int32_t *fallback_count, int32_t *fallback_list,
                               hipStream_t st) {
     (void)x;
@@ -902,11 +1054,13 @@ hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, 
     a.qf = qf;
     a.nq = n;
     a.bn = plan.bn;
-    a.kk = plan.kk;
+    a.kk = plan.kk_final;
+    a.kl = plan.kk;
     a.cap = plan.cap;
     a.nsplit = plan.nsplit;
     a.cand_v = cand_v;
     a.cand_i = cand_i;
+    a.gthr = gthr;
     a.bound = bound;
     a.assign = assign;
     a.best_sq = best_sq;

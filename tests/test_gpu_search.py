@@ -243,3 +243,25 @@ def test_faisdart_fixtures(vs):
         assert list(r.ids[:, 0]) == list(range(20))
         Dr, Ir = oracle.flat_search(xb, xb, 5, 1, 1)
         assert_knn_parity(r.distances, r.ids, Dr, Ir, 1)
+
+
+@pytest.mark.parametrize("k", [10, 50, 100])
+def test_short_lists_are_verified(vs, monkeypatch, k):
+    """Per-wave lists may keep fewer than the merged candidates; the merge
+    proves no list dropped a winner or re-runs the query with full lists.
+    Rows sorted by distance to query 0 put all its winners in one list, and a
+    forced 4-entry list keep makes the proof fail: the re-run must still
+    give the oracle's answer."""
+    g = syn.rng(21, 0)
+    xq = g.standard_normal((3, 32)).astype(np.float32)
+    xb = g.standard_normal((8000, 32)).astype(np.float32)
+    xb = xb[np.argsort(((xb.astype(np.float64) - xq[0]) ** 2).sum(1), kind="stable")]
+    monkeypatch.setenv("VS_SCAN_KKW", "4")
+    idx = vs.GpuIndexFlat.l2(32, storage="f32")
+    idx.add(xb)
+    r = idx.search(xq, k)
+    reruns, _ = idx.prof_get("fallback")
+    idx.close()
+    Dr, Ir = oracle.flat_search(xb, xq, k, 0, NT)
+    assert_knn_parity(r.distances, r.ids, Dr, Ir, 0)
+    assert reruns >= 1
