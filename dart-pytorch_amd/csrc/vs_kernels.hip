@@ -571,20 +571,18 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanKArgs a) {
         }
         if (!__ballot(pass)) continue;
 
-#pragma unroll
-        for (int tm = 0; tm < TM; ++tm) {
-            const int64_t rbase = t0 + tm * 16 + 4 * g;
-            if constexpr (MODE == 0) {
-                // make room: a list a 16-row block could overflow is cut back
-                // to its kk best first
+        if constexpr (MODE == 0) {
+            // make room: a list this tile could overflow (a query gains at
+            // most 16 * TM entries per tile) is cut back to its kk best first
+            {
                 bool need = false;
                 if (g == 0) {
 #pragma unroll
-                    for (int qb = 0; qb < NQB; ++qb) need |= cnt_w[qb * 16 + r16] > a.cap - 16;
+                    for (int qb = 0; qb < NQB; ++qb) need |= cnt_w[qb * 16 + r16] > a.cap - 16 * TM;
                 }
                 if (__ballot(need)) {
                     for (int q = 0; q < BN; ++q) {
-                        if (cnt_w[q] > a.cap - 16)
+                        if (cnt_w[q] > a.cap - 16 * TM)
                             flush_list(cv + (int64_t)q * a.cap, ci + (int64_t)q * a.cap, &cnt_w[q],
                                        &thr_w[q], &thr[q], BN, &a.gthr[q0 + q], sv_w, si_w, a.cap,
                                        a.kk, a.kk_final, a.publish_block, lane);
@@ -593,28 +591,50 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanKArgs a) {
                     for (int qb = 0; qb < NQB; ++qb)
                         thr_r[qb] = fminf(thr_r[qb], thr_w[qb * 16 + r16]);
                 }
+            }
+            // append: one LDS reservation per lane and query block for all of
+            // the lane's passing values, visiting only blocks with a pass
 #pragma unroll
-                for (int qb = 0; qb < NQB; ++qb) {
-                    const int q = qb * 16 + r16;
+            for (int qb = 0; qb < NQB; ++qb) {
+                int c = 0;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const float v = acc[tm][qb][i];
-                        if (v < thr_r[qb]) {
-                            const int pos = atomicAdd(&cnt_w[q], 1);
-                            cv[(int64_t)q * a.cap + pos] = v;
-                            ci[(int64_t)q * a.cap + pos] = (int32_t)(rbase + i);
+                for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) c += acc[tm][qb][i] < thr_r[qb] ? 1 : 0;
+                if (!__ballot(c > 0)) continue;
+                const int q = qb * 16 + r16;
+                if (c > 0) {
+                    int pos = atomicAdd(&cnt_w[q], c);
+                    float *cvq = cv + (int64_t)q * a.cap;
+                    int32_t *ciq = ci + (int64_t)q * a.cap;
+#pragma unroll
+                    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const float v = acc[tm][qb][i];
+                            if (v < thr_r[qb]) {
+                                cvq[pos] = v;
+                                ciq[pos] = (int32_t)(t0 + tm * 16 + 4 * g + i);
+                                ++pos;
+                            }
                         }
-                    }
                 }
-                lds_wave_sync();
-            } else {
+            }
+            lds_wave_sync();
+        } else {
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm) {
+                const int64_t rbase = t0 + tm * 16 + 4 * g;
 #pragma unroll
                 for (int qb = 0; qb < NQB; ++qb) {
+                    const f32x4_t v4 = acc[tm][qb];
+                    const float m4 = fminf(fminf(v4[0], v4[1]), fminf(v4[2], v4[3]));
+                    if (!__ballot(m4 <= thr_r[qb])) continue;
                     const int64_t qg = q0 + qb * 16 + r16;
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int64_t row = rbase + i;
-                        if (acc[tm][qb][i] <= thr_r[qb] && (!a.self_join || row > qg)) {
+                        if (v4[i] <= thr_r[qb] && (!a.self_join || row > qg)) {
                             const unsigned long long pos = atomicAdd(a.count, 1ull);
                             if (pos < (unsigned long long)a.out_cap) {
                                 a.out_q[pos] = (int32_t)qg;
