@@ -154,6 +154,18 @@ struct ProfScope {
     }
 };
 
+// Counts which scan variant a launch used (always on; read back through
+// vs_prof_get with the families "tiled" and "streamed").
+void note_scan_kind(vs_index *x, const vs::ScanPlan &plan) {
+    x->prof[plan.kind == 1 ? "tiled" : "streamed"].launches++;
+    if (plan.kind == 1) {  // and per tiled shape, e.g. "tile:1,1,4,2,64,4"
+        char key[64];
+        snprintf(key, sizeof key, "tile:%d,%d,%d,%d,%d,%d", plan.tile_st, plan.tile_pb,
+                 plan.bn / 32, plan.tile_rb, plan.tile_kc, plan.lw);
+        x->prof[key].launches++;
+    }
+}
+
 void prof_collect(vs_index *x) {
     if (x->pending.empty()) return;
     (void)hipStreamSynchronize(x->st);
@@ -176,7 +188,7 @@ int check_index(const vs_index *x) {
 }
 
 // Grows device storage to hold `need` rows; rows past ntotal stay zero and
-// kRowCapAlign slack rows follow the capacity so whole-tile reads of the
+// kRowSlack slack rows follow the capacity so whole-tile reads of the
 // last rows stay inside the allocation.
 int ensure_capacity(vs_index *x, int64_t need) {
     if (need <= x->cap) return VS_OK;
@@ -186,8 +198,8 @@ int ensure_capacity(vs_index *x, int64_t need) {
     const int64_t rb = row_bytes(x);
     void *nxb = nullptr;
     float *nxn = nullptr;
-    const size_t xbytes = (size_t)(nc + kRowCapAlign) * rb;
-    const size_t nbytes = (size_t)(nc + kRowCapAlign) * sizeof(float);
+    const size_t xbytes = (size_t)(nc + kRowSlack) * rb;
+    const size_t nbytes = (size_t)(nc + kRowSlack) * sizeof(float);
     VS_HIP(hipMalloc(&nxb, xbytes), "allocating vector storage");
     if (hipMalloc((void **)&nxn, nbytes) != hipSuccess) {
         (void)hipFree(nxb);
@@ -240,8 +252,8 @@ int widen_storage(vs_index *x) {
     const int64_t nc = std::max<int64_t>(x->cap, 1024);
     void *nxb = nullptr;
     float *nxn = nullptr;
-    const size_t xbytes = (size_t)(nc + kRowCapAlign) * new_ld * 4;
-    const size_t nbytes = (size_t)(nc + kRowCapAlign) * sizeof(float);
+    const size_t xbytes = (size_t)(nc + kRowSlack) * new_ld * 4;
+    const size_t nbytes = (size_t)(nc + kRowSlack) * sizeof(float);
     VS_HIP(hipMalloc(&nxb, xbytes), "allocating fp32 storage");
     if (hipMalloc((void **)&nxn, nbytes) != hipSuccess) {
         (void)hipFree(nxb);
@@ -301,6 +313,93 @@ int env_int(const char *name, int dflt) {
     return v && *v ? atoi(v) : dflt;
 }
 
+// Tiled-scan planning (large batches): picks the first built shape (query
+// blocks, row blocks, K-chunk, waves) whose resident query planes fit the
+// LDS, then the number of database splits so that the grid fills whole
+// rounds of workgroups.  Knobs (for sweeps): VS_TILE (1 enables),
+// VS_TILE_MIN_NQ (smallest batch that uses it), VS_TILE_QB / VS_TILE_RB /
+// VS_TILE_KC / VS_TILE_NW (force a shape), VS_TILE_ROUNDS (target workgroups
+// per CU), VS_TILE_GROUP (query blocks per XCD group).
+bool plan_tile(const vs_index *x, int64_t nq, int64_t nrows, int planes, int storage,
+               vs::ScanPlan *p) {
+    // opt-in until it outruns the streaming scan on the measured workloads
+    if (!env_int("VS_TILE", 0) || nq < env_int("VS_TILE_MIN_NQ", 256)) return false;
+    struct Shape {
+        int st, pb, qb, rb, kc, nw;
+    };
+#define VS_SHAPE_ENTRY(ST_, PB_, QB_, RB_, KC_, NW_) {ST_, PB_, QB_, RB_, KC_, NW_},
+    static const Shape shapes[] = {VS_TILE_SHAPES(VS_SHAPE_ENTRY)};
+#undef VS_SHAPE_ENTRY
+    const int fqb = env_int("VS_TILE_QB", 0), frb = env_int("VS_TILE_RB", 0);
+    const int fkc = env_int("VS_TILE_KC", 0), fnw = env_int("VS_TILE_NW", 0);
+    const Shape *pick = nullptr;
+    int cap = 0;
+    size_t lds = 0;
+    for (const Shape &sh : shapes) {
+        if (sh.st != storage || sh.pb != planes) continue;
+        if (fqb && sh.qb != fqb) continue;
+        if (frb && sh.rb != frb) continue;
+        if (fkc && sh.kc != fkc) continue;
+        if (fnw && sh.nw != fnw) continue;
+        if (x->ld % (2 * sh.kc)) continue;  // >= 2 whole K-chunks per row
+        // a wave may append up to 32 * rb entries per query and row tile
+        cap = (int)next_pow2(p->kk + 32 * sh.rb + 16);
+        lds = vs::tile_lds_bytes(sh.qb, sh.pb, sh.nw, cap, x->ld);
+        if (lds > x->lds_max) continue;
+        pick = &sh;
+        break;
+    }
+    if (!pick) return false;
+    p->kind = 1;
+    p->cap = cap;
+    p->bn = 32 * pick->qb;
+    p->tile_rb = pick->rb;
+    p->tile_kc = pick->kc;
+    p->lw = pick->nw;
+    p->tile_st = pick->st;
+    p->tile_pb = pick->pb;
+    p->nks = 0;
+    p->lds_bytes = lds;
+    p->nqblk = (nq + p->bn - 1) / p->bn;
+    // query blocks per XCD group: the workgroups running together on an XCD
+    // share each database row they read through its L2
+    p->tile_group = std::max<int64_t>(1, std::min<int64_t>(p->nqblk, env_int("VS_TILE_GROUP", 32)));
+    const int64_t tile_rows = (int64_t)pick->nw * 32 * pick->rb;
+    const int64_t ncu = (int64_t)std::max(1, x->num_cu);
+    const int64_t max_split = std::max<int64_t>(1, nrows / (tile_rows * 4));
+    const int64_t rounds = env_int("VS_TILE_ROUNDS", 2);
+    // smallest split count whose grid covers the target rounds of CUs and
+    // fills >= 90% of its last round; else the best fill seen
+    int64_t best = 1;
+    double best_score = -1.0;
+    for (int64_t ns = 1; ns <= max_split; ++ns) {
+        const int64_t blocks = p->nqblk * ns;
+        const double eff = (double)blocks / (double)(((blocks + ncu - 1) / ncu) * ncu);
+        if (blocks >= rounds * ncu && eff >= 0.9) {
+            best = ns;
+            break;
+        }
+        const double score = std::min(1.0, (double)blocks / (double)(rounds * ncu)) * eff;
+        if (score > best_score) {
+            best_score = score;
+            best = ns;
+        }
+        if (blocks >= 4 * rounds * ncu) break;
+    }
+    int64_t rps = round_up((nrows + best - 1) / best, tile_rows);
+    if (rps <= 0) rps = tile_rows;
+    p->rows_per_split = rps;
+    p->nsplit = std::max<int64_t>(1, (nrows + rps - 1) / rps);
+    if (env_int("VS_DEBUG_PLAN", 0))
+        fprintf(stderr,
+                "[vs plan] tiled nq=%lld rows=%lld bn=%d rb=%d kc=%d nw=%d group=%lld kk=%d "
+                "kk_final=%d cap=%d nqblk=%lld nsplit=%lld rows/split=%lld lds=%zu\n",
+                (long long)nq, (long long)nrows, p->bn, p->tile_rb, p->tile_kc, p->lw,
+                (long long)p->tile_group, p->kk, p->kk_final, p->cap, (long long)p->nqblk,
+                (long long)p->nsplit, (long long)p->rows_per_split, p->lds_bytes);
+    return true;
+}
+
 // Scan planning.  kk_final candidates per query survive the merge; each
 // wave's list keeps kk of them: kk_final itself up to 32, else kk_final / 4
 // (then four lists of a block together bound the kk_final-th value, and the
@@ -319,8 +418,12 @@ int plan_scan(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t 
     p->kk_final = (int)kk_final;
     p->kk = (int)kk;
     p->cap = (int)next_pow2(kk + 48);
-    p->tm = env_int("VS_SCAN_TM", 2);
+    // 16-row blocks per wave tile: one for short rows (d <= 128: measured
+    // faster on 1M x 128, the epilogue dominates), two otherwise
+    p->tm = env_int("VS_SCAN_TM", x->ld <= 128 && storage == 1 ? 1 : 2);
     if (p->tm != 1 && p->tm != 2 && p->tm != 4) p->tm = 2;
+    p->kind = 0;
+    if (plan_tile(x, nq, nrows, planes, storage, p)) return VS_OK;
     const int nks = (int)(x->ld / 32);
     const int force_bn = env_int("VS_SCAN_BN", 0);
     const int cands[3] = {64, 32, 16};
@@ -352,13 +455,34 @@ int plan_scan(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t 
     if (rps <= 0) rps = tile_rows;
     p->rows_per_split = rps;
     p->nsplit = std::max<int64_t>(1, (nrows + rps - 1) / rps);
+    if (env_int("VS_DEBUG_PLAN", 0))
+        fprintf(stderr,
+                "[vs plan] streamed nq=%lld rows=%lld bn=%d tm=%d nks=%d kk=%d kk_final=%d cap=%d "
+                "nqblk=%lld nsplit=%lld rows/split=%lld lds=%zu\n",
+                (long long)nq, (long long)nrows, p->bn, p->tm, p->nks, p->kk, p->kk_final, p->cap,
+                (long long)p->nqblk, (long long)p->nsplit, (long long)p->rows_per_split,
+                p->lds_bytes);
+    return VS_OK;
+}
+
+// Rows of prepared queries (and of the per-query shared thresholds): a
+// multiple of 256 plus 256 spare rows, so the query blocks of any scan plan
+// -- nqblk * bn <= nq + bn - 1 with bn <= 256, and bn need not divide 256 --
+// lie inside the buffers.  scan_fits() checks every plan against it.
+int64_t query_pad(int64_t nq) { return round_up(std::max<int64_t>(nq, 1), 256) + 256; }
+
+int scan_fits(const vs::ScanPlan &plan, const vs::PreparedQueries &pq) {
+    if (plan.bn > 256 || plan.nqblk * plan.bn > pq.nq_pad)
+        return set_err(VS_ERR_UNSUPPORTED,
+                       "internal: scan plan covers %lld query rows, only %lld are prepared",
+                       (long long)(plan.nqblk * plan.bn), (long long)pq.nq_pad);
     return VS_OK;
 }
 
 int prepare_queries(vs_index *x, const void *q_dev, int q_dtype, int64_t stride, int64_t nq,
                     vs::PreparedQueries *pq, uint32_t *flags_out) {
     pq->nq = nq;
-    pq->nq_pad = round_up(std::max<int64_t>(nq, 1), 64);
+    pq->nq_pad = query_pad(nq);
     VS_HIP(x->qp.ensure((size_t)pq->nq_pad * 2 * x->ld * 2), "query planes");
     VS_HIP(x->qf.ensure((size_t)std::max<int64_t>(nq, 1) * x->d * 4), "query copy");
     VS_HIP(x->qnorm.ensure((size_t)pq->nq_pad * 4), "query norms");
@@ -414,7 +538,8 @@ int search_device(vs_index *x, const void *q_dev, int q_dtype, int64_t nq, int64
     vs::ScanPlan plan;
     rc = plan_scan(x, nq, x->ntotal, pq.planes, kk, x->storage, &plan, safe);
     if (rc) return rc;
-    const size_t nlists = (size_t)plan.nqblk * plan.nsplit * 4 * plan.bn;
+    if ((rc = scan_fits(plan, pq))) return rc;
+    const size_t nlists = (size_t)plan.nqblk * plan.nsplit * plan.lw * plan.bn;
     const size_t nlist = nlists * plan.cap;
     VS_HIP(x->cand_v.ensure(nlist * 4), "candidate lists");
     VS_HIP(x->cand_i.ensure(nlist * 4), "candidate lists");
@@ -427,6 +552,7 @@ int search_device(vs_index *x, const void *q_dev, int q_dtype, int64_t nq, int64
         VS_HIP(x->vf.ensure((size_t)(nq + 1) * 4), "verification list");
         VS_HIP(hipMemsetAsync(x->vf.p, 0, 4, x->st), "verification count");
     }
+    note_scan_kind(x, plan);
     {
         ProfScope ps(x, "scan");
         VS_HIP(vs::launch_scan_topk(x->xb, x->storage, x->ld, x->xn, x->ntotal, x->metric, pq, plan,
@@ -509,6 +635,7 @@ int range_core(vs_index *x, const vs::PreparedQueries &pq, double radius, int se
     vs::ScanPlan plan;
     int rc = plan_scan(x, pq.nq, x->ntotal, pq.planes, 8, x->storage, &plan);
     if (rc) return rc;
+    if ((rc = scan_fits(plan, pq))) return rc;
     const float xmax = xnorm_max(x);
     VS_HIP(x->athr.ensure((size_t)pq.nq * 4), "range bounds");
     const int exact_q = (qflags & vs::kFlagNotBf16) ? 0 : 1;
@@ -523,6 +650,7 @@ int range_core(vs_index *x, const vs::PreparedQueries &pq, double radius, int se
         VS_HIP(x->rq.ensure((size_t)cap * 4), "range candidates");
         VS_HIP(x->ri.ensure((size_t)cap * 4), "range candidates");
         VS_HIP(hipMemsetAsync(x->rcount.p, 0, sizeof(unsigned long long), x->st), "range counter");
+        note_scan_kind(x, plan);
         {
             ProfScope ps(x, self_join ? "join" : "range");
             VS_HIP(vs::launch_scan_range(x->xb, x->storage, x->ld, x->xn, x->ntotal, pq, plan,
@@ -787,8 +915,8 @@ int vs_index_remove_ids(vs_index *x, const int64_t *ids, int64_t n, int64_t *nre
     const int64_t rb = row_bytes(x);
     void *nxb = nullptr;
     float *nxn = nullptr;
-    const size_t xbytes = (size_t)(x->cap + kRowCapAlign) * rb;
-    const size_t nbytes = (size_t)(x->cap + kRowCapAlign) * 4;
+    const size_t xbytes = (size_t)(x->cap + kRowSlack) * rb;
+    const size_t nbytes = (size_t)(x->cap + kRowSlack) * 4;
     VS_HIP(hipMalloc(&nxb, xbytes), "removeIds storage");
     if (hipMalloc((void **)&nxn, nbytes) != hipSuccess) {
         (void)hipFree(nxb);
@@ -962,10 +1090,10 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     std::vector<float> cen_in(centroids_in, centroids_in + K * d);  // centroids_out may alias
 
     // centroid storage: fp32 rows of ld, slack rows zero, plus norms
-    VS_HIP(x->km_cen.ensure((size_t)(K + kRowCapAlign) * ld * 4), "centroid storage");
-    VS_HIP(x->km_cxn.ensure((size_t)(K + kRowCapAlign) * 4), "centroid norms");
-    VS_HIP(hipMemsetAsync(x->km_cen.p, 0, (size_t)(K + kRowCapAlign) * ld * 4, x->st), "clear");
-    VS_HIP(hipMemsetAsync(x->km_cxn.p, 0, (size_t)(K + kRowCapAlign) * 4, x->st), "clear");
+    VS_HIP(x->km_cen.ensure((size_t)(K + kRowSlack) * ld * 4), "centroid storage");
+    VS_HIP(x->km_cxn.ensure((size_t)(K + kRowSlack) * 4), "centroid norms");
+    VS_HIP(hipMemsetAsync(x->km_cen.p, 0, (size_t)(K + kRowSlack) * ld * 4, x->st), "clear");
+    VS_HIP(hipMemsetAsync(x->km_cxn.p, 0, (size_t)(K + kRowSlack) * 4, x->st), "clear");
     VS_HIP(x->stage.ensure((size_t)K * d * 4), "centroid staging");
     VS_HIP(hipMemcpyAsync(x->stage.p, cen_in.data(), (size_t)K * d * 4, hipMemcpyHostToDevice,
                           x->st),
@@ -994,12 +1122,14 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     vs::ScanPlan plan;
     rc = plan_scan(&cview, n, K, pq.planes, 16, 0, &plan);
     if (rc) return rc;
-    const size_t nlist = (size_t)plan.nqblk * plan.nsplit * 4 * plan.bn * plan.cap;
+    if ((rc = scan_fits(plan, pq))) return rc;
+    const size_t nlist = (size_t)plan.nqblk * plan.nsplit * plan.lw * plan.bn * plan.cap;
     VS_HIP(x->cand_v.ensure(nlist * 4), "candidate lists");
     VS_HIP(x->cand_i.ensure(nlist * 4), "candidate lists");
     VS_HIP(x->gthr.ensure((size_t)pq.nq_pad * 4), "shared thresholds");
     VS_HIP(hipMemsetD32Async((hipDeviceptr_t)x->gthr.p, (int)vs::kGthrInit, (size_t)pq.nq_pad, x->st),
            "shared thresholds");
+    note_scan_kind(x, plan);
     {
         ProfScope ps(x, "assign");
         VS_HIP(vs::launch_scan_topk(x->km_cen.p, 0, ld, x->km_cxn.as<float>(), K, 0, pq, plan,

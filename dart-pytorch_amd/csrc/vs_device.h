@@ -1,0 +1,175 @@
+// vs_device.h -- device helpers shared by the scan kernels of libvs_hip.so.
+#pragma once
+
+#include <limits.h>
+
+#include "vs_internal.h"
+
+namespace vs {
+
+#define VS_INF __builtin_huge_valf()
+
+// Lane-group synchronisation for data exchanged through LDS or global
+// memory between lanes of one wave (all waves of a workgroup share the CU's
+// L1, so workgroup-scope fences order both).
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// Orders LDS accesses between lanes of one wave: LDS instructions of a wave
+// execute in order, so only the compiler must not move them across.
+__device__ __forceinline__ void lds_wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
+// ---------------------------------------------------------------------------
+// Wave-level bitonic sort of (v, i) pairs in LDS, ascending by (v, i).
+// ---------------------------------------------------------------------------
+__device__ inline void bitonic_sort_wave(float *sv, int *si, int n, int lane) {
+    for (int size = 2; size <= n; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int t = lane; t < (n >> 1); t += 64) {
+                const int i = 2 * t - (t & (stride - 1));
+                const int j = i + stride;
+                const bool asc = (i & size) == 0;
+                const float vi = sv[i], vj = sv[j];
+                const int ii = si[i], ij = si[j];
+                const bool gt = vi > vj || (vi == vj && ii > ij);
+                if (gt == asc) {
+                    sv[i] = vj;
+                    sv[j] = vi;
+                    si[i] = ij;
+                    si[j] = ii;
+                }
+            }
+            lds_wave_sync();
+        }
+    }
+}
+
+struct ScanKArgs {
+    const void *xb;
+    int64_t ld;
+    const float *xn;
+    int64_t n;
+    const uint16_t *qp;
+    int64_t nq;
+    int64_t nqblk, nsplit, rows_per_split;
+    int64_t qgroup;      // tiled scan: query blocks per XCD group
+    int kk, cap, metric;
+    int kk_final;        // candidates the merge keeps per query
+    int publish_block;   // 4 * kk >= kk_final: a block's four lists bound the kk_final-th value
+    float *lbound;       // per list: its own final threshold (verification of kk < kk_final)
+    float *cand_v;
+    int32_t *cand_i;
+    uint32_t *gthr;  // per-query threshold shared by every list (order-preserving code)
+    const float *athr;
+    int self_join;
+    int32_t *out_q, *out_i;
+    unsigned long long *count;
+    int64_t out_cap;
+};
+
+// Order-preserving map of finite floats to uint32 (a < b  <=>  enc(a) < enc(b)),
+// so a shared threshold can be tightened with an integer atomicMin.
+__device__ __forceinline__ uint32_t enc_order(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float dec_order(uint32_t u) {
+    return __uint_as_float((u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u);
+}
+
+// Flush one (wave, query) list: sort, keep its kk best, set count and the
+// list's own threshold, and tighten the query's shared threshold with a
+// value that provably has kk_final candidates at or below it: the list's own
+// kk-th value when kk == kk_final, otherwise (4 * kk >= kk_final) the largest
+// of the four waves' thresholds of this block.  thr_q0 points at wave 0's
+// threshold of the query; waves are bn apart.
+__device__ inline void flush_list(float *cvq, int32_t *ciq, int *cnt_q, float *thr_q, const float *thr_q0,
+                           int bn, uint32_t *gthr_q, float *sv, int *si, int cap, int kk,
+                           int kk_final, int publish_block, int lane) {
+    wave_sync();  // the list's global entries were appended by other lanes
+    const int c = *cnt_q;
+    for (int j = lane; j < cap; j += 64) {
+        const bool in = j < c;
+        sv[j] = in ? cvq[j] : VS_INF;
+        si[j] = in ? ciq[j] : INT_MAX;
+    }
+    lds_wave_sync();
+    bitonic_sort_wave(sv, si, cap, lane);
+    const int keep = c < kk ? c : kk;
+    for (int j = lane; j < kk; j += 64) {
+        cvq[j] = j < keep ? sv[j] : VS_INF;
+        ciq[j] = j < keep ? si[j] : -1;
+    }
+    if (lane == 0) {
+        *cnt_q = keep;
+        if (c >= kk) {
+            const float kth = fminf(*thr_q, sv[kk - 1]);
+            *thr_q = kth;
+            if (kk >= kk_final) {
+                atomicMin(gthr_q, enc_order(kth));
+            } else if (publish_block) {
+                const float b = fmaxf(fmaxf(thr_q0[0], thr_q0[bn]), fmaxf(thr_q0[2 * bn], thr_q0[3 * bn]));
+                if (b < VS_INF) atomicMin(gthr_q, enc_order(b));
+            }
+        }
+    }
+    wave_sync();
+}
+
+__device__ __forceinline__ f32x4_t mfma_bf16(bf16x8_t a, bf16x8_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// v_mfma_f32_32x32x16_bf16.  Lane l supplies row l % 32 of A and column
+// l % 32 of B, K elements 8 * (l / 32) .. + 7 of the 16-wide K-step; it
+// receives column l % 32 of D, register v holding row
+// 8 * (v / 4) + 4 * (l / 32) + v % 4 (checked on gfx950 with a probe kernel
+// whose D equals its row index, its column index and the sum over K).
+__device__ __forceinline__ f32x16_t mfma32_bf16(bf16x8_t a, bf16x8_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Maps a flat block index to (split, query block) so that the query blocks
+// of one split land on the same XCD (blocks are dealt to the 8 XCDs round-
+// robin) back to back: they read the same database rows at about the same
+// time and share that XCD's L2.
+__device__ __forceinline__ bool map_block(int64_t nqblk, int64_t nsplit, int64_t *split,
+                                          int64_t *qblk) {
+    const int64_t total = nqblk * nsplit;
+    const int64_t per_xcd = (total + 7) / 8;
+    const int64_t w = (int64_t)(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (w >= total) return false;
+    *split = w / nqblk;
+    *qblk = w % nqblk;
+    return true;
+}
+
+// Grid of the tiled scan: the query blocks are cut into groups of qg
+// consecutive blocks, and the flat index space (group, split, query block in
+// group) is dealt to the 8 XCDs in contiguous ranges (workgroup i runs on XCD
+// i % 8).  The workgroups running together on one XCD thus cover a few
+// database splits for one group of query blocks: each database row they read
+// is shared by up to qg workgroups through that XCD's L2, and the group's
+// query planes stay resident in it.
+__host__ __device__ inline int64_t tile_grid_space(int64_t nqblk, int64_t nsplit, int64_t qg) {
+    return ((nqblk + qg - 1) / qg) * qg * nsplit;
+}
+__device__ __forceinline__ bool map_block_grouped(int64_t nqblk, int64_t nsplit, int64_t qg,
+                                                  int64_t *split, int64_t *qblk) {
+    const int64_t space = tile_grid_space(nqblk, nsplit, qg);
+    const int64_t per_xcd = (space + 7) / 8;
+    const int64_t w = (int64_t)(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (w >= space) return false;
+    const int64_t grp = w / (qg * nsplit), rem = w % (qg * nsplit);
+    *split = rem / qg;
+    *qblk = grp * qg + rem % qg;
+    return *qblk < nqblk;
+}
+
+}  // namespace vs

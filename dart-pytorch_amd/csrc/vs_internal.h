@@ -8,14 +8,20 @@
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 // Row storage is padded so that one row is a whole number of 256-byte
 // segments: the scan kernels consume rows in 64-byte K-steps, four at a time,
 // without tail handling.
 constexpr int64_t kRowAlignBytes = 256;
-// Device row capacity is a multiple of this, and rows past ntotal are zero,
-// so the last tile of a scan may read whole tiles without bounds checks.
+// Device row capacity is a multiple of kRowCapAlign; kRowSlack zero rows
+// follow the capacity (rows past ntotal are zero too), so the last row tile
+// of a scan -- at most kRowSlack rows -- may be read whole without bounds
+// checks.
 constexpr int64_t kRowCapAlign = 256;
+constexpr int64_t kRowSlack = 512;
 
 // ---------------------------------------------------------------------------
 // bf16 helpers (round to nearest even; inputs are finite)
@@ -78,6 +84,12 @@ struct ScanPlan {
     int kk_final = 16;    // candidates kept per query by the merge (power of two, >= kk)
     int cap = 64;         // per-list buffer capacity (power of two)
     int nks = 0;          // >0: queries held in registers for this many K-steps
+    int lw = 4;           // candidate lists per (workgroup, query): the workgroup's waves
+    int kind = 0;         // 0: streaming scan (vs_kernels.hip); 1: LDS-tiled scan (vs_tile.hip)
+    int tile_rb = 2;      // tiled scan: 32-row blocks per wave (row tile = 128 * tile_rb rows)
+    int tile_kc = 64;     // tiled scan: K-chunk per pipeline step (elements)
+    int tile_st = 1, tile_pb = 1;  // tiled scan: storage and query planes it was planned for
+    int64_t tile_group = 8;        // tiled scan: query blocks per XCD group (grid order)
     int64_t nqblk = 0;    // query blocks
     int64_t nsplit = 0;   // database splits
     int64_t rows_per_split = 0;
@@ -85,7 +97,7 @@ struct ScanPlan {
 };
 
 // Top-k scan: per (query block, split, wave) lists of the kk best approximate
-// candidates, written to cand_v / cand_i ([nqblk][nsplit][4][bn][cap]).
+// candidates, written to cand_v / cand_i ([nqblk][nsplit][lw][bn][cap]).
 // gthr [nq_pad] holds each query's shared threshold in an order-preserving
 // uint32 code; it must start at the code of +inf (kGthrInit).
 hipError_t launch_scan_topk(const void *xb, int storage, int64_t ld, const float *xn, int64_t n,
@@ -163,5 +175,28 @@ hipError_t launch_gen_normal(void *dst, int out_dtype, int64_t n, int64_t d, uin
 // Shape rules shared by the host planner and the kernels.
 int64_t storage_ld(int64_t d, int storage);  // elements per stored row
 size_t scan_lds_bytes(int bn, int planes, int64_t ld, int cap);
+// LDS of the tiled scan: qb query blocks of 16, rb row blocks of 16 per wave,
+// K-chunk kc, pa row planes, pb query planes, list capacity cap.
+size_t tile_lds_bytes(int qb, int pb, int nw, int cap, int64_t ld);
+
+// The built shapes of the tiled scan, in the planner's order of preference:
+// X(storage, query planes, query blocks of 32, row blocks of 32 per wave,
+//   K-chunk, waves per workgroup).  The block's query planes stay in LDS.
+#define VS_TILE_SHAPES(X)                                                                     \
+    X(1, 1, 4, 2, 64, 4)                                                                      \
+    X(1, 1, 4, 2, 32, 8)                                                                      \
+    X(1, 1, 3, 2, 64, 4)                                                                      \
+    X(1, 1, 3, 2, 32, 8)                                                                      \
+    X(1, 1, 2, 2, 64, 4)                                                                      \
+    X(1, 2, 2, 2, 64, 4)                                                                      \
+    X(0, 2, 4, 2, 32, 4)                                                                      \
+    X(0, 2, 2, 2, 32, 4)                                                                      \
+    X(0, 1, 4, 2, 32, 4)                                                                      \
+    X(0, 1, 2, 2, 32, 4)
+
+struct ScanKArgs;
+template <int MODE>
+hipError_t launch_tile_scan(int storage, int planes, const ScanPlan &plan, const ScanKArgs &args,
+                            hipStream_t st);
 
 }  // namespace vs

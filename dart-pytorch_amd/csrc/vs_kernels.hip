@@ -18,27 +18,9 @@
 #include <limits.h>
 #include <math.h>
 
-#include "vs_internal.h"
+#include "vs_device.h"
 
 namespace vs {
-
-#define VS_INF __builtin_huge_valf()
-
-// Lane-group synchronisation for data exchanged through LDS or global
-// memory between lanes of one wave (all waves of a workgroup share the CU's
-// L1, so workgroup-scope fences order both).
-__device__ __forceinline__ void wave_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-}
-
-// Orders LDS accesses between lanes of one wave: LDS instructions of a wave
-// execute in order, so only the compiler must not move them across.
-__device__ __forceinline__ void lds_wave_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-}
 
 template <typename T>
 __device__ __forceinline__ float load_f32(const T *p, int64_t i);
@@ -174,31 +156,6 @@ hipError_t launch_prepare_queries(const void *src, int src_dtype, int64_t src_st
     return hipGetLastError();
 }
 
-// ---------------------------------------------------------------------------
-// Wave-level bitonic sort of (v, i) pairs in LDS, ascending by (v, i).
-// ---------------------------------------------------------------------------
-__device__ void bitonic_sort_wave(float *sv, int *si, int n, int lane) {
-    for (int size = 2; size <= n; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int t = lane; t < (n >> 1); t += 64) {
-                const int i = 2 * t - (t & (stride - 1));
-                const int j = i + stride;
-                const bool asc = (i & size) == 0;
-                const float vi = sv[i], vj = sv[j];
-                const int ii = si[i], ij = si[j];
-                const bool gt = vi > vj || (vi == vj && ii > ij);
-                if (gt == asc) {
-                    sv[i] = vj;
-                    sv[j] = vi;
-                    si[i] = ij;
-                    si[j] = ii;
-                }
-            }
-            lds_wave_sync();
-        }
-    }
-}
-
 // Block-level bitonic sort (blockDim.x threads) of n (power of two) pairs.
 __device__ void bitonic_sort_block(float *sv, int *si, int n) {
     for (int size = 2; size <= n; size <<= 1) {
@@ -245,105 +202,15 @@ __device__ void bitonic_sort_block(float *sv, int *si, int n) {
 // MODE 1 (range): accumulators within the per-query bound are appended to a
 // global (query, id) candidate list for exact re-testing.
 // ---------------------------------------------------------------------------
-struct ScanKArgs {
-    const void *xb;
-    int64_t ld;
-    const float *xn;
-    int64_t n;
-    const uint16_t *qp;
-    int64_t nq;
-    int64_t nqblk, nsplit, rows_per_split;
-    int kk, cap, metric;
-    int kk_final;        // candidates the merge keeps per query
-    int publish_block;   // 4 * kk >= kk_final: a block's four lists bound the kk_final-th value
-    float *lbound;       // per list: its own final threshold (verification of kk < kk_final)
-    float *cand_v;
-    int32_t *cand_i;
-    uint32_t *gthr;  // per-query threshold shared by every list (order-preserving code)
-    const float *athr;
-    int self_join;
-    int32_t *out_q, *out_i;
-    unsigned long long *count;
-    int64_t out_cap;
-};
-
 // planes == 0: the queries live in registers and need no LDS copy.
 size_t scan_lds_bytes(int bn, int planes, int64_t ld, int cap) {
     return (size_t)bn * planes * (size_t)(ld + 8) * 2 + (size_t)4 * bn * 8 + (size_t)4 * cap * 8;
-}
-
-// Order-preserving map of finite floats to uint32 (a < b  <=>  enc(a) < enc(b)),
-// so a shared threshold can be tightened with an integer atomicMin.
-__device__ __forceinline__ uint32_t enc_order(float f) {
-    const uint32_t u = __float_as_uint(f);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-__device__ __forceinline__ float dec_order(uint32_t u) {
-    return __uint_as_float((u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u);
-}
-
-// Flush one (wave, query) list: sort, keep its kk best, set count and the
-// list's own threshold, and tighten the query's shared threshold with a
-// value that provably has kk_final candidates at or below it: the list's own
-// kk-th value when kk == kk_final, otherwise (4 * kk >= kk_final) the largest
-// of the four waves' thresholds of this block.  thr_q0 points at wave 0's
-// threshold of the query; waves are bn apart.
-__device__ void flush_list(float *cvq, int32_t *ciq, int *cnt_q, float *thr_q, const float *thr_q0,
-                           int bn, uint32_t *gthr_q, float *sv, int *si, int cap, int kk,
-                           int kk_final, int publish_block, int lane) {
-    wave_sync();  // the list's global entries were appended by other lanes
-    const int c = *cnt_q;
-    for (int j = lane; j < cap; j += 64) {
-        const bool in = j < c;
-        sv[j] = in ? cvq[j] : VS_INF;
-        si[j] = in ? ciq[j] : INT_MAX;
-    }
-    lds_wave_sync();
-    bitonic_sort_wave(sv, si, cap, lane);
-    const int keep = c < kk ? c : kk;
-    for (int j = lane; j < kk; j += 64) {
-        cvq[j] = j < keep ? sv[j] : VS_INF;
-        ciq[j] = j < keep ? si[j] : -1;
-    }
-    if (lane == 0) {
-        *cnt_q = keep;
-        if (c >= kk) {
-            const float kth = fminf(*thr_q, sv[kk - 1]);
-            *thr_q = kth;
-            if (kk >= kk_final) {
-                atomicMin(gthr_q, enc_order(kth));
-            } else if (publish_block) {
-                const float b = fmaxf(fmaxf(thr_q0[0], thr_q0[bn]), fmaxf(thr_q0[2 * bn], thr_q0[3 * bn]));
-                if (b < VS_INF) atomicMin(gthr_q, enc_order(b));
-            }
-        }
-    }
-    wave_sync();
 }
 
 typedef float f32x8_t __attribute__((ext_vector_type(8)));
 struct U8x2 {
     uint4 a, b;
 };
-
-__device__ __forceinline__ f32x4_t mfma_bf16(bf16x8_t a, bf16x8_t b, f32x4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-
-// Maps a flat block index to (split, query block) so that the query blocks
-// of one split land on the same XCD (blocks are dealt to the 8 XCDs round-
-// robin) back to back: they read the same database rows at about the same
-// time and share that XCD's L2.
-__device__ __forceinline__ bool map_block(int64_t nqblk, int64_t nsplit, int64_t *split,
-                                          int64_t *qblk) {
-    const int64_t total = nqblk * nsplit;
-    const int64_t per_xcd = (total + 7) / 8;
-    const int64_t w = (int64_t)(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-    if (w >= total) return false;
-    *split = w / nqblk;
-    *qblk = w % nqblk;
-    return true;
-}
 
 template <int ST>
 struct AFrag;
@@ -677,6 +544,7 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanKArgs a) {
 template <int MODE>
 static hipError_t launch_scan_mode(int storage, const PreparedQueries &pq, const ScanPlan &plan,
                                    const ScanKArgs &args, hipStream_t st) {
+    if (plan.kind == 1) return launch_tile_scan<MODE>(storage, pq.planes, plan, args, st);
     const int64_t total = plan.nqblk * plan.nsplit;
     const int64_t grid = ((total + 7) / 8) * 8;
     const size_t lds = plan.lds_bytes;
@@ -828,6 +696,7 @@ struct MergeKArgs {
     const float *qf;
     int64_t nq;
     int bn, kk, cap;
+    int lw;  // lists per (workgroup, query)
     int64_t nsplit;
     const float *cand_v;
     const int32_t *cand_i;
@@ -864,7 +733,7 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
     const int kk = a.kk;
     const int kl = a.kl;
     const int64_t qblk = qg / a.bn, q = qg % a.bn;
-    const int64_t nlists = a.nsplit * 4;
+    const int64_t nlists = a.nsplit * a.lw;
     const int64_t total = nlists * kl;
 
     for (int t = tid; t < kk; t += 256) {
@@ -887,8 +756,8 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
         const int64_t e = base + 4 * tid;
         if (e < total) {
             const int64_t list = e / kl, j = e % kl;
-            const int64_t split = list >> 2, w = list & 3;
-            const int64_t off = (((qblk * a.nsplit + split) * 4 + w) * a.bn + q) * a.cap + j;
+            const int64_t split = list / a.lw, w = list % a.lw;
+            const int64_t off = (((qblk * a.nsplit + split) * a.lw + w) * a.bn + q) * a.cap + j;
             const float4 v4 = *(const float4 *)(a.cand_v + off);
             const int4 i4 = *(const int4 *)(a.cand_i + off);
             const float vs4[4] = {v4.x, v4.y, v4.z, v4.w};
@@ -933,8 +802,8 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
         __shared__ float s_lmin[4];
         float lmin = VS_INF;
         for (int64_t l = tid; l < nlists; l += 256) {
-            const int64_t split = l >> 2, w = l & 3;
-            lmin = fminf(lmin, a.lbound[((qblk * a.nsplit + split) * 4 + w) * a.bn + q]);
+            const int64_t split = l / a.lw, w = l % a.lw;
+            lmin = fminf(lmin, a.lbound[((qblk * a.nsplit + split) * a.lw + w) * a.bn + q]);
         }
         for (int o = 32; o > 0; o >>= 1) lmin = fminf(lmin, __shfl_xor(lmin, o));
         if ((tid & 63) == 0) s_lmin[tid >> 6] = lmin;
@@ -1033,6 +902,7 @@ hipError_t launch_merge_refine(const void *xb, int storage, int64_t ld, int64_t 
     a.qf = pq.qf;
     a.nq = pq.nq;
     a.bn = plan.bn;
+    a.lw = plan.lw;
     a.kk = plan.kk_final;
     a.kl = plan.kk;
     a.cap = plan.cap;
@@ -1074,6 +944,7 @@ hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, 
     a.qf = qf;
     a.nq = n;
     a.bn = plan.bn;
+    a.lw = plan.lw;
     a.kk = plan.kk_final;
     a.kl = plan.kk;
     a.cap = plan.cap;

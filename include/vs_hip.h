@@ -173,7 +173,12 @@ VS_API int vs_gen_normal(int device, void *dst_dev, int out_dtype, int64_t n, in
 /* Per-kernel timing on the index's stream with HIP events: when enabled,
  * every launch of the named kernel family is bracketed by events and its
  * duration accumulated.  Families: "scan", "merge", "range", "assign",
- * "update", "join". */
+ * "update", "join".  The families "tiled" and "streamed" count, whether or
+ * not timing is enabled, the distance scans that ran on the LDS-tiled kernel
+ * (large batches) and on the streaming kernel (small batches); the family
+ * "tile:S,P,Q,R,K,W" counts the tiled scans of one built shape (storage,
+ * query planes, 32-query blocks, 32-row blocks per wave, K-chunk, waves per
+ * workgroup). */
 VS_API int vs_prof_enable(vs_index *idx, int on);
 VS_API int vs_prof_get(vs_index *idx, const char *family, int64_t *launches, double *total_ms);
 VS_API int vs_prof_reset(vs_index *idx);
