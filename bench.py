@@ -74,19 +74,19 @@ def run_search_workload(args, vs, syn, N):
     from vector_store import _native as NN
 
     if args.workload == "c2":
-        n, d, nq, k, metric = args.n or 1_000_000, 128, args.nq or 10_000, 100, 0
+        n, d, nq, k, metric = args.n or 1_000_000, 128, args.nq or 10_000, args.k or 100, 0
         xb = syn.int_grid(n, d, args.seed, 0)
         xq = syn.int_grid(nq, d, args.seed, 1)
         storage, qdt = "auto", NN.VS_DTYPE_F32
         desc = f"c2: exact L2 top-{k}, {n} x {d} fp32 integers 0..255, {nq} queries"
     elif args.workload == "c1":
-        n, d, nq, k, metric = args.n or 10_000, 384, args.nq or 100, 10, 1
+        n, d, nq, k, metric = args.n or 10_000, 384, args.nq or 100, args.k or 10, 1
         xb = syn.normal_unit(n, d, args.seed, 0)
         xq = syn.normal_unit(nq, d, args.seed, 1)
         storage, qdt = "f32", NN.VS_DTYPE_F32
         desc = f"c1: exact IP top-{k}, {n} x {d} fp32 unit N(0,1), {nq} queries"
     elif args.workload == "c3":
-        n, d, nq, k, metric = args.n or 20_000_000, 768, args.nq or args.batch, 10, 1
+        n, d, nq, k, metric = args.n or 20_000_000, 768, args.nq or args.batch, args.k or 10, 1
         xb = None
         xq = syn.to_bf16_bits(syn.normal_unit(nq, d, args.seed, 1))
         storage, qdt = "bf16", NN.VS_DTYPE_BF16
@@ -174,6 +174,28 @@ def run_search_workload(args, vs, syn, N):
     return out
 
 
+def run_copy_calibration(args):
+    """A plain device copy of known size (torch's copy kernel), the yardstick
+    for the FETCH_SIZE / WRITE_SIZE counters: under rocprofv3 --pmc its
+    per-dispatch KiB, divided by the bytes it must move, is the scale factor
+    applied to the scan kernel's counter readings."""
+    import torch
+
+    nbytes = (args.n or 1 << 30)
+    a = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(args.warmup):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    for _ in range(args.steps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t) / args.steps
+    return {"workload": "copy", "bytes_read": nbytes, "bytes_written": nbytes,
+            "ms": round(dt * 1e3, 4), "GBps_read_plus_write": round(2 * nbytes / dt / 1e9, 1)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -184,6 +206,7 @@ def main():
     ap.add_argument("--n", type=int, default=0)
     ap.add_argument("--nq", type=int, default=0)
     ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--k", type=int, default=0, help="override the workload's k")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
@@ -196,7 +219,10 @@ def main():
 
     if vs.device_count() < 1:
         raise SystemExit("no HIP device visible")
-    out = run_search_workload(args, vs, syn, None)
+    if args.workload == "copy":
+        out = run_copy_calibration(args)
+    else:
+        out = run_search_workload(args, vs, syn, None)
     print(json.dumps(out), flush=True)
 
 

@@ -157,7 +157,17 @@ struct ProfScope {
 // Counts which scan variant a launch used (always on; read back through
 // vs_prof_get with the families "tiled" and "streamed").
 void note_scan_kind(vs_index *x, const vs::ScanPlan &plan) {
-    x->prof[plan.kind == 1 ? "tiled" : "streamed"].launches++;
+    x->prof[plan.kind == 2 ? "gemm" : plan.kind == 1 ? "tiled" : "streamed"].launches++;
+    if (plan.kind == 2) {  // and per GEMM shape: "gemm:1,1,2,4,4,2,32" or "gemmdma:1,2,4,4,2,4"
+        char key[64];
+        if (plan.g_ns > 0)
+            snprintf(key, sizeof key, "gemmdma:%d,%d,%d,%d,%d,%d", plan.tile_pb, plan.lw,
+                     plan.g_wq, plan.tile_rb, plan.g_qb, plan.g_ns);
+        else
+            snprintf(key, sizeof key, "gemm:%d,%d,%d,%d,%d,%d,%d", plan.tile_st, plan.tile_pb,
+                     plan.lw, plan.g_wq, plan.tile_rb, plan.g_qb, plan.tile_kc);
+        x->prof[key].launches++;
+    }
     if (plan.kind == 1) {  // and per tiled shape, e.g. "tile:1,1,4,2,64,4"
         char key[64];
         snprintf(key, sizeof key, "tile:%d,%d,%d,%d,%d,%d", plan.tile_st, plan.tile_pb,
@@ -400,6 +410,129 @@ bool plan_tile(const vs_index *x, int64_t nq, int64_t nrows, int planes, int sto
     return true;
 }
 
+// GEMM-tiled planning (large batches): the first built shape for this
+// storage and query-plane count whose LDS fits, then the number of database
+// splits so that the grid fills whole rounds of workgroups.  Each query has
+// one candidate list per row wave (lw) in a workgroup, so a list keeps at
+// least kk_final / lw entries and the block's lists together bound the
+// query's kk_final-th value.  Knobs (for sweeps): VS_GEMM (0 disables),
+// VS_GEMM_MIN_NQ (smallest batch that uses it), VS_GEMM_WQ / VS_GEMM_QB /
+// VS_GEMM_KC (force a shape), VS_GEMM_ROUNDS (target workgroups per CU),
+// VS_GEMM_GROUP (query blocks per XCD group).
+// The LDS-DMA kernel (gemm_dma_kernel) is switched off: its first run on an
+// MI355X (8-wave shape, d = 200, L2, k = 10) left the GPU faulted, and no
+// mistake in its indexing, waits or barriers has been shown yet.
+constexpr bool kGemmDmaEnabled = false;
+
+bool plan_gemm(const vs_index *x, int64_t nq, int64_t nrows, int planes, int storage,
+               bool kk_forced, vs::ScanPlan *p) {
+    if (!env_int("VS_GEMM", 0) || nq < env_int("VS_GEMM_MIN_NQ", 256)) return false;
+    struct Shape {
+        int st, pb, wr, wq, rb, qb, kc;
+    };
+#define VS_GSHAPE_ENTRY(ST_, PB_, WR_, WQ_, RB_, QB_, KC_) {ST_, PB_, WR_, WQ_, RB_, QB_, KC_},
+    static const Shape shapes[] = {VS_GEMM_SHAPES(VS_GSHAPE_ENTRY)};
+#undef VS_GSHAPE_ENTRY
+    const int fwq = env_int("VS_GEMM_WQ", 0), fqb = env_int("VS_GEMM_QB", 0);
+    const int fkc = env_int("VS_GEMM_KC", 0);
+    const Shape *pick = nullptr;
+    int kk = p->kk, cap = 0, ns = 0;
+    size_t lds = 0;
+    // LDS-DMA shapes first (bf16 rows; VS_GEMM_DMA=0 disables them)
+    struct DShape {
+        int pb, wr, wq, rb, qb, ns;
+    };
+#define VS_DSHAPE_ENTRY(PB_, WR_, WQ_, RB_, QB_, NS_) {PB_, WR_, WQ_, RB_, QB_, NS_},
+    static const DShape dshapes[] = {VS_GEMM_DMA_SHAPES(VS_DSHAPE_ENTRY)};
+#undef VS_DSHAPE_ENTRY
+    static Shape dpick;
+    if (kGemmDmaEnabled && storage == 1 && env_int("VS_GEMM_DMA", 1) && (!fkc || fkc == 32) &&
+        x->ld % 32 == 0) {
+        for (const DShape &sh : dshapes) {
+            if (sh.pb != planes) continue;
+            if (fwq && sh.wq != fwq) continue;
+            if (fqb && sh.qb != fqb) continue;
+            kk = p->kk;
+            if (!kk_forced && kk < p->kk_final) kk = std::max(kk, p->kk_final / sh.wr);
+            cap = (int)next_pow2(kk + 32 * sh.rb + 16);
+            lds = vs::gemm_dma_lds_bytes(sh.pb, sh.wr, sh.wq, sh.rb, sh.qb, sh.ns, cap);
+            if (lds > x->lds_max) continue;
+            dpick = Shape{1, sh.pb, sh.wr, sh.wq, sh.rb, sh.qb, 32};
+            pick = &dpick;
+            ns = sh.ns;
+            break;
+        }
+    }
+    for (const Shape &sh : shapes) {
+        if (pick) break;
+        if (sh.st != storage || sh.pb != planes) continue;
+        if (fwq && sh.wq != fwq) continue;
+        if (fqb && sh.qb != fqb) continue;
+        if (fkc && sh.kc != fkc) continue;
+        if (x->ld % sh.kc) continue;
+        kk = p->kk;
+        if (!kk_forced && kk < p->kk_final) kk = std::max(kk, p->kk_final / sh.wr);
+        // a wave may append up to 32 * rb entries per query and row tile
+        cap = (int)next_pow2(kk + 32 * sh.rb + 16);
+        lds = vs::gemm_lds_bytes(sh.st, sh.pb, sh.wr, sh.wq, sh.rb, sh.qb, sh.kc, cap);
+        if (lds > x->lds_max) continue;
+        pick = &sh;
+        break;
+    }
+    if (!pick) return false;
+    p->kind = 2;
+    p->g_ns = ns;
+    p->kk = kk;
+    p->cap = cap;
+    p->bn = 32 * pick->wq * pick->qb;
+    p->lw = pick->wr;
+    p->g_wq = pick->wq;
+    p->g_qb = pick->qb;
+    p->tile_rb = pick->rb;
+    p->tile_kc = pick->kc;
+    p->tile_st = pick->st;
+    p->tile_pb = pick->pb;
+    p->nks = 0;
+    p->lds_bytes = lds;
+    p->nqblk = (nq + p->bn - 1) / p->bn;
+    p->tile_group = std::max<int64_t>(1, std::min<int64_t>(p->nqblk, env_int("VS_GEMM_GROUP", 32)));
+    const int64_t tile_rows = (int64_t)pick->wr * 32 * pick->rb;
+    const int64_t ncu = (int64_t)std::max(1, x->num_cu);
+    const int64_t max_split = std::max<int64_t>(1, nrows / (tile_rows * 4));
+    const int64_t rounds = env_int("VS_GEMM_ROUNDS", 2);
+    // smallest split count whose grid covers the target rounds of CUs and
+    // fills >= 90% of its last round; else the best fill seen
+    int64_t best = 1;
+    double best_score = -1.0;
+    for (int64_t ns = 1; ns <= max_split; ++ns) {
+        const int64_t blocks = p->nqblk * ns;
+        const double eff = (double)blocks / (double)(((blocks + ncu - 1) / ncu) * ncu);
+        if (blocks >= rounds * ncu && eff >= 0.9) {
+            best = ns;
+            break;
+        }
+        const double score = std::min(1.0, (double)blocks / (double)(rounds * ncu)) * eff;
+        if (score > best_score) {
+            best_score = score;
+            best = ns;
+        }
+        if (blocks >= 4 * rounds * ncu) break;
+    }
+    int64_t rps = round_up((nrows + best - 1) / best, tile_rows);
+    if (rps <= 0) rps = tile_rows;
+    p->rows_per_split = rps;
+    p->nsplit = std::max<int64_t>(1, (nrows + rps - 1) / rps);
+    if (env_int("VS_DEBUG_PLAN", 0))
+        fprintf(stderr,
+                "[vs plan] gemm ns=%d nq=%lld rows=%lld bq=%d wr=%d wq=%d rb=%d qb=%d kc=%d group=%lld "
+                "kk=%d kk_final=%d cap=%d nqblk=%lld nsplit=%lld rows/split=%lld lds=%zu\n",
+                p->g_ns, (long long)nq, (long long)nrows, p->bn, p->lw, p->g_wq, p->tile_rb, p->g_qb,
+                p->tile_kc, (long long)p->tile_group, p->kk, p->kk_final, p->cap,
+                (long long)p->nqblk, (long long)p->nsplit, (long long)p->rows_per_split,
+                p->lds_bytes);
+    return true;
+}
+
 // Scan planning.  kk_final candidates per query survive the merge; each
 // wave's list keeps kk of them: kk_final itself up to 32, else kk_final / 4
 // (then four lists of a block together bound the kk_final-th value, and the
@@ -423,6 +556,7 @@ int plan_scan(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t 
     p->tm = env_int("VS_SCAN_TM", x->ld <= 128 && storage == 1 ? 1 : 2);
     if (p->tm != 1 && p->tm != 2 && p->tm != 4) p->tm = 2;
     p->kind = 0;
+    if (plan_gemm(x, nq, nrows, planes, storage, kkw > 0 || safe, p)) return VS_OK;
     if (plan_tile(x, nq, nrows, planes, storage, p)) return VS_OK;
     const int nks = (int)(x->ld / 32);
     const int force_bn = env_int("VS_SCAN_BN", 0);

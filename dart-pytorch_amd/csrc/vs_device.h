@@ -61,7 +61,7 @@ struct ScanKArgs {
     int64_t qgroup;      // tiled scan: query blocks per XCD group
     int kk, cap, metric;
     int kk_final;        // candidates the merge keeps per query
-    int publish_block;   // 4 * kk >= kk_final: a block's four lists bound the kk_final-th value
+    int publish_block;   // nl * kk >= kk_final: a block's nl lists of a query bound its kk_final-th value
     float *lbound;       // per list: its own final threshold (verification of kk < kk_final)
     float *cand_v;
     int32_t *cand_i;
@@ -86,21 +86,26 @@ __device__ __forceinline__ float dec_order(uint32_t u) {
 // Flush one (wave, query) list: sort, keep its kk best, set count and the
 // list's own threshold, and tighten the query's shared threshold with a
 // value that provably has kk_final candidates at or below it: the list's own
-// kk-th value when kk == kk_final, otherwise (4 * kk >= kk_final) the largest
-// of the four waves' thresholds of this block.  thr_q0 points at wave 0's
-// threshold of the query; waves are bn apart.
+// kk-th value when kk == kk_final, otherwise (publish_block: nl * kk >=
+// kk_final) the largest of the thresholds of the block's nl lists of this
+// query.  thr_q0 points at list 0's threshold of the query; lists are bn
+// apart.  Every threshold is +inf until its list has held kk entries.
 __device__ inline void flush_list(float *cvq, int32_t *ciq, int *cnt_q, float *thr_q, const float *thr_q0,
-                           int bn, uint32_t *gthr_q, float *sv, int *si, int cap, int kk,
+                           int bn, int nl, uint32_t *gthr_q, float *sv, int *si, int cap, int kk,
                            int kk_final, int publish_block, int lane) {
     wave_sync();  // the list's global entries were appended by other lanes
     const int c = *cnt_q;
-    for (int j = lane; j < cap; j += 64) {
+    // sort only the smallest power of two that holds the list (<= cap)
+    int n = 2;
+    while (n < c) n <<= 1;
+    if (n > cap) n = cap;
+    for (int j = lane; j < n; j += 64) {
         const bool in = j < c;
         sv[j] = in ? cvq[j] : VS_INF;
         si[j] = in ? ciq[j] : INT_MAX;
     }
     lds_wave_sync();
-    bitonic_sort_wave(sv, si, cap, lane);
+    bitonic_sort_wave(sv, si, n, lane);
     const int keep = c < kk ? c : kk;
     for (int j = lane; j < kk; j += 64) {
         cvq[j] = j < keep ? sv[j] : VS_INF;
@@ -114,7 +119,8 @@ __device__ inline void flush_list(float *cvq, int32_t *ciq, int *cnt_q, float *t
             if (kk >= kk_final) {
                 atomicMin(gthr_q, enc_order(kth));
             } else if (publish_block) {
-                const float b = fmaxf(fmaxf(thr_q0[0], thr_q0[bn]), fmaxf(thr_q0[2 * bn], thr_q0[3 * bn]));
+                float b = thr_q0[0];
+                for (int i = 1; i < nl; ++i) b = fmaxf(b, thr_q0[i * bn]);
                 if (b < VS_INF) atomicMin(gthr_q, enc_order(b));
             }
         }

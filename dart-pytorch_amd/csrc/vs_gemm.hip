@@ -1,0 +1,817 @@
+// vs_gemm.hip -- the GEMM-tiled distance scan of libvs_hip.so for large
+// query batches (gfx950).
+//
+// One workgroup of WR x WQ waves owns a block of BQ = WQ*32*QB queries and
+// one split of the database rows, which it walks in row tiles of BR =
+// WR*32*RB rows.  Per K-chunk of KC elements both operands are staged in LDS:
+// the tile's database rows (A) and the block's prepared query planes (B),
+// each loaded once per workgroup with 16-byte global loads, so every byte
+// read from L2 feeds BQ queries (rows) or BR rows (queries).  Wave (wr, wq)
+// multiplies rows wr*32*RB .. +32*RB by queries wq*32*QB .. +32*QB with
+// v_mfma_f32_32x32x16_bf16, holding QB x RB accumulator blocks of 32 x 32.
+// Two LDS stages: while the waves multiply one K-chunk, the next chunk's
+// global loads are in flight in registers; they are written to the other
+// stage after the multiply, and one barrier per chunk orders the two.
+//
+// Operands follow the convention of the other scans (vs_kernels.hip): the
+// queries are bf16 planes of s*q (s = -2 for L2, -1 for IP) and the
+// accumulator starts at the row norm xn (L2) or 0 (IP), so it is "smaller is
+// better" for both metrics.  fp32 rows are split into bf16 hi and lo planes
+// when they are written to LDS; the products are hi*q0 + lo*q0 (+ hi*q1 when
+// the queries need a second plane).  The row norms of a tile travel with its
+// first K-chunk.
+//
+// Epilogue per row tile: per-(row wave, query) candidate lists in global
+// memory with per-query shared thresholds (MODE 0), or range appends (MODE
+// 1), read by the same merge, re-rank, k-means and range kernels as the
+// other scans.  The full distance matrix is never written.
+#include <limits.h>
+
+#include <type_traits>
+
+#include "vs_device.h"
+
+namespace vs {
+
+template <int ST, int PB, int WR, int WQ, int RB, int QB, int KC>
+struct GemmShape {
+    static constexpr int NW = WR * WQ, NT = 64 * NW;
+    static constexpr int BR = WR * 32 * RB, BQ = WQ * 32 * QB;
+    static constexpr int AP = ST == 0 ? 2 : 1;  // row planes in LDS: bf16 hi (, lo)
+    static constexpr int KP = KC + 8;           // LDS row stride in elements
+    static constexpr int ESZ = ST == 0 ? 4 : 2;  // bytes per stored element
+    static constexpr int A_CPR = KC * ESZ / 16;  // 16-byte global chunks per row and K-chunk
+    static constexpr int A_LOADS = BR * A_CPR / NT;
+    static constexpr int B_CPR = KC * 2 / 16;  // 16-byte chunks per query plane and K-chunk
+    static constexpr int B_LOADS = BQ * PB * B_CPR / NT;
+    static constexpr int STAGE_ELEMS = (AP * BR + PB * BQ) * KP;
+    static constexpr size_t STAGE_BYTES = (size_t)STAGE_ELEMS * 2 + (size_t)BR * 4;
+    static_assert(KC % 16 == 0, "K-chunk is whole MFMA K-steps");
+    static_assert(BR * A_CPR % NT == 0 && BQ * PB * B_CPR % NT == 0, "whole loads per thread");
+    static_assert(BR / 4 <= NT, "one thread per 4 row norms");
+    static_assert(BR <= kRowSlack, "the last row tile reads at most kRowSlack rows past the end");
+    static_assert((KP * 2) % 16 == 0, "16-byte aligned LDS rows");
+};
+
+size_t gemm_lds_bytes(int st, int pb, int wr, int wq, int rb, int qb, int kc, int cap) {
+    const size_t br = (size_t)wr * 32 * rb, bq = (size_t)wq * 32 * qb, kp = (size_t)kc + 8;
+    const size_t stage = ((st == 0 ? 2 : 1) * br + (size_t)pb * bq) * kp * 2 + br * 4;
+    return 2 * stage + (size_t)wr * bq * 8 + (size_t)wr * wq * cap * 8;
+}
+
+// Epilogue of one row tile (shared by both kernels).  Lane (l32, h) of wave
+// (wr, wq) holds query qw0 + 32 qb + l32 and, in register v of row block rb,
+// row wr0 + 32 rb + 8 (v / 4) + 4 h + v % 4.
+struct EpiCtx {
+    int64_t q0, r1;
+    int qw0, l32, h, lane;
+    int *cnt, *cnt_w;
+    float *thr, *thr_w, *sv_w;
+    int *si_w;
+    float *cv;
+    int32_t *ci;
+};
+
+template <int WR, int BQ, int RB, int QB, int MODE>
+__device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[QB][RB], const ScanKArgs &a,
+                                              const EpiCtx &e, int64_t wr0, float (&thr_r)[QB],
+                                              const uint32_t (&gt)[QB], bool &seeded) {
+    const int64_t q0 = e.q0, r1 = e.r1;
+    const int qw0 = e.qw0, l32 = e.l32, h = e.h, lane = e.lane;
+    int *cnt_w = e.cnt_w;
+    float *thr = e.thr, *thr_w = e.thr_w, *sv_w = e.sv_w;
+    int *si_w = e.si_w;
+    float *cv = e.cv;
+    int32_t *ci = e.ci;
+    (void)gt;
+    (void)seeded;
+    // ---- epilogue of the tile; lane (l32, h) holds query
+    // qw0 + 32 qb + l32 and, in register v of row block rb, row
+    // wr0 + 32 rb + 8 (v / 4) + 4 h + v % 4 ----
+    // rows past the split end (the last tile only) never qualify:
+    // the rare append paths test the row offset against lim; the
+    // fast min/ballot test may pass on them, which only costs time
+    const int lim = (int)min((int64_t)(32 * RB), r1 - wr0);
+    if constexpr (MODE == 0) {
+        if (!seeded && lim == 32 * RB) {
+            // First tile: instead of appending every value while the
+            // lists have no threshold, each lane finds (by bisection
+            // on the order-preserving code) a value T_lane with at
+            // least ceil(kk / 2) of its values at or below it; the
+            // list of (row wave, query) -- two lanes, h = 0 and 1 --
+            // then holds >= kk values at or below the larger of the
+            // two, which becomes its threshold, and only those are
+            // appended.  Rows past the split end hold +inf and are
+            // never appended; if they leave fewer than kk finite
+            // values, the threshold is +inf and stays unset.
+            const int need = (a.kk + 1) / 2;
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+                float fmn = VS_INF, fmx = -VS_INF;
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        fmn = fminf(fmn, acc[qb][rb][v]);
+                        fmx = fmaxf(fmx, acc[qb][rb][v]);
+                    }
+                // invariant: count(value <= dec(hi)) >= need (all 16 RB >= need)
+                uint32_t lo = enc_order(fmn), hi = enc_order(fmx);
+                for (int itb = 0; itb < 20 && lo < hi; ++itb) {
+                    const uint32_t mid = lo + ((hi - lo) >> 1);
+                    const float fm = dec_order(mid);
+                    int c = 0;
+#pragma unroll
+                    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) c += acc[qb][rb][v] <= fm ? 1 : 0;
+                    if (c >= need)
+                        hi = mid;
+                    else
+                        lo = mid + 1;
+                }
+                const uint32_t tl = max(hi, (uint32_t)__shfl_xor((int)hi, 32));
+                const float tv = dec_order(tl);
+                const int q = qw0 + qb * 32 + l32;
+                const bool valid = q0 + q < a.nq;
+                int c = 0;
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v)
+                        c += valid && acc[qb][rb][v] <= tv && acc[qb][rb][v] < VS_INF ? 1 : 0;
+                int pos = 0;
+                if (c > 0) pos = atomicAdd(&cnt_w[q], c);
+                if (c > 0) {
+                    float *cvq = cv + (int64_t)q * a.cap;
+                    int32_t *ciq = ci + (int64_t)q * a.cap;
+#pragma unroll
+                    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) {
+                            const float val = acc[qb][rb][v];
+                            if (val <= tv && val < VS_INF) {
+                                cvq[pos] = val;
+                                ciq[pos] = (int32_t)(wr0 + rb * 32 + 8 * (v / 4) + 4 * h + v % 4);
+                                ++pos;
+                            }
+                        }
+                }
+                // the list now holds >= kk values <= tv (none if the
+                // tile has fewer than kk valid rows: then tv is +inf)
+                if (valid && h == 0) thr_w[q] = fminf(thr_w[q], tv);
+                lds_wave_sync();
+                if (valid) thr_r[qb] = fminf(thr_r[qb], thr_w[q]);
+            }
+            seeded = true;
+        } else {
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+                thr_r[qb] = fminf(thr_r[qb], dec_order(gt[qb]));
+                float m = VS_INF;
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) m = fminf(m, acc[qb][rb][v]);
+                if (!__ballot(m < thr_r[qb])) continue;
+                const int q = qw0 + qb * 32 + l32;
+                // make room: a list this tile could overflow (a query
+                // gains at most 32 * RB entries per tile from this
+                // wave) is cut to its kk best first
+                if (__ballot(h == 0 && cnt_w[q] > a.cap - 32 * RB)) {
+                    for (int j = 0; j < 32; ++j) {
+                        const int qq = qw0 + qb * 32 + j;
+                        if (cnt_w[qq] > a.cap - 32 * RB)
+                            flush_list(cv + (int64_t)qq * a.cap, ci + (int64_t)qq * a.cap,
+                                       &cnt_w[qq], &thr_w[qq], &thr[qq], BQ, WR,
+                                       &a.gthr[q0 + qq], sv_w, si_w, a.cap, a.kk,
+                                       a.kk_final, a.publish_block, lane);
+                    }
+                    thr_r[qb] = fminf(thr_r[qb], thr_w[q]);
+                }
+                int c = 0;
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v)
+                        c += acc[qb][rb][v] < thr_r[qb] && rb * 32 + 8 * (v / 4) + 4 * h + v % 4 < lim
+                                 ? 1 : 0;
+                if (c > 0) {
+                    int pos = atomicAdd(&cnt_w[q], c);
+                    float *cvq = cv + (int64_t)q * a.cap;
+                    int32_t *ciq = ci + (int64_t)q * a.cap;
+#pragma unroll
+                    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) {
+                            const float val = acc[qb][rb][v];
+                            if (val < thr_r[qb] && rb * 32 + 8 * (v / 4) + 4 * h + v % 4 < lim) {
+                                cvq[pos] = val;
+                                ciq[pos] =
+                                    (int32_t)(wr0 + rb * 32 + 8 * (v / 4) + 4 * h + v % 4);
+                                ++pos;
+                            }
+                        }
+                }
+                lds_wave_sync();
+            }
+        }
+    } else {
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+            float m = VS_INF;
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) m = fminf(m, acc[qb][rb][v]);
+            if (!__ballot(m <= thr_r[qb])) continue;
+            const int64_t qg = q0 + qw0 + qb * 32 + l32;
+            // row offsets within the wave's tile rows that may be
+            // reported: below lim, and above the query (self-join)
+            const int omin =
+                a.self_join ? (int)max((int64_t)0, min((int64_t)(32 * RB), qg - wr0 + 1)) : 0;
+            // one reservation per lane for all of its hits
+            int c = 0;
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int off = rb * 32 + 8 * (v / 4) + 4 * h + v % 4;
+                    c += acc[qb][rb][v] <= thr_r[qb] && off < lim && off >= omin ? 1 : 0;
+                }
+            if (c > 0) {
+                unsigned long long pos = atomicAdd(a.count, (unsigned long long)c);
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        const int off = rb * 32 + 8 * (v / 4) + 4 * h + v % 4;
+                        if (acc[qb][rb][v] <= thr_r[qb] && off < lim && off >= omin) {
+                            if (pos < (unsigned long long)a.out_cap) {
+                                a.out_q[pos] = (int32_t)qg;
+                                a.out_i[pos] = (int32_t)(wr0 + off);
+                            }
+                            ++pos;
+                        }
+                    }
+            }
+        }
+    }
+}
+
+template <int ST, int PB, int WR, int WQ, int RB, int QB, int KC, int MODE>
+__global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
+    using S = GemmShape<ST, PB, WR, WQ, RB, QB, KC>;
+    constexpr int NT = S::NT, BR = S::BR, BQ = S::BQ, KP = S::KP;
+    extern __shared__ __align__(16) char smem[];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
+    const int wr = wave % WR, wq = wave / WR;
+
+    int64_t split, qblk;
+    if (!map_block_grouped(a.nqblk, a.nsplit, a.qgroup, &split, &qblk)) return;
+    int64_t r0 = split * a.rows_per_split;
+    const int64_t r1 = min(a.n, r0 + a.rows_per_split);
+    const int64_t q0 = qblk * BQ;
+    if (MODE == 1 && a.self_join) r0 = max(r0, q0);  // only ids > query
+    if (r0 >= r1) return;
+
+    // LDS: two stages, then the lists' counters and thresholds [WR][BQ] and
+    // the per-wave sort buffers [NW][cap]
+    int *cnt = (int *)(smem + 2 * S::STAGE_BYTES);
+    float *thr = (float *)(cnt + WR * BQ);
+    float *sv = thr + WR * BQ;
+    int *si = (int *)(sv + S::NW * a.cap);
+    for (int t = tid; t < WR * BQ; t += NT) {
+        cnt[t] = 0;
+        thr[t] = q0 + (t % BQ) < a.nq ? VS_INF : -VS_INF;
+    }
+    int *cnt_w = cnt + wr * BQ;
+    float *thr_w = thr + wr * BQ;
+    float *sv_w = sv + wave * a.cap;
+    int *si_w = si + wave * a.cap;
+    const int64_t list_base = ((qblk * a.nsplit + split) * WR + wr) * (int64_t)BQ * a.cap;
+    float *cv = MODE == 0 ? a.cand_v + list_base : nullptr;
+    int32_t *ci = MODE == 0 ? a.cand_i + list_base : nullptr;
+    const int qw0 = wq * 32 * QB;  // the wave's first query in the block
+    const EpiCtx ectx{q0, r1, qw0, l32, h, lane, cnt, cnt_w, thr, thr_w, sv_w, si_w, cv, ci};
+
+    float thr_r[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+        const int64_t qg = q0 + qw0 + qb * 32 + l32;
+        if (MODE == 0)
+            thr_r[qb] = qg < a.nq ? VS_INF : -VS_INF;
+        else
+            thr_r[qb] = qg < a.nq ? a.athr[qg] : -VS_INF;
+    }
+
+    const int nkc = (int)(a.ld / KC);
+    const int64_t row_bytes = a.ld * S::ESZ;
+    const bool l2 = a.metric == 0;
+
+    // global -> register staging of one K-chunk: A rows, B query planes and
+    // (first chunk of a tile) the tile's row norms
+    u32x4_t ra[S::A_LOADS], rq[S::B_LOADS];
+    f32x4_t rn;
+    auto gload = [&](int64_t trow, int kc) __attribute__((always_inline)) {
+        const char *abase = (const char *)a.xb + trow * row_bytes + (int64_t)kc * KC * S::ESZ;
+#pragma unroll
+        for (int j = 0; j < S::A_LOADS; ++j) {
+            const int i = tid + j * NT, row = i / S::A_CPR, c = i % S::A_CPR;
+            ra[j] = *(const u32x4_t *)(abase + row * row_bytes + c * 16);
+        }
+#pragma unroll
+        for (int j = 0; j < S::B_LOADS; ++j) {
+            const int i = tid + j * NT, qr = i / S::B_CPR, c = i % S::B_CPR;
+            const int q = qr / PB, p = qr % PB;
+            rq[j] = *(const u32x4_t *)(a.qp + ((q0 + q) * 2 + p) * a.ld + kc * KC + c * 8);
+        }
+        if (kc == 0 && l2 && tid < BR / 4) rn = *(const f32x4_t *)(a.xn + trow + 4 * tid);
+    };
+    auto lstore = [&](char *stage, int kc) __attribute__((always_inline)) {
+        uint16_t *As = (uint16_t *)stage;
+        uint16_t *Bs = As + S::AP * BR * KP;
+#pragma unroll
+        for (int j = 0; j < S::A_LOADS; ++j) {
+            const int i = tid + j * NT, row = i / S::A_CPR, c = i % S::A_CPR;
+            if constexpr (ST == 1) {
+                *(u32x4_t *)(As + row * KP + c * 8) = ra[j];
+            } else {
+                typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+                const f32x4_t f = __builtin_bit_cast(f32x4_t, ra[j]);
+                const bf16x4_t hi = __builtin_convertvector(f, bf16x4_t);
+                const bf16x4_t lo =
+                    __builtin_convertvector(f - __builtin_convertvector(hi, f32x4_t), bf16x4_t);
+                *(u32x2_t *)(As + row * KP + c * 4) = __builtin_bit_cast(u32x2_t, hi);
+                *(u32x2_t *)(As + BR * KP + row * KP + c * 4) = __builtin_bit_cast(u32x2_t, lo);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < S::B_LOADS; ++j) {
+            const int i = tid + j * NT, qr = i / S::B_CPR, c = i % S::B_CPR;
+            const int q = qr / PB, p = qr % PB;
+            *(u32x4_t *)(Bs + (p * BQ + q) * KP + c * 8) = rq[j];
+        }
+        if (kc == 0 && l2 && tid < BR / 4)
+            *(f32x4_t *)((float *)(As + S::STAGE_ELEMS) + 4 * tid) = rn;
+    };
+
+    f32x16_t acc[QB][RB];
+    uint32_t gt[QB];
+
+    // One K-chunk of MFMAs from LDS stage `stage`.  FIRST: the tile's first
+    // chunk, whose first K-step takes the row norms (L2) or zero (IP) as its
+    // C operand.
+    auto compute = [&](const char *stage, auto first_c) __attribute__((always_inline)) {
+        constexpr bool FIRST = decltype(first_c)::value;
+        const uint16_t *As = (const uint16_t *)stage;
+        const uint16_t *Bs = As + S::AP * BR * KP;
+        const uint16_t *al_ = As + (wr * 32 * RB + l32) * KP + 8 * h;
+        const uint16_t *bl_ = Bs + (qw0 + l32) * KP + 8 * h;
+        const float *Ns = (const float *)(As + S::STAGE_ELEMS) + wr * 32 * RB + 4 * h;
+#pragma unroll
+        for (int ks = 0; ks < KC / 16; ++ks) {
+            bf16x8_t b0[QB], b1[QB];
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+                b0[qb] = __builtin_bit_cast(bf16x8_t,
+                                            *(const u32x4_t *)(bl_ + qb * 32 * KP + ks * 16));
+                if constexpr (PB == 2)
+                    b1[qb] = __builtin_bit_cast(
+                        bf16x8_t, *(const u32x4_t *)(bl_ + BQ * KP + qb * 32 * KP + ks * 16));
+            }
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) {
+                const bf16x8_t ah = __builtin_bit_cast(
+                    bf16x8_t, *(const u32x4_t *)(al_ + rb * 32 * KP + ks * 16));
+                bf16x8_t alo;
+                if constexpr (ST == 0)
+                    alo = __builtin_bit_cast(
+                        bf16x8_t, *(const u32x4_t *)(al_ + BR * KP + rb * 32 * KP + ks * 16));
+                f32x16_t x16;
+                if (FIRST && ks == 0) {
+                    if (l2) {
+                        f32x4_t q4[4];
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) q4[u] = *(const f32x4_t *)(Ns + rb * 32 + 8 * u);
+                        x16 = __builtin_bit_cast(f32x16_t, q4);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 16; ++e) x16[e] = 0.f;
+                    }
+                }
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb) {
+                    acc[qb][rb] = mfma32_bf16(ah, b0[qb], (FIRST && ks == 0) ? x16 : acc[qb][rb]);
+                    if constexpr (ST == 0) acc[qb][rb] = mfma32_bf16(alo, b0[qb], acc[qb][rb]);
+                    if constexpr (PB == 2) acc[qb][rb] = mfma32_bf16(ah, b1[qb], acc[qb][rb]);
+                }
+            }
+        }
+    };
+
+    gload(r0, 0);
+    lstore(smem, 0);
+    __syncthreads();
+
+    int par = 0;  // stage holding the current chunk
+    // the first tile seeds the lists' thresholds when two lanes can hold kk
+    // values (ceil(kk / 2) <= 16 * RB)
+    bool seeded = (a.kk + 1) / 2 > 16 * RB;
+    for (int64_t t0 = r0; t0 < r1; t0 += BR) {
+        const bool last_tile = t0 + BR >= r1;
+        for (int kc = 0; kc < nkc; ++kc) {
+            char *cur = smem + par * S::STAGE_BYTES;
+            char *nxt = smem + (par ^ 1) * S::STAGE_BYTES;
+            const bool last_chunk = kc + 1 == nkc;
+            const bool more = !(last_chunk && last_tile);
+            const int kc_next = last_chunk ? 0 : kc + 1;
+            const int64_t t_next = last_chunk ? t0 + BR : t0;
+            if (more) gload(t_next, kc_next);
+            if (kc == 0) {
+                if constexpr (MODE == 0) {
+#pragma unroll
+                    for (int qb = 0; qb < QB; ++qb)
+                        gt[qb] = __hip_atomic_load(&a.gthr[q0 + qw0 + qb * 32 + l32],
+                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                compute(cur, std::true_type{});
+            } else {
+                compute(cur, std::false_type{});
+            }
+            if (more) lstore(nxt, kc_next);
+            par ^= 1;
+            if (!last_chunk) {
+                __syncthreads();
+                continue;
+            }
+
+            gemm_epilogue<WR, BQ, RB, QB, MODE>(acc, a, ectx, t0 + wr * 32 * RB, thr_r, gt, seeded);
+            __syncthreads();
+        }
+    }
+
+    if constexpr (MODE == 0) {
+        // final: every list of this wave's queries holds its kk best in
+        // slots [0, kk), padded
+        wave_sync();
+        for (int q = qw0; q < qw0 + 32 * QB; ++q) {
+            const int c = cnt_w[q];
+            if (c > a.kk) {
+                flush_list(cv + (int64_t)q * a.cap, ci + (int64_t)q * a.cap, &cnt_w[q], &thr_w[q],
+                           &thr[q], BQ, WR, &a.gthr[q0 + q], sv_w, si_w, a.cap, a.kk, a.kk_final,
+                           a.publish_block, lane);
+            } else {
+                for (int j = c + lane; j < a.kk; j += 64) {
+                    cv[(int64_t)q * a.cap + j] = VS_INF;
+                    ci[(int64_t)q * a.cap + j] = -1;
+                }
+            }
+        }
+        // a list cut to kk < kk_final entries may have dropped rows at or
+        // above its own final threshold: the merge checks that value against
+        // the query's final kk_final-th value
+        if (a.lbound) {
+            wave_sync();
+            const int64_t lb = ((qblk * a.nsplit + split) * WR + wr) * (int64_t)BQ;
+            for (int q = qw0 + lane; q < qw0 + 32 * QB; q += 64) a.lbound[lb + q] = thr_w[q];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// LDS-DMA variant for bf16 rows.  Every operand byte goes HBM/L2 -> LDS with
+// global_load_lds_dwordx4 (lane i of a wave writes 16 bytes at M0 + 16 i; one
+// instruction fills 1 KB), so no VGPRs stage the loads and NS stages are in
+// flight: chunk c + NS - 1 is issued while chunk c is multiplied.  Rows are
+// 64 bytes per K-chunk of 32, unpadded; 16-byte chunk c of row r sits at
+// position c ^ f(r), f(r) = ((r >> 1) ^ (r >> 2)) & 3, which spreads the 32
+// rows of an MFMA fragment read over all LDS banks (32- or 64-bank layouts).
+// The DMA loads are issued from inline assembly, so the compiler does not
+// treat them as LDS writes; an explicit vmcnt wait plus a barrier per chunk
+// orders them (vector memory loads complete in issue order, so "at most N
+// outstanding" with N later loads means the chunk has landed).  The tile's
+// row norms and the queries' shared thresholds arrive the same way with the
+// tile's first chunk.
+// ---------------------------------------------------------------------------
+template <int PB, int WR, int WQ, int RB, int QB, int NS>
+struct DmaShape {
+    static constexpr int NW = WR * WQ, NT = 64 * NW;
+    static constexpr int BR = WR * 32 * RB, BQ = WQ * 32 * QB;
+    static constexpr int KC = 32;  // elements per K-chunk: 64 bytes per row
+    static constexpr int A_INS = BR * 64 / 1024, B_INS = PB * BQ * 64 / 1024;
+    static constexpr int A_PW = A_INS / NW, B_PW = B_INS / NW;
+    static constexpr int L = A_PW + B_PW;  // DMA loads per wave and chunk (norms aside)
+    static constexpr int A_BYTES = BR * 64, B_BYTES = PB * BQ * 64;
+    static constexpr int N_OFF = A_BYTES + B_BYTES;  // row norms [BR] f32
+    static constexpr int G_OFF = N_OFF + BR * 4;      // shared thresholds [BQ] u32
+    static constexpr int STAGE_BYTES = G_OFF + BQ * 4;
+    static_assert(A_INS % NW == 0 && B_INS % NW == 0, "whole DMA loads per wave");
+    static_assert(BR % 256 == 0 && BR / 256 <= NW && BQ <= 256, "norm and threshold loads");
+    static_assert(BR <= kRowSlack, "the last row tile reads at most kRowSlack rows past the end");
+    static_assert(NS >= 2, "at least two stages");
+};
+
+size_t gemm_dma_lds_bytes(int pb, int wr, int wq, int rb, int qb, int ns, int cap) {
+    const size_t br = (size_t)wr * 32 * rb, bq = (size_t)wq * 32 * qb;
+    const size_t stage = br * 64 + (size_t)pb * bq * 64 + br * 4 + bq * 4;
+    return (size_t)ns * stage + (size_t)wr * bq * 8 + (size_t)wr * wq * cap * 8;
+}
+
+__device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
+
+// One 1-KB LDS DMA: lane i's 16 bytes at base + voff go to LDS byte lds +
+// 16 i (base and lds are wave-uniform; voff is the lane's byte offset).
+__device__ __forceinline__ void dma16(const void *base, uint32_t voff, uint32_t lds) {
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    const uint64_t bu = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32) |
+                        (uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+    uint32_t save;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %2, %3\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(save)
+        : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(bu)
+        : "memory");
+}
+
+// dma16 with voff = 16 * lane, computed inside the assembly so that it is
+// never kept live (a spilled offset would cost a reload, whose wait for
+// vmcnt(0) would also drain every LDS DMA in flight).
+__device__ __forceinline__ void dma16_lane(const void *base, uint32_t lds) {
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    const uint64_t bu = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32) |
+                        (uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+    uint32_t save, voff;
+    asm volatile(
+        "v_mbcnt_lo_u32_b32 %1, -1, 0\n\t"
+        "v_mbcnt_hi_u32_b32 %1, -1, %1\n\t"
+        "v_lshlrev_b32 %1, 4, %1\n\t"
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %3\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(save), "=&v"(voff)
+        : "s"(__builtin_amdgcn_readfirstlane(lds)), "s"(bu)
+        : "memory");
+}
+
+// s_waitcnt vmcnt(n) (gfx9 encoding: vmcnt bits 3:0 and 15:14; expcnt and
+// lgkmcnt left at their maxima, i.e. not waited on)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+template <int PB, int WR, int WQ, int RB, int QB, int NS, int MODE>
+__global__ __launch_bounds__(64 * WR * WQ) void gemm_dma_kernel(ScanKArgs a) {
+    using S = DmaShape<PB, WR, WQ, RB, QB, NS>;
+    constexpr int NT = S::NT, BR = S::BR, BQ = S::BQ, L = S::L;
+    extern __shared__ __align__(16) char smem[];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
+    const int wr = wave % WR, wq = wave / WR;
+    (void)NT;
+
+    int64_t split, qblk;
+    if (!map_block_grouped(a.nqblk, a.nsplit, a.qgroup, &split, &qblk)) return;
+    int64_t r0 = split * a.rows_per_split;
+    const int64_t r1 = min(a.n, r0 + a.rows_per_split);
+    const int64_t q0 = qblk * BQ;
+    if (MODE == 1 && a.self_join) r0 = max(r0, q0);  // only ids > query
+    if (r0 >= r1) return;
+
+    int *cnt = (int *)(smem + NS * S::STAGE_BYTES);
+    float *thr = (float *)(cnt + WR * BQ);
+    float *sv = thr + WR * BQ;
+    int *si = (int *)(sv + S::NW * a.cap);
+    for (int t = tid; t < WR * BQ; t += S::NT) {
+        cnt[t] = 0;
+        thr[t] = q0 + (t % BQ) < a.nq ? VS_INF : -VS_INF;
+    }
+    int *cnt_w = cnt + wr * BQ;
+    float *thr_w = thr + wr * BQ;
+    float *sv_w = sv + wave * a.cap;
+    int *si_w = si + wave * a.cap;
+    const int64_t list_base = ((qblk * a.nsplit + split) * WR + wr) * (int64_t)BQ * a.cap;
+    float *cv = MODE == 0 ? a.cand_v + list_base : nullptr;
+    int32_t *ci = MODE == 0 ? a.cand_i + list_base : nullptr;
+    const int qw0 = wq * 32 * QB;
+    const EpiCtx ectx{q0, r1, qw0, l32, h, lane, cnt, cnt_w, thr, thr_w, sv_w, si_w, cv, ci};
+
+    float thr_r[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+        const int64_t qg = q0 + qw0 + qb * 32 + l32;
+        if (MODE == 0)
+            thr_r[qb] = qg < a.nq ? VS_INF : -VS_INF;
+        else
+            thr_r[qb] = qg < a.nq ? a.athr[qg] : -VS_INF;
+    }
+
+    const int nkc = (int)(a.ld / S::KC);
+    const int64_t row_bytes = a.ld * 2;
+    const bool l2 = a.metric == 0;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
+
+    // per-lane global byte offsets of this wave's DMA loads (fixed per slot)
+    int aoff[S::A_PW], boff[S::B_PW];
+#pragma unroll
+    for (int j = 0; j < S::A_PW; ++j) {
+        const int r = 16 * (wave * S::A_PW + j) + (lane >> 2);
+        aoff[j] = r * (int)row_bytes + 16 * ((lane & 3) ^ swz(r));
+    }
+#pragma unroll
+    for (int j = 0; j < S::B_PW; ++j) {
+        const int br = 16 * (wave * S::B_PW + j) + (lane >> 2);  // plane-major B row
+        const int p = br / BQ, q = br % BQ;
+        boff[j] = (2 * q + p) * (int)row_bytes + 16 * ((lane & 3) ^ swz(q));
+    }
+    const char *qbase = (const char *)a.qp + (q0 * 2) * row_bytes;
+
+    // issue the loads of chunk (tile row t, K-chunk kc) into stage st
+    auto issue = [&](int64_t t, int kc, int st) __attribute__((always_inline)) {
+        const uint32_t sb = lds0 + st * S::STAGE_BYTES;
+        const char *ab = (const char *)a.xb + t * row_bytes + kc * 64;
+#pragma unroll
+        for (int j = 0; j < S::A_PW; ++j)
+            dma16(ab, (uint32_t)aoff[j], sb + (wave * S::A_PW + j) * 1024);
+        const char *bb = qbase + kc * 64;
+#pragma unroll
+        for (int j = 0; j < S::B_PW; ++j)
+            dma16(bb, (uint32_t)boff[j], sb + S::A_BYTES + (wave * S::B_PW + j) * 1024);
+        if (kc == 0) {
+            if (l2 && wave < BR / 256)
+                dma16_lane(a.xn + t + 256 * wave, sb + S::N_OFF + 1024 * wave);
+            if (MODE == 0 && wave == S::NW - 1 && lane < BQ / 4)
+                dma16_lane(a.gthr + q0, sb + S::G_OFF);
+        }
+    };
+
+    f32x16_t acc[QB][RB];
+    uint32_t gt[QB];
+    const int xo0 = 16 * ((0 + h) ^ swz(l32)), xo1 = 16 * ((2 + h) ^ swz(l32));
+
+    auto compute = [&](const char *stage, auto first_c) __attribute__((always_inline)) {
+        constexpr bool FIRST = decltype(first_c)::value;
+        const char *Ab = stage + (wr * 32 * RB + l32) * 64;
+        const char *Bb = stage + S::A_BYTES + (qw0 + l32) * 64;
+        const float *Ns = (const float *)(stage + S::N_OFF) + wr * 32 * RB + 4 * h;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const int xo = ks == 0 ? xo0 : xo1;
+            bf16x8_t b0[QB], b1[QB];
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+                b0[qb] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t *)(Bb + qb * 32 * 64 + xo));
+                if constexpr (PB == 2)
+                    b1[qb] = __builtin_bit_cast(
+                        bf16x8_t, *(const u32x4_t *)(Bb + BQ * 64 + qb * 32 * 64 + xo));
+            }
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) {
+                const bf16x8_t ah =
+                    __builtin_bit_cast(bf16x8_t, *(const u32x4_t *)(Ab + rb * 32 * 64 + xo));
+                f32x16_t x16;
+                if (FIRST && ks == 0) {
+                    if (l2) {
+                        f32x4_t q4[4];
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) q4[u] = *(const f32x4_t *)(Ns + rb * 32 + 8 * u);
+                        x16 = __builtin_bit_cast(f32x16_t, q4);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 16; ++e) x16[e] = 0.f;
+                    }
+                }
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb) {
+                    acc[qb][rb] = mfma32_bf16(ah, b0[qb], (FIRST && ks == 0) ? x16 : acc[qb][rb]);
+                    if constexpr (PB == 2) acc[qb][rb] = mfma32_bf16(ah, b1[qb], acc[qb][rb]);
+                }
+            }
+        }
+        if constexpr (FIRST && MODE == 0) {
+            const uint32_t *G = (const uint32_t *)(stage + S::G_OFF) + qw0 + l32;
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) gt[qb] = G[qb * 32];
+        }
+    };
+
+    const int64_t ntiles = (r1 - r0 + BR - 1) / BR;
+    const int64_t total = ntiles * nkc;
+    // prologue: chunks 0 .. NS - 2
+    int64_t it_t = r0;  // next chunk to issue: tile row and K-chunk
+    int it_kc = 0;
+    int64_t issued = 0;
+    for (; issued < NS - 1 && issued < total; ++issued) {
+        issue(it_t, it_kc, (int)issued);
+        if (++it_kc == nkc) {
+            it_kc = 0;
+            it_t += BR;
+        }
+    }
+
+    bool seeded = (a.kk + 1) / 2 > 16 * RB;
+    int64_t it = 0;
+    for (int64_t t0 = r0; t0 < r1; t0 += BR) {
+        for (int kc = 0; kc < nkc; ++kc, ++it) {
+            // chunk `it` has landed once at most (issued - 1 - it) chunks of
+            // later loads are outstanding
+            const int64_t later = issued - 1 - it;
+            if constexpr (NS >= 4) {
+                if (later >= 2) wait_vm<2 * L>();
+                else if (later == 1) wait_vm<L>();
+                else wait_vm<0>();
+            } else if constexpr (NS == 3) {
+                if (later >= 1) wait_vm<L>();
+                else wait_vm<0>();
+            } else {
+                wait_vm<0>();
+            }
+            __syncthreads();
+            if (issued < total) {
+                issue(it_t, it_kc, (int)(issued % NS));
+                ++issued;
+                if (++it_kc == nkc) {
+                    it_kc = 0;
+                    it_t += BR;
+                }
+            }
+            const char *cur = smem + (it % NS) * S::STAGE_BYTES;
+            if (kc == 0)
+                compute(cur, std::true_type{});
+            else
+                compute(cur, std::false_type{});
+            if (kc + 1 == nkc)
+                gemm_epilogue<WR, BQ, RB, QB, MODE>(acc, a, ectx, t0 + wr * 32 * RB, thr_r, gt,
+                                                    seeded);
+        }
+    }
+
+    if constexpr (MODE == 0) {
+        wave_sync();
+        for (int q = qw0; q < qw0 + 32 * QB; ++q) {
+            const int c = cnt_w[q];
+            if (c > a.kk) {
+                flush_list(cv + (int64_t)q * a.cap, ci + (int64_t)q * a.cap, &cnt_w[q], &thr_w[q],
+                           &thr[q], BQ, WR, &a.gthr[q0 + q], sv_w, si_w, a.cap, a.kk, a.kk_final,
+                           a.publish_block, lane);
+            } else {
+                for (int j = c + lane; j < a.kk; j += 64) {
+                    cv[(int64_t)q * a.cap + j] = VS_INF;
+                    ci[(int64_t)q * a.cap + j] = -1;
+                }
+            }
+        }
+        if (a.lbound) {
+            wave_sync();
+            const int64_t lb = ((qblk * a.nsplit + split) * WR + wr) * (int64_t)BQ;
+            for (int q = qw0 + lane; q < qw0 + 32 * QB; q += 64) a.lbound[lb + q] = thr_w[q];
+        }
+    }
+}
+
+template <int MODE>
+hipError_t launch_gemm_scan(int storage, int planes, const ScanPlan &plan, const ScanKArgs &args,
+                            hipStream_t st) {
+    const int64_t grid = ((tile_grid_space(plan.nqblk, plan.nsplit, plan.tile_group) + 7) / 8) * 8;
+    ScanKArgs ga = args;
+    ga.qgroup = plan.tile_group;
+    ga.publish_block = plan.lw * plan.kk >= plan.kk_final;
+    void (*fn)(ScanKArgs) = nullptr;
+#define VS_DPICK(PB_, WR_, WQ_, RB_, QB_, NS_)                                                 \
+    if (storage == 1 && planes == PB_ && plan.lw == WR_ && plan.g_wq == WQ_ &&                  \
+        plan.tile_rb == RB_ && plan.g_qb == QB_ && plan.g_ns == NS_)                              \
+        fn = gemm_dma_kernel<PB_, WR_, WQ_, RB_, QB_, NS_, MODE>;
+    if (plan.g_ns > 0) {
+        VS_GEMM_DMA_SHAPES(VS_DPICK)
+    }
+#undef VS_DPICK
+#define VS_GPICK(ST_, PB_, WR_, WQ_, RB_, QB_, KC_)                                            \
+    if (storage == ST_ && planes == PB_ && plan.lw == WR_ && plan.g_wq == WQ_ &&                 \
+        plan.tile_rb == RB_ && plan.g_qb == QB_ && plan.tile_kc == KC_ && plan.g_ns == 0)        \
+        fn = gemm_scan_kernel<ST_, PB_, WR_, WQ_, RB_, QB_, KC_, MODE>;
+    VS_GEMM_SHAPES(VS_GPICK)
+#undef VS_GPICK
+    if (!fn) return hipErrorInvalidValue;
+    const size_t lds = plan.lds_bytes;
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute((const void *)fn,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(64 * plan.lw * plan.g_wq), lds, st, ga);
+    return hipGetLastError();
+}
+
+template hipError_t launch_gemm_scan<0>(int, int, const ScanPlan &, const ScanKArgs &, hipStream_t);
+template hipError_t launch_gemm_scan<1>(int, int, const ScanPlan &, const ScanKArgs &, hipStream_t);
+
+}  // namespace vs

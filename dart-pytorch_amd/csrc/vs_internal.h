@@ -85,7 +85,12 @@ struct ScanPlan {
     int cap = 64;         // per-list buffer capacity (power of two)
     int nks = 0;          // >0: queries held in registers for this many K-steps
     int lw = 4;           // candidate lists per (workgroup, query): the workgroup's waves
-    int kind = 0;         // 0: streaming scan (vs_kernels.hip); 1: LDS-tiled scan (vs_tile.hip)
+    int kind = 0;         // 0: streaming scan (vs_kernels.hip); 1: LDS-tiled scan (vs_tile.hip);
+                          // 2: GEMM-tiled scan (vs_gemm.hip)
+    int g_ns = 0;            // GEMM-tiled scan: LDS-DMA stages (0: register-staged kernel)
+    int g_wq = 2, g_qb = 4;  // GEMM-tiled scan: query waves, 32-query blocks per wave
+                             // (row waves = lw, 32-row blocks per wave = tile_rb,
+                             // K-chunk = tile_kc)
     int tile_rb = 2;      // tiled scan: 32-row blocks per wave (row tile = 128 * tile_rb rows)
     int tile_kc = 64;     // tiled scan: K-chunk per pipeline step (elements)
     int tile_st = 1, tile_pb = 1;  // tiled scan: storage and query planes it was planned for
@@ -194,7 +199,36 @@ size_t tile_lds_bytes(int qb, int pb, int nw, int cap, int64_t ld);
     X(0, 1, 4, 2, 32, 4)                                                                      \
     X(0, 1, 2, 2, 32, 4)
 
+// The built shapes of the GEMM-tiled scan, in the planner's order of
+// preference: X(storage, query planes, row waves, query waves, 32-row blocks
+// per wave, 32-query blocks per wave, K-chunk).  A workgroup covers
+// 32 * row waves * row blocks database rows by 32 * query waves * query
+// blocks queries per tile.
+#define VS_GEMM_SHAPES(X)                                                                     \
+    X(1, 1, 2, 4, 4, 2, 32)                                                                   \
+    X(1, 1, 2, 2, 4, 2, 32)                                                                   \
+    X(1, 2, 2, 4, 4, 2, 32)                                                                   \
+    X(1, 2, 2, 2, 4, 2, 32)                                                                   \
+    X(0, 2, 2, 4, 4, 2, 16)                                                                   \
+    X(0, 2, 2, 2, 4, 2, 32)                                                                   \
+    X(0, 1, 2, 4, 4, 2, 32)                                                                   \
+    X(0, 1, 2, 2, 4, 2, 32)
+
+// The LDS-DMA shapes of the GEMM-tiled scan (bf16 rows, K-chunk 32), tried
+// before the register-staged ones: X(query planes, row waves, query waves,
+// 32-row blocks per wave, 32-query blocks per wave, LDS stages).
+#define VS_GEMM_DMA_SHAPES(X)                                                                 \
+    X(1, 2, 4, 4, 2, 4)                                                                       \
+    X(1, 2, 2, 4, 2, 4)
+
+// LDS of the GEMM-tiled scans (stages plus list bookkeeping).
+size_t gemm_dma_lds_bytes(int pb, int wr, int wq, int rb, int qb, int ns, int cap);
+size_t gemm_lds_bytes(int st, int pb, int wr, int wq, int rb, int qb, int kc, int cap);
+
 struct ScanKArgs;
+template <int MODE>
+hipError_t launch_gemm_scan(int storage, int planes, const ScanPlan &plan, const ScanKArgs &args,
+                            hipStream_t st);
 template <int MODE>
 hipError_t launch_tile_scan(int storage, int planes, const ScanPlan &plan, const ScanKArgs &args,
                             hipStream_t st);

@@ -451,7 +451,7 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanKArgs a) {
                     for (int q = 0; q < BN; ++q) {
                         if (cnt_w[q] > a.cap - 16 * TM)
                             flush_list(cv + (int64_t)q * a.cap, ci + (int64_t)q * a.cap, &cnt_w[q],
-                                       &thr_w[q], &thr[q], BN, &a.gthr[q0 + q], sv_w, si_w, a.cap,
+                                       &thr_w[q], &thr[q], BN, 4, &a.gthr[q0 + q], sv_w, si_w, a.cap,
                                        a.kk, a.kk_final, a.publish_block, lane);
                     }
 #pragma unroll
@@ -521,7 +521,7 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanKArgs a) {
             const int c = cnt_w[q];
             if (c > a.kk) {
                 flush_list(cv + (int64_t)q * a.cap, ci + (int64_t)q * a.cap, &cnt_w[q], &thr_w[q],
-                           &thr[q], BN, &a.gthr[q0 + q], sv_w, si_w, a.cap, a.kk, a.kk_final,
+                           &thr[q], BN, 4, &a.gthr[q0 + q], sv_w, si_w, a.cap, a.kk, a.kk_final,
                            a.publish_block, lane);
             } else {
                 for (int j = c + lane; j < a.kk; j += 64) {
@@ -545,6 +545,7 @@ template <int MODE>
 static hipError_t launch_scan_mode(int storage, const PreparedQueries &pq, const ScanPlan &plan,
                                    const ScanKArgs &args, hipStream_t st) {
     if (plan.kind == 1) return launch_tile_scan<MODE>(storage, pq.planes, plan, args, st);
+    if (plan.kind == 2) return launch_gemm_scan<MODE>(storage, pq.planes, plan, args, st);
     const int64_t total = plan.nqblk * plan.nsplit;
     const int64_t grid = ((total + 7) / 8) * 8;
     const size_t lds = plan.lds_bytes;

@@ -278,7 +278,7 @@ __global__ __launch_bounds__(64 * NW) void tile_scan_kernel(ScanKArgs a) {
                         const int qq = qb * 32 + j;
                         if (cnt_w[qq] > a.cap - WR)
                             flush_list(cv + (int64_t)qq * a.cap, ci + (int64_t)qq * a.cap,
-                                       &cnt_w[qq], &thr_w[qq], &thr[qq], BQ, &a.gthr[q0 + qq], sv_w,
+                                       &cnt_w[qq], &thr_w[qq], &thr[qq], BQ, 4, &a.gthr[q0 + qq], sv_w,
                                        si_w, a.cap, a.kk, a.kk_final, a.publish_block, lane);
                     }
                     thr_r[qb] = fminf(thr_r[qb], thr_w[q]);
@@ -346,7 +346,7 @@ __global__ __launch_bounds__(64 * NW) void tile_scan_kernel(ScanKArgs a) {
             const int c = cnt_w[q];
             if (c > a.kk) {
                 flush_list(cv + (int64_t)q * a.cap, ci + (int64_t)q * a.cap, &cnt_w[q], &thr_w[q],
-                           &thr[q], BQ, &a.gthr[q0 + q], sv_w, si_w, a.cap, a.kk, a.kk_final,
+                           &thr[q], BQ, 4, &a.gthr[q0 + q], sv_w, si_w, a.cap, a.kk, a.kk_final,
                            a.publish_block, lane);
             } else {
                 for (int j = c + lane; j < a.kk; j += 64) {

@@ -16,8 +16,15 @@ def _close(a, b, rtol, atol):
     return both_inf | (np.abs(a - b) <= atol + rtol * np.maximum(np.abs(a), np.abs(b)))
 
 
-def assert_knn_parity(D, I, Dr, Ir, metric, rtol=1e-5, atol=1e-6, exact_shared=True):
-    """metric 0 = L2 (ascending), 1 = IP (descending)."""
+def assert_knn_parity(D, I, Dr, Ir, metric, rtol=1e-5, atol=1e-6, exact_shared=True,
+                      xb=None, xq=None):
+    """metric 0 = L2 (ascending), 1 = IP (descending).
+
+    The last tie group -- oracle distances tied with the k-th -- may continue
+    past k, so the ids there may differ (the reference keeps whichever tied
+    rows its heap history left, index.dart:248-260).  Given xb and xq, every
+    GPU id the oracle does not list is checked to lie at its reported
+    distance (recomputed in fp64)."""
     D, I, Dr, Ir = map(np.asarray, (D, I, Dr, Ir))
     assert D.shape == Dr.shape and I.shape == Ir.shape, (D.shape, Dr.shape)
     nq, k = Dr.shape
@@ -47,10 +54,21 @@ def assert_knn_parity(D, I, Dr, Ir, metric, rtol=1e-5, atol=1e-6, exact_shared=T
             lo = Dr[q][j - 1] if j > 0 else None
             hi = Dr[q][j + 1] if j + 1 < k and Ir[q][j + 1] >= 0 else None
             tied = (lo is not None and _close(lo, Dr[q][j], rtol, atol)) or (
-                hi is not None and _close(hi, Dr[q][j], rtol, atol))
+                hi is not None and _close(hi, Dr[q][j], rtol, atol)) or (
+                _close(kth, Dr[q][j], rtol, atol))
             if not tied and I[q][j] != Ir[q][j]:
                 bad.append((q, "id", j, I[q][j], Ir[q][j]))
                 break
+        if xb is not None:
+            known = set(Ir[q].tolist())
+            for i, d in zip(I[q], D[q]):
+                if int(i) >= 0 and int(i) not in known:
+                    x = np.asarray(xb[int(i)], np.float64)
+                    y = np.asarray(xq[q], np.float64)
+                    true = float(np.sum((x - y) ** 2)) if metric == 0 else float(np.dot(x, y))
+                    if not _close(true, d, rtol, atol):
+                        bad.append((q, "wrong distance for extra id", int(i), float(d), true))
+                        break
         if exact_shared:
             ref = {int(i): float(d) for i, d in zip(Ir[q], Dr[q]) if i >= 0}
             for i, d in zip(I[q], D[q]):

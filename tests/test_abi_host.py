@@ -81,6 +81,17 @@ def test_parity_helper_rejects_planted_mistakes():
         assert_knn_parity(D, np.array([[10, 11, 99, 13]], np.int32), D, I, 0)
     Dt = np.array([[1.0, 2.0, 2.0, 4.0]], np.float32)  # tie: order may differ
     assert_knn_parity(Dt, I[:, [0, 2, 1, 3]], Dt, I, 0)
+    # the last tie group may continue past k: row 2 ties row 1 at distance 1
+    # (L2 to the query 0), so either may fill the last slot -- but an extra id
+    # must really lie at the reported distance
+    xb = np.array([[0.0], [1.0], [1.0], [3.0]], np.float32)
+    xq = np.zeros((1, 1), np.float32)
+    Dk = np.array([[0.0, 1.0]], np.float32)
+    assert_knn_parity(Dk, np.array([[0, 2]], np.int32), Dk, np.array([[0, 1]], np.int32), 0,
+                      xb=xb, xq=xq)
+    with pytest.raises(AssertionError):  # row 3 is at distance 9, not 1
+        assert_knn_parity(Dk, np.array([[0, 3]], np.int32), Dk, np.array([[0, 1]], np.int32), 0,
+                          xb=xb, xq=xq)
     lims = np.array([0, 2]); Dr = np.array([1.0, 2.0], np.float32); Ir = np.array([3, 5], np.int32)
     assert_range_parity(lims, Dr, Ir, lims, Dr, Ir)
     with pytest.raises(AssertionError):

@@ -1,0 +1,255 @@
+"""Parity of the GEMM-tiled distance scan (large query batches, both operands
+staged in LDS) against the CPU oracle (restating IndexFlat.search /
+rangeSearch, index_flat.dart:62-137, and the Kmeans assign/update steps,
+kmeans.dart:91-140).
+
+Every built shape is forced here: bf16 rows with one or two query planes,
+fp32 rows (split into bf16 hi/lo planes in LDS) with one or two query
+planes, 128- and 256-query blocks, 4 and 8 waves.  Row counts end inside a
+row tile, query counts inside a query block, d is ragged, both metrics, k
+from 1 to 100.  Each test also checks, through the always-on "gemm" launch
+counters, that the GEMM-tiled kernel really ran in the forced shape."""
+import numpy as np
+import pytest
+
+import oracle
+from _parity import assert_knn_parity, assert_range_parity
+from vector_store import synthetic as syn
+
+pytestmark = pytest.mark.gpu
+NT = oracle.default_threads()
+
+# The built shapes (storage, query planes, row waves, query waves, 32-row
+# blocks per wave, 32-query blocks per wave, K-chunk), as listed by
+# VS_GEMM_SHAPES in dart-pytorch_amd/csrc/vs_internal.h.
+SHAPES = [
+    (1, 1, 2, 4, 4, 2, 32),
+    (1, 1, 2, 2, 4, 2, 32),
+    (1, 2, 2, 4, 4, 2, 32),
+    (1, 2, 2, 2, 4, 2, 32),
+    (0, 2, 2, 4, 4, 2, 16),
+    (0, 2, 2, 2, 4, 2, 32),
+    (0, 1, 2, 4, 4, 2, 32),
+    (0, 1, 2, 2, 4, 2, 32),
+]
+
+
+def _key(shape):
+    return "gemm:" + ",".join(map(str, shape))
+
+
+@pytest.fixture(autouse=True)
+def _gemm(monkeypatch):
+    """The GEMM-tiled scan is switched on for every test here."""
+    monkeypatch.setenv("VS_GEMM", "1")
+    monkeypatch.setenv("VS_GEMM_MIN_NQ", "256")
+
+
+# The LDS-DMA shapes (query planes, row waves, query waves, 32-row blocks per
+# wave, 32-query blocks per wave, LDS stages) of VS_GEMM_DMA_SHAPES; bf16 rows
+# only, tried before the register-staged shapes.
+DMA_SHAPES = [
+    (1, 2, 4, 4, 2, 4),
+    (1, 2, 2, 4, 2, 4),
+]
+
+
+def _force(monkeypatch, shape):
+    """Force a register-staged shape (the LDS-DMA shapes switched off)."""
+    _, _, _, wq, _, qb, kc = shape
+    monkeypatch.setenv("VS_GEMM_DMA", "0")
+    for name, v in (("WQ", wq), ("QB", qb), ("KC", kc)):
+        monkeypatch.setenv("VS_GEMM_" + name, str(v))
+
+
+def _search(vs, xb, xq, k, metric, storage, shape=None, key=None):
+    idx = vs.GpuIndexFlat(xb.shape[1], vs.Metric(metric), storage=storage)
+    idx.add(xb)
+    r = idx.search(xq, k)
+    gemm, _ = idx.prof_get("gemm")
+    if shape is not None or key is not None:
+        key = key or _key(shape)
+        n, _ = idx.prof_get(key)
+        assert n >= 1, f"{key} did not run"
+    idx.close()
+    return r.distances, r.ids, gemm
+
+
+def _inputs(shape, d, seed, n=9000, nq=300):
+    """Rows and queries whose storage and query planes select `shape`: bf16
+    rows (bf16 bits) or fp32 rows; bf16-exact or general fp32 queries.
+    9,000 rows end inside a row tile and 300 queries inside a query block."""
+    st, pb = shape[0], shape[1]
+    xb = syn.normal_unit(n, d, seed, 0)
+    xq = syn.normal_unit(nq, d, seed, 1)
+    if st == 1:
+        xb = syn.to_bf16_bits(xb)
+    if pb == 1:
+        xq = syn.bf16_bits_to_f32(syn.to_bf16_bits(xq))
+    return xb, xq, ("bf16" if st == 1 else "f32")
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "-".join(map(str, s)))
+@pytest.mark.parametrize("metric", [0, 1])
+@pytest.mark.parametrize("k,d", [(10, 200), (100, 768), (1, 72)])
+def test_gemm_shape_parity(vs, monkeypatch, shape, metric, k, d):
+    _force(monkeypatch, shape)
+    xb, xq, storage = _inputs(shape, d, 31 + metric)
+    D, I, gemm = _search(vs, xb, xq, k, metric, storage, shape)
+    assert gemm >= 1
+    xbf = syn.bf16_bits_to_f32(xb) if storage == "bf16" else xb
+    Dr, Ir = oracle.flat_search(xbf, xq, k, metric, NT)
+    assert_knn_parity(D, I, Dr, Ir, metric, rtol=1e-3 if storage == "bf16" else 1e-5)
+
+
+DMA_OFF = ("the LDS-DMA kernel is switched off (kGemmDmaEnabled = false in vs_api.hip): its "
+           "first GPU run (8-wave shape, d = 200, L2, k = 10) left the GPU faulted and the "
+           "cause has not been shown")
+
+
+@pytest.mark.skip(reason=DMA_OFF)
+@pytest.mark.parametrize("shape", DMA_SHAPES, ids=lambda s: "-".join(map(str, s)))
+@pytest.mark.parametrize("metric", [0, 1])
+@pytest.mark.parametrize("k,d", [(10, 200), (100, 768), (1, 72)])
+def test_gemm_dma_shape_parity(vs, monkeypatch, shape, metric, k, d):
+    """The LDS-DMA kernel in each built shape: bf16 rows and bf16 queries."""
+    _, _, wq, _, qb, _ = shape
+    monkeypatch.setenv("VS_GEMM_WQ", str(wq))
+    monkeypatch.setenv("VS_GEMM_QB", str(qb))
+    xb, xq, storage = _inputs((1, 1), d, 51 + metric)
+    D, I, gemm = _search(vs, xb, xq, k, metric, storage,
+                         key="gemmdma:" + ",".join(map(str, shape)))
+    assert gemm >= 1
+    Dr, Ir = oracle.flat_search(syn.bf16_bits_to_f32(xb), xq, k, metric, NT)
+    assert_knn_parity(D, I, Dr, Ir, metric, rtol=1e-3)
+
+
+@pytest.mark.parametrize("dma", [pytest.param(1, marks=pytest.mark.skip(reason=DMA_OFF)), 0])
+@pytest.mark.parametrize("wq,qb", [(4, 2), (2, 2)])
+def test_gemm_config2_exact(vs, monkeypatch, wq, qb, dma):
+    """configs[1] arithmetic on a 100k slice with 1,000 queries: integer
+    distances, bit-exact, k = 100, on the LDS-DMA and register-staged
+    kernels."""
+    monkeypatch.setenv("VS_GEMM_WQ", str(wq))
+    monkeypatch.setenv("VS_GEMM_QB", str(qb))
+    monkeypatch.setenv("VS_GEMM_DMA", str(dma))
+    xb = syn.int_grid(100_000, 128, 1234, 0)
+    xq = syn.int_grid(1000, 128, 1234, 1)
+    key = f"gemmdma:1,2,{wq},4,{qb},4" if dma else _key((1, 1, 2, wq, 4, qb, 32))
+    D, I, gemm = _search(vs, xb, xq, 100, 0, "auto", key=key)
+    assert gemm >= 1
+    Dr, Ir = oracle.flat_search(xb, xq, 100, 0, NT)
+    assert_knn_parity(D, I, Dr, Ir, 0, rtol=0.0, atol=0.0, xb=xb, xq=xq)
+    assert np.all(D == np.round(D))
+
+
+def test_gemm_matches_streaming(vs, monkeypatch):
+    """Same inputs through the GEMM-tiled and streaming scans give the same
+    answers (integer data: exact distances)."""
+    xb = syn.int_grid(30_000, 64, 3, 0)
+    xq = syn.int_grid(700, 64, 3, 1)
+    D1, I1, g1 = _search(vs, xb, xq, 16, 0, "auto")
+    monkeypatch.setenv("VS_GEMM", "0")
+    D0, I0, g0 = _search(vs, xb, xq, 16, 0, "auto")
+    assert g1 >= 1 and g0 == 0
+    assert np.array_equal(D0, D1)
+    Dr, Ir = oracle.flat_search(xb, xq, 16, 0, NT)
+    assert_knn_parity(D1, I1, Dr, Ir, 0, rtol=0.0, atol=0.0, xb=xb, xq=xq)
+
+
+def test_gemm_verification_path(vs, monkeypatch):
+    """Lists forced down to 4 entries (VS_SCAN_KKW) with k = 60: the merge
+    must detect queries whose lists may have dropped a winner and search
+    them again; the answer stays exact."""
+    monkeypatch.setenv("VS_SCAN_KKW", "4")
+    xb = syn.int_grid(20_000, 64, 5, 0)
+    xq = syn.int_grid(300, 64, 5, 1)
+    D, I, gemm = _search(vs, xb, xq, 60, 0, "auto")
+    assert gemm >= 1
+    Dr, Ir = oracle.flat_search(xb, xq, 60, 0, NT)
+    assert_knn_parity(D, I, Dr, Ir, 0, rtol=0.0, atol=0.0, xb=xb, xq=xq)
+
+
+def test_gemm_query_blocks_past_padding(vs):
+    """1,300 queries in 256-query blocks: the last block reaches query row
+    1,535, inside the prepared-query padding."""
+    xb16 = syn.to_bf16_bits(syn.normal_unit(5000, 768, 41, 0))
+    xq16 = syn.to_bf16_bits(syn.normal_unit(1300, 768, 41, 1))
+    D, I, gemm = _search(vs, xb16, xq16, 10, 1, "bf16")
+    assert gemm >= 1
+    Dr, Ir = oracle.flat_search(syn.bf16_bits_to_f32(xb16), syn.bf16_bits_to_f32(xq16), 10, 1, NT)
+    assert_knn_parity(D, I, Dr, Ir, 1, rtol=1e-3)
+
+
+@pytest.mark.parametrize("metric", [0, 1])
+def test_gemm_range_search(vs, metric):
+    """Range search with 600 queries runs on the GEMM-tiled kernel (MODE 1)."""
+    xb = syn.normal_unit(8000, 96, 17, 0)
+    xq = np.concatenate([xb[:300] + 0.02, syn.normal_unit(300, 96, 17, 1)]).astype(np.float32)
+    radius = 0.05 if metric == 0 else 0.6
+    g = vs.GpuIndexFlat(96, vs.Metric(metric), storage="f32")
+    g.add(xb)
+    rr = g.range_search(xq, radius)
+    gemm, _ = g.prof_get("gemm")
+    g.close()
+    assert gemm >= 1
+    lims, D, I = oracle.flat_range_search(xb, xq, radius, metric, NT)
+    assert lims[-1] >= 300
+    assert_range_parity(rr.limits, rr.distances, rr.ids, lims, D, I)
+
+
+def test_gemm_self_join(vs):
+    """Self-join (upper triangle, MODE 1) of 3,000 unit vectors with planted
+    near-duplicates on the GEMM-tiled kernel: the pair list equals the
+    oracle's range search filtered to i < j."""
+    base = syn.normal_unit(2800, 64, 23, 0)
+    rng = np.random.default_rng(23)
+    src = rng.integers(0, 2800, 200)
+    dup = base[src] + rng.normal(0, 0.01, (200, 64)).astype(np.float32)
+    dup /= np.linalg.norm(dup.astype(np.float64), axis=1, keepdims=True).astype(np.float32)
+    xb = np.concatenate([base, dup.astype(np.float32)])
+    g = vs.GpuIndexFlat(64, vs.Metric(1), storage="f32")
+    g.add(xb)
+    i, j, s = g.self_join(0.95)
+    gemm, _ = g.prof_get("gemm")
+    g.close()
+    assert gemm >= 1
+    ri, rj, rs = oracle.self_join(xb, 0.95, nthreads=NT)
+    assert len(ri) >= 200
+    assert np.array_equal(i, ri) and np.array_equal(j, rj)
+    assert np.array_equal(s.view(np.uint32), rs.view(np.uint32))
+
+
+def test_gemm_kmeans_step(vs):
+    """k-means steps with 20,000 points as queries run on the GEMM-tiled
+    kernel (fp32 rows, two query planes): assignments, objective and
+    centroids bit-identical to the oracle's."""
+    x, _ = syn.gaussian_mixture(20_000, 256, 64, 0.1, 1234)
+    cen = x[syn.seeded_subset(len(x), 256, 1234)].copy()
+    pts = vs.GpuIndexFlat.l2(256, storage="f32")
+    pts.add(x)
+    for it in range(2):
+        u = syn.rng(77, it).random(256 * 256)
+        a, newc, cnt, obj = vs.kmeans_step(pts, cen, 1, u)
+        ar, _, objr = oracle.kmeans_assign(x, cen, NT)
+        assert np.array_equal(a, ar), f"iteration {it}: {np.sum(a != ar)} assignments differ"
+        assert obj == objr
+        cr, cntr, _ = oracle.kmeans_update(x, ar, cen, 1, u)
+        assert np.array_equal(cnt, cntr)
+        assert np.array_equal(newc.view(np.uint32), cr.view(np.uint32))
+        cen = newc
+    gemm, _ = pts.prof_get("gemm")
+    pts.close()
+    assert gemm >= 2
+
+
+def test_gemm_large_k_unseeded(vs):
+    """k = 300: lists keep 256 entries, more than the two lanes of a list
+    hold in one tile, so the first tile is not seeded (the plain append
+    path runs from the start); the answer stays exact."""
+    xb = syn.int_grid(40_000, 64, 9, 0)
+    xq = syn.int_grid(300, 64, 9, 1)
+    D, I, gemm = _search(vs, xb, xq, 300, 0, "auto")
+    assert gemm >= 1
+    Dr, Ir = oracle.flat_search(xb, xq, 300, 0, NT)
+    assert_knn_parity(D, I, Dr, Ir, 0, rtol=0.0, atol=0.0, xb=xb, xq=xq)

@@ -81,7 +81,7 @@ def test_config2_slice_exact(vs, nq):
     assert idx.storage == "bf16"  # lossless: every value is a bf16 value
     r = idx.search(xq, 100)
     Dr, Ir = oracle.flat_search(xb, xq, 100, 0, NT)
-    assert_knn_parity(r.distances, r.ids, Dr, Ir, 0, rtol=0.0, atol=0.0)
+    assert_knn_parity(r.distances, r.ids, Dr, Ir, 0, rtol=0.0, atol=0.0, xb=xb, xq=xq)
     assert np.all(r.distances == np.round(r.distances))
 
 

@@ -99,7 +99,7 @@ def test_tile_config2_exact(vs, monkeypatch, nw):
     D, I, tiled, _ = _search(vs, xb, xq, 100, 0, "auto")
     assert tiled >= 1
     Dr, Ir = oracle.flat_search(xb, xq, 100, 0, NT)
-    assert_knn_parity(D, I, Dr, Ir, 0, rtol=0.0, atol=0.0)
+    assert_knn_parity(D, I, Dr, Ir, 0, rtol=0.0, atol=0.0, xb=xb, xq=xq)
     assert np.all(D == np.round(D))
 
 
@@ -113,7 +113,7 @@ def test_tile_matches_streaming(vs, monkeypatch):
     assert t1 >= 1 and s0 >= 1 and t0 == 0
     assert np.array_equal(D0, D1)
     Dr, Ir = oracle.flat_search(xb, xq, 16, 0, NT)
-    assert_knn_parity(D1, I1, Dr, Ir, 0, rtol=0.0, atol=0.0)
+    assert_knn_parity(D1, I1, Dr, Ir, 0, rtol=0.0, atol=0.0, xb=xb, xq=xq)
 
 
 @pytest.mark.parametrize("metric", [0, 1])
