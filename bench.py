@@ -174,24 +174,145 @@ def run_search_workload(args, vs, syn, N):
     return out
 
 
-def run_copy_calibration(args):
-    """A plain device copy of known size (torch's copy kernel), the yardstick
-    for the FETCH_SIZE / WRITE_SIZE counters: under rocprofv3 --pmc its
-    per-dispatch KiB, divided by the bytes it must move, is the scale factor
-    applied to the scan kernel's counter readings."""
-    import torch
+def run_kmeans_workload(args, vs, syn):
+    """one Lloyd iteration (assign + update) per step over 2M x 256
+    fp32 points from a 1,024-component mixture, 4,096 centroids from a seeded
+    subset; the centroids of step i feed step i + 1 (kmeans.dart:91-140)."""
+    import oracle
 
-    nbytes = (args.n or 1 << 30)
-    a = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
-    b = torch.empty_like(a)
+    n, d, ncomp, K = args.n or 2_000_000, 256, 1024, 4096
+    x, _ = syn.gaussian_mixture(n, d, ncomp, 0.1, args.seed)
+    cen = x[syn.seeded_subset(n, K, args.seed)].copy()
+    pts = vs.GpuIndexFlat.l2(d, storage="f32")
+    pts.add(x)
+    # jitter draws for empty clusters (the reference takes them from dart:math
+    # Random, kmeans.dart:128-138): seeded uniforms, one stream per step
+    def jitter(step):
+        return syn.rng(args.seed + 7, step).random(K * d)
+
+    for w in range(args.warmup):
+        _, cen, _, _ = vs.kmeans_step(pts, cen, 1, jitter(w))
+    pts.prof_enable(True)
+    pts.prof_reset()
+    cen0 = cen.copy()
+    t = time.perf_counter()
+    for i in range(args.steps):
+        _, cen, _, obj = vs.kmeans_step(pts, cen, 1, jitter(args.warmup + i))
+        log(f"[bench] k-means step {i + 1}/{args.steps}: objective {obj:.6g}")
+    wall = time.perf_counter() - t
+    pts.prof_enable(False)
+    fam = {f: pts.prof_get(f) for f in ("assign", "pick", "exhaustive", "update")}
+    nfb = pts.prof_get("kmeans_fallback_points")[0]
+    nsc, scan_ms = fam["assign"]
+    scan_s = scan_ms / max(nsc, 1) / 1e3
+    flops = 2.0 * n * K * d
+    passes = 3  # fp32 rows x fp32 points: bf16 hi*q0 + lo*q0 + hi*q1
+    achieved = flops / scan_s / 1e12
+    peak = PEAK["bf16_mfma_tflops"] / passes
+    out = {"metric": "k-means assign+update, points per second per iteration",
+           "value": round(n * args.steps / wall, 1), "unit": "points/s",
+           "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": round(wall / args.steps * 1e3, 3), "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+           "config": {"workload": f"c4: k-means step, {n} x {d} fp32 mixture of {ncomp}, "
+                                  f"K={K}, host centroids in/out", "n": n, "d": d, "K": K},
+           "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": round(peak, 1),
+                        "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": None,
+                        "kernel": "assign scan", "avg_ms": round(scan_s * 1e3, 3),
+                        "algorithmic_flops_per_launch": flops,
+                        "peak_note": "bf16 dense MFMA peak / 3 passes (fp32 via split bf16)"},
+           "families_ms": {f: round(v[1] / max(v[0], 1), 3) for f, v in fam.items()},
+           "exhaustive_points_per_step": nfb / args.steps}
+    if not args.no_cpu:
+        cpu, cores = host_info()
+        threads = min(cores, 16)
+        m = min(n, max(threads * 8, int(args.cpu_seconds * 400)))
+        t = time.perf_counter()
+        oracle.kmeans_assign(x[:m], cen0, threads)
+        dt = time.perf_counter() - t
+        out["cpu_baseline"] = {"value": round(m / dt, 1), "unit": "points/s (assign only)",
+                               "cores": threads, "kind": "port",
+                               "sample": f"assign of the first {m} points against {K} centroids "
+                                         f"({dt:.1f} s), fp64 oracle", "cpu": cpu}
+    pts.close()
+    return out
+
+
+def run_join_workload(args, vs, syn):
+    """near-duplicate cosine self-join of 500k x 512 fp32 unit
+    vectors (5% planted copies), all pairs i < j with dot >= 0.95 sorted by
+    (i, j) (vector_dedup_demo.dart:115-128).  One step = one self-join."""
+    import oracle
+
+    n, d, thr = args.n or 500_000, 512, 0.95
+    x = syn.dedup_set(n, d, 0.05, 0.01, args.seed)
+    g = vs.GpuIndexFlat(d, vs.Metric(1), storage="f32")
+    g.add(x)
     for _ in range(args.warmup):
-        b.copy_(a)
-    torch.cuda.synchronize()
+        g.self_join(thr)
+    g.prof_enable(True)
+    g.prof_reset()
+    t = time.perf_counter()
+    for i in range(args.steps):
+        pi, pj, ps = g.self_join(thr)
+        log(f"[bench] self-join {i + 1}/{args.steps}: {len(pi)} pairs")
+    wall = time.perf_counter() - t
+    g.prof_enable(False)
+    nj, join_ms = g.prof_get("join")
+    join_s = join_ms / max(nj, 1) / 1e3
+    flops = 2.0 * d * n * (n - 1) / 2
+    passes = 3
+    achieved = flops / join_s / 1e12
+    peak = PEAK["bf16_mfma_tflops"] / passes
+    out = {"metric": "cosine self-join, vectors per second", "value": round(n * args.steps / wall, 1),
+           "unit": "vectors/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": round(wall / args.steps * 1e3, 3), "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+           "config": {"workload": f"c5: self-join {n} x {d} fp32 unit, 5% planted duplicates, "
+                                  f"cos >= {thr}", "n": n, "d": d, "pairs": int(len(pi))},
+           "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": round(peak, 1),
+                        "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": None,
+                        "kernel": "join scan (upper triangle)", "avg_ms": round(join_s * 1e3, 3),
+                        "algorithmic_flops_per_launch": flops,
+                        "peak_note": "bf16 dense MFMA peak / 3 passes (fp32 via split bf16)"}}
+    if not args.no_cpu:
+        cpu, cores = host_info()
+        threads = min(cores, 16)
+        rows = max(threads, int(args.cpu_seconds * 4))
+        t = time.perf_counter()
+        ri, rj, _ = oracle.self_join(x, thr, row_begin=0, row_end=rows, nthreads=threads)
+        dt = time.perf_counter() - t
+        work = sum(n - 1 - i for i in range(rows))
+        total = n * (n - 1) / 2
+        agree = bool(np.array_equal(ri, pi[pi < rows]) and np.array_equal(rj, pj[pi < rows]))
+        out["cpu_baseline"] = {"value": round(n / (dt * total / work), 3), "unit": "vectors/s",
+                               "cores": threads, "kind": "port",
+                               "sample": f"rows 0..{rows - 1} of the upper triangle ({dt:.1f} s), "
+                                         f"extrapolated linearly to all {n} rows; fp64 oracle",
+                               "cpu": cpu}
+        out["pairs_match_cpu_sample"] = agree
+    g.close()
+    return out
+
+
+def run_copy_calibration(args):
+    """A plain device copy of known size (the library's copy16 kernel), the
+    yardstick for the FETCH_SIZE / WRITE_SIZE counters: under rocprofv3 --pmc
+    its per-dispatch KiB, divided by the bytes it must move, is the scale
+    factor applied to the scan kernel's counter readings."""
+    from vector_store import _native as NN
+
+    nbytes = args.n or 1 << 30
+    src, dst = NN.DeviceBuffer(nbytes), NN.DeviceBuffer(nbytes)
+    lib = NN.load()
+    for _ in range(args.warmup):
+        NN.check(lib.vs_dev_copy(0, dst.ptr, src.ptr, nbytes))
     t = time.perf_counter()
     for _ in range(args.steps):
-        b.copy_(a)
-    torch.cuda.synchronize()
+        NN.check(lib.vs_dev_copy(0, dst.ptr, src.ptr, nbytes))
     dt = (time.perf_counter() - t) / args.steps
+    src.free()
+    dst.free()
     return {"workload": "copy", "bytes_read": nbytes, "bytes_written": nbytes,
             "ms": round(dt * 1e3, 4), "GBps_read_plus_write": round(2 * nbytes / dt / 1e9, 1)}
 
@@ -221,6 +342,10 @@ def main():
         raise SystemExit("no HIP device visible")
     if args.workload == "copy":
         out = run_copy_calibration(args)
+    elif args.workload == "c4":
+        out = run_kmeans_workload(args, vs, syn)
+    elif args.workload == "c5":
+        out = run_join_workload(args, vs, syn)
     else:
         out = run_search_workload(args, vs, syn, None)
     print(json.dumps(out), flush=True)

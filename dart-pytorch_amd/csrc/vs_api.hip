@@ -415,10 +415,11 @@ bool plan_tile(const vs_index *x, int64_t nq, int64_t nrows, int planes, int sto
 // splits so that the grid fills whole rounds of workgroups.  Each query has
 // one candidate list per row wave (lw) in a workgroup, so a list keeps at
 // least kk_final / lw entries and the block's lists together bound the
-// query's kk_final-th value.  Knobs (for sweeps): VS_GEMM (0 disables),
-// VS_GEMM_MIN_NQ (smallest batch that uses it), VS_GEMM_WQ / VS_GEMM_QB /
+// query's kk_final-th value.  Knobs (for sweeps): VS_GEMM (0 disables, 1
+// allows every d; default: rows of >= 256 elements), VS_GEMM_MIN_NQ
+// (smallest batch that uses it; default 512, 256 when forced on), VS_GEMM_WQ / VS_GEMM_QB /
 // VS_GEMM_KC (force a shape), VS_GEMM_ROUNDS (target workgroups per CU),
-// VS_GEMM_GROUP (query blocks per XCD group).
+// VS_GEMM_GROUP (query blocks per XCD group), VS_GEMM_FLUSH (list flush point).
 // The LDS-DMA kernel (gemm_dma_kernel) is switched off: its first run on an
 // MI355X (8-wave shape, d = 200, L2, k = 10) left the GPU faulted, and no
 // mistake in its indexing, waits or barriers has been shown yet.
@@ -426,7 +427,14 @@ constexpr bool kGemmDmaEnabled = false;
 
 bool plan_gemm(const vs_index *x, int64_t nq, int64_t nrows, int planes, int storage,
                bool kk_forced, vs::ScanPlan *p) {
-    if (!env_int("VS_GEMM", 0) || nq < env_int("VS_GEMM_MIN_NQ", 256)) return false;
+    // default: large batches of long rows (measured on MI355X: the GEMM-tiled
+    // scan beats the streaming one at d = 768, batch >= 1024, and on the
+    // k-means assign at d = 256; at d = 128 the streaming scan's 20 waves per
+    // CU hide its list work better)
+    const int mode = env_int("VS_GEMM", -1);
+    if (mode == 0) return false;
+    if (mode < 0 && x->ld < 256) return false;
+    if (nq < env_int("VS_GEMM_MIN_NQ", mode < 0 ? 512 : 256)) return false;
     struct Shape {
         int st, pb, wr, wq, rb, qb, kc;
     };
@@ -482,6 +490,7 @@ bool plan_gemm(const vs_index *x, int64_t nq, int64_t nrows, int planes, int sto
     if (!pick) return false;
     p->kind = 2;
     p->g_ns = ns;
+    p->g_flush = env_int("VS_GEMM_FLUSH", 0);
     p->kk = kk;
     p->cap = cap;
     p->bn = 32 * pick->wq * pick->qb;
@@ -766,15 +775,24 @@ int range_core(vs_index *x, const vs::PreparedQueries &pq, double radius, int se
     out->id.clear();
     out->s.clear();
     if (pq.nq == 0 || x->ntotal == 0) return VS_OK;
+    // one-pass selection of fp32 rows where the GEMM-tiled scan runs it: the
+    // acceptance bounds widen to its error and every hit is re-tested exactly
     vs::ScanPlan plan;
-    int rc = plan_scan(x, pq.nq, x->ntotal, pq.planes, 8, x->storage, &plan);
-    if (rc) return rc;
+    int rc = VS_OK;
+    bool coarse = x->storage == 0 && env_int("VS_COARSE", 1) != 0;
+    if (coarse) coarse = plan_scan(x, pq.nq, x->ntotal, 1, 8, vs::kSelectCoarse, &plan) == VS_OK &&
+                         plan.kind == 2;
+    if (!coarse) {
+        plan = vs::ScanPlan();
+        rc = plan_scan(x, pq.nq, x->ntotal, pq.planes, 8, x->storage, &plan);
+        if (rc) return rc;
+    }
     if ((rc = scan_fits(plan, pq))) return rc;
     const float xmax = xnorm_max(x);
     VS_HIP(x->athr.ensure((size_t)pq.nq * 4), "range bounds");
     const int exact_q = (qflags & vs::kFlagNotBf16) ? 0 : 1;
     const int exact_x = x->storage == 1 ? 1 : 0;
-    VS_HIP(vs::launch_range_bounds(pq, x->d, x->metric, radius, xmax, exact_q, exact_x,
+    VS_HIP(vs::launch_range_bounds(pq, x->d, x->metric, radius, xmax, exact_q, exact_x, coarse,
                                    x->athr.as<float>(), x->st),
            "range bounds");
     VS_HIP(x->rcount.ensure(sizeof(unsigned long long)), "range counter");
@@ -1253,9 +1271,17 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     cview.d = d;
     cview.lds_max = x->lds_max;
     cview.num_cu = x->num_cu;
+    // one-pass selection (bf16 hi planes of points and centroids) where the
+    // GEMM-tiled scan runs it; the shortlist proof below widens its bound
     vs::ScanPlan plan;
-    rc = plan_scan(&cview, n, K, pq.planes, 16, 0, &plan);
-    if (rc) return rc;
+    bool coarse = env_int("VS_COARSE", 1) != 0;
+    if (coarse) coarse = plan_scan(&cview, n, K, 1, 16, vs::kSelectCoarse, &plan) == VS_OK &&
+                         plan.kind == 2;
+    if (!coarse) {
+        plan = vs::ScanPlan();
+        rc = plan_scan(&cview, n, K, pq.planes, 16, 0, &plan);
+        if (rc) return rc;
+    }
     if ((rc = scan_fits(plan, pq))) return rc;
     const size_t nlist = (size_t)plan.nqblk * plan.nsplit * plan.lw * plan.bn * plan.cap;
     VS_HIP(x->cand_v.ensure(nlist * 4), "candidate lists");
@@ -1280,9 +1306,19 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
         VS_HIP(hipStreamSynchronize(x->st), "max");
     }
     const float pmax = xnorm_max(x);
+    // Error of the accumulator |c|^2 - 2 x.c (point x, centroid c):
+    //  - operands: each product of the MFMA operands lies within r |2 x_j c_j|
+    //    of -2 x_j c_j, r = 2^-8 for the one-pass selection (both operands
+    //    rounded to bf16, 2^-9 each) and 2^-15 for the split-bf16 passes (hi
+    //    + lo within 2^-18 of each value, the dropped lo * q1 term);
+    //  - fp32 accumulation of at most 3 d + 1 terms: gamma = (3 d + 4) 2^-24;
+    // so |error| <= 2 r |x| |c| + gamma (|c|^2 + 2 |x| |c|) (Cauchy-Schwarz),
+    // taken with a 25% margin.
     const double u = 1.0 / 16777216.0;
-    const double rel = 4.0 * (d + 4) * u + 8.0 / 65536.0;
-    const float bound = (float)(rel * (2.0 * pmax * std::sqrt((double)cmax) + cmax) * 2.0 + 1e-6);
+    const double r = coarse ? 1.0 / 256.0 : 1.0 / 32768.0;
+    const double gam = (3.0 * d + 4.0) * u;
+    const double pc = (double)pmax * std::sqrt((double)cmax);
+    const float bound = (float)(1.25 * (2.0 * r * pc + gam * ((double)cmax + 2.0 * pc)) + 1e-6);
 
     VS_HIP(x->km_assign.ensure((size_t)n * 4), "assignments");
     VS_HIP(x->km_best.ensure((size_t)n * 8), "distances");
@@ -1292,7 +1328,7 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     int32_t *fb_list = fb_count + 1;
     {
         ProfScope ps(x, "pick");
-        VS_HIP(vs::launch_kmeans_pick(x->km_cen.as<float>(), ld, d, n, x->km_cen.as<float>(), K,
+        VS_HIP(vs::launch_kmeans_pick((const float *)x->xb, ld, d, n, x->km_cen.as<float>(), K,
                                       x->cand_v.as<float>(), x->cand_i.as<int32_t>(),
                                       x->gthr.as<uint32_t>(), plan, bound,
                                       pq.qf, x->km_assign.as<int32_t>(), x->km_best.as<double>(),
@@ -1302,6 +1338,7 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     int32_t nfb = 0;
     VS_HIP(hipMemcpyAsync(&nfb, fb_count, 4, hipMemcpyDeviceToHost, x->st), "fallbacks");
     VS_HIP(hipStreamSynchronize(x->st), "assign");
+    x->prof["kmeans_fallback_points"].launches += nfb;
     if (nfb > 0) {
         ProfScope ps(x, "exhaustive");
         VS_HIP(vs::launch_kmeans_exhaustive((const float *)x->xb, ld, d, x->km_cen.as<float>(), K,
@@ -1420,6 +1457,16 @@ int vs_dev_free(int device, void *p) {
 int vs_dev_upload(int device, void *dst, const void *src, int64_t bytes) {
     DeviceGuard g(device);
     VS_HIP(hipMemcpy(dst, src, (size_t)bytes, hipMemcpyHostToDevice), "upload");
+    return VS_OK;
+}
+
+int vs_dev_copy(int device, void *dst, const void *src, int64_t bytes) {
+    if (!dst || !src || bytes < 0 || bytes % 16 || ((uintptr_t)dst | (uintptr_t)src) % 16)
+        return set_err(VS_ERR_INVALID, "vs_dev_copy: 16-byte aligned buffers and sizes only");
+    DeviceGuard g(device);
+    if (g.err != hipSuccess) return hip_err(g.err, "hipSetDevice");
+    VS_HIP(vs::launch_copy16(src, dst, bytes / 16, nullptr), "copy kernel");
+    VS_HIP(hipDeviceSynchronize(), "copy kernel");
     return VS_OK;
 }
 

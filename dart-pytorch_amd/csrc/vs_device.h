@@ -59,6 +59,8 @@ struct ScanKArgs {
     int64_t nq;
     int64_t nqblk, nsplit, rows_per_split;
     int64_t qgroup;      // tiled scan: query blocks per XCD group
+    int flush_at;        // GEMM-tiled scan: a list holding more entries is cut to kk
+                         // before the next append (so its threshold keeps tightening)
     int kk, cap, metric;
     int kk_final;        // candidates the merge keeps per query
     int publish_block;   // nl * kk >= kk_final: a block's nl lists of a query bound its kk_final-th value

@@ -18,7 +18,9 @@
 // accumulator starts at the row norm xn (L2) or 0 (IP), so it is "smaller is
 // better" for both metrics.  fp32 rows are split into bf16 hi and lo planes
 // when they are written to LDS; the products are hi*q0 + lo*q0 (+ hi*q1 when
-// the queries need a second plane).  The row norms of a tile travel with its
+// the queries need a second plane).  Storage code 2 is the one-pass selection
+// of fp32 rows: only the bf16 hi plane of the rows and the first query plane
+// are multiplied (the callers widen their margins and re-test exactly).  The row norms of a tile travel with its
 // first K-chunk.
 //
 // Epilogue per row tile: per-(row wave, query) candidate lists in global
@@ -26,6 +28,8 @@
 // 1), read by the same merge, re-rank, k-means and range kernels as the
 // other scans.  The full distance matrix is never written.
 #include <limits.h>
+
+#include <algorithm>
 
 #include <type_traits>
 
@@ -39,7 +43,7 @@ struct GemmShape {
     static constexpr int BR = WR * 32 * RB, BQ = WQ * 32 * QB;
     static constexpr int AP = ST == 0 ? 2 : 1;  // row planes in LDS: bf16 hi (, lo)
     static constexpr int KP = KC + 8;           // LDS row stride in elements
-    static constexpr int ESZ = ST == 0 ? 4 : 2;  // bytes per stored element
+    static constexpr int ESZ = ST == 1 ? 2 : 4;  // bytes per stored element
     static constexpr int A_CPR = KC * ESZ / 16;  // 16-byte global chunks per row and K-chunk
     static constexpr int A_LOADS = BR * A_CPR / NT;
     static constexpr int B_CPR = KC * 2 / 16;  // 16-byte chunks per query plane and K-chunk
@@ -56,7 +60,7 @@ struct GemmShape {
 size_t gemm_lds_bytes(int st, int pb, int wr, int wq, int rb, int qb, int kc, int cap) {
     const size_t br = (size_t)wr * 32 * rb, bq = (size_t)wq * 32 * qb, kp = (size_t)kc + 8;
     const size_t stage = ((st == 0 ? 2 : 1) * br + (size_t)pb * bq) * kp * 2 + br * 4;
-    return 2 * stage + (size_t)wr * bq * 8 + (size_t)wr * wq * cap * 8;
+    return 2 * stage + (size_t)wr * bq * 8 + (size_t)wr * wq * cap * 8;  // st 2: one hi plane
 }
 
 // Epilogue of one row tile (shared by both kernels).  Lane (l32, h) of wave
@@ -177,11 +181,13 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[QB][RB], const Sca
                 const int q = qw0 + qb * 32 + l32;
                 // make room: a list this tile could overflow (a query
                 // gains at most 32 * RB entries per tile from this
-                // wave) is cut to its kk best first
-                if (__ballot(h == 0 && cnt_w[q] > a.cap - 32 * RB)) {
+                // wave), or one past its flush point, is cut to its kk
+                // best first (which also tightens its threshold)
+                const int room = min(a.cap - 32 * RB, a.flush_at);
+                if (__ballot(h == 0 && cnt_w[q] > room)) {
                     for (int j = 0; j < 32; ++j) {
                         const int qq = qw0 + qb * 32 + j;
-                        if (cnt_w[qq] > a.cap - 32 * RB)
+                        if (cnt_w[qq] > room)
                             flush_list(cv + (int64_t)qq * a.cap, ci + (int64_t)qq * a.cap,
                                        &cnt_w[qq], &thr_w[qq], &thr[qq], BQ, WR,
                                        &a.gthr[q0 + qq], sv_w, si_w, a.cap, a.kk,
@@ -337,6 +343,10 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
             const int i = tid + j * NT, row = i / S::A_CPR, c = i % S::A_CPR;
             if constexpr (ST == 1) {
                 *(u32x4_t *)(As + row * KP + c * 8) = ra[j];
+            } else if constexpr (ST == 2) {  // one-pass selection: the bf16 hi plane only
+                typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+                const bf16x4_t hi = __builtin_convertvector(__builtin_bit_cast(f32x4_t, ra[j]), bf16x4_t);
+                *(u32x2_t *)(As + row * KP + c * 4) = __builtin_bit_cast(u32x2_t, hi);
             } else {
                 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
                 const f32x4_t f = __builtin_bit_cast(f32x4_t, ra[j]);
@@ -785,6 +795,9 @@ hipError_t launch_gemm_scan(int storage, int planes, const ScanPlan &plan, const
     ScanKArgs ga = args;
     ga.qgroup = plan.tile_group;
     ga.publish_block = plan.lw * plan.kk >= plan.kk_final;
+    // cut lists at twice their keep: each cut tightens the list's threshold
+    // for the price of one sort of ~2 kk entries
+    ga.flush_at = plan.g_flush > 0 ? plan.g_flush : std::max(2 * plan.kk, 16);
     void (*fn)(ScanKArgs) = nullptr;
 #define VS_DPICK(PB_, WR_, WQ_, RB_, QB_, NS_)                                                 \
     if (storage == 1 && planes == PB_ && plan.lw == WR_ && plan.g_wq == WQ_ &&                  \

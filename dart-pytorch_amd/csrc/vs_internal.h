@@ -88,6 +88,7 @@ struct ScanPlan {
     int kind = 0;         // 0: streaming scan (vs_kernels.hip); 1: LDS-tiled scan (vs_tile.hip);
                           // 2: GEMM-tiled scan (vs_gemm.hip)
     int g_ns = 0;            // GEMM-tiled scan: LDS-DMA stages (0: register-staged kernel)
+    int g_flush = 0;         // GEMM-tiled scan: list flush point (0: twice the keep)
     int g_wq = 2, g_qb = 4;  // GEMM-tiled scan: query waves, 32-query blocks per wave
                              // (row waves = lw, 32-row blocks per wave = tile_rb,
                              // K-chunk = tile_kc)
@@ -136,8 +137,11 @@ hipError_t launch_range_refine(const void *xb, int storage, int64_t ld, int64_t 
 
 // Per-query acceptance bounds for the range scan (accumulator space).
 hipError_t launch_range_bounds(const PreparedQueries &pq, int64_t d, int metric, double radius,
-                               float xnorm_max, int exact_q, int exact_x, float *athr,
+                               float xnorm_max, int exact_q, int exact_x, int coarse, float *athr,
                                hipStream_t st);
+
+// dst = src, n16 16-byte words (both 16-byte aligned)
+hipError_t launch_copy16(const void *src, void *dst, int64_t n16, hipStream_t st);
 
 // max over rows of xn (for margins)
 hipError_t launch_max_reduce(const float *x, int64_t n, float *out, hipStream_t st);
@@ -203,9 +207,12 @@ size_t tile_lds_bytes(int qb, int pb, int nw, int cap, int64_t ld);
 // preference: X(storage, query planes, row waves, query waves, 32-row blocks
 // per wave, 32-query blocks per wave, K-chunk).  A workgroup covers
 // 32 * row waves * row blocks database rows by 32 * query waves * query
-// blocks queries per tile.
+// blocks queries per tile.  Storage 2 = fp32 rows read as their bf16 hi
+// plane only (one-pass selection, kSelectCoarse below).
 #define VS_GEMM_SHAPES(X)                                                                     \
     X(1, 1, 2, 4, 4, 2, 32)                                                                   \
+    X(2, 1, 2, 4, 4, 2, 32)                                                                   \
+    X(2, 1, 2, 2, 4, 2, 32)                                                                   \
     X(1, 1, 2, 2, 4, 2, 32)                                                                   \
     X(1, 2, 2, 4, 4, 2, 32)                                                                   \
     X(1, 2, 2, 2, 4, 2, 32)                                                                   \
@@ -220,6 +227,10 @@ size_t tile_lds_bytes(int qb, int pb, int nw, int cap, int64_t ld);
 #define VS_GEMM_DMA_SHAPES(X)                                                                 \
     X(1, 2, 4, 4, 2, 4)                                                                       \
     X(1, 2, 2, 4, 2, 4)
+
+// Storage code of the one-pass selection (fp32 rows, bf16 hi plane and the
+// first query plane only): the GEMM-tiled scan's shapes with storage 2.
+constexpr int kSelectCoarse = 2;
 
 // LDS of the GEMM-tiled scans (stages plus list bookkeeping).
 size_t gemm_dma_lds_bytes(int pb, int wr, int wq, int rb, int qb, int ns, int cap);

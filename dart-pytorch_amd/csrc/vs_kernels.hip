@@ -15,6 +15,8 @@
 // fp32 rows are split in registers into bf16 hi + lo, so an fp32 dot is
 // hi*q0 + lo*q0 (+ hi*q1 when the query needs a second plane).
 #include <float.h>
+
+#include <algorithm>
 #include <limits.h>
 #include <math.h>
 
@@ -545,7 +547,7 @@ template <int MODE>
 static hipError_t launch_scan_mode(int storage, const PreparedQueries &pq, const ScanPlan &plan,
                                    const ScanKArgs &args, hipStream_t st) {
     if (plan.kind == 1) return launch_tile_scan<MODE>(storage, pq.planes, plan, args, st);
-    if (plan.kind == 2) return launch_gemm_scan<MODE>(storage, pq.planes, plan, args, st);
+    if (plan.kind == 2) return launch_gemm_scan<MODE>(plan.tile_st, plan.tile_pb, plan, args, st);
     const int64_t total = plan.nqblk * plan.nsplit;
     const int64_t grid = ((total + 7) / 8) * 8;
     const size_t lds = plan.lds_bytes;
@@ -692,6 +694,7 @@ __device__ double exact_score(const float *qrow, const void *xb, int64_t ld, int
 // ---------------------------------------------------------------------------
 struct MergeKArgs {
     const void *xb;
+    const float *pts;  // k-means pick: the points' stored rows (ld values each)
     int64_t ld, d;
     int metric;
     const float *qf;
@@ -928,17 +931,20 @@ hipError_t launch_merge_refine(const void *xb, int storage, int64_t ld, int64_t 
     return hipGetLastError();
 }
 
+template <int KK>
+__global__ void kmeans_pick_kernel(MergeKArgs a);
+
 hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, const float *cen,
                               int64_t K, const float *cand_v, const int32_t *cand_i,
                               const uint32_t *gthr, const ScanPlan &plan, float bound,
                               const float *qf, int32_t *assign,
                               double *best_sq, int32_t *fallback_count, int32_t *fallback_list,
                               hipStream_t st) {
-    (void)x;
     (void)K;
     if (n <= 0) return hipSuccess;
     MergeKArgs a{};
     a.xb = cen;
+    a.pts = x;
     a.ld = ld;
     a.d = d;
     a.metric = 0;
@@ -958,6 +964,10 @@ hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, 
     a.best_sq = best_sq;
     a.fb_count = fallback_count;
     a.fb_list = fallback_list;
+    if (plan.kk_final == 16 && plan.kk == 16) {
+        kmeans_pick_kernel<16><<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(a);
+        return hipGetLastError();
+    }
     const size_t lds = merge_lds(ld);
     void (*fn)(MergeKArgs) = merge_refine_kernel<0, 1>;
     if (lds > 64 * 1024) {
@@ -967,6 +977,106 @@ hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, 
     }
     hipLaunchKernelGGL(fn, dim3((unsigned)n), dim3(256), lds, st, a);
     return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// k-means shortlist pick, one lane per point (the lists of a point hold at
+// most KK candidates each, KK = the shortlist length kk_final).  The lane
+// keeps the KK smallest (accumulator, id) pairs of its lists in registers,
+// re-scores exactly -- fp64, dimensions in order, as kmeans.dart:93-101 --
+// only the candidates whose accumulator lies within 2 * bound of the best
+// one (any other is provably worse than that one), and takes the argmin
+// with the lowest id among equal scores.  The pick is proven when every
+// centroid outside the shortlist (accumulator >= the KK-th smallest a_last)
+// is provably worse; unproven points go to the exhaustive kernel.
+// ---------------------------------------------------------------------------
+template <int KK>
+__global__ __launch_bounds__(256) void kmeans_pick_kernel(MergeKArgs a) {
+    const int64_t qg = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (qg >= a.nq) return;
+    const int64_t qblk = qg / a.bn, q = qg % a.bn;
+    float bv[KK];
+    int bi[KK];
+#pragma unroll
+    for (int i = 0; i < KK; ++i) {
+        bv[i] = VS_INF;
+        bi[i] = INT_MAX;
+    }
+    // entries above the point's final shared threshold are not among the KK
+    // smallest (at least KK candidates lie at or below it)
+    const float tfinal = a.gthr ? dec_order(a.gthr[qg]) : VS_INF;
+    const int64_t nlists = a.nsplit * a.lw;
+    for (int64_t l = 0; l < nlists; ++l) {
+        const int64_t split = l / a.lw, w = l % a.lw;
+        const int64_t off = (((qblk * a.nsplit + split) * a.lw + w) * a.bn + q) * a.cap;
+        for (int j = 0; j < a.kl; j += 4) {  // kl is a multiple of 4
+            const float4 v4 = *(const float4 *)(a.cand_v + off + j);
+            const int4 i4 = *(const int4 *)(a.cand_i + off + j);
+            const float vs4[4] = {v4.x, v4.y, v4.z, v4.w};
+            const int is4[4] = {i4.x, i4.y, i4.z, i4.w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                float cv = vs4[u];
+                int ci = is4[u];
+                if (ci < 0 || cv > tfinal) continue;
+                if (!(cv < bv[KK - 1] || (cv == bv[KK - 1] && ci < bi[KK - 1]))) continue;
+#pragma unroll
+                for (int i = 0; i < KK; ++i) {  // insertion into the sorted pairs
+                    const bool lt = cv < bv[i] || (cv == bv[i] && ci < bi[i]);
+                    const float tv = lt ? bv[i] : cv;
+                    const int ti = lt ? bi[i] : ci;
+                    bv[i] = lt ? cv : bv[i];
+                    bi[i] = lt ? ci : bi[i];
+                    cv = tv;
+                    ci = ti;
+                }
+            }
+        }
+    }
+    // exact scores: the point's stored row and the centroid rows, both ld
+    // values with zeros past d (the padding adds +0.0), read 16 bytes at a
+    // time and summed in dimension order; |x|^2 in order alongside the first
+    const float4 *xr = (const float4 *)(a.pts + qg * a.ld);
+    const float *cen = (const float *)a.xb;
+    const float lim = bv[0] + 2.0f * a.bound;
+    const int64_t n4 = a.ld / 4;
+    double best = __builtin_huge_val(), xx = 0.0;
+    int bid = INT_MAX;
+#pragma unroll
+    for (int i = 0; i < KK; ++i) {
+        if (bi[i] != INT_MAX && (i == 0 || bv[i] <= lim)) {
+            const float4 *cr = (const float4 *)(cen + (int64_t)bi[i] * a.ld);
+            double s = 0.0;
+            for (int64_t j4 = 0; j4 < n4; ++j4) {
+                const float4 xv = xr[j4];
+                const float4 cv = cr[j4];
+                const double d0 = (double)xv.x - (double)cv.x, d1 = (double)xv.y - (double)cv.y;
+                const double d2 = (double)xv.z - (double)cv.z, d3 = (double)xv.w - (double)cv.w;
+                s = s + d0 * d0;
+                s = s + d1 * d1;
+                s = s + d2 * d2;
+                s = s + d3 * d3;
+                if (i == 0) {
+                    xx = xx + (double)xv.x * (double)xv.x;
+                    xx = xx + (double)xv.y * (double)xv.y;
+                    xx = xx + (double)xv.z * (double)xv.z;
+                    xx = xx + (double)xv.w * (double)xv.w;
+                }
+            }
+            if (s < best || (s == best && bi[i] < bid)) {
+                best = s;
+                bid = bi[i];
+            }
+        }
+    }
+    // accumulators are within `bound` of |c|^2 - 2 x.c = score - |x|^2
+    const float a_last = bv[KK - 1];
+    const bool safe = bid != INT_MAX &&
+                      (a_last == VS_INF ||
+                       (double)a_last - (double)a.bound > (best - xx) + 1e-9 * (fabs(xx) + 1.0));
+    a.assign[qg] = bid == INT_MAX ? 0 : bid;
+    a.best_sq[qg] = best;
+    if (!safe) a.fb_list[atomicAdd(a.fb_count, 1)] = (int32_t)qg;
 }
 
 // ---------------------------------------------------------------------------
@@ -980,18 +1090,29 @@ __global__ __launch_bounds__(256) void kmeans_exhaustive_kernel(const float *__r
                                                                 const int32_t *__restrict__ list,
                                                                 int32_t *assign,
                                                                 double *best_sq) {
+    extern __shared__ __align__(16) float xs[];  // the point's row, ld values (zero past d)
     __shared__ double dsh[256];
     __shared__ int ish[256];
     const int64_t p = list[blockIdx.x];
-    const float *xp = x + p * ld;
+    for (int64_t j = threadIdx.x; j < ld; j += 256) xs[j] = x[p * ld + j];
+    __syncthreads();
     double best = __builtin_huge_val();
     int bid = INT_MAX;
+    // one centroid per thread; its row is read in 16-byte pieces and summed
+    // in dimension order (the zero padding past d adds +0.0)
     for (int64_t c = threadIdx.x; c < K; c += 256) {
-        const float *cc = cen + c * ld;
+        const float4 *cc = (const float4 *)(cen + c * ld);
         double s = 0.0;
-        for (int64_t j = 0; j < d; ++j) {
-            const double diff = (double)xp[j] - (double)cc[j];
-            s = s + diff * diff;
+#pragma unroll 4
+        for (int64_t j4 = 0; j4 < ld / 4; ++j4) {
+            const float4 cv = cc[j4];
+            const float4 xv = ((const float4 *)xs)[j4];
+            const double d0 = (double)xv.x - (double)cv.x, d1 = (double)xv.y - (double)cv.y;
+            const double d2 = (double)xv.z - (double)cv.z, d3 = (double)xv.w - (double)cv.w;
+            s = s + d0 * d0;
+            s = s + d1 * d1;
+            s = s + d2 * d2;
+            s = s + d3 * d3;
         }
         if (s < best) {  // c increases: keeps the lowest id among equals
             best = s;
@@ -1022,8 +1143,8 @@ hipError_t launch_kmeans_exhaustive(const float *x, int64_t ld, int64_t d, const
                                     int64_t K, const int32_t *list, int64_t m, int32_t *assign,
                                     double *best_sq, hipStream_t st) {
     if (m <= 0) return hipSuccess;
-    kmeans_exhaustive_kernel<<<dim3((unsigned)m), dim3(256), 0, st>>>(x, ld, d, cen, K, list,
-                                                                      assign, best_sq);
+    kmeans_exhaustive_kernel<<<dim3((unsigned)m), dim3(256), (size_t)ld * 4, st>>>(
+        x, ld, d, cen, K, list, assign, best_sq);
     return hipGetLastError();
 }
 
@@ -1102,16 +1223,19 @@ __global__ void range_bounds_kernel(const float *__restrict__ qnorm, int64_t nq,
 }
 
 hipError_t launch_range_bounds(const PreparedQueries &pq, int64_t d, int metric, double radius,
-                               float xnorm_max, int exact_q, int exact_x, float *athr,
+                               float xnorm_max, int exact_q, int exact_x, int coarse, float *athr,
                                hipStream_t st) {
     if (pq.nq <= 0) return hipSuccess;
     // relative error of the split-bf16 dot product with fp32 accumulation:
     // products: each operand within 2^-16 relative of its value (hi + lo),
     // 2^-8 when a query is rounded to one bf16 plane; accumulation gamma_d.
+    // One-pass selection rounds both operands to bf16 (2^-9 each, taken
+    // four times for margin).
     const double u = 1.0 / 16777216.0;
     double rel = 4.0 * (double)(d + 4) * u + 1.0 / 1048576.0;
     if (!exact_x) rel += 4.0 / 65536.0;
     if (!exact_q) rel += 4.0 / 65536.0;
+    if (coarse) rel += 4.0 / 256.0;
     range_bounds_kernel<<<dim3((unsigned)((pq.nq + 255) / 256)), dim3(256), 0, st>>>(
         pq.qnorm, pq.nq, metric, radius, xnorm_max, (float)rel, athr);
     return hipGetLastError();
@@ -1169,6 +1293,25 @@ hipError_t launch_max_reduce(const float *x, int64_t n, float *out, hipStream_t 
     hipError_t e = hipMemsetAsync(out, 0, sizeof(float), st);
     if (e != hipSuccess || n <= 0) return e;
     max_reduce_kernel<<<dim3(1024), dim3(256), 0, st>>>(x, n, out);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Plain device copy (16-byte vector loads and stores, grid-stride), the
+// yardstick for the memory counters: its bytes moved are known exactly.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void copy16_kernel(const u32x4_t *__restrict__ src,
+                                                     u32x4_t *__restrict__ dst, int64_t n16) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16;
+         i += (int64_t)gridDim.x * 256)
+        dst[i] = src[i];
+}
+
+hipError_t launch_copy16(const void *src, void *dst, int64_t n16, hipStream_t st) {
+    if (n16 <= 0) return hipSuccess;
+    const int64_t blocks = std::min<int64_t>((n16 + 255) / 256, 256 * 32);
+    copy16_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>((const u32x4_t *)src,
+                                                                (u32x4_t *)dst, n16);
     return hipGetLastError();
 }
 

@@ -158,6 +158,9 @@ VS_API int vs_dev_alloc(int device, int64_t bytes, void **out);
 VS_API int vs_dev_free(int device, void *p);
 VS_API int vs_dev_upload(int device, void *dst_dev, const void *src_host, int64_t bytes);
 VS_API int vs_dev_download(int device, void *dst_host, const void *src_dev, int64_t bytes);
+/* dst_dev = src_dev with a plain 16-byte-per-lane copy kernel (the yardstick
+ * of the FETCH_SIZE / WRITE_SIZE counters); sizes and pointers 16-byte aligned. */
+VS_API int vs_dev_copy(int device, void *dst_dev, const void *src_dev, int64_t bytes);
 VS_API int vs_device_count(int *count);
 VS_API int vs_device_name(int device, char *buf, int64_t len);
 

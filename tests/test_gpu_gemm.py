@@ -253,3 +253,92 @@ def test_gemm_large_k_unseeded(vs):
     assert gemm >= 1
     Dr, Ir = oracle.flat_search(xb, xq, 300, 0, NT)
     assert_knn_parity(D, I, Dr, Ir, 0, rtol=0.0, atol=0.0, xb=xb, xq=xq)
+
+
+COARSE_KEY = "gemm:2,1,2,4,4,2,32"  # one-pass selection shape (storage code 2)
+
+
+@pytest.mark.parametrize("coarse", [1, 0])
+def test_coarse_self_join(vs, monkeypatch, coarse):
+    """configs[4] shape at 4,000 rows (d = 512, 5% planted copies, cos >=
+    0.95): the one-pass selection (bf16 hi planes, widened margins, exact
+    fp64 re-test) and the three-pass one give the oracle's pair list."""
+    monkeypatch.setenv("VS_GEMM", "-1")  # the default planner rule
+    monkeypatch.setenv("VS_COARSE", str(coarse))
+    x = syn.dedup_set(4000, 512, 0.05, 0.01, 11)
+    g = vs.GpuIndexFlat(512, vs.Metric(1), storage="f32")
+    g.add(x)
+    i, j, s = g.self_join(0.95)
+    n1, _ = g.prof_get(COARSE_KEY)
+    gemm, _ = g.prof_get("gemm")
+    g.close()
+    assert gemm >= 1 and (n1 >= 1) == bool(coarse)
+    ri, rj, rs = oracle.self_join(x, 0.95, nthreads=NT)
+    assert len(ri) >= 200
+    assert np.array_equal(i, ri) and np.array_equal(j, rj)
+    assert np.array_equal(s.view(np.uint32), rs.view(np.uint32))
+
+
+@pytest.mark.parametrize("coarse", [1, 0])
+def test_coarse_kmeans(vs, monkeypatch, coarse):
+    """configs[3] arithmetic at 30,000 points (d = 256, 1,024 mixture
+    components, 4,096 centroids): assignments, objective and centroids equal
+    the oracle's with and without the one-pass selection."""
+    monkeypatch.setenv("VS_GEMM", "-1")
+    monkeypatch.setenv("VS_COARSE", str(coarse))
+    x, _ = syn.gaussian_mixture(30_000, 256, 1024, 0.1, 77)
+    cen = x[syn.seeded_subset(len(x), 4096, 77)].copy()
+    pts = vs.GpuIndexFlat.l2(256, storage="f32")
+    pts.add(x)
+    u = syn.rng(78, 0).random(4096 * 256)
+    a, newc, cnt, obj = vs.kmeans_step(pts, cen, 1, u)
+    n1, _ = pts.prof_get(COARSE_KEY)
+    pts.close()
+    assert (n1 >= 1) == bool(coarse)
+    ar, _, objr = oracle.kmeans_assign(x, cen, NT)
+    assert np.array_equal(a, ar), f"{np.sum(a != ar)} assignments differ"
+    assert obj == objr
+    cr, cntr, _ = oracle.kmeans_update(x, ar, cen, 1, u)
+    assert np.array_equal(cnt, cntr)
+    assert np.array_equal(newc.view(np.uint32), cr.view(np.uint32))
+
+
+@pytest.mark.parametrize("metric", [0, 1])
+def test_coarse_range_search(vs, monkeypatch, metric):
+    """Range search of 700 fp32 queries (d = 256) on the one-pass selection:
+    the CSR result equals the oracle's bit for bit."""
+    monkeypatch.setenv("VS_GEMM", "-1")
+    xb = syn.normal_unit(6000, 256, 19, 0)
+    xq = np.concatenate([xb[:350] + 0.01, syn.normal_unit(350, 256, 19, 1)]).astype(np.float32)
+    radius = 0.05 if metric == 0 else 0.5
+    g = vs.GpuIndexFlat(256, vs.Metric(metric), storage="f32")
+    g.add(xb)
+    rr = g.range_search(xq, radius)
+    n1, _ = g.prof_get(COARSE_KEY)
+    g.close()
+    assert n1 >= 1
+    lims, D, I = oracle.flat_range_search(xb, xq, radius, metric, NT)
+    assert lims[-1] >= 350
+    assert_range_parity(rr.limits, rr.distances, rr.ids, lims, D, I)
+
+
+@pytest.mark.parametrize("coarse", [1, 0])
+def test_kmeans_exhaustive_fallback(vs, monkeypatch, coarse):
+    """Twenty identical copies of one centroid fill the 16-entry shortlist
+    of the points near it, so their pick cannot be proven and the exhaustive
+    exact scan runs: the answer is the lowest index among the copies (the
+    strict '<' scan, kmeans.dart:93-101), as the oracle gives."""
+    monkeypatch.setenv("VS_GEMM", "-1")
+    monkeypatch.setenv("VS_COARSE", str(coarse))
+    x, _ = syn.gaussian_mixture(6000, 256, 16, 0.1, 5)
+    cen = x[syn.seeded_subset(len(x), 300, 5)].copy()
+    cen[100:120] = cen[3]  # 20 copies of centroid 3
+    pts = vs.GpuIndexFlat.l2(256, storage="f32")
+    pts.add(x)
+    a, newc, cnt, obj = vs.kmeans_step(pts, cen, 1, syn.rng(6, 0).random(300 * 256))
+    nfb, _ = pts.prof_get("kmeans_fallback_points")
+    pts.close()
+    assert nfb >= 1
+    ar, _, objr = oracle.kmeans_assign(x, cen, NT)
+    assert np.array_equal(a, ar) and obj == objr
+    assert not np.any((a >= 100) & (a < 120))  # copies lose to centroid 3

@@ -36,8 +36,10 @@ SHAPES = [
 
 @pytest.fixture(autouse=True)
 def _tiled(monkeypatch):
-    """The tiled scan is opt-in (VS_TILE=1); every test here turns it on."""
+    """The tiled scan is opt-in (VS_TILE=1); every test here turns it on, and
+    the GEMM-tiled scan (planned before it for large batches) off."""
     monkeypatch.setenv("VS_TILE", "1")
+    monkeypatch.setenv("VS_GEMM", "0")
 
 
 def _force(monkeypatch, shape):
