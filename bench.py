@@ -128,6 +128,7 @@ def run_search_workload(args, vs, syn, N):
     idx.prof_enable(False)
     nscan, scan_ms = idx.prof_get("scan")
     nmerge, merge_ms = idx.prof_get("merge")
+    npre, pre_ms = idx.prof_get("prepass")
 
     D = np.empty((nq, k), np.float32)
     I = np.empty((nq, k), np.int32)
@@ -142,7 +143,8 @@ def run_search_workload(args, vs, syn, N):
     roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
             "frac": round(achieved / peak, 4), "traffic": None,
             "kernel": "scan_kernel", "launches": nscan, "avg_ms": round(scan_avg_s * 1e3, 4),
-            "algorithmic_flops_per_launch": flops, "merge_avg_ms": round(merge_ms / max(nmerge, 1), 4)}
+            "algorithmic_flops_per_launch": flops, "merge_avg_ms": round(merge_ms / max(nmerge, 1), 4),
+            "prepass_ms_per_step": round(pre_ms / args.steps, 4) if npre else None}
     if nq <= 64:  # streaming regime: the database bytes bound the kernel
         db_bytes = n * d * (2 if bf16 else 4)
         gbs = db_bytes / scan_avg_s / 1e9

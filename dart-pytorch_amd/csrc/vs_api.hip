@@ -552,7 +552,7 @@ bool plan_gemm(const vs_index *x, int64_t nq, int64_t nrows, int planes, int sto
 // register-resident queries), VS_SCAN_KKW (per-list keep, for tests of the
 // verification path).
 int plan_scan(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t kk_final,
-              int storage, vs::ScanPlan *p, bool safe = false) {
+              int storage, vs::ScanPlan *p, bool safe = false, int64_t max_lists = 0) {
     int64_t kk = kk_final <= 32 ? kk_final : kk_final / 4;
     const int kkw = env_int("VS_SCAN_KKW", 0);
     if (kkw > 0) kk = std::min<int64_t>(kk_final, std::max<int64_t>(4, next_pow2(kkw)));
@@ -565,8 +565,8 @@ int plan_scan(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t 
     p->tm = env_int("VS_SCAN_TM", x->ld <= 128 && storage == 1 ? 1 : 2);
     if (p->tm != 1 && p->tm != 2 && p->tm != 4) p->tm = 2;
     p->kind = 0;
-    if (plan_gemm(x, nq, nrows, planes, storage, kkw > 0 || safe, p)) return VS_OK;
-    if (plan_tile(x, nq, nrows, planes, storage, p)) return VS_OK;
+    if (!max_lists && plan_gemm(x, nq, nrows, planes, storage, kkw > 0 || safe, p)) return VS_OK;
+    if (!max_lists && plan_tile(x, nq, nrows, planes, storage, p)) return VS_OK;
     const int nks = (int)(x->ld / 32);
     const int force_bn = env_int("VS_SCAN_BN", 0);
     const int cands[3] = {64, 32, 16};
@@ -577,7 +577,7 @@ int plan_scan(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t 
         if (!force_bn && bn > 16 && round_up(nq, 16) < bn) continue;
         const bool qreg = env_int("VS_SCAN_QREG", 1) && storage == 1 && planes == 1 &&
                           (nks == 4 || nks == 8) && nks * (bn / 16) <= 16;
-        if (vs::scan_lds_bytes(bn, qreg ? 0 : planes, x->ld, p->cap) <= x->lds_max) {
+        if (vs::scan_lds_bytes(bn, qreg ? 0 : planes, x->ld, p->cap, 4) <= x->lds_max) {
             p->bn = bn;
             p->nks = qreg ? nks : 0;
             break;
@@ -587,13 +587,22 @@ int plan_scan(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t 
         return set_err(VS_ERR_UNSUPPORTED,
                        "d=%lld is too large for the LDS-resident query block of this build",
                        (long long)x->d);
-    p->lds_bytes = vs::scan_lds_bytes(p->bn, p->nks ? 0 : planes, x->ld, p->cap);
+    // eight waves per workgroup when the LDS-resident query block leaves room
+    // for a single workgroup per CU (bf16 rows): twice the loads in flight
+    // (opt-in, VS_SCAN_NW8=1: measured slightly slower than four on configs[2])
+    p->lw = 4;
+    if (storage == 1 && !p->nks && p->tm == 2 && env_int("VS_SCAN_NW8", 0) &&
+        2 * vs::scan_lds_bytes(p->bn, planes, x->ld, p->cap, 4) > x->lds_max &&
+        vs::scan_lds_bytes(p->bn, planes, x->ld, p->cap, 8) <= x->lds_max)
+        p->lw = 8;
+    p->lds_bytes = vs::scan_lds_bytes(p->bn, p->nks ? 0 : planes, x->ld, p->cap, p->lw);
     p->nqblk = (nq + p->bn - 1) / p->bn;
-    const int64_t tile_rows = 64 * p->tm;  // rows per block per round
+    const int64_t tile_rows = 16 * p->lw * p->tm;  // rows per block per round
     const int64_t target = (int64_t)x->num_cu * env_int("VS_SCAN_BLOCKS_PER_CU", 8);
     int64_t nsplit = std::max<int64_t>(1, (target + p->nqblk - 1) / p->nqblk);
     const int64_t min_rows = tile_rows * 8;
     nsplit = std::min<int64_t>(nsplit, std::max<int64_t>(1, (nrows + min_rows - 1) / min_rows));
+    if (max_lists > 0) nsplit = std::min<int64_t>(nsplit, std::max<int64_t>(1, max_lists / p->lw));
     int64_t rps = round_up((nrows + nsplit - 1) / nsplit, tile_rows);
     if (rps <= 0) rps = tile_rows;
     p->rows_per_split = rps;
@@ -654,6 +663,46 @@ __global__ void fill_sentinels_kernel(float *D, int32_t *I, int64_t m, float v) 
     }
 }
 
+// A plan warms up badly when it makes many lists per query over many rows.
+bool needs_seed(const vs_index *x, const vs::ScanPlan &plan) {
+    return plan.kind == 0 && plan.nsplit * plan.lw >= 512 && x->ntotal >= (1 << 18);
+}
+
+// Seeds every query's shared threshold (gthr) from the first S rows: a scan
+// of those rows with the ordinary plan -- itself seeded from the first S / 32
+// rows when that plan would warm up badly too -- and a merge that sets the
+// threshold one code above the kk_final-th smallest accumulator value of the
+// query's lists.  kk_final rows of the full scan lie strictly below it, so
+// the full scan loses nothing; thresholds only ever tighten.  The candidate
+// lists are scratch here (the full scan rewrites them).
+int seed_thresholds(vs_index *x, const vs::PreparedQueries &pq, int64_t S, int64_t kk_final,
+                    size_t min_list_elems) {
+    S = std::min<int64_t>(S, x->ntotal);
+    vs::ScanPlan pp;
+    int rc = plan_scan(x, pq.nq, S, pq.planes, kk_final, x->storage, &pp, false,
+                       env_int("VS_PREPASS_LISTS", 0));
+    if (rc) return rc;
+    if ((rc = scan_fits(pp, pq))) return rc;
+    const int div = std::max(2, env_int("VS_PREPASS_DIV", 32));
+    if (pp.kind == 0 && pp.nsplit * pp.lw >= 512 && S >= (1 << 18)) {
+        rc = seed_thresholds(x, pq, std::max<int64_t>(1 << 16, S / div), kk_final, min_list_elems);
+        if (rc) return rc;
+    }
+    const size_t pn = std::max(min_list_elems, (size_t)pp.nqblk * pp.nsplit * pp.lw * pp.bn * pp.cap);
+    VS_HIP(x->cand_v.ensure(pn * 4), "candidate lists");
+    VS_HIP(x->cand_i.ensure(pn * 4), "candidate lists");
+    ProfScope ps(x, "prepass");
+    VS_HIP(vs::launch_scan_topk(x->xb, x->storage, x->ld, x->xn, S, x->metric, pq, pp,
+                                x->cand_v.as<float>(), x->cand_i.as<int32_t>(),
+                                x->gthr.as<uint32_t>(), nullptr, x->st),
+           "seeding scan");
+    VS_HIP(vs::launch_merge_threshold(pq, pp, x->cand_v.as<float>(), x->cand_i.as<int32_t>(),
+                                      x->gthr.as<uint32_t>(), x->ld, x->st),
+           "seeding threshold");
+    x->prof["prepass_scans"].launches++;
+    return VS_OK;
+}
+
 int search_device(vs_index *x, const void *q_dev, int q_dtype, int64_t nq, int64_t k, float *D,
                   int32_t *I, bool safe = false) {
     if (nq < 0 || k < 0) return set_err(VS_ERR_INVALID, "nq and k must be >= 0");
@@ -695,7 +744,18 @@ int search_device(vs_index *x, const void *q_dev, int q_dtype, int64_t nq, int64
         VS_HIP(x->vf.ensure((size_t)(nq + 1) * 4), "verification list");
         VS_HIP(hipMemsetAsync(x->vf.p, 0, 4, x->st), "verification count");
     }
+    // Small batches over many rows make many short lists, each warming up on
+    // its own (every list must fill kk entries before its threshold means
+    // anything).  Seeding the shared thresholds from samples first (see
+    // seed_thresholds) lets the full scan start tight.
+    if (!safe && needs_seed(x, plan) && env_int("VS_PREPASS", 1)) {
+        rc = seed_thresholds(x, pq,
+                             std::max<int64_t>(1 << 16, x->ntotal / std::max(2, env_int("VS_PREPASS_DIV", 32))),
+                             kk, nlist);
+        if (rc) return rc;
+    }
     note_scan_kind(x, plan);
+    VS_HIP(hipMemsetAsync(x->flags.p, 0, sizeof(uint32_t), x->st), "clearing flags");
     {
         ProfScope ps(x, "scan");
         VS_HIP(vs::launch_scan_topk(x->xb, x->storage, x->ld, x->xn, x->ntotal, x->metric, pq, plan,
@@ -709,9 +769,12 @@ int search_device(vs_index *x, const void *q_dev, int q_dtype, int64_t nq, int64
                                        x->cand_v.as<float>(), x->cand_i.as<int32_t>(),
                                        x->gthr.as<uint32_t>(), x->lbound.as<float>(),
                                        x->vf.as<int32_t>(), x->vf.as<int32_t>() + 1, k, D, I,
-                                       x->st),
+                                       x->ntotal, x->flags.as<uint32_t>(), x->st),
                "merge kernel");
     }
+    uint32_t mflags = 0;
+    VS_HIP(hipMemcpyAsync(&mflags, x->flags.p, sizeof mflags, hipMemcpyDeviceToHost, x->st),
+           "merge flags");
     if (verify) {
         // queries whose shortened lists may have dropped a winner are searched
         // again with full-length lists (exact; rare for unordered data)
@@ -748,6 +811,8 @@ int search_device(vs_index *x, const void *q_dev, int q_dtype, int64_t nq, int64
         }
     }
     VS_HIP(hipStreamSynchronize(x->st), "search");
+    if (mflags & vs::kFlagBadId)
+        return set_err(VS_ERR_HIP, "internal error: a candidate id outside the index reached the merge");
     return VS_OK;
 }
 
@@ -823,9 +888,11 @@ int range_core(vs_index *x, const vs::PreparedQueries &pq, double radius, int se
     VS_HIP(x->rkeep.ensure((size_t)m), "range flags");
     {
         ProfScope ps(x, "refine");
+        VS_HIP(hipMemsetAsync(x->flags.p, 0, sizeof(uint32_t), x->st), "clearing flags");
         VS_HIP(vs::launch_range_refine(x->xb, x->storage, x->ld, x->d, x->metric, pq.qf,
                                        x->rq.as<int32_t>(), x->ri.as<int32_t>(), m, radius,
-                                       x->rs.as<float>(), x->rkeep.as<uint8_t>(), x->st),
+                                       x->rs.as<float>(), x->rkeep.as<uint8_t>(), x->ntotal, pq.nq,
+                                       x->flags.as<uint32_t>(), x->st),
                "range refine");
     }
     std::vector<int32_t> cq(m), ci(m);
@@ -835,7 +902,11 @@ int range_core(vs_index *x, const vs::PreparedQueries &pq, double radius, int se
     VS_HIP(hipMemcpyAsync(ci.data(), x->ri.p, (size_t)m * 4, hipMemcpyDeviceToHost, x->st), "D2H");
     VS_HIP(hipMemcpyAsync(cs.data(), x->rs.p, (size_t)m * 4, hipMemcpyDeviceToHost, x->st), "D2H");
     VS_HIP(hipMemcpyAsync(keep.data(), x->rkeep.p, (size_t)m, hipMemcpyDeviceToHost, x->st), "D2H");
+    uint32_t rflags = 0;
+    VS_HIP(hipMemcpyAsync(&rflags, x->flags.p, sizeof rflags, hipMemcpyDeviceToHost, x->st), "D2H");
     VS_HIP(hipStreamSynchronize(x->st), "range results");
+    if (rflags & vs::kFlagBadId)
+        return set_err(VS_ERR_HIP, "internal error: a range candidate outside the index");
     std::vector<int64_t> idx;
     idx.reserve(m);
     for (int64_t t = 0; t < m; ++t)
@@ -1326,18 +1397,23 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     VS_HIP(hipMemsetAsync(x->km_fb.p, 0, 4, x->st), "fallback count");
     int32_t *fb_count = x->km_fb.as<int32_t>();
     int32_t *fb_list = fb_count + 1;
+    VS_HIP(hipMemsetAsync(x->flags.p, 0, sizeof(uint32_t), x->st), "clearing flags");
     {
         ProfScope ps(x, "pick");
         VS_HIP(vs::launch_kmeans_pick((const float *)x->xb, ld, d, n, x->km_cen.as<float>(), K,
                                       x->cand_v.as<float>(), x->cand_i.as<int32_t>(),
                                       x->gthr.as<uint32_t>(), plan, bound,
                                       pq.qf, x->km_assign.as<int32_t>(), x->km_best.as<double>(),
-                                      fb_count, fb_list, x->st),
+                                      fb_count, fb_list, x->flags.as<uint32_t>(), x->st),
                "assign pick");
     }
     int32_t nfb = 0;
+    uint32_t pflags = 0;
     VS_HIP(hipMemcpyAsync(&nfb, fb_count, 4, hipMemcpyDeviceToHost, x->st), "fallbacks");
+    VS_HIP(hipMemcpyAsync(&pflags, x->flags.p, 4, hipMemcpyDeviceToHost, x->st), "pick flags");
     VS_HIP(hipStreamSynchronize(x->st), "assign");
+    if (pflags & vs::kFlagBadId)
+        return set_err(VS_ERR_HIP, "internal error: a k-means candidate outside the centroids");
     x->prof["kmeans_fallback_points"].launches += nfb;
     if (nfb > 0) {
         ProfScope ps(x, "exhaustive");

@@ -56,7 +56,9 @@ struct PreparedQueries {
 };
 
 // Status flags written by the query-preparation kernel.
-enum : uint32_t { kFlagNonFinite = 1u, kFlagNotBf16 = 2u };
+// kFlagBadId: a kernel met a candidate id outside the rows it indexes (an
+// internal error, reported instead of reading past the rows).
+enum : uint32_t { kFlagNonFinite = 1u, kFlagNotBf16 = 2u, kFlagBadId = 4u };
 
 // order-preserving code of +inf (see enc_order in vs_kernels.hip)
 constexpr uint32_t kGthrInit = 0xFF800000u;
@@ -117,7 +119,15 @@ hipError_t launch_merge_refine(const void *xb, int storage, int64_t ld, int64_t 
                                const PreparedQueries &pq, const ScanPlan &plan,
                                const float *cand_v, const int32_t *cand_i, const uint32_t *gthr,
                                const float *lbound, int32_t *vf_count, int32_t *vf_list,
-                               int64_t k, float *D, int32_t *I, hipStream_t st);
+                               int64_t k, float *D, int32_t *I, int64_t nrows, uint32_t *flags,
+                               hipStream_t st);
+
+// Threshold seeding from a pre-pass scan: every query's shared threshold
+// (gthr) is tightened to one code above the kk_final-th smallest accumulator
+// value its lists hold.
+hipError_t launch_merge_threshold(const PreparedQueries &pq, const ScanPlan &plan,
+                                  const float *cand_v, const int32_t *cand_i, uint32_t *gthr,
+                                  int64_t ld, hipStream_t st);
 
 // Range scan: appends (query, id) of every approximate score within the
 // per-query acceptance bound athr (accumulator space) to out_q / out_i
@@ -133,7 +143,8 @@ hipError_t launch_scan_range(const void *xb, int storage, int64_t ld, const floa
 // = s <= radius (L2) or s >= radius (IP); out_s[j] = fp32(s).
 hipError_t launch_range_refine(const void *xb, int storage, int64_t ld, int64_t d, int metric,
                                const float *qf, const int32_t *cq, const int32_t *ci, int64_t m,
-                               double radius, float *out_s, uint8_t *keep, hipStream_t st);
+                               double radius, float *out_s, uint8_t *keep, int64_t nrows,
+                               int64_t nq, uint32_t *flags, hipStream_t st);
 
 // Per-query acceptance bounds for the range scan (accumulator space).
 hipError_t launch_range_bounds(const PreparedQueries &pq, int64_t d, int metric, double radius,
@@ -164,7 +175,7 @@ hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, 
                               const uint32_t *gthr, const ScanPlan &plan, float bound,
                               const float *qf, int32_t *assign,
                               double *best_sq, int32_t *fallback_count, int32_t *fallback_list,
-                              hipStream_t st);
+                              uint32_t *flags, hipStream_t st);
 
 hipError_t launch_kmeans_count(const int32_t *assign, int64_t n, int32_t *counts, hipStream_t st);
 
@@ -183,7 +194,7 @@ hipError_t launch_gen_normal(void *dst, int out_dtype, int64_t n, int64_t d, uin
 
 // Shape rules shared by the host planner and the kernels.
 int64_t storage_ld(int64_t d, int storage);  // elements per stored row
-size_t scan_lds_bytes(int bn, int planes, int64_t ld, int cap);
+size_t scan_lds_bytes(int bn, int planes, int64_t ld, int cap, int nw);
 // LDS of the tiled scan: qb query blocks of 16, rb row blocks of 16 per wave,
 // K-chunk kc, pa row planes, pb query planes, list capacity cap.
 size_t tile_lds_bytes(int qb, int pb, int nw, int cap, int64_t ld);

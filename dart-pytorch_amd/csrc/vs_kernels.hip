@@ -205,8 +205,8 @@ __device__ void bitonic_sort_block(float *sv, int *si, int n) {
 // global (query, id) candidate list for exact re-testing.
 // ---------------------------------------------------------------------------
 // planes == 0: the queries live in registers and need no LDS copy.
-size_t scan_lds_bytes(int bn, int planes, int64_t ld, int cap) {
-    return (size_t)bn * planes * (size_t)(ld + 8) * 2 + (size_t)4 * bn * 8 + (size_t)4 * cap * 8;
+size_t scan_lds_bytes(int bn, int planes, int64_t ld, int cap, int nw) {
+    return (size_t)bn * planes * (size_t)(ld + 8) * 2 + (size_t)nw * bn * 8 + (size_t)nw * cap * 8;
 }
 
 typedef float f32x8_t __attribute__((ext_vector_type(8)));
@@ -235,8 +235,8 @@ struct AFrag<0> {  // fp32 row: 8 values (32 B) per lane and K-step
 // prefetches its next tile whole while computing the current one.
 // NKS == 0: queries in LDS; rows are consumed in chunks of UK K-steps with the
 // next chunk (or the next tile's first chunk) in flight.
-template <int ST, int PQ, int NQB, int TM, int MODE, int NKS>
-__global__ __launch_bounds__(256) void scan_kernel(ScanKArgs a) {
+template <int ST, int PQ, int NQB, int TM, int MODE, int NKS, int NW>
+__global__ __launch_bounds__(64 * NW) void scan_kernel(ScanKArgs a) {
     extern __shared__ __align__(16) char smem[];
     constexpr int BN = 16 * NQB;
     constexpr bool QREG = NKS > 0;
@@ -256,22 +256,22 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanKArgs a) {
     const int64_t ldp = a.ld + 8;
     uint16_t *qs = (uint16_t *)smem;  // [BN][QPL][ldp]
     int *cnt = (int *)(smem + (size_t)BN * QPL * ldp * 2);
-    float *thr = (float *)(cnt + 4 * BN);
-    float *sv = thr + 4 * BN;
-    int *si = (int *)(sv + 4 * a.cap);
+    float *thr = (float *)(cnt + NW * BN);
+    float *sv = thr + NW * BN;
+    int *si = (int *)(sv + NW * a.cap);
 
     const int64_t q0 = qblk * BN;
     if constexpr (QPL > 0) {
         const int64_t cpr = a.ld / 8;  // 16-byte chunks per plane row
         const int64_t nch = (int64_t)BN * QPL * cpr;
-        for (int64_t c = threadIdx.x; c < nch; c += 256) {
+        for (int64_t c = threadIdx.x; c < nch; c += 64 * NW) {
             const int64_t row = c / cpr, ch = c % cpr;
             const int64_t q = row / QPL, p = row % QPL;
             const uint4 v = *(const uint4 *)(a.qp + ((q0 + q) * 2 + p) * a.ld + ch * 8);
             *(uint4 *)(qs + row * ldp + ch * 8) = v;
         }
     }
-    for (int t = threadIdx.x; t < 4 * BN; t += 256) {
+    for (int t = threadIdx.x; t < NW * BN; t += 64 * NW) {
         cnt[t] = 0;
         thr[t] = q0 + (t % BN) < a.nq ? VS_INF : -VS_INF;
     }
@@ -281,7 +281,7 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanKArgs a) {
     float *thr_w = thr + wave * BN;
     float *sv_w = sv + wave * a.cap;
     int *si_w = si + wave * a.cap;
-    const int64_t list_base = ((qblk * a.nsplit + split) * 4 + wave) * (int64_t)BN * a.cap;
+    const int64_t list_base = ((qblk * a.nsplit + split) * NW + wave) * (int64_t)BN * a.cap;
     float *cv = MODE == 0 ? a.cand_v + list_base : nullptr;
     int32_t *ci = MODE == 0 ? a.cand_i + list_base : nullptr;
 
@@ -333,7 +333,7 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanKArgs a) {
         }
     }
 
-    for (; t0 < r1; t0 += 64 * TM) {
+    for (; t0 < r1; t0 += NW * 16 * TM) {
         uint32_t gt[NQB];
         if constexpr (MODE == 0) {
 #pragma unroll
@@ -347,7 +347,7 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanKArgs a) {
 #pragma unroll
             for (int qb = 0; qb < NQB; ++qb) acc[tm][qb] = xn_cur[tm];
 
-        const int64_t tn = t0 + 64 * TM;
+        const int64_t tn = t0 + NW * 16 * TM;
         for (int ks = 0; ks < nks; ks += UK) {
             // prefetch: the next chunk of this tile, else the next tile's first
             if (ks + UK < nks) {
@@ -537,7 +537,7 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanKArgs a) {
         // value against the query's final kk_final-th value
         if (a.lbound) {
             wave_sync();
-            const int64_t lb = ((qblk * a.nsplit + split) * 4 + wave) * (int64_t)BN;
+            const int64_t lb = ((qblk * a.nsplit + split) * NW + wave) * (int64_t)BN;
             for (int q = lane; q < BN; q += 64) a.lbound[lb + q] = thr_w[q];
         }
     }
@@ -554,8 +554,18 @@ static hipError_t launch_scan_mode(int storage, const PreparedQueries &pq, const
     void (*fn)(ScanKArgs) = nullptr;
     const int nqb = plan.bn / 16;
 #define VS_PICK(ST_, PQ_, NQB_, TM_, NKS_)                                                  \
-    if (storage == ST_ && pq.planes == PQ_ && nqb == NQB_ && plan.tm == TM_ && plan.nks == NKS_) \
-        fn = scan_kernel<ST_, PQ_, NQB_, TM_, MODE, NKS_>;
+    if (storage == ST_ && pq.planes == PQ_ && nqb == NQB_ && plan.tm == TM_ && plan.nks == NKS_ && \
+        plan.lw == 4)                                                                              \
+        fn = scan_kernel<ST_, PQ_, NQB_, TM_, MODE, NKS_, 4>;
+    // eight waves sharing one LDS-resident query block (small batches of long
+    // rows, where the block's LDS allows a single workgroup per CU)
+#define VS_PICK8(PQ_, NQB_, TM_)                                                             \
+    if (storage == 1 && pq.planes == PQ_ && nqb == NQB_ && plan.tm == TM_ && plan.nks == 0 &&   \
+        plan.lw == 8)                                                                             \
+        fn = scan_kernel<1, PQ_, NQB_, TM_, MODE, 0, 8>;
+    VS_PICK8(1, 1, 2) VS_PICK8(1, 2, 2) VS_PICK8(1, 4, 2) VS_PICK8(2, 1, 2) VS_PICK8(2, 2, 2)
+    VS_PICK8(2, 4, 2)
+#undef VS_PICK8
 #define VS_PICK_TM(ST_, PQ_, NQB_, NKS_) \
     VS_PICK(ST_, PQ_, NQB_, 1, NKS_) VS_PICK(ST_, PQ_, NQB_, 2, NKS_) VS_PICK(ST_, PQ_, NQB_, 4, NKS_)
 #define VS_PICK_NQB(ST_, PQ_, NKS_) \
@@ -575,7 +585,7 @@ static hipError_t launch_scan_mode(int storage, const PreparedQueries &pq, const
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(256), lds, st, args);
+    hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(64 * plan.lw), lds, st, args);
     return hipGetLastError();
 }
 
@@ -694,6 +704,9 @@ __device__ double exact_score(const float *qrow, const void *xb, int64_t ld, int
 // ---------------------------------------------------------------------------
 struct MergeKArgs {
     const void *xb;
+    uint32_t *gthr_w;  // threshold seeding: the shared thresholds to tighten
+    int64_t nrows;     // rows of xb: candidate ids must lie in [0, nrows)
+    uint32_t *flags;   // kFlagBadId is or-ed in for an id outside them
     const float *pts;  // k-means pick: the points' stored rows (ld values each)
     int64_t ld, d;
     int metric;
@@ -799,6 +812,14 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
         __syncthreads();
     }
 
+    if constexpr (MODE == 2) {
+        // threshold seeding: kk candidates lie at or below the kk-th merged
+        // value, so its successor code bounds the query's kk-th best strictly
+        if (tid == 0 && bi[kk - 1] != INT_MAX && bv[kk - 1] < VS_INF)
+            atomicMin(&a.gthr_w[qg], enc_order(bv[kk - 1]) + 1u);
+        return;
+    }
+
     // Lists that kept only kl < kk entries dropped rows at or above their own
     // final threshold; the merged result is exact when none of those
     // thresholds is below the kk-th kept value.  Otherwise flag the query.
@@ -829,7 +850,10 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
     for (int t = tid; t < kk; t += 256) {
         const int id = bi[t];
         float key = VS_INF;
-        if (id != INT_MAX) {
+        if (id != INT_MAX && (id < 0 || (int64_t)id >= a.nrows)) {
+            atomicOr(a.flags, kFlagBadId);
+            bi[t] = INT_MAX;
+        } else if (id != INT_MAX) {
             const double ex = exact_score<ST>(qsh, a.xb, a.ld, id, a.d, a.metric);
             key = a.metric == 0 ? (float)ex : -(float)ex;
             if (MODE == 1 && (ex < best_ex || (ex == best_ex && id < best_id))) {
@@ -896,10 +920,13 @@ hipError_t launch_merge_refine(const void *xb, int storage, int64_t ld, int64_t 
                                const PreparedQueries &pq, const ScanPlan &plan,
                                const float *cand_v, const int32_t *cand_i, const uint32_t *gthr,
                                const float *lbound, int32_t *vf_count, int32_t *vf_list,
-                               int64_t k, float *D, int32_t *I, hipStream_t st) {
+                               int64_t k, float *D, int32_t *I, int64_t nrows, uint32_t *flags,
+                               hipStream_t st) {
     if (pq.nq <= 0) return hipSuccess;
     MergeKArgs a{};
     a.xb = xb;
+    a.nrows = nrows;
+    a.flags = flags;
     a.ld = ld;
     a.d = d;
     a.metric = metric;
@@ -934,17 +961,50 @@ hipError_t launch_merge_refine(const void *xb, int storage, int64_t ld, int64_t 
 template <int KK>
 __global__ void kmeans_pick_kernel(MergeKArgs a);
 
+// Threshold seeding from a pre-pass: for every query, the kk_final-th
+// smallest accumulator value over its lists tightens its shared threshold.
+hipError_t launch_merge_threshold(const PreparedQueries &pq, const ScanPlan &plan,
+                                  const float *cand_v, const int32_t *cand_i, uint32_t *gthr,
+                                  int64_t ld, hipStream_t st) {
+    if (pq.nq <= 0) return hipSuccess;
+    MergeKArgs a{};
+    a.ld = ld;
+    a.d = 0;
+    a.qf = pq.qf;
+    a.nq = pq.nq;
+    a.bn = plan.bn;
+    a.lw = plan.lw;
+    a.kk = plan.kk_final;
+    a.kl = plan.kk;
+    a.cap = plan.cap;
+    a.nsplit = plan.nsplit;
+    a.cand_v = cand_v;
+    a.cand_i = cand_i;
+    a.gthr = gthr;
+    a.gthr_w = gthr;
+    const size_t lds = merge_lds(ld);
+    void (*fn)(MergeKArgs) = merge_refine_kernel<1, 2>;
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute((const void *)fn,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(fn, dim3((unsigned)pq.nq), dim3(256), lds, st, a);
+    return hipGetLastError();
+}
+
 hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, const float *cen,
                               int64_t K, const float *cand_v, const int32_t *cand_i,
                               const uint32_t *gthr, const ScanPlan &plan, float bound,
                               const float *qf, int32_t *assign,
                               double *best_sq, int32_t *fallback_count, int32_t *fallback_list,
-                              hipStream_t st) {
-    (void)K;
+                              uint32_t *flags, hipStream_t st) {
     if (n <= 0) return hipSuccess;
     MergeKArgs a{};
     a.xb = cen;
     a.pts = x;
+    a.nrows = K;
+    a.flags = flags;
     a.ld = ld;
     a.d = d;
     a.metric = 0;
@@ -1044,7 +1104,9 @@ __global__ __launch_bounds__(256) void kmeans_pick_kernel(MergeKArgs a) {
     int bid = INT_MAX;
 #pragma unroll
     for (int i = 0; i < KK; ++i) {
-        if (bi[i] != INT_MAX && (i == 0 || bv[i] <= lim)) {
+        if (bi[i] != INT_MAX && (bi[i] < 0 || (int64_t)bi[i] >= a.nrows)) {
+            atomicOr(a.flags, kFlagBadId);
+        } else if (bi[i] != INT_MAX && (i == 0 || bv[i] <= lim)) {
             const float4 *cr = (const float4 *)(cen + (int64_t)bi[i] * a.ld);
             double s = 0.0;
             for (int64_t j4 = 0; j4 < n4; ++j4) {
@@ -1245,10 +1307,17 @@ template <int ST>
 __global__ void range_refine_kernel(const void *xb, int64_t ld, int64_t d, int metric,
                                     const float *__restrict__ qf, const int32_t *__restrict__ cq,
                                     const int32_t *__restrict__ ci, int64_t m, double radius,
-                                    float *__restrict__ out_s, uint8_t *__restrict__ keep) {
+                                    float *__restrict__ out_s, uint8_t *__restrict__ keep,
+                                    int64_t nrows, int64_t nq, uint32_t *flags) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= m) return;
     const int64_t q = cq[t], id = ci[t];
+    if (q < 0 || q >= nq || id < 0 || id >= nrows) {
+        atomicOr(flags, kFlagBadId);
+        out_s[t] = 0.f;
+        keep[t] = 0;
+        return;
+    }
     const float *qrow = qf + q * d;
     double s = 0.0;
     for (int64_t j = 0; j < d; ++j) {
@@ -1268,15 +1337,16 @@ __global__ void range_refine_kernel(const void *xb, int64_t ld, int64_t d, int m
 
 hipError_t launch_range_refine(const void *xb, int storage, int64_t ld, int64_t d, int metric,
                                const float *qf, const int32_t *cq, const int32_t *ci, int64_t m,
-                               double radius, float *out_s, uint8_t *keep, hipStream_t st) {
+                               double radius, float *out_s, uint8_t *keep, int64_t nrows,
+                               int64_t nq, uint32_t *flags, hipStream_t st) {
     if (m <= 0) return hipSuccess;
     const dim3 grid((unsigned)((m + 255) / 256)), block(256);
     if (storage == 1)
         range_refine_kernel<1><<<grid, block, 0, st>>>(xb, ld, d, metric, qf, cq, ci, m, radius,
-                                                       out_s, keep);
+                                                       out_s, keep, nrows, nq, flags);
     else
         range_refine_kernel<0><<<grid, block, 0, st>>>(xb, ld, d, metric, qf, cq, ci, m, radius,
-                                                       out_s, keep);
+                                                       out_s, keep, nrows, nq, flags);
     return hipGetLastError();
 }
 

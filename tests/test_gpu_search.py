@@ -265,3 +265,26 @@ def test_short_lists_are_verified(vs, monkeypatch, k):
     Dr, Ir = oracle.flat_search(xb, xq, k, 0, NT)
     assert_knn_parity(r.distances, r.ids, Dr, Ir, 0)
     assert reruns >= 1
+
+
+@pytest.mark.parametrize("nq,k,metric", [(1, 10, 1), (37, 10, 0), (64, 100, 0), (16, 100, 1)])
+def test_small_batch_prepass(vs, monkeypatch, nq, k, metric):
+    """Small batches over 300,000 rows plan many short lists, so a pre-pass
+    over a sample of the rows seeds every query's shared threshold before
+    the full scan.  Integer data (exact distances): the result equals the
+    oracle's, and the distances equal those of a search without the
+    pre-pass (VS_PREPASS=0)."""
+    xb = syn.int_grid(300_000, 64, 8, 0)
+    xq = syn.int_grid(nq, 64, 8, 1)
+    idx = vs.GpuIndexFlat(64, vs.Metric(metric), storage="auto")
+    idx.add(xb)
+    r1 = idx.search(xq, k)
+    npre, _ = idx.prof_get("prepass_scans")
+    monkeypatch.setenv("VS_PREPASS", "0")
+    r0 = idx.search(xq, k)
+    npre0, _ = idx.prof_get("prepass_scans")
+    idx.close()
+    assert npre >= 1 and npre0 == npre
+    Dr, Ir = oracle.flat_search(xb, xq, k, metric, NT)
+    assert_knn_parity(r1.distances, r1.ids, Dr, Ir, metric, rtol=0.0, atol=0.0, xb=xb, xq=xq)
+    assert np.array_equal(r1.distances, r0.distances)
