@@ -228,7 +228,11 @@ def run_kmeans_workload(args, vs, syn):
     if not args.no_cpu:
         cpu, cores = host_info()
         threads = min(cores, 16)
-        m = min(n, max(threads * 8, int(args.cpu_seconds * 400)))
+        m0 = min(n, threads * 64)
+        t = time.perf_counter()
+        oracle.kmeans_assign(x[:m0], cen0, threads)
+        per_point = (time.perf_counter() - t) / m0
+        m = int(min(n, max(m0, args.cpu_seconds / max(per_point, 1e-9))))
         t = time.perf_counter()
         oracle.kmeans_assign(x[:m], cen0, threads)
         dt = time.perf_counter() - t
@@ -280,7 +284,10 @@ def run_join_workload(args, vs, syn):
     if not args.no_cpu:
         cpu, cores = host_info()
         threads = min(cores, 16)
-        rows = max(threads, int(args.cpu_seconds * 4))
+        t = time.perf_counter()
+        oracle.self_join(x, thr, row_begin=0, row_end=threads, nthreads=threads)
+        per_row = (time.perf_counter() - t) / threads
+        rows = int(max(threads, args.cpu_seconds / max(per_row, 1e-9)))
         t = time.perf_counter()
         ri, rj, _ = oracle.self_join(x, thr, row_begin=0, row_end=rows, nthreads=threads)
         dt = time.perf_counter() - t

@@ -113,6 +113,7 @@ struct vs_index {
     int storage = 0;            // current: 0 fp32, 1 bf16
     int64_t ld = 0;
     int64_t ntotal = 0, cap = 0;
+    uint64_t version = 0;  // bumped whenever the stored rows change
     void *xb = nullptr;
     float *xn = nullptr;
     hipStream_t st = nullptr;
@@ -123,6 +124,11 @@ struct vs_index {
         athr, rq, ri, rs, rkeep, rcount, misc;
     DevBuf km_cen, km_cxn, km_assign, km_best, km_fb, km_keys, km_order, km_tmp, km_counts,
         km_offsets, km_out, km_iota;
+    // k-means: the points prepared as queries, kept while the rows are unchanged
+    DevBuf km_qp, km_qf, km_qnorm;
+    vs::PreparedQueries km_pq;
+    uint32_t km_pflags = 0;
+    uint64_t km_prep_version = ~0ull;
     bool prof_on = false;
     std::map<std::string, ProfEntry> prof;
     std::vector<PendingEvent> pending;
@@ -284,6 +290,7 @@ int widen_storage(vs_index *x) {
     x->cap = nc;
     x->ld = new_ld;
     x->storage = 0;
+    ++x->version;
     return VS_OK;
 }
 
@@ -306,6 +313,7 @@ int add_device_rows(vs_index *x, const void *src, int dtype, int64_t n) {
            "storing rows");
     VS_HIP(hipStreamSynchronize(x->st), "storing rows");
     x->ntotal += n;
+    ++x->version;
     return VS_OK;
 }
 
@@ -632,16 +640,20 @@ int scan_fits(const vs::ScanPlan &plan, const vs::PreparedQueries &pq) {
 }
 
 int prepare_queries(vs_index *x, const void *q_dev, int q_dtype, int64_t stride, int64_t nq,
-                    vs::PreparedQueries *pq, uint32_t *flags_out) {
+                    vs::PreparedQueries *pq, uint32_t *flags_out, DevBuf *qp = nullptr,
+                    DevBuf *qf = nullptr, DevBuf *qnorm = nullptr) {
+    if (!qp) qp = &x->qp;
+    if (!qf) qf = &x->qf;
+    if (!qnorm) qnorm = &x->qnorm;
     pq->nq = nq;
     pq->nq_pad = query_pad(nq);
-    VS_HIP(x->qp.ensure((size_t)pq->nq_pad * 2 * x->ld * 2), "query planes");
-    VS_HIP(x->qf.ensure((size_t)std::max<int64_t>(nq, 1) * x->d * 4), "query copy");
-    VS_HIP(x->qnorm.ensure((size_t)pq->nq_pad * 4), "query norms");
+    VS_HIP(qp->ensure((size_t)pq->nq_pad * 2 * x->ld * 2), "query planes");
+    VS_HIP(qf->ensure((size_t)std::max<int64_t>(nq, 1) * x->d * 4), "query copy");
+    VS_HIP(qnorm->ensure((size_t)pq->nq_pad * 4), "query norms");
     VS_HIP(x->flags.ensure(sizeof(uint32_t)), "flags buffer");
-    pq->qp = x->qp.as<uint16_t>();
-    pq->qf = x->qf.as<float>();
-    pq->qnorm = x->qnorm.as<float>();
+    pq->qp = qp->as<uint16_t>();
+    pq->qf = qf->as<float>();
+    pq->qnorm = qnorm->as<float>();
     VS_HIP(hipMemsetAsync(x->flags.p, 0, sizeof(uint32_t), x->st), "clearing flags");
     VS_HIP(vs::launch_prepare_queries(q_dev, q_dtype, stride, nq, x->d, x->ld, x->metric, *pq,
                                       x->flags.as<uint32_t>(), x->st),
@@ -1029,6 +1041,7 @@ int vs_index_reset(vs_index *x) {
         VS_HIP(hipStreamSynchronize(x->st), "reset");
     }
     x->ntotal = 0;
+    ++x->version;
     return VS_OK;
 }
 
@@ -1083,6 +1096,7 @@ int vs_index_add(vs_index *x, const void *xs, int src_dtype, int64_t n) {
         VS_HIP(hipStreamSynchronize(x->st), "storing rows");
     }
     x->ntotal += n;
+    ++x->version;
     return VS_OK;
 }
 
@@ -1160,6 +1174,7 @@ int vs_index_remove_ids(vs_index *x, const int64_t *ids, int64_t n, int64_t *nre
     x->xb = nxb;
     x->xn = nxn;
     x->ntotal = w;
+    ++x->version;
     if (nremoved) *nremoved = removed;
     return VS_OK;
 }
@@ -1331,11 +1346,17 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     VS_HIP(hipStreamSynchronize(x->st), "centroids");
     if (cf & vs::kFlagNonFinite) return set_err(VS_ERR_NONFINITE, "centroids contain NaN or infinity");
 
-    // points as prepared queries against the centroid "database"
-    vs::PreparedQueries pq;
-    uint32_t pf = 0;
-    int rc = prepare_queries(x, x->xb, 0, ld, n, &pq, &pf);
-    if (rc) return rc;
+    // points as prepared queries against the centroid "database" (kept
+    // across iterations while the stored rows are unchanged)
+    if (x->km_prep_version != x->version) {
+        x->km_prep_version = ~0ull;
+        int rc0 = prepare_queries(x, x->xb, 0, ld, n, &x->km_pq, &x->km_pflags, &x->km_qp,
+                                  &x->km_qf, &x->km_qnorm);
+        if (rc0) return rc0;
+        x->km_prep_version = x->version;
+    }
+    const vs::PreparedQueries pq = x->km_pq;
+    int rc = VS_OK;
     // the distance kernels index the centroid rows with the points' ld
     vs_index cview;
     cview.ld = ld;

@@ -75,7 +75,10 @@ __global__ __launch_bounds__(256) void store_rows_kernel(const TS *__restrict__ 
     }
     if (lane == 0) {
         xn[row] = (float)ss;
-        if (f) atomicOr(flags, f);
+        // one atomic per new bit: rows of the same data set the same bits, and
+        // millions of atomics on one word would serialise
+        if (f && (__hip_atomic_load(flags, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & f) != f)
+            atomicOr(flags, f);
     }
 }
 
@@ -137,7 +140,10 @@ __global__ __launch_bounds__(256) void prep_queries_kernel(const TS *__restrict_
     }
     if (lane == 0) {
         if (valid) qnorm[row] = (float)sqrt(ss);
-        if (f) atomicOr(flags, f);
+        // one atomic per new bit: rows of the same data set the same bits, and
+        // millions of atomics on one word would serialise
+        if (f && (__hip_atomic_load(flags, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & f) != f)
+            atomicOr(flags, f);
     }
 }
 

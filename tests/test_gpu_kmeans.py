@@ -51,3 +51,25 @@ def test_kmeans_train_monotone(vs):
     assert res.centroids.shape == (8, 16) and res.assignments.shape == (400,)
     _, _, reobj = oracle.kmeans_assign(x, res.centroids, 1)
     assert reobj <= res.objective * 1.05 + 1e-6
+
+
+def test_kmeans_prepared_points_follow_adds(vs):
+    """The points prepared for the assign scan are kept across iterations;
+    adding rows (or removing some) must invalidate them: each step still
+    equals the oracle on the index's current rows."""
+    x, _ = syn.gaussian_mixture(5000, 64, 8, 0.1, 3)
+    cen = x[:16].copy()
+    pts = vs.GpuIndexFlat.l2(64, storage="f32")
+    pts.add(x[:3000])
+    a1, _, _, o1 = vs.kmeans_step(pts, cen, 1, syn.rng(4, 0).random(16 * 64))
+    ar1, _, or1 = oracle.kmeans_assign(x[:3000], cen, NT)
+    assert np.array_equal(a1, ar1) and o1 == or1
+    pts.add(x[3000:])
+    a2, _, _, o2 = vs.kmeans_step(pts, cen, 1, syn.rng(4, 1).random(16 * 64))
+    ar2, _, or2 = oracle.kmeans_assign(x, cen, NT)
+    assert np.array_equal(a2, ar2) and o2 == or2
+    pts.remove_ids(list(range(0, 5000, 2)))
+    a3, _, _, o3 = vs.kmeans_step(pts, cen, 1, syn.rng(4, 2).random(16 * 64))
+    ar3, _, or3 = oracle.kmeans_assign(x[1::2], cen, NT)
+    assert np.array_equal(a3, ar3) and o3 == or3
+    pts.close()
