@@ -120,7 +120,7 @@ struct vs_index {
     int num_cu = 256;
     size_t lds_max = 64 * 1024;
     // scratch (grown on demand, reused across calls)
-    DevBuf stage, qp, qf, qnorm, flags, cand_v, cand_i, gthr, lbound, vf, fbq, fbD, fbI, outD, outI,
+    DevBuf stage, qp, qf, qnorm, flags, cand_v, cand_i, lcnt, gthr, lbound, vf, fbq, fbD, fbI, outD, outI,
         athr, rq, ri, rs, rkeep, rcount, misc;
     DevBuf km_cen, km_cxn, km_assign, km_best, km_fb, km_keys, km_order, km_tmp, km_counts,
         km_offsets, km_out, km_iota;
@@ -163,7 +163,8 @@ struct ProfScope {
 // Counts which scan variant a launch used (always on; read back through
 // vs_prof_get with the families "tiled" and "streamed").
 void note_scan_kind(vs_index *x, const vs::ScanPlan &plan) {
-    x->prof[plan.kind == 2 ? "gemm" : plan.kind == 1 ? "tiled" : "streamed"].launches++;
+    x->prof[plan.kind == 3 ? "shared" : plan.kind == 2 ? "gemm" : plan.kind == 1 ? "tiled" : "streamed"]
+        .launches++;
     if (plan.kind == 2) {  // and per GEMM shape: "gemm:1,1,2,4,4,2,32" or "gemmdma:1,2,4,4,2,4"
         char key[64];
         if (plan.g_ns > 0)
@@ -433,6 +434,57 @@ bool plan_tile(const vs_index *x, int64_t nq, int64_t nrows, int planes, int sto
 // mistake in its indexing, waits or barriers has been shown yet.
 constexpr bool kGemmDmaEnabled = false;
 
+// Row-shared scan (top-k only): bf16 rows of 128 or 256 elements, one query
+// plane, large batches.  Every list keeps kk_final entries (one list per
+// query and workgroup).  VS_SHARE: -1 = default rule (rows of 128 elements,
+// batch >= VS_SHARE_MIN_NQ), 0 = off, 1 = also rows of 256 elements.
+// VS_SHARE_ROUNDS: grid size in multiples of the resident workgroups.
+bool plan_share(const vs_index *x, int64_t nq, int64_t nrows, int planes, int storage,
+                vs::ScanPlan *p, int64_t max_split) {
+    const int mode = env_int("VS_SHARE", -1);
+    if (mode == 0 || storage != 1 || planes != 1) return false;
+    if (!(x->ld == 128 || (x->ld == 256 && mode > 0))) return false;
+    if (nq < env_int("VS_SHARE_MIN_NQ", 256)) return false;
+    const int nks = (int)(x->ld / 32), nqb = nks == 4 ? 4 : 2, rt = 4;
+    // a list of the row-shared scan gains up to 16 entries per 16-row block
+    // and query; 256 slots at least keep cuts rare while its threshold is
+    // still loose (the list is sorted only up to its fill)
+    const int kk = p->kk_final;
+    const int cap = (int)std::max<int64_t>(256, next_pow2(kk + 48));
+    const size_t lds = vs::share_lds_bytes(nks, nqb, rt, cap);
+    if (lds > x->lds_max) return false;
+    p->kind = 3;
+    p->kk = kk;
+    p->cap = cap;
+    p->nks = nks;
+    p->bn = 64 * nqb;
+    p->tm = rt;
+    p->lw = 1;
+    p->lds_bytes = lds;
+    p->nqblk = (nq + p->bn - 1) / p->bn;
+    const int64_t tile_rows = 16 * rt;
+    // Splits: the whole grid resident at once (or whole rounds of it), so the
+    // query blocks of a split -- dealt to one XCD back to back -- walk its
+    // rows together through that XCD's L2, and no round is left half empty.
+    const int bpc = std::max(1, vs::share_blocks_per_cu(nks, p->bn, rt, x->ld, lds));
+    const int64_t resident = (int64_t)std::max(1, x->num_cu) * bpc;
+    const int64_t target = resident * std::max(1, env_int("VS_SHARE_ROUNDS", 2));
+    int64_t nsplit = std::max<int64_t>(1, target / p->nqblk);
+    nsplit = std::min<int64_t>(nsplit, std::max<int64_t>(1, nrows / (tile_rows * 8)));
+    if (max_split > 0) nsplit = std::min<int64_t>(nsplit, max_split);
+    int64_t rps = round_up((nrows + nsplit - 1) / nsplit, tile_rows);
+    if (rps <= 0) rps = tile_rows;
+    p->rows_per_split = rps;
+    p->nsplit = std::max<int64_t>(1, (nrows + rps - 1) / rps);
+    if (env_int("VS_DEBUG_PLAN", 0))
+        fprintf(stderr,
+                "[vs plan] share nq=%lld rows=%lld bn=%d nks=%d rt=%d kk=%d cap=%d nqblk=%lld "
+                "nsplit=%lld rows/split=%lld lds=%zu\n",
+                (long long)nq, (long long)nrows, p->bn, nks, rt, p->kk, p->cap, (long long)p->nqblk,
+                (long long)p->nsplit, (long long)p->rows_per_split, p->lds_bytes);
+    return true;
+}
+
 bool plan_gemm(const vs_index *x, int64_t nq, int64_t nrows, int planes, int storage,
                bool kk_forced, vs::ScanPlan *p) {
     // default: large batches of long rows (measured on MI355X: the GEMM-tiled
@@ -560,7 +612,8 @@ bool plan_gemm(const vs_index *x, int64_t nq, int64_t nrows, int planes, int sto
 // register-resident queries), VS_SCAN_KKW (per-list keep, for tests of the
 // verification path).
 int plan_scan(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t kk_final,
-              int storage, vs::ScanPlan *p, bool safe = false, int64_t max_lists = 0) {
+              int storage, vs::ScanPlan *p, bool safe = false, int64_t max_lists = 0,
+              bool range = false) {
     int64_t kk = kk_final <= 32 ? kk_final : kk_final / 4;
     const int kkw = env_int("VS_SCAN_KKW", 0);
     if (kkw > 0) kk = std::min<int64_t>(kk_final, std::max<int64_t>(4, next_pow2(kkw)));
@@ -573,6 +626,8 @@ int plan_scan(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t 
     p->tm = env_int("VS_SCAN_TM", x->ld <= 128 && storage == 1 ? 1 : 2);
     if (p->tm != 1 && p->tm != 2 && p->tm != 4) p->tm = 2;
     p->kind = 0;
+    if (!range && kkw <= 0 && plan_share(x, nq, nrows, planes, storage, p, max_lists))
+        return VS_OK;
     if (!max_lists && plan_gemm(x, nq, nrows, planes, storage, kkw > 0 || safe, p)) return VS_OK;
     if (!max_lists && plan_tile(x, nq, nrows, planes, storage, p)) return VS_OK;
     const int nks = (int)(x->ld / 32);
@@ -687,13 +742,25 @@ bool needs_seed(const vs_index *x, const vs::ScanPlan &plan) {
 // query's lists.  kk_final rows of the full scan lie strictly below it, so
 // the full scan loses nothing; thresholds only ever tighten.  The candidate
 // lists are scratch here (the full scan rewrites them).
+//
+// seed_rank > 0 makes the threshold an estimate instead of a bound: one code
+// above the seed_rank-th smallest value of the sample, which the caller
+// chooses so that the full scan very likely holds kk_final rows below it;
+// the merge then flags the queries for which it does not (guess_thresholds).
 int seed_thresholds(vs_index *x, const vs::PreparedQueries &pq, int64_t S, int64_t kk_final,
-                    size_t min_list_elems) {
+                    size_t min_list_elems, int seed_rank = 0, int64_t max_lists = -1) {
     S = std::min<int64_t>(S, x->ntotal);
     vs::ScanPlan pp;
-    int rc = plan_scan(x, pq.nq, S, pq.planes, kk_final, x->storage, &pp, false,
-                       env_int("VS_PREPASS_LISTS", 0));
+    if (max_lists < 0) max_lists = env_int("VS_PREPASS_LISTS", 0);
+    int rc = plan_scan(x, pq.nq, S, pq.planes, kk_final, x->storage, &pp, false, max_lists);
     if (rc) return rc;
+    // an estimate needs only the values of the sample's seed_rank smallest:
+    // the row-shared scan then keeps each lane's smallest in registers
+    // instead of lists (exact unless one lane met more than m of them; then
+    // the estimate is larger, never smaller)
+    if (pp.kind == 3 && seed_rank > 0 && seed_rank <= 4 * vs::share_topm() &&
+        env_int("VS_GUESS_TOPM", 1))
+        pp.share_topm = vs::share_topm();
     if ((rc = scan_fits(pp, pq))) return rc;
     const int div = std::max(2, env_int("VS_PREPASS_DIV", 32));
     if (pp.kind == 0 && pp.nsplit * pp.lw >= 512 && S >= (1 << 18)) {
@@ -703,16 +770,46 @@ int seed_thresholds(vs_index *x, const vs::PreparedQueries &pq, int64_t S, int64
     const size_t pn = std::max(min_list_elems, (size_t)pp.nqblk * pp.nsplit * pp.lw * pp.bn * pp.cap);
     VS_HIP(x->cand_v.ensure(pn * 4), "candidate lists");
     VS_HIP(x->cand_i.ensure(pn * 4), "candidate lists");
+    const size_t pl = (size_t)pp.nqblk * pp.nsplit * pp.lw * pp.bn;
+    VS_HIP(x->lcnt.ensure((pl + 1) * 4), "list counts");
+    VS_HIP(hipMemsetAsync(x->lcnt.as<int32_t>() + pl, 0, 4, x->st), "list counts");
     ProfScope ps(x, "prepass");
     VS_HIP(vs::launch_scan_topk(x->xb, x->storage, x->ld, x->xn, S, x->metric, pq, pp,
                                 x->cand_v.as<float>(), x->cand_i.as<int32_t>(),
-                                x->gthr.as<uint32_t>(), nullptr, x->st),
+                                x->gthr.as<uint32_t>(), nullptr, x->lcnt.as<int32_t>(), x->st),
            "seeding scan");
     VS_HIP(vs::launch_merge_threshold(pq, pp, x->cand_v.as<float>(), x->cand_i.as<int32_t>(),
-                                      x->gthr.as<uint32_t>(), x->ld, x->st),
+                                      x->gthr.as<uint32_t>(), x->ld, seed_rank,
+                                      x->lcnt.as<int32_t>(), x->st),
            "seeding threshold");
     x->prof["prepass_scans"].launches++;
     return VS_OK;
+}
+
+// Large batches: every list of the full scan warms up on its own share of
+// the rows, and their thresholds stay far above the query's final
+// kk_final-th value for most of the scan.  An estimate taken from a sample
+// is much tighter: with S of the N rows scanned first, the j-th smallest
+// sample value has on average j * N / S rows of the full scan below it, and
+// fewer than kk_final only when kk_final rows would hold j sample rows,
+// about P(Poisson(kk_final * S / N) >= j) for rows in random order.  j is
+// chosen four standard deviations and four rows above that mean (below 1e-5
+// per query for every kk_final this build allows).  Queries whose estimate
+// was too tight are found by the merge and searched again exactly.
+bool needs_guess(const vs_index *x, const vs::ScanPlan &plan, int64_t nq) {
+    return env_int("VS_GUESS", 1) && nq >= env_int("VS_GUESS_MIN_NQ", 256) &&
+           x->ntotal >= (1 << 18) && plan.nsplit * plan.lw * plan.kk >= 4 * plan.kk_final;
+}
+
+int guess_thresholds(vs_index *x, const vs::PreparedQueries &pq, int64_t kk_final,
+                     size_t min_list_elems) {
+    const int64_t div = std::max(2, env_int("VS_GUESS_DIV", 32));
+    const int64_t S = std::min<int64_t>(x->ntotal, std::max<int64_t>(4096, x->ntotal / div));
+    const double lam = (double)kk_final * (double)S / (double)x->ntotal;
+    const int j = (int)std::ceil(lam + 4.0 * std::sqrt(lam) + 4.0);
+    const int64_t kkp = std::max<int64_t>(8, next_pow2(j));
+    x->prof["guess_scans"].launches++;
+    return seed_thresholds(x, pq, S, kkp, min_list_elems, j, env_int("VS_GUESS_LISTS", 8));
 }
 
 int search_device(vs_index *x, const void *q_dev, int q_dtype, int64_t nq, int64_t k, float *D,
@@ -747,20 +844,26 @@ int search_device(vs_index *x, const void *q_dev, int q_dtype, int64_t nq, int64
     const size_t nlist = nlists * plan.cap;
     VS_HIP(x->cand_v.ensure(nlist * 4), "candidate lists");
     VS_HIP(x->cand_i.ensure(nlist * 4), "candidate lists");
+    VS_HIP(x->lcnt.ensure((nlists + 1) * 4), "list counts");
     VS_HIP(x->gthr.ensure((size_t)pq.nq_pad * 4), "shared thresholds");
     VS_HIP(hipMemsetD32Async((hipDeviceptr_t)x->gthr.p, (int)vs::kGthrInit, (size_t)pq.nq_pad, x->st),
            "shared thresholds");
     const bool verify = plan.kk < plan.kk_final;
-    if (verify) {
-        VS_HIP(x->lbound.ensure(nlists * 4), "list bounds");
+    const bool guess = !safe && needs_guess(x, plan, nq);
+    if (verify) VS_HIP(x->lbound.ensure(nlists * 4), "list bounds");
+    if (verify || guess) {
         VS_HIP(x->vf.ensure((size_t)(nq + 1) * 4), "verification list");
         VS_HIP(hipMemsetAsync(x->vf.p, 0, 4, x->st), "verification count");
     }
     // Small batches over many rows make many short lists, each warming up on
     // its own (every list must fill kk entries before its threshold means
     // anything).  Seeding the shared thresholds from samples first (see
-    // seed_thresholds) lets the full scan start tight.
-    if (!safe && needs_seed(x, plan) && env_int("VS_PREPASS", 1)) {
+    // seed_thresholds) lets the full scan start tight; large batches start
+    // from an estimate (guess_thresholds).
+    if (guess) {
+        rc = guess_thresholds(x, pq, kk, nlist);
+        if (rc) return rc;
+    } else if (!safe && needs_seed(x, plan) && env_int("VS_PREPASS", 1)) {
         rc = seed_thresholds(x, pq,
                              std::max<int64_t>(1 << 16, x->ntotal / std::max(2, env_int("VS_PREPASS_DIV", 32))),
                              kk, nlist);
@@ -768,11 +871,13 @@ int search_device(vs_index *x, const void *q_dev, int q_dtype, int64_t nq, int64
     }
     note_scan_kind(x, plan);
     VS_HIP(hipMemsetAsync(x->flags.p, 0, sizeof(uint32_t), x->st), "clearing flags");
+    VS_HIP(hipMemsetAsync(x->lcnt.as<int32_t>() + nlists, 0, 4, x->st), "list counts");
     {
         ProfScope ps(x, "scan");
         VS_HIP(vs::launch_scan_topk(x->xb, x->storage, x->ld, x->xn, x->ntotal, x->metric, pq, plan,
                                     x->cand_v.as<float>(), x->cand_i.as<int32_t>(),
-                                    x->gthr.as<uint32_t>(), x->lbound.as<float>(), x->st),
+                                    x->gthr.as<uint32_t>(), x->lbound.as<float>(),
+                                    x->lcnt.as<int32_t>(), x->st),
                "scan kernel");
     }
     {
@@ -781,15 +886,18 @@ int search_device(vs_index *x, const void *q_dev, int q_dtype, int64_t nq, int64
                                        x->cand_v.as<float>(), x->cand_i.as<int32_t>(),
                                        x->gthr.as<uint32_t>(), x->lbound.as<float>(),
                                        x->vf.as<int32_t>(), x->vf.as<int32_t>() + 1, k, D, I,
-                                       x->ntotal, x->flags.as<uint32_t>(), x->st),
+                                       x->ntotal, x->flags.as<uint32_t>(), guess ? 1 : 0,
+                                       x->lcnt.as<int32_t>(), x->st),
                "merge kernel");
     }
     uint32_t mflags = 0;
     VS_HIP(hipMemcpyAsync(&mflags, x->flags.p, sizeof mflags, hipMemcpyDeviceToHost, x->st),
            "merge flags");
-    if (verify) {
-        // queries whose shortened lists may have dropped a winner are searched
-        // again with full-length lists (exact; rare for unordered data)
+    if (verify || guess) {
+        // queries whose shortened lists may have dropped a winner, or whose
+        // estimated threshold left fewer than kk_final candidates, are
+        // searched again with full-length lists and no estimate (exact; rare
+        // for unordered data)
         int32_t nvf = 0;
         VS_HIP(hipMemcpyAsync(&nvf, x->vf.p, 4, hipMemcpyDeviceToHost, x->st), "verification");
         VS_HIP(hipStreamSynchronize(x->st), "search");
@@ -861,7 +969,7 @@ int range_core(vs_index *x, const vs::PreparedQueries &pq, double radius, int se
                          plan.kind == 2;
     if (!coarse) {
         plan = vs::ScanPlan();
-        rc = plan_scan(x, pq.nq, x->ntotal, pq.planes, 8, x->storage, &plan);
+        rc = plan_scan(x, pq.nq, x->ntotal, pq.planes, 8, x->storage, &plan, false, 0, true);
         if (rc) return rc;
     }
     if ((rc = scan_fits(plan, pq))) return rc;
@@ -1386,7 +1494,7 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
         ProfScope ps(x, "assign");
         VS_HIP(vs::launch_scan_topk(x->km_cen.p, 0, ld, x->km_cxn.as<float>(), K, 0, pq, plan,
                                     x->cand_v.as<float>(), x->cand_i.as<int32_t>(),
-                                    x->gthr.as<uint32_t>(), nullptr, x->st),
+                                    x->gthr.as<uint32_t>(), nullptr, nullptr, x->st),
                "assign scan");
     }
     // error bound of the accumulator (split-bf16 products + fp32 sums)

@@ -65,6 +65,7 @@ struct ScanKArgs {
     int kk_final;        // candidates the merge keeps per query
     int publish_block;   // nl * kk >= kk_final: a block's nl lists of a query bound its kk_final-th value
     float *lbound;       // per list: its own final threshold (verification of kk < kk_final)
+    int32_t *list_cnt;   // per list: its entry count (lists left uncut and unpadded), or null
     float *cand_v;
     int32_t *cand_i;
     uint32_t *gthr;  // per-query threshold shared by every list (order-preserving code)

@@ -402,10 +402,12 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
                 f32x16_t x16;
                 if (FIRST && ks == 0) {
                     if (l2) {
-                        f32x4_t q4[4];
 #pragma unroll
-                        for (int u = 0; u < 4; ++u) q4[u] = *(const f32x4_t *)(Ns + rb * 32 + 8 * u);
-                        x16 = __builtin_bit_cast(f32x16_t, q4);
+                        for (int u = 0; u < 4; ++u) {
+                            const f32x4_t q4 = *(const f32x4_t *)(Ns + rb * 32 + 8 * u);
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) x16[4 * u + e] = q4[e];
+                        }
                     } else {
 #pragma unroll
                         for (int e = 0; e < 16; ++e) x16[e] = 0.f;
@@ -691,10 +693,12 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_dma_kernel(ScanKArgs a) {
                 f32x16_t x16;
                 if (FIRST && ks == 0) {
                     if (l2) {
-                        f32x4_t q4[4];
 #pragma unroll
-                        for (int u = 0; u < 4; ++u) q4[u] = *(const f32x4_t *)(Ns + rb * 32 + 8 * u);
-                        x16 = __builtin_bit_cast(f32x16_t, q4);
+                        for (int u = 0; u < 4; ++u) {
+                            const f32x4_t q4 = *(const f32x4_t *)(Ns + rb * 32 + 8 * u);
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) x16[4 * u + e] = q4[e];
+                        }
                     } else {
 #pragma unroll
                         for (int e = 0; e < 16; ++e) x16[e] = 0.f;

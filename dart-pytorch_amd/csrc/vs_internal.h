@@ -88,7 +88,8 @@ struct ScanPlan {
     int nks = 0;          // >0: queries held in registers for this many K-steps
     int lw = 4;           // candidate lists per (workgroup, query): the workgroup's waves
     int kind = 0;         // 0: streaming scan (vs_kernels.hip); 1: LDS-tiled scan (vs_tile.hip);
-                          // 2: GEMM-tiled scan (vs_gemm.hip)
+                          // 2: GEMM-tiled scan (vs_gemm.hip); 3: row-shared scan (vs_share.hip:
+                          // nks K-steps, bn = 64 * query blocks per wave, tm = 16-row blocks per tile)
     int g_ns = 0;            // GEMM-tiled scan: LDS-DMA stages (0: register-staged kernel)
     int g_flush = 0;         // GEMM-tiled scan: list flush point (0: twice the keep)
     int g_wq = 2, g_qb = 4;  // GEMM-tiled scan: query waves, 32-query blocks per wave
@@ -98,6 +99,8 @@ struct ScanPlan {
     int tile_kc = 64;     // tiled scan: K-chunk per pipeline step (elements)
     int tile_st = 1, tile_pb = 1;  // tiled scan: storage and query planes it was planned for
     int64_t tile_group = 8;        // tiled scan: query blocks per XCD group (grid order)
+    int share_topm = 0;   // row-shared scan: >0 keeps per-lane register top-m values (sample
+                          // estimates; lists get 4 * m values per query and workgroup, ids 0)
     int64_t nqblk = 0;    // query blocks
     int64_t nsplit = 0;   // database splits
     int64_t rows_per_split = 0;
@@ -107,27 +110,35 @@ struct ScanPlan {
 // Top-k scan: per (query block, split, wave) lists of the kk best approximate
 // candidates, written to cand_v / cand_i ([nqblk][nsplit][lw][bn][cap]).
 // gthr [nq_pad] holds each query's shared threshold in an order-preserving
-// uint32 code; it must start at the code of +inf (kGthrInit).
+// uint32 code; it must start at the code of +inf (kGthrInit).  The row-shared
+// scan (kind 3) leaves its lists uncut and writes their entry counts to
+// list_cnt ([nqblk][nsplit][lw][bn], then the largest count, which must start
+// at 0; required for that kind, others ignore it).
 hipError_t launch_scan_topk(const void *xb, int storage, int64_t ld, const float *xn, int64_t n,
                             int metric, const PreparedQueries &pq, const ScanPlan &plan,
                             float *cand_v, int32_t *cand_i, uint32_t *gthr, float *lbound,
-                            hipStream_t st);
+                            int32_t *list_cnt, hipStream_t st);
 
 // Merge the per-wave lists of each query, re-rank the kk survivors with the
 // exact fp64 distance and write the k best (sentinel-filled) to D / I.
+// Queries the merge cannot prove exact are appended to vf_list (count in
+// *vf_count): lists shortened below kk_final (lbound non-null) or, when
+// guess != 0, fewer than kk_final candidates found below an estimated
+// threshold.
 hipError_t launch_merge_refine(const void *xb, int storage, int64_t ld, int64_t d, int metric,
                                const PreparedQueries &pq, const ScanPlan &plan,
                                const float *cand_v, const int32_t *cand_i, const uint32_t *gthr,
                                const float *lbound, int32_t *vf_count, int32_t *vf_list,
                                int64_t k, float *D, int32_t *I, int64_t nrows, uint32_t *flags,
-                               hipStream_t st);
+                               int guess, const int32_t *list_cnt, hipStream_t st);
 
 // Threshold seeding from a pre-pass scan: every query's shared threshold
-// (gthr) is tightened to one code above the kk_final-th smallest accumulator
-// value its lists hold.
+// (gthr) is tightened to one code above the seed_rank-th (0: kk_final-th)
+// smallest accumulator value its lists hold.
 hipError_t launch_merge_threshold(const PreparedQueries &pq, const ScanPlan &plan,
                                   const float *cand_v, const int32_t *cand_i, uint32_t *gthr,
-                                  int64_t ld, hipStream_t st);
+                                  int64_t ld, int seed_rank, const int32_t *list_cnt,
+                                  hipStream_t st);
 
 // Range scan: appends (query, id) of every approximate score within the
 // per-query acceptance bound athr (accumulator space) to out_q / out_i
@@ -247,7 +258,15 @@ constexpr int kSelectCoarse = 2;
 size_t gemm_dma_lds_bytes(int pb, int wr, int wq, int rb, int qb, int ns, int cap);
 size_t gemm_lds_bytes(int st, int pb, int wr, int wq, int rb, int qb, int kc, int cap);
 
+// LDS of the row-shared scan (two row stages plus list bookkeeping).
+size_t share_lds_bytes(int nks, int nqb, int rt, int cap);
+// Row-shared scan workgroups one CU holds at once (0: no such shape).
+int share_blocks_per_cu(int nks, int bn, int rt, int64_t ld, size_t lds);
+// m of the row-shared scan's register top-m variant.
+int share_topm();
+
 struct ScanKArgs;
+hipError_t launch_share_scan(const ScanPlan &plan, const ScanKArgs &args, hipStream_t st);
 template <int MODE>
 hipError_t launch_gemm_scan(int storage, int planes, const ScanPlan &plan, const ScanKArgs &args,
                             hipStream_t st);

@@ -217,22 +217,22 @@ size_t scan_lds_bytes(int bn, int planes, int64_t ld, int cap, int nw) {
 
 typedef float f32x8_t __attribute__((ext_vector_type(8)));
 struct U8x2 {
-    uint4 a, b;
+    u32x4_t a, b;
 };
 
 template <int ST>
 struct AFrag;
 template <>
 struct AFrag<1> {  // bf16 row: 8 values (16 B) per lane and K-step
-    uint4 v;
-    __device__ __forceinline__ void load(const char *p) { v = *(const uint4 *)p; }
+    u32x4_t v;
+    __device__ __forceinline__ void load(const char *p) { v = *(const u32x4_t *)p; }
 };
 template <>
 struct AFrag<0> {  // fp32 row: 8 values (32 B) per lane and K-step
     U8x2 v;
     __device__ __forceinline__ void load(const char *p) {
-        v.a = *(const uint4 *)p;
-        v.b = *(const uint4 *)(p + 16);
+        v.a = *(const u32x4_t *)p;
+        v.b = *(const u32x4_t *)(p + 16);
     }
 };
 
@@ -306,14 +306,14 @@ __global__ __launch_bounds__(64 * NW) void scan_kernel(ScanKArgs a) {
     const char *xbase = (const char *)a.xb + (ST == 1 ? g * 16 : g * 32);
     const uint16_t *qlane = qs + (int64_t)r16 * QPL * ldp + 8 * g;
 
-    uint4 bq[QREG ? NKS : 1][NQB];
+    u32x4_t bq[QREG ? NKS : 1][NQB];
     if constexpr (QREG) {
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
             for (int qb = 0; qb < NQB; ++qb)
                 bq[ks][qb] =
-                    *(const uint4 *)(a.qp + ((q0 + qb * 16 + r16) * 2) * a.ld + ks * 32 + 8 * g);
+                    *(const u32x4_t *)(a.qp + ((q0 + qb * 16 + r16) * 2) * a.ld + ks * 32 + 8 * g);
     }
 
     AFrag<ST> cur[UK][TM], nxt[UK][TM];
@@ -398,9 +398,9 @@ __global__ __launch_bounds__(64 * NW) void scan_kernel(ScanKArgs a) {
                     } else {
                         const uint16_t *qrow =
                             qlane + (int64_t)qb * 16 * QPL * ldp + (int64_t)(ks + u) * 32;
-                        b0 = __builtin_bit_cast(bf16x8_t, *(const uint4 *)qrow);
+                        b0 = __builtin_bit_cast(bf16x8_t, *(const u32x4_t *)qrow);
                         if constexpr (PQ == 2)
-                            b1 = __builtin_bit_cast(bf16x8_t, *(const uint4 *)(qrow + ldp));
+                            b1 = __builtin_bit_cast(bf16x8_t, *(const u32x4_t *)(qrow + ldp));
                     }
 #pragma unroll
                     for (int tm = 0; tm < TM; ++tm) {
@@ -554,6 +554,7 @@ static hipError_t launch_scan_mode(int storage, const PreparedQueries &pq, const
                                    const ScanKArgs &args, hipStream_t st) {
     if (plan.kind == 1) return launch_tile_scan<MODE>(storage, pq.planes, plan, args, st);
     if (plan.kind == 2) return launch_gemm_scan<MODE>(plan.tile_st, plan.tile_pb, plan, args, st);
+    if (plan.kind == 3) return MODE == 0 ? launch_share_scan(plan, args, st) : hipErrorInvalidValue;
     const int64_t total = plan.nqblk * plan.nsplit;
     const int64_t grid = ((total + 7) / 8) * 8;
     const size_t lds = plan.lds_bytes;
@@ -598,8 +599,10 @@ static hipError_t launch_scan_mode(int storage, const PreparedQueries &pq, const
 hipError_t launch_scan_topk(const void *xb, int storage, int64_t ld, const float *xn, int64_t n,
                             int metric, const PreparedQueries &pq, const ScanPlan &plan,
                             float *cand_v, int32_t *cand_i, uint32_t *gthr, float *lbound,
-                            hipStream_t st) {
+                            int32_t *list_cnt, hipStream_t st) {
     ScanKArgs a{};
+    a.list_cnt = plan.kind == 3 ? list_cnt : nullptr;
+    if (plan.kind == 3 && !list_cnt) return hipErrorInvalidValue;
     a.xb = xb;
     a.ld = ld;
     a.xn = xn;
@@ -726,8 +729,13 @@ struct MergeKArgs {
     const uint32_t *gthr;
     int kl;               // entries per list (<= kk)
     const float *lbound;  // per-list own thresholds, or null
+    const int32_t *list_cnt;  // per-list entry counts (kl = list capacity), or null; the
+                              // largest count follows them, at list_cnt[lists in the scan]
+    int64_t nlists_all;       // lists in the scan (index of the largest count)
     int32_t *vf_count;    // queries whose lists may have dropped a winner
     int32_t *vf_list;
+    int guess;            // thresholds were estimated: flag queries left short
+    int seed_rank;        // MODE 2: rank whose value sets the threshold (0: kk)
     int64_t k;
     float *D;
     int32_t *I;
@@ -754,7 +762,9 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
     const int64_t qg = blockIdx.x;
     const int tid = threadIdx.x;
     const int kk = a.kk;
-    const int kl = a.kl;
+    // counted lists: only the longest list's fill (rounded up to whole
+    // 4-entry reads) needs visiting
+    const int kl = a.list_cnt ? max(0, min(a.kl, (a.list_cnt[a.nlists_all] + 3) & ~3)) : a.kl;
     const int64_t qblk = qg / a.bn, q = qg % a.bn;
     const int64_t nlists = a.nsplit * a.lw;
     const int64_t total = nlists * kl;
@@ -780,21 +790,25 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
         if (e < total) {
             const int64_t list = e / kl, j = e % kl;
             const int64_t split = list / a.lw, w = list % a.lw;
-            const int64_t off = (((qblk * a.nsplit + split) * a.lw + w) * a.bn + q) * a.cap + j;
-            const float4 v4 = *(const float4 *)(a.cand_v + off);
-            const int4 i4 = *(const int4 *)(a.cand_i + off);
-            const float vs4[4] = {v4.x, v4.y, v4.z, v4.w};
-            const int is4[4] = {i4.x, i4.y, i4.z, i4.w};
-            const float th = s_thr;
-            const int thi = s_thr_id;
+            const int64_t li = ((qblk * a.nsplit + split) * a.lw + w) * a.bn + q;
+            const int64_t lc = a.list_cnt ? a.list_cnt[li] : kl;  // entries past it are stale
+            if (j < lc) {
+                const int64_t off = li * a.cap + j;
+                const float4 v4 = *(const float4 *)(a.cand_v + off);
+                const int4 i4 = *(const int4 *)(a.cand_i + off);
+                const float vs4[4] = {v4.x, v4.y, v4.z, v4.w};
+                const int is4[4] = {i4.x, i4.y, i4.z, i4.w};
+                const float th = s_thr;
+                const int thi = s_thr_id;
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const float v = vs4[u];
-                const int id = is4[u];
-                if (id >= 0 && v <= tfinal && (v < th || (v == th && id < thi))) {
-                    const int pos = atomicAdd(&s_cnt, 1);
-                    bv[kk + pos] = v;
-                    bi[kk + pos] = id;
+                for (int u = 0; u < 4; ++u) {
+                    const float v = vs4[u];
+                    const int id = is4[u];
+                    if (j + u < lc && id >= 0 && v <= tfinal && (v < th || (v == th && id < thi))) {
+                        const int pos = atomicAdd(&s_cnt, 1);
+                        bv[kk + pos] = v;
+                        bi[kk + pos] = id;
+                    }
                 }
             }
         }
@@ -819,29 +833,37 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
     }
 
     if constexpr (MODE == 2) {
-        // threshold seeding: kk candidates lie at or below the kk-th merged
-        // value, so its successor code bounds the query's kk-th best strictly
-        if (tid == 0 && bi[kk - 1] != INT_MAX && bv[kk - 1] < VS_INF)
-            atomicMin(&a.gthr_w[qg], enc_order(bv[kk - 1]) + 1u);
+        // threshold seeding: r candidates lie at or below the r-th merged
+        // value (r = kk: a bound on the query's kk-th best; r < kk: an
+        // estimate of a larger rank of the full scan), and its successor
+        // code keeps that value itself below the threshold
+        const int r = a.seed_rank > 0 ? a.seed_rank : kk;
+        if (tid == 0 && bi[r - 1] != INT_MAX && bv[r - 1] < VS_INF)
+            atomicMin(&a.gthr_w[qg], enc_order(bv[r - 1]) + 1u);
         return;
     }
 
     // Lists that kept only kl < kk entries dropped rows at or above their own
     // final threshold; the merged result is exact when none of those
-    // thresholds is below the kk-th kept value.  Otherwise flag the query.
-    if (MODE == 0 && a.lbound) {
+    // thresholds is below the kk-th kept value.  An estimated threshold
+    // dropped every row at or above it; the result is exact when kk
+    // candidates were still found below it.  Otherwise flag the query.
+    if (MODE == 0 && (a.lbound || a.guess)) {
         __shared__ float s_lmin[4];
         float lmin = VS_INF;
-        for (int64_t l = tid; l < nlists; l += 256) {
-            const int64_t split = l / a.lw, w = l % a.lw;
-            lmin = fminf(lmin, a.lbound[((qblk * a.nsplit + split) * a.lw + w) * a.bn + q]);
+        if (a.lbound) {
+            for (int64_t l = tid; l < nlists; l += 256) {
+                const int64_t split = l / a.lw, w = l % a.lw;
+                lmin = fminf(lmin, a.lbound[((qblk * a.nsplit + split) * a.lw + w) * a.bn + q]);
+            }
         }
         for (int o = 32; o > 0; o >>= 1) lmin = fminf(lmin, __shfl_xor(lmin, o));
         if ((tid & 63) == 0) s_lmin[tid >> 6] = lmin;
         __syncthreads();
         if (tid == 0) {
             const float m = fminf(fminf(s_lmin[0], s_lmin[1]), fminf(s_lmin[2], s_lmin[3]));
-            if (m < bv[kk - 1]) a.vf_list[atomicAdd(a.vf_count, 1)] = (int32_t)qg;
+            const bool short_list = a.guess && bi[kk - 1] == INT_MAX && a.nrows >= kk;
+            if (m < bv[kk - 1] || short_list) a.vf_list[atomicAdd(a.vf_count, 1)] = (int32_t)qg;
         }
     }
 
@@ -927,9 +949,12 @@ hipError_t launch_merge_refine(const void *xb, int storage, int64_t ld, int64_t 
                                const float *cand_v, const int32_t *cand_i, const uint32_t *gthr,
                                const float *lbound, int32_t *vf_count, int32_t *vf_list,
                                int64_t k, float *D, int32_t *I, int64_t nrows, uint32_t *flags,
-                               hipStream_t st) {
+                               int guess, const int32_t *list_cnt, hipStream_t st) {
     if (pq.nq <= 0) return hipSuccess;
     MergeKArgs a{};
+    a.guess = guess;
+    a.list_cnt = plan.kind == 3 ? list_cnt : nullptr;
+    if (plan.kind == 3 && !list_cnt) return hipErrorInvalidValue;
     a.xb = xb;
     a.nrows = nrows;
     a.flags = flags;
@@ -941,7 +966,11 @@ hipError_t launch_merge_refine(const void *xb, int storage, int64_t ld, int64_t 
     a.bn = plan.bn;
     a.lw = plan.lw;
     a.kk = plan.kk_final;
-    a.kl = plan.kk;
+    a.kl = a.list_cnt ? plan.cap : plan.kk;
+    a.nlists_all = plan.nqblk * plan.nsplit * plan.lw * plan.bn;
+
+    a.nlists_all = plan.nqblk * plan.nsplit * plan.lw * plan.bn;
+
     a.cap = plan.cap;
     a.nsplit = plan.nsplit;
     a.cand_v = cand_v;
@@ -971,9 +1000,14 @@ __global__ void kmeans_pick_kernel(MergeKArgs a);
 // smallest accumulator value over its lists tightens its shared threshold.
 hipError_t launch_merge_threshold(const PreparedQueries &pq, const ScanPlan &plan,
                                   const float *cand_v, const int32_t *cand_i, uint32_t *gthr,
-                                  int64_t ld, hipStream_t st) {
+                                  int64_t ld, int seed_rank, const int32_t *list_cnt,
+                                  hipStream_t st) {
     if (pq.nq <= 0) return hipSuccess;
+    if (seed_rank < 0 || seed_rank > plan.kk_final) return hipErrorInvalidValue;
     MergeKArgs a{};
+    a.seed_rank = seed_rank;
+    a.list_cnt = plan.kind == 3 ? list_cnt : nullptr;
+    if (plan.kind == 3 && !list_cnt) return hipErrorInvalidValue;
     a.ld = ld;
     a.d = 0;
     a.qf = pq.qf;
@@ -981,7 +1015,7 @@ hipError_t launch_merge_threshold(const PreparedQueries &pq, const ScanPlan &pla
     a.bn = plan.bn;
     a.lw = plan.lw;
     a.kk = plan.kk_final;
-    a.kl = plan.kk;
+    a.kl = a.list_cnt ? plan.cap : plan.kk;
     a.cap = plan.cap;
     a.nsplit = plan.nsplit;
     a.cand_v = cand_v;

@@ -1,0 +1,373 @@
+// vs_share.hip -- the row-shared scan of libvs_hip.so: large query batches
+// over short bf16 rows (gfx950).
+//
+// One workgroup of four waves owns a block of 4 x 16*NQB queries and one
+// split of the database rows.  Each wave keeps the B fragments of its own
+// 16*NQB queries in registers for the whole kernel (NKS K-steps of 32 bf16
+// values: rows of ld = 32*NKS elements).  The split's rows are walked in
+// tiles of 16*RT rows; every tile is read from L2 once per workgroup (16-byte
+// loads into registers while the previous tile is multiplied), written to
+// one of two LDS stages, and multiplied by all 64*NQB queries of the block:
+// four times the query reuse per row byte of the streaming scan, whose waves
+// each read their own rows.  One barrier per tile.
+//
+// Operand layout of v_mfma_f32_16x16x32_bf16, as in the streaming scan
+// (lane l, r = l % 16, g = l / 16): A lane holds row r, K elements
+// 8g..8g+7 of the 32-wide K-step; B lane holds query r, the same K
+// elements; D lane holds rows 4g..4g+3 of query r.  The accumulator starts at
+// the row norm xn (L2) or 0 (IP) and the queries are bf16 planes of s*q
+// (s = -2 for L2, -1 for IP), so it is "smaller is better" for both metrics.
+//
+// Epilogue per 16-row block: one min and one compare per query block decide
+// whether any value passes its query's threshold; passing values are
+// appended to the (wave, query) list in global memory.  Every query has one
+// list per workgroup and each list keeps kk_final entries, so a list cut
+// publishes its own kk_final-th value as a bound on the query's shared
+// threshold.  The merge, re-rank and verification are those of the other
+// scans; lists are laid out [nqblk][nsplit][1][4 * 16 * NQB][cap] and end at
+// their counts (list_cnt) instead of being cut to kk_final entries.
+#include "vs_device.h"
+
+namespace vs {
+
+template <int NKS, int NQB, int RT>
+struct ShareShape {
+    static constexpr int NW = 4, NT = 256;
+    static constexpr int LD = 32 * NKS;         // elements per stored row
+    static constexpr int KP = LD + 8;           // LDS row stride (elements)
+    static constexpr int TR = 16 * RT;          // rows per tile
+    static constexpr int BNW = 16 * NQB;        // queries per wave
+    static constexpr int BN = NW * BNW;         // queries per block
+    static constexpr int CPR = LD * 2 / 16;     // 16-byte chunks per row
+    static constexpr int LOADS = TR * CPR / NT; // 16-byte loads per thread and tile
+    static constexpr size_t STAGE_BYTES = (size_t)TR * KP * 2 + (size_t)TR * 4;
+    static_assert(TR * CPR % NT == 0, "whole loads per thread");
+    static_assert(TR / 4 <= NT, "one thread per 4 row norms");
+    static_assert(TR <= kRowSlack, "the last tile reads at most kRowSlack rows past the end");
+    static_assert(BN <= 256, "query blocks fit the query padding");
+};
+
+size_t share_lds_bytes(int nks, int nqb, int rt, int cap) {
+    const size_t kp = (size_t)32 * nks + 8, tr = (size_t)16 * rt;
+    const size_t stage = tr * kp * 2 + tr * 4;
+    return 2 * stage + (size_t)4 * 16 * nqb * 8 + (size_t)4 * cap * 8;
+}
+
+// MODE 0: candidate lists as described above.  MODE 2 (threshold estimates
+// from a sample of the rows): no lists are kept during the scan; each lane
+// keeps the TOPM smallest values it met per query block, sorted in
+// registers, and writes them out at the end (4 * TOPM values per query and
+// workgroup, ids 0).  The r-th smallest value of their union is the query's
+// r-th smallest over the rows whenever no lane met more than TOPM of those r,
+// and larger otherwise, never smaller.
+constexpr int kShareTopM = 8;
+
+template <int NKS, int NQB, int RT, int MODE>
+__global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
+    using S = ShareShape<NKS, NQB, RT>;
+    constexpr int TOPM = kShareTopM;
+    constexpr int TR = S::TR, KP = S::KP, BNW = S::BNW;
+    extern __shared__ __align__(16) char smem[];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r16 = lane & 15, g = lane >> 4;
+
+    int64_t split, qblk;
+    if (!map_block(a.nqblk, a.nsplit, &split, &qblk)) return;
+    const int64_t r0 = split * a.rows_per_split;
+    const int64_t r1 = min(a.n, r0 + a.rows_per_split);
+    if (r0 >= r1) return;
+
+    // LDS: two stages [TR][KP] bf16 + [TR] row norms, then the lists'
+    // counters and thresholds [BN] and the per-wave sort buffers [4][cap]
+    int *cnt = (int *)(smem + 2 * S::STAGE_BYTES);
+    float *thr = (float *)(cnt + S::BN);
+    float *sv = thr + S::BN;
+    int *si = (int *)(sv + S::NW * a.cap);
+    const int64_t q0 = qblk * S::BN;
+    for (int t = tid; t < S::BN; t += S::NT) {
+        cnt[t] = 0;
+        thr[t] = q0 + t < a.nq ? VS_INF : -VS_INF;
+    }
+    const int qw = wave * BNW;  // the wave's first query in the block
+    int *cnt_w = cnt + qw;
+    float *thr_w = thr + qw;
+    float *sv_w = sv + wave * a.cap;
+    int *si_w = si + wave * a.cap;
+    const int64_t list_base = (qblk * a.nsplit + split) * (int64_t)S::BN * a.cap;
+    float *cv = a.cand_v + list_base;
+    int32_t *ci = a.cand_i + list_base;
+    const bool l2 = a.metric == 0;
+
+    // the wave's queries, plane 0, for the whole kernel
+    u32x4_t bq[NKS][NQB];
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb)
+            bq[ks][qb] = *(const u32x4_t *)(a.qp + ((q0 + qw + qb * 16 + r16) * 2) * a.ld + ks * 32 +
+                                          8 * g);
+
+    // global -> register staging of one tile of rows (and its row norms)
+    const int64_t row_bytes = (int64_t)S::LD * 2;
+    u32x4_t ra[S::LOADS];
+    f32x4_t rn = {0.f, 0.f, 0.f, 0.f};
+    auto gload = [&](int64_t t) __attribute__((always_inline)) {
+        const char *base = (const char *)a.xb + t * row_bytes;
+#pragma unroll
+        for (int j = 0; j < S::LOADS; ++j) {
+            const int i = tid + j * S::NT, row = i / S::CPR, c = i % S::CPR;
+            ra[j] = *(const u32x4_t *)(base + row * row_bytes + c * 16);
+        }
+        if (l2 && tid < TR / 4) rn = *(const f32x4_t *)(a.xn + t + 4 * tid);
+    };
+    auto lstore = [&](char *stage) __attribute__((always_inline)) {
+        uint16_t *As = (uint16_t *)stage;
+#pragma unroll
+        for (int j = 0; j < S::LOADS; ++j) {
+            const int i = tid + j * S::NT, row = i / S::CPR, c = i % S::CPR;
+            *(u32x4_t *)(As + row * KP + c * 8) = ra[j];
+        }
+        if (l2 && tid < TR / 4) *(f32x4_t *)((float *)(As + TR * KP) + 4 * tid) = rn;
+    };
+
+    gload(r0);
+    lstore(smem);
+    __syncthreads();
+
+    float thr_r[NQB];
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) thr_r[qb] = thr_w[qb * 16 + r16];
+
+    // the shared thresholds are read at the start of a tile and applied at
+    // its end, when the read has long completed
+    uint32_t gt[NQB];
+    auto gthr_load = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb)
+            gt[qb] = __hip_atomic_load(&a.gthr[q0 + qw + qb * 16 + r16], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+    };
+    gthr_load();
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) thr_r[qb] = fminf(thr_r[qb], dec_order(gt[qb]));
+
+    float top[MODE == 2 ? NQB : 1][TOPM];
+#pragma unroll
+    for (int qb = 0; qb < (MODE == 2 ? NQB : 1); ++qb)
+#pragma unroll
+        for (int m = 0; m < TOPM; ++m) top[qb][m] = VS_INF;
+
+    const f32x4_t zero4 = {0.f, 0.f, 0.f, 0.f};
+    int par = 0;
+    for (int64_t t0 = r0; t0 < r1; t0 += TR) {
+        const int64_t tn = t0 + TR;
+        const bool more = tn < r1;
+        gthr_load();
+        if (more) gload(tn);
+        const uint16_t *As = (const uint16_t *)(smem + par * S::STAGE_BYTES);
+        const float *Ns = (const float *)(As + TR * KP);
+        const uint16_t *al = As + r16 * KP + 8 * g;
+
+#pragma unroll
+        for (int rb = 0; rb < RT; ++rb) {
+            f32x4_t acc[NQB];
+            const f32x4_t init = l2 ? *(const f32x4_t *)(Ns + rb * 16 + 4 * g) : zero4;
+#pragma unroll
+            for (int qb = 0; qb < NQB; ++qb) acc[qb] = init;
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) {
+                const bf16x8_t av =
+                    __builtin_bit_cast(bf16x8_t, *(const u32x4_t *)(al + rb * 16 * KP + ks * 32));
+#pragma unroll
+                for (int qb = 0; qb < NQB; ++qb)
+                    acc[qb] = mfma_bf16(av, __builtin_bit_cast(bf16x8_t, bq[ks][qb]), acc[qb]);
+            }
+            const int64_t rbase = t0 + rb * 16 + 4 * g;  // the lane's first row
+            if (t0 + rb * 16 + 16 > r1) {  // rows past the split end never qualify
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (rbase + i >= r1) {
+#pragma unroll
+                        for (int qb = 0; qb < NQB; ++qb) acc[qb][i] = VS_INF;
+                    }
+            }
+
+            if constexpr (MODE == 2) {
+                // sorted insertion of each value below the lane's TOPM-th
+#pragma unroll
+                for (int qb = 0; qb < NQB; ++qb) {
+                    const float m4 =
+                        fminf(fminf(acc[qb][0], acc[qb][1]), fminf(acc[qb][2], acc[qb][3]));
+                    if (!__ballot(m4 < top[qb][TOPM - 1])) continue;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        float v = acc[qb][i];
+                        if (v < top[qb][TOPM - 1]) {
+#pragma unroll
+                            for (int m = 0; m < TOPM; ++m) {
+                                const float lo = fminf(top[qb][m], v);
+                                v = fmaxf(top[qb][m], v);
+                                top[qb][m] = lo;
+                            }
+                        }
+                    }
+                }
+                continue;
+            }
+
+            // ---- epilogue of the 16-row block ----
+            bool pass = false;
+#pragma unroll
+            for (int qb = 0; qb < NQB; ++qb) {
+                const float m = fminf(fminf(acc[qb][0], acc[qb][1]), fminf(acc[qb][2], acc[qb][3]));
+                pass |= m < thr_r[qb];
+            }
+            if (!__ballot(pass)) continue;
+            // make room: a query gains at most 16 entries per row block
+            {
+                bool need = false;
+                if (g == 0) {
+#pragma unroll
+                    for (int qb = 0; qb < NQB; ++qb) need |= cnt_w[qb * 16 + r16] > a.cap - 16;
+                }
+                if (__ballot(need)) {
+                    for (int q = 0; q < BNW; ++q) {
+                        if (cnt_w[q] > a.cap - 16)
+                            flush_list(cv + (int64_t)(qw + q) * a.cap, ci + (int64_t)(qw + q) * a.cap,
+                                       &cnt_w[q], &thr_w[q], &thr_w[q], S::BN, 1,
+                                       &a.gthr[q0 + qw + q], sv_w, si_w, a.cap, a.kk, a.kk_final, 0,
+                                       lane);
+                    }
+#pragma unroll
+                    for (int qb = 0; qb < NQB; ++qb)
+                        thr_r[qb] = fminf(thr_r[qb], thr_w[qb * 16 + r16]);
+                }
+            }
+#pragma unroll
+            for (int qb = 0; qb < NQB; ++qb) {
+                int c = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) c += acc[qb][i] < thr_r[qb] ? 1 : 0;
+                if (!__ballot(c > 0)) continue;
+                if (c > 0) {
+                    const int q = qw + qb * 16 + r16;
+                    int pos = atomicAdd(&cnt_w[qb * 16 + r16], c);
+                    float *cvq = cv + (int64_t)q * a.cap;
+                    int32_t *ciq = ci + (int64_t)q * a.cap;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        if (acc[qb][i] < thr_r[qb]) {
+                            cvq[pos] = acc[qb][i];
+                            ciq[pos] = (int32_t)(rbase + i);
+                            ++pos;
+                        }
+                    }
+                }
+            }
+            lds_wave_sync();
+        }
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) thr_r[qb] = fminf(thr_r[qb], dec_order(gt[qb]));
+        // the other stage was last read before the previous barrier
+        if (more) lstore(smem + (par ^ 1) * S::STAGE_BYTES);
+        __syncthreads();
+        par ^= 1;
+    }
+
+    if constexpr (MODE == 2) {
+        // lane (r16, g) writes its TOPM values of query qw + 16 qb + r16 to
+        // slots [g * TOPM, (g + 1) * TOPM) of that query's list
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) {
+            const int q = qw + qb * 16 + r16;
+            float *cvq = cv + (int64_t)q * a.cap + g * TOPM;
+            int32_t *ciq = ci + (int64_t)q * a.cap + g * TOPM;
+#pragma unroll
+            for (int m = 0; m < TOPM; ++m) {
+                cvq[m] = top[qb][m];
+                ciq[m] = 0;
+            }
+        }
+        int32_t *lc = a.list_cnt + (qblk * a.nsplit + split) * (int64_t)S::BN + qw;
+        for (int q = lane; q < BNW; q += 64) lc[q] = 4 * TOPM;
+        if (lane == 0) atomicMax(a.list_cnt + a.nqblk * a.nsplit * S::BN, 4 * TOPM);
+        return;
+    }
+    // final: the lists' entry counts for the merge (which filters by the
+    // final shared threshold and keeps the kk_final best itself)
+    wave_sync();
+    if (a.list_cnt) {
+        // counts, and the largest one (after all lists, for the merge)
+        int32_t *lc = a.list_cnt + (qblk * a.nsplit + split) * (int64_t)S::BN + qw;
+        int mx = 0;
+        for (int q = lane; q < BNW; q += 64) {
+            lc[q] = cnt_w[q];
+            mx = max(mx, cnt_w[q]);
+        }
+        for (int o = 32; o > 0; o >>= 1) mx = max(mx, __shfl_xor(mx, o));
+        if (lane == 0) atomicMax(a.list_cnt + a.nqblk * a.nsplit * S::BN, mx);
+        return;
+    }
+    // or: every list holds its kk best in slots [0, kk), padded
+    for (int q = 0; q < BNW; ++q) {
+        const int c = cnt_w[q];
+        float *cvq = cv + (int64_t)(qw + q) * a.cap;
+        int32_t *ciq = ci + (int64_t)(qw + q) * a.cap;
+        if (c > a.kk) {
+            flush_list(cvq, ciq, &cnt_w[q], &thr_w[q], &thr_w[q], S::BN, 1, &a.gthr[q0 + qw + q],
+                       sv_w, si_w, a.cap, a.kk, a.kk_final, 0, lane);
+        } else {
+            for (int j = c + lane; j < a.kk; j += 64) {
+                cvq[j] = VS_INF;
+                ciq[j] = -1;
+            }
+        }
+    }
+}
+
+// The built shapes: X(K-steps, 16-query blocks per wave, 16-row blocks per tile).
+#define VS_SHARE_SHAPES(X) X(4, 4, 4) X(8, 2, 4)
+
+static void (*share_kernel(int nks, int bn, int rt, int64_t ld, int topm))(ScanKArgs) {
+#define VS_SHARE_PICK(NKS_, NQB_, RT_)                                                      \
+    if (nks == NKS_ && bn == 64 * NQB_ && rt == RT_ && ld == 32 * NKS_)                       \
+        return topm ? share_scan_kernel<NKS_, NQB_, RT_, 2> : share_scan_kernel<NKS_, NQB_, RT_, 0>;
+    VS_SHARE_SHAPES(VS_SHARE_PICK)
+#undef VS_SHARE_PICK
+    return nullptr;
+}
+
+int share_topm() { return kShareTopM; }
+
+// Workgroups of the shape that one CU holds at once (registers and LDS).
+int share_blocks_per_cu(int nks, int bn, int rt, int64_t ld, size_t lds) {
+    void (*fn)(ScanKArgs) = share_kernel(nks, bn, rt, ld, 0);
+    if (!fn) return 0;
+    if (lds > 64 * 1024 && hipFuncSetAttribute((const void *)fn,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               (int)lds) != hipSuccess)
+        return 0;
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, 256, lds) != hipSuccess) return 0;
+    return nb;
+}
+
+hipError_t launch_share_scan(const ScanPlan &plan, const ScanKArgs &args, hipStream_t st) {
+    if (plan.kk != plan.kk_final || plan.cap < plan.kk + 16 || plan.lw != 1 || !args.list_cnt)
+        return hipErrorInvalidValue;
+    if (plan.share_topm && (plan.share_topm != kShareTopM || plan.cap < 4 * kShareTopM))
+        return hipErrorInvalidValue;
+    const int64_t total = plan.nqblk * plan.nsplit;
+    const int64_t grid = ((total + 7) / 8) * 8;
+    void (*fn)(ScanKArgs) = share_kernel(plan.nks, plan.bn, plan.tm, args.ld, plan.share_topm);
+    if (!fn) return hipErrorInvalidValue;
+    const size_t lds = plan.lds_bytes;
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute((const void *)fn,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(256), lds, st, args);
+    return hipGetLastError();
+}
+
+}  // namespace vs

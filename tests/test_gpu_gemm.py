@@ -40,8 +40,10 @@ def _key(shape):
 
 @pytest.fixture(autouse=True)
 def _gemm(monkeypatch):
-    """The GEMM-tiled scan is switched on for every test here."""
+    """The GEMM-tiled scan is switched on for every test here (the row-shared
+    scan, planned before it, off)."""
     monkeypatch.setenv("VS_GEMM", "1")
+    monkeypatch.setenv("VS_SHARE", "0")
     monkeypatch.setenv("VS_GEMM_MIN_NQ", "256")
 
 

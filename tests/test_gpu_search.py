@@ -288,3 +288,56 @@ def test_small_batch_prepass(vs, monkeypatch, nq, k, metric):
     Dr, Ir = oracle.flat_search(xb, xq, k, metric, NT)
     assert_knn_parity(r1.distances, r1.ids, Dr, Ir, metric, rtol=0.0, atol=0.0, xb=xb, xq=xq)
     assert np.array_equal(r1.distances, r0.distances)
+
+
+@pytest.mark.parametrize("nq,k,metric", [(512, 100, 0), (300, 10, 1), (1024, 1, 0)])
+def test_large_batch_estimated_threshold(vs, monkeypatch, nq, k, metric):
+    """Large batches over 2^18+ rows start every query's threshold from an
+    estimate taken on a sample of the rows (a rank of the sample chosen so
+    that kk_final rows of the full scan very likely lie below it).  Integer
+    data: the result equals the oracle's and a search without the estimate
+    (VS_GUESS=0), and no query needed the exact re-search."""
+    xb = syn.int_grid(300_000, 32, 11, 0)
+    xq = syn.int_grid(nq, 32, 11, 1)
+    idx = vs.GpuIndexFlat(32, vs.Metric(metric), storage="auto")
+    idx.add(xb)
+    idx.prof_reset()
+    r1 = idx.search(xq, k)
+    ng, _ = idx.prof_get("guess_scans")
+    nfb, _ = idx.prof_get("fallback")
+    monkeypatch.setenv("VS_GUESS", "0")
+    r0 = idx.search(xq, k)
+    ng0, _ = idx.prof_get("guess_scans")
+    idx.close()
+    assert ng == 1 and ng0 == 1 and nfb == 0
+    sub = np.arange(0, nq, 7)
+    Dr, Ir = oracle.flat_search(xb, xq[sub], k, metric, NT)
+    assert_knn_parity(r1.distances[sub], r1.ids[sub], Dr, Ir, metric, rtol=0.0, atol=0.0,
+                      xb=xb, xq=xq[sub])
+    assert np.array_equal(r1.distances, r0.distances)
+
+
+def test_estimated_threshold_too_tight_falls_back(vs):
+    """A sample that is not representative: the first 1/16 of the rows holds
+    64 near copies of every query, the rest lies far away.  The estimate
+    (the 24th sample value at k = 100) then leaves only about 64 rows of the
+    full scan below it, fewer than the 128 the merge needs, so every query
+    is searched again exactly -- and the result still equals the oracle's."""
+    n, d, nq, k = 1 << 18, 16, 256, 100
+    g = syn.rng(5, 3)
+    xq = g.integers(0, 64, size=(nq, d)).astype(np.float32)
+    xb = g.integers(128, 256, size=(n, d)).astype(np.float32)
+    near = n // 16
+    xb[:near] = xq[np.arange(near) % nq] + g.integers(0, 3, size=(near, d)).astype(np.float32)
+    idx = vs.GpuIndexFlat(d, vs.Metric(0), storage="auto")
+    idx.add(xb)
+    idx.prof_reset()
+    r = idx.search(xq, k)
+    ng, _ = idx.prof_get("guess_scans")
+    nfb, _ = idx.prof_get("fallback")
+    idx.close()
+    assert ng == 1 and nfb == nq
+    sub = np.arange(0, nq, 5)
+    Dr, Ir = oracle.flat_search(xb, xq[sub], k, 0, NT)
+    assert_knn_parity(r.distances[sub], r.ids[sub], Dr, Ir, 0, rtol=0.0, atol=0.0,
+                      xb=xb, xq=xq[sub])

@@ -1,0 +1,90 @@
+"""Parity of the row-shared scan (large query batches over bf16 rows of 128
+or 256 elements; each workgroup stages its row tiles in LDS once for four
+waves of register-resident queries) against the CPU oracle (restating
+IndexFlat.search, index_flat.dart:62-97).
+
+Row counts end inside a row tile and inside a split, query counts inside a
+query block, d is ragged below the stored row length, both metrics, k from
+1 to 400 and k above the row count.  Each test checks, through the always-on
+"shared" launch counter, that the row-shared kernel really ran."""
+import numpy as np
+import pytest
+
+import oracle
+from _parity import assert_knn_parity
+from vector_store import synthetic as syn
+
+pytestmark = pytest.mark.gpu
+NT = oracle.default_threads()
+
+
+@pytest.fixture(autouse=True)
+def _share(monkeypatch):
+    """The row-shared scan is on for both row lengths in every test here."""
+    monkeypatch.setenv("VS_SHARE", "1")
+
+
+def _search(vs, xb, xq, k, metric, storage="auto", expect_shared=True):
+    idx = vs.GpuIndexFlat(xb.shape[1], vs.Metric(metric), storage=storage)
+    idx.add(xb)
+    r = idx.search(xq, k)
+    n, _ = idx.prof_get("shared")
+    idx.close()
+    if expect_shared:
+        assert n >= 1, "the row-shared scan did not run"
+    return r.distances, r.ids
+
+
+@pytest.mark.parametrize("n,d,nq,k,metric", [
+    (5000, 128, 300, 10, 0),
+    (4097, 100, 257, 100, 1),
+    (300, 16, 512, 1, 0),
+    (50, 64, 256, 100, 0),        # k > n: sentinels
+    (20011, 128, 1000, 400, 1),  # kk_final 512
+    (3001, 200, 300, 10, 0),     # rows of 256 elements
+    (9000, 256, 600, 100, 1),
+])
+def test_integer_rows_exact(vs, n, d, nq, k, metric):
+    """Integer rows 0..255 are bf16-exact, so every accumulator is an exact
+    integer: the result is bit-identical to the oracle's (ties aside)."""
+    xb = syn.int_grid(n, d, 3, 0)
+    xq = syn.int_grid(nq, d, 3, 1)
+    D, I = _search(vs, xb, xq, k, metric)
+    Dr, Ir = oracle.flat_search(xb, xq, k, metric, NT)
+    assert_knn_parity(D, I, Dr, Ir, metric, rtol=0.0, atol=0.0, xb=xb, xq=xq)
+
+
+@pytest.mark.parametrize("metric", [0, 1])
+def test_bf16_unit_vectors(vs, metric):
+    """bf16 storage of unit vectors with bf16 queries (one query plane); the
+    oracle sees the stored bf16 values upcast to fp32."""
+    xb16 = syn.to_bf16_bits(syn.normal_unit(30_000, 128, 21, 0))
+    xq16 = syn.to_bf16_bits(syn.normal_unit(700, 128, 21, 1))
+    D, I = _search(vs, xb16, xq16, 10, metric, storage="bf16")
+    Dr, Ir = oracle.flat_search(syn.bf16_bits_to_f32(xb16), syn.bf16_bits_to_f32(xq16), 10,
+                                metric, NT)
+    assert_knn_parity(D, I, Dr, Ir, metric, rtol=1e-5)
+
+
+def test_matches_streaming_scan_large(vs, monkeypatch):
+    """configs[1] shape on a 300k-row slice (estimated thresholds active):
+    the row-shared scan returns the same distances as the streaming scan,
+    and the oracle's on a query sample."""
+    xb = syn.int_grid(300_000, 128, 4, 0)
+    xq = syn.int_grid(1024, 128, 4, 1)
+    D1, I1 = _search(vs, xb, xq, 100, 0)
+    monkeypatch.setenv("VS_SHARE", "0")
+    D0, I0 = _search(vs, xb, xq, 100, 0, expect_shared=False)
+    assert np.array_equal(D1, D0)
+    sub = np.arange(0, 1024, 31)
+    Dr, Ir = oracle.flat_search(xb, xq[sub], 100, 0, NT)
+    assert_knn_parity(D1[sub], I1[sub], Dr, Ir, 0, rtol=0.0, atol=0.0, xb=xb, xq=xq[sub])
+
+
+def test_small_batch_not_shared(vs):
+    """Below the batch threshold the streaming scan runs instead."""
+    xb = syn.int_grid(2000, 128, 5, 0)
+    xq = syn.int_grid(100, 128, 5, 1)
+    D, I = _search(vs, xb, xq, 10, 0, expect_shared=False)
+    Dr, Ir = oracle.flat_search(xb, xq, 10, 0, NT)
+    assert_knn_parity(D, I, Dr, Ir, 0, rtol=0.0, atol=0.0, xb=xb, xq=xq)

@@ -40,6 +40,7 @@ def _tiled(monkeypatch):
     the GEMM-tiled scan (planned before it for large batches) off."""
     monkeypatch.setenv("VS_TILE", "1")
     monkeypatch.setenv("VS_GEMM", "0")
+    monkeypatch.setenv("VS_SHARE", "0")
 
 
 def _force(monkeypatch, shape):
