@@ -39,7 +39,7 @@ PEAK = {"bf16_mfma_tflops": 2500.0, "fp32_mfma_tflops": 157.3, "hbm_gbs": 8000.0
 # (workload, n, nq, k).  The command and readings are in the named profile;
 # configurations without a measurement report traffic null.
 MEASURED_TRAFFIC = {
-    ("c2", 1_000_000, 10_000, 100): (9.72e9, "profiles/scan_c2_1Mx128_k100.md"),
+    ("c2", 1_000_000, 10_000, 100): (1.11e9, "profiles/scan_c2_1Mx128_k100.md"),
     ("c3", 20_000_000, 1, 10): (30.88e9, "profiles/scan_c3_20Mx768_b1_b64.md"),
 }
 
@@ -166,7 +166,8 @@ def run_search_workload(args, vs, syn, N):
     roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
             "frac": round(achieved / peak, 4), "traffic": measured_traffic(args.workload, n, nq, k)[0],
             "traffic_source": measured_traffic(args.workload, n, nq, k)[1],
-            "kernel": "scan_kernel", "launches": nscan, "avg_ms": round(scan_avg_s * 1e3, 4),
+            "kernel": "scan", "scan_kinds": {f: idx.prof_get(f)[0] for f in ("shared", "gemm", "tiled", "streamed") if idx.prof_get(f)[0]},
+            "launches": nscan, "avg_ms": round(scan_avg_s * 1e3, 4),
             "algorithmic_flops_per_launch": flops, "merge_avg_ms": round(merge_ms / max(nmerge, 1), 4),
             "prepass_ms_per_step": round(pre_ms / args.steps, 4) if npre else None}
     if nq <= 64:  # streaming regime: the database bytes bound the kernel

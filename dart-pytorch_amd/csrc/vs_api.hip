@@ -628,8 +628,10 @@ int plan_scan(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t 
     p->kind = 0;
     if (!range && kkw <= 0 && plan_share(x, nq, nrows, planes, storage, p, max_lists))
         return VS_OK;
-    if (!max_lists && plan_gemm(x, nq, nrows, planes, storage, kkw > 0 || safe, p)) return VS_OK;
-    if (!max_lists && plan_tile(x, nq, nrows, planes, storage, p)) return VS_OK;
+    // (a list limit shapes the split count of the row-shared and streaming
+    // scans; the tiled scans make few lists per query anyway)
+    if (plan_gemm(x, nq, nrows, planes, storage, kkw > 0 || safe, p)) return VS_OK;
+    if (plan_tile(x, nq, nrows, planes, storage, p)) return VS_OK;
     const int nks = (int)(x->ld / 32);
     const int force_bn = env_int("VS_SCAN_BN", 0);
     const int cands[3] = {64, 32, 16};

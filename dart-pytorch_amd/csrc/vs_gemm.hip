@@ -138,12 +138,17 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[QB][RB], const Sca
                 const float tv = dec_order(tl);
                 const int q = qw0 + qb * 32 + l32;
                 const bool valid = q0 + q < a.nq;
+                uint32_t mk[RB];
                 int c = 0;
 #pragma unroll
-                for (int rb = 0; rb < RB; ++rb)
+                for (int rb = 0; rb < RB; ++rb) {
+                    mk[rb] = 0u;
 #pragma unroll
                     for (int v = 0; v < 16; ++v)
-                        c += valid && acc[qb][rb][v] <= tv && acc[qb][rb][v] < VS_INF ? 1 : 0;
+                        mk[rb] |= (valid && acc[qb][rb][v] <= tv && acc[qb][rb][v] < VS_INF) ? (1u << v)
+                                                                                           : 0u;
+                    c += __builtin_popcount(mk[rb]);
+                }
                 int pos = 0;
                 if (c > 0) pos = atomicAdd(&cnt_w[q], c);
                 if (c > 0) {
@@ -153,9 +158,8 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[QB][RB], const Sca
                     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
                         for (int v = 0; v < 16; ++v) {
-                            const float val = acc[qb][rb][v];
-                            if (val <= tv && val < VS_INF) {
-                                cvq[pos] = val;
+                            if (mk[rb] & (1u << v)) {
+                                cvq[pos] = acc[qb][rb][v];
                                 ciq[pos] = (int32_t)(wr0 + rb * 32 + 8 * (v / 4) + 4 * h + v % 4);
                                 ++pos;
                             }
@@ -195,13 +199,21 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[QB][RB], const Sca
                     }
                     thr_r[qb] = fminf(thr_r[qb], thr_w[q]);
                 }
+                // the passing values of each 32-row block as a bit mask in a
+                // VGPR (no lane mask per value stays live across the append)
+                uint32_t mk[RB];
                 int c = 0;
 #pragma unroll
-                for (int rb = 0; rb < RB; ++rb)
+                for (int rb = 0; rb < RB; ++rb) {
+                    mk[rb] = 0u;
 #pragma unroll
                     for (int v = 0; v < 16; ++v)
-                        c += acc[qb][rb][v] < thr_r[qb] && rb * 32 + 8 * (v / 4) + 4 * h + v % 4 < lim
-                                 ? 1 : 0;
+                        mk[rb] |= (acc[qb][rb][v] < thr_r[qb] &&
+                                   rb * 32 + 8 * (v / 4) + 4 * h + v % 4 < lim)
+                                      ? (1u << v)
+                                      : 0u;
+                    c += __builtin_popcount(mk[rb]);
+                }
                 if (c > 0) {
                     int pos = atomicAdd(&cnt_w[q], c);
                     float *cvq = cv + (int64_t)q * a.cap;
@@ -210,9 +222,8 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[QB][RB], const Sca
                     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
                         for (int v = 0; v < 16; ++v) {
-                            const float val = acc[qb][rb][v];
-                            if (val < thr_r[qb] && rb * 32 + 8 * (v / 4) + 4 * h + v % 4 < lim) {
-                                cvq[pos] = val;
+                            if (mk[rb] & (1u << v)) {
+                                cvq[pos] = acc[qb][rb][v];
                                 ciq[pos] =
                                     (int32_t)(wr0 + rb * 32 + 8 * (v / 4) + 4 * h + v % 4);
                                 ++pos;
@@ -236,26 +247,30 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[QB][RB], const Sca
             // reported: below lim, and above the query (self-join)
             const int omin =
                 a.self_join ? (int)max((int64_t)0, min((int64_t)(32 * RB), qg - wr0 + 1)) : 0;
-            // one reservation per lane for all of its hits
+            // one reservation per lane for all of its hits, found as bit
+            // masks in VGPRs (no lane mask per value stays live)
+            uint32_t mk[RB];
             int c = 0;
 #pragma unroll
-            for (int rb = 0; rb < RB; ++rb)
+            for (int rb = 0; rb < RB; ++rb) {
+                mk[rb] = 0u;
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
                     const int off = rb * 32 + 8 * (v / 4) + 4 * h + v % 4;
-                    c += acc[qb][rb][v] <= thr_r[qb] && off < lim && off >= omin ? 1 : 0;
+                    mk[rb] |= (acc[qb][rb][v] <= thr_r[qb] && off < lim && off >= omin) ? (1u << v) : 0u;
                 }
+                c += __builtin_popcount(mk[rb]);
+            }
             if (c > 0) {
                 unsigned long long pos = atomicAdd(a.count, (unsigned long long)c);
 #pragma unroll
                 for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
                     for (int v = 0; v < 16; ++v) {
-                        const int off = rb * 32 + 8 * (v / 4) + 4 * h + v % 4;
-                        if (acc[qb][rb][v] <= thr_r[qb] && off < lim && off >= omin) {
+                        if (mk[rb] & (1u << v)) {
                             if (pos < (unsigned long long)a.out_cap) {
                                 a.out_q[pos] = (int32_t)qg;
-                                a.out_i[pos] = (int32_t)(wr0 + off);
+                                a.out_i[pos] = (int32_t)(wr0 + rb * 32 + 8 * (v / 4) + 4 * h + v % 4);
                             }
                             ++pos;
                         }
