@@ -437,15 +437,19 @@ constexpr bool kGemmDmaEnabled = false;
 // Row-shared scan (top-k only): bf16 rows of 128 or 256 elements, one query
 // plane, large batches.  Every list keeps kk_final entries (one list per
 // query and workgroup).  VS_SHARE: -1 = default rule (rows of 128 elements,
-// batch >= VS_SHARE_MIN_NQ), 0 = off, 1 = also rows of 256 elements.
+// batch >= VS_SHARE_MIN_NQ), 0 = off, 1 = also rows of 256 elements.  The
+// one-pass selection of fp32 rows (storage kSelectCoarse, k-means) takes
+// rows of 128 and 256 elements.
 // VS_SHARE_ROUNDS: grid size in multiples of the resident workgroups.
 bool plan_share(const vs_index *x, int64_t nq, int64_t nrows, int planes, int storage,
                 vs::ScanPlan *p, int64_t max_split) {
     const int mode = env_int("VS_SHARE", -1);
-    if (mode == 0 || storage != 1 || planes != 1) return false;
-    if (!(x->ld == 128 || (x->ld == 256 && mode > 0))) return false;
+    if (mode == 0 || (storage != 1 && storage != vs::kSelectCoarse) || planes != 1) return false;
+    if (!(x->ld == 128 || (x->ld == 256 && (mode > 0 || storage == vs::kSelectCoarse))))
+        return false;
     if (nq < env_int("VS_SHARE_MIN_NQ", 256)) return false;
-    const int nks = (int)(x->ld / 32), nqb = nks == 4 ? 4 : 2, rt = 4;
+    const int nks = (int)(x->ld / 32), nqb = nks == 4 ? 4 : 2;
+    const int rt = storage == 1 ? 4 : 2;  // fp32 tiles: half the rows, the same staging registers
     // a list of the row-shared scan gains up to 16 entries per 16-row block
     // and query; 256 slots at least keep cuts rare while its threshold is
     // still loose (the list is sorted only up to its fill)
@@ -454,6 +458,9 @@ bool plan_share(const vs_index *x, int64_t nq, int64_t nrows, int planes, int st
     const size_t lds = vs::share_lds_bytes(nks, nqb, rt, cap);
     if (lds > x->lds_max) return false;
     p->kind = 3;
+    p->tile_st = storage;
+    p->share_topm = 0;
+    p->share_ids = 0;
     p->kk = kk;
     p->cap = cap;
     p->nks = nks;
@@ -466,7 +473,7 @@ bool plan_share(const vs_index *x, int64_t nq, int64_t nrows, int planes, int st
     // Splits: the whole grid resident at once (or whole rounds of it), so the
     // query blocks of a split -- dealt to one XCD back to back -- walk its
     // rows together through that XCD's L2, and no round is left half empty.
-    const int bpc = std::max(1, vs::share_blocks_per_cu(nks, p->bn, rt, x->ld, lds));
+    const int bpc = std::max(1, vs::share_blocks_per_cu(storage, nks, p->bn, rt, x->ld, lds, 0));
     const int64_t resident = (int64_t)std::max(1, x->num_cu) * bpc;
     const int64_t target = resident * std::max(1, env_int("VS_SHARE_ROUNDS", 2));
     int64_t nsplit = std::max<int64_t>(1, target / p->nqblk);
@@ -967,8 +974,10 @@ int range_core(vs_index *x, const vs::PreparedQueries &pq, double radius, int se
     vs::ScanPlan plan;
     int rc = VS_OK;
     bool coarse = x->storage == 0 && env_int("VS_COARSE", 1) != 0;
-    if (coarse) coarse = plan_scan(x, pq.nq, x->ntotal, 1, 8, vs::kSelectCoarse, &plan) == VS_OK &&
-                         plan.kind == 2;
+    if (coarse)
+        coarse = plan_scan(x, pq.nq, x->ntotal, 1, 8, vs::kSelectCoarse, &plan, false, 0, true) ==
+                     VS_OK &&
+                 plan.kind == 2;
     if (!coarse) {
         plan = vs::ScanPlan();
         rc = plan_scan(x, pq.nq, x->ntotal, pq.planes, 8, x->storage, &plan, false, 0, true);
@@ -1478,16 +1487,25 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     vs::ScanPlan plan;
     bool coarse = env_int("VS_COARSE", 1) != 0;
     if (coarse) coarse = plan_scan(&cview, n, K, 1, 16, vs::kSelectCoarse, &plan) == VS_OK &&
-                         plan.kind == 2;
+                         (plan.kind == 2 || plan.kind == 3);
+    // on the row-shared scan the shortlists are per-lane register top-m
+    // pairs (no lists to cut; the pick bounds the rest by each lane's m-th)
+    if (coarse && plan.kind == 3) {
+        plan.share_topm = vs::share_topm();
+        plan.share_ids = 1;
+    }
     if (!coarse) {
         plan = vs::ScanPlan();
         rc = plan_scan(&cview, n, K, pq.planes, 16, 0, &plan);
         if (rc) return rc;
     }
     if ((rc = scan_fits(plan, pq))) return rc;
-    const size_t nlist = (size_t)plan.nqblk * plan.nsplit * plan.lw * plan.bn * plan.cap;
+    const size_t nlists = (size_t)plan.nqblk * plan.nsplit * plan.lw * plan.bn;
+    const size_t nlist = nlists * plan.cap;
     VS_HIP(x->cand_v.ensure(nlist * 4), "candidate lists");
     VS_HIP(x->cand_i.ensure(nlist * 4), "candidate lists");
+    VS_HIP(x->lcnt.ensure((nlists + 1) * 4), "list counts");
+    VS_HIP(hipMemsetAsync(x->lcnt.as<int32_t>() + nlists, 0, 4, x->st), "list counts");
     VS_HIP(x->gthr.ensure((size_t)pq.nq_pad * 4), "shared thresholds");
     VS_HIP(hipMemsetD32Async((hipDeviceptr_t)x->gthr.p, (int)vs::kGthrInit, (size_t)pq.nq_pad, x->st),
            "shared thresholds");
@@ -1496,7 +1514,7 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
         ProfScope ps(x, "assign");
         VS_HIP(vs::launch_scan_topk(x->km_cen.p, 0, ld, x->km_cxn.as<float>(), K, 0, pq, plan,
                                     x->cand_v.as<float>(), x->cand_i.as<int32_t>(),
-                                    x->gthr.as<uint32_t>(), nullptr, nullptr, x->st),
+                                    x->gthr.as<uint32_t>(), nullptr, x->lcnt.as<int32_t>(), x->st),
                "assign scan");
     }
     // error bound of the accumulator (split-bf16 products + fp32 sums)
@@ -1625,20 +1643,22 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     for (int64_t i = 0; i < n; ++i) o += best[(size_t)i];
     if (obj) *obj = o;
     // empty clusters, in centroid order, in place (kmeans.dart:127-139): the
-    // largest cluster's centroid is already updated when it precedes c
+    // largest cluster's centroid holds its new value when it precedes c, and
+    // still its old one otherwise (c itself included)
     int64_t used = 0;
     for (int64_t c = 0; c < K; ++c) {
         if (counts[c] >= min_points) continue;
         int64_t big = 0;
         for (int64_t cc = 1; cc < K; ++cc)
             if (counts[cc] > counts[big]) big = cc;
+        const float *src = big < c ? &cen_new[(size_t)(big * d)] : &cen_in[(size_t)(big * d)];
         for (int64_t j = 0; j < d; ++j) {
             if (used >= njitter)
                 return set_err(VS_ERR_INVALID,
                                "empty cluster needs more jitter values than the %lld given",
                                (long long)njitter);
             const double jit = (jitter_u[used++] - 0.5) * 1e-4;
-            cen_new[(size_t)(c * d + j)] = (float)((double)cen_new[(size_t)(big * d + j)] + jit);
+            cen_new[(size_t)(c * d + j)] = (float)((double)src[j] + jit);
         }
     }
     memcpy(centroids_out, cen_new.data(), (size_t)K * d * 4);

@@ -101,6 +101,7 @@ struct ScanPlan {
     int64_t tile_group = 8;        // tiled scan: query blocks per XCD group (grid order)
     int share_topm = 0;   // row-shared scan: >0 keeps per-lane register top-m values (sample
                           // estimates; lists get 4 * m values per query and workgroup, ids 0)
+    int share_ids = 0;    // with share_topm: the ids too, lane g's m pairs at slots [g m, g m + m)
     int64_t nqblk = 0;    // query blocks
     int64_t nsplit = 0;   // database splits
     int64_t rows_per_split = 0;
@@ -260,8 +261,9 @@ size_t gemm_lds_bytes(int st, int pb, int wr, int wq, int rb, int qb, int kc, in
 
 // LDS of the row-shared scan (two row stages plus list bookkeeping).
 size_t share_lds_bytes(int nks, int nqb, int rt, int cap);
-// Row-shared scan workgroups one CU holds at once (0: no such shape).
-int share_blocks_per_cu(int nks, int bn, int rt, int64_t ld, size_t lds);
+// Row-shared scan workgroups one CU holds at once (0: no such shape; mode 0
+// lists, 2 top-m values, 3 top-m values and ids).
+int share_blocks_per_cu(int st, int nks, int bn, int rt, int64_t ld, size_t lds, int mode);
 // m of the row-shared scan's register top-m variant.
 int share_topm();
 

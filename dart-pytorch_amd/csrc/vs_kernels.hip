@@ -735,6 +735,8 @@ struct MergeKArgs {
     int32_t *vf_count;    // queries whose lists may have dropped a winner
     int32_t *vf_list;
     int guess;            // thresholds were estimated: flag queries left short
+    int seg_m;            // k-means pick: lists are 4 sorted segments of seg_m pairs, one per
+                          // scan lane; rows a lane dropped are >= its segment's last value
     int seed_rank;        // MODE 2: rank whose value sets the threshold (0: kk)
     int64_t k;
     float *D;
@@ -995,6 +997,7 @@ hipError_t launch_merge_refine(const void *xb, int storage, int64_t ld, int64_t 
 
 template <int KK>
 __global__ void kmeans_pick_kernel(MergeKArgs a);
+__global__ void kmeans_pick_seg_kernel(MergeKArgs a);
 
 // Threshold seeding from a pre-pass: for every query, the kk_final-th
 // smallest accumulator value over its lists tightens its shared threshold.
@@ -1064,6 +1067,17 @@ hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, 
     a.best_sq = best_sq;
     a.fb_count = fallback_count;
     a.fb_list = fallback_list;
+    if (plan.kind == 3) {
+        // per-lane register shortlists of the row-shared scan: 4 segments of
+        // m pairs per list
+        if (!plan.share_topm || !plan.share_ids || 4 * plan.share_topm != 32 ||
+            plan.cap < 4 * plan.share_topm)
+            return hipErrorInvalidValue;
+        a.kl = 4 * plan.share_topm;
+        a.seg_m = plan.share_topm;
+        kmeans_pick_seg_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(a);
+        return hipGetLastError();
+    }
     if (plan.kk_final == 16 && plan.kk == 16) {
         kmeans_pick_kernel<16><<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(a);
         return hipGetLastError();
@@ -1176,6 +1190,85 @@ __global__ __launch_bounds__(256) void kmeans_pick_kernel(MergeKArgs a) {
     const bool safe = bid != INT_MAX &&
                       (a_last == VS_INF ||
                        (double)a_last - (double)a.bound > (best - xx) + 1e-9 * (fabs(xx) + 1.0));
+    a.assign[qg] = bid == INT_MAX ? 0 : bid;
+    a.best_sq[qg] = best;
+    if (!safe) a.fb_list[atomicAdd(a.fb_count, 1)] = (int32_t)qg;
+}
+
+// ---------------------------------------------------------------------------
+// k-means pick over per-lane register shortlists (the row-shared scan): one
+// lane per point.  Each list holds 4 sorted segments of seg_m (accumulator,
+// centroid) pairs, one per scan lane, and every centroid a lane dropped has
+// an accumulator at or above the last value of its segment.  Pass 1 finds
+// the smallest accumulator and that bound; pass 2 re-scores exactly -- fp64,
+// dimensions in order -- every candidate within 2 * bound of the smallest
+// (any other is provably worse than it) and takes the argmin with the lowest
+// id among equal scores.  The pick is proven when every centroid outside the
+// segments is provably worse; unproven points go to the exhaustive kernel.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void kmeans_pick_seg_kernel(MergeKArgs a) {
+    const int64_t qg = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (qg >= a.nq) return;
+    const int64_t qblk = qg / a.bn, q = qg % a.bn;
+    const int64_t nlists = a.nsplit * a.lw;
+    auto list_off = [&](int64_t l) {
+        const int64_t split = l / a.lw, w = l % a.lw;
+        return (((qblk * a.nsplit + split) * a.lw + w) * a.bn + q) * a.cap;
+    };
+    float vmin = VS_INF, seg_bound = VS_INF;
+    for (int64_t l = 0; l < nlists; ++l) {
+        const int64_t off = list_off(l);
+        for (int sgi = 0; sgi < 4; ++sgi) {
+            const float head = a.cand_v[off + sgi * a.seg_m];
+            const int hid = a.cand_i[off + sgi * a.seg_m];
+            if (hid >= 0) vmin = fminf(vmin, head);
+            seg_bound = fminf(seg_bound, a.cand_v[off + sgi * a.seg_m + a.seg_m - 1]);
+        }
+    }
+    const float lim = vmin + 2.0f * a.bound;
+    const float4 *xr = (const float4 *)(a.pts + qg * a.ld);
+    const float *cen = (const float *)a.xb;
+    const int64_t n4 = a.ld / 4;
+    double best = __builtin_huge_val(), xx = 0.0;
+    int bid = INT_MAX;
+    for (int64_t j4 = 0; j4 < n4; ++j4) {
+        const float4 xv = xr[j4];
+        xx = xx + (double)xv.x * (double)xv.x;
+        xx = xx + (double)xv.y * (double)xv.y;
+        xx = xx + (double)xv.z * (double)xv.z;
+        xx = xx + (double)xv.w * (double)xv.w;
+    }
+    for (int64_t l = 0; l < nlists; ++l) {
+        const int64_t off = list_off(l);
+        for (int e = 0; e < a.kl; ++e) {
+            const int id = a.cand_i[off + e];
+            if (id < 0 || a.cand_v[off + e] > lim) continue;
+            if ((int64_t)id >= a.nrows) {
+                atomicOr(a.flags, kFlagBadId);
+                continue;
+            }
+            const float4 *cr = (const float4 *)(cen + (int64_t)id * a.ld);
+            double sc = 0.0;
+            for (int64_t j4 = 0; j4 < n4; ++j4) {
+                const float4 xv = xr[j4];
+                const float4 cv = cr[j4];
+                const double d0 = (double)xv.x - (double)cv.x, d1 = (double)xv.y - (double)cv.y;
+                const double d2 = (double)xv.z - (double)cv.z, d3 = (double)xv.w - (double)cv.w;
+                sc = sc + d0 * d0;
+                sc = sc + d1 * d1;
+                sc = sc + d2 * d2;
+                sc = sc + d3 * d3;
+            }
+            if (sc < best || (sc == best && id < bid)) {
+                best = sc;
+                bid = id;
+            }
+        }
+    }
+    // accumulators are within `bound` of |c|^2 - 2 x.c = score - |x|^2
+    const bool safe = bid != INT_MAX &&
+                      (seg_bound == VS_INF ||
+                       (double)seg_bound - (double)a.bound > (best - xx) + 1e-9 * (fabs(xx) + 1.0));
     a.assign[qg] = bid == INT_MAX ? 0 : bid;
     a.best_sq[qg] = best;
     if (!safe) a.fb_list[atomicAdd(a.fb_count, 1)] = (int32_t)qg;

@@ -30,15 +30,19 @@
 
 namespace vs {
 
-template <int NKS, int NQB, int RT>
+// ST 1: bf16 rows.  ST 2: fp32 rows whose bf16 rounding (the hi plane) is
+// multiplied: the one-pass selection, whose callers widen their margins and
+// decide exactly.
+template <int ST, int NKS, int NQB, int RT>
 struct ShareShape {
     static constexpr int NW = 4, NT = 256;
     static constexpr int LD = 32 * NKS;         // elements per stored row
-    static constexpr int KP = LD + 8;           // LDS row stride (elements)
+    static constexpr int ESZ = ST == 1 ? 2 : 4; // bytes per stored element
+    static constexpr int KP = LD + 8;           // LDS row stride (bf16 elements)
     static constexpr int TR = 16 * RT;          // rows per tile
     static constexpr int BNW = 16 * NQB;        // queries per wave
     static constexpr int BN = NW * BNW;         // queries per block
-    static constexpr int CPR = LD * 2 / 16;     // 16-byte chunks per row
+    static constexpr int CPR = LD * ESZ / 16;   // 16-byte global chunks per row
     static constexpr int LOADS = TR * CPR / NT; // 16-byte loads per thread and tile
     static constexpr size_t STAGE_BYTES = (size_t)TR * KP * 2 + (size_t)TR * 4;
     static_assert(TR * CPR % NT == 0, "whole loads per thread");
@@ -59,12 +63,15 @@ size_t share_lds_bytes(int nks, int nqb, int rt, int cap) {
 // registers, and writes them out at the end (4 * TOPM values per query and
 // workgroup, ids 0).  The r-th smallest value of their union is the query's
 // r-th smallest over the rows whenever no lane met more than TOPM of those r,
-// and larger otherwise, never smaller.
+// and larger otherwise, never smaller.  MODE 3 (shortlists, k-means): the
+// same with the row ids; lane g's TOPM pairs fill slots [g TOPM, (g + 1)
+// TOPM) of the query's list, sorted, so every row the lane dropped is at or
+// above the last of its slots.
 constexpr int kShareTopM = 8;
 
-template <int NKS, int NQB, int RT, int MODE>
+template <int ST, int NKS, int NQB, int RT, int MODE>
 __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
-    using S = ShareShape<NKS, NQB, RT>;
+    using S = ShareShape<ST, NKS, NQB, RT>;
     constexpr int TOPM = kShareTopM;
     constexpr int TR = S::TR, KP = S::KP, BNW = S::BNW;
     extern __shared__ __align__(16) char smem[];
@@ -107,7 +114,7 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
                                           8 * g);
 
     // global -> register staging of one tile of rows (and its row norms)
-    const int64_t row_bytes = (int64_t)S::LD * 2;
+    const int64_t row_bytes = (int64_t)S::LD * S::ESZ;
     u32x4_t ra[S::LOADS];
     f32x4_t rn = {0.f, 0.f, 0.f, 0.f};
     auto gload = [&](int64_t t) __attribute__((always_inline)) {
@@ -124,7 +131,13 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
 #pragma unroll
         for (int j = 0; j < S::LOADS; ++j) {
             const int i = tid + j * S::NT, row = i / S::CPR, c = i % S::CPR;
-            *(u32x4_t *)(As + row * KP + c * 8) = ra[j];
+            if constexpr (ST == 1) {
+                *(u32x4_t *)(As + row * KP + c * 8) = ra[j];
+            } else {  // 4 fp32 values -> their bf16 rounding
+                typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+                const bf16x4_t hi = __builtin_convertvector(__builtin_bit_cast(f32x4_t, ra[j]), bf16x4_t);
+                *(u32x2_t *)(As + row * KP + c * 4) = __builtin_bit_cast(u32x2_t, hi);
+            }
         }
         if (l2 && tid < TR / 4) *(f32x4_t *)((float *)(As + TR * KP) + 4 * tid) = rn;
     };
@@ -150,11 +163,16 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb) thr_r[qb] = fminf(thr_r[qb], dec_order(gt[qb]));
 
-    float top[MODE == 2 ? NQB : 1][TOPM];
+    constexpr bool TOPMODE = MODE >= 2;
+    float top[TOPMODE ? NQB : 1][TOPM];
+    int topi[MODE == 3 ? NQB : 1][TOPM];
 #pragma unroll
-    for (int qb = 0; qb < (MODE == 2 ? NQB : 1); ++qb)
+    for (int qb = 0; qb < (TOPMODE ? NQB : 1); ++qb)
 #pragma unroll
-        for (int m = 0; m < TOPM; ++m) top[qb][m] = VS_INF;
+        for (int m = 0; m < TOPM; ++m) {
+            top[qb][m] = VS_INF;
+            if constexpr (MODE == 3) topi[qb][m] = -1;
+        }
 
     const f32x4_t zero4 = {0.f, 0.f, 0.f, 0.f};
     int par = 0;
@@ -191,8 +209,10 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
                     }
             }
 
-            if constexpr (MODE == 2) {
+            if constexpr (TOPMODE) {
                 // sorted insertion of each value below the lane's TOPM-th
+                // (rows arrive in increasing order per lane: a tie keeps the
+                // lower id first)
 #pragma unroll
                 for (int qb = 0; qb < NQB; ++qb) {
                     const float m4 =
@@ -202,11 +222,25 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
                     for (int i = 0; i < 4; ++i) {
                         float v = acc[qb][i];
                         if (v < top[qb][TOPM - 1]) {
+                            if constexpr (MODE == 2) {
 #pragma unroll
-                            for (int m = 0; m < TOPM; ++m) {
-                                const float lo = fminf(top[qb][m], v);
-                                v = fmaxf(top[qb][m], v);
-                                top[qb][m] = lo;
+                                for (int m = 0; m < TOPM; ++m) {
+                                    const float lo = fminf(top[qb][m], v);
+                                    v = fmaxf(top[qb][m], v);
+                                    top[qb][m] = lo;
+                                }
+                            } else {
+                                int id = (int)(rbase + i);
+#pragma unroll
+                                for (int m = 0; m < TOPM; ++m) {
+                                    const bool lt = v < top[qb][m];
+                                    const float tv = lt ? top[qb][m] : v;
+                                    const int ti = lt ? topi[qb][m] : id;
+                                    top[qb][m] = lt ? v : top[qb][m];
+                                    topi[qb][m] = lt ? id : topi[qb][m];
+                                    v = tv;
+                                    id = ti;
+                                }
                             }
                         }
                     }
@@ -273,9 +307,9 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
         par ^= 1;
     }
 
-    if constexpr (MODE == 2) {
-        // lane (r16, g) writes its TOPM values of query qw + 16 qb + r16 to
-        // slots [g * TOPM, (g + 1) * TOPM) of that query's list
+    if constexpr (TOPMODE) {
+        // lane (r16, g) writes its TOPM values (and ids) of query qw + 16 qb
+        // + r16 to slots [g * TOPM, (g + 1) * TOPM) of that query's list
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb) {
             const int q = qw + qb * 16 + r16;
@@ -284,7 +318,7 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
 #pragma unroll
             for (int m = 0; m < TOPM; ++m) {
                 cvq[m] = top[qb][m];
-                ciq[m] = 0;
+                ciq[m] = MODE == 3 ? topi[qb][m] : 0;
             }
         }
         int32_t *lc = a.list_cnt + (qblk * a.nsplit + split) * (int64_t)S::BN + qw;
@@ -324,13 +358,17 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
     }
 }
 
-// The built shapes: X(K-steps, 16-query blocks per wave, 16-row blocks per tile).
-#define VS_SHARE_SHAPES(X) X(4, 4, 4) X(8, 2, 4)
+// The built shapes: X(storage, K-steps, 16-query blocks per wave, 16-row
+// blocks per tile).
+#define VS_SHARE_SHAPES(X) X(1, 4, 4, 4) X(1, 8, 2, 4) X(2, 4, 4, 2) X(2, 8, 2, 2)
 
-static void (*share_kernel(int nks, int bn, int rt, int64_t ld, int topm))(ScanKArgs) {
-#define VS_SHARE_PICK(NKS_, NQB_, RT_)                                                      \
-    if (nks == NKS_ && bn == 64 * NQB_ && rt == RT_ && ld == 32 * NKS_)                       \
-        return topm ? share_scan_kernel<NKS_, NQB_, RT_, 2> : share_scan_kernel<NKS_, NQB_, RT_, 0>;
+// mode: 0 lists, 2 top-m values, 3 top-m values and ids
+static void (*share_kernel(int st, int nks, int bn, int rt, int64_t ld, int mode))(ScanKArgs) {
+#define VS_SHARE_PICK(ST_, NKS_, NQB_, RT_)                                                     \
+    if (st == ST_ && nks == NKS_ && bn == 64 * NQB_ && rt == RT_ && ld == 32 * NKS_)              \
+        return mode == 3   ? share_scan_kernel<ST_, NKS_, NQB_, RT_, 3>                           \
+               : mode == 2 ? share_scan_kernel<ST_, NKS_, NQB_, RT_, 2>                           \
+                           : share_scan_kernel<ST_, NKS_, NQB_, RT_, 0>;
     VS_SHARE_SHAPES(VS_SHARE_PICK)
 #undef VS_SHARE_PICK
     return nullptr;
@@ -339,8 +377,8 @@ static void (*share_kernel(int nks, int bn, int rt, int64_t ld, int topm))(ScanK
 int share_topm() { return kShareTopM; }
 
 // Workgroups of the shape that one CU holds at once (registers and LDS).
-int share_blocks_per_cu(int nks, int bn, int rt, int64_t ld, size_t lds) {
-    void (*fn)(ScanKArgs) = share_kernel(nks, bn, rt, ld, 0);
+int share_blocks_per_cu(int st, int nks, int bn, int rt, int64_t ld, size_t lds, int mode) {
+    void (*fn)(ScanKArgs) = share_kernel(st, nks, bn, rt, ld, mode);
     if (!fn) return 0;
     if (lds > 64 * 1024 && hipFuncSetAttribute((const void *)fn,
                                                hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -358,7 +396,9 @@ hipError_t launch_share_scan(const ScanPlan &plan, const ScanKArgs &args, hipStr
         return hipErrorInvalidValue;
     const int64_t total = plan.nqblk * plan.nsplit;
     const int64_t grid = ((total + 7) / 8) * 8;
-    void (*fn)(ScanKArgs) = share_kernel(plan.nks, plan.bn, plan.tm, args.ld, plan.share_topm);
+    const int mode = !plan.share_topm ? 0 : plan.share_ids ? 3 : 2;
+    void (*fn)(ScanKArgs) =
+        share_kernel(plan.tile_st, plan.nks, plan.bn, plan.tm, args.ld, mode);
     if (!fn) return hipErrorInvalidValue;
     const size_t lds = plan.lds_bytes;
     if (lds > 64 * 1024) {

@@ -44,6 +44,30 @@ def test_kmeans_empty_cluster_jitter(vs):
     assert np.array_equal(newc.view(np.uint32), cr.view(np.uint32))
 
 
+def test_kmeans_empty_cluster_before_largest(vs):
+    """An empty cluster preceding the largest one copies the largest
+    cluster's old centroid (the in-place loop of kmeans.dart:107-140 has not
+    updated it yet); one after it copies the new centroid.  The oracle
+    updates in place the same way; the centroids must be bit-identical."""
+    g = syn.rng(9, 0)
+    a_pts = (g.standard_normal((500, 16)) * 0.1).astype(np.float32)
+    b_pts = (g.standard_normal((2000, 16)) * 0.1 + 5.0).astype(np.float32)
+    x = np.concatenate([a_pts, b_pts]).astype(np.float32)
+    far = np.full((1, 16), 1e3, np.float32)
+    cen = np.concatenate([far, x[:1] + 0.3, x[600:601] + 0.3, far * 2]).astype(np.float32)
+    u = syn.rng(9, 1).random(2 * 16)
+    pts = vs.GpuIndexFlat.l2(16, storage="f32")
+    pts.add(x)
+    a, newc, cnt, obj = vs.kmeans_step(pts, cen, 1, u)
+    ar, _, objr = oracle.kmeans_assign(x, cen, NT)
+    cr, cntr, used = oracle.kmeans_update(x, ar, cen, 1, u)
+    assert list(cntr) == [0, 500, 2000, 0] and used == 32
+    assert np.array_equal(a, ar) and obj == objr and np.array_equal(cnt, cntr)
+    assert np.array_equal(newc.view(np.uint32), cr.view(np.uint32))
+    # the first empty cluster took the largest cluster's old centroid
+    assert np.abs(newc[0] - cen[2]).max() < 1e-3 and np.abs(newc[3] - cr[2]).max() < 1e-3
+
+
 def test_kmeans_train_monotone(vs):
     """vector_store_test.dart:91-111: re-assignment objective <= 1.05 x training objective."""
     x, _ = syn.gaussian_mixture(400, 16, 8, 0.05, 1)

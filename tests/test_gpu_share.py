@@ -88,3 +88,49 @@ def test_small_batch_not_shared(vs):
     D, I = _search(vs, xb, xq, 10, 0, expect_shared=False)
     Dr, Ir = oracle.flat_search(xb, xq, 10, 0, NT)
     assert_knn_parity(D, I, Dr, Ir, 0, rtol=0.0, atol=0.0, xb=xb, xq=xq)
+
+
+def _kmeans_check(vs, x, cen, min_points=1, seed=0, expect_fallback=False):
+    pts = vs.GpuIndexFlat.l2(x.shape[1], storage="f32")
+    pts.add(x)
+    K = len(cen)
+    u = syn.rng(seed + 1, 0).random(K * x.shape[1])
+    a, newc, cnt, obj = vs.kmeans_step(pts, cen, min_points, u)
+    shared, _ = pts.prof_get("shared")
+    nfb, _ = pts.prof_get("kmeans_fallback_points")
+    pts.close()
+    assert shared >= 1, "the row-shared scan did not run"
+    if expect_fallback:
+        assert nfb >= 1
+    ar, _, objr = oracle.kmeans_assign(x, cen, NT)
+    assert np.array_equal(a, ar), f"{np.sum(a != ar)} assignments differ"
+    assert obj == objr
+    cr, cntr, _ = oracle.kmeans_update(x, ar, cen, min_points, u)
+    assert np.array_equal(cnt, cntr)
+    assert np.array_equal(newc.view(np.uint32), cr.view(np.uint32))
+    return a
+
+
+@pytest.mark.parametrize("n,d,ncomp,K", [(30_000, 256, 1024, 4096), (9_000, 100, 64, 500),
+                                         (3_000, 256, 8, 20)])
+def test_kmeans_register_shortlists(vs, n, d, ncomp, K):
+    """k-means assign on the row-shared scan (fp32 points and centroids,
+    one-pass bf16 selection): each scan lane keeps its 8 smallest
+    (accumulator, centroid) pairs in registers, the pick re-scores them in
+    fp64 and proves the argmin with the smallest value any lane dropped.
+    Assignments, objective and centroids equal the oracle's (K = 20: lanes
+    see fewer than 8 centroids each)."""
+    x, _ = syn.gaussian_mixture(n, d, ncomp, 0.1, 41)
+    cen = x[syn.seeded_subset(n, K, 41)].copy()
+    _kmeans_check(vs, x, cen)
+
+
+def test_kmeans_register_shortlists_fallback(vs):
+    """Forty copies of one centroid fill every lane's 8 slots for the points
+    near it, so no pick is provable and the exhaustive exact scan decides:
+    the lowest index among the copies loses to the original (kmeans.dart:93-101)."""
+    x, _ = syn.gaussian_mixture(6000, 256, 16, 0.1, 5)
+    cen = x[syn.seeded_subset(len(x), 300, 5)].copy()
+    cen[100:140] = cen[3]
+    a = _kmeans_check(vs, x, cen, expect_fallback=True)
+    assert not np.any((a >= 100) & (a < 140))
