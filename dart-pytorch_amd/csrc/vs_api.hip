@@ -129,6 +129,7 @@ struct vs_index {
     vs::PreparedQueries km_pq;
     uint32_t km_pflags = 0;
     uint64_t km_prep_version = ~0ull;
+    int64_t km_iota_n = -1;  // km_iota holds 0 .. km_iota_n - 1
     bool prof_on = false;
     std::map<std::string, ProfEntry> prof;
     std::vector<PendingEvent> pending;
@@ -1584,14 +1585,19 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     VS_HIP(vs::launch_kmeans_count(x->km_assign.as<int32_t>(), n, x->km_counts.as<int32_t>(),
                                    x->st),
            "counts");
-    VS_HIP(x->km_iota.ensure((size_t)n * 4), "iota");
     {
-        std::vector<int32_t> iota((size_t)n);
-        std::iota(iota.begin(), iota.end(), 0);
-        VS_HIP(hipMemcpyAsync(x->km_iota.p, iota.data(), (size_t)n * 4, hipMemcpyHostToDevice,
-                              x->st),
-               "iota");
-        VS_HIP(hipStreamSynchronize(x->st), "iota");
+        // the point indices 0 .. n - 1 (the sort's values), kept across steps
+        void *before = x->km_iota.p;
+        VS_HIP(x->km_iota.ensure((size_t)n * 4), "iota");
+        if (x->km_iota.p != before || x->km_iota_n != n) {
+            std::vector<int32_t> iota((size_t)n);
+            std::iota(iota.begin(), iota.end(), 0);
+            VS_HIP(hipMemcpyAsync(x->km_iota.p, iota.data(), (size_t)n * 4, hipMemcpyHostToDevice,
+                                  x->st),
+                   "iota");
+            VS_HIP(hipStreamSynchronize(x->st), "iota");
+            x->km_iota_n = n;
+        }
     }
     VS_HIP(x->km_keys.ensure((size_t)n * 4), "sort keys");
     VS_HIP(x->km_order.ensure((size_t)n * 4), "sort values");
@@ -1638,10 +1644,11 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     VS_HIP(hipMemcpyAsync(cen_new.data(), x->km_out.p, (size_t)K * d * 4, hipMemcpyDeviceToHost,
                           x->st),
            "reading centroids");
-    VS_HIP(hipStreamSynchronize(x->st), "update");
+    // the objective (read before the counts) while the update runs
     double o = 0.0;
     for (int64_t i = 0; i < n; ++i) o += best[(size_t)i];
     if (obj) *obj = o;
+    VS_HIP(hipStreamSynchronize(x->st), "update");
     // empty clusters, in centroid order, in place (kmeans.dart:127-139): the
     // largest cluster's centroid holds its new value when it precedes c, and
     // still its old one otherwise (c itself included)

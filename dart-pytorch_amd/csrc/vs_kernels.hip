@@ -999,6 +999,56 @@ template <int KK>
 __global__ void kmeans_pick_kernel(MergeKArgs a);
 __global__ void kmeans_pick_seg_kernel(MergeKArgs a);
 
+// Threshold estimates from a pre-pass (seed_rank <= 64): one wave per query.
+// Every lane keeps the 8 smallest values it reads from the query's lists,
+// sorted in registers; then seed_rank rounds of a wave-wide minimum pop the
+// smallest remaining value (from the lowest lane holding it).  The last one
+// popped is the seed_rank-th smallest of the lists whenever no lane held
+// more than 8 of those, and larger otherwise (never smaller, so the rows of
+// the sample at or below it are at least seed_rank).  With fewer than
+// seed_rank values the threshold stays.
+__global__ __launch_bounds__(256) void merge_estimate_kernel(MergeKArgs a) {
+    constexpr int L = 8;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t qg = (int64_t)blockIdx.x * 4 + wave;
+    if (qg >= a.nq) return;
+    const int64_t qblk = qg / a.bn, q = qg % a.bn;
+    const int64_t nlists = a.nsplit * a.lw;
+    const float tfinal = dec_order(a.gthr[qg]);
+    float loc[L];
+#pragma unroll
+    for (int i = 0; i < L; ++i) loc[i] = VS_INF;
+    for (int64_t l = 0; l < nlists; ++l) {
+        const int64_t split = l / a.lw, w = l % a.lw;
+        const int64_t li = ((qblk * a.nsplit + split) * a.lw + w) * a.bn + q;
+        const int64_t lc = a.list_cnt ? min((int64_t)a.kl, (int64_t)a.list_cnt[li]) : a.kl;
+        for (int64_t e = lane; e < lc; e += 64) {
+            float v = a.cand_v[li * a.cap + e];
+            if (a.cand_i[li * a.cap + e] < 0 || !(v <= tfinal) || !(v < loc[L - 1])) continue;
+#pragma unroll
+            for (int i = 0; i < L; ++i) {
+                const float lo = fminf(loc[i], v);
+                v = fmaxf(loc[i], v);
+                loc[i] = lo;
+            }
+        }
+    }
+    float kth = VS_INF;
+    for (int k = 0; k < a.seed_rank; ++k) {
+        float m = loc[0];
+        for (int o = 32; o > 0; o >>= 1) m = fminf(m, __shfl_xor(m, o));
+        if (!(m < VS_INF)) break;  // fewer than seed_rank values
+        const unsigned long long holders = __ballot(loc[0] == m);
+        if (lane == __ffsll((long long)holders) - 1) {
+#pragma unroll
+            for (int i = 0; i + 1 < L; ++i) loc[i] = loc[i + 1];
+            loc[L - 1] = VS_INF;
+        }
+        if (k + 1 == a.seed_rank) kth = m;
+    }
+    if (lane == 0 && kth < VS_INF) atomicMin(&a.gthr_w[qg], enc_order(kth) + 1u);
+}
+
 // Threshold seeding from a pre-pass: for every query, the kk_final-th
 // smallest accumulator value over its lists tightens its shared threshold.
 hipError_t launch_merge_threshold(const PreparedQueries &pq, const ScanPlan &plan,
@@ -1025,6 +1075,10 @@ hipError_t launch_merge_threshold(const PreparedQueries &pq, const ScanPlan &pla
     a.cand_i = cand_i;
     a.gthr = gthr;
     a.gthr_w = gthr;
+    if (seed_rank > 0 && seed_rank <= 64) {
+        merge_estimate_kernel<<<dim3((unsigned)((pq.nq + 3) / 4)), dim3(256), 0, st>>>(a);
+        return hipGetLastError();
+    }
     const size_t lds = merge_lds(ld);
     void (*fn)(MergeKArgs) = merge_refine_kernel<1, 2>;
     if (lds > 64 * 1024) {
