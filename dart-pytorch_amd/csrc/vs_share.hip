@@ -185,9 +185,9 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
         const float *Ns = (const float *)(As + TR * KP);
         const uint16_t *al = As + r16 * KP + 8 * g;
 
-#pragma unroll
-        for (int rb = 0; rb < RT; ++rb) {
-            f32x4_t acc[NQB];
+        // the MFMAs of row block rb + 1 are issued before the epilogue of
+        // row block rb, so its compares run while they execute
+        auto mma = [&](int rb, f32x4_t (&acc)[NQB]) __attribute__((always_inline)) {
             const f32x4_t init = l2 ? *(const f32x4_t *)(Ns + rb * 16 + 4 * g) : zero4;
 #pragma unroll
             for (int qb = 0; qb < NQB; ++qb) acc[qb] = init;
@@ -199,6 +199,8 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
                 for (int qb = 0; qb < NQB; ++qb)
                     acc[qb] = mfma_bf16(av, __builtin_bit_cast(bf16x8_t, bq[ks][qb]), acc[qb]);
             }
+        };
+        auto epi = [&](int rb, f32x4_t (&acc)[NQB]) __attribute__((always_inline)) {
             const int64_t rbase = t0 + rb * 16 + 4 * g;  // the lane's first row
             if (t0 + rb * 16 + 16 > r1) {  // rows past the split end never qualify
 #pragma unroll
@@ -245,7 +247,7 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
                         }
                     }
                 }
-                continue;
+                return;
             }
 
             // ---- epilogue of the 16-row block ----
@@ -255,7 +257,7 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
                 const float m = fminf(fminf(acc[qb][0], acc[qb][1]), fminf(acc[qb][2], acc[qb][3]));
                 pass |= m < thr_r[qb];
             }
-            if (!__ballot(pass)) continue;
+            if (!__ballot(pass)) return;
             // make room: a query gains at most 16 entries per row block
             {
                 bool need = false;
@@ -298,6 +300,13 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
                 }
             }
             lds_wave_sync();
+        };
+        f32x4_t accs[2][NQB];
+        mma(0, accs[0]);
+#pragma unroll
+        for (int rb = 0; rb < RT; ++rb) {
+            if (rb + 1 < RT) mma(rb + 1, accs[(rb + 1) & 1]);
+            epi(rb, accs[rb & 1]);
         }
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb) thr_r[qb] = fminf(thr_r[qb], dec_order(gt[qb]));
