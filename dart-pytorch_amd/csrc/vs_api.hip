@@ -155,6 +155,7 @@ struct vs_index {
     // scratch (grown on demand, reused across calls)
     DevBuf stage, qp, qf, qnorm, flags, cand_v, cand_i, lcnt, gthr, lbound, vf, fbq, fbD, fbI, outD, outI,
         athr, rq, ri, rs, rkeep, rcount, misc;
+    DevBuf km_cen16, km_c16n;  // k-means: bf16 copy of the centroid rows (and its unused norms)
     DevBuf km_cen, km_cxn, km_assign, km_best, km_fb, km_keys, km_order, km_tmp, km_counts,
         km_offsets, km_out, km_iota;
     // k-means: the points prepared as queries, kept while the rows are unchanged
@@ -1176,7 +1177,7 @@ void vs_index_destroy(vs_index *x) {
                       &x->misc,    &x->km_cen,    &x->km_cxn,   &x->km_assign, &x->km_best,
                       &x->km_fb,   &x->km_keys,   &x->km_order, &x->km_tmp,   &x->km_counts,
                       &x->km_offsets, &x->km_out, &x->km_iota, &x->lcnt,   &x->km_qp,
-                      &x->km_qf,   &x->km_qnorm};
+                      &x->km_qf,   &x->km_qnorm,  &x->km_cen16, &x->km_c16n};
     for (DevBuf *b : bufs) b->release();
     x->km_hbest.release();
     x->km_hassign.release();
@@ -1507,6 +1508,11 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
            "storing centroids");
     uint32_t cf = 0;
     VS_HIP(hipMemcpyAsync(&cf, x->flags.p, 4, hipMemcpyDeviceToHost, x->st), "flags");
+    // the largest centroid norm, for the accumulator's error bound
+    float cmax = 0.f;
+    VS_HIP(x->misc.ensure(4), "misc");
+    VS_HIP(vs::launch_max_reduce(x->km_cxn.as<float>(), K, x->misc.as<float>(), x->st), "max");
+    VS_HIP(hipMemcpyAsync(&cmax, x->misc.p, 4, hipMemcpyDeviceToHost, x->st), "max");
     VS_HIP(hipStreamSynchronize(x->st), "centroids");
     if (cf & vs::kFlagNonFinite) return set_err(VS_ERR_NONFINITE, "centroids contain NaN or infinity");
 
@@ -1533,42 +1539,10 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     bool coarse = env_int("VS_COARSE", 1) != 0;
     if (coarse) coarse = plan_scan(&cview, n, K, 1, 16, vs::kSelectCoarse, &plan) == VS_OK &&
                          (plan.kind == 2 || plan.kind == 3);
-    // on the row-shared scan the shortlists are per-lane register top-m
-    // pairs (no lists to cut; the pick bounds the rest by each lane's m-th)
-    if (coarse && plan.kind == 3) {
-        plan.share_topm = vs::share_topm();
-        plan.share_ids = 1;
-    }
     if (!coarse) {
         plan = vs::ScanPlan();
         rc = plan_scan(&cview, n, K, pq.planes, 16, 0, &plan);
         if (rc) return rc;
-    }
-    if ((rc = scan_fits(plan, pq))) return rc;
-    const size_t nlists = (size_t)plan.nqblk * plan.nsplit * plan.lw * plan.bn;
-    const size_t nlist = nlists * plan.cap;
-    VS_HIP(x->cand_v.ensure(nlist * 4), "candidate lists");
-    VS_HIP(x->cand_i.ensure(nlist * 4), "candidate lists");
-    VS_HIP(x->lcnt.ensure((nlists + 1) * 4), "list counts");
-    VS_HIP(hipMemsetAsync(x->lcnt.as<int32_t>() + nlists, 0, 4, x->st), "list counts");
-    VS_HIP(x->gthr.ensure((size_t)pq.nq_pad * 4), "shared thresholds");
-    VS_HIP(hipMemsetD32Async((hipDeviceptr_t)x->gthr.p, (int)vs::kGthrInit, (size_t)pq.nq_pad, x->st),
-           "shared thresholds");
-    note_scan_kind(x, plan);
-    {
-        ProfScope ps(x, "assign");
-        VS_HIP(vs::launch_scan_topk(x->km_cen.p, 0, ld, x->km_cxn.as<float>(), K, 0, pq, plan,
-                                    x->cand_v.as<float>(), x->cand_i.as<int32_t>(),
-                                    x->gthr.as<uint32_t>(), nullptr, x->lcnt.as<int32_t>(), x->st),
-               "assign scan");
-    }
-    // error bound of the accumulator (split-bf16 products + fp32 sums)
-    float cmax = 0.f;
-    {
-        VS_HIP(x->misc.ensure(4), "misc");
-        VS_HIP(vs::launch_max_reduce(x->km_cxn.as<float>(), K, x->misc.as<float>(), x->st), "max");
-        VS_HIP(hipMemcpyAsync(&cmax, x->misc.p, 4, hipMemcpyDeviceToHost, x->st), "max");
-        VS_HIP(hipStreamSynchronize(x->st), "max");
     }
     const float pmax = xnorm_max(x);
     // Error of the accumulator |c|^2 - 2 x.c (point x, centroid c):
@@ -1584,6 +1558,55 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     const double gam = (3.0 * d + 4.0) * u;
     const double pc = (double)pmax * std::sqrt((double)cmax);
     const float bound = (float)(1.25 * (2.0 * r * pc + gam * ((double)cmax + 2.0 * pc)) + 1e-6);
+    // On the row-shared scan each lane appends every value below its running
+    // minimum + 2.5 bound to its list (the pick re-scores those within 2 bound
+    // of the smallest and proves the rest worse with the other half bound);
+    // VS_KMIN=0: per-lane register top-m pairs instead (the pick bounds the
+    // rest by each lane's m-th).
+    if (coarse && plan.kind == 3) {
+        if (env_int("VS_KMIN", 1) != 0) {
+            plan.share_kmin = 1;
+            plan.kmin_margin = 2.5f * bound;
+        } else {
+            plan.share_topm = vs::share_topm();
+            plan.share_ids = 1;
+        }
+    }
+    if ((rc = scan_fits(plan, pq))) return rc;
+    const size_t nlists = (size_t)plan.nqblk * plan.nsplit * plan.lw * plan.bn;
+    const size_t nlist = nlists * plan.cap;
+    VS_HIP(x->cand_v.ensure(nlist * 4), "candidate lists");
+    VS_HIP(x->cand_i.ensure(nlist * 4), "candidate lists");
+    VS_HIP(x->lcnt.ensure((nlists + 1) * 4), "list counts");
+    VS_HIP(hipMemsetAsync(x->lcnt.as<int32_t>() + nlists, 0, 4, x->st), "list counts");
+    VS_HIP(x->gthr.ensure((size_t)pq.nq_pad * 4), "shared thresholds");
+    VS_HIP(hipMemsetD32Async((hipDeviceptr_t)x->gthr.p, (int)vs::kGthrInit, (size_t)pq.nq_pad, x->st),
+           "shared thresholds");
+    // the one-pass selection multiplies the bf16 rounding of the centroids:
+    // the row-shared scan reads a bf16 copy of them (half the bytes of the
+    // fp32 rows it would round itself) with the fp32 rows' norms
+    const void *scan_rows = x->km_cen.p;
+    int scan_storage = 0;
+    if (plan.kind == 3 && plan.share_kmin && plan.tile_st == vs::kSelectCoarse && plan.nks == 8 &&
+        env_int("VS_KM16", 1) != 0) {
+        VS_HIP(x->km_cen16.ensure((size_t)(K + kRowSlack) * ld * 2), "centroid copy");
+        VS_HIP(x->km_c16n.ensure((size_t)(K + kRowSlack) * 4), "centroid copy");
+        VS_HIP(hipMemsetAsync(x->km_cen16.p, 0, (size_t)(K + kRowSlack) * ld * 2, x->st), "clear");
+        VS_HIP(vs::launch_store_rows(x->km_cen.p, 0, ld, K, ld, x->km_cen16.p, 1, ld,
+                                     x->km_c16n.as<float>(), x->flags.as<uint32_t>(), x->st),
+               "centroid copy");
+        plan.tile_st = 1;
+        scan_rows = x->km_cen16.p;
+        scan_storage = 1;
+    }
+    note_scan_kind(x, plan);
+    {
+        ProfScope ps(x, "assign");
+        VS_HIP(vs::launch_scan_topk(scan_rows, scan_storage, ld, x->km_cxn.as<float>(), K, 0, pq, plan,
+                                    x->cand_v.as<float>(), x->cand_i.as<int32_t>(),
+                                    x->gthr.as<uint32_t>(), nullptr, x->lcnt.as<int32_t>(), x->st),
+               "assign scan");
+    }
 
     VS_HIP(x->km_assign.ensure((size_t)n * 4), "assignments");
     VS_HIP(x->km_best.ensure((size_t)n * 8), "distances");
@@ -1598,7 +1621,8 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
                                       x->cand_v.as<float>(), x->cand_i.as<int32_t>(),
                                       x->gthr.as<uint32_t>(), plan, bound,
                                       pq.qf, x->km_assign.as<int32_t>(), x->km_best.as<double>(),
-                                      fb_count, fb_list, x->flags.as<uint32_t>(), x->st),
+                                      fb_count, fb_list, x->flags.as<uint32_t>(),
+                                      x->lcnt.as<int32_t>(), x->st),
                "assign pick");
     }
     int32_t nfb = 0;

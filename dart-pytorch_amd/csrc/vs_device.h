@@ -74,6 +74,8 @@ struct ScanKArgs {
     int32_t *out_q, *out_i;
     unsigned long long *count;
     int64_t out_cap;
+    float kmin_margin;   // row-shared scan, k-means lists: each lane appends the values below
+                         // its running minimum plus this margin
 };
 
 // Order-preserving map of finite floats to uint32 (a < b  <=>  enc(a) < enc(b)),

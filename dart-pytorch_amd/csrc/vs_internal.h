@@ -102,6 +102,10 @@ struct ScanPlan {
     int share_topm = 0;   // row-shared scan: >0 keeps per-lane register top-m values (sample
                           // estimates; lists get 4 * m values per query and workgroup, ids 0)
     int share_ids = 0;    // with share_topm: the ids too, lane g's m pairs at slots [g m, g m + m)
+    int share_kmin = 0;   // row-shared scan: k-means lists (each lane appends what lies below its
+                          // running minimum + kmin_margin; a list that would fill is marked
+                          // full, count cap + 1, and takes no more)
+    float kmin_margin = 0.f;
     int64_t nqblk = 0;    // query blocks
     int64_t nsplit = 0;   // database splits
     int64_t rows_per_split = 0;
@@ -187,7 +191,7 @@ hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, 
                               const uint32_t *gthr, const ScanPlan &plan, float bound,
                               const float *qf, int32_t *assign,
                               double *best_sq, int32_t *fallback_count, int32_t *fallback_list,
-                              uint32_t *flags, hipStream_t st);
+                              uint32_t *flags, const int32_t *list_cnt, hipStream_t st);
 
 hipError_t launch_kmeans_count(const int32_t *assign, int64_t n, int32_t *counts, hipStream_t st);
 hipError_t launch_exclusive_scan_i32(const int32_t *in, int64_t n, int32_t *out, hipStream_t st);

@@ -621,6 +621,7 @@ hipError_t launch_scan_topk(const void *xb, int storage, int64_t ld, const float
     a.kk_final = plan.kk_final;
     a.publish_block = 4 * plan.kk >= plan.kk_final;
     a.lbound = plan.kk < plan.kk_final ? lbound : nullptr;
+    a.kmin_margin = plan.kmin_margin;
     return launch_scan_mode<0>(storage, pq, plan, a, st);
 }
 
@@ -738,6 +739,7 @@ struct MergeKArgs {
     int seg_m;            // k-means pick: lists are 4 sorted segments of seg_m pairs, one per
                           // scan lane; rows a lane dropped are >= its segment's last value
     int seed_rank;        // MODE 2: rank whose value sets the threshold (0: kk)
+    float kmin_margin;    // k-means pick over the row-shared scan's k-means lists
     int64_t k;
     float *D;
     int32_t *I;
@@ -998,7 +1000,7 @@ hipError_t launch_merge_refine(const void *xb, int storage, int64_t ld, int64_t 
 template <int KK>
 __global__ void kmeans_pick_kernel(MergeKArgs a);
 __global__ void kmeans_pick_seg_kernel(MergeKArgs a);
-template <int E, int CH>
+template <int E, int CH, bool LISTS>
 __global__ void kmeans_pick_wave_kernel(MergeKArgs a);
 
 // Threshold estimates from a pre-pass (seed_rank <= 64): one wave per query.
@@ -1103,7 +1105,7 @@ hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, 
                               const uint32_t *gthr, const ScanPlan &plan, float bound,
                               const float *qf, int32_t *assign,
                               double *best_sq, int32_t *fallback_count, int32_t *fallback_list,
-                              uint32_t *flags, hipStream_t st) {
+                              uint32_t *flags, const int32_t *list_cnt, hipStream_t st) {
     if (n <= 0) return hipSuccess;
     MergeKArgs a{};
     a.xb = cen;
@@ -1129,6 +1131,17 @@ hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, 
     a.best_sq = best_sq;
     a.fb_count = fallback_count;
     a.fb_list = fallback_list;
+    if (plan.kind == 3 && plan.share_kmin) {
+        // count-terminated k-means lists of the row-shared scan
+        if (!list_cnt || ld % 16 || plan.share_topm || !(plan.kmin_margin > 0.f))
+            return hipErrorInvalidValue;
+        a.list_cnt = list_cnt;
+        a.kmin_margin = plan.kmin_margin;
+        a.kl = plan.cap;
+        kmeans_pick_wave_kernel<32, 16, true>
+            <<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(a);
+        return hipGetLastError();
+    }
     if (plan.kind == 3) {
         // per-lane register shortlists of the row-shared scan: 4 segments of
         // m pairs per list
@@ -1138,7 +1151,7 @@ hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, 
         a.kl = 4 * plan.share_topm;
         a.seg_m = plan.share_topm;
         if (ld % 16 == 0 && pick_wave_enabled())
-            kmeans_pick_wave_kernel<32, 16><<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(a);
+            kmeans_pick_wave_kernel<32, 16, false><<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(a);
         else
             kmeans_pick_seg_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(a);
         return hipGetLastError();
@@ -1350,8 +1363,14 @@ __global__ __launch_bounds__(256) void kmeans_pick_seg_kernel(MergeKArgs a) {
 // row piece) into LDS laid out dimension-major, and every lane continues its
 // own fp64 sums in dimension order -- the order, and so the rounding, of
 // the one-lane-per-point kernel above.
+//
+// LISTS: the scan's k-means lists instead of segments (count-terminated;
+// every lane appended what lay below its running minimum + kmin_margin, so
+// every centroid outside the lists has an accumulator at or above vmin +
+// kmin_margin, rounded as the scan rounds it; a list marked full, count cap
+// + 1, sends its point to the exhaustive kernel).
 // ---------------------------------------------------------------------------
-template <int E, int CH>
+template <int E, int CH, bool LISTS>
 __global__ __launch_bounds__(256) void kmeans_pick_wave_kernel(MergeKArgs a) {
     constexpr int RS = 65;  // LDS words per staged dimension (64 rows + 1: no bank conflicts on reads)
     constexpr int PIECES = CH / 4;            // 16-byte pieces per row chunk
@@ -1375,21 +1394,42 @@ __global__ __launch_bounds__(256) void kmeans_pick_wave_kernel(MergeKArgs a) {
         return (((qblk * a.nsplit + split) * a.lw + w) * a.bn + q) * a.cap;
     };
     float vmin = VS_INF, seg_bound = VS_INF;
+    bool over = false;
+    auto list_len = [&](int64_t l) -> int {
+        if constexpr (LISTS) {
+            const int64_t split = l / a.lw, w = l % a.lw;
+            const int c = a.list_cnt[((qblk * a.nsplit + split) * a.lw + w) * a.bn + q];
+            return c > a.cap ? 0 : c;
+        } else {
+            return a.kl;
+        }
+    };
     for (int64_t l = 0; l < nlists; ++l) {
         const int64_t off = list_off(l);
-        for (int sgi = 0; sgi < 4; ++sgi) {
-            const float head = a.cand_v[off + sgi * a.seg_m];
-            const int hid = a.cand_i[off + sgi * a.seg_m];
-            if (hid >= 0) vmin = fminf(vmin, head);
-            seg_bound = fminf(seg_bound, a.cand_v[off + sgi * a.seg_m + a.seg_m - 1]);
+        if constexpr (LISTS) {
+            const int64_t split = l / a.lw, w = l % a.lw;
+            if (a.list_cnt[((qblk * a.nsplit + split) * a.lw + w) * a.bn + q] > a.cap) over = true;
+            const int lc = list_len(l);
+            for (int e = 0; e < lc; ++e)
+                if (a.cand_i[off + e] >= 0) vmin = fminf(vmin, a.cand_v[off + e]);
+        } else {
+            for (int sgi = 0; sgi < 4; ++sgi) {
+                const float head = a.cand_v[off + sgi * a.seg_m];
+                const int hid = a.cand_i[off + sgi * a.seg_m];
+                if (hid >= 0) vmin = fminf(vmin, head);
+                seg_bound = fminf(seg_bound, a.cand_v[off + sgi * a.seg_m + a.seg_m - 1]);
+            }
         }
     }
+    // every centroid outside the lists: accumulator >= vmin + margin (the
+    // scan's fp32 sum, monotone in vmin)
+    if constexpr (LISTS) seg_bound = vmin + a.kmin_margin;
     const float lim = vmin + 2.0f * a.bound;
     int ne = 0;
-    bool over = false;
     for (int64_t l = 0; l < nlists; ++l) {
         const int64_t off = list_off(l);
-        for (int e = 0; e < a.kl; ++e) {
+        const int lc = list_len(l);
+        for (int e = 0; e < lc; ++e) {
             const int id = a.cand_i[off + e];
             if (id < 0 || a.cand_v[off + e] > lim) continue;
             if ((int64_t)id >= a.nrows) {

@@ -164,11 +164,19 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
             gt[qb] = __hip_atomic_load(&a.gthr[q0 + qw + qb * 16 + r16], __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
     };
-    gthr_load();
+    // MODE 4 (k-means lists) keeps its thresholds to itself: each lane
+    // appends what lies below its own running minimum + kmin_margin
+    constexpr bool KMIN = MODE == 4;
+    float best_r[KMIN ? NQB : 1];
 #pragma unroll
-    for (int qb = 0; qb < NQB; ++qb) thr_r[qb] = fminf(thr_r[qb], dec_order(gt[qb]));
+    for (int qb = 0; qb < (KMIN ? NQB : 1); ++qb) best_r[qb] = VS_INF;
+    if constexpr (!KMIN) {
+        gthr_load();
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) thr_r[qb] = fminf(thr_r[qb], dec_order(gt[qb]));
+    }
 
-    constexpr bool TOPMODE = MODE >= 2;
+    constexpr bool TOPMODE = MODE == 2 || MODE == 3;
     float top[TOPMODE ? NQB : 1][TOPM];
     int topi[MODE == 3 ? NQB : 1][TOPM];
 #pragma unroll
@@ -184,7 +192,7 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
     for (int64_t t0 = r0; t0 < r1; t0 += TR) {
         const int64_t tn = t0 + TR;
         const bool more = tn < r1;
-        gthr_load();
+        if constexpr (!KMIN) gthr_load();
         if (more) gload(tn);
         const uint16_t *As = (const uint16_t *)(smem + par * S::STAGE_BYTES);
         const float *Ns = (const float *)(As + TR * KP);
@@ -256,6 +264,22 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
             }
 
             // ---- epilogue of the 16-row block ----
+            if constexpr (KMIN) {
+                // the running minimum of the query over its four lanes (rows
+                // 4g .. 4g + 3 of every block): two cross-row swaps
+#pragma unroll
+                for (int qb = 0; qb < NQB; ++qb) {
+                    float m = fminf(fminf(acc[qb][0], acc[qb][1]), fminf(acc[qb][2], acc[qb][3]));
+                    const uint32_t mu = __float_as_uint(m);
+                    const auto s1 = __builtin_amdgcn_permlane16_swap(mu, mu, false, false);
+                    m = fminf(__uint_as_float(s1[0]), __uint_as_float(s1[1]));
+                    const uint32_t pu = __float_as_uint(m);
+                    const auto s2 = __builtin_amdgcn_permlane32_swap(pu, pu, false, false);
+                    m = fminf(__uint_as_float(s2[0]), __uint_as_float(s2[1]));
+                    best_r[qb] = fminf(best_r[qb], m);
+                    thr_r[qb] = fminf(thr_r[qb], best_r[qb] + a.kmin_margin);
+                }
+            }
             bool pass = false;
 #pragma unroll
             for (int qb = 0; qb < NQB; ++qb) {
@@ -268,7 +292,16 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
                 bool need = false;
 #pragma unroll
                 for (int qb = 0; qb < NQB; ++qb) need |= cnt_r[qb] > a.cap - 16;
-                if (__ballot(need)) {
+                if (KMIN && __ballot(need)) {
+                    // a full list takes no more entries and is marked (count
+                    // cap + 1): its points go to the exhaustive search
+#pragma unroll
+                    for (int qb = 0; qb < NQB; ++qb)
+                        if (cnt_r[qb] > a.cap - 16) {
+                            cnt_r[qb] = a.cap + 1;
+                            thr_r[qb] = -VS_INF;
+                        }
+                } else if (__ballot(need)) {
                     if (g == 0) {
 #pragma unroll
                         for (int qb = 0; qb < NQB; ++qb) cnt_w[qb * 16 + r16] = cnt_r[qb];
@@ -338,8 +371,10 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
             if (rb + 1 < RT) mma(rb + 1, accs[(rb + 1) & 1]);
             epi(rb, accs[rb & 1]);
         }
+        if constexpr (!KMIN) {
 #pragma unroll
-        for (int qb = 0; qb < NQB; ++qb) thr_r[qb] = fminf(thr_r[qb], dec_order(gt[qb]));
+            for (int qb = 0; qb < NQB; ++qb) thr_r[qb] = fminf(thr_r[qb], dec_order(gt[qb]));
+        }
         // the other stage was last read before the previous barrier
         if (more) lstore(smem + (par ^ 1) * S::STAGE_BYTES);
         __syncthreads();
@@ -401,15 +436,27 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
     }
 }
 
+// mode 4 (the k-means assign) is built for the one-pass selection: fp32
+// rows (storage 2), or for 256-element rows their bf16 copy (storage 1, the
+// tile shape of storage 2)
+template <int ST, int NKS, int NQB, int RT>
+static void (*share_kmin_kernel())(ScanKArgs) {
+    if constexpr (ST == 2 || (NKS == 8 && RT == 2))
+        return share_scan_kernel<ST, NKS, NQB, RT, 4>;
+    else
+        return nullptr;
+}
+
 // The built shapes: X(storage, K-steps, 16-query blocks per wave, 16-row
 // blocks per tile).
-#define VS_SHARE_SHAPES(X) X(1, 4, 4, 4) X(1, 8, 2, 4) X(2, 4, 4, 2) X(2, 8, 2, 2)
+#define VS_SHARE_SHAPES(X) X(1, 4, 4, 4) X(1, 8, 2, 4) X(2, 4, 4, 2) X(2, 8, 2, 2) X(1, 8, 2, 2)
 
 // mode: 0 lists, 2 top-m values, 3 top-m values and ids
 static void (*share_kernel(int st, int nks, int bn, int rt, int64_t ld, int mode))(ScanKArgs) {
 #define VS_SHARE_PICK(ST_, NKS_, NQB_, RT_)                                                     \
     if (st == ST_ && nks == NKS_ && bn == 64 * NQB_ && rt == RT_ && ld == 32 * NKS_)              \
-        return mode == 3   ? share_scan_kernel<ST_, NKS_, NQB_, RT_, 3>                           \
+        return mode == 4   ? share_kmin_kernel<ST_, NKS_, NQB_, RT_>()                             \
+               : mode == 3 ? share_scan_kernel<ST_, NKS_, NQB_, RT_, 3>                           \
                : mode == 2 ? share_scan_kernel<ST_, NKS_, NQB_, RT_, 2>                           \
                            : share_scan_kernel<ST_, NKS_, NQB_, RT_, 0>;
     VS_SHARE_SHAPES(VS_SHARE_PICK)
@@ -439,7 +486,8 @@ hipError_t launch_share_scan(const ScanPlan &plan, const ScanKArgs &args, hipStr
         return hipErrorInvalidValue;
     const int64_t total = plan.nqblk * plan.nsplit;
     const int64_t grid = ((total + 7) / 8) * 8;
-    const int mode = !plan.share_topm ? 0 : plan.share_ids ? 3 : 2;
+    if (plan.share_kmin && (plan.share_topm || !(plan.kmin_margin > 0.f))) return hipErrorInvalidValue;
+    const int mode = plan.share_kmin ? 4 : !plan.share_topm ? 0 : plan.share_ids ? 3 : 2;
     void (*fn)(ScanKArgs) =
         share_kernel(plan.tile_st, plan.nks, plan.bn, plan.tm, args.ld, mode);
     if (!fn) return hipErrorInvalidValue;

@@ -111,26 +111,55 @@ def _kmeans_check(vs, x, cen, min_points=1, seed=0, expect_fallback=False):
     return a
 
 
+@pytest.mark.parametrize("kmin", ["1", "0"])
 @pytest.mark.parametrize("n,d,ncomp,K", [(30_000, 256, 1024, 4096), (9_000, 100, 64, 500),
                                          (3_000, 256, 8, 20)])
-def test_kmeans_register_shortlists(vs, n, d, ncomp, K):
+def test_kmeans_register_shortlists(vs, monkeypatch, n, d, ncomp, K, kmin):
     """k-means assign on the row-shared scan (fp32 points and centroids,
-    one-pass bf16 selection): each scan lane keeps its 8 smallest
-    (accumulator, centroid) pairs in registers, the pick re-scores them in
-    fp64 and proves the argmin with the smallest value any lane dropped.
-    Assignments, objective and centroids equal the oracle's (K = 20: lanes
-    see fewer than 8 centroids each)."""
+    one-pass bf16 selection).  kmin 1 (default): each scan lane appends the
+    values below its running minimum + 2.5 bound to the point's list; the
+    pick re-scores those within 2 bound of the smallest in fp64 and the rest
+    are provably worse.  kmin 0: each lane keeps its 8 smallest (accumulator,
+    centroid) pairs in registers and the pick proves the argmin with the
+    smallest value any lane dropped.  Assignments, objective and centroids
+    equal the oracle's (K = 20: lanes see fewer than 8 centroids each)."""
+    monkeypatch.setenv("VS_KMIN", kmin)
     x, _ = syn.gaussian_mixture(n, d, ncomp, 0.1, 41)
     cen = x[syn.seeded_subset(n, K, 41)].copy()
     _kmeans_check(vs, x, cen)
 
 
-def test_kmeans_register_shortlists_fallback(vs):
-    """Forty copies of one centroid fill every lane's 8 slots for the points
-    near it, so no pick is provable and the exhaustive exact scan decides:
-    the lowest index among the copies loses to the original (kmeans.dart:93-101)."""
+@pytest.mark.parametrize("kmin", ["1", "0"])
+def test_kmeans_register_shortlists_fallback(vs, monkeypatch, kmin):
+    """Forty copies of one centroid: more candidates within 2 bound of the
+    smallest than the pick's 32 slots (kmin 1), or every lane's 8 slots
+    full (kmin 0), so the exhaustive exact scan decides those points: the
+    lowest index among the copies loses to the original (kmeans.dart:93-101)."""
+    monkeypatch.setenv("VS_KMIN", kmin)
     x, _ = syn.gaussian_mixture(6000, 256, 16, 0.1, 5)
     cen = x[syn.seeded_subset(len(x), 300, 5)].copy()
     cen[100:140] = cen[3]
     a = _kmeans_check(vs, x, cen, expect_fallback=True)
     assert not np.any((a >= 100) & (a < 140))
+
+
+def test_kmeans_lists_full(vs, monkeypatch):
+    """Three hundred copies of one centroid overflow the points' k-means
+    lists (more than cap - 16 appends): the lists are marked full and their
+    points go to the exhaustive exact scan, whose argmin is the oracle's."""
+    monkeypatch.setenv("VS_KMIN", "1")
+    x, _ = syn.gaussian_mixture(4000, 256, 8, 0.1, 6)
+    cen = x[syn.seeded_subset(len(x), 700, 6)].copy()
+    cen[200:500] = cen[7]
+    a = _kmeans_check(vs, x, cen, expect_fallback=True)
+    assert not np.any((a >= 200) & (a < 500))
+
+
+def test_kmeans_lists_fp32_rows(vs, monkeypatch):
+    """The k-means lists over the fp32 centroid rows rounded in the scan
+    (VS_KM16=0) instead of their bf16 copy: the same assignments."""
+    monkeypatch.setenv("VS_KMIN", "1")
+    monkeypatch.setenv("VS_KM16", "0")
+    x, _ = syn.gaussian_mixture(30_000, 256, 1024, 0.1, 44)
+    cen = x[syn.seeded_subset(30_000, 4096, 44)].copy()
+    _kmeans_check(vs, x, cen)
