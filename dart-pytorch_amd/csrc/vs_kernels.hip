@@ -1409,9 +1409,16 @@ __global__ __launch_bounds__(256) void kmeans_pick_wave_kernel(MergeKArgs a) {
         if constexpr (LISTS) {
             const int64_t split = l / a.lw, w = l % a.lw;
             if (a.list_cnt[((qblk * a.nsplit + split) * a.lw + w) * a.bn + q] > a.cap) over = true;
+            // every appended entry has a real id; 16-byte reads (lists hold
+            // a multiple of 4 slots)
             const int lc = list_len(l);
-            for (int e = 0; e < lc; ++e)
-                if (a.cand_i[off + e] >= 0) vmin = fminf(vmin, a.cand_v[off + e]);
+            for (int e = 0; e < lc; e += 4) {
+                const float4 v4 = *(const float4 *)(a.cand_v + off + e);
+                vmin = fminf(vmin, v4.x);
+                if (e + 1 < lc) vmin = fminf(vmin, v4.y);
+                if (e + 2 < lc) vmin = fminf(vmin, v4.z);
+                if (e + 3 < lc) vmin = fminf(vmin, v4.w);
+            }
         } else {
             for (int sgi = 0; sgi < 4; ++sgi) {
                 const float head = a.cand_v[off + sgi * a.seg_m];
@@ -1430,8 +1437,18 @@ __global__ __launch_bounds__(256) void kmeans_pick_wave_kernel(MergeKArgs a) {
         const int64_t off = list_off(l);
         const int lc = list_len(l);
         for (int e = 0; e < lc; ++e) {
+            if constexpr (LISTS) {  // values four at a time; ids of the candidates only
+                if ((e & 3) == 0) {
+                    const float4 v4 = *(const float4 *)(a.cand_v + off + e);
+                    if (!(v4.x <= lim || v4.y <= lim || v4.z <= lim || v4.w <= lim)) {
+                        e += 3;
+                        continue;
+                    }
+                }
+            }
+            if (a.cand_v[off + e] > lim) continue;
             const int id = a.cand_i[off + e];
-            if (id < 0 || a.cand_v[off + e] > lim) continue;
+            if (id < 0) continue;
             if ((int64_t)id >= a.nrows) {
                 atomicOr(a.flags, kFlagBadId);
                 continue;
