@@ -46,10 +46,10 @@ MEASURED_TRAFFIC = {
 
 def mfma_passes(idx):
     """bf16 MFMA passes per distance of an fp32-row scan: 1 when the one-pass
-    bf16 selection ran (GEMM shapes of storage code 2, or the row-shared scan,
-    which reads fp32 rows only that way), else 3 (hi*q0 + lo*q0 + hi*q1 of the
-    split-bf16 planes)."""
-    coarse = sum(idx.prof_get(f"gemm:2,1,2,{wq},4,2,32")[0] for wq in (2, 4))
+    bf16 selection ran (GEMM shapes of storage code 2, or 1 on the bf16 copy
+    of the rows, or the row-shared scan, which reads fp32 rows only that
+    way), else 3 (hi*q0 + lo*q0 + hi*q1 of the split-bf16 planes)."""
+    coarse = sum(idx.prof_get(f"gemm:{st},1,2,{wq},4,2,32")[0] for st in (1, 2) for wq in (2, 4))
     coarse += idx.prof_get("shared")[0]
     return 1 if coarse else 3
 

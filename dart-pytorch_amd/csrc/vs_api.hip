@@ -166,6 +166,10 @@ struct vs_index {
     vs::PreparedQueries km_pq;
     uint32_t km_pflags = 0;
     uint64_t km_prep_version = ~0ull;
+    // bf16 copy of fp32 rows for the GEMM-tiled one-pass selection (range,
+    // self-join), kept while the rows are unchanged
+    DevBuf xb16, xb16n;
+    uint64_t xb16_version = ~0ull;
     int64_t km_iota_n = -1;  // km_iota holds 0 .. km_iota_n - 1
     bool prof_on = false;
     std::map<std::string, ProfEntry> prof;
@@ -1022,6 +1026,35 @@ int range_core(vs_index *x, const vs::PreparedQueries &pq, double radius, int se
         if (rc) return rc;
     }
     if ((rc = scan_fits(plan, pq))) return rc;
+    // the one-pass selection multiplies the rows' bf16 rounding: it reads a
+    // bf16 copy of them (half the bytes, no conversion in the kernel) with
+    // the fp32 rows' norms, when the copy fits in memory
+    const void *scan_rows = x->xb;
+    int scan_storage = x->storage;
+    if (coarse && plan.tile_st == vs::kSelectCoarse && env_int("VS_COPY16", 1) != 0) {
+        const size_t bytes = (size_t)(x->ntotal + kRowSlack) * x->ld * 2;
+        if (x->xb16_version != x->version) {
+            x->xb16_version = ~0ull;
+            if (x->xb16.ensure(bytes) == hipSuccess &&
+                x->xb16n.ensure((size_t)(x->ntotal + kRowSlack) * 4) == hipSuccess) {
+                VS_HIP(hipMemsetAsync(x->xb16.p, 0, bytes, x->st), "row copy");
+                VS_HIP(x->flags.ensure(4), "flags");
+                VS_HIP(vs::launch_store_rows(x->xb, 0, x->ld, x->ntotal, x->ld, x->xb16.p, 1, x->ld,
+                                             x->xb16n.as<float>(), x->flags.as<uint32_t>(), x->st),
+                       "row copy");
+                x->xb16_version = x->version;
+            } else {
+                (void)hipGetLastError();
+                x->xb16.release();
+                x->xb16n.release();
+            }
+        }
+        if (x->xb16_version == x->version) {
+            plan.tile_st = 1;
+            scan_rows = x->xb16.p;
+            scan_storage = 1;
+        }
+    }
     const float xmax = xnorm_max(x);
     VS_HIP(x->athr.ensure((size_t)pq.nq * 4), "range bounds");
     const int exact_q = (qflags & vs::kFlagNotBf16) ? 0 : 1;
@@ -1039,7 +1072,7 @@ int range_core(vs_index *x, const vs::PreparedQueries &pq, double radius, int se
         note_scan_kind(x, plan);
         {
             ProfScope ps(x, self_join ? "join" : "range");
-            VS_HIP(vs::launch_scan_range(x->xb, x->storage, x->ld, x->xn, x->ntotal, pq, plan,
+            VS_HIP(vs::launch_scan_range(scan_rows, scan_storage, x->ld, x->xn, x->ntotal, pq, plan,
                                          x->athr.as<float>(), self_join, x->metric,
                                          x->rq.as<int32_t>(), x->ri.as<int32_t>(),
                                          x->rcount.as<unsigned long long>(), cap, x->st),
@@ -1177,7 +1210,8 @@ void vs_index_destroy(vs_index *x) {
                       &x->misc,    &x->km_cen,    &x->km_cxn,   &x->km_assign, &x->km_best,
                       &x->km_fb,   &x->km_keys,   &x->km_order, &x->km_tmp,   &x->km_counts,
                       &x->km_offsets, &x->km_out, &x->km_iota, &x->lcnt,   &x->km_qp,
-                      &x->km_qf,   &x->km_qnorm,  &x->km_cen16, &x->km_c16n};
+                      &x->km_qf,   &x->km_qnorm,  &x->km_cen16, &x->km_c16n, &x->xb16,
+                      &x->xb16n};
     for (DevBuf *b : bufs) b->release();
     x->km_hbest.release();
     x->km_hassign.release();
