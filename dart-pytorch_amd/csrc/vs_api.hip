@@ -809,9 +809,9 @@ int seed_thresholds(vs_index *x, const vs::PreparedQueries &pq, int64_t S, int64
     // the row-shared scan then keeps each lane's smallest in registers
     // instead of lists (exact unless one lane met more than m of them; then
     // the estimate is larger, never smaller)
-    if (pp.kind == 3 && seed_rank > 0 && seed_rank <= 4 * vs::share_topm() &&
+    if (pp.kind == 3 && seed_rank > 0 && seed_rank <= 4 * vs::share_topm(false) &&
         env_int("VS_GUESS_TOPM", 1))
-        pp.share_topm = vs::share_topm();
+        pp.share_topm = vs::share_topm(false);
     if ((rc = scan_fits(pp, pq))) return rc;
     const int div = std::max(2, env_int("VS_PREPASS_DIV", 32));
     if (pp.kind == 0 && pp.nsplit * pp.lw >= 512 && S >= (1 << 18)) {
@@ -860,7 +860,7 @@ int guess_thresholds(vs_index *x, const vs::PreparedQueries &pq, int64_t kk_fina
     const int j = (int)std::ceil(lam + 4.0 * std::sqrt(lam) + 4.0);
     const int64_t kkp = std::max<int64_t>(8, next_pow2(j));
     x->prof["guess_scans"].launches++;
-    return seed_thresholds(x, pq, S, kkp, min_list_elems, j, env_int("VS_GUESS_LISTS", 8));
+    return seed_thresholds(x, pq, S, kkp, min_list_elems, j, env_int("VS_GUESS_LISTS", 12));
 }
 
 int search_device(vs_index *x, const void *q_dev, int q_dtype, int64_t nq, int64_t k, float *D,
@@ -1602,7 +1602,7 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
             plan.share_kmin = 1;
             plan.kmin_margin = 2.5f * bound;
         } else {
-            plan.share_topm = vs::share_topm();
+            plan.share_topm = vs::share_topm(true);
             plan.share_ids = 1;
         }
     }

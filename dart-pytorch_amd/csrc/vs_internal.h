@@ -270,7 +270,7 @@ size_t share_lds_bytes(int nks, int nqb, int rt, int cap);
 // lists, 2 top-m values, 3 top-m values and ids).
 int share_blocks_per_cu(int st, int nks, int bn, int rt, int64_t ld, size_t lds, int mode);
 // m of the row-shared scan's register top-m variant.
-int share_topm();
+int share_topm(bool ids);  // slots per lane: with ids (k-means) or values only (estimates)
 
 struct ScanKArgs;
 hipError_t launch_share_scan(const ScanPlan &plan, const ScanKArgs &args, hipStream_t st);

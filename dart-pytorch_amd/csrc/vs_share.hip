@@ -67,12 +67,14 @@ size_t share_lds_bytes(int nks, int nqb, int rt, int cap) {
 // same with the row ids; lane g's TOPM pairs fill slots [g TOPM, (g + 1)
 // TOPM) of the query's list, sorted, so every row the lane dropped is at or
 // above the last of its slots.
-constexpr int kShareTopM = 8;
+constexpr int kShareTopM = 8;    // MODE 3
+constexpr int kShareTopMEst = 4; // MODE 2: the estimate needs the 16 smallest of a sample
+                                 // spread over many lanes; fewer slots, cheaper insertions
 
 template <int ST, int NKS, int NQB, int RT, int MODE>
 __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
     using S = ShareShape<ST, NKS, NQB, RT>;
-    constexpr int TOPM = kShareTopM;
+    constexpr int TOPM = MODE == 2 ? kShareTopMEst : kShareTopM;
     constexpr int TR = S::TR, KP = S::KP, BNW = S::BNW;
     extern __shared__ __align__(16) char smem[];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r16 = lane & 15, g = lane >> 4;
@@ -464,7 +466,7 @@ static void (*share_kernel(int st, int nks, int bn, int rt, int64_t ld, int mode
     return nullptr;
 }
 
-int share_topm() { return kShareTopM; }
+int share_topm(bool ids) { return ids ? kShareTopM : kShareTopMEst; }
 
 // Workgroups of the shape that one CU holds at once (registers and LDS).
 int share_blocks_per_cu(int st, int nks, int bn, int rt, int64_t ld, size_t lds, int mode) {
@@ -482,7 +484,8 @@ int share_blocks_per_cu(int st, int nks, int bn, int rt, int64_t ld, size_t lds,
 hipError_t launch_share_scan(const ScanPlan &plan, const ScanKArgs &args, hipStream_t st) {
     if (plan.kk != plan.kk_final || plan.cap < plan.kk + 16 || plan.lw != 1 || !args.list_cnt)
         return hipErrorInvalidValue;
-    if (plan.share_topm && (plan.share_topm != kShareTopM || plan.cap < 4 * kShareTopM))
+    if (plan.share_topm && (plan.share_topm != share_topm(plan.share_ids != 0) ||
+                            plan.cap < 4 * plan.share_topm))
         return hipErrorInvalidValue;
     const int64_t total = plan.nqblk * plan.nsplit;
     const int64_t grid = ((total + 7) / 8) * 8;
