@@ -257,7 +257,13 @@ def test_gemm_large_k_unseeded(vs):
     assert_knn_parity(D, I, Dr, Ir, 0, rtol=0.0, atol=0.0, xb=xb, xq=xq)
 
 
-COARSE_KEY = "gemm:2,1,2,4,4,2,32"  # one-pass selection shape (storage code 2)
+# one-pass selection shapes: fp32 rows rounded in the kernel (storage code 2)
+# or their bf16 copy (storage code 1, range search and self-join)
+COARSE_KEYS = ("gemm:2,1,2,4,4,2,32", "gemm:1,1,2,4,4,2,32")
+
+
+def _one_pass_runs(g):
+    return sum(g.prof_get(k)[0] for k in COARSE_KEYS)
 
 
 @pytest.mark.parametrize("coarse", [1, 0])
@@ -271,7 +277,7 @@ def test_coarse_self_join(vs, monkeypatch, coarse):
     g = vs.GpuIndexFlat(512, vs.Metric(1), storage="f32")
     g.add(x)
     i, j, s = g.self_join(0.95)
-    n1, _ = g.prof_get(COARSE_KEY)
+    n1 = _one_pass_runs(g)
     gemm, _ = g.prof_get("gemm")
     g.close()
     assert gemm >= 1 and (n1 >= 1) == bool(coarse)
@@ -294,7 +300,7 @@ def test_coarse_kmeans(vs, monkeypatch, coarse):
     pts.add(x)
     u = syn.rng(78, 0).random(4096 * 256)
     a, newc, cnt, obj = vs.kmeans_step(pts, cen, 1, u)
-    n1, _ = pts.prof_get(COARSE_KEY)
+    n1 = _one_pass_runs(pts)
     pts.close()
     assert (n1 >= 1) == bool(coarse)
     ar, _, objr = oracle.kmeans_assign(x, cen, NT)
@@ -316,7 +322,7 @@ def test_coarse_range_search(vs, monkeypatch, metric):
     g = vs.GpuIndexFlat(256, vs.Metric(metric), storage="f32")
     g.add(xb)
     rr = g.range_search(xq, radius)
-    n1, _ = g.prof_get(COARSE_KEY)
+    n1 = _one_pass_runs(g)
     g.close()
     assert n1 >= 1
     lims, D, I = oracle.flat_range_search(xb, xq, radius, metric, NT)
