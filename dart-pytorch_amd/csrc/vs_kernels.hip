@@ -758,7 +758,114 @@ struct MergeKArgs {
     int32_t *fb_list;
 };
 
-constexpr int kMergeBuf = 4096;
+constexpr int kMergeBuf = 2048;
+constexpr int kMergeKeepMax = 512;  // kk_final of this build is at most 512
+
+// Block-wide radix selection (256 threads) among the entries t in [0, n)
+// that satisfy pred(t): the rank-th smallest key(t) (rank >= 1), found 8
+// bits at a time from the top with per-wave histograms in LDS.  Returns the
+// key and, in *rank_out, its rank among the entries with exactly that key.
+struct SelScratch {
+    int hist[4][256];
+    int bin, below, n_lt, n_eq;
+};
+
+template <typename KeyF, typename PredF>
+__device__ uint32_t radix_select_block(int n, int rank, KeyF key, PredF pred, SelScratch &ss,
+                                       int *rank_out) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    uint32_t prefix = 0, mask = 0;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        for (int t = tid; t < 4 * 256; t += 256) (&ss.hist[0][0])[t] = 0;
+        __syncthreads();
+        for (int t = tid; t < n; t += 256) {
+            if (!pred(t)) continue;
+            const uint32_t k = key(t);
+            if ((k & mask) == prefix) atomicAdd(&ss.hist[wave][(k >> shift) & 255], 1);
+        }
+        __syncthreads();
+        if (wave == 0) {  // lane owns bins 4 lane .. 4 lane + 3
+            int c[4], s = 0;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int b = 4 * lane + u;
+                c[u] = ss.hist[0][b] + ss.hist[1][b] + ss.hist[2][b] + ss.hist[3][b];
+                s += c[u];
+            }
+            int inc = s;
+            for (int o = 1; o < 64; o <<= 1) {
+                const int y = __shfl_up(inc, o);
+                if (lane >= o) inc += y;
+            }
+            int cum = inc - s;
+            if (cum < rank && rank <= inc) {  // one lane holds the bin of the rank-th key
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    if (cum + c[u] >= rank) {
+                        ss.bin = 4 * lane + u;
+                        ss.below = cum;
+                        break;
+                    }
+                    cum += c[u];
+                }
+            }
+        }
+        __syncthreads();
+        rank -= ss.below;
+        prefix |= (uint32_t)ss.bin << shift;
+        mask |= 0xFFu << shift;
+    }
+    *rank_out = rank;
+    return prefix;
+}
+
+// The kk smallest (v, id) pairs of sv/si[0, n), n >= kk, in (v, id) order
+// -- v finite or +inf, real ids distinct, sentinels (+inf, INT_MAX) --
+// move to slots [0, kk) in no particular order; the largest of them is
+// returned in (*kth_v, *kth_i).  Selection on the order-preserving code of
+// v, then on the ids of the pairs tied at that code.
+__device__ void select_block(float *sv, int *si, int n, int kk, float *tmp_v, int *tmp_i,
+                             SelScratch &ss, float *kth_v, int *kth_i) {
+    const int tid = threadIdx.x;
+    int need = 0, unused = 0;
+    const uint32_t T = radix_select_block(
+        n, kk, [&](int t) { return enc_order(sv[t]); }, [](int) { return true; }, ss, &need);
+    const uint32_t I = radix_select_block(
+        n, need, [&](int t) { return (uint32_t)si[t]; },
+        [&](int t) { return enc_order(sv[t]) == T; }, ss, &unused);
+    // kk - need pairs lie strictly below the pivot code and take slots
+    // [0, kk - need); the tied ones take the rest, at most need of them (equal
+    // sentinels can tie beyond need)
+    if (tid == 0) {
+        ss.n_lt = 0;
+        ss.n_eq = 0;
+    }
+    __syncthreads();
+    for (int t = tid; t < n; t += 256) {
+        const uint32_t c = enc_order(sv[t]);
+        int p = -1;
+        if (c < T) {
+            p = atomicAdd(&ss.n_lt, 1);
+        } else if (c == T && (uint32_t)si[t] <= I) {
+            const int q = atomicAdd(&ss.n_eq, 1);
+            if (q < need) p = kk - need + q;
+        }
+        if (p >= 0) {
+            tmp_v[p] = sv[t];
+            tmp_i[p] = si[t];
+        }
+    }
+    __syncthreads();
+    for (int t = tid; t < kk; t += 256) {
+        sv[t] = tmp_v[t];
+        si[t] = tmp_i[t];
+    }
+    if (tid == 0) {
+        *kth_v = dec_order(T);
+        *kth_i = (int)I;
+    }
+    __syncthreads();
+}
 
 template <int ST, int MODE>
 __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
@@ -766,6 +873,9 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
     float *bv = (float *)smem;                  // [kMergeBuf]
     int *bi = (int *)(bv + kMergeBuf);          // [kMergeBuf]
     float *qsh = (float *)(bi + kMergeBuf);     // [ld]
+    float *tmp_v = qsh + a.ld;                  // [kMergeKeepMax]
+    int *tmp_i = (int *)(tmp_v + kMergeKeepMax);  // [kMergeKeepMax]
+    __shared__ SelScratch sel;
     __shared__ int s_cnt;
     __shared__ float s_thr;
     __shared__ int s_thr_id;
@@ -826,18 +936,23 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
         __syncthreads();
         const int c = s_cnt;
         if (c > kMergeBuf - kk - 1024 || (base + 1024 >= total && c > 0)) {
-            int sz = 1;
-            while (sz < kk + c) sz <<= 1;
-            for (int t = kk + c + tid; t < sz; t += 256) {
-                bv[t] = VS_INF;
-                bi[t] = INT_MAX;
-            }
-            __syncthreads();
-            bitonic_sort_block(bv, bi, sz);
-            if (tid == 0) {
-                s_cnt = 0;
-                s_thr = bv[kk - 1];
-                s_thr_id = bi[kk - 1];
+            if constexpr (MODE == 2) {  // the r-th value is wanted: sorted
+                int sz = 1;
+                while (sz < kk + c) sz <<= 1;
+                for (int t = kk + c + tid; t < sz; t += 256) {
+                    bv[t] = VS_INF;
+                    bi[t] = INT_MAX;
+                }
+                __syncthreads();
+                bitonic_sort_block(bv, bi, sz);
+                if (tid == 0) {
+                    s_cnt = 0;
+                    s_thr = bv[kk - 1];
+                    s_thr_id = bi[kk - 1];
+                }
+            } else {  // the kk best in any order, and the kk-th
+                select_block(bv, bi, kk + c, kk, tmp_v, tmp_i, sel, &s_thr, &s_thr_id);
+                if (tid == 0) s_cnt = 0;
             }
         }
         __syncthreads();
@@ -873,8 +988,9 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
         __syncthreads();
         if (tid == 0) {
             const float m = fminf(fminf(s_lmin[0], s_lmin[1]), fminf(s_lmin[2], s_lmin[3]));
-            const bool short_list = a.guess && bi[kk - 1] == INT_MAX && a.nrows >= kk;
-            if (m < bv[kk - 1] || short_list) a.vf_list[atomicAdd(a.vf_count, 1)] = (int32_t)qg;
+            // (s_thr, s_thr_id): the kk-th kept pair, a sentinel if fewer were found
+            const bool short_list = a.guess && s_thr_id == INT_MAX && a.nrows >= kk;
+            if (m < s_thr || short_list) a.vf_list[atomicAdd(a.vf_count, 1)] = (int32_t)qg;
         }
     }
 
@@ -884,7 +1000,7 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
     double best_ex = __builtin_huge_val();
     int best_id = INT_MAX;
     float a_last = 0.f;
-    if constexpr (MODE == 1) a_last = bv[kk - 1];
+    if constexpr (MODE == 1) a_last = s_thr;
     __syncthreads();
     for (int t = tid; t < kk; t += 256) {
         const int id = bi[t];
@@ -953,7 +1069,9 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
     }
 }
 
-static size_t merge_lds(int64_t ld) { return (size_t)kMergeBuf * 8 + (size_t)ld * 4; }
+static size_t merge_lds(int64_t ld) {
+    return (size_t)kMergeBuf * 8 + (size_t)ld * 4 + (size_t)kMergeKeepMax * 8;
+}
 
 hipError_t launch_merge_refine(const void *xb, int storage, int64_t ld, int64_t d, int metric,
                                const PreparedQueries &pq, const ScanPlan &plan,
