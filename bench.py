@@ -359,6 +359,31 @@ def run_copy_calibration(args):
             "ms": round(dt * 1e3, 4), "GBps_read_plus_write": round(2 * nbytes / dt / 1e9, 1)}
 
 
+def run_library_gemm(args):
+    """For scale only (not the product path): the vendor library's bf16 GEMM
+    through torch (hipBLASLt on ROCm) on the K = 768 shapes of configs[2] at
+    batch 1024 and 8192, output written in bf16, no selection."""
+    import torch
+
+    rows = []
+    for m, n in ((1024, 262_144), (1024, 1_048_576), (8192, 65_536)):
+        a = torch.randn(m, 768, device="cuda", dtype=torch.bfloat16)
+        b = torch.randn(n, 768, device="cuda", dtype=torch.bfloat16)
+        for _ in range(max(args.warmup, 1)):
+            c = a @ b.t()
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for _ in range(args.steps):
+            c = a @ b.t()
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t) / args.steps
+        rows.append({"m": m, "n": n, "k": 768, "ms": round(dt * 1e3, 3),
+                     "tflops": round(2 * m * n * 768 / dt / 1e12, 1)})
+        del a, b, c
+    return {"workload": "libgemm", "note": "library bf16 GEMM for scale, not the product path",
+            "shapes": rows}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -377,6 +402,9 @@ def main():
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the multi-GPU "
               "sharding of this path is a design note, not built.", file=sys.stderr)
         sys.exit(2)
+    if args.workload == "libgemm":  # torch only; the library is not loaded
+        print(json.dumps(run_library_gemm(args)), flush=True)
+        return
     import vector_store as vs
     from vector_store import synthetic as syn
 
