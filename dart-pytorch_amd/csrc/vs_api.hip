@@ -163,6 +163,10 @@ struct vs_index {
     // k-means: pinned copies of the distances, assignments and new centroids
     HostBuf km_hbest, km_hassign, km_hcen;
     hipStream_t st_copy = nullptr;  // k-means: reads results back beside the update
+    // k-means: km_order holds the last step's points grouped by cluster, for
+    // these rows (version) and this many points
+    uint64_t km_order_version = ~0ull;
+    int64_t km_order_n = 0;
     vs::PreparedQueries km_pq;
     uint32_t km_pflags = 0;
     uint64_t km_prep_version = ~0ull;
@@ -1656,7 +1660,12 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
                                       x->gthr.as<uint32_t>(), plan, bound,
                                       pq.qf, x->km_assign.as<int32_t>(), x->km_best.as<double>(),
                                       fb_count, fb_list, x->flags.as<uint32_t>(),
-                                      x->lcnt.as<int32_t>(), x->st),
+                                      x->lcnt.as<int32_t>(),
+                                      x->km_order_version == x->version && x->km_order_n == n &&
+                                              env_int("VS_PICK_ORDER", 1) != 0
+                                          ? x->km_order.as<int32_t>()
+                                          : nullptr,
+                                      x->st),
                "assign pick");
     }
     int32_t nfb = 0;
@@ -1742,6 +1751,8 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
                                  x->km_keys.as<int32_t>(), x->km_iota.as<int32_t>(),
                                  x->km_order.as<int32_t>(), n, key_bits, x->st),
            "grouping points");
+    x->km_order_version = x->version;
+    x->km_order_n = n;
     VS_HIP(x->km_offsets.ensure((size_t)K * 4), "offsets");
     VS_HIP(vs::launch_exclusive_scan_i32(x->km_counts.as<int32_t>(), K,
                                          x->km_offsets.as<int32_t>(), x->st),

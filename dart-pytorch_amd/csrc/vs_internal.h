@@ -191,7 +191,8 @@ hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, 
                               const uint32_t *gthr, const ScanPlan &plan, float bound,
                               const float *qf, int32_t *assign,
                               double *best_sq, int32_t *fallback_count, int32_t *fallback_list,
-                              uint32_t *flags, const int32_t *list_cnt, hipStream_t st);
+                              uint32_t *flags, const int32_t *list_cnt, const int32_t *order,
+                              hipStream_t st);
 
 hipError_t launch_kmeans_count(const int32_t *assign, int64_t n, int32_t *counts, hipStream_t st);
 hipError_t launch_exclusive_scan_i32(const int32_t *in, int64_t n, int32_t *out, hipStream_t st);

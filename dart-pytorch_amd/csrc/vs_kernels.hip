@@ -747,6 +747,7 @@ struct MergeKArgs {
                           // scan lane; rows a lane dropped are >= its segment's last value
     int seed_rank;        // MODE 2: rank whose value sets the threshold (0: kk)
     float kmin_margin;    // k-means pick over the row-shared scan's k-means lists
+    const int32_t *order; // k-means pick: points in this order (a permutation of [0, nq)), or null
     int64_t k;
     float *D;
     int32_t *I;
@@ -1230,7 +1231,8 @@ hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, 
                               const uint32_t *gthr, const ScanPlan &plan, float bound,
                               const float *qf, int32_t *assign,
                               double *best_sq, int32_t *fallback_count, int32_t *fallback_list,
-                              uint32_t *flags, const int32_t *list_cnt, hipStream_t st) {
+                              uint32_t *flags, const int32_t *list_cnt, const int32_t *order,
+                              hipStream_t st) {
     if (n <= 0) return hipSuccess;
     MergeKArgs a{};
     a.xb = cen;
@@ -1263,6 +1265,7 @@ hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, 
         a.list_cnt = list_cnt;
         a.kmin_margin = plan.kmin_margin;
         a.kl = plan.cap;
+        a.order = order;
         kmeans_pick_wave_kernel<32, 16, true>
             <<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(a);
         return hipGetLastError();
@@ -1509,9 +1512,13 @@ __global__ __launch_bounds__(256) void kmeans_pick_wave_kernel(MergeKArgs a) {
     int *ids = id_all[wave];
     const int64_t p0 = ((int64_t)blockIdx.x * 4 + wave) * 64;
     if (p0 >= a.nq) return;  // whole waves only: every lane below stays to the end
-    const int64_t qg = p0 + lane;
-    const bool live = qg < a.nq;
-    const int64_t qc = live ? qg : p0;  // lanes past the end mirror the wave's first point
+    // slot s of the walk is point order[s] (the previous step's grouping by
+    // cluster: a wave's points then share most candidates), or s itself
+    auto point = [&](int64_t s) -> int64_t { return a.order ? (int64_t)a.order[s] : s; };
+    const bool live = p0 + lane < a.nq;
+    // lanes past the end mirror the wave's first point
+    const int64_t qg = point(live ? p0 + lane : p0);
+    const int64_t qc = qg;
     const int64_t qblk = qc / a.bn, q = qc % a.bn;
     const int64_t nlists = a.nsplit * a.lw;
     auto list_off = [&](int64_t l) {
@@ -1598,7 +1605,7 @@ __global__ __launch_bounds__(256) void kmeans_pick_wave_kernel(MergeKArgs a) {
 #pragma unroll
         for (int i = 0; i < PIECES; ++i) {
             const int r = i * ROWS_PER + prow;
-            const int64_t pr = p0 + r < a.nq ? p0 + r : p0;
+            const int64_t pr = point(p0 + r < a.nq ? p0 + r : p0);
             const float4 v = *(const float4 *)(a.pts + pr * a.ld + c0 + pcol);
             xs[(pcol + 0) * RS + r] = v.x;
             xs[(pcol + 1) * RS + r] = v.y;

@@ -163,3 +163,23 @@ def test_kmeans_lists_fp32_rows(vs, monkeypatch):
     x, _ = syn.gaussian_mixture(30_000, 256, 1024, 0.1, 44)
     cen = x[syn.seeded_subset(30_000, 4096, 44)].copy()
     _kmeans_check(vs, x, cen)
+
+
+def test_kmeans_second_step_grouped_order(vs, monkeypatch):
+    """The pick of a second step walks the points grouped by the first
+    step's clusters (a permutation): the same assignments, objective and
+    centroids as the oracle's, and as walking them in index order."""
+    x, _ = syn.gaussian_mixture(30_000, 256, 512, 0.1, 45)
+    cen = x[syn.seeded_subset(30_000, 2048, 45)].copy()
+    u = syn.rng(46, 0).random(2048 * 256)
+    pts = vs.GpuIndexFlat.l2(256, storage="f32")
+    pts.add(x)
+    _, cen1, _, _ = vs.kmeans_step(pts, cen, 1, u)
+    a2, c2, n2, o2 = vs.kmeans_step(pts, cen1, 1, u)
+    monkeypatch.setenv("VS_PICK_ORDER", "0")
+    a3, c3, n3, o3 = vs.kmeans_step(pts, cen1, 1, u)
+    pts.close()
+    assert np.array_equal(a2, a3) and o2 == o3
+    assert np.array_equal(c2.view(np.uint32), c3.view(np.uint32)) and np.array_equal(n2, n3)
+    ar, _, objr = oracle.kmeans_assign(x, cen1, NT)
+    assert np.array_equal(a2, ar) and o2 == objr
