@@ -1634,6 +1634,17 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
                                      x->km_c16n.as<float>(), x->flags.as<uint32_t>(), x->st),
                "centroid copy");
         plan.tile_st = 1;
+        // bf16 rows stage twice the rows per tile in the same registers
+        const int rt = env_int("VS_KM16_RT", 4);
+        if (rt == 4) {
+            const size_t lds = vs::share_lds_bytes(plan.nks, plan.bn / 64, 4, plan.cap);
+            if (lds <= x->lds_max) {
+                plan.tm = 4;
+                plan.lds_bytes = lds;
+                plan.rows_per_split = round_up(plan.rows_per_split, 64);
+                plan.nsplit = std::max<int64_t>(1, (K + plan.rows_per_split - 1) / plan.rows_per_split);
+            }
+        }
         scan_rows = x->km_cen16.p;
         scan_storage = 1;
     }

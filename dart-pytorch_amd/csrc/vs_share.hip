@@ -439,11 +439,10 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
 }
 
 // mode 4 (the k-means assign) is built for the one-pass selection: fp32
-// rows (storage 2), or for 256-element rows their bf16 copy (storage 1, the
-// tile shape of storage 2)
+// rows (storage 2), or for 256-element rows their bf16 copy (storage 1)
 template <int ST, int NKS, int NQB, int RT>
 static void (*share_kmin_kernel())(ScanKArgs) {
-    if constexpr (ST == 2 || (NKS == 8 && RT == 2))
+    if constexpr (ST == 2 || NKS == 8)
         return share_scan_kernel<ST, NKS, NQB, RT, 4>;
     else
         return nullptr;

@@ -155,11 +155,14 @@ def test_kmeans_lists_full(vs, monkeypatch):
     assert not np.any((a >= 200) & (a < 500))
 
 
-def test_kmeans_lists_fp32_rows(vs, monkeypatch):
+@pytest.mark.parametrize("km16,rt", [("0", "4"), ("1", "2")])
+def test_kmeans_lists_fp32_rows(vs, monkeypatch, km16, rt):
     """The k-means lists over the fp32 centroid rows rounded in the scan
-    (VS_KM16=0) instead of their bf16 copy: the same assignments."""
+    (VS_KM16=0), or over their bf16 copy in 32-row tiles (VS_KM16_RT=2)
+    instead of 64-row ones: the oracle's assignments."""
     monkeypatch.setenv("VS_KMIN", "1")
-    monkeypatch.setenv("VS_KM16", "0")
+    monkeypatch.setenv("VS_KM16", km16)
+    monkeypatch.setenv("VS_KM16_RT", rt)
     x, _ = syn.gaussian_mixture(30_000, 256, 1024, 0.1, 44)
     cen = x[syn.seeded_subset(30_000, 4096, 44)].copy()
     _kmeans_check(vs, x, cen)
