@@ -664,9 +664,12 @@ bool plan_gemm(const vs_index *x, int64_t nq, int64_t nrows, int planes, int sto
 // VS_SCAN_BLOCKS_PER_CU (target workgroups per CU), VS_SCAN_QREG (0 disables
 // register-resident queries), VS_SCAN_KKW (per-list keep, for tests of the
 // verification path).
+// min_tiles: the fewest row tiles a split of the streaming scan gets (its
+// lists warm up over them; the threshold-seeding scans over small samples
+// use fewer, so that their short sample still spreads over every CU)
 int plan_scan(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t kk_final,
               int storage, vs::ScanPlan *p, bool safe = false, int64_t max_lists = 0,
-              bool range = false) {
+              bool range = false, int min_tiles = 8) {
     int64_t kk = kk_final <= 32 ? kk_final : kk_final / 4;
     const int kkw = env_int("VS_SCAN_KKW", 0);
     if (kkw > 0) kk = std::min<int64_t>(kk_final, std::max<int64_t>(4, next_pow2(kkw)));
@@ -718,7 +721,7 @@ int plan_scan(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t 
     const int64_t tile_rows = 16 * p->lw * p->tm;  // rows per block per round
     const int64_t target = (int64_t)x->num_cu * env_int("VS_SCAN_BLOCKS_PER_CU", 8);
     int64_t nsplit = std::max<int64_t>(1, (target + p->nqblk - 1) / p->nqblk);
-    const int64_t min_rows = tile_rows * 8;
+    const int64_t min_rows = tile_rows * std::max(1, min_tiles);
     nsplit = std::min<int64_t>(nsplit, std::max<int64_t>(1, (nrows + min_rows - 1) / min_rows));
     if (max_lists > 0) nsplit = std::min<int64_t>(nsplit, std::max<int64_t>(1, max_lists / p->lw));
     int64_t rps = round_up((nrows + nsplit - 1) / nsplit, tile_rows);
@@ -807,7 +810,8 @@ int seed_thresholds(vs_index *x, const vs::PreparedQueries &pq, int64_t S, int64
     S = std::min<int64_t>(S, x->ntotal);
     vs::ScanPlan pp;
     if (max_lists < 0) max_lists = env_int("VS_PREPASS_LISTS", 0);
-    int rc = plan_scan(x, pq.nq, S, pq.planes, kk_final, x->storage, &pp, false, max_lists);
+    int rc = plan_scan(x, pq.nq, S, pq.planes, kk_final, x->storage, &pp, false, max_lists, false,
+                       env_int("VS_PREPASS_MIN_TILES", 2));
     if (rc) return rc;
     // an estimate needs only the values of the sample's seed_rank smallest:
     // the row-shared scan then keeps each lane's smallest in registers
@@ -817,7 +821,7 @@ int seed_thresholds(vs_index *x, const vs::PreparedQueries &pq, int64_t S, int64
         env_int("VS_GUESS_TOPM", 1))
         pp.share_topm = vs::share_topm(false);
     if ((rc = scan_fits(pp, pq))) return rc;
-    const int div = std::max(2, env_int("VS_PREPASS_DIV", 32));
+    const int div = std::max(2, env_int("VS_PREPASS_DIV", 1024));
     if (pp.kind == 0 && pp.nsplit * pp.lw >= 512 && S >= (1 << 18)) {
         rc = seed_thresholds(x, pq, std::max<int64_t>(1 << 16, S / div), kk_final, min_list_elems);
         if (rc) return rc;
@@ -920,7 +924,7 @@ int search_device(vs_index *x, const void *q_dev, int q_dtype, int64_t nq, int64
         if (rc) return rc;
     } else if (!safe && needs_seed(x, plan) && env_int("VS_PREPASS", 1)) {
         rc = seed_thresholds(x, pq,
-                             std::max<int64_t>(1 << 16, x->ntotal / std::max(2, env_int("VS_PREPASS_DIV", 32))),
+                             std::max<int64_t>(1 << 16, x->ntotal / std::max(2, env_int("VS_PREPASS_DIV", 1024))),
                              kk, nlist);
         if (rc) return rc;
     }
