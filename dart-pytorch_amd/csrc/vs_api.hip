@@ -495,7 +495,8 @@ bool plan_share(const vs_index *x, int64_t nq, int64_t nrows, int planes, int st
         return false;
     if (nq < env_int("VS_SHARE_MIN_NQ", 256)) return false;
     const int nks = (int)(x->ld / 32), nqb = nks == 4 ? 4 : 2;
-    const int rt = storage == 1 ? 4 : 2;  // fp32 tiles: half the rows, the same staging registers
+    // fp32 tiles: half the rows, the same staging registers
+    const int rt = storage == 1 ? (nks == 4 ? env_int("VS_SHARE_RT", 8) : 4) : 2;
     // a list of the row-shared scan gains up to 16 entries per 16-row block
     // and query; 256 slots at least keep cuts rare while its threshold is
     // still loose (the list is sorted only up to its fill)
