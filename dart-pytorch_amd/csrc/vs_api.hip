@@ -522,7 +522,7 @@ bool plan_share(const vs_index *x, int64_t nq, int64_t nrows, int planes, int st
     // rows together through that XCD's L2, and no round is left half empty.
     const int bpc = std::max(1, vs::share_blocks_per_cu(storage, nks, p->bn, rt, x->ld, lds, 0));
     const int64_t resident = (int64_t)std::max(1, x->num_cu) * bpc;
-    const int64_t target = resident * std::max(1, env_int("VS_SHARE_ROUNDS", 2));
+    const int64_t target = resident * std::max(1, env_int("VS_SHARE_ROUNDS", 4));
     int64_t nsplit = std::max<int64_t>(1, target / p->nqblk);
     nsplit = std::min<int64_t>(nsplit, std::max<int64_t>(1, nrows / (tile_rows * 8)));
     if (max_split > 0) nsplit = std::min<int64_t>(nsplit, max_split);
