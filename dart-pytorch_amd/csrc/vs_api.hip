@@ -720,7 +720,7 @@ int plan_scan(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t 
     p->lds_bytes = vs::scan_lds_bytes(p->bn, p->nks ? 0 : planes, x->ld, p->cap, p->lw);
     p->nqblk = (nq + p->bn - 1) / p->bn;
     const int64_t tile_rows = 16 * p->lw * p->tm;  // rows per block per round
-    const int64_t target = (int64_t)x->num_cu * env_int("VS_SCAN_BLOCKS_PER_CU", 8);
+    const int64_t target = (int64_t)x->num_cu * env_int("VS_SCAN_BLOCKS_PER_CU", 4);
     int64_t nsplit = std::max<int64_t>(1, (target + p->nqblk - 1) / p->nqblk);
     const int64_t min_rows = tile_rows * std::max(1, min_tiles);
     nsplit = std::min<int64_t>(nsplit, std::max<int64_t>(1, (nrows + min_rows - 1) / min_rows));
