@@ -1751,8 +1751,18 @@ __global__ __launch_bounds__(256) void kmeans_update_kernel(const float *__restr
     const int off = offsets[c];
     const double inv = 1.0 / (double)cnt;
     for (int64_t j = threadIdx.x; j < d; j += blockDim.x) {
+        // the points' values are loaded eight at a time (independent loads
+        // in flight together), then added one by one in point order
         float s = 0.0f;
-        for (int t = 0; t < cnt; ++t) s = s + x[(int64_t)order[off + t] * ld + j];
+        int t = 0;
+        for (; t + 8 <= cnt; t += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = x[(int64_t)order[off + t + u] * ld + j];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) s = s + v[u];
+        }
+        for (; t < cnt; ++t) s = s + x[(int64_t)order[off + t] * ld + j];
         cen_out[c * d + j] = (float)((double)s * inv);
     }
 }
