@@ -162,6 +162,7 @@ struct vs_index {
     DevBuf km_qp, km_qf, km_qnorm;
     // k-means: pinned copies of the distances, assignments and new centroids
     HostBuf km_hbest, km_hassign, km_hcen;
+    HostBuf rstage;  // reconstruct: pinned staging of stored rows
     hipStream_t st_copy = nullptr;  // k-means: reads results back beside the update
     // k-means: km_order holds the last step's points grouped by cluster, for
     // these rows (version) and this many points
@@ -176,7 +177,12 @@ struct vs_index {
     uint64_t xb16_version = ~0ull;
     int64_t km_iota_n = -1;  // km_iota holds 0 .. km_iota_n - 1
     bool prof_on = false;
+    bool prof_fixed = false;  // inside an allocation-free call: no profiling bookkeeping
     std::map<std::string, ProfEntry> prof;
+    // largest stored row norm, for the version of the rows it was taken at
+    float xmax_cache = 0.f;
+    uint64_t xmax_version = ~0ull;
+    DevBuf vx, ctl;  // top-k: exact-path query list, control words
     std::vector<PendingEvent> pending;
 };
 
@@ -192,7 +198,7 @@ struct ProfScope {
     const char *fam;
     hipEvent_t a = nullptr, b = nullptr;
     ProfScope(vs_index *x_, const char *fam_) : x(x_), fam(fam_) {
-        if (!x->prof_on) return;
+        if (!x->prof_on || x->prof_fixed) return;
         if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) {
             a = b = nullptr;
             return;
@@ -211,6 +217,7 @@ struct ProfScope {
 void note_scan_kind(vs_index *x, const vs::ScanPlan &plan) {
     x->prof[plan.kind == 3 ? "shared" : plan.kind == 2 ? "gemm" : plan.kind == 1 ? "tiled" : "streamed"]
         .launches++;
+    if (plan.kind == 0 && plan.lw == 8) x->prof["streamed8"].launches++;
     if (plan.kind == 2) {  // and per GEMM shape: "gemm:1,1,2,4,4,2,32" or "gemmdma:1,2,4,4,2,4"
         char key[64];
         if (plan.g_ns > 0)
@@ -668,9 +675,11 @@ bool plan_gemm(const vs_index *x, int64_t nq, int64_t nrows, int planes, int sto
 // min_tiles: the fewest row tiles a split of the streaming scan gets (its
 // lists warm up over them; the threshold-seeding scans over small samples
 // use fewer, so that their short sample still spreads over every CU)
+// list_budget > 0: the candidate lists may take at most this many bytes
+// (streaming scan only; its split count shrinks to fit).
 int plan_scan(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t kk_final,
               int storage, vs::ScanPlan *p, bool safe = false, int64_t max_lists = 0,
-              bool range = false, int min_tiles = 8) {
+              bool range = false, int min_tiles = 8, size_t list_budget = 0) {
     int64_t kk = kk_final <= 32 ? kk_final : kk_final / 4;
     const int kkw = env_int("VS_SCAN_KKW", 0);
     if (kkw > 0) kk = std::min<int64_t>(kk_final, std::max<int64_t>(4, next_pow2(kkw)));
@@ -683,12 +692,13 @@ int plan_scan(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t 
     p->tm = env_int("VS_SCAN_TM", x->ld <= 128 && storage == 1 ? 1 : 2);
     if (p->tm != 1 && p->tm != 2 && p->tm != 4) p->tm = 2;
     p->kind = 0;
-    if (!range && kkw <= 0 && plan_share(x, nq, nrows, planes, storage, p, max_lists))
+    if (!range && kkw <= 0 && !list_budget &&
+        plan_share(x, nq, nrows, planes, storage, p, max_lists))
         return VS_OK;
     // (a list limit shapes the split count of the row-shared and streaming
     // scans; the tiled scans make few lists per query anyway)
-    if (plan_gemm(x, nq, nrows, planes, storage, kkw > 0 || safe, p)) return VS_OK;
-    if (plan_tile(x, nq, nrows, planes, storage, p)) return VS_OK;
+    if (!list_budget && plan_gemm(x, nq, nrows, planes, storage, kkw > 0 || safe, p)) return VS_OK;
+    if (!list_budget && plan_tile(x, nq, nrows, planes, storage, p)) return VS_OK;
     const int nks = (int)(x->ld / 32);
     const int force_bn = env_int("VS_SCAN_BN", 0);
     const int cands[3] = {64, 32, 16};
@@ -725,6 +735,10 @@ int plan_scan(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t 
     const int64_t min_rows = tile_rows * std::max(1, min_tiles);
     nsplit = std::min<int64_t>(nsplit, std::max<int64_t>(1, (nrows + min_rows - 1) / min_rows));
     if (max_lists > 0) nsplit = std::min<int64_t>(nsplit, std::max<int64_t>(1, max_lists / p->lw));
+    if (list_budget > 0) {
+        const size_t per_split = (size_t)p->nqblk * p->lw * p->bn * p->cap * 8;
+        nsplit = std::min<int64_t>(nsplit, std::max<int64_t>(1, (int64_t)(list_budget / per_split)));
+    }
     int64_t rps = round_up((nrows + nsplit - 1) / nsplit, tile_rows);
     if (rps <= 0) rps = tile_rows;
     p->rows_per_split = rps;
@@ -738,6 +752,56 @@ int plan_scan(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t 
                 p->lds_bytes);
     return VS_OK;
 }
+
+// Device scratch of one call.  Ordinary calls use the index's grow-on-demand
+// buffers, plus call-local ones for the fallback paths; the allocation-free
+// entry point carves every piece, in order, from one fixed device region
+// (mark / reset release what a finished sub-step carved).
+struct Arena {
+    char *base = nullptr;  // fixed region, or null
+    size_t cap = 0, used = 0;
+    std::vector<DevBuf> local;  // ordinary calls: call-local buffers
+    Arena() = default;
+    Arena(const Arena &) = delete;
+    Arena &operator=(const Arena &) = delete;
+    ~Arena() {
+        for (auto &b : local) b.release();
+    }
+    bool fixed() const { return base != nullptr; }
+    int carve(size_t bytes, void **p, const char *what) {
+        const size_t off = (used + 255) & ~(size_t)255;
+        if (off + bytes > cap)
+            return set_err(VS_ERR_UNSUPPORTED,
+                           "%s: %zu bytes past the end of the %zu-byte fixed scratch", what,
+                           off + bytes - cap, cap);
+        *p = base + off;
+        used = off + bytes;
+        return VS_OK;
+    }
+    // the index's buffer b with at least `bytes` (a fresh piece when fixed)
+    int get(DevBuf &b, size_t bytes, void **p, const char *what) {
+        if (base) return carve(bytes, p, what);
+        VS_HIP(b.ensure(bytes), what);
+        *p = b.p;
+        return VS_OK;
+    }
+    // a buffer of this call only
+    int tmp(size_t bytes, void **p, const char *what) {
+        if (base) return carve(bytes, p, what);
+        local.emplace_back();
+        VS_HIP(local.back().ensure(bytes), what);
+        *p = local.back().p;
+        return VS_OK;
+    }
+    size_t mark() const { return used; }
+    void reset(size_t m) { used = m; }
+};
+
+#define VS_TAKE(arena_call)          \
+    do {                             \
+        int rc_ = (arena_call);      \
+        if (rc_) return rc_;         \
+    } while (0)
 
 // Rows of prepared queries (and of the per-query shared thresholds): a
 // multiple of 256 plus 256 spare rows, so the query blocks of any scan plan
@@ -753,32 +817,40 @@ int scan_fits(const vs::ScanPlan &plan, const vs::PreparedQueries &pq) {
     return VS_OK;
 }
 
-int prepare_queries(vs_index *x, const void *q_dev, int q_dtype, int64_t stride, int64_t nq,
-                    vs::PreparedQueries *pq, uint32_t *flags_out, DevBuf *qp = nullptr,
-                    DevBuf *qf = nullptr, DevBuf *qnorm = nullptr) {
-    if (!qp) qp = &x->qp;
-    if (!qf) qf = &x->qf;
-    if (!qnorm) qnorm = &x->qnorm;
+// Builds the MFMA query planes, the fp32 copy and the norms of nq query rows
+// (device memory, `stride` elements apart); *flags_out receives the query
+// flags (non-finite, not bf16).  The planes and copies go to qp / qf / qnorm
+// (the index's buffers) or, in a fixed arena, to fresh pieces of it.
+int prepare_queries(vs_index *x, Arena &A, const void *q_dev, int q_dtype, int64_t stride,
+                    int64_t nq, vs::PreparedQueries *pq, uint32_t *flags_out, DevBuf &qp,
+                    DevBuf &qf, DevBuf &qnorm) {
     pq->nq = nq;
     pq->nq_pad = query_pad(nq);
-    VS_HIP(qp->ensure((size_t)pq->nq_pad * 2 * x->ld * 2), "query planes");
-    VS_HIP(qf->ensure((size_t)std::max<int64_t>(nq, 1) * x->d * 4), "query copy");
-    VS_HIP(qnorm->ensure((size_t)pq->nq_pad * 4), "query norms");
-    VS_HIP(x->flags.ensure(sizeof(uint32_t)), "flags buffer");
-    pq->qp = qp->as<uint16_t>();
-    pq->qf = qf->as<float>();
-    pq->qnorm = qnorm->as<float>();
-    VS_HIP(hipMemsetAsync(x->flags.p, 0, sizeof(uint32_t), x->st), "clearing flags");
+    void *p_qp, *p_qf, *p_qn, *p_fl;
+    VS_TAKE(A.get(qp, (size_t)pq->nq_pad * 2 * x->ld * 2, &p_qp, "query planes"));
+    VS_TAKE(A.get(qf, (size_t)std::max<int64_t>(nq, 1) * x->d * 4, &p_qf, "query copy"));
+    VS_TAKE(A.get(qnorm, (size_t)pq->nq_pad * 4, &p_qn, "query norms"));
+    VS_TAKE(A.get(x->flags, sizeof(uint32_t), &p_fl, "flags buffer"));
+    pq->qp = (uint16_t *)p_qp;
+    pq->qf = (float *)p_qf;
+    pq->qnorm = (float *)p_qn;
+    VS_HIP(vs::launch_fill32(p_fl, 1, 0u, x->st), "clearing flags");
     VS_HIP(vs::launch_prepare_queries(q_dev, q_dtype, stride, nq, x->d, x->ld, x->metric, *pq,
-                                      x->flags.as<uint32_t>(), x->st),
+                                      (uint32_t *)p_fl, x->st),
            "preparing queries");
     uint32_t f = 0;
-    VS_HIP(hipMemcpyAsync(&f, x->flags.p, sizeof f, hipMemcpyDeviceToHost, x->st), "query flags");
+    VS_HIP(hipMemcpyAsync(&f, p_fl, sizeof f, hipMemcpyDeviceToHost, x->st), "query flags");
     VS_HIP(hipStreamSynchronize(x->st), "preparing queries");
     if (f & vs::kFlagNonFinite) return set_err(VS_ERR_NONFINITE, "queries contain NaN or infinity");
     pq->planes = (f & vs::kFlagNotBf16) ? 2 : 1;
     if (flags_out) *flags_out = f;
     return VS_OK;
+}
+
+int prepare_queries(vs_index *x, Arena &A, const void *q_dev, int q_dtype, int64_t stride,
+                    int64_t nq, vs::PreparedQueries *pq, uint32_t *flags_out) {
+    return prepare_queries(x, A, q_dev, q_dtype, stride, nq, pq, flags_out, x->qp, x->qf,
+                           x->qnorm);
 }
 
 __global__ void fill_sentinels_kernel(float *D, int32_t *I, int64_t m, float v) {
@@ -787,6 +859,34 @@ __global__ void fill_sentinels_kernel(float *D, int32_t *I, int64_t m, float v) 
         D[t] = v;
         I[t] = -1;
     }
+}
+
+// Candidate lists of a scan and of its threshold pre-passes (which run
+// first and reuse the same memory): values, ids, and per-list counts with
+// the largest count after them.
+struct ListBufs {
+    float *v = nullptr;
+    int32_t *i = nullptr;
+    int32_t *cnt = nullptr;
+    size_t elems = 0, lists = 0;
+};
+
+size_t list_elems(const vs::ScanPlan &p) {
+    return (size_t)p.nqblk * p.nsplit * p.lw * p.bn * p.cap;
+}
+size_t list_count(const vs::ScanPlan &p) { return (size_t)p.nqblk * p.nsplit * p.lw * p.bn; }
+
+int take_lists(vs_index *x, Arena &A, size_t elems, size_t lists, ListBufs *L) {
+    void *pv, *pi, *pc;
+    VS_TAKE(A.get(x->cand_v, elems * 4, &pv, "candidate lists"));
+    VS_TAKE(A.get(x->cand_i, elems * 4, &pi, "candidate lists"));
+    VS_TAKE(A.get(x->lcnt, (lists + 1) * 4, &pc, "list counts"));
+    L->v = (float *)pv;
+    L->i = (int32_t *)pi;
+    L->cnt = (int32_t *)pc;
+    L->elems = elems;
+    L->lists = lists;
+    return VS_OK;
 }
 
 // A plan warms up badly when it makes many lists per query over many rows.
@@ -806,13 +906,17 @@ bool needs_seed(const vs_index *x, const vs::ScanPlan &plan) {
 // above the seed_rank-th smallest value of the sample, which the caller
 // chooses so that the full scan very likely holds kk_final rows below it;
 // the merge then flags the queries for which it does not (guess_thresholds).
+//
+// L == nullptr plans only: *need_elems / *need_lists grow to what the
+// pre-pass scans need.
 int seed_thresholds(vs_index *x, const vs::PreparedQueries &pq, int64_t S, int64_t kk_final,
-                    size_t min_list_elems, int seed_rank = 0, int64_t max_lists = -1) {
+                    uint32_t *gthr, ListBufs *L, size_t *need_elems, size_t *need_lists,
+                    int seed_rank = 0, int64_t max_lists = -1, size_t list_budget = 0) {
     S = std::min<int64_t>(S, x->ntotal);
     vs::ScanPlan pp;
     if (max_lists < 0) max_lists = env_int("VS_PREPASS_LISTS", 0);
     int rc = plan_scan(x, pq.nq, S, pq.planes, kk_final, x->storage, &pp, false, max_lists, false,
-                       env_int("VS_PREPASS_MIN_TILES", 2));
+                       env_int("VS_PREPASS_MIN_TILES", 2), list_budget);
     if (rc) return rc;
     // an estimate needs only the values of the sample's seed_rank smallest:
     // the row-shared scan then keeps each lane's smallest in registers
@@ -824,25 +928,28 @@ int seed_thresholds(vs_index *x, const vs::PreparedQueries &pq, int64_t S, int64
     if ((rc = scan_fits(pp, pq))) return rc;
     const int div = std::max(2, env_int("VS_PREPASS_DIV", 1024));
     if (pp.kind == 0 && pp.nsplit * pp.lw >= 512 && S >= (1 << 18)) {
-        rc = seed_thresholds(x, pq, std::max<int64_t>(1 << 16, S / div), kk_final, min_list_elems);
+        rc = seed_thresholds(x, pq, std::max<int64_t>(1 << 16, S / div), kk_final, gthr, L,
+                             need_elems, need_lists, 0, -1, list_budget);
         if (rc) return rc;
     }
-    const size_t pn = std::max(min_list_elems, (size_t)pp.nqblk * pp.nsplit * pp.lw * pp.bn * pp.cap);
-    VS_HIP(x->cand_v.ensure(pn * 4), "candidate lists");
-    VS_HIP(x->cand_i.ensure(pn * 4), "candidate lists");
-    const size_t pl = (size_t)pp.nqblk * pp.nsplit * pp.lw * pp.bn;
-    VS_HIP(x->lcnt.ensure((pl + 1) * 4), "list counts");
-    VS_HIP(hipMemsetAsync(x->lcnt.as<int32_t>() + pl, 0, 4, x->st), "list counts");
-    ProfScope ps(x, "prepass");
-    VS_HIP(vs::launch_scan_topk(x->xb, x->storage, x->ld, x->xn, S, x->metric, pq, pp,
-                                x->cand_v.as<float>(), x->cand_i.as<int32_t>(),
-                                x->gthr.as<uint32_t>(), nullptr, x->lcnt.as<int32_t>(), x->st),
-           "seeding scan");
-    VS_HIP(vs::launch_merge_threshold(pq, pp, x->cand_v.as<float>(), x->cand_i.as<int32_t>(),
-                                      x->gthr.as<uint32_t>(), x->ld, seed_rank,
-                                      x->lcnt.as<int32_t>(), x->st),
+    if (!L) {
+        *need_elems = std::max(*need_elems, list_elems(pp));
+        *need_lists = std::max(*need_lists, list_count(pp));
+        return VS_OK;
+    }
+    if (list_elems(pp) > L->elems || list_count(pp) > L->lists)
+        return set_err(VS_ERR_HIP, "internal: pre-pass lists larger than planned");
+    const bool prof = !x->prof_fixed;
+    VS_HIP(vs::launch_fill32(L->cnt + list_count(pp), 1, 0u, x->st), "list counts");
+    {
+        ProfScope ps(x, "prepass");
+        VS_HIP(vs::launch_scan_topk(x->xb, x->storage, x->ld, x->xn, S, x->metric, pq, pp, L->v,
+                                    L->i, gthr, nullptr, L->cnt, x->st),
+               "seeding scan");
+    }
+    VS_HIP(vs::launch_merge_threshold(pq, pp, L->v, L->i, gthr, x->ld, seed_rank, L->cnt, x->st),
            "seeding threshold");
-    x->prof["prepass_scans"].launches++;
+    if (prof) x->prof["prepass_scans"].launches++;
     return VS_OK;
 }
 
@@ -862,18 +969,158 @@ bool needs_guess(const vs_index *x, const vs::ScanPlan &plan, int64_t nq) {
 }
 
 int guess_thresholds(vs_index *x, const vs::PreparedQueries &pq, int64_t kk_final,
-                     size_t min_list_elems) {
+                     uint32_t *gthr, ListBufs *L, size_t *need_elems, size_t *need_lists) {
     const int64_t div = std::max(2, env_int("VS_GUESS_DIV", 32));
     const int64_t S = std::min<int64_t>(x->ntotal, std::max<int64_t>(4096, x->ntotal / div));
     const double lam = (double)kk_final * (double)S / (double)x->ntotal;
     const int j = (int)std::ceil(lam + 4.0 * std::sqrt(lam) + 4.0);
     const int64_t kkp = std::max<int64_t>(8, next_pow2(j));
-    x->prof["guess_scans"].launches++;
-    return seed_thresholds(x, pq, S, kkp, min_list_elems, j, env_int("VS_GUESS_LISTS", 12));
+    if (L && !x->prof_fixed) x->prof["guess_scans"].launches++;
+    return seed_thresholds(x, pq, S, kkp, gthr, L, need_elems, need_lists, j,
+                           env_int("VS_GUESS_LISTS", 12));
 }
 
-int search_device(vs_index *x, const void *q_dev, int q_dtype, int64_t nq, int64_t k, float *D,
-                  int32_t *I, bool safe = false) {
+// The largest stored row norm (times 1 + 1e-6), cached per row version.
+int xnorm_max(vs_index *x, Arena &A, float *out) {
+    if (x->ntotal == 0) {
+        *out = 0.f;
+        return VS_OK;
+    }
+    if (x->xmax_version != x->version) {
+        void *p;
+        VS_TAKE(A.get(x->misc, sizeof(float), &p, "norm maximum"));
+        VS_HIP(vs::launch_max_reduce(x->xn, x->ntotal, (float *)p, x->st), "norm maximum");
+        float m = 0.f;
+        VS_HIP(hipMemcpyAsync(&m, p, sizeof m, hipMemcpyDeviceToHost, x->st), "norm maximum");
+        VS_HIP(hipStreamSynchronize(x->st), "norm maximum");
+        x->xmax_cache = std::sqrt(m) * (1.0f + 1e-6f);
+        x->xmax_version = x->version;
+    }
+    *out = x->xmax_cache;
+    return VS_OK;
+}
+
+// Accumulator error model of a top-k scan of these rows with these queries
+// (relative error of one product of MFMA operands; the accumulation factor
+// covers up to three passes of d products and the fp32 row norms):
+//   bf16 rows, queries exactly bf16 (one plane): products exact;
+//   bf16 rows, two query planes: the dropped residual, below 2^-18;
+//   fp32 rows (hi + lo planes), one query plane: below 2^-18;
+//   fp32 rows, two query planes: lo * q1 and the residuals, below 3.1 * 2^-18.
+// The factors below are 2.7 to 4 times those.
+void topk_error_model(const vs_index *x, int planes, vs::TopkCheck *chk) {
+    const double u = 1.0 / 16777216.0;
+    chk->err_g = (float)((3.0 * (double)x->d + 4.0) * u);
+    if (x->storage == 1)
+        chk->err_r = planes == 1 ? 0.f : (float)(1.0 / 65536.0);
+    else
+        chk->err_r = planes == 1 ? (float)(1.0 / 65536.0) : (float)(1.0 / 32768.0);
+}
+
+int search_device(vs_index *x, Arena &A, const void *q_dev, int q_dtype, int64_t nq, int64_t k,
+                  float *D, int32_t *I, bool safe = false, size_t list_budget = 0);
+
+// Exact top-k of nq fp32 query rows (device, [nq][d]) without the MFMA
+// selection: per-(query, split) lists of the kk best exact keys, then the
+// merge (k <= kMaxFusedK), or a per-query sort of every row's key (larger
+// k; not in a fixed arena).
+int exact_search(vs_index *x, Arena &A, const float *qf, int64_t nq, int64_t k, float *D,
+                 int32_t *I) {
+    if (nq <= 0) return VS_OK;
+    const int64_t kk = std::max<int64_t>(8, next_pow2(k + std::max<int64_t>(4, k / 4)));
+    if (kk <= 512) {
+        // splits: a few workgroups per CU over all queries, >= 1024 rows each
+        const int64_t target = (int64_t)x->num_cu * 4;
+        int64_t ns = std::max<int64_t>(1, (target + nq - 1) / nq);
+        ns = std::min<int64_t>(ns, std::max<int64_t>(1, x->ntotal / 1024));
+        if (A.fixed())  // the lists stay within 16 MiB
+            ns = std::max<int64_t>(1, std::min<int64_t>(ns, (int64_t)(16 << 20) / (nq * kk * 8)));
+        const int64_t rps = round_up((x->ntotal + ns - 1) / ns, 256);
+        ns = (x->ntotal + rps - 1) / rps;
+        void *pv, *pi;
+        VS_TAKE(A.tmp((size_t)nq * ns * kk * 4, &pv, "exact lists"));
+        VS_TAKE(A.tmp((size_t)nq * ns * kk * 4, &pi, "exact lists"));
+        VS_HIP(vs::launch_exact_lists(x->xb, x->storage, x->ld, x->d, x->metric, qf, nq, x->ntotal,
+                                      (int)kk, ns, rps, (float *)pv, (int32_t *)pi, x->st),
+               "exact lists");
+        vs::PreparedQueries pq;
+        pq.qf = (float *)qf;
+        pq.nq = nq;
+        pq.nq_pad = nq;
+        vs::ScanPlan plan;
+        plan.kind = 0;
+        plan.bn = 1;
+        plan.lw = 1;
+        plan.kk = (int)kk;
+        plan.kk_final = (int)kk;
+        plan.cap = (int)kk;
+        plan.nqblk = nq;
+        plan.nsplit = ns;
+        void *pf;
+        VS_TAKE(A.get(x->flags, sizeof(uint32_t), &pf, "flags buffer"));
+        VS_HIP(vs::launch_fill32(pf, 1, 0u, x->st), "clearing flags");
+        VS_HIP(vs::launch_merge_refine(x->xb, x->storage, x->ld, x->d, x->metric, pq, plan,
+                                       (float *)pv, (int32_t *)pi, nullptr, nullptr, nullptr,
+                                       nullptr, k, D, I, x->ntotal, (uint32_t *)pf, 0, nullptr,
+                                       nullptr, x->st),
+               "exact merge");
+        if (!x->prof_fixed) x->prof["exact_queries"].launches += nq;
+        return VS_OK;
+    }
+    if (A.fixed())
+        return set_err(VS_ERR_UNSUPPORTED, "k=%lld needs the sorting path, which allocates",
+                       (long long)k);
+    // one query chunk of keys within 1 GiB, plus the sort's output and scratch
+    const int64_t n = x->ntotal;
+    const int64_t qchunk = std::max<int64_t>(1, std::min<int64_t>(nq, (int64_t)(1 << 27) / n));
+    size_t tmp_bytes = 0;
+    VS_HIP(vs::exact_sort_topk(x->xb, x->storage, x->ld, x->d, x->metric, qf, nq, n, k, D, I,
+                               nullptr, qchunk, nullptr, tmp_bytes, x->st),
+           "sort size");
+    void *keys, *tmp;
+    VS_TAKE(A.tmp((size_t)(qchunk + 1) * n * 8, &keys, "sort keys"));
+    VS_TAKE(A.tmp(tmp_bytes + 256, &tmp, "sort scratch"));
+    VS_HIP(vs::exact_sort_topk(x->xb, x->storage, x->ld, x->d, x->metric, qf, nq, n, k, D, I,
+                               (uint64_t *)keys, qchunk, tmp, tmp_bytes, x->st),
+           "exact sort");
+    if (!x->prof_fixed) x->prof["exact_sort_queries"].launches += nq;
+    return VS_OK;
+}
+
+// Re-search of the queries listed in list_dev (device, m entries) of the
+// prepared queries pq: their rows are gathered, searched by `how` (0: the
+// MFMA selection again with full-length lists and no estimates; 1: the
+// exact path), and their k results scattered back into D / I.
+int research_listed(vs_index *x, Arena &A, const vs::PreparedQueries &pq, const int32_t *list_dev,
+                    int64_t m, int64_t k, float *D, int32_t *I, int how) {
+    if (m <= 0) return VS_OK;
+    void *lst, *fq, *fD, *fI;
+    VS_TAKE(A.tmp((size_t)m * 4, &lst, "fallback list"));
+    VS_TAKE(A.tmp((size_t)m * x->d * 4, &fq, "fallback queries"));
+    VS_TAKE(A.tmp((size_t)m * k * 4, &fD, "fallback results"));
+    VS_TAKE(A.tmp((size_t)m * k * 4, &fI, "fallback results"));
+    VS_HIP(hipMemcpyAsync(lst, list_dev, (size_t)m * 4, hipMemcpyDeviceToDevice, x->st),
+           "fallback list");
+    VS_HIP(vs::launch_gather_rows(pq.qf, (const int32_t *)lst, m, x->d, fq, x->st),
+           "fallback gather");
+    const size_t mk = A.mark();
+    int rc = how == 0 ? search_device(x, A, fq, VS_DTYPE_F32, m, k, (float *)fD, (int32_t *)fI,
+                                      true, A.fixed() ? (size_t)(48 << 20) : 0)
+                      : exact_search(x, A, (const float *)fq, m, k, (float *)fD, (int32_t *)fI);
+    if (rc) return rc;
+    VS_HIP(vs::launch_scatter_rows(fD, (const int32_t *)lst, m, k, D, x->st), "fallback scatter");
+    VS_HIP(vs::launch_scatter_rows(fI, (const int32_t *)lst, m, k, I, x->st), "fallback scatter");
+    A.reset(mk);
+    if (!x->prof_fixed) x->prof[how == 0 ? "fallback" : "exact_fallback"].launches += m;
+    return VS_OK;
+}
+
+// Top-k search of nq device query rows into device D / I [nq][k].  safe:
+// full-length lists and no threshold estimates (the re-search of queries
+// the merge could not prove exact).  list_budget > 0 bounds the bytes of
+// the candidate lists (the streaming scan's split count adapts).
+int search_device(vs_index *x, Arena &A, const void *q_dev, int q_dtype, int64_t nq, int64_t k,
+                  float *D, int32_t *I, bool safe, size_t list_budget) {
     if (nq < 0 || k < 0) return set_err(VS_ERR_INVALID, "nq and k must be >= 0");
     if (nq == 0) return VS_OK;
     if (k == 0) {
@@ -889,123 +1136,92 @@ int search_device(vs_index *x, const void *q_dev, int q_dtype, int64_t nq, int64
         VS_HIP(hipStreamSynchronize(x->st), "search");
         return VS_OK;
     }
-    const int64_t kk = std::max<int64_t>(8, next_pow2(k + std::max<int64_t>(4, k / 4)));
-    if (kk > 512)
-        return set_err(VS_ERR_UNSUPPORTED, "k=%lld exceeds the fused top-k limit of this build (400)",
-                       (long long)k);
     vs::PreparedQueries pq;
-    int rc = prepare_queries(x, q_dev, q_dtype, x->d, nq, &pq, nullptr);
+    int rc = prepare_queries(x, A, q_dev, q_dtype, x->d, nq, &pq, nullptr);
     if (rc) return rc;
+    const int64_t kk = std::max<int64_t>(8, next_pow2(k + std::max<int64_t>(4, k / 4)));
+    if (kk > 512) {  // beyond the fused selection: the sorting path
+        rc = exact_search(x, A, pq.qf, nq, k, D, I);
+        if (rc) return rc;
+        VS_HIP(hipStreamSynchronize(x->st), "search");
+        return VS_OK;
+    }
     vs::ScanPlan plan;
-    rc = plan_scan(x, nq, x->ntotal, pq.planes, kk, x->storage, &plan, safe);
+    rc = plan_scan(x, nq, x->ntotal, pq.planes, kk, x->storage, &plan, safe, 0, false, 8,
+                   list_budget);
     if (rc) return rc;
     if ((rc = scan_fits(plan, pq))) return rc;
-    const size_t nlists = (size_t)plan.nqblk * plan.nsplit * plan.lw * plan.bn;
-    const size_t nlist = nlists * plan.cap;
-    VS_HIP(x->cand_v.ensure(nlist * 4), "candidate lists");
-    VS_HIP(x->cand_i.ensure(nlist * 4), "candidate lists");
-    VS_HIP(x->lcnt.ensure((nlists + 1) * 4), "list counts");
-    VS_HIP(x->gthr.ensure((size_t)pq.nq_pad * 4), "shared thresholds");
-    VS_HIP(hipMemsetD32Async((hipDeviceptr_t)x->gthr.p, (int)vs::kGthrInit, (size_t)pq.nq_pad, x->st),
-           "shared thresholds");
     const bool verify = plan.kk < plan.kk_final;
     const bool guess = !safe && needs_guess(x, plan, nq);
-    if (verify) VS_HIP(x->lbound.ensure(nlists * 4), "list bounds");
-    if (verify || guess) {
-        VS_HIP(x->vf.ensure((size_t)(nq + 1) * 4), "verification list");
-        VS_HIP(hipMemsetAsync(x->vf.p, 0, 4, x->st), "verification count");
-    }
+    const bool seed = !guess && !safe && needs_seed(x, plan) && env_int("VS_PREPASS", 1);
+    const int64_t seed_S =
+        std::max<int64_t>(1 << 16, x->ntotal / std::max(2, env_int("VS_PREPASS_DIV", 1024)));
+    // candidate lists for the scan and its pre-passes
+    size_t elems = list_elems(plan), lists = list_count(plan);
+    if (guess) rc = guess_thresholds(x, pq, kk, nullptr, nullptr, &elems, &lists);
+    else if (seed) rc = seed_thresholds(x, pq, seed_S, kk, nullptr, nullptr, &elems, &lists, 0, -1, list_budget);
+    if (rc) return rc;
+    ListBufs L;
+    VS_TAKE(take_lists(x, A, elems, lists, &L));
+    void *p_gthr, *p_lb = nullptr, *p_vf, *p_vx, *p_ctl;
+    VS_TAKE(A.get(x->gthr, (size_t)pq.nq_pad * 4, &p_gthr, "shared thresholds"));
+    if (verify) VS_TAKE(A.get(x->lbound, list_count(plan) * 4, &p_lb, "list bounds"));
+    VS_TAKE(A.get(x->vf, (size_t)(nq + 1) * 4, &p_vf, "verification list"));
+    VS_TAKE(A.get(x->vx, (size_t)(nq + 1) * 4, &p_vx, "exactness list"));
+    // control words: flags, then the counts of the two lists
+    VS_TAKE(A.get(x->ctl, 4 * sizeof(int32_t), &p_ctl, "control words"));
+    int32_t *ctl = (int32_t *)p_ctl;
+    uint32_t *gthr = (uint32_t *)p_gthr;
+    VS_HIP(vs::launch_fill32(gthr, pq.nq_pad, vs::kGthrInit, x->st), "shared thresholds");
+    VS_HIP(vs::launch_fill32(ctl, 4, 0u, x->st), "control words");
     // Small batches over many rows make many short lists, each warming up on
     // its own (every list must fill kk entries before its threshold means
     // anything).  Seeding the shared thresholds from samples first (see
     // seed_thresholds) lets the full scan start tight; large batches start
     // from an estimate (guess_thresholds).
-    if (guess) {
-        rc = guess_thresholds(x, pq, kk, nlist);
-        if (rc) return rc;
-    } else if (!safe && needs_seed(x, plan) && env_int("VS_PREPASS", 1)) {
-        rc = seed_thresholds(x, pq,
-                             std::max<int64_t>(1 << 16, x->ntotal / std::max(2, env_int("VS_PREPASS_DIV", 1024))),
-                             kk, nlist);
-        if (rc) return rc;
-    }
-    note_scan_kind(x, plan);
-    VS_HIP(hipMemsetAsync(x->flags.p, 0, sizeof(uint32_t), x->st), "clearing flags");
-    VS_HIP(hipMemsetAsync(x->lcnt.as<int32_t>() + nlists, 0, 4, x->st), "list counts");
+    size_t e0 = 0, l0 = 0;
+    if (guess) rc = guess_thresholds(x, pq, kk, gthr, &L, &e0, &l0);
+    else if (seed) rc = seed_thresholds(x, pq, seed_S, kk, gthr, &L, &e0, &l0, 0, -1, list_budget);
+    if (rc) return rc;
+    if (!x->prof_fixed) note_scan_kind(x, plan);
+    VS_HIP(vs::launch_fill32(L.cnt + list_count(plan), 1, 0u, x->st), "list counts");
     {
         ProfScope ps(x, "scan");
         VS_HIP(vs::launch_scan_topk(x->xb, x->storage, x->ld, x->xn, x->ntotal, x->metric, pq, plan,
-                                    x->cand_v.as<float>(), x->cand_i.as<int32_t>(),
-                                    x->gthr.as<uint32_t>(), x->lbound.as<float>(),
-                                    x->lcnt.as<int32_t>(), x->st),
+                                    L.v, L.i, gthr, (float *)p_lb, L.cnt, x->st),
                "scan kernel");
     }
+    vs::TopkCheck chk;
+    VS_TAKE(xnorm_max(x, A, &chk.xmax));
+    topk_error_model(x, pq.planes, &chk);
+    chk.vx_count = ctl + 2;
+    chk.vx_list = (int32_t *)p_vx;
     {
         ProfScope ps(x, "merge");
-        VS_HIP(vs::launch_merge_refine(x->xb, x->storage, x->ld, x->d, x->metric, pq, plan,
-                                       x->cand_v.as<float>(), x->cand_i.as<int32_t>(),
-                                       x->gthr.as<uint32_t>(), x->lbound.as<float>(),
-                                       x->vf.as<int32_t>(), x->vf.as<int32_t>() + 1, k, D, I,
-                                       x->ntotal, x->flags.as<uint32_t>(), guess ? 1 : 0,
-                                       x->lcnt.as<int32_t>(), x->st),
+        VS_HIP(vs::launch_merge_refine(x->xb, x->storage, x->ld, x->d, x->metric, pq, plan, L.v, L.i,
+                                       gthr, (float *)p_lb, ctl + 1, (int32_t *)p_vf, k, D, I,
+                                       x->ntotal, (uint32_t *)ctl, guess ? 1 : 0, L.cnt, &chk,
+                                       x->st),
                "merge kernel");
     }
-    uint32_t mflags = 0;
-    VS_HIP(hipMemcpyAsync(&mflags, x->flags.p, sizeof mflags, hipMemcpyDeviceToHost, x->st),
-           "merge flags");
-    if (verify || guess) {
-        // queries whose shortened lists may have dropped a winner, or whose
-        // estimated threshold left fewer than kk_final candidates, are
-        // searched again with full-length lists and no estimate (exact; rare
-        // for unordered data)
-        int32_t nvf = 0;
-        VS_HIP(hipMemcpyAsync(&nvf, x->vf.p, 4, hipMemcpyDeviceToHost, x->st), "verification");
-        VS_HIP(hipStreamSynchronize(x->st), "search");
-        if (nvf > 0) {
-            std::vector<int32_t> lst((size_t)nvf);
-            VS_HIP(hipMemcpy(lst.data(), x->vf.as<int32_t>() + 1, (size_t)nvf * 4,
-                             hipMemcpyDeviceToHost),
-                   "verification list");
-            std::sort(lst.begin(), lst.end());
-            VS_HIP(x->fbq.ensure((size_t)nvf * x->d * 4), "fallback queries");
-            for (int32_t i = 0; i < nvf; ++i)
-                VS_HIP(hipMemcpyAsync(x->fbq.as<float>() + (size_t)i * x->d,
-                                      pq.qf + (size_t)lst[(size_t)i] * x->d, (size_t)x->d * 4,
-                                      hipMemcpyDeviceToDevice, x->st),
-                       "fallback gather");
-            VS_HIP(x->fbD.ensure((size_t)nvf * k * 4), "fallback results");
-            VS_HIP(x->fbI.ensure((size_t)nvf * k * 4), "fallback results");
-            rc = search_device(x, x->fbq.p, VS_DTYPE_F32, nvf, k, x->fbD.as<float>(),
-                               x->fbI.as<int32_t>(), true);
-            if (rc) return rc;
-            for (int32_t i = 0; i < nvf; ++i) {
-                VS_HIP(hipMemcpyAsync(D + (size_t)lst[(size_t)i] * k, x->fbD.as<float>() + (size_t)i * k,
-                                      (size_t)k * 4, hipMemcpyDeviceToDevice, x->st),
-                       "fallback scatter");
-                VS_HIP(hipMemcpyAsync(I + (size_t)lst[(size_t)i] * k, x->fbI.as<int32_t>() + (size_t)i * k,
-                                      (size_t)k * 4, hipMemcpyDeviceToDevice, x->st),
-                       "fallback scatter");
-            }
-            auto &e = x->prof["fallback"];
-            e.launches += nvf;
-        }
-    }
+    int32_t hc[4] = {0, 0, 0, 0};
+    VS_HIP(hipMemcpyAsync(hc, ctl, sizeof hc, hipMemcpyDeviceToHost, x->st), "merge flags");
     VS_HIP(hipStreamSynchronize(x->st), "search");
-    if (mflags & vs::kFlagBadId)
+    if ((uint32_t)hc[0] & vs::kFlagBadId)
         return set_err(VS_ERR_HIP, "internal error: a candidate id outside the index reached the merge");
+    // queries whose shortened lists may have dropped a winner, or whose
+    // estimated threshold left fewer than kk_final candidates, are searched
+    // again with full-length lists and no estimate; queries whose selection
+    // the accumulator's error could have changed go to the exact path
+    // (both rare for unordered data)
+    // (the exact path first: the re-search prepares its queries into the
+    // index's query buffers, which both gathers read)
+    rc = research_listed(x, A, pq, (const int32_t *)p_vx, hc[2], k, D, I, 1);
+    if (rc) return rc;
+    rc = research_listed(x, A, pq, (const int32_t *)p_vf, hc[1], k, D, I, 0);
+    if (rc) return rc;
+    VS_HIP(hipStreamSynchronize(x->st), "search");
     return VS_OK;
-}
-
-float xnorm_max(vs_index *x) {
-    if (x->ntotal == 0) return 0.f;
-    if (x->misc.ensure(sizeof(float)) != hipSuccess) return INFINITY;
-    if (vs::launch_max_reduce(x->xn, x->ntotal, x->misc.as<float>(), x->st) != hipSuccess)
-        return INFINITY;
-    float m = 0.f;
-    if (hipMemcpyAsync(&m, x->misc.p, sizeof m, hipMemcpyDeviceToHost, x->st) != hipSuccess)
-        return INFINITY;
-    if (hipStreamSynchronize(x->st) != hipSuccess) return INFINITY;
-    return std::sqrt(m) * (1.0f + 1e-6f);
 }
 
 struct RangeHits {
@@ -1064,7 +1280,9 @@ int range_core(vs_index *x, const vs::PreparedQueries &pq, double radius, int se
             scan_storage = 1;
         }
     }
-    const float xmax = xnorm_max(x);
+    Arena A;
+    float xmax = 0.f;
+    VS_TAKE(xnorm_max(x, A, &xmax));
     VS_HIP(x->athr.ensure((size_t)pq.nq * 4), "range bounds");
     const int exact_q = (qflags & vs::kFlagNotBf16) ? 0 : 1;
     const int exact_x = x->storage == 1 ? 1 : 0;
@@ -1220,11 +1438,12 @@ void vs_index_destroy(vs_index *x) {
                       &x->km_fb,   &x->km_keys,   &x->km_order, &x->km_tmp,   &x->km_counts,
                       &x->km_offsets, &x->km_out, &x->km_iota, &x->lcnt,   &x->km_qp,
                       &x->km_qf,   &x->km_qnorm,  &x->km_cen16, &x->km_c16n, &x->xb16,
-                      &x->xb16n};
+                      &x->xb16n,   &x->vx,        &x->ctl};
     for (DevBuf *b : bufs) b->release();
     x->km_hbest.release();
     x->km_hassign.release();
     x->km_hcen.release();
+    x->rstage.release();
     if (x->st_copy) {
         (void)hipStreamSynchronize(x->st_copy);
         (void)hipStreamDestroy(x->st_copy);
@@ -1329,16 +1548,28 @@ int vs_index_reconstruct(vs_index *x, int64_t i0, int64_t n, float *out) {
     if (!out) return set_err(VS_ERR_INVALID, "null output");
     DeviceGuard g(x->device);
     const int64_t rb = row_bytes(x);
-    std::vector<char> tmp((size_t)n * rb);
-    VS_HIP(hipMemcpyAsync(tmp.data(), (const char *)x->xb + (size_t)i0 * rb, (size_t)n * rb,
-                          hipMemcpyDeviceToHost, x->st),
-           "reading rows");
-    VS_HIP(hipStreamSynchronize(x->st), "reading rows");
-    for (int64_t r = 0; r < n; ++r)
-        for (int64_t j = 0; j < x->d; ++j)
-            out[r * x->d + j] = x->storage == 1
-                                    ? bf16_to_f32(((const uint16_t *)(tmp.data() + r * rb))[j])
-                                    : ((const float *)(tmp.data() + r * rb))[j];
+    // rows come through a pinned staging buffer of at most 64 MiB
+    const int64_t per = std::max<int64_t>(1, std::min<int64_t>(n, (int64_t)(64 << 20) / rb));
+    VS_HIP(x->rstage.ensure((size_t)per * rb), "pinned staging");
+    for (int64_t r0 = 0; r0 < n; r0 += per) {
+        const int64_t m = std::min(per, n - r0);
+        VS_HIP(hipMemcpyAsync(x->rstage.p, (const char *)x->xb + (size_t)(i0 + r0) * rb,
+                              (size_t)m * rb, hipMemcpyDeviceToHost, x->st),
+               "reading rows");
+        VS_HIP(hipStreamSynchronize(x->st), "reading rows");
+        const char *src = x->rstage.as<char>();
+        float *dst = out + r0 * x->d;
+        if (x->storage == 1) {
+            for (int64_t r = 0; r < m; ++r) {
+                const uint16_t *h = (const uint16_t *)(src + r * rb);
+                float *o = dst + r * x->d;
+                for (int64_t j = 0; j < x->d; ++j) o[j] = bf16_to_f32(h[j]);
+            }
+        } else {
+            for (int64_t r = 0; r < m; ++r)
+                memcpy(dst + r * x->d, src + r * rb, (size_t)x->d * 4);
+        }
+    }
     return VS_OK;
 }
 
@@ -1394,7 +1625,8 @@ int vs_index_search_device(vs_index *x, const void *q_dev, int q_dtype, int64_t 
     if (nq > 0 && k > 0 && (!q_dev || !D_dev || !I_dev))
         return set_err(VS_ERR_INVALID, "null query or output buffer");
     DeviceGuard g(x->device);
-    return search_device(x, q_dev, q_dtype, nq, k, D_dev, I_dev);
+    Arena A;
+    return search_device(x, A, q_dev, q_dtype, nq, k, D_dev, I_dev);
 }
 
 int vs_index_search(vs_index *x, const void *q, int q_dtype, int64_t nq, int64_t k, float *D,
@@ -1408,10 +1640,12 @@ int vs_index_search(vs_index *x, const void *q, int q_dtype, int64_t nq, int64_t
     const size_t qbytes = (size_t)nq * x->d * (q_dtype == 1 ? 2 : 4);
     VS_HIP(x->stage.ensure(qbytes), "query staging");
     VS_HIP(hipMemcpyAsync(x->stage.p, q, qbytes, hipMemcpyHostToDevice, x->st), "uploading queries");
-    if (k == 0) return search_device(x, x->stage.p, q_dtype, nq, k, nullptr, nullptr);
+    Arena A;
+    if (k == 0) return search_device(x, A, x->stage.p, q_dtype, nq, k, nullptr, nullptr);
     VS_HIP(x->outD.ensure((size_t)nq * k * 4), "result buffer");
     VS_HIP(x->outI.ensure((size_t)nq * k * 4), "result buffer");
-    int rc = search_device(x, x->stage.p, q_dtype, nq, k, x->outD.as<float>(), x->outI.as<int32_t>());
+    int rc = search_device(x, A, x->stage.p, q_dtype, nq, k, x->outD.as<float>(),
+                           x->outI.as<int32_t>());
     if (rc) return rc;
     VS_HIP(hipMemcpyAsync(D, x->outD.p, (size_t)nq * k * 4, hipMemcpyDeviceToHost, x->st),
            "reading distances");
@@ -1439,7 +1673,8 @@ int vs_index_range_search(vs_index *x, const void *q, int q_dtype, int64_t nq, d
                "uploading queries");
         vs::PreparedQueries pq;
         uint32_t f = 0;
-        int rc = prepare_queries(x, x->stage.p, q_dtype, x->d, nq, &pq, &f);
+        Arena A;
+        int rc = prepare_queries(x, A, x->stage.p, q_dtype, x->d, nq, &pq, &f);
         if (rc) return rc;
         rc = range_core(x, pq, radius, 0, f, &hits);
         if (rc) return rc;
@@ -1483,7 +1718,8 @@ int vs_index_self_join(vs_index *x, double threshold, vs_pairs **out) {
     if (x->ntotal > 1) {
         vs::PreparedQueries pq;
         uint32_t f = 0;
-        int rc = prepare_queries(x, x->xb, x->storage, x->ld, x->ntotal, &pq, &f);
+        Arena A;
+        int rc = prepare_queries(x, A, x->xb, x->storage, x->ld, x->ntotal, &pq, &f);
         if (rc) return rc;
         rc = range_core(x, pq, threshold, 1, f, &hits);
         if (rc) return rc;
@@ -1532,6 +1768,7 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
                        (long long)K, (long long)x->ntotal);
     if (K > (int64_t)INT32_MAX) return set_err(VS_ERR_INVALID, "K too large");
     DeviceGuard g(x->device);
+    Arena A;
     const int64_t n = x->ntotal, d = x->d, ld = x->ld;
     std::vector<float> cen_in(centroids_in, centroids_in + K * d);  // centroids_out may alias
 
@@ -1563,8 +1800,8 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     // across iterations while the stored rows are unchanged)
     if (x->km_prep_version != x->version) {
         x->km_prep_version = ~0ull;
-        int rc0 = prepare_queries(x, x->xb, 0, ld, n, &x->km_pq, &x->km_pflags, &x->km_qp,
-                                  &x->km_qf, &x->km_qnorm);
+        int rc0 = prepare_queries(x, A, x->xb, 0, ld, n, &x->km_pq, &x->km_pflags, x->km_qp,
+                                  x->km_qf, x->km_qnorm);
         if (rc0) return rc0;
         x->km_prep_version = x->version;
     }
@@ -1587,7 +1824,8 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
         rc = plan_scan(&cview, n, K, pq.planes, 16, 0, &plan);
         if (rc) return rc;
     }
-    const float pmax = xnorm_max(x);
+    float pmax = 0.f;
+    VS_TAKE(xnorm_max(x, A, &pmax));
     // Error of the accumulator |c|^2 - 2 x.c (point x, centroid c):
     //  - operands: each product of the MFMA operands lies within r |2 x_j c_j|
     //    of -2 x_j c_j, r = 2^-8 for the one-pass selection (both operands

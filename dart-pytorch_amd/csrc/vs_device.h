@@ -183,4 +183,61 @@ __device__ __forceinline__ bool map_block_grouped(int64_t nqblk, int64_t nsplit,
     return *qblk < nqblk;
 }
 
+// ---------------------------------------------------------------------------
+// Exact score of (query, row) in the reference's arithmetic: fp64 sum over
+// j = 0..d-1 in order of q[j]*x[j] (IP) or (q[j]-x[j])^2 (L2), with the fp32
+// values promoted to fp64 (index_flat.dart:78-88; index.dart:181-200).
+// Rows are zero past d and so is q (qrow must hold ld values, zero past d):
+// the extra terms add +0.0 to the sum.
+// ---------------------------------------------------------------------------
+template <int ST>
+__device__ double exact_score(const float *qrow, const void *xb, int64_t ld, int64_t id,
+                              int64_t d, int metric) {
+    // the row is read 64 elements at a time (one batch of independent 16-byte
+    // loads, so a candidate costs a few memory round trips, not one per 16
+    // bytes); ld is a multiple of 64 elements, so every load stays in the
+    // row.  Elements past d are zero in the row and in qrow: their terms are
+    // +0, and s (which starts at +0 and is never -0) is unchanged by them.
+    double s = 0.0;
+    const int64_t dend = (d + 7) & ~(int64_t)7;
+    auto term = [&](double qv, double xv) __attribute__((always_inline)) {
+        if (metric == 0) {
+            const double diff = qv - xv;
+            s = s + diff * diff;
+        } else {
+            s = s + qv * xv;
+        }
+    };
+    if constexpr (ST == 1) {
+        const uint16_t *x = (const uint16_t *)xb + id * ld;
+        for (int64_t j0 = 0; j0 < dend; j0 += 64) {
+            uint4 raw[8];
+#pragma unroll
+            for (int c = 0; c < 8; ++c) raw[c] = *(const uint4 *)(x + j0 + 8 * c);
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const uint16_t *h = (const uint16_t *)&raw[c];
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    term((double)qrow[j0 + 8 * c + u], (double)bf16_to_f32(h[u]));
+            }
+        }
+    } else {
+        const float *x = (const float *)xb + id * ld;
+        for (int64_t j0 = 0; j0 < dend; j0 += 64) {
+            float4 raw[16];
+#pragma unroll
+            for (int c = 0; c < 16; ++c) raw[c] = *(const float4 *)(x + j0 + 4 * c);
+#pragma unroll
+            for (int c = 0; c < 16; ++c) {
+                term((double)qrow[j0 + 4 * c + 0], (double)raw[c].x);
+                term((double)qrow[j0 + 4 * c + 1], (double)raw[c].y);
+                term((double)qrow[j0 + 4 * c + 2], (double)raw[c].z);
+                term((double)qrow[j0 + 4 * c + 3], (double)raw[c].w);
+            }
+        }
+    }
+    return s;
+}
+
 }  // namespace vs

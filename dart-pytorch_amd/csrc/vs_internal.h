@@ -124,6 +124,18 @@ hipError_t launch_scan_topk(const void *xb, int storage, int64_t ld, const float
                             float *cand_v, int32_t *cand_i, uint32_t *gthr, float *lbound,
                             int32_t *list_cnt, hipStream_t st);
 
+// Exactness check of a top-k merge: the largest stored row norm and the
+// accumulator's error model (relative error err_r of one product of MFMA
+// operands, accumulation factor err_g); queries whose selection cannot be
+// proven exact are appended to vx_list (count in *vx_count).
+struct TopkCheck {
+    float xmax = 0.f;
+    float err_r = 0.f;
+    float err_g = 0.f;
+    int32_t *vx_count = nullptr;
+    int32_t *vx_list = nullptr;
+};
+
 // Merge the per-wave lists of each query, re-rank the kk survivors with the
 // exact fp64 distance and write the k best (sentinel-filled) to D / I.
 // Queries the merge cannot prove exact are appended to vf_list (count in
@@ -135,7 +147,34 @@ hipError_t launch_merge_refine(const void *xb, int storage, int64_t ld, int64_t 
                                const float *cand_v, const int32_t *cand_i, const uint32_t *gthr,
                                const float *lbound, int32_t *vf_count, int32_t *vf_list,
                                int64_t k, float *D, int32_t *I, int64_t nrows, uint32_t *flags,
-                               int guess, const int32_t *list_cnt, hipStream_t st);
+                               int guess, const int32_t *list_cnt, const TopkCheck *chk,
+                               hipStream_t st);
+
+// Exact top-kk lists of nq queries (fp32 rows qf [nq][d]): rows of split s
+// are [s * rows_per_split, ...); lists cand_v / cand_i [nq][nsplit][kk] hold
+// (fp32 key, id), key = score (L2) or -score (IP), sentinels (+inf, -1).
+// kk: a multiple of 4 in [4, 512].
+hipError_t launch_exact_lists(const void *xb, int storage, int64_t ld, int64_t d, int metric,
+                              const float *qf, int64_t nq, int64_t n, int kk, int64_t nsplit,
+                              int64_t rows_per_split, float *cand_v, int32_t *cand_i,
+                              hipStream_t st);
+
+// Row gather / scatter of w 32-bit words per row by an index list, and a
+// 32-bit fill.
+hipError_t launch_gather_rows(const void *src, const int32_t *list, int64_t m, int64_t w,
+                              void *dst, hipStream_t st);
+hipError_t launch_scatter_rows(const void *src, const int32_t *list, int64_t m, int64_t w,
+                               void *dst, hipStream_t st);
+hipError_t launch_fill32(void *p, int64_t n, uint32_t v, hipStream_t st);
+
+// Exact top-k by sorting (any k): for nq queries (fp32 rows qf [nq][d]) the
+// fp64 score of every row, as keys (fp32 key code, id), sorted per query;
+// D / I [nq][k] receive the k first, sentinel-filled past n.  keys holds
+// qchunk * n + n words of 64 bits, tmp tmp_bytes (query with tmp == nullptr).
+hipError_t exact_sort_topk(const void *xb, int storage, int64_t ld, int64_t d, int metric,
+                           const float *qf, int64_t nq, int64_t n, int64_t k, float *D, int32_t *I,
+                           uint64_t *keys, int64_t qchunk, void *tmp, size_t &tmp_bytes,
+                           hipStream_t st);
 
 // Threshold seeding from a pre-pass scan: every query's shared threshold
 // (gthr) is tightened to one code above the seed_rank-th (0: kk_final-th)

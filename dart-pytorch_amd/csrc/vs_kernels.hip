@@ -653,63 +653,6 @@ hipError_t launch_scan_range(const void *xb, int storage, int64_t ld, const floa
 }
 
 // ---------------------------------------------------------------------------
-// Exact score of (query, row) in the reference's arithmetic: fp64 sum over
-// j = 0..d-1 in order of q[j]*x[j] (IP) or (q[j]-x[j])^2 (L2), with the fp32
-// values promoted to fp64 (index_flat.dart:78-88; index.dart:181-200).
-// Rows are zero past d and so is q (qrow must hold ld values, zero past d):
-// the extra terms add +0.0 to the sum.
-// ---------------------------------------------------------------------------
-template <int ST>
-__device__ double exact_score(const float *qrow, const void *xb, int64_t ld, int64_t id,
-                              int64_t d, int metric) {
-    // the row is read 64 elements at a time (one batch of independent 16-byte
-    // loads, so a candidate costs a few memory round trips, not one per 16
-    // bytes); ld is a multiple of 64 elements, so every load stays in the
-    // row.  Elements past d are zero in the row and in qrow: their terms are
-    // +0, and s (which starts at +0 and is never -0) is unchanged by them.
-    double s = 0.0;
-    const int64_t dend = (d + 7) & ~(int64_t)7;
-    auto term = [&](double qv, double xv) __attribute__((always_inline)) {
-        if (metric == 0) {
-            const double diff = qv - xv;
-            s = s + diff * diff;
-        } else {
-            s = s + qv * xv;
-        }
-    };
-    if constexpr (ST == 1) {
-        const uint16_t *x = (const uint16_t *)xb + id * ld;
-        for (int64_t j0 = 0; j0 < dend; j0 += 64) {
-            uint4 raw[8];
-#pragma unroll
-            for (int c = 0; c < 8; ++c) raw[c] = *(const uint4 *)(x + j0 + 8 * c);
-#pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                const uint16_t *h = (const uint16_t *)&raw[c];
-#pragma unroll
-                for (int u = 0; u < 8; ++u)
-                    term((double)qrow[j0 + 8 * c + u], (double)bf16_to_f32(h[u]));
-            }
-        }
-    } else {
-        const float *x = (const float *)xb + id * ld;
-        for (int64_t j0 = 0; j0 < dend; j0 += 64) {
-            float4 raw[16];
-#pragma unroll
-            for (int c = 0; c < 16; ++c) raw[c] = *(const float4 *)(x + j0 + 4 * c);
-#pragma unroll
-            for (int c = 0; c < 16; ++c) {
-                term((double)qrow[j0 + 4 * c + 0], (double)raw[c].x);
-                term((double)qrow[j0 + 4 * c + 1], (double)raw[c].y);
-                term((double)qrow[j0 + 4 * c + 2], (double)raw[c].z);
-                term((double)qrow[j0 + 4 * c + 3], (double)raw[c].w);
-            }
-        }
-    }
-    return s;
-}
-
-// ---------------------------------------------------------------------------
 // Merge + exact re-rank.  One workgroup (256 threads) per query.
 //   1. stream the query's per-wave lists, keeping entries that beat the
 //      current kk-th best, sorting when the LDS buffer fills;
@@ -751,6 +694,17 @@ struct MergeKArgs {
     int64_t k;
     float *D;
     int32_t *I;
+    // Exactness check of the top-k selection (MODE 0, vx_list non-null).
+    // Every row outside the kk kept ones has an accumulator at or above the
+    // kk-th kept value, and an accumulator lies within
+    //   err(q) = 1.25 (err_r s |q| xmax + err_g (xn_max + s |q| xmax))
+    // of the exact xn - 2 q.x (L2, s = 2, xn_max = xmax^2) or -q.x (IP,
+    // s = 1, xn_max = 0).  A query whose exact k-th result does not lie
+    // below (kk-th kept value - err(q)) is appended to vx_list.
+    const float *qnorm;
+    float xmax, err_r, err_g;
+    int32_t *vx_count;
+    int32_t *vx_list;
     // k-means argmin mode
     float bound;
     int32_t *assign;
@@ -975,6 +929,8 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
     // thresholds is below the kk-th kept value.  An estimated threshold
     // dropped every row at or above it; the result is exact when kk
     // candidates were still found below it.  Otherwise flag the query.
+    __shared__ int s_vf;  // the query went to vf_list
+    if (tid == 0) s_vf = 0;
     if (MODE == 0 && (a.lbound || a.guess)) {
         __shared__ float s_lmin[4];
         float lmin = VS_INF;
@@ -991,7 +947,10 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
             const float m = fminf(fminf(s_lmin[0], s_lmin[1]), fminf(s_lmin[2], s_lmin[3]));
             // (s_thr, s_thr_id): the kk-th kept pair, a sentinel if fewer were found
             const bool short_list = a.guess && s_thr_id == INT_MAX && a.nrows >= kk;
-            if (m < s_thr || short_list) a.vf_list[atomicAdd(a.vf_count, 1)] = (int32_t)qg;
+            if (m < s_thr || short_list) {
+                a.vf_list[atomicAdd(a.vf_count, 1)] = (int32_t)qg;
+                s_vf = 1;
+            }
         }
     }
 
@@ -1028,6 +987,31 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
             a.D[qg * a.k + t] = ok ? (a.metric == 0 ? bv[t] : -bv[t])
                                    : (a.metric == 0 ? VS_INF : -VS_INF);
             a.I[qg * a.k + t] = ok ? bi[t] : -1;
+        }
+        // Exactness of the selection: any row outside the kk kept has an
+        // exact accumulator >= s_thr - err(q).  The k-th result's exact
+        // accumulator (score - |q|^2 for L2, -score for IP; its fp32 key is
+        // within 2^-24 relative of the fp64 score) must lie below that, or
+        // the query is flagged for the exact path.  Queries already sent to
+        // vf_list are searched again anyway.
+        if (a.vx_list && tid < 64 && a.k <= kk) {
+            double qq = 0.0;
+            if (a.metric == 0) {
+                for (int64_t j = tid; j < a.d; j += 64) qq += (double)qsh[j] * (double)qsh[j];
+                for (int o = 32; o > 0; o >>= 1) qq += __shfl_xor(qq, o);
+            }
+            if (tid == 0 && !s_vf && bi[a.k - 1] != INT_MAX && s_thr < VS_INF) {
+                const double s = a.metric == 0 ? 2.0 : 1.0;
+                const double qn = a.qnorm[qg], xm = a.xmax;
+                const double err = 1.25 * ((double)a.err_r * s * qn * xm +
+                                           (double)a.err_g * ((a.metric == 0 ? xm * xm : 0.0) +
+                                                              s * qn * xm)) +
+                                   1e-30;
+                const double key = bv[a.k - 1];
+                double ek = key + fabs(key) * (1.0 / 8388608.0);
+                if (a.metric == 0) ek -= qq * (1.0 - 1e-12);  // qq: fp64 sum, error < d 2^-53 qq
+                if (!(ek < (double)s_thr - err)) a.vx_list[atomicAdd(a.vx_count, 1)] = (int32_t)qg;
+            }
         }
     } else {
         // argmin over (exact score, id): smallest score, lowest id among
@@ -1079,10 +1063,19 @@ hipError_t launch_merge_refine(const void *xb, int storage, int64_t ld, int64_t 
                                const float *cand_v, const int32_t *cand_i, const uint32_t *gthr,
                                const float *lbound, int32_t *vf_count, int32_t *vf_list,
                                int64_t k, float *D, int32_t *I, int64_t nrows, uint32_t *flags,
-                               int guess, const int32_t *list_cnt, hipStream_t st) {
+                               int guess, const int32_t *list_cnt, const TopkCheck *chk,
+                               hipStream_t st) {
     if (pq.nq <= 0) return hipSuccess;
     MergeKArgs a{};
     a.guess = guess;
+    if (chk) {
+        a.qnorm = pq.qnorm;
+        a.xmax = chk->xmax;
+        a.err_r = chk->err_r;
+        a.err_g = chk->err_g;
+        a.vx_count = chk->vx_count;
+        a.vx_list = chk->vx_list;
+    }
     a.list_cnt = plan.kind == 3 ? list_cnt : nullptr;
     if (plan.kind == 3 && !list_cnt) return hipErrorInvalidValue;
     a.xb = xb;
@@ -1097,8 +1090,6 @@ hipError_t launch_merge_refine(const void *xb, int storage, int64_t ld, int64_t 
     a.lw = plan.lw;
     a.kk = plan.kk_final;
     a.kl = a.list_cnt ? plan.cap : plan.kk;
-    a.nlists_all = plan.nqblk * plan.nsplit * plan.lw * plan.bn;
-
     a.nlists_all = plan.nqblk * plan.nsplit * plan.lw * plan.bn;
 
     a.cap = plan.cap;
@@ -1120,6 +1111,150 @@ hipError_t launch_merge_refine(const void *xb, int storage, int64_t ld, int64_t 
         if (e != hipSuccess) return e;
     }
     hipLaunchKernelGGL(fn, dim3((unsigned)pq.nq), dim3(256), lds, st, a);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Exact top-kk lists: one workgroup per (query, split) scores every row of
+// its split with the reference's fp64 arithmetic (exact_score) and keeps the
+// kk best (key, id) pairs, key = fp32 score (L2) or -fp32 score (IP), in
+// (key, id) order -- the order the merge's re-rank sorts by.  The lists
+// ([nq][nsplit][kk], sentinels (+inf, -1)) then go through the merge, whose
+// selection over exact keys is exact.  This is the path for queries whose
+// approximate selection could not be proven exact.
+// ---------------------------------------------------------------------------
+struct ExactKArgs {
+    const void *xb;
+    int64_t ld, d;
+    int metric;
+    const float *qf;  // [nq][d]
+    int64_t nq, n;
+    int kk;
+    int64_t nsplit, rows_per_split;
+    float *cand_v;
+    int32_t *cand_i;
+};
+
+template <int ST>
+__global__ __launch_bounds__(256) void exact_lists_kernel(ExactKArgs a) {
+    extern __shared__ __align__(16) char smem[];
+    float *bv = (float *)smem;                    // [kMergeBuf]
+    int *bi = (int *)(bv + kMergeBuf);            // [kMergeBuf]
+    float *qsh = (float *)(bi + kMergeBuf);       // [ld]
+    float *tmp_v = qsh + a.ld;                    // [kMergeKeepMax]
+    int *tmp_i = (int *)(tmp_v + kMergeKeepMax);  // [kMergeKeepMax]
+    __shared__ SelScratch sel;
+    __shared__ int s_cnt;
+    __shared__ float s_thr;
+    __shared__ int s_thr_id;
+
+    const int64_t q = blockIdx.x % a.nq, split = blockIdx.x / a.nq;
+    const int tid = threadIdx.x;
+    const int kk = a.kk;
+    for (int t = tid; t < kk; t += 256) {
+        bv[t] = VS_INF;
+        bi[t] = INT_MAX;
+    }
+    if (tid == 0) {
+        s_cnt = 0;
+        s_thr = VS_INF;
+        s_thr_id = INT_MAX;
+    }
+    for (int64_t j = tid; j < a.ld; j += 256) qsh[j] = j < a.d ? a.qf[q * a.d + j] : 0.0f;
+    __syncthreads();
+    const int64_t r0 = split * a.rows_per_split;
+    const int64_t r1 = min(a.n, r0 + a.rows_per_split);
+    for (int64_t base = r0; base < r1; base += 256) {
+        const int64_t t = base + tid;
+        if (t < r1) {
+            const double ex = exact_score<ST>(qsh, a.xb, a.ld, t, a.d, a.metric);
+            const float key = a.metric == 0 ? (float)ex : -(float)ex;
+            const float th = s_thr;
+            const int thi = s_thr_id;
+            if (key < th || (key == th && (int)t < thi)) {
+                const int pos = atomicAdd(&s_cnt, 1);
+                bv[kk + pos] = key;
+                bi[kk + pos] = (int)t;
+            }
+        }
+        __syncthreads();
+        const int c = s_cnt;
+        if (c > kMergeBuf - kk - 256 || (base + 256 >= r1 && c > 0)) {
+            select_block(bv, bi, kk + c, kk, tmp_v, tmp_i, sel, &s_thr, &s_thr_id);
+            if (tid == 0) s_cnt = 0;
+        }
+        __syncthreads();
+    }
+    for (int t = tid; t < kk; t += 256) {
+        const int64_t off = (q * a.nsplit + split) * kk + t;
+        const bool real = bi[t] != INT_MAX;
+        a.cand_v[off] = real ? bv[t] : VS_INF;
+        a.cand_i[off] = real ? bi[t] : -1;
+    }
+}
+
+hipError_t launch_exact_lists(const void *xb, int storage, int64_t ld, int64_t d, int metric,
+                              const float *qf, int64_t nq, int64_t n, int kk, int64_t nsplit,
+                              int64_t rows_per_split, float *cand_v, int32_t *cand_i,
+                              hipStream_t st) {
+    if (nq <= 0) return hipSuccess;
+    if (kk < 4 || kk > kMergeKeepMax || (kk & 3) || nsplit < 1 || nq * nsplit > INT32_MAX)
+        return hipErrorInvalidValue;
+    ExactKArgs a{xb, ld, d, metric, qf, nq, n, kk, nsplit, rows_per_split, cand_v, cand_i};
+    const size_t lds = merge_lds(ld);
+    void (*fn)(ExactKArgs) = storage == 1 ? exact_lists_kernel<1> : exact_lists_kernel<0>;
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute((const void *)fn,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(fn, dim3((unsigned)(nq * nsplit)), dim3(256), lds, st, a);
+    return hipGetLastError();
+}
+
+// dst[i][0..w) = src[list[i]][0..w), 32-bit words
+__global__ void gather_rows_kernel(const uint32_t *__restrict__ src, const int32_t *__restrict__ list,
+                                   int64_t m, int64_t w, uint32_t *__restrict__ dst) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= m * w) return;
+    const int64_t i = t / w, j = t % w;
+    dst[t] = src[(int64_t)list[i] * w + j];
+}
+
+// dst[list[i]][0..w) = src[i][0..w), 32-bit words
+__global__ void scatter_rows_kernel(const uint32_t *__restrict__ src, const int32_t *__restrict__ list,
+                                    int64_t m, int64_t w, uint32_t *__restrict__ dst) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= m * w) return;
+    const int64_t i = t / w, j = t % w;
+    dst[(int64_t)list[i] * w + j] = src[t];
+}
+
+hipError_t launch_gather_rows(const void *src, const int32_t *list, int64_t m, int64_t w,
+                              void *dst, hipStream_t st) {
+    if (m <= 0 || w <= 0) return hipSuccess;
+    gather_rows_kernel<<<dim3((unsigned)((m * w + 255) / 256)), dim3(256), 0, st>>>(
+        (const uint32_t *)src, list, m, w, (uint32_t *)dst);
+    return hipGetLastError();
+}
+
+hipError_t launch_scatter_rows(const void *src, const int32_t *list, int64_t m, int64_t w,
+                               void *dst, hipStream_t st) {
+    if (m <= 0 || w <= 0) return hipSuccess;
+    scatter_rows_kernel<<<dim3((unsigned)((m * w + 255) / 256)), dim3(256), 0, st>>>(
+        (const uint32_t *)src, list, m, w, (uint32_t *)dst);
+    return hipGetLastError();
+}
+
+// fill n 32-bit words with v (a kernel rather than a memset node)
+__global__ void fill32_kernel(uint32_t *p, int64_t n, uint32_t v) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t < n) p[t] = v;
+}
+
+hipError_t launch_fill32(void *p, int64_t n, uint32_t v, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    fill32_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>((uint32_t *)p, n, v);
     return hipGetLastError();
 }
 
@@ -1922,7 +2057,7 @@ __global__ void max_reduce_kernel(const float *__restrict__ x, int64_t n, float 
 }
 
 hipError_t launch_max_reduce(const float *x, int64_t n, float *out, hipStream_t st) {
-    hipError_t e = hipMemsetAsync(out, 0, sizeof(float), st);
+    hipError_t e = launch_fill32(out, 1, 0u, st);
     if (e != hipSuccess || n <= 0) return e;
     max_reduce_kernel<<<dim3(1024), dim3(256), 0, st>>>(x, n, out);
     return hipGetLastError();
@@ -1977,9 +2112,15 @@ hipError_t launch_compact_rows(const void *src, void *dst, const float *xn_src, 
 // ---------------------------------------------------------------------------
 // Synthetic data: Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random
 // numbers: as easy as 1, 2, 3", SC'11) keyed by the seed, counter = (element
-// group, row-major position / 4, stream); Box-Muller on pairs of uniforms.
-// One wave per row; with normalize the row is scaled by 1/sqrt(fp64 sum of
-// squares), the L2NormTransform convention (l2_norm_transform.dart:23-46).
+// group g as 64 bits, stream as 64 bits) with g = row * groups + group, four
+// values per group.  Box-Muller in fp64 on each pair of 32-bit outputs (a, b):
+// u1 = ((a >> 8) + 1) 2^-24 in (0, 1], u2 = (b >> 8) 2^-24 in [0, 1),
+// r = sqrt(-2 log u1), z0 = fp32(r cos(2 pi u2)), z1 = fp32(r sin(2 pi u2)).
+// With normalize each row is scaled the L2NormTransform way
+// (l2_norm_transform.dart:23-46): s = the fp64 sum of v * v in dimension
+// order, inv = 1 / sqrt(s), o = fp32(v * inv), zero rows stay zero; bf16
+// output rounds o to nearest even.  One wave per row: each lane makes its
+// groups' values, and the in-order sum reads them lane by lane.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ uint4 philox4x32_10(uint4 c, uint2 k) {
     const uint32_t M0 = 0xD2511F53u, M1 = 0xCD9E8D57u, W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
@@ -1995,13 +2136,22 @@ __device__ __forceinline__ uint4 philox4x32_10(uint4 c, uint2 k) {
 }
 
 __device__ __forceinline__ void box_muller(uint32_t a, uint32_t b, float &z0, float &z1) {
-    const float u1 = ((float)(a >> 8) + 1.0f) * (1.0f / 16777216.0f);  // (0, 1]
-    const float u2 = (float)(b >> 8) * (1.0f / 16777216.0f);           // [0, 1)
-    const float r = sqrtf(-2.0f * logf(u1));
-    float sn, cs;
-    sincosf(6.283185307179586f * u2, &sn, &cs);
-    z0 = r * cs;
-    z1 = r * sn;
+    const double u1 = ((double)(a >> 8) + 1.0) * (1.0 / 16777216.0);  // (0, 1]
+    const double u2 = (double)(b >> 8) * (1.0 / 16777216.0);           // [0, 1)
+    const double r = sqrt(-2.0 * log(u1));
+    const double t = 6.283185307179586 * u2;
+    z0 = (float)(r * cos(t));
+    z1 = (float)(r * sin(t));
+}
+
+__device__ __forceinline__ void gen_group(int64_t row, int64_t groups, int64_t gi, uint64_t stream,
+                                          uint2 key, float z[4]) {
+    const uint64_t ctr = (uint64_t)row * (uint64_t)groups + (uint64_t)gi;
+    const uint4 r = philox4x32_10(make_uint4((uint32_t)ctr, (uint32_t)(ctr >> 32), (uint32_t)stream,
+                                             (uint32_t)(stream >> 32)),
+                                  key);
+    box_muller(r.x, r.y, z[0], z[1]);
+    box_muller(r.z, r.w, z[2], z[3]);
 }
 
 template <int OUT_BF16>
@@ -2013,38 +2163,39 @@ __global__ __launch_bounds__(256) void gen_normal_kernel(void *dst, int64_t n, i
     if (row >= n) return;
     const uint2 key = make_uint2((uint32_t)seed, (uint32_t)(seed >> 32));
     const int64_t groups = (d + 3) / 4;
-    double ss = 0.0;
-    // first pass: sum of squares (values regenerated in the second pass)
-    for (int pass = 0; pass < 2; ++pass) {
-        double inv = 1.0;
-        if (pass == 1 && normalize) inv = ss > 0.0 ? 1.0 / sqrt(ss) : 0.0;
-        if (pass == 0 && !normalize) continue;
-        for (int64_t gi = lane; gi < groups; gi += 64) {
-            const uint64_t ctr = (uint64_t)row * (uint64_t)groups + (uint64_t)gi;
-            const uint4 r = philox4x32_10(
-                make_uint4((uint32_t)ctr, (uint32_t)(ctr >> 32), (uint32_t)stream,
-                           (uint32_t)(stream >> 32)),
-                key);
-            float z[4];
-            box_muller(r.x, r.y, z[0], z[1]);
-            box_muller(r.z, r.w, z[2], z[3]);
+    double inv = 1.0;
+    if (normalize) {
+        // s in dimension order: chunk c holds groups 64 c .. 64 c + 63, lane l
+        // group 64 c + l; every lane adds the chunk's values lane by lane
+        double s = 0.0;
+        for (int64_t c0 = 0; c0 < groups; c0 += 64) {
+            float z[4] = {0.f, 0.f, 0.f, 0.f};
+            if (c0 + lane < groups) gen_group(row, groups, c0 + lane, stream, key, z);
+            const int64_t lanes = min((int64_t)64, groups - c0);
+            for (int l = 0; l < (int)lanes; ++l) {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int64_t j = gi * 4 + u;
-                if (j >= d) break;
-                if (pass == 0) {
-                    ss += (double)z[u] * (double)z[u];
-                } else {
-                    const float o = normalize ? (float)((double)z[u] * inv) : z[u];
-                    if (OUT_BF16)
-                        ((uint16_t *)dst)[row * d + j] = f32_to_bf16_rne(o);
-                    else
-                        ((float *)dst)[row * d + j] = o;
+                for (int u = 0; u < 4; ++u) {
+                    const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(z[u]), l));
+                    if ((c0 + l) * 4 + u < d) s = s + (double)v * (double)v;
                 }
             }
         }
-        if (pass == 0)
-            for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+        const double norm = sqrt(s);
+        inv = norm > 0.0 ? 1.0 / norm : 0.0;
+    }
+    for (int64_t gi = lane; gi < groups; gi += 64) {
+        float z[4];
+        gen_group(row, groups, gi, stream, key, z);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t j = gi * 4 + u;
+            if (j >= d) break;
+            const float o = normalize ? (float)((double)z[u] * inv) : z[u];
+            if (OUT_BF16)
+                ((uint16_t *)dst)[row * d + j] = f32_to_bf16_rne(o);
+            else
+                ((float *)dst)[row * d + j] = o;
+        }
     }
 }
 

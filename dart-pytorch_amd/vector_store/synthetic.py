@@ -3,7 +3,8 @@
 Host generation uses numpy's Philox bit generator; one host buffer is fed to
 both the GPU library and the CPU checker in the same run, so the two sides
 always see identical bytes.  The 20M x 768 configuration is generated on the
-device instead (vs_gen_normal) and checked on rows read back.
+device instead (vs_gen_normal, add_device_normal below); its rows are
+checked against a host restatement of that generator on rows read back.
 
 Normalisation follows L2NormTransform (l2_norm_transform.dart:23-46): fp64
 sum of squares, inv = 1/sqrt, o = v * inv rounded to fp32 (zero rows stay
@@ -71,3 +72,24 @@ def dedup_set(n: int, d: int, dup_frac: float, noise: float, seed: int) -> np.nd
     allv = np.concatenate([base, l2_normalize(cop)], axis=0)
     perm = rng(seed, 3).permutation(n)
     return np.ascontiguousarray(allv[perm])
+
+
+DEVICE_STREAM_BASE = 1 << 32
+
+
+def add_device_normal(idx, n: int, d: int, seed: int, chunk: int = 1 << 20) -> None:
+    """Fill a bf16 index with n L2-normalised N(0,1) rows made on the device
+    (config 3's database): rows [r, r + chunk) come from vs_gen_normal with
+    stream DEVICE_STREAM_BASE + r and row counters 0 .. chunk - 1."""
+    from . import _native as NN
+
+    idx.reserve(n)
+    buf = NN.DeviceBuffer(min(chunk, n) * d * 2)
+    try:
+        for r in range(0, n, chunk):
+            m = min(chunk, n - r)
+            NN.check(NN.load().vs_gen_normal(0, buf.ptr, NN.VS_DTYPE_BF16, m, d, seed,
+                                             DEVICE_STREAM_BASE + r, 1))
+            idx.add_device(buf, m, NN.VS_DTYPE_BF16)
+    finally:
+        buf.free()

@@ -98,6 +98,24 @@ def test_bf16_storage_ip(vs, nq):
     assert_knn_parity(r.distances, r.ids, Dr, Ir, 1, rtol=1e-3)
 
 
+def test_eight_wave_streaming_scan(vs, monkeypatch):
+    """Regression test of the 8-wave streaming scan (VS_SCAN_NW8=1), whose
+    LDS id area once started at the 4-wave offset: the batch-64 shape of
+    test_bf16_storage_ip, where it runs, against the oracle."""
+    monkeypatch.setenv("VS_SCAN_NW8", "1")
+    xb16 = syn.to_bf16_bits(syn.normal_unit(60_000, 768, 99, 0))
+    xq16 = syn.to_bf16_bits(syn.normal_unit(64, 768, 99, 1))
+    idx = vs.GpuIndexFlat(768, vs.Metric.innerProduct, storage="bf16")
+    idx.add(xb16)
+    idx.prof_reset()
+    r = idx.search(xq16, 10)
+    n8 = idx.prof_get("streamed8")[0]
+    idx.close()
+    assert n8 >= 1, "the 8-wave scan did not run"
+    Dr, Ir = oracle.flat_search(syn.bf16_bits_to_f32(xb16), syn.bf16_bits_to_f32(xq16), 10, 1, NT)
+    assert_knn_parity(r.distances, r.ids, Dr, Ir, 1, rtol=1e-3)
+
+
 def test_bf16_storage_fp32_queries(vs):
     """bf16 rows, fp32 queries (two query planes): the oracle sees the stored
     bf16 values and the fp32 queries as given."""
@@ -168,8 +186,9 @@ def test_edge_cases(vs):
     with pytest.raises(vs.VsError):
         idx.search(bad, 2)
     assert idx.ntotal == 4  # failed add left nothing behind
-    with pytest.raises(NotImplementedError):
-        idx.search(np.ones((1, 8), np.float32), 1000)
+    r = idx.search(np.ones((1, 8), np.float32), 1000)  # any k, as TopK accepts it
+    assert np.all(r.ids[0, :4] >= 0) and np.all(r.ids[0, 4:] == -1)
+    assert np.all(np.isinf(r.distances[0, 4:])) and np.all(r.distances[0, :4] == 0.0)
     idx.close()
 
 

@@ -220,3 +220,33 @@ def test_reference_fixtures_against_numpy_goldens():
         m = g["max_offdiag"]
         lims, _, _ = oracle.flat_range_search(x, x, m + 1e-6, oracle.IP)
         assert np.array_equal(np.diff(lims), np.ones(hdr["ntotal"]))
+
+
+@pytest.mark.parametrize("metric", [oracle.L2, oracle.IP])
+def test_range_search_brute_force_numpy(metric):
+    """Range search at d > 1 with n not a multiple of 4 (the oracle's scalar
+    tail): hits = numpy fp64 scores against the radius, ids ascending."""
+    g = syn.rng(13, metric)
+    xb = g.standard_normal((701, 37)).astype(np.float32)
+    xq = g.standard_normal((11, 37)).astype(np.float32)
+    s = np_scores(xb, xq, metric)
+    radius = float(np.quantile(s, 0.02 if metric == oracle.L2 else 0.98))
+    lims, D, I = oracle.flat_range_search(xb, xq, radius, metric, 3)
+    for q in range(len(xq)):
+        want = np.nonzero(s[q] <= radius if metric == oracle.L2 else s[q] >= radius)[0]
+        got = I[lims[q]:lims[q + 1]]
+        assert np.array_equal(got, want)
+        assert np.allclose(D[lims[q]:lims[q + 1]], s[q][want].astype(np.float32), rtol=2e-7,
+                           atol=1e-6)
+
+
+def test_self_join_brute_force_numpy():
+    """IP self-join at d = 29, n = 513: every pair i < j with fp64 dot >= t,
+    sorted by (i, j), against numpy (vector_dedup_demo.dart:115-128)."""
+    x = syn.dedup_set(513, 29, 0.1, 0.05, 4)
+    s = x.astype(np.float64) @ x.astype(np.float64).T
+    t = 0.8
+    ii, jj = np.nonzero(np.triu(s >= t, k=1))
+    i, j, sc = oracle.self_join(x, t, nthreads=2)
+    assert np.array_equal(i, ii) and np.array_equal(j, jj) and len(i) > 20
+    assert np.allclose(sc, s[ii, jj].astype(np.float32), rtol=2e-7)
