@@ -7,6 +7,7 @@
 #include <cstdio>
 #include <cstring>
 #include <map>
+#include <mutex>
 #include <numeric>
 #include <string>
 #include <vector>
@@ -16,15 +17,14 @@
 
 namespace {
 
-thread_local std::string g_err;
+// (a fixed buffer: reporting an error allocates nothing)
+thread_local char g_err[512];
 
 int set_err(int code, const char *fmt, ...) {
-    char buf[512];
     va_list ap;
     va_start(ap, fmt);
-    vsnprintf(buf, sizeof buf, fmt, ap);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
     va_end(ap);
-    g_err = buf;
     return code;
 }
 
@@ -1356,12 +1356,55 @@ int range_core(vs_index *x, const vs::PreparedQueries &pq, double radius, int se
 
 }  // namespace
 
+namespace {
+
+// ---------------------------------------------------------------------------
+// Fixed scratch of the allocation-free search (vs_index_search_device_noalloc).
+// Each device holds its own instance of `scratch` from module load until the
+// process ends; host code never passes the array's name to a kernel (it is a
+// host-side stand-in), only the device address hipGetSymbolAddress returns,
+// taken once per device with that device current.
+// ---------------------------------------------------------------------------
+constexpr size_t kFixedScratchBytes = (size_t)128 << 20;
+constexpr size_t kFixedListBudget = (size_t)32 << 20;  // main scan's candidate lists
+constexpr int64_t kFixedMaxNq = 64, kFixedMaxK = 128, kFixedMaxD = 4096;
+constexpr int kMaxDevices = 64;
+
+}  // namespace
+
+static __device__ __align__(256) char scratch[kFixedScratchBytes];
+
+namespace {
+
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of this device's scratch (the current device must be
+// `device`).
+int fixed_scratch(int device, char **out) {
+    if (device < 0 || device >= kMaxDevices)
+        return set_err(VS_ERR_UNSUPPORTED, "device %d: fixed scratch covers devices 0..%d", device,
+                       kMaxDevices - 1);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[device]) {
+        void *p = nullptr;
+        hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_err(e, "hipGetSymbolAddress(scratch)");
+        if (!p) return set_err(VS_ERR_HIP, "hipGetSymbolAddress(scratch) returned null");
+        g_scratch_ptr[device] = p;
+    }
+    *out = (char *)g_scratch_ptr[device];
+    return VS_OK;
+}
+
+}  // namespace
+
 // ===========================================================================
 // ABI
 // ===========================================================================
 extern "C" {
 
-const char *vs_last_error(void) { return g_err.c_str(); }
+const char *vs_last_error(void) { return g_err; }
 
 int vs_device_count(int *count) {
     if (!count) return set_err(VS_ERR_INVALID, "null count");
@@ -1627,6 +1670,34 @@ int vs_index_search_device(vs_index *x, const void *q_dev, int q_dtype, int64_t 
     DeviceGuard g(x->device);
     Arena A;
     return search_device(x, A, q_dev, q_dtype, nq, k, D_dev, I_dev);
+}
+
+int vs_index_search_device_noalloc(vs_index *x, const void *q_dev, int q_dtype, int64_t nq,
+                                   int64_t k, float *D_dev, int32_t *I_dev) {
+    if (int rc = check_index(x)) return rc;
+    if (int rc = check_dtype(q_dtype)) return rc;
+    if (nq < 0 || k < 0) return set_err(VS_ERR_INVALID, "nq and k must be >= 0");
+    if (nq > kFixedMaxNq || k > kFixedMaxK || x->d > kFixedMaxD)
+        return set_err(VS_ERR_UNSUPPORTED,
+                       "allocation-free search: nq <= %lld, k <= %lld, d <= %lld (got nq=%lld, "
+                       "k=%lld, d=%lld)",
+                       (long long)kFixedMaxNq, (long long)kFixedMaxK, (long long)kFixedMaxD,
+                       (long long)nq, (long long)k, (long long)x->d);
+    if (nq > 0 && k > 0 && (!q_dev || !D_dev || !I_dev))
+        return set_err(VS_ERR_INVALID, "null query or output buffer");
+    DeviceGuard g(x->device);
+    if (g.err != hipSuccess) return hip_err(g.err, "hipSetDevice");
+    char *base = nullptr;
+    if (int rc = fixed_scratch(x->device, &base)) return rc;
+    Arena A;
+    A.base = base;
+    A.cap = kFixedScratchBytes;
+    struct FixedScope {
+        vs_index *x;
+        ~FixedScope() { x->prof_fixed = false; }
+    } fs{x};
+    x->prof_fixed = true;
+    return search_device(x, A, q_dev, q_dtype, nq, k, D_dev, I_dev, false, kFixedListBudget);
 }
 
 int vs_index_search(vs_index *x, const void *q, int q_dtype, int64_t nq, int64_t k, float *D,

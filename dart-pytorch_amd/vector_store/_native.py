@@ -32,7 +32,8 @@ EXPORTED = [
     "vs_index_create", "vs_index_destroy", "vs_index_reserve", "vs_index_reset",
     "vs_index_ntotal", "vs_index_d", "vs_index_metric", "vs_index_storage",
     "vs_index_add", "vs_index_add_device", "vs_index_reconstruct", "vs_index_remove_ids",
-    "vs_index_search", "vs_index_search_device", "vs_index_range_search", "vs_range_result_free",
+    "vs_index_search", "vs_index_search_device", "vs_index_search_device_noalloc",
+    "vs_index_range_search", "vs_range_result_free",
     "vs_index_self_join", "vs_pairs_free", "vs_kmeans_step", "vs_last_error",
     "vs_dev_alloc", "vs_dev_free", "vs_dev_upload", "vs_dev_download", "vs_dev_copy", "vs_device_count",
     "vs_device_name", "vs_gen_normal", "vs_prof_enable", "vs_prof_get", "vs_prof_reset",
@@ -108,6 +109,7 @@ def load() -> ctypes.CDLL:
         "vs_index_remove_ids": ([p, p, i64, ctypes.POINTER(ctypes.c_int64)], i32),
         "vs_index_search": ([p, p, i32, i64, i64, p, p], i32),
         "vs_index_search_device": ([p, p, i32, i64, i64, p, p], i32),
+        "vs_index_search_device_noalloc": ([p, p, i32, i64, i64, p, p], i32),
         "vs_index_range_search": ([p, p, i32, i64, ctypes.c_double,
                                    ctypes.POINTER(ctypes.POINTER(RangeSearchC))], i32),
         "vs_range_result_free": ([ctypes.POINTER(RangeSearchC)], None),

@@ -122,6 +122,19 @@ VS_API int vs_index_search(vs_index *idx, const void *q, int q_dtype, int64_t nq
 VS_API int vs_index_search_device(vs_index *idx, const void *q_dev, int q_dtype, int64_t nq,
                                   int64_t k, float *D_dev, int32_t *I_dev);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): vs_index_search_device with every scratch buffer --
+ * prepared queries, candidate lists, thresholds, counters and the fallback
+ * paths' lists -- carved from one fixed region per device, a 128 MiB
+ * static device array the library holds from load until the process ends.
+ * It calls no hipMalloc / hipFree and allocates no host memory.  Limits:
+ * nq <= 64, k <= 128, d <= 4096 (VS_ERR_UNSUPPORTED beyond).  Results equal
+ * those of vs_index_search_device.  All calls on one GPU share its region:
+ * calls that overlap on one GPU (from several threads or handles) race. */
+VS_API int vs_index_search_device_noalloc(vs_index *idx, const void *q_dev, int q_dtype,
+                                          int64_t nq, int64_t k, float *D_dev, int32_t *I_dev);
+
 /* IndexFlat.rangeSearch (index_flat.dart:99-137): every stored vector with
  * dist <= radius (L2) or dot >= radius (IP), tested on the fp64 score.
  * *out is library-allocated; free it with vs_range_result_free. */
