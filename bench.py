@@ -1,19 +1,46 @@
 """Benchmark of the MI355X flat k-NN path (one JSON line on stdout).
 
-Default workload = BASELINE.json configs[1]: exact L2 top-100 over a
-1,000,000 x 128 database of integers 0..255 stored as fp32, 10,000 queries of
-the same distribution.  One step = one search of the whole query batch with
-the database, the queries and the result buffers resident in HBM.
+Default run (no flags): every BASELINE.json configuration, in one process.
+The headline line is configs[1] (C2): exact L2 top-100 over a 1,000,000 x 128
+database of integers 0..255 stored as fp32, 10,000 queries of the same
+distribution; one step = one search of the whole query batch with the
+database, the queries and the result buffers resident in HBM.  The other
+configurations sit under "workloads":
 
-value = queries per second over the K timed steps.  roofline = the scan
-kernel (the dominant launch) timed with HIP events on the index's stream:
-algorithmic flops per launch (2 * nq * N * d) over its mean duration, against
-the peak of the MFMA instruction it runs (bf16 for lossless-bf16 storage).
-cpu_baseline = the CPU oracle (a restatement of IndexFlat.search,
-index_flat.dart:62-97) on this host's cores over a bounded query sample of
-the same database, scaled to queries per second.
+  c1  10k x 384 fp32 unit rows, IP, 100 queries, k = 10 (the CPU-runnable case);
+  c3  20M x 768 bf16 unit rows (device-generated), IP, k = 10, batches
+      1 / 64 / 1024 / 8192;
+  c4  k-means step, 2M x 256 fp32 mixture points, K = 4096;
+  c5  cosine self-join of 500k x 512 fp32 unit rows, threshold 0.95.
 
-Other workloads (--workload c1|c3|c4|c5) exist for exploration and profiling.
+Every workload reports:
+  value / ms_per_step   whole-job rate over the K timed steps (inputs in HBM);
+  steps_ms              best / median / p50 / p95 / p99 of the step times
+                        (the benchIndex protocol, bench.dart:90-184: warmup,
+                        repeated timed passes, best and median);
+  roofline              the dominant kernel timed with HIP events on the
+                        index's stream over the timed region: algorithmic
+                        bytes (HBM-bound: batch <= 64) or flops (MFMA-bound)
+                        per launch over its mean duration, against the spec
+                        peak and against the measured peaks (vs_dev_probe);
+  cpu_baseline          the CPU oracle (oracle/oracle.c, a restatement of
+                        IndexFlat.search / rangeSearch / Kmeans, index_flat.dart,
+                        kmeans.dart) timed on this host: all cores (threads
+                        over queries, at most the box's 16-core share) and one
+                        core (the reference's own parallelism: one Dart isolate);
+  parity                GPU results against the oracle on the same inputs:
+                        tie-aware top-k comparison (distances bit-identical,
+                        ids equal outside exact-tie groups), identical k-means
+                        assignments and centroids, identical pair lists.
+
+C2 also reports the PCIe-inclusive rate of the host-buffer entry point
+(vs_index_search) and benchIndex rows in the reference's CSV / Markdown
+formats (toBenchCsv / toBenchMarkdown, bench.dart:217-312); --csv / --md write
+them to files.
+
+Single workloads (--workload c1|c2|c3|c4|c5, --batch for c3) print that
+workload's line alone (profiling runs use them); --workload copy / libgemm are
+the counter yardstick and the vendor GEMM for scale.
 """
 from __future__ import annotations
 
@@ -32,16 +59,118 @@ for _p in (ROOT, os.path.join(ROOT, "dart-pytorch_amd")):
 
 METRIC = "QPS, flat top-k k-NN (1M×128 fp32, 20M×768 bf16); % HBM / MFMA roofline"
 PEAK = {"bf16_mfma_tflops": 2500.0, "fp32_mfma_tflops": 157.3, "hbm_gbs": 8000.0}
+CPU_SHARE = 16  # host cores of one GPU's share on the measurement boxes
 
-# HBM bytes per launch of the dominant kernel, measured with two rocprofv3
-# --pmc runs (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0: the factors a plain 16-byte
-# copy of known size reads, profiles/copy16_calibration.md), keyed by
+# HBM bytes per launch of the dominant kernel, from two rocprofv3 --pmc runs
+# (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0: the factors a plain 16-byte copy of
+# known size reads, profiles/copy16_calibration.md), keyed by
 # (workload, n, nq, k).  The command and readings are in the named profile;
 # configurations without a measurement report traffic null.
 MEASURED_TRAFFIC = {
     ("c2", 1_000_000, 10_000, 100): (1.09e9, "profiles/scan_c2_1Mx128_k100.md"),
     ("c3", 20_000_000, 1, 10): (30.88e9, "profiles/scan_c3_20Mx768_b1_b64.md"),
 }
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+# --------------------------------------------------------------------------
+# host facts, peaks, timing statistics
+# --------------------------------------------------------------------------
+def host_info():
+    cpu, mem, ident = "unknown", None, {}
+    try:
+        for line in open("/proc/cpuinfo"):
+            key = line.split(":", 1)[0].strip()
+            if key in ("model name", "cpu family", "model", "stepping", "cpu MHz") and key not in ident:
+                ident[key] = line.split(":", 1)[1].strip()
+            if key == "processor" and ident:
+                break
+        cpu = ident.get("model name", cpu)
+        for line in open("/proc/meminfo"):
+            if line.startswith("MemTotal"):
+                mem = round(int(line.split()[1]) / 2 ** 20, 1)
+                break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count() or 1
+    return {"cpu_model": cpu, "cpu_family_model_stepping": [ident.get("cpu family"),
+                                                               ident.get("model"),
+                                                               ident.get("stepping")],
+            "cpu_mhz": ident.get("cpu MHz"), "nproc": os.cpu_count(), "affinity_cores": affinity,
+            "mem_gib": mem, "threads_all_core": max(1, min(affinity, CPU_SHARE))}
+
+
+def measured_peaks(NN):
+    """Achievable read bandwidth and bf16 MFMA rate on this GPU (vs_dev_probe)."""
+    import ctypes
+
+    out = {}
+    for what, key, nbytes in ((0, "hbm_read_gbs", 8 << 30), (1, "bf16_mfma_tflops", 0)):
+        v = ctypes.c_double(0.0)
+        rc = NN.load().vs_dev_probe(0, what, nbytes, ctypes.byref(v))
+        out[key] = round(v.value, 1) if rc == 0 else None
+    return out
+
+
+def step_stats(times_s):
+    t = np.sort(np.asarray(times_s) * 1e3)
+    n = len(t)
+
+    def pct(q):  # nearest rank, as benchIndex (bench.dart:167-171)
+        return float(t[int(np.floor((n - 1) * q + 0.5))])
+
+    return {"best_ms": round(float(t[0]), 4), "median_ms": round(float(np.median(t)), 4),
+            "mean_ms": round(float(t.mean()), 4), "p50_ms": round(pct(0.5), 4),
+            "p95_ms": round(pct(0.95), 4), "p99_ms": round(pct(0.99), 4), "n": n}
+
+
+def time_steps(fn, steps, warmup, label):
+    for _ in range(warmup):
+        fn()
+    times = []
+    t0 = time.perf_counter()
+    for i in range(steps):
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+    wall = time.perf_counter() - t0
+    log(f"[bench] {label}: {steps} steps in {wall:.3f} s")
+    return wall, times
+
+
+def roofline(kind, work, avg_s, peaks, kernel, launches, traffic=None, traffic_src=None,
+             peak_div=1, extra=None):
+    """kind 'hbm': work = algorithmic bytes per launch; 'mfma': flops per launch."""
+    if kind == "hbm":
+        ach = work / avg_s / 1e9
+        peak, meas, unit = PEAK["hbm_gbs"], peaks.get("hbm_read_gbs"), "GB/s"
+    else:
+        ach = work / avg_s / 1e12
+        peak = PEAK["bf16_mfma_tflops"] / peak_div
+        m = peaks.get("bf16_mfma_tflops")
+        meas, unit = (m / peak_div if m else None), "TFLOP/s"
+    r = {"bound": kind, "achieved": round(ach, 2), "peak": round(peak, 1), "unit": unit,
+         "frac": round(ach / peak, 4), "traffic": traffic,
+         "measured_peak": round(meas, 1) if meas else None,
+         "frac_of_measured": round(ach / meas, 4) if meas else None,
+         "kernel": kernel, "launches": launches, "avg_ms": round(avg_s * 1e3, 4),
+         ("algorithmic_bytes_per_launch" if kind == "hbm" else "algorithmic_flops_per_launch"): work}
+    if traffic_src:
+        r["traffic_source"] = traffic_src
+    if extra:
+        r.update(extra)
+    return r
+
+
+def kernel_avg(idx, fam):
+    n, ms = idx.prof_get(fam)
+    return n, (ms / max(n, 1)) / 1e3
 
 
 def mfma_passes(idx):
@@ -54,234 +183,364 @@ def mfma_passes(idx):
     return 1 if coarse else 3
 
 
-def measured_traffic(workload, n, nq, k):
-    hit = MEASURED_TRAFFIC.get((workload, n, nq, k))
-    return (hit[0], hit[1]) if hit else (None, None)
-
-
-def log(msg):
-    print(msg, file=sys.stderr, flush=True)
-
-
-def host_info():
-    cpu = "unknown"
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    try:
-        cores = len(os.sched_getaffinity(0))
-    except AttributeError:
-        cores = os.cpu_count() or 1
-    return cpu, cores
-
-
-def cpu_baseline(xb, xq, k, metric, target_s, threads):
-    """Times the oracle on a bounded sample of the batch; returns (qps, sample, results)."""
+# --------------------------------------------------------------------------
+# CPU oracle timing
+# --------------------------------------------------------------------------
+def cpu_search(xb, xq, k, metric, threads, target_s):
+    """The oracle on a bounded query sample of the batch: (qps, queries, seconds, (D, I))."""
     import oracle
 
-    n0 = min(len(xq), max(threads, 4))
+    n0 = min(len(xq), max(threads, 1))
     t = time.perf_counter()
     oracle.flat_search(xb, xq[:n0], k, metric, threads)
     per_q = (time.perf_counter() - t) / n0
     ns = int(min(len(xq), max(n0, target_s / max(per_q, 1e-9))))
-    ns = max(threads, (ns // threads) * threads) if ns >= threads else ns
+    if ns >= threads:
+        ns = (ns // threads) * threads
     t = time.perf_counter()
     D, I = oracle.flat_search(xb, xq[:ns], k, metric, threads)
     dt = time.perf_counter() - t
     return ns / dt, ns, dt, (D, I)
 
 
-def run_search_workload(args, vs, syn, N):
-    from vector_store import _native as NN
+def cpu_baseline_entry(all_core, one_core, unit, sample, host):
+    qa, na, ta = all_core
+    out = {"value": round(qa, 3), "unit": unit, "cores": host["threads_all_core"], "kind": "port",
+           "sample": sample.format(n=na, t=ta), "cpu": host["cpu_model"], "nproc": host["nproc"]}
+    if one_core is not None:
+        q1, n1, t1 = one_core
+        out["single_core"] = {"value": round(q1, 3), "unit": unit, "cores": 1,
+                              "sample": sample.format(n=n1, t=t1)}
+    return out
 
-    if args.workload == "c2":
+
+# --------------------------------------------------------------------------
+# C1 / C2: flat search with host-generated inputs
+# --------------------------------------------------------------------------
+def search_setup(vs, NN, workload, args):
+    from vector_store import synthetic as syn
+
+    if workload == "c2":
         n, d, nq, k, metric = args.n or 1_000_000, 128, args.nq or 10_000, args.k or 100, 0
-        xb = syn.int_grid(n, d, args.seed, 0)
-        xq = syn.int_grid(nq, d, args.seed, 1)
-        storage, qdt = "auto", NN.VS_DTYPE_F32
+        xb, xq = syn.int_grid(n, d, args.seed, 0), syn.int_grid(nq, d, args.seed, 1)
+        storage = "auto"
         desc = f"c2: exact L2 top-{k}, {n} x {d} fp32 integers 0..255, {nq} queries"
-    elif args.workload == "c1":
+    else:
         n, d, nq, k, metric = args.n or 10_000, 384, args.nq or 100, args.k or 10, 1
-        xb = syn.normal_unit(n, d, args.seed, 0)
-        xq = syn.normal_unit(nq, d, args.seed, 1)
-        storage, qdt = "f32", NN.VS_DTYPE_F32
+        xb, xq = syn.normal_unit(n, d, args.seed, 0), syn.normal_unit(nq, d, args.seed, 1)
+        storage = "f32"
         desc = f"c1: exact IP top-{k}, {n} x {d} fp32 unit N(0,1), {nq} queries"
-    elif args.workload == "c3":
-        n, d, nq, k, metric = args.n or 20_000_000, 768, args.nq or args.batch, args.k or 10, 1
-        xb = None
-        xq = syn.to_bf16_bits(syn.normal_unit(nq, d, args.seed, 1))
-        storage, qdt = "bf16", NN.VS_DTYPE_BF16
-        desc = f"c3: exact IP top-{k}, {n} x {d} bf16 unit N(0,1) (device-generated), batch {nq}"
-    else:
-        raise SystemExit(f"unknown search workload {args.workload}")
+    return n, d, nq, k, metric, xb, xq, storage, desc
 
+
+def run_search(vs, NN, workload, args, ctx, full=False):
+    import oracle
+    from oracle.parity import knn_failures
+
+    n, d, nq, k, metric, xb, xq, storage, desc = search_setup(vs, NN, workload, args)
     idx = vs.GpuIndexFlat(d, vs.Metric(metric), storage=storage)
-    t0 = time.perf_counter()
-    if xb is not None:
-        idx.add(xb)
-    else:
-        idx.reserve(n)
-        chunk = 1 << 20
-        buf = NN.DeviceBuffer(chunk * d * 2)
-        for r in range(0, n, chunk):
-            m = min(chunk, n - r)
-            NN.check(NN.load().vs_gen_normal(0, buf.ptr, NN.VS_DTYPE_BF16, m, d, args.seed,
-                                             (1 << 32) + r, 1))
-            idx.add_device(buf, m, NN.VS_DTYPE_BF16)
-        buf.free()
-    log(f"[bench] {desc}: add {time.perf_counter() - t0:.1f}s, storage={idx.storage}")
-
-    esz = 2 if qdt == NN.VS_DTYPE_BF16 else 4
-    qbuf = NN.DeviceBuffer(nq * d * esz)
+    idx.add(xb)
+    qbuf = NN.DeviceBuffer(xq.nbytes)
     qbuf.upload(xq)
-    Dbuf = NN.DeviceBuffer(nq * k * 4)
-    Ibuf = NN.DeviceBuffer(nq * k * 4)
+    Dbuf, Ibuf = NN.DeviceBuffer(nq * k * 4), NN.DeviceBuffer(nq * k * 4)
+
+    def step():
+        idx.search_device(qbuf, nq, k, Dbuf, Ibuf, NN.VS_DTYPE_F32)
 
     for _ in range(args.warmup):
-        idx.search_device(qbuf, nq, k, Dbuf, Ibuf, qdt)
+        step()
     idx.prof_enable(True)
     idx.prof_reset()
-    t = time.perf_counter()
-    for i in range(args.steps):
-        idx.search_device(qbuf, nq, k, Dbuf, Ibuf, qdt)
-        log(f"[bench] step {i + 1}/{args.steps} done")
-    wall = time.perf_counter() - t
+    wall, times = time_steps(step, args.steps, 0, desc)
     idx.prof_enable(False)
-    nscan, scan_ms = idx.prof_get("scan")
-    nmerge, merge_ms = idx.prof_get("merge")
+    nscan, scan_s = kernel_avg(idx, "scan")
+    nmerge, merge_s = kernel_avg(idx, "merge")
     npre, pre_ms = idx.prof_get("prepass")
-
     D = np.empty((nq, k), np.float32)
     I = np.empty((nq, k), np.int32)
     Dbuf.download(D)
     Ibuf.download(I)
-
-    flops = 2.0 * nq * n * d
-    scan_avg_s = scan_ms / max(nscan, 1) / 1e3
     bf16 = idx.storage == "bf16"
-    peak = PEAK["bf16_mfma_tflops"] / (1 if bf16 else 3)  # fp32 rows: three split-bf16 passes
-    achieved = flops / scan_avg_s / 1e12
-    roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
-            "frac": round(achieved / peak, 4), "traffic": measured_traffic(args.workload, n, nq, k)[0],
-            "traffic_source": measured_traffic(args.workload, n, nq, k)[1],
-            "kernel": "scan", "scan_kinds": {f: idx.prof_get(f)[0] for f in ("shared", "gemm", "tiled", "streamed") if idx.prof_get(f)[0]},
-            "launches": nscan, "avg_ms": round(scan_avg_s * 1e3, 4),
-            "algorithmic_flops_per_launch": flops, "merge_avg_ms": round(merge_ms / max(nmerge, 1), 4),
-            "prepass_ms_per_step": round(pre_ms / args.steps, 4) if npre else None}
-    if nq <= 64:  # streaming regime: the database bytes bound the kernel
-        db_bytes = n * d * (2 if bf16 else 4)
-        gbs = db_bytes / scan_avg_s / 1e9
-        roof.update({"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK["hbm_gbs"],
-                     "unit": "GB/s", "frac": round(gbs / PEAK["hbm_gbs"], 4),
-                     "algorithmic_bytes_per_launch": db_bytes})
-
+    traffic, tsrc = MEASURED_TRAFFIC.get((workload, n, nq, k), (None, None))
+    roof = roofline("mfma", 2.0 * nq * n * d, scan_s, ctx["peaks"], "scan", nscan, traffic, tsrc,
+                    peak_div=1 if bf16 else 3,
+                    extra={"scan_kinds": {f: idx.prof_get(f)[0] for f in
+                                          ("shared", "gemm", "tiled", "streamed")
+                                          if idx.prof_get(f)[0]},
+                           "merge_avg_ms": round(merge_s * 1e3, 4),
+                           "prepass_ms_per_step": round(pre_ms / args.steps, 4) if npre else None,
+                           "exact_fallback_queries": idx.prof_get("exact_fallback")[0]})
     out = {"metric": METRIC, "value": round(nq * args.steps / wall, 1), "unit": "queries/s",
            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "ms_per_step": round(wall / args.steps * 1e3, 3), "higher_is_better": True,
-           "scaling": "weak", "vs_baseline": None,
-           "dtype": "bf16" if bf16 else "fp32", "data": "synthetic",
-           "config": {"workload": desc, "n": n, "d": d, "nq": nq, "k": k,
-                      "metric": "L2" if metric == 0 else "IP", "storage": idx.storage},
-           "roofline": roof}
+           "scaling": "weak", "vs_baseline": None, "dtype": "bf16" if bf16 else "fp32",
+           "data": "synthetic", "config": {"workload": desc, "n": n, "d": d, "nq": nq, "k": k,
+                                           "metric": "L2" if metric == 0 else "IP",
+                                           "storage": idx.storage},
+           "steps_ms": step_stats(times), "roofline": roof}
 
-    if not args.no_cpu and xb is not None:
-        cpu, cores = host_info()
-        threads = min(cores, 16)
-        qps, ns, dt, (Dc, Ic) = cpu_baseline(xb, xq, k, metric, args.cpu_seconds, threads)
-        rec = float(np.mean([len(set(I[i]) & set(Ic[i])) / k for i in range(ns)]))
-        out["cpu_baseline"] = {"value": round(qps, 3), "unit": "queries/s", "cores": threads,
-                               "kind": "port",
-                               "sample": f"first {ns} of the {nq} queries against the full "
-                                         f"{n}-row database ({dt:.1f} s), fp64 oracle",
-                               "cpu": cpu}
-        out["recall_vs_cpu_sample"] = round(rec, 6)
+    if full:
+        # PCIe-inclusive rate of the host-buffer entry point (never `value`)
+        wall_h, _ = time_steps(lambda: idx.search(xq, k), max(3, args.steps // 2), 1,
+                               f"{workload} host buffers")
+        out["host_buffer_qps"] = round(nq * max(3, args.steps // 2) / wall_h, 1)
+        # benchIndex rows (bench.dart:90-184) on query subsets with oracle truth
+        from vector_store import SearchResult
+        from vector_store.bench import (BenchOptions, bench_index, to_bench_csv,
+                                        to_bench_markdown)
+
+        nb, npq = min(nq, 512), min(nq, 128)
+        Dt, It = oracle.flat_search(xb, xq[:nb], k, metric, ctx["host"]["threads_all_core"])
+        truth = SearchResult(Dt, It)
+        rows = [bench_index(idx, xq[:nb], k, truth, label="GpuIndexFlat [batched]",
+                            options=BenchOptions(warmup=1, repeats=3, per_query=False)),
+                bench_index(idx, xq[:npq], k, SearchResult(Dt[:npq], It[:npq]),
+                            label="GpuIndexFlat", options=BenchOptions(warmup=1, repeats=3))]
+        out["bench_index"] = [r.__dict__ for r in rows]
+        out["bench_csv"] = to_bench_csv(rows)
+        out["bench_markdown"] = to_bench_markdown(rows)
+        ctx["bench_rows"] = rows
+
+    if not args.no_cpu:
+        host = ctx["host"]
+        th = host["threads_all_core"]
+        qa, na, ta, (Dc, Ic) = cpu_search(xb, xq, k, metric, th, args.cpu_seconds)
+        one = None
+        if not args.no_single_core:
+            q1, n1, t1, _ = cpu_search(xb, xq, k, metric, 1, args.cpu_seconds / 2)
+            one = (q1, n1, t1)
+        out["cpu_baseline"] = cpu_baseline_entry(
+            (qa, na, ta), one, "queries/s",
+            "first {n} of the " + f"{nq} queries against the full {n}-row database " + "({t:.1f} s), fp64 oracle",
+            host)
+        bad = knn_failures(D[:na], I[:na], Dc, Ic, metric, rtol=1e-5)
+        out["parity"] = {"ok": not bad, "checked_queries": int(na), "failures": len(bad),
+                         "rule": "tie-aware top-k vs the oracle: distances bit-identical, ids "
+                                 "equal outside exact ties (rel 1e-5)",
+                         "first_failures": [str(b)[:200] for b in bad[:3]]}
+    qbuf.free()
+    Dbuf.free()
+    Ibuf.free()
     idx.close()
     return out
 
 
-def run_kmeans_workload(args, vs, syn):
+# --------------------------------------------------------------------------
+# C3: 20M x 768 bf16, batches 1 / 64 / 1024 / 8192
+# --------------------------------------------------------------------------
+C3_SAMPLE = [0, 1, 31, 63, 100, 511, 777, 1023, 2048, 3333, 4095, 4096, 6000, 7777, 8190, 8191]
+
+
+def run_c3(vs, NN, args, ctx, batches):
+    import oracle
+    from oracle.parity import knn_failures
+    from vector_store import synthetic as syn
+
+    n, d, k = args.n or 20_000_000, 768, args.k or 10
+    t0 = time.perf_counter()
+    idx = vs.GpuIndexFlat(d, vs.Metric.innerProduct, storage="bf16")
+    syn.add_device_normal(idx, n, d, args.seed)
+    log(f"[bench] c3: {n} x {d} bf16 rows generated on the device in "
+        f"{time.perf_counter() - t0:.1f} s")
+    bmax = max(batches)
+    xq16 = syn.to_bf16_bits(syn.normal_unit(bmax, d, args.seed, 1))
+    qbuf = NN.DeviceBuffer(xq16.nbytes)
+    qbuf.upload(xq16)
+    Dbuf, Ibuf = NN.DeviceBuffer(bmax * k * 4), NN.DeviceBuffer(bmax * k * 4)
+    per_batch = {}
+    results = {}
+    for B in batches:
+        def step():
+            idx.search_device(qbuf, B, k, Dbuf, Ibuf, NN.VS_DTYPE_BF16)
+
+        for _ in range(args.warmup):
+            step()
+        idx.prof_enable(True)
+        idx.prof_reset()
+        wall, times = time_steps(step, args.steps, 0, f"c3 batch {B}")
+        idx.prof_enable(False)
+        nscan, scan_s = kernel_avg(idx, "scan")
+        npre, pre_ms = idx.prof_get("prepass")
+        nmerge, merge_s = kernel_avg(idx, "merge")
+        D = np.empty((B, k), np.float32)
+        I = np.empty((B, k), np.int32)
+        Dbuf.download(D)
+        Ibuf.download(I)
+        pos = [p for p in C3_SAMPLE if p < B]
+        results[B] = (D[pos], I[pos], pos)
+        traffic, tsrc = MEASURED_TRAFFIC.get(("c3", n, B, k), (None, None))
+        extra = {"scan_kinds": {f: idx.prof_get(f)[0] for f in ("shared", "gemm", "tiled", "streamed")
+                                if idx.prof_get(f)[0]},
+                 "merge_avg_ms": round(merge_s * 1e3, 4),
+                 "prepass_ms_per_step": round(pre_ms / args.steps, 4) if npre else None,
+                 "exact_fallback_queries": idx.prof_get("exact_fallback")[0]}
+        if B <= 64:
+            roof = roofline("hbm", n * d * 2, scan_s, ctx["peaks"], "scan", nscan, traffic, tsrc,
+                            extra=extra)
+            roof["step_frac"] = round(n * d * 2 / (wall / args.steps) / 1e9 / PEAK["hbm_gbs"], 4)
+        else:
+            roof = roofline("mfma", 2.0 * B * n * d, scan_s, ctx["peaks"], "scan", nscan, traffic,
+                            tsrc, extra=extra)
+            roof["step_frac"] = round(2.0 * B * n * d / (wall / args.steps) / 1e12 /
+                                      PEAK["bf16_mfma_tflops"], 4)
+        per_batch[str(B)] = {"value": round(B * args.steps / wall, 1), "unit": "queries/s",
+                             "ms_per_step": round(wall / args.steps * 1e3, 3),
+                             "steps_ms": step_stats(times), "roofline": roof}
+    out = {"config": {"workload": f"c3: exact IP top-{k}, {n} x {d} bf16 unit N(0,1) "
+                                  "(device-generated, checked against the host generator in "
+                                  "tests/test_gpu_c3.py), batch sweep", "n": n, "d": d, "k": k,
+                      "batches": batches, "storage": "bf16"},
+           "dtype": "bf16", "steps": args.steps, "warmup": args.warmup, "batches": per_batch}
+
+    if not args.no_cpu:
+        # the oracle over the whole database, streamed to the host in chunks:
+        # all cores on the sample queries, one core on query 0
+        host = ctx["host"]
+        th = host["threads_all_core"]
+        sample = [p for p in C3_SAMPLE if p < bmax]
+        xq = syn.bf16_bits_to_f32(xq16[sample])
+        chunk = 1 << 20
+        cd, ci, c1d, c1i = [], [], [], []
+        t_all = t_one = 0.0
+        for r0 in range(0, n, chunk):
+            rows = idx.reconstruct_n(r0, min(chunk, n - r0))
+            t = time.perf_counter()
+            Dc, Ic = oracle.flat_search(rows, xq, k, oracle.IP, th)
+            t_all += time.perf_counter() - t
+            cd.append(Dc)
+            ci.append(np.where(Ic >= 0, Ic + r0, -1))
+            if not args.no_single_core:
+                t = time.perf_counter()
+                oracle.flat_search(rows, xq[:1], k, oracle.IP, 1)
+                t_one += time.perf_counter() - t
+            del rows
+        cd, ci = np.concatenate(cd, 1), np.concatenate(ci, 1)
+        Dr = np.empty((len(sample), k), np.float32)
+        Ir = np.empty((len(sample), k), np.int32)
+        for j in range(len(sample)):
+            o = np.lexsort((ci[j], -cd[j].astype(np.float64)))[:k]
+            Dr[j], Ir[j] = cd[j][o], ci[j][o]
+        where = {p: j for j, p in enumerate(sample)}
+        for B in batches:
+            D, I, pos = results[B]
+            rows_r = [where[p] for p in pos]
+            bad = knn_failures(D, I, Dr[rows_r], Ir[rows_r], 1, rtol=1e-3)
+            per_batch[str(B)]["parity"] = {
+                "ok": not bad, "checked_queries": len(pos), "failures": len(bad),
+                "rule": "tie-aware top-k vs the oracle over all rows (bf16 values fed to both; "
+                        "rel 1e-3 ties)", "positions": pos}
+        one = (1 / t_one, 1, t_one) if not args.no_single_core else None
+        out["cpu_baseline"] = cpu_baseline_entry(
+            (len(sample) / t_all, len(sample), t_all), one, "queries/s",
+            "{n} queries against all " + f"{n} rows, streamed in 1M-row chunks" +
+            " ({t:.1f} s of oracle time), fp64 oracle", host)
+    qbuf.free()
+    Dbuf.free()
+    Ibuf.free()
+    idx.close()
+    return out
+
+
+# --------------------------------------------------------------------------
+# C4: k-means step
+# --------------------------------------------------------------------------
+def run_kmeans(vs, NN, args, ctx):
     """one Lloyd iteration (assign + update) per step over 2M x 256
     fp32 points from a 1,024-component mixture, 4,096 centroids from a seeded
     subset; the centroids of step i feed step i + 1 (kmeans.dart:91-140)."""
     import oracle
+    from vector_store import synthetic as syn
 
     n, d, ncomp, K = args.n or 2_000_000, 256, 1024, 4096
     x, _ = syn.gaussian_mixture(n, d, ncomp, 0.1, args.seed)
     cen = x[syn.seeded_subset(n, K, args.seed)].copy()
     pts = vs.GpuIndexFlat.l2(d, storage="f32")
     pts.add(x)
-    # jitter draws for empty clusters (the reference takes them from dart:math
-    # Random, kmeans.dart:128-138): seeded uniforms, one stream per step
-    def jitter(step):
+
+    def jitter(step):  # the reference draws these from dart:math Random (kmeans.dart:128-138)
         return syn.rng(args.seed + 7, step).random(K * d)
 
     for w in range(args.warmup):
         _, cen, _, _ = vs.kmeans_step(pts, cen, 1, jitter(w))
-    # the draws are inputs: made before the timed steps
     jits = [jitter(args.warmup + i) for i in range(args.steps)]
     pts.prof_enable(True)
     pts.prof_reset()
-    cen0 = cen.copy()
-    t = time.perf_counter()
+    cen_first = cen.copy()
+    first = None
+    times = []
+    t0 = time.perf_counter()
     for i in range(args.steps):
-        _, cen, _, obj = vs.kmeans_step(pts, cen, 1, jits[i])
-        log(f"[bench] k-means step {i + 1}/{args.steps}: objective {obj:.6g}")
-    wall = time.perf_counter() - t
+        t = time.perf_counter()
+        a, cen, cnt, obj = vs.kmeans_step(pts, cen, 1, jits[i])
+        times.append(time.perf_counter() - t)
+        if first is None:
+            first = (a, cen.copy(), obj)
+    wall = time.perf_counter() - t0
+    log(f"[bench] c4: {args.steps} k-means steps in {wall:.3f} s")
     pts.prof_enable(False)
     fam = {f: pts.prof_get(f) for f in ("assign", "pick", "exhaustive", "update")}
-    nfb = pts.prof_get("kmeans_fallback_points")[0]
-    nsc, scan_ms = fam["assign"]
-    scan_s = scan_ms / max(nsc, 1) / 1e3
-    flops = 2.0 * n * K * d
+    nsc, scan_s = kernel_avg(pts, "assign")
     passes = mfma_passes(pts)
-    achieved = flops / scan_s / 1e12
-    peak = PEAK["bf16_mfma_tflops"] / passes
+    roof = roofline("mfma", 2.0 * n * K * d, scan_s, ctx["peaks"], "assign scan", nsc,
+                    peak_div=passes,
+                    extra={"peak_note": f"bf16 dense MFMA peak / {passes} pass(es) per distance"})
     out = {"metric": "k-means assign+update, points per second per iteration",
-           "value": round(n * args.steps / wall, 1), "unit": "points/s",
-           "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-           "ms_per_step": round(wall / args.steps * 1e3, 3), "higher_is_better": True,
-           "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
-           "config": {"workload": f"c4: k-means step, {n} x {d} fp32 mixture of {ncomp}, "
-                                  f"K={K}, host centroids in/out", "n": n, "d": d, "K": K},
-           "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": round(peak, 1),
-                        "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": None,
-                        "kernel": "assign scan", "avg_ms": round(scan_s * 1e3, 3),
-                        "algorithmic_flops_per_launch": flops,
-                        "peak_note": f"bf16 dense MFMA peak / {passes} pass(es) per distance"},
+           "value": round(n * args.steps / wall, 1), "unit": "points/s", "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 3),
+           "steps_ms": step_stats(times), "dtype": "fp32",
+           "config": {"workload": f"c4: k-means step, {n} x {d} fp32 mixture of {ncomp}, K={K}, "
+                                  "host centroids in/out", "n": n, "d": d, "K": K},
+           "roofline": roof,
            "families_ms": {f: round(v[1] / max(v[0], 1), 3) for f, v in fam.items()},
-           "exhaustive_points_per_step": nfb / args.steps}
+           "exhaustive_points_per_step": pts.prof_get("kmeans_fallback_points")[0] / args.steps}
     if not args.no_cpu:
-        cpu, cores = host_info()
-        threads = min(cores, 16)
-        m0 = min(n, threads * 64)
-        t = time.perf_counter()
-        oracle.kmeans_assign(x[:m0], cen0, threads)
-        per_point = (time.perf_counter() - t) / m0
-        for _ in range(3):  # re-aim while the sample runs under half the target time
-            m = int(min(n, max(m0, args.cpu_seconds / max(per_point, 1e-9))))
+        host = ctx["host"]
+        th = host["threads_all_core"]
+
+        def timed_assign(threads, target):
+            m0 = min(n, threads * 64)
             t = time.perf_counter()
-            oracle.kmeans_assign(x[:m], cen0, threads)
+            oracle.kmeans_assign(x[:m0], cen_first, threads)
+            per_point = (time.perf_counter() - t) / m0
+            m = int(min(n, max(m0, target / max(per_point, 1e-9))))
+            t = time.perf_counter()
+            a_or, _, _ = oracle.kmeans_assign(x[:m], cen_first, threads)
             dt = time.perf_counter() - t
-            per_point = dt / m
-            if dt >= 0.5 * args.cpu_seconds or m == n:
-                break
-        out["cpu_baseline"] = {"value": round(m / dt, 1), "unit": "points/s (assign only)",
-                               "cores": threads, "kind": "port",
-                               "sample": f"assign of the first {m} points against {K} centroids "
-                                         f"({dt:.1f} s), fp64 oracle", "cpu": cpu}
+            return m / dt, m, dt, a_or
+
+        qa, ma, ta, a_or = timed_assign(th, args.cpu_seconds)
+        one = None
+        if not args.no_single_core:
+            q1, m1, t1, _ = timed_assign(1, args.cpu_seconds / 2)
+            one = (q1, m1, t1)
+        out["cpu_baseline"] = cpu_baseline_entry(
+            (qa, ma, ta), one, "points/s (assign only)",
+            "assign of the first {n} points against " + f"{K} centroids" + " ({t:.1f} s), fp64 oracle",
+            host)
+        # parity of the first timed step: assignments on the oracle's prefix,
+        # and the whole update recomputed by the oracle from the GPU's
+        # (prefix-checked) assignments
+        a_gpu, cen_gpu, _ = first
+        same_assign = bool(np.array_equal(a_gpu[:ma], a_or))
+        cen_or, _, _ = oracle.kmeans_update(x, a_gpu, cen_first, 1, jits[0])
+        same_cen = bool(np.array_equal(cen_or.view(np.uint32), cen_gpu.view(np.uint32)))
+        out["parity"] = {"ok": same_assign and same_cen, "assign_equal_on_prefix": same_assign,
+                         "prefix_points": int(ma), "centroids_bit_identical": same_cen,
+                         "rule": "first timed step: assignments identical to the oracle's on the "
+                                 "timed prefix; new centroids bit-identical to the oracle's update"}
     pts.close()
     return out
 
 
-def run_join_workload(args, vs, syn):
+# --------------------------------------------------------------------------
+# C5: self-join
+# --------------------------------------------------------------------------
+def run_join(vs, NN, args, ctx):
     """near-duplicate cosine self-join of 500k x 512 fp32 unit
     vectors (5% planted copies), all pairs i < j with dot >= 0.95 sorted by
     (i, j) (vector_dedup_demo.dart:115-128).  One step = one self-join."""
     import oracle
+    from vector_store import synthetic as syn
 
     n, d, thr = args.n or 500_000, 512, 0.95
     x = syn.dedup_set(n, d, 0.05, 0.01, args.seed)
@@ -291,52 +550,65 @@ def run_join_workload(args, vs, syn):
         g.self_join(thr)
     g.prof_enable(True)
     g.prof_reset()
-    t = time.perf_counter()
-    for i in range(args.steps):
-        pi, pj, ps = g.self_join(thr)
-        log(f"[bench] self-join {i + 1}/{args.steps}: {len(pi)} pairs")
-    wall = time.perf_counter() - t
+    res = {}
+
+    def step():
+        res["p"] = g.self_join(thr)
+
+    wall, times = time_steps(step, args.steps, 0, "c5 self-join")
     g.prof_enable(False)
-    nj, join_ms = g.prof_get("join")
-    join_s = join_ms / max(nj, 1) / 1e3
-    flops = 2.0 * d * n * (n - 1) / 2
+    pi, pj, ps = res["p"]
+    nj, join_s = kernel_avg(g, "join")
     passes = mfma_passes(g)
-    achieved = flops / join_s / 1e12
-    peak = PEAK["bf16_mfma_tflops"] / passes
+    roof = roofline("mfma", 2.0 * d * n * (n - 1) / 2, join_s, ctx["peaks"],
+                    "join scan (upper triangle)", nj, peak_div=passes,
+                    extra={"peak_note": f"bf16 dense MFMA peak / {passes} pass(es) per distance",
+                           "refine_avg_ms": round(kernel_avg(g, "refine")[1] * 1e3, 3)})
     out = {"metric": "cosine self-join, vectors per second", "value": round(n * args.steps / wall, 1),
-           "unit": "vectors/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-           "ms_per_step": round(wall / args.steps * 1e3, 3), "higher_is_better": True,
-           "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+           "unit": "vectors/s", "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": round(wall / args.steps * 1e3, 3), "steps_ms": step_stats(times),
+           "dtype": "fp32",
            "config": {"workload": f"c5: self-join {n} x {d} fp32 unit, 5% planted duplicates, "
                                   f"cos >= {thr}", "n": n, "d": d, "pairs": int(len(pi))},
-           "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": round(peak, 1),
-                        "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": None,
-                        "kernel": "join scan (upper triangle)", "avg_ms": round(join_s * 1e3, 3),
-                        "algorithmic_flops_per_launch": flops,
-                        "peak_note": f"bf16 dense MFMA peak / {passes} pass(es) per distance"}}
+           "roofline": roof}
     if not args.no_cpu:
-        cpu, cores = host_info()
-        threads = min(cores, 16)
-        t = time.perf_counter()
-        oracle.self_join(x, thr, row_begin=0, row_end=threads, nthreads=threads)
-        per_row = (time.perf_counter() - t) / threads
-        rows = int(max(threads, args.cpu_seconds / max(per_row, 1e-9)))
-        t = time.perf_counter()
-        ri, rj, _ = oracle.self_join(x, thr, row_begin=0, row_end=rows, nthreads=threads)
-        dt = time.perf_counter() - t
-        work = sum(n - 1 - i for i in range(rows))
-        total = n * (n - 1) / 2
-        agree = bool(np.array_equal(ri, pi[pi < rows]) and np.array_equal(rj, pj[pi < rows]))
-        out["cpu_baseline"] = {"value": round(n / (dt * total / work), 3), "unit": "vectors/s",
-                               "cores": threads, "kind": "port",
-                               "sample": f"rows 0..{rows - 1} of the upper triangle ({dt:.1f} s), "
-                                         f"extrapolated linearly to all {n} rows; fp64 oracle",
-                               "cpu": cpu}
-        out["pairs_match_cpu_sample"] = agree
+        host = ctx["host"]
+
+        def timed_rows(threads, target):
+            t = time.perf_counter()
+            oracle.self_join(x, thr, row_begin=0, row_end=threads, nthreads=threads)
+            per_row = (time.perf_counter() - t) / threads
+            rows = int(max(threads, target / max(per_row, 1e-9)))
+            rows = min(rows, n)
+            t = time.perf_counter()
+            ri, rj, _ = oracle.self_join(x, thr, row_begin=0, row_end=rows, nthreads=threads)
+            dt = time.perf_counter() - t
+            work = sum(n - 1 - i for i in range(rows))
+            total = n * (n - 1) / 2
+            return n / (dt * total / work), rows, dt, (ri, rj)
+
+        th = host["threads_all_core"]
+        qa, ra, ta, (ri, rj) = timed_rows(th, args.cpu_seconds)
+        one = None
+        if not args.no_single_core:
+            q1, r1, t1, _ = timed_rows(1, args.cpu_seconds / 2)
+            one = (q1, r1, t1)
+        out["cpu_baseline"] = cpu_baseline_entry(
+            (qa, ra, ta), one, "vectors/s",
+            "rows 0..{n} of the upper triangle ({t:.1f} s), extrapolated linearly to all " +
+            f"{n} rows; fp64 oracle", host)
+        sel = pi < ra
+        agree = bool(np.array_equal(ri, pi[sel]) and np.array_equal(rj, pj[sel]))
+        out["parity"] = {"ok": agree, "rows_checked": int(ra), "pairs_checked": int(len(ri)),
+                         "rule": "pair list (i, j) identical to the oracle's for every i in the "
+                                 "checked rows"}
     g.close()
     return out
 
 
+# --------------------------------------------------------------------------
+# yardsticks
+# --------------------------------------------------------------------------
 def run_copy_calibration(args):
     """A plain device copy of known size (the library's copy16 kernel), the
     yardstick for the FETCH_SIZE / WRITE_SIZE counters: under rocprofv3 --pmc
@@ -384,19 +656,32 @@ def run_library_gemm(args):
             "shapes": rows}
 
 
+def guarded(name, fn):
+    try:
+        return fn()
+    except Exception as e:  # one failing workload must not hide the others
+        log(f"[bench] {name} failed: {type(e).__name__}: {e}")
+        return {"error": f"{type(e).__name__}: {e}"[:500]}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", default="c2")
-    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--workload", default="all",
+                    choices=["all", "c1", "c2", "c3", "c4", "c5", "copy", "libgemm"])
+    ap.add_argument("--batch", type=int, default=0, help="c3 alone: one batch size")
+    ap.add_argument("--c3-batches", default="1,64,1024,8192")
     ap.add_argument("--n", type=int, default=0)
     ap.add_argument("--nq", type=int, default=0)
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--k", type=int, default=0, help="override the workload's k")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-single-core", action="store_true")
+    ap.add_argument("--csv", default="", help="write the benchIndex rows as CSV (toBenchCsv)")
+    ap.add_argument("--md", default="", help="write the benchIndex rows as Markdown")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the multi-GPU "
@@ -406,18 +691,52 @@ def main():
         print(json.dumps(run_library_gemm(args)), flush=True)
         return
     import vector_store as vs
-    from vector_store import synthetic as syn
+    from vector_store import _native as NN
 
     if vs.device_count() < 1:
         raise SystemExit("no HIP device visible")
     if args.workload == "copy":
-        out = run_copy_calibration(args)
+        print(json.dumps(run_copy_calibration(args)), flush=True)
+        return
+    ctx = {"host": host_info(), "peaks": measured_peaks(NN)}
+    log(f"[bench] host {ctx['host']}, measured peaks {ctx['peaks']}")
+    if args.workload == "all":
+        out = run_search(vs, NN, "c2", args, ctx, full=True)
+        batches = [int(b) for b in args.c3_batches.split(",") if b]
+        args_n = args.n
+        args.n = 0  # --n applies to single workloads only
+        out["workloads"] = {
+            "c1": guarded("c1", lambda: run_search(vs, NN, "c1", args, ctx)),
+            "c3": guarded("c3", lambda: run_c3(vs, NN, args, ctx, batches)),
+            "c4": guarded("c4", lambda: run_kmeans(vs, NN, args, ctx)),
+            "c5": guarded("c5", lambda: run_join(vs, NN, args, ctx)),
+        }
+        args.n = args_n
+        oks = [out.get("parity", {}).get("ok")]
+        for w, r in out["workloads"].items():
+            if w == "c3" and "batches" in r:
+                oks += [b.get("parity", {}).get("ok") for b in r["batches"].values()]
+            else:
+                oks.append(r.get("parity", {}).get("ok"))
+        out["parity_all_ok"] = all(o is True for o in oks) if not args.no_cpu else None
+    elif args.workload in ("c1", "c2"):
+        out = run_search(vs, NN, args.workload, args, ctx, full=True)
+    elif args.workload == "c3":
+        batches = [args.batch] if args.batch else [int(b) for b in args.c3_batches.split(",") if b]
+        out = run_c3(vs, NN, args, ctx, batches)
     elif args.workload == "c4":
-        out = run_kmeans_workload(args, vs, syn)
-    elif args.workload == "c5":
-        out = run_join_workload(args, vs, syn)
+        out = run_kmeans(vs, NN, args, ctx)
     else:
-        out = run_search_workload(args, vs, syn, None)
+        out = run_join(vs, NN, args, ctx)
+    out["host"] = ctx["host"]
+    out["measured_peaks"] = ctx["peaks"]
+    if ctx.get("bench_rows"):
+        from vector_store.bench import to_bench_csv, to_bench_markdown
+
+        if args.csv:
+            open(args.csv, "w").write(to_bench_csv(ctx["bench_rows"]))
+        if args.md:
+            open(args.md, "w").write(to_bench_markdown(ctx["bench_rows"]))
     print(json.dumps(out), flush=True)
 
 

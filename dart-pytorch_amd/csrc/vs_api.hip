@@ -2167,6 +2167,52 @@ int vs_dev_copy(int device, void *dst, const void *src, int64_t bytes) {
     return VS_OK;
 }
 
+int vs_dev_probe(int device, int what, int64_t bytes, double *result) {
+    if (!result || (what != 0 && what != 1) || (what == 0 && (bytes < (1 << 20) || bytes % 16)))
+        return set_err(VS_ERR_INVALID, "vs_dev_probe: what 0 (bytes >= 1 MiB, 16-byte multiple) or 1");
+    DeviceGuard g(device);
+    if (g.err != hipSuccess) return hip_err(g.err, "hipSetDevice");
+    void *buf = nullptr;
+    VS_HIP(hipMalloc(&buf, what == 0 ? (size_t)bytes + 256 : 256), "probe buffer");
+    struct Free {
+        void *p;
+        ~Free() { (void)hipFree(p); }
+    } fr{buf};
+    hipEvent_t a, b;
+    VS_HIP(hipEventCreate(&a), "event");
+    VS_HIP(hipEventCreate(&b), "event");
+    struct Ev {
+        hipEvent_t a, b;
+        ~Ev() {
+            (void)hipEventDestroy(a);
+            (void)hipEventDestroy(b);
+        }
+    } ev{a, b};
+    int num_cu = 256;
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, device) == hipSuccess) num_cu = p.multiProcessorCount;
+    const int iters = 4096, blocks = num_cu * 8;
+    if (what == 0) VS_HIP(hipMemset(buf, 1, (size_t)bytes), "probe fill");
+    double best = 0.0;
+    for (int rep = 0; rep < 6; ++rep) {
+        VS_HIP(hipEventRecord(a, nullptr), "event");
+        if (what == 0)
+            VS_HIP(vs::launch_read16(buf, bytes / 16, (uint32_t *)((char *)buf + bytes), nullptr),
+                   "read probe");
+        else
+            VS_HIP(vs::launch_mfma_peak(blocks, iters, (float *)buf, nullptr), "mfma probe");
+        VS_HIP(hipEventRecord(b, nullptr), "event");
+        VS_HIP(hipEventSynchronize(b), "probe");
+        float ms = 0.f;
+        VS_HIP(hipEventElapsedTime(&ms, a, b), "probe");
+        const double v = what == 0 ? (double)bytes / (ms * 1e-3) / 1e9
+                                   : (double)blocks * 4 * iters * 8 * 32768.0 / (ms * 1e-3) / 1e12;
+        if (rep > 0) best = std::max(best, v);  // the first run warms up
+    }
+    *result = best;
+    return VS_OK;
+}
+
 int vs_dev_download(int device, void *dst, const void *src, int64_t bytes) {
     DeviceGuard g(device);
     VS_HIP(hipMemcpy(dst, src, (size_t)bytes, hipMemcpyDeviceToHost), "download");

@@ -2083,6 +2083,69 @@ hipError_t launch_copy16(const void *src, void *dst, int64_t n16, hipStream_t st
 }
 
 // ---------------------------------------------------------------------------
+// Measured-peak probes (bench support): a read-only stream of 16-byte loads
+// over a buffer, and back-to-back bf16 MFMAs on registers.
+// ---------------------------------------------------------------------------
+// 8 independent 16-byte loads in flight per lane and step (8 KiB per wave
+// step, 1 KiB contiguous per load instruction)
+__global__ __launch_bounds__(256) void read16_kernel(const u32x4_t *__restrict__ src, int64_t n16,
+                                                     uint32_t *out) {
+    u32x4_t acc[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc[u] = u32x4_t{0u, 0u, 0u, 0u};
+    for (int64_t b = (int64_t)blockIdx.x * 2048 + threadIdx.x; b < n16;
+         b += (int64_t)gridDim.x * 2048) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (b + u * 256 < n16) acc[u] ^= src[b + u * 256];
+    }
+    u32x4_t a = acc[0];
+#pragma unroll
+    for (int u = 1; u < 8; ++u) a ^= acc[u];
+    const uint32_t v = a[0] ^ a[1] ^ a[2] ^ a[3];
+    if (v == 0x9E3779B9u) out[0] = v;  // keeps the loads; the value is never expected
+}
+
+hipError_t launch_read16(const void *src, int64_t n16, uint32_t *out, hipStream_t st) {
+    if (n16 <= 0) return hipSuccess;
+    const int64_t blocks = std::min<int64_t>((n16 + 2047) / 2048, 256 * 8);
+    read16_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>((const u32x4_t *)src, n16, out);
+    return hipGetLastError();
+}
+
+// each wave: iters rounds of 8 independent v_mfma_f32_32x32x16_bf16
+// (32 x 32 x 16 x 2 flop each) on register operands
+__global__ __launch_bounds__(256) void mfma_peak_kernel(int iters, float *out) {
+    const int lane = threadIdx.x & 63;
+    bf16x8_t a, b;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        a[i] = (__bf16)(float)((lane + i) & 7);
+        b[i] = (__bf16)(float)((lane * 3 + i) & 7);
+    }
+    f32x16_t c[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) c[j][v] = 0.f;
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) c[j] = mfma32_bf16(a, b, c[j]);
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) s += c[j][v];
+    if (s == -1.0f) out[0] = s;  // sums of non-negative products: never taken
+}
+
+hipError_t launch_mfma_peak(int blocks, int iters, float *out, hipStream_t st) {
+    mfma_peak_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(iters, out);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // removeIds compaction (index_flat.dart:139-160): row r moves to
 // dst_index[r] (or is dropped when -1).  One wave per row.
 // ---------------------------------------------------------------------------
