@@ -1771,6 +1771,103 @@ int vs_index_range_search(vs_index *x, const void *q, int q_dtype, int64_t nq, d
     return VS_OK;
 }
 
+int vs_index_score_all(vs_index *x, const float *q, float *out) {
+    if (int rc = check_index(x)) return rc;
+    if (!q || (x->ntotal > 0 && !out)) return set_err(VS_ERR_INVALID, "null query or output");
+    if (x->ntotal == 0) return VS_OK;
+    DeviceGuard g(x->device);
+    Arena A;
+    void *pq, *po;
+    VS_TAKE(A.tmp((size_t)x->d * 4, &pq, "query"));
+    VS_TAKE(A.tmp((size_t)x->ntotal * 4, &po, "scores"));
+    for (int64_t j = 0; j < x->d; ++j)
+        if (!std::isfinite(q[j])) return set_err(VS_ERR_NONFINITE, "query contains NaN or infinity");
+    VS_HIP(hipMemcpyAsync(pq, q, (size_t)x->d * 4, hipMemcpyHostToDevice, x->st), "query upload");
+    VS_HIP(vs::launch_exact_all(x->xb, x->storage, x->ld, x->d, x->metric, (const float *)pq,
+                                x->ntotal, (float *)po, x->st),
+           "exact scores");
+    VS_HIP(hipMemcpyAsync(out, po, (size_t)x->ntotal * 4, hipMemcpyDeviceToHost, x->st),
+           "scores download");
+    VS_HIP(hipStreamSynchronize(x->st), "exact scores");
+    return VS_OK;
+}
+
+int vs_index_search_subsets(vs_index *x, const void *q, int q_dtype, int64_t nq, int64_t k,
+                            const int32_t *ids, int64_t nids, const int64_t *seg_off,
+                            const int64_t *seg_len, int64_t nseg, float *D, int32_t *I) {
+    if (int rc = check_index(x)) return rc;
+    if (int rc = check_dtype(q_dtype)) return rc;
+    if (nq < 0 || k < 0 || nids < 0 || nseg < 0)
+        return set_err(VS_ERR_INVALID, "nq, k, nids and nseg must be >= 0");
+    if (nq == 0) return VS_OK;
+    if (k == 0) return set_err(VS_ERR_INVALID, "k must be >= 1");
+    const int64_t kk = std::max<int64_t>(8, next_pow2(k + std::max<int64_t>(4, k / 4)));
+    if (kk > 512)
+        return set_err(VS_ERR_UNSUPPORTED, "subset search: k <= 409 (got %lld)", (long long)k);
+    if (!q || !D || !I || (nq * nseg > 0 && (!seg_off || !seg_len)) || (nids > 0 && !ids))
+        return set_err(VS_ERR_INVALID, "null buffer");
+    for (int64_t t = 0; t < nq * nseg; ++t)
+        if (seg_off[t] < 0 || seg_len[t] < 0 || seg_off[t] + seg_len[t] > nids)
+            return set_err(VS_ERR_INVALID, "segment %lld [%lld, +%lld) outside the %lld ids",
+                           (long long)t, (long long)seg_off[t], (long long)seg_len[t],
+                           (long long)nids);
+    DeviceGuard g(x->device);
+    Arena A;
+    const size_t qbytes = (size_t)nq * x->d * (q_dtype == 1 ? 2 : 4);
+    VS_HIP(x->stage.ensure(qbytes), "query staging");
+    VS_HIP(hipMemcpyAsync(x->stage.p, q, qbytes, hipMemcpyHostToDevice, x->st), "uploading queries");
+    vs::PreparedQueries pq;
+    if (int rc = prepare_queries(x, A, x->stage.p, q_dtype, x->d, nq, &pq, nullptr)) return rc;
+    const int64_t ns = std::max<int64_t>(1, nseg);
+    void *pids, *poff, *plen, *pv, *pi, *pf, *pD, *pI;
+    VS_TAKE(A.tmp((size_t)std::max<int64_t>(nids, 1) * 4, &pids, "ids"));
+    VS_TAKE(A.tmp((size_t)nq * ns * 8, &poff, "segments"));
+    VS_TAKE(A.tmp((size_t)nq * ns * 8, &plen, "segments"));
+    VS_TAKE(A.tmp((size_t)nq * ns * kk * 4, &pv, "lists"));
+    VS_TAKE(A.tmp((size_t)nq * ns * kk * 4, &pi, "lists"));
+    VS_TAKE(A.tmp(4, &pf, "flags"));
+    VS_TAKE(A.tmp((size_t)nq * k * 4, &pD, "results"));
+    VS_TAKE(A.tmp((size_t)nq * k * 4, &pI, "results"));
+    if (nids > 0)
+        VS_HIP(hipMemcpyAsync(pids, ids, (size_t)nids * 4, hipMemcpyHostToDevice, x->st), "ids");
+    if (nseg > 0) {
+        VS_HIP(hipMemcpyAsync(poff, seg_off, (size_t)nq * nseg * 8, hipMemcpyHostToDevice, x->st),
+               "segments");
+        VS_HIP(hipMemcpyAsync(plen, seg_len, (size_t)nq * nseg * 8, hipMemcpyHostToDevice, x->st),
+               "segments");
+    } else {  // one empty segment per query
+        VS_HIP(vs::launch_fill32(poff, nq * 2, 0u, x->st), "segments");
+        VS_HIP(vs::launch_fill32(plen, nq * 2, 0u, x->st), "segments");
+    }
+    VS_HIP(vs::launch_fill32(pf, 1, 0u, x->st), "flags");
+    VS_HIP(vs::launch_exact_lists(x->xb, x->storage, x->ld, x->d, x->metric, pq.qf, nq, x->ntotal,
+                                  (int)kk, ns, 0, (float *)pv, (int32_t *)pi, x->st,
+                                  (const int32_t *)pids, (const int64_t *)poff,
+                                  (const int64_t *)plen, (uint32_t *)pf),
+           "subset lists");
+    vs::ScanPlan plan;
+    plan.kind = 0;
+    plan.bn = 1;
+    plan.lw = 1;
+    plan.kk = (int)kk;
+    plan.kk_final = (int)kk;
+    plan.cap = (int)kk;
+    plan.nqblk = nq;
+    plan.nsplit = ns;
+    VS_HIP(vs::launch_merge_refine(x->xb, x->storage, x->ld, x->d, x->metric, pq, plan,
+                                   (float *)pv, (int32_t *)pi, nullptr, nullptr, nullptr, nullptr,
+                                   k, (float *)pD, (int32_t *)pI, x->ntotal, (uint32_t *)pf, 0,
+                                   nullptr, nullptr, x->st),
+           "subset merge");
+    uint32_t f = 0;
+    VS_HIP(hipMemcpyAsync(&f, pf, 4, hipMemcpyDeviceToHost, x->st), "flags");
+    VS_HIP(hipMemcpyAsync(D, pD, (size_t)nq * k * 4, hipMemcpyDeviceToHost, x->st), "results");
+    VS_HIP(hipMemcpyAsync(I, pI, (size_t)nq * k * 4, hipMemcpyDeviceToHost, x->st), "results");
+    VS_HIP(hipStreamSynchronize(x->st), "subset search");
+    if (f & vs::kFlagBadId) return set_err(VS_ERR_INVALID, "an id in the lists is outside [0, ntotal)");
+    return VS_OK;
+}
+
 void vs_range_result_free(vs_range_result *r) {
     if (!r) return;
     free(r->lims);
@@ -2133,6 +2230,160 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     }
     memcpy(centroids_out, cen_new.data(), (size_t)K * d * 4);
     return VS_OK;
+}
+
+// ---- flat index files (FAISDART kind 0x01, FAISS IxF2 / IxFI / IxFl) ----
+
+}  // extern "C"
+
+namespace {
+
+// Sequential little-endian reader over a file or a caller's buffer.
+struct BlobReader {
+    FILE *f = nullptr;
+    const unsigned char *buf = nullptr;
+    int64_t len = 0, pos = 0;
+    ~BlobReader() {
+        if (f) fclose(f);
+    }
+    // reads n bytes; false at end of data
+    bool read(void *dst, int64_t n) {
+        if (n <= 0) return true;
+        if (f) {
+            if (fread(dst, 1, (size_t)n, f) != (size_t)n) return false;
+            pos += n;
+            return true;
+        }
+        if (pos + n > len) return false;
+        memcpy(dst, buf + pos, (size_t)n);
+        pos += n;
+        return true;
+    }
+    template <typename T>
+    bool get(T *v) {
+        return read(v, sizeof(T));
+    }
+};
+
+// Parses the header (d, metric code of this library, ntotal, is_trained)
+// and leaves the reader at the first fp32 of the row-major payload.
+//   FAISDART (index_io.dart:8-26, IndexFlat.readFrom index_flat.dart:176-188):
+//     'FAISDART', u32 version 1, u32 kind 0x01, u32 d, u32 metric (0 L2 /
+//     1 IP), u32 ntotal, u8 isTrained, ntotal * d fp32;
+//   FAISS (readFaissIndex, faiss_io.dart:1690-1716; header :419-440):
+//     fourcc 'IxF2' / 'IxFI' / 'IxFl', i32 d, i64 ntotal, i64, i64, u8
+//     is_trained, i32 metric (FAISS codes 0 IP / 1 L2), u64 byte count
+//     (= ntotal * d * 4), the rows.
+int parse_flat_header(BlobReader &r, int64_t *d, int *metric, int64_t *ntotal, int *trained) {
+    unsigned char magic[8];
+    if (!r.read(magic, 4)) return set_err(VS_ERR_INVALID, "truncated index blob (no magic)");
+    if (memcmp(magic, "IxF2", 4) == 0 || memcmp(magic, "IxFI", 4) == 0 ||
+        memcmp(magic, "IxFl", 4) == 0) {
+        int32_t dd = 0, fm = 0;
+        int64_t nt = 0, dummy = 0;
+        uint8_t tr = 0;
+        uint64_t nbytes = 0;
+        if (!r.get(&dd) || !r.get(&nt) || !r.get(&dummy) || !r.get(&dummy) || !r.get(&tr) ||
+            !r.get(&fm) || !r.get(&nbytes))
+            return set_err(VS_ERR_INVALID, "truncated FAISS IndexFlat header");
+        if (fm != 0 && fm != 1)
+            return set_err(VS_ERR_INVALID, "Unsupported FAISS metric code %d", (int)fm);
+        if (dd <= 0 || nt < 0) return set_err(VS_ERR_INVALID, "bad FAISS header: d=%d ntotal=%lld",
+                                              (int)dd, (long long)nt);
+        if ((int64_t)nbytes != nt * dd * 4)
+            return set_err(VS_ERR_INVALID, "IndexFlat payload size %llu != ntotal*d*4 = %lld",
+                           (unsigned long long)nbytes, (long long)(nt * dd * 4));
+        *d = dd;
+        *metric = fm == 1 ? VS_METRIC_L2 : VS_METRIC_IP;
+        *ntotal = nt;
+        *trained = tr != 0;
+        return VS_OK;
+    }
+    if (!r.read(magic + 4, 4) || memcmp(magic, "FAISDART", 8) != 0)
+        return set_err(VS_ERR_INVALID, "not a FAISDART or FAISS IndexFlat blob (bad magic)");
+    uint32_t version = 0, kind = 0, dd = 0, m = 0, nt = 0;
+    uint8_t tr = 0;
+    if (!r.get(&version) || !r.get(&kind))
+        return set_err(VS_ERR_INVALID, "truncated FAISDART header");
+    if (version != 1) return set_err(VS_ERR_INVALID, "unsupported FAISDART version %u", version);
+    if (kind != 0x01) return set_err(VS_ERR_UNSUPPORTED, "FAISDART kind %#x is not IndexFlat", kind);
+    if (!r.get(&dd) || !r.get(&m) || !r.get(&nt) || !r.get(&tr))
+        return set_err(VS_ERR_INVALID, "truncated FAISDART header");
+    if (m > 1) return set_err(VS_ERR_INVALID, "Unknown metric code %u", m);
+    if (dd == 0) return set_err(VS_ERR_INVALID, "bad FAISDART header: d=0");
+    *d = dd;
+    *metric = (int)m;
+    *ntotal = nt;
+    *trained = tr != 0;
+    return VS_OK;
+}
+
+int load_flat(int device, BlobReader &r, int storage, vs_index **out, int *is_trained) {
+    int64_t d = 0, ntotal = 0;
+    int metric = 0, trained = 0;
+    if (int rc = parse_flat_header(r, &d, &metric, &ntotal, &trained)) return rc;
+    if (ntotal > (int64_t)INT32_MAX)
+        return set_err(VS_ERR_INVALID, "ids are int32: ntotal %lld too large", (long long)ntotal);
+    vs_index *x = nullptr;
+    if (int rc = vs_index_create(device, d, metric, storage, &x)) return rc;
+    struct Owner {
+        vs_index *x;
+        ~Owner() {
+            if (x) vs_index_destroy(x);
+        }
+    } own{x};
+    if (ntotal > 0) {
+        if (int rc = vs_index_reserve(x, ntotal)) return rc;
+        // the payload goes through one pinned staging buffer of <= 64 MiB
+        const int64_t rowb = d * 4;
+        const int64_t per = std::max<int64_t>(1, std::min<int64_t>(ntotal, (int64_t)(64 << 20) / rowb));
+        HostBuf hb;
+        struct Rel {
+            HostBuf *h;
+            ~Rel() { h->release(); }
+        } rel{&hb};
+        {
+            DeviceGuard g(device);
+            VS_HIP(hb.ensure((size_t)per * rowb), "pinned staging");
+        }
+        for (int64_t r0 = 0; r0 < ntotal; r0 += per) {
+            const int64_t m = std::min(per, ntotal - r0);
+            if (!r.read(hb.p, m * rowb))
+                return set_err(VS_ERR_INVALID, "truncated payload: rows from %lld of %lld missing",
+                               (long long)r0, (long long)ntotal);
+            if (int rc = vs_index_add(x, hb.p, VS_DTYPE_F32, m)) return rc;
+        }
+    }
+    if (is_trained) *is_trained = trained;
+    *out = x;
+    own.x = nullptr;
+    return VS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int vs_index_load_flat(int device, const char *path, int storage, vs_index **out,
+                       int *is_trained) {
+    if (!out) return set_err(VS_ERR_INVALID, "null output handle");
+    *out = nullptr;
+    if (!path) return set_err(VS_ERR_INVALID, "null path");
+    BlobReader r;
+    r.f = fopen(path, "rb");
+    if (!r.f) return set_err(VS_ERR_INVALID, "cannot open %s", path);
+    return load_flat(device, r, storage, out, is_trained);
+}
+
+int vs_index_load_flat_buffer(int device, const void *buf, int64_t len, int storage,
+                              vs_index **out, int *is_trained) {
+    if (!out) return set_err(VS_ERR_INVALID, "null output handle");
+    *out = nullptr;
+    if (!buf || len < 0) return set_err(VS_ERR_INVALID, "null or negative-length buffer");
+    BlobReader r;
+    r.buf = (const unsigned char *)buf;
+    r.len = len;
+    return load_flat(device, r, storage, out, is_trained);
 }
 
 // ---- bench / test support ----

@@ -154,10 +154,20 @@ hipError_t launch_merge_refine(const void *xb, int storage, int64_t ld, int64_t 
 // are [s * rows_per_split, ...); lists cand_v / cand_i [nq][nsplit][kk] hold
 // (fp32 key, id), key = score (L2) or -score (IP), sentinels (+inf, -1).
 // kk: a multiple of 4 in [4, 512].
+// With ids non-null, list (q, s) covers the rows ids[seg_off[q nsplit + s]
+// .. + seg_len[q nsplit + s]) instead of a split (ids outside [0, n) set
+// kFlagBadId in *flags and are skipped).
 hipError_t launch_exact_lists(const void *xb, int storage, int64_t ld, int64_t d, int metric,
                               const float *qf, int64_t nq, int64_t n, int kk, int64_t nsplit,
                               int64_t rows_per_split, float *cand_v, int32_t *cand_i,
-                              hipStream_t st);
+                              hipStream_t st, const int32_t *ids = nullptr,
+                              const int64_t *seg_off = nullptr, const int64_t *seg_len = nullptr,
+                              uint32_t *flags = nullptr);
+
+// out[r] = fp32 of the exact fp64 score of each of the n rows against the
+// fp32 query qf[d] (L2: squared distance, IP: dot).
+hipError_t launch_exact_all(const void *xb, int storage, int64_t ld, int64_t d, int metric,
+                            const float *qf, int64_t n, float *out, hipStream_t st);
 
 // Row gather / scatter of w 32-bit words per row by an index list, and a
 // 32-bit fill.

@@ -1133,6 +1133,11 @@ struct ExactKArgs {
     int64_t nsplit, rows_per_split;
     float *cand_v;
     int32_t *cand_i;
+    // row subsets instead of splits (ids non-null): list (q, s) scans the
+    // rows ids[seg_off[q nsplit + s] .. + seg_len[q nsplit + s])
+    const int32_t *ids;
+    const int64_t *seg_off, *seg_len;
+    uint32_t *flags;  // kFlagBadId for an id outside [0, n)
 };
 
 template <int ST>
@@ -1162,19 +1167,34 @@ __global__ __launch_bounds__(256) void exact_lists_kernel(ExactKArgs a) {
     }
     for (int64_t j = tid; j < a.ld; j += 256) qsh[j] = j < a.d ? a.qf[q * a.d + j] : 0.0f;
     __syncthreads();
-    const int64_t r0 = split * a.rows_per_split;
-    const int64_t r1 = min(a.n, r0 + a.rows_per_split);
+    // rows [r0, r1) of the split, or positions [r0, r1) of the id list
+    int64_t r0 = split * a.rows_per_split;
+    int64_t r1 = min(a.n, r0 + a.rows_per_split);
+    if (a.ids) {
+        r0 = a.seg_off[q * a.nsplit + split];
+        r1 = r0 + a.seg_len[q * a.nsplit + split];
+    }
     for (int64_t base = r0; base < r1; base += 256) {
         const int64_t t = base + tid;
         if (t < r1) {
-            const double ex = exact_score<ST>(qsh, a.xb, a.ld, t, a.d, a.metric);
-            const float key = a.metric == 0 ? (float)ex : -(float)ex;
-            const float th = s_thr;
-            const int thi = s_thr_id;
-            if (key < th || (key == th && (int)t < thi)) {
-                const int pos = atomicAdd(&s_cnt, 1);
-                bv[kk + pos] = key;
-                bi[kk + pos] = (int)t;
+            int64_t row = t;
+            if (a.ids) {
+                row = a.ids[t];
+                if (row < 0 || row >= a.n) {
+                    atomicOr(a.flags, kFlagBadId);
+                    row = -1;
+                }
+            }
+            if (row >= 0) {
+                const double ex = exact_score<ST>(qsh, a.xb, a.ld, row, a.d, a.metric);
+                const float key = a.metric == 0 ? (float)ex : -(float)ex;
+                const float th = s_thr;
+                const int thi = s_thr_id;
+                if (key < th || (key == th && (int)row < thi)) {
+                    const int pos = atomicAdd(&s_cnt, 1);
+                    bv[kk + pos] = key;
+                    bi[kk + pos] = (int)row;
+                }
             }
         }
         __syncthreads();
@@ -1196,11 +1216,15 @@ __global__ __launch_bounds__(256) void exact_lists_kernel(ExactKArgs a) {
 hipError_t launch_exact_lists(const void *xb, int storage, int64_t ld, int64_t d, int metric,
                               const float *qf, int64_t nq, int64_t n, int kk, int64_t nsplit,
                               int64_t rows_per_split, float *cand_v, int32_t *cand_i,
-                              hipStream_t st) {
+                              hipStream_t st, const int32_t *ids, const int64_t *seg_off,
+                              const int64_t *seg_len, uint32_t *flags) {
     if (nq <= 0) return hipSuccess;
     if (kk < 4 || kk > kMergeKeepMax || (kk & 3) || nsplit < 1 || nq * nsplit > INT32_MAX)
         return hipErrorInvalidValue;
-    ExactKArgs a{xb, ld, d, metric, qf, nq, n, kk, nsplit, rows_per_split, cand_v, cand_i};
+    if (ids && (!seg_off || !seg_len || !flags)) return hipErrorInvalidValue;
+    ExactKArgs a{xb,     ld,     d,      metric,         qf,      nq,      n,
+                 kk,     nsplit, rows_per_split, cand_v, cand_i, ids, seg_off,
+                 seg_len, flags};
     const size_t lds = merge_lds(ld);
     void (*fn)(ExactKArgs) = storage == 1 ? exact_lists_kernel<1> : exact_lists_kernel<0>;
     if (lds > 64 * 1024) {
@@ -1209,6 +1233,35 @@ hipError_t launch_exact_lists(const void *xb, int storage, int64_t ld, int64_t d
         if (e != hipSuccess) return e;
     }
     hipLaunchKernelGGL(fn, dim3((unsigned)(nq * nsplit)), dim3(256), lds, st, a);
+    return hipGetLastError();
+}
+
+// out[r] = fp32 of the exact fp64 score of row r against one query
+template <int ST>
+__global__ __launch_bounds__(256) void exact_all_kernel(const void *xb, int64_t ld, int64_t d,
+                                                        int metric, const float *qf, int64_t n,
+                                                        float *out) {
+    extern __shared__ __align__(16) char smem[];
+    float *qsh = (float *)smem;  // [ld], zero past d
+    for (int64_t j = threadIdx.x; j < ld; j += 256) qsh[j] = j < d ? qf[j] : 0.0f;
+    __syncthreads();
+    const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (r < n) out[r] = (float)exact_score<ST>(qsh, xb, ld, r, d, metric);
+}
+
+hipError_t launch_exact_all(const void *xb, int storage, int64_t ld, int64_t d, int metric,
+                            const float *qf, int64_t n, float *out, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    const size_t lds = (size_t)ld * 4;
+    void (*fn)(const void *, int64_t, int64_t, int, const float *, int64_t, float *) =
+        storage == 1 ? exact_all_kernel<1> : exact_all_kernel<0>;
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute((const void *)fn,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(fn, dim3((unsigned)((n + 255) / 256)), dim3(256), lds, st, xb, ld, d, metric,
+                       qf, n, out);
     return hipGetLastError();
 }
 

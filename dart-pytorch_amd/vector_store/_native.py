@@ -32,7 +32,9 @@ EXPORTED = [
     "vs_index_create", "vs_index_destroy", "vs_index_reserve", "vs_index_reset",
     "vs_index_ntotal", "vs_index_d", "vs_index_metric", "vs_index_storage",
     "vs_index_add", "vs_index_add_device", "vs_index_reconstruct", "vs_index_remove_ids",
+    "vs_index_load_flat", "vs_index_load_flat_buffer",
     "vs_index_search", "vs_index_search_device", "vs_index_search_device_noalloc",
+    "vs_index_search_subsets", "vs_index_score_all",
     "vs_index_range_search", "vs_range_result_free",
     "vs_index_self_join", "vs_pairs_free", "vs_kmeans_step", "vs_last_error",
     "vs_dev_alloc", "vs_dev_free", "vs_dev_upload", "vs_dev_download", "vs_dev_copy", "vs_dev_probe",
@@ -108,9 +110,13 @@ def load() -> ctypes.CDLL:
         "vs_index_add_device": ([p, p, i32, i64], i32),
         "vs_index_reconstruct": ([p, i64, i64, p], i32),
         "vs_index_remove_ids": ([p, p, i64, ctypes.POINTER(ctypes.c_int64)], i32),
+        "vs_index_load_flat": ([i32, ctypes.c_char_p, i32, pp, ctypes.POINTER(i32)], i32),
+        "vs_index_load_flat_buffer": ([i32, p, i64, i32, pp, ctypes.POINTER(i32)], i32),
         "vs_index_search": ([p, p, i32, i64, i64, p, p], i32),
         "vs_index_search_device": ([p, p, i32, i64, i64, p, p], i32),
         "vs_index_search_device_noalloc": ([p, p, i32, i64, i64, p, p], i32),
+        "vs_index_search_subsets": ([p, p, i32, i64, i64, p, i64, p, p, i64, p, p], i32),
+        "vs_index_score_all": ([p, p, p], i32),
         "vs_index_range_search": ([p, p, i32, i64, ctypes.c_double,
                                    ctypes.POINTER(ctypes.POINTER(RangeSearchC))], i32),
         "vs_range_result_free": ([ctypes.POINTER(RangeSearchC)], None),

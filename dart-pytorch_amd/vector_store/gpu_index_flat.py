@@ -58,6 +58,24 @@ class GpuIndexFlat(Index):
         return cls(d, Metric.innerProduct, **kw)
 
     @classmethod
+    def _adopt(cls, handle, device: int = 0) -> "GpuIndexFlat":
+        """Wrap an index handle the library created (e.g. vs_index_load_flat)."""
+        lib = N.load()
+        g = cls.__new__(cls)
+        Index.__init__(g, int(lib.vs_index_d(handle)), Metric(lib.vs_index_metric(handle)))
+        g._lib = lib
+        g.device = device
+        g._h = handle
+        return g
+
+    @classmethod
+    def load(cls, src, storage: str = "auto", device: int = 0) -> "GpuIndexFlat":
+        """readIndex / readFaissIndex of a flat index straight into HBM."""
+        from .io import load_flat
+
+        return load_flat(src, storage=storage, device=device)
+
+    @classmethod
     def wrap(cls, src, **kw) -> "GpuIndexFlat":
         """Adopt an existing flat index (anything with d, metric, ntotal and
         reconstruct_n), copying its vectors to the GPU once."""
@@ -154,6 +172,37 @@ class GpuIndexFlat(Index):
         """Queries and results resident in device memory."""
         N.check(self._lib.vs_index_search_device(self._h, qbuf.ptr, dtype, int(nq), int(k), Dbuf.ptr,
                                                  Ibuf.ptr))
+
+    def search_subsets(self, queries, k: int, ids, seg_off, seg_len) -> SearchResult:
+        """Exact top-k of each query over its own row subsets: query i scans
+        ids[seg_off[i, s] : seg_off[i, s] + seg_len[i, s]] for every s (the
+        fine scan of IndexIVFFlat.search, index_ivf_flat.dart:131-170)."""
+        q, code = _dtype_code(queries if isinstance(queries, np.ndarray) else as_rows(queries, self.d))
+        nq = q.shape[0] if q.ndim == 2 else 0
+        if nq == 0:
+            return SearchResult(np.zeros((0, k), np.float32), np.zeros((0, k), np.int32))
+        ids = np.ascontiguousarray(ids, np.int32)
+        off = np.ascontiguousarray(seg_off, np.int64).reshape(nq, -1)
+        ln = np.ascontiguousarray(seg_len, np.int64).reshape(nq, -1)
+        D = np.empty((nq, k), np.float32)
+        I = np.empty((nq, k), np.int32)
+        vp = ctypes.c_void_p
+        N.check(self._lib.vs_index_search_subsets(
+            self._h, q.ctypes.data_as(vp), code, nq, int(k), ids.ctypes.data_as(vp), ids.size,
+            off.ctypes.data_as(vp), ln.ctypes.data_as(vp), off.shape[1], D.ctypes.data_as(vp),
+            I.ctypes.data_as(vp)))
+        return SearchResult(D, I)
+
+    def score_all(self, q) -> np.ndarray:
+        """fp32 of the exact fp64 score of every stored row against q
+        (l2sq / dot, index.dart:181-200)."""
+        v = np.ascontiguousarray(q, np.float32).reshape(-1)
+        if v.size != self.d:
+            raise ValueError(f"query length {v.size} != {self.d}")
+        out = np.empty(self.ntotal, np.float32)
+        N.check(self._lib.vs_index_score_all(self._h, v.ctypes.data_as(ctypes.c_void_p),
+                                             out.ctypes.data_as(ctypes.c_void_p)))
+        return out
 
     def range_search(self, queries, radius: float) -> RangeSearchResult:
         """index_flat.dart:99-137: dist <= radius (L2) or dot >= radius (IP), fp64 test."""

@@ -1,4 +1,6 @@
-"""Flat-index on-disk formats, loaded straight into a GPU index.
+"""Flat-index on-disk formats, loaded straight into a GPU index (load_flat,
+through the library's loader) and read / written on the host (the
+read_* / write_* helpers, used by the tests as the format's checker).
 
 FAISDART (the reference's own format, index_io.dart:8-26): magic
 'FAISDART', u32 version (1), u32 kind (0x01 = IndexFlat), then the common
@@ -92,14 +94,27 @@ def write_faiss_flat(d: int, metric: int, x: np.ndarray, is_trained: bool = True
     return out + struct.pack("<Q", len(payload)) + payload
 
 
-def load_flat(src, **kw):
-    """Read either format and return a GpuIndexFlat holding its vectors in HBM."""
+def load_flat(src, storage: str = "auto", device: int = 0):
+    """A GpuIndexFlat holding the vectors of a FAISDART or FAISS IndexFlat
+    blob (a path, or bytes): the library parses the header and streams the
+    rows into HBM (vs_index_load_flat / vs_index_load_flat_buffer); the host
+    never holds the whole payload when given a path."""
+    import ctypes
+
+    from . import _native as N
     from .gpu_index_flat import GpuIndexFlat
 
-    b = _bytes(src)
-    hdr, x = read_faisdart_flat(b) if b[:8] == FAISDART_MAGIC else read_faiss_flat(b)
-    g = GpuIndexFlat(hdr["d"], Metric(hdr["metric"]), **kw)
-    if hdr["ntotal"]:
-        g.add(x)
-    g.is_trained = hdr["is_trained"]
+    lib = N.load()
+    h = ctypes.c_void_p()
+    trained = ctypes.c_int(0)
+    code = GpuIndexFlat._STORAGE[storage]
+    if isinstance(src, (bytes, bytearray, memoryview)):
+        buf = bytes(src)
+        N.check(lib.vs_index_load_flat_buffer(device, buf, len(buf), code, ctypes.byref(h),
+                                              ctypes.byref(trained)))
+    else:
+        N.check(lib.vs_index_load_flat(device, str(src).encode(), code, ctypes.byref(h),
+                                       ctypes.byref(trained)))
+    g = GpuIndexFlat._adopt(h, device)
+    g.is_trained = bool(trained.value)
     return g

@@ -6,11 +6,15 @@ objective in point order; kmeans.dart:91-105) and update step (fp32 running
 sums in point order scaled by fp64 1/count, empty clusters copied from the
 largest one plus jitter; kmeans.dart:107-140).
 
-Initialisation differs by necessity: the reference's k-means++ draws from
-dart:math Random (kmeans.dart:48-85), whose stream cannot be reproduced
-outside the Dart VM.  Kmeans here seeds with a uniform random subset of the
-points (Philox-seeded numpy generator) unless init_centroids is given; the
-jitter of empty clusters uses the same generator.
+Initialisation is the reference's k-means++ (kmeans.dart:48-85): a uniform
+first pick, closestSq = fp32 of the fp64 squared distance to the nearest
+chosen centroid (refreshed on the GPU by vs_index_score_all after each
+pick), the fp64 running sum in point order, target = u * sum and the first
+point whose running sum reaches it, a uniform pick when the sum is 0.  The
+one generator drives the picks and, in centroid order, the jitter of empty
+clusters only (each step's unused draws are rewound).  The generator is
+numpy's Philox: dart:math Random's stream cannot be reproduced outside the
+Dart VM, so the picks differ from the reference's; the arithmetic does not.
 """
 from __future__ import annotations
 
@@ -52,6 +56,28 @@ def kmeans_step(points: GpuIndexFlat, centroids: np.ndarray, min_points: int = 1
     return assign, out, counts, float(obj.value)
 
 
+def kmeans_pp_init(points: GpuIndexFlat, x: np.ndarray, k: int, rng) -> np.ndarray:
+    """k-means++ seeding (kmeans.dart:48-85) with the points resident in
+    `points` (fp32 storage, the rows of x); rng.integers / rng.random stand
+    for Random.nextInt / nextDouble."""
+    n, d = x.shape
+    cen = np.empty((k, d), np.float32)
+    cen[0] = x[int(rng.integers(n))]
+    closest = points.score_all(cen[0])  # Float32List closestSq (fp32 of the fp64 sum)
+    for c in range(1, k):
+        acc = np.cumsum(closest, dtype=np.float64)  # sum += closestSq[i], in point order
+        total = float(acc[-1])
+        if total <= 0:
+            cen[c] = x[int(rng.integers(n))]
+        else:
+            target = rng.random() * total
+            pick = int(np.searchsorted(acc, target, side="left"))  # first acc >= target
+            cen[c] = x[min(pick, n - 1)]
+        # dsq < closestSq[i] on the fp64 value stores fp32(dsq): the fp32 minimum
+        closest = np.minimum(closest, points.score_all(cen[c]))
+    return cen
+
+
 class Kmeans:
     """kmeans.dart:26-41: Kmeans(d, k, niter=20, seed=1234, minPointsPerCentroid=1)."""
 
@@ -68,18 +94,25 @@ class Kmeans:
         if n < self.k:
             raise ValueError(f"k-means: need at least k={self.k} vectors, got {n}")
         rng = np.random.Generator(np.random.Philox(self.seed))
-        if init_centroids is None:
-            cen = x[rng.choice(n, size=self.k, replace=False)].copy()
-        else:
-            cen = np.ascontiguousarray(init_centroids, dtype=np.float32).copy()
         pts = GpuIndexFlat(self.d, Metric.l2, storage="f32", device=self.device)
         try:
             pts.add(x)
+            if init_centroids is None:
+                cen = kmeans_pp_init(pts, x, self.k, rng)
+            else:
+                cen = np.ascontiguousarray(init_centroids, dtype=np.float32).copy()
             assign = np.zeros(n, np.int32)
             obj = 0.0
             for it in range(self.niter):
-                jitter = rng.random(self.k * self.d)
-                assign, cen, _counts, obj = kmeans_step(pts, cen, self.min_points_per_centroid, jitter)
+                # the step takes jitter draws for its empty clusters, in
+                # centroid order: offer k * d of them, then advance the
+                # generator by only as many as were used
+                state = rng.bit_generator.state
+                offer = rng.random(self.k * self.d)
+                assign, cen, counts, obj = kmeans_step(pts, cen, self.min_points_per_centroid, offer)
+                used = int(np.count_nonzero(counts < self.min_points_per_centroid)) * self.d
+                rng.bit_generator.state = state
+                rng.random(used)
                 if self.verbose:
                     print(f"  k-means iter {it} obj={obj:.4f}")
         finally:

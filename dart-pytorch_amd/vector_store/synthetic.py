@@ -20,10 +20,12 @@ def rng(seed: int, stream: int = 0) -> np.random.Generator:
 
 
 def l2_normalize(x: np.ndarray) -> np.ndarray:
-    x64 = x.astype(np.float64)
-    ss = np.einsum("ij,ij->i", x64, x64)
-    inv = np.where(ss > 0, 1.0 / np.sqrt(np.where(ss > 0, ss, 1.0)), 0.0)
-    return (x64 * inv[:, None]).astype(np.float32)
+    """L2NormTransform.apply: the fp64 sum of squares in dimension order
+    (an accumulating sum, not a pairwise one), norm = sqrt, inv = 1 / norm,
+    fp32(v * inv); zero rows stay zero."""
+    from .wrappers import L2NormTransform
+
+    return L2NormTransform(x.shape[1]).apply(np.asarray(x, np.float32))
 
 
 def to_bf16_bits(x: np.ndarray) -> np.ndarray:

@@ -109,6 +109,21 @@ VS_API int vs_index_reconstruct(vs_index *idx, int64_t i0, int64_t n, float *out
  * [0, ntotal) and duplicates are ignored, as a Set<int> lookup does. */
 VS_API int vs_index_remove_ids(vs_index *idx, const int64_t *ids, int64_t n, int64_t *nremoved);
 
+/* Loads a flat index file into a new index on `device` (storage as
+ * vs_index_create): the reference's FAISDART IndexFlat blob (magic
+ * 'FAISDART', version 1, kind 0x01; index_io.dart:8-26, IndexFlat.readFrom
+ * index_flat.dart:176-188) or a FAISS IndexFlat blob (fourcc IxF2 / IxFI /
+ * IxFl; readFaissIndex faiss_io.dart:1690-1716).  The header is parsed on
+ * the host and the fp32 rows stream into HBM through a pinned staging buffer
+ * of at most 64 MiB.  *is_trained (may be null) receives the header's flag.
+ * Malformed headers give VS_ERR_INVALID with the reference's messages
+ * ("Unknown metric code", "IndexFlat payload size ... != ntotal*d*4"). */
+VS_API int vs_index_load_flat(int device, const char *path, int storage, vs_index **out,
+                              int *is_trained);
+/* Same from a caller's memory buffer of len bytes. */
+VS_API int vs_index_load_flat_buffer(int device, const void *buf, int64_t len, int storage,
+                                     vs_index **out, int *is_trained);
+
 /* ---- search ---- */
 
 /* IndexFlat.search (index_flat.dart:62-97) / GpuIndexFlat.search
@@ -134,6 +149,23 @@ VS_API int vs_index_search_device(vs_index *idx, const void *q_dev, int q_dtype,
  * calls that overlap on one GPU (from several threads or handles) race. */
 VS_API int vs_index_search_device_noalloc(vs_index *idx, const void *q_dev, int q_dtype,
                                           int64_t nq, int64_t k, float *D_dev, int32_t *I_dev);
+
+/* Exact top-k of each query over subsets of the stored rows: query i scans
+ * the rows ids[seg_off[i nseg + s] .. + seg_len[i nseg + s]) for s < nseg --
+ * the fine scan of IndexIVFFlat.search over its probed inverted lists
+ * (index_ivf_flat.dart:131-170): fp64 scores in dimension order, the k best
+ * by (fp32 score, id), sentinels when fewer rows were scanned.  Host
+ * buffers; k <= 409.  An id outside [0, ntotal) gives VS_ERR_INVALID. */
+VS_API int vs_index_search_subsets(vs_index *idx, const void *q, int q_dtype, int64_t nq,
+                                   int64_t k, const int32_t *ids, int64_t nids,
+                                   const int64_t *seg_off, const int64_t *seg_len, int64_t nseg,
+                                   float *D, int32_t *I);
+
+/* out[r] = the exact score of every stored row r against one fp32 query
+ * (host, d values): l2sq / dot of index.dart:181-200 in fp64, rounded to
+ * fp32 -- the closestSq refresh of the k-means++ seeding (kmeans.dart:53-84).
+ * out holds ntotal floats (host). */
+VS_API int vs_index_score_all(vs_index *idx, const float *q, float *out);
 
 /* IndexFlat.rangeSearch (index_flat.dart:99-137): every stored vector with
  * dist <= radius (L2) or dot >= radius (IP), tested on the fp64 score.

@@ -112,3 +112,27 @@ def test_synthetic_generators():
     assert list(syn.bf16_bits_to_f32(b)) == [1.0, 1.0078125, 1.0, 1.015625, -2.5]
     x = syn.dedup_set(1000, 16, 0.05, 0.01, 3)
     assert x.shape == (1000, 16)
+
+
+def test_l2_normalize_is_the_reference_order():
+    """L2NormTransform.apply (l2_norm_transform.dart:23-46) restated with
+    scalar loops: s += v * v in dimension order, inv = 1 / sqrt(s),
+    fp32(v * inv); a zero row stays zero.  The host normaliser must match
+    it bit for bit (a pairwise or reordered sum differs in the last bits of
+    some rows)."""
+    from vector_store import synthetic as syn
+    from vector_store.wrappers import L2NormTransform
+
+    g = np.random.default_rng(8)
+    x = g.standard_normal((40, 301)).astype(np.float32)
+    x[7] = 0.0
+    want = np.empty_like(x)
+    for i, row in enumerate(x):
+        s = 0.0
+        for v in row:
+            s = s + float(v) * float(v)
+        norm = float(np.sqrt(s))
+        want[i] = [np.float32(float(v) * (1.0 / norm)) if norm > 0 else 0.0 for v in row]
+    assert np.array_equal(syn.l2_normalize(x).view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(L2NormTransform(301).apply(x).view(np.uint32), want.view(np.uint32))
+    assert not want[7].any()
