@@ -265,7 +265,7 @@ def run_search(vs, NN, workload, args, ctx, full=False):
     roof = roofline("mfma", 2.0 * nq * n * d, scan_s, ctx["peaks"], "scan", nscan, traffic, tsrc,
                     peak_div=1 if bf16 else 3,
                     extra={"scan_kinds": {f: idx.prof_get(f)[0] for f in
-                                          ("shared", "gemm", "tiled", "streamed")
+                                          ("shared", "gemm", "streamed")
                                           if idx.prof_get(f)[0]},
                            "merge_avg_ms": round(merge_s * 1e3, 4),
                            "prepass_ms_per_step": round(pre_ms / args.steps, 4) if npre else None,
@@ -369,7 +369,7 @@ def run_c3(vs, NN, args, ctx, batches):
         pos = [p for p in C3_SAMPLE if p < B]
         results[B] = (D[pos], I[pos], pos)
         traffic, tsrc = MEASURED_TRAFFIC.get(("c3", n, B, k), (None, None))
-        extra = {"scan_kinds": {f: idx.prof_get(f)[0] for f in ("shared", "gemm", "tiled", "streamed")
+        extra = {"scan_kinds": {f: idx.prof_get(f)[0] for f in ("shared", "gemm", "streamed")
                                 if idx.prof_get(f)[0]},
                  "merge_avg_ms": round(merge_s * 1e3, 4),
                  "prepass_ms_per_step": round(pre_ms / args.steps, 4) if npre else None,

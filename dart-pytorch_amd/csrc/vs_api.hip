@@ -138,8 +138,29 @@ int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
 }  // namespace
 
+// Per-handle planner options (vs_index_set_option).  The defaults are the
+// tuned plan; the others force a path or a shape so that tests can reach
+// every kernel variant on small inputs.
+struct VsOptions {
+    int gemm = -1;         // GEMM-tiled scan: -1 planner rule (rows >= 256 elements), 0 off, 1 any d
+    int gemm_min_nq = 0;   // smallest batch on the GEMM-tiled scan (0: 512 by rule, 256 when forced)
+    int gemm_wq = 0, gemm_qb = 0, gemm_kc = 0;  // force a GEMM shape field (0: any)
+    int gemm_dma = 1;      // LDS-DMA shapes allowed (only where the build enables them)
+    int share = -1;        // row-shared scan: -1 rule (rows of 128 elements), 0 off, 1 also 256
+    int coarse = 1;        // one-pass bf16 selection of fp32 rows (range, self-join, k-means)
+    int copy16 = 1;        // the one-pass selection reads a bf16 copy of the fp32 rows
+    int guess = 1;         // large batches: estimated thresholds from a row sample
+    int prepass = 1;       // small batches: threshold seeding pre-pass
+    int scan_kkw = 0;      // >0: per-list keep forced down to this (tests of the verification)
+    int scan_nw8 = 0;      // streaming scan: eight waves per workgroup where it fits
+    int km16 = 1;          // k-means: the scan reads a bf16 copy of the centroids
+    int km16_rt = 4;       // k-means on that copy: 16-row blocks per tile (2 or 4)
+    int pick_order = 1;    // k-means: the pick walks points grouped by the last step's clusters
+};
+
 struct vs_index {
     int device = 0;
+    VsOptions opt;
     int64_t d = 0;
     int metric = 0;
     int mode = VS_STORAGE_F32;  // requested
@@ -213,9 +234,10 @@ struct ProfScope {
 };
 
 // Counts which scan variant a launch used (always on; read back through
-// vs_prof_get with the families "tiled" and "streamed").
+// vs_prof_get with the families "shared", "gemm", "streamed" and
+// "streamed8", and per GEMM shape).
 void note_scan_kind(vs_index *x, const vs::ScanPlan &plan) {
-    x->prof[plan.kind == 3 ? "shared" : plan.kind == 2 ? "gemm" : plan.kind == 1 ? "tiled" : "streamed"]
+    x->prof[plan.kind == 3 ? "shared" : plan.kind == 2 ? "gemm" : "streamed"]
         .launches++;
     if (plan.kind == 0 && plan.lw == 8) x->prof["streamed8"].launches++;
     if (plan.kind == 2) {  // and per GEMM shape: "gemm:1,1,2,4,4,2,32" or "gemmdma:1,2,4,4,2,4"
@@ -226,12 +248,6 @@ void note_scan_kind(vs_index *x, const vs::ScanPlan &plan) {
         else
             snprintf(key, sizeof key, "gemm:%d,%d,%d,%d,%d,%d,%d", plan.tile_st, plan.tile_pb,
                      plan.lw, plan.g_wq, plan.tile_rb, plan.g_qb, plan.tile_kc);
-        x->prof[key].launches++;
-    }
-    if (plan.kind == 1) {  // and per tiled shape, e.g. "tile:1,1,4,2,64,4"
-        char key[64];
-        snprintf(key, sizeof key, "tile:%d,%d,%d,%d,%d,%d", plan.tile_st, plan.tile_pb,
-                 plan.bn / 32, plan.tile_rb, plan.tile_kc, plan.lw);
         x->prof[key].launches++;
     }
 }
@@ -380,108 +396,15 @@ int check_dtype(int dt) {
 // ---------------------------------------------------------------------------
 // Planning
 // ---------------------------------------------------------------------------
-int env_int(const char *name, int dflt) {
-    const char *v = getenv(name);
-    return v && *v ? atoi(v) : dflt;
-}
-
-// Tiled-scan planning (large batches): picks the first built shape (query
-// blocks, row blocks, K-chunk, waves) whose resident query planes fit the
-// LDS, then the number of database splits so that the grid fills whole
-// rounds of workgroups.  Knobs (for sweeps): VS_TILE (1 enables),
-// VS_TILE_MIN_NQ (smallest batch that uses it), VS_TILE_QB / VS_TILE_RB /
-// VS_TILE_KC / VS_TILE_NW (force a shape), VS_TILE_ROUNDS (target workgroups
-// per CU), VS_TILE_GROUP (query blocks per XCD group).
-bool plan_tile(const vs_index *x, int64_t nq, int64_t nrows, int planes, int storage,
-               vs::ScanPlan *p) {
-    // opt-in until it outruns the streaming scan on the measured workloads
-    if (!env_int("VS_TILE", 0) || nq < env_int("VS_TILE_MIN_NQ", 256)) return false;
-    struct Shape {
-        int st, pb, qb, rb, kc, nw;
-    };
-#define VS_SHAPE_ENTRY(ST_, PB_, QB_, RB_, KC_, NW_) {ST_, PB_, QB_, RB_, KC_, NW_},
-    static const Shape shapes[] = {VS_TILE_SHAPES(VS_SHAPE_ENTRY)};
-#undef VS_SHAPE_ENTRY
-    const int fqb = env_int("VS_TILE_QB", 0), frb = env_int("VS_TILE_RB", 0);
-    const int fkc = env_int("VS_TILE_KC", 0), fnw = env_int("VS_TILE_NW", 0);
-    const Shape *pick = nullptr;
-    int cap = 0;
-    size_t lds = 0;
-    for (const Shape &sh : shapes) {
-        if (sh.st != storage || sh.pb != planes) continue;
-        if (fqb && sh.qb != fqb) continue;
-        if (frb && sh.rb != frb) continue;
-        if (fkc && sh.kc != fkc) continue;
-        if (fnw && sh.nw != fnw) continue;
-        if (x->ld % (2 * sh.kc)) continue;  // >= 2 whole K-chunks per row
-        // a wave may append up to 32 * rb entries per query and row tile
-        cap = (int)next_pow2(p->kk + 32 * sh.rb + 16);
-        lds = vs::tile_lds_bytes(sh.qb, sh.pb, sh.nw, cap, x->ld);
-        if (lds > x->lds_max) continue;
-        pick = &sh;
-        break;
-    }
-    if (!pick) return false;
-    p->kind = 1;
-    p->cap = cap;
-    p->bn = 32 * pick->qb;
-    p->tile_rb = pick->rb;
-    p->tile_kc = pick->kc;
-    p->lw = pick->nw;
-    p->tile_st = pick->st;
-    p->tile_pb = pick->pb;
-    p->nks = 0;
-    p->lds_bytes = lds;
-    p->nqblk = (nq + p->bn - 1) / p->bn;
-    // query blocks per XCD group: the workgroups running together on an XCD
-    // share each database row they read through its L2
-    p->tile_group = std::max<int64_t>(1, std::min<int64_t>(p->nqblk, env_int("VS_TILE_GROUP", 32)));
-    const int64_t tile_rows = (int64_t)pick->nw * 32 * pick->rb;
-    const int64_t ncu = (int64_t)std::max(1, x->num_cu);
-    const int64_t max_split = std::max<int64_t>(1, nrows / (tile_rows * 4));
-    const int64_t rounds = env_int("VS_TILE_ROUNDS", 2);
-    // smallest split count whose grid covers the target rounds of CUs and
-    // fills >= 90% of its last round; else the best fill seen
-    int64_t best = 1;
-    double best_score = -1.0;
-    for (int64_t ns = 1; ns <= max_split; ++ns) {
-        const int64_t blocks = p->nqblk * ns;
-        const double eff = (double)blocks / (double)(((blocks + ncu - 1) / ncu) * ncu);
-        if (blocks >= rounds * ncu && eff >= 0.9) {
-            best = ns;
-            break;
-        }
-        const double score = std::min(1.0, (double)blocks / (double)(rounds * ncu)) * eff;
-        if (score > best_score) {
-            best_score = score;
-            best = ns;
-        }
-        if (blocks >= 4 * rounds * ncu) break;
-    }
-    int64_t rps = round_up((nrows + best - 1) / best, tile_rows);
-    if (rps <= 0) rps = tile_rows;
-    p->rows_per_split = rps;
-    p->nsplit = std::max<int64_t>(1, (nrows + rps - 1) / rps);
-    if (env_int("VS_DEBUG_PLAN", 0))
-        fprintf(stderr,
-                "[vs plan] tiled nq=%lld rows=%lld bn=%d rb=%d kc=%d nw=%d group=%lld kk=%d "
-                "kk_final=%d cap=%d nqblk=%lld nsplit=%lld rows/split=%lld lds=%zu\n",
-                (long long)nq, (long long)nrows, p->bn, p->tile_rb, p->tile_kc, p->lw,
-                (long long)p->tile_group, p->kk, p->kk_final, p->cap, (long long)p->nqblk,
-                (long long)p->nsplit, (long long)p->rows_per_split, p->lds_bytes);
-    return true;
-}
-
 // GEMM-tiled planning (large batches): the first built shape for this
 // storage and query-plane count whose LDS fits, then the number of database
 // splits so that the grid fills whole rounds of workgroups.  Each query has
 // one candidate list per row wave (lw) in a workgroup, so a list keeps at
 // least kk_final / lw entries and the block's lists together bound the
-// query's kk_final-th value.  Knobs (for sweeps): VS_GEMM (0 disables, 1
-// allows every d; default: rows of >= 256 elements), VS_GEMM_MIN_NQ
-// (smallest batch that uses it; default 512, 256 when forced on), VS_GEMM_WQ / VS_GEMM_QB /
-// VS_GEMM_KC (force a shape), VS_GEMM_ROUNDS (target workgroups per CU),
-// VS_GEMM_GROUP (query blocks per XCD group), VS_GEMM_FLUSH (list flush point).
+// query's kk_final-th value.  The grid targets two rounds of workgroups per
+// CU; query blocks go in groups of 32 per XCD.  The options gemm,
+// gemm_min_nq and gemm_wq / gemm_qb / gemm_kc force it on or off and pick a
+// shape.
 // The LDS-DMA kernel (gemm_dma_kernel) is switched off: its first run on an
 // MI355X (8-wave shape, d = 200, L2, k = 10) left the GPU faulted, and no
 // mistake in its indexing, waits or barriers has been shown yet.
@@ -489,21 +412,21 @@ constexpr bool kGemmDmaEnabled = false;
 
 // Row-shared scan (top-k only): bf16 rows of 128 or 256 elements, one query
 // plane, large batches.  Every list keeps kk_final entries (one list per
-// query and workgroup).  VS_SHARE: -1 = default rule (rows of 128 elements,
-// batch >= VS_SHARE_MIN_NQ), 0 = off, 1 = also rows of 256 elements.  The
+// query and workgroup).  Option share: -1 = planner rule (rows of 128
+// elements, batch >= 256), 0 = off, 1 = also rows of 256 elements.  The
 // one-pass selection of fp32 rows (storage kSelectCoarse, k-means) takes
-// rows of 128 and 256 elements.
-// VS_SHARE_ROUNDS: grid size in multiples of the resident workgroups.
+// rows of 128 and 256 elements.  The grid is four times the resident
+// workgroups.
 bool plan_share(const vs_index *x, int64_t nq, int64_t nrows, int planes, int storage,
                 vs::ScanPlan *p, int64_t max_split) {
-    const int mode = env_int("VS_SHARE", -1);
+    const int mode = x->opt.share;
     if (mode == 0 || (storage != 1 && storage != vs::kSelectCoarse) || planes != 1) return false;
     if (!(x->ld == 128 || (x->ld == 256 && (mode > 0 || storage == vs::kSelectCoarse))))
         return false;
-    if (nq < env_int("VS_SHARE_MIN_NQ", 256)) return false;
+    if (nq < 256) return false;
     const int nks = (int)(x->ld / 32), nqb = nks == 4 ? 4 : 2;
     // fp32 tiles: half the rows, the same staging registers
-    const int rt = storage == 1 ? (nks == 4 ? env_int("VS_SHARE_RT", 8) : 4) : 2;
+    const int rt = storage == 1 ? (nks == 4 ? 8 : 4) : 2;
     // a list of the row-shared scan gains up to 16 entries per 16-row block
     // and query; 256 slots at least keep cuts rare while its threshold is
     // still loose (the list is sorted only up to its fill)
@@ -514,7 +437,6 @@ bool plan_share(const vs_index *x, int64_t nq, int64_t nrows, int planes, int st
     p->kind = 3;
     p->tile_st = storage;
     p->share_topm = 0;
-    p->share_ids = 0;
     p->kk = kk;
     p->cap = cap;
     p->nks = nks;
@@ -529,7 +451,7 @@ bool plan_share(const vs_index *x, int64_t nq, int64_t nrows, int planes, int st
     // rows together through that XCD's L2, and no round is left half empty.
     const int bpc = std::max(1, vs::share_blocks_per_cu(storage, nks, p->bn, rt, x->ld, lds, 0));
     const int64_t resident = (int64_t)std::max(1, x->num_cu) * bpc;
-    const int64_t target = resident * std::max(1, env_int("VS_SHARE_ROUNDS", 4));
+    const int64_t target = resident * 4;
     int64_t nsplit = std::max<int64_t>(1, target / p->nqblk);
     nsplit = std::min<int64_t>(nsplit, std::max<int64_t>(1, nrows / (tile_rows * 8)));
     if (max_split > 0) nsplit = std::min<int64_t>(nsplit, max_split);
@@ -537,12 +459,6 @@ bool plan_share(const vs_index *x, int64_t nq, int64_t nrows, int planes, int st
     if (rps <= 0) rps = tile_rows;
     p->rows_per_split = rps;
     p->nsplit = std::max<int64_t>(1, (nrows + rps - 1) / rps);
-    if (env_int("VS_DEBUG_PLAN", 0))
-        fprintf(stderr,
-                "[vs plan] share nq=%lld rows=%lld bn=%d nks=%d rt=%d kk=%d cap=%d nqblk=%lld "
-                "nsplit=%lld rows/split=%lld lds=%zu\n",
-                (long long)nq, (long long)nrows, p->bn, nks, rt, p->kk, p->cap, (long long)p->nqblk,
-                (long long)p->nsplit, (long long)p->rows_per_split, p->lds_bytes);
     return true;
 }
 
@@ -552,22 +468,22 @@ bool plan_gemm(const vs_index *x, int64_t nq, int64_t nrows, int planes, int sto
     // scan beats the streaming one at d = 768, batch >= 1024, and on the
     // k-means assign at d = 256; at d = 128 the streaming scan's 20 waves per
     // CU hide its list work better)
-    const int mode = env_int("VS_GEMM", -1);
+    const VsOptions &o = x->opt;
+    const int mode = o.gemm;
     if (mode == 0) return false;
     if (mode < 0 && x->ld < 256) return false;
-    if (nq < env_int("VS_GEMM_MIN_NQ", mode < 0 ? 512 : 256)) return false;
+    if (nq < (o.gemm_min_nq > 0 ? o.gemm_min_nq : mode < 0 ? 512 : 256)) return false;
     struct Shape {
         int st, pb, wr, wq, rb, qb, kc;
     };
 #define VS_GSHAPE_ENTRY(ST_, PB_, WR_, WQ_, RB_, QB_, KC_) {ST_, PB_, WR_, WQ_, RB_, QB_, KC_},
     static const Shape shapes[] = {VS_GEMM_SHAPES(VS_GSHAPE_ENTRY)};
 #undef VS_GSHAPE_ENTRY
-    const int fwq = env_int("VS_GEMM_WQ", 0), fqb = env_int("VS_GEMM_QB", 0);
-    const int fkc = env_int("VS_GEMM_KC", 0);
+    const int fwq = o.gemm_wq, fqb = o.gemm_qb, fkc = o.gemm_kc;
     const Shape *pick = nullptr;
     int kk = p->kk, cap = 0, ns = 0;
     size_t lds = 0;
-    // LDS-DMA shapes first (bf16 rows; VS_GEMM_DMA=0 disables them)
+    // LDS-DMA shapes first (bf16 rows; option gemm_dma = 0 disables them)
     struct DShape {
         int pb, wr, wq, rb, qb, ns;
     };
@@ -575,7 +491,7 @@ bool plan_gemm(const vs_index *x, int64_t nq, int64_t nrows, int planes, int sto
     static const DShape dshapes[] = {VS_GEMM_DMA_SHAPES(VS_DSHAPE_ENTRY)};
 #undef VS_DSHAPE_ENTRY
     static Shape dpick;
-    if (kGemmDmaEnabled && storage == 1 && env_int("VS_GEMM_DMA", 1) && (!fkc || fkc == 32) &&
+    if (kGemmDmaEnabled && storage == 1 && o.gemm_dma && (!fkc || fkc == 32) &&
         x->ld % 32 == 0) {
         for (const DShape &sh : dshapes) {
             if (sh.pb != planes) continue;
@@ -611,7 +527,6 @@ bool plan_gemm(const vs_index *x, int64_t nq, int64_t nrows, int planes, int sto
     if (!pick) return false;
     p->kind = 2;
     p->g_ns = ns;
-    p->g_flush = env_int("VS_GEMM_FLUSH", 0);
     p->kk = kk;
     p->cap = cap;
     p->bn = 32 * pick->wq * pick->qb;
@@ -625,11 +540,11 @@ bool plan_gemm(const vs_index *x, int64_t nq, int64_t nrows, int planes, int sto
     p->nks = 0;
     p->lds_bytes = lds;
     p->nqblk = (nq + p->bn - 1) / p->bn;
-    p->tile_group = std::max<int64_t>(1, std::min<int64_t>(p->nqblk, env_int("VS_GEMM_GROUP", 32)));
+    p->tile_group = std::max<int64_t>(1, std::min<int64_t>(p->nqblk, 32));
     const int64_t tile_rows = (int64_t)pick->wr * 32 * pick->rb;
     const int64_t ncu = (int64_t)std::max(1, x->num_cu);
     const int64_t max_split = std::max<int64_t>(1, nrows / (tile_rows * 4));
-    const int64_t rounds = env_int("VS_GEMM_ROUNDS", 2);
+    const int64_t rounds = 2;
     // smallest split count whose grid covers the target rounds of CUs and
     // fills >= 90% of its last round; else the best fill seen
     int64_t best = 1;
@@ -652,26 +567,15 @@ bool plan_gemm(const vs_index *x, int64_t nq, int64_t nrows, int planes, int sto
     if (rps <= 0) rps = tile_rows;
     p->rows_per_split = rps;
     p->nsplit = std::max<int64_t>(1, (nrows + rps - 1) / rps);
-    if (env_int("VS_DEBUG_PLAN", 0))
-        fprintf(stderr,
-                "[vs plan] gemm ns=%d nq=%lld rows=%lld bq=%d wr=%d wq=%d rb=%d qb=%d kc=%d group=%lld "
-                "kk=%d kk_final=%d cap=%d nqblk=%lld nsplit=%lld rows/split=%lld lds=%zu\n",
-                p->g_ns, (long long)nq, (long long)nrows, p->bn, p->lw, p->g_wq, p->tile_rb, p->g_qb,
-                p->tile_kc, (long long)p->tile_group, p->kk, p->kk_final, p->cap,
-                (long long)p->nqblk, (long long)p->nsplit, (long long)p->rows_per_split,
-                p->lds_bytes);
     return true;
 }
 
 // Scan planning.  kk_final candidates per query survive the merge; each
 // wave's list keeps kk of them: kk_final itself up to 32, else kk_final / 4
 // (then four lists of a block together bound the kk_final-th value, and the
-// merge verifies that no list dropped a winner; safe forces kk = kk_final).
-// Tuning knobs (for sweeps; defaults are the tuned values): VS_SCAN_TM
-// (16-row blocks per wave tile), VS_SCAN_BN (queries per block),
-// VS_SCAN_BLOCKS_PER_CU (target workgroups per CU), VS_SCAN_QREG (0 disables
-// register-resident queries), VS_SCAN_KKW (per-list keep, for tests of the
-// verification path).
+// merge verifies that no list dropped a winner; safe forces kk = kk_final;
+// the option scan_kkw forces a shorter keep, for tests of the verification
+// path).  The streaming scan targets four workgroups per CU.
 // min_tiles: the fewest row tiles a split of the streaming scan gets (its
 // lists warm up over them; the threshold-seeding scans over small samples
 // use fewer, so that their short sample still spreads over every CU)
@@ -681,7 +585,7 @@ int plan_scan(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t 
               int storage, vs::ScanPlan *p, bool safe = false, int64_t max_lists = 0,
               bool range = false, int min_tiles = 8, size_t list_budget = 0) {
     int64_t kk = kk_final <= 32 ? kk_final : kk_final / 4;
-    const int kkw = env_int("VS_SCAN_KKW", 0);
+    const int kkw = x->opt.scan_kkw;
     if (kkw > 0) kk = std::min<int64_t>(kk_final, std::max<int64_t>(4, next_pow2(kkw)));
     if (safe) kk = kk_final;
     p->kk_final = (int)kk_final;
@@ -689,26 +593,22 @@ int plan_scan(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t 
     p->cap = (int)next_pow2(kk + 48);
     // 16-row blocks per wave tile: one for short rows (d <= 128: measured
     // faster on 1M x 128, the epilogue dominates), two otherwise
-    p->tm = env_int("VS_SCAN_TM", x->ld <= 128 && storage == 1 ? 1 : 2);
-    if (p->tm != 1 && p->tm != 2 && p->tm != 4) p->tm = 2;
+    p->tm = x->ld <= 128 && storage == 1 ? 1 : 2;
     p->kind = 0;
     if (!range && kkw <= 0 && !list_budget &&
         plan_share(x, nq, nrows, planes, storage, p, max_lists))
         return VS_OK;
     // (a list limit shapes the split count of the row-shared and streaming
-    // scans; the tiled scans make few lists per query anyway)
+    // scans; the GEMM-tiled scan makes few lists per query anyway)
     if (!list_budget && plan_gemm(x, nq, nrows, planes, storage, kkw > 0 || safe, p)) return VS_OK;
-    if (!list_budget && plan_tile(x, nq, nrows, planes, storage, p)) return VS_OK;
     const int nks = (int)(x->ld / 32);
-    const int force_bn = env_int("VS_SCAN_BN", 0);
     const int cands[3] = {64, 32, 16};
     p->bn = 0;
     p->nks = 0;
     for (int bn : cands) {
-        if (force_bn && bn != force_bn) continue;
-        if (!force_bn && bn > 16 && round_up(nq, 16) < bn) continue;
-        const bool qreg = env_int("VS_SCAN_QREG", 1) && storage == 1 && planes == 1 &&
-                          (nks == 4 || nks == 8) && nks * (bn / 16) <= 16;
+        if (bn > 16 && round_up(nq, 16) < bn) continue;
+        const bool qreg = storage == 1 && planes == 1 && (nks == 4 || nks == 8) &&
+                          nks * (bn / 16) <= 16;
         if (vs::scan_lds_bytes(bn, qreg ? 0 : planes, x->ld, p->cap, 4) <= x->lds_max) {
             p->bn = bn;
             p->nks = qreg ? nks : 0;
@@ -721,16 +621,17 @@ int plan_scan(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t 
                        (long long)x->d);
     // eight waves per workgroup when the LDS-resident query block leaves room
     // for a single workgroup per CU (bf16 rows): twice the loads in flight
-    // (opt-in, VS_SCAN_NW8=1: measured slightly slower than four on configs[2])
+    // (option scan_nw8: measured slightly slower than four waves on
+    // 20M x 768 bf16, so off by default)
     p->lw = 4;
-    if (storage == 1 && !p->nks && p->tm == 2 && env_int("VS_SCAN_NW8", 0) &&
+    if (storage == 1 && !p->nks && p->tm == 2 && x->opt.scan_nw8 &&
         2 * vs::scan_lds_bytes(p->bn, planes, x->ld, p->cap, 4) > x->lds_max &&
         vs::scan_lds_bytes(p->bn, planes, x->ld, p->cap, 8) <= x->lds_max)
         p->lw = 8;
     p->lds_bytes = vs::scan_lds_bytes(p->bn, p->nks ? 0 : planes, x->ld, p->cap, p->lw);
     p->nqblk = (nq + p->bn - 1) / p->bn;
     const int64_t tile_rows = 16 * p->lw * p->tm;  // rows per block per round
-    const int64_t target = (int64_t)x->num_cu * env_int("VS_SCAN_BLOCKS_PER_CU", 4);
+    const int64_t target = (int64_t)x->num_cu * 4;
     int64_t nsplit = std::max<int64_t>(1, (target + p->nqblk - 1) / p->nqblk);
     const int64_t min_rows = tile_rows * std::max(1, min_tiles);
     nsplit = std::min<int64_t>(nsplit, std::max<int64_t>(1, (nrows + min_rows - 1) / min_rows));
@@ -743,13 +644,6 @@ int plan_scan(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t 
     if (rps <= 0) rps = tile_rows;
     p->rows_per_split = rps;
     p->nsplit = std::max<int64_t>(1, (nrows + rps - 1) / rps);
-    if (env_int("VS_DEBUG_PLAN", 0))
-        fprintf(stderr,
-                "[vs plan] streamed nq=%lld rows=%lld bn=%d tm=%d nks=%d kk=%d kk_final=%d cap=%d "
-                "nqblk=%lld nsplit=%lld rows/split=%lld lds=%zu\n",
-                (long long)nq, (long long)nrows, p->bn, p->tm, p->nks, p->kk, p->kk_final, p->cap,
-                (long long)p->nqblk, (long long)p->nsplit, (long long)p->rows_per_split,
-                p->lds_bytes);
     return VS_OK;
 }
 
@@ -890,6 +784,9 @@ int take_lists(vs_index *x, Arena &A, size_t elems, size_t lists, ListBufs *L) {
 }
 
 // A plan warms up badly when it makes many lists per query over many rows.
+// Rows per sampled row of the small-batch threshold pre-pass.
+constexpr int kPrepassDiv = 1024;
+
 bool needs_seed(const vs_index *x, const vs::ScanPlan &plan) {
     return plan.kind == 0 && plan.nsplit * plan.lw >= 512 && x->ntotal >= (1 << 18);
 }
@@ -914,19 +811,18 @@ int seed_thresholds(vs_index *x, const vs::PreparedQueries &pq, int64_t S, int64
                     int seed_rank = 0, int64_t max_lists = -1, size_t list_budget = 0) {
     S = std::min<int64_t>(S, x->ntotal);
     vs::ScanPlan pp;
-    if (max_lists < 0) max_lists = env_int("VS_PREPASS_LISTS", 0);
+    if (max_lists < 0) max_lists = 0;
     int rc = plan_scan(x, pq.nq, S, pq.planes, kk_final, x->storage, &pp, false, max_lists, false,
-                       env_int("VS_PREPASS_MIN_TILES", 2), list_budget);
+                       2, list_budget);
     if (rc) return rc;
     // an estimate needs only the values of the sample's seed_rank smallest:
     // the row-shared scan then keeps each lane's smallest in registers
     // instead of lists (exact unless one lane met more than m of them; then
     // the estimate is larger, never smaller)
-    if (pp.kind == 3 && seed_rank > 0 && seed_rank <= 4 * vs::share_topm(false) &&
-        env_int("VS_GUESS_TOPM", 1))
-        pp.share_topm = vs::share_topm(false);
+    if (pp.kind == 3 && seed_rank > 0 && seed_rank <= 4 * vs::share_topm_est())
+        pp.share_topm = vs::share_topm_est();
     if ((rc = scan_fits(pp, pq))) return rc;
-    const int div = std::max(2, env_int("VS_PREPASS_DIV", 1024));
+    const int div = kPrepassDiv;
     if (pp.kind == 0 && pp.nsplit * pp.lw >= 512 && S >= (1 << 18)) {
         rc = seed_thresholds(x, pq, std::max<int64_t>(1 << 16, S / div), kk_final, gthr, L,
                              need_elems, need_lists, 0, -1, list_budget);
@@ -964,20 +860,19 @@ int seed_thresholds(vs_index *x, const vs::PreparedQueries &pq, int64_t S, int64
 // per query for every kk_final this build allows).  Queries whose estimate
 // was too tight are found by the merge and searched again exactly.
 bool needs_guess(const vs_index *x, const vs::ScanPlan &plan, int64_t nq) {
-    return env_int("VS_GUESS", 1) && nq >= env_int("VS_GUESS_MIN_NQ", 256) &&
+    return x->opt.guess && nq >= 256 &&
            x->ntotal >= (1 << 18) && plan.nsplit * plan.lw * plan.kk >= 4 * plan.kk_final;
 }
 
 int guess_thresholds(vs_index *x, const vs::PreparedQueries &pq, int64_t kk_final,
                      uint32_t *gthr, ListBufs *L, size_t *need_elems, size_t *need_lists) {
-    const int64_t div = std::max(2, env_int("VS_GUESS_DIV", 32));
+    const int64_t div = 32;
     const int64_t S = std::min<int64_t>(x->ntotal, std::max<int64_t>(4096, x->ntotal / div));
     const double lam = (double)kk_final * (double)S / (double)x->ntotal;
     const int j = (int)std::ceil(lam + 4.0 * std::sqrt(lam) + 4.0);
     const int64_t kkp = std::max<int64_t>(8, next_pow2(j));
     if (L && !x->prof_fixed) x->prof["guess_scans"].launches++;
-    return seed_thresholds(x, pq, S, kkp, gthr, L, need_elems, need_lists, j,
-                           env_int("VS_GUESS_LISTS", 12));
+    return seed_thresholds(x, pq, S, kkp, gthr, L, need_elems, need_lists, j, 12);
 }
 
 // The largest stored row norm (times 1 + 1e-6), cached per row version.
@@ -1153,9 +1048,8 @@ int search_device(vs_index *x, Arena &A, const void *q_dev, int q_dtype, int64_t
     if ((rc = scan_fits(plan, pq))) return rc;
     const bool verify = plan.kk < plan.kk_final;
     const bool guess = !safe && needs_guess(x, plan, nq);
-    const bool seed = !guess && !safe && needs_seed(x, plan) && env_int("VS_PREPASS", 1);
-    const int64_t seed_S =
-        std::max<int64_t>(1 << 16, x->ntotal / std::max(2, env_int("VS_PREPASS_DIV", 1024)));
+    const bool seed = !guess && !safe && needs_seed(x, plan) && x->opt.prepass;
+    const int64_t seed_S = std::max<int64_t>(1 << 16, x->ntotal / kPrepassDiv);
     // candidate lists for the scan and its pre-passes
     size_t elems = list_elems(plan), lists = list_count(plan);
     if (guess) rc = guess_thresholds(x, pq, kk, nullptr, nullptr, &elems, &lists);
@@ -1240,7 +1134,7 @@ int range_core(vs_index *x, const vs::PreparedQueries &pq, double radius, int se
     // acceptance bounds widen to its error and every hit is re-tested exactly
     vs::ScanPlan plan;
     int rc = VS_OK;
-    bool coarse = x->storage == 0 && env_int("VS_COARSE", 1) != 0;
+    bool coarse = x->storage == 0 && x->opt.coarse;
     if (coarse)
         coarse = plan_scan(x, pq.nq, x->ntotal, 1, 8, vs::kSelectCoarse, &plan, false, 0, true) ==
                      VS_OK &&
@@ -1256,7 +1150,7 @@ int range_core(vs_index *x, const vs::PreparedQueries &pq, double radius, int se
     // the fp32 rows' norms, when the copy fits in memory
     const void *scan_rows = x->xb;
     int scan_storage = x->storage;
-    if (coarse && plan.tile_st == vs::kSelectCoarse && env_int("VS_COPY16", 1) != 0) {
+    if (coarse && plan.tile_st == vs::kSelectCoarse && x->opt.copy16) {
         const size_t bytes = (size_t)(x->ntotal + kRowSlack) * x->ld * 2;
         if (x->xb16_version != x->version) {
             x->xb16_version = ~0ull;
@@ -1981,10 +1875,11 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     cview.d = d;
     cview.lds_max = x->lds_max;
     cview.num_cu = x->num_cu;
+    cview.opt = x->opt;
     // one-pass selection (bf16 hi planes of points and centroids) where the
     // GEMM-tiled scan runs it; the shortlist proof below widens its bound
     vs::ScanPlan plan;
-    bool coarse = env_int("VS_COARSE", 1) != 0;
+    bool coarse = x->opt.coarse != 0;
     if (coarse) coarse = plan_scan(&cview, n, K, 1, 16, vs::kSelectCoarse, &plan) == VS_OK &&
                          (plan.kind == 2 || plan.kind == 3);
     if (!coarse) {
@@ -2009,17 +1904,10 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     const float bound = (float)(1.25 * (2.0 * r * pc + gam * ((double)cmax + 2.0 * pc)) + 1e-6);
     // On the row-shared scan each lane appends every value below its running
     // minimum + 2.5 bound to its list (the pick re-scores those within 2 bound
-    // of the smallest and proves the rest worse with the other half bound);
-    // VS_KMIN=0: per-lane register top-m pairs instead (the pick bounds the
-    // rest by each lane's m-th).
+    // of the smallest and proves the rest worse with the other half bound).
     if (coarse && plan.kind == 3) {
-        if (env_int("VS_KMIN", 1) != 0) {
-            plan.share_kmin = 1;
-            plan.kmin_margin = 2.5f * bound;
-        } else {
-            plan.share_topm = vs::share_topm(true);
-            plan.share_ids = 1;
-        }
+        plan.share_kmin = 1;
+        plan.kmin_margin = 2.5f * bound;
     }
     if ((rc = scan_fits(plan, pq))) return rc;
     const size_t nlists = (size_t)plan.nqblk * plan.nsplit * plan.lw * plan.bn;
@@ -2037,7 +1925,7 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     const void *scan_rows = x->km_cen.p;
     int scan_storage = 0;
     if (plan.kind == 3 && plan.share_kmin && plan.tile_st == vs::kSelectCoarse && plan.nks == 8 &&
-        env_int("VS_KM16", 1) != 0) {
+        x->opt.km16) {
         VS_HIP(x->km_cen16.ensure((size_t)(K + kRowSlack) * ld * 2), "centroid copy");
         VS_HIP(x->km_c16n.ensure((size_t)(K + kRowSlack) * 4), "centroid copy");
         VS_HIP(hipMemsetAsync(x->km_cen16.p, 0, (size_t)(K + kRowSlack) * ld * 2, x->st), "clear");
@@ -2046,7 +1934,7 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
                "centroid copy");
         plan.tile_st = 1;
         // bf16 rows stage twice the rows per tile in the same registers
-        const int rt = env_int("VS_KM16_RT", 4);
+        const int rt = x->opt.km16_rt;
         if (rt == 4) {
             const size_t lds = vs::share_lds_bytes(plan.nks, plan.bn / 64, 4, plan.cap);
             if (lds <= x->lds_max) {
@@ -2084,7 +1972,7 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
                                       fb_count, fb_list, x->flags.as<uint32_t>(),
                                       x->lcnt.as<int32_t>(),
                                       x->km_order_version == x->version && x->km_order_n == n &&
-                                              env_int("VS_PICK_ORDER", 1) != 0
+                                              x->opt.pick_order
                                           ? x->km_order.as<int32_t>()
                                           : nullptr,
                                       x->st),
@@ -2512,6 +2400,43 @@ int vs_index_sync(vs_index *x) {
     DeviceGuard g(x->device);
     VS_HIP(hipStreamSynchronize(x->st), "sync");
     return VS_OK;
+}
+
+int vs_index_set_option(vs_index *x, const char *name, int64_t value) {
+    if (int rc = check_index(x)) return rc;
+    if (!name) return set_err(VS_ERR_INVALID, "null option name");
+    struct Opt {
+        const char *name;
+        int VsOptions::*field;
+        int lo, hi;
+    };
+    static const Opt opts[] = {
+        {"gemm", &VsOptions::gemm, -1, 1},
+        {"gemm_min_nq", &VsOptions::gemm_min_nq, 0, 1 << 30},
+        {"gemm_wq", &VsOptions::gemm_wq, 0, 8},
+        {"gemm_qb", &VsOptions::gemm_qb, 0, 8},
+        {"gemm_kc", &VsOptions::gemm_kc, 0, 64},
+        {"gemm_dma", &VsOptions::gemm_dma, 0, 1},
+        {"share", &VsOptions::share, -1, 1},
+        {"coarse", &VsOptions::coarse, 0, 1},
+        {"copy16", &VsOptions::copy16, 0, 1},
+        {"guess", &VsOptions::guess, 0, 1},
+        {"prepass", &VsOptions::prepass, 0, 1},
+        {"scan_kkw", &VsOptions::scan_kkw, 0, 4096},
+        {"scan_nw8", &VsOptions::scan_nw8, 0, 1},
+        {"km16", &VsOptions::km16, 0, 1},
+        {"km16_rt", &VsOptions::km16_rt, 2, 4},
+        {"pick_order", &VsOptions::pick_order, 0, 1},
+    };
+    for (const Opt &o : opts) {
+        if (strcmp(o.name, name) != 0) continue;
+        if (value < o.lo || value > o.hi || (o.field == &VsOptions::km16_rt && value == 3))
+            return set_err(VS_ERR_INVALID, "option %s: value %lld outside [%d, %d]", name,
+                           (long long)value, o.lo, o.hi);
+        x->opt.*(o.field) = (int)value;
+        return VS_OK;
+    }
+    return set_err(VS_ERR_INVALID, "unknown option \"%s\"", name);
 }
 
 }  // extern "C"

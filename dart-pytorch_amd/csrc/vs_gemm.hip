@@ -816,7 +816,7 @@ hipError_t launch_gemm_scan(int storage, int planes, const ScanPlan &plan, const
     ga.publish_block = plan.lw * plan.kk >= plan.kk_final;
     // cut lists at twice their keep: each cut tightens the list's threshold
     // for the price of one sort of ~2 kk entries
-    ga.flush_at = plan.g_flush > 0 ? plan.g_flush : std::max(2 * plan.kk, 16);
+    ga.flush_at = std::max(2 * plan.kk, 16);
     void (*fn)(ScanKArgs) = nullptr;
 #define VS_DPICK(PB_, WR_, WQ_, RB_, QB_, NS_)                                                 \
     if (storage == 1 && planes == PB_ && plan.lw == WR_ && plan.g_wq == WQ_ &&                  \

@@ -87,21 +87,20 @@ struct ScanPlan {
     int cap = 64;         // per-list buffer capacity (power of two)
     int nks = 0;          // >0: queries held in registers for this many K-steps
     int lw = 4;           // candidate lists per (workgroup, query): the workgroup's waves
-    int kind = 0;         // 0: streaming scan (vs_kernels.hip); 1: LDS-tiled scan (vs_tile.hip);
+    int kind = 0;         // 0: streaming scan (vs_kernels.hip);
                           // 2: GEMM-tiled scan (vs_gemm.hip); 3: row-shared scan (vs_share.hip:
                           // nks K-steps, bn = 64 * query blocks per wave, tm = 16-row blocks per tile)
     int g_ns = 0;            // GEMM-tiled scan: LDS-DMA stages (0: register-staged kernel)
-    int g_flush = 0;         // GEMM-tiled scan: list flush point (0: twice the keep)
     int g_wq = 2, g_qb = 4;  // GEMM-tiled scan: query waves, 32-query blocks per wave
                              // (row waves = lw, 32-row blocks per wave = tile_rb,
                              // K-chunk = tile_kc)
-    int tile_rb = 2;      // tiled scan: 32-row blocks per wave (row tile = 128 * tile_rb rows)
-    int tile_kc = 64;     // tiled scan: K-chunk per pipeline step (elements)
-    int tile_st = 1, tile_pb = 1;  // tiled scan: storage and query planes it was planned for
-    int64_t tile_group = 8;        // tiled scan: query blocks per XCD group (grid order)
+    int tile_rb = 2;      // GEMM-tiled scan: 32-row blocks per wave
+    int tile_kc = 32;     // GEMM-tiled scan: K-chunk per pipeline step (elements)
+    int tile_st = 1, tile_pb = 1;  // GEMM-tiled and row-shared scans: storage and query planes
+                                   // they were planned for
+    int64_t tile_group = 8;        // GEMM-tiled scan: query blocks per XCD group (grid order)
     int share_topm = 0;   // row-shared scan: >0 keeps per-lane register top-m values (sample
                           // estimates; lists get 4 * m values per query and workgroup, ids 0)
-    int share_ids = 0;    // with share_topm: the ids too, lane g's m pairs at slots [g m, g m + m)
     int share_kmin = 0;   // row-shared scan: k-means lists (each lane appends what lies below its
                           // running minimum + kmin_margin; a list that would fill is marked
                           // full, count cap + 1, and takes no more)
@@ -268,25 +267,6 @@ hipError_t launch_gen_normal(void *dst, int out_dtype, int64_t n, int64_t d, uin
 // Shape rules shared by the host planner and the kernels.
 int64_t storage_ld(int64_t d, int storage);  // elements per stored row
 size_t scan_lds_bytes(int bn, int planes, int64_t ld, int cap, int nw);
-// LDS of the tiled scan: qb query blocks of 16, rb row blocks of 16 per wave,
-// K-chunk kc, pa row planes, pb query planes, list capacity cap.
-size_t tile_lds_bytes(int qb, int pb, int nw, int cap, int64_t ld);
-
-// The built shapes of the tiled scan, in the planner's order of preference:
-// X(storage, query planes, query blocks of 32, row blocks of 32 per wave,
-//   K-chunk, waves per workgroup).  The block's query planes stay in LDS.
-#define VS_TILE_SHAPES(X)                                                                     \
-    X(1, 1, 4, 2, 64, 4)                                                                      \
-    X(1, 1, 4, 2, 32, 8)                                                                      \
-    X(1, 1, 3, 2, 64, 4)                                                                      \
-    X(1, 1, 3, 2, 32, 8)                                                                      \
-    X(1, 1, 2, 2, 64, 4)                                                                      \
-    X(1, 2, 2, 2, 64, 4)                                                                      \
-    X(0, 2, 4, 2, 32, 4)                                                                      \
-    X(0, 2, 2, 2, 32, 4)                                                                      \
-    X(0, 1, 4, 2, 32, 4)                                                                      \
-    X(0, 1, 2, 2, 32, 4)
-
 // The built shapes of the GEMM-tiled scan, in the planner's order of
 // preference: X(storage, query planes, row waves, query waves, 32-row blocks
 // per wave, 32-query blocks per wave, K-chunk).  A workgroup covers
@@ -323,18 +303,16 @@ size_t gemm_lds_bytes(int st, int pb, int wr, int wq, int rb, int qb, int kc, in
 // LDS of the row-shared scan (two row stages plus list bookkeeping).
 size_t share_lds_bytes(int nks, int nqb, int rt, int cap);
 // Row-shared scan workgroups one CU holds at once (0: no such shape; mode 0
-// lists, 2 top-m values, 3 top-m values and ids).
+// lists, 2 top-m values, 4 k-means lists).
 int share_blocks_per_cu(int st, int nks, int bn, int rt, int64_t ld, size_t lds, int mode);
-// m of the row-shared scan's register top-m variant.
-int share_topm(bool ids);  // slots per lane: with ids (k-means) or values only (estimates)
+// m of the row-shared scan's register top-m variant (threshold estimates):
+// values kept per lane and query.
+int share_topm_est();
 
 struct ScanKArgs;
 hipError_t launch_share_scan(const ScanPlan &plan, const ScanKArgs &args, hipStream_t st);
 template <int MODE>
 hipError_t launch_gemm_scan(int storage, int planes, const ScanPlan &plan, const ScanKArgs &args,
-                            hipStream_t st);
-template <int MODE>
-hipError_t launch_tile_scan(int storage, int planes, const ScanPlan &plan, const ScanKArgs &args,
                             hipStream_t st);
 
 }  // namespace vs

@@ -552,7 +552,6 @@ __global__ __launch_bounds__(64 * NW) void scan_kernel(ScanKArgs a) {
 template <int MODE>
 static hipError_t launch_scan_mode(int storage, const PreparedQueries &pq, const ScanPlan &plan,
                                    const ScanKArgs &args, hipStream_t st) {
-    if (plan.kind == 1) return launch_tile_scan<MODE>(storage, pq.planes, plan, args, st);
     if (plan.kind == 2) return launch_gemm_scan<MODE>(plan.tile_st, plan.tile_pb, plan, args, st);
     if (plan.kind == 3) return MODE == 0 ? launch_share_scan(plan, args, st) : hipErrorInvalidValue;
     const int64_t total = plan.nqblk * plan.nsplit;
@@ -686,8 +685,6 @@ struct MergeKArgs {
     int32_t *vf_count;    // queries whose lists may have dropped a winner
     int32_t *vf_list;
     int guess;            // thresholds were estimated: flag queries left short
-    int seg_m;            // k-means pick: lists are 4 sorted segments of seg_m pairs, one per
-                          // scan lane; rows a lane dropped are >= its segment's last value
     int seed_rank;        // MODE 2: rank whose value sets the threshold (0: kk)
     float kmin_margin;    // k-means pick over the row-shared scan's k-means lists
     const int32_t *order; // k-means pick: points in this order (a permutation of [0, nq)), or null
@@ -1313,8 +1310,7 @@ hipError_t launch_fill32(void *p, int64_t n, uint32_t v, hipStream_t st) {
 
 template <int KK>
 __global__ void kmeans_pick_kernel(MergeKArgs a);
-__global__ void kmeans_pick_seg_kernel(MergeKArgs a);
-template <int E, int CH, bool LISTS>
+template <int E, int CH>
 __global__ void kmeans_pick_wave_kernel(MergeKArgs a);
 
 // Threshold estimates from a pre-pass (seed_rank <= 64): one wave per query.
@@ -1408,12 +1404,6 @@ hipError_t launch_merge_threshold(const PreparedQueries &pq, const ScanPlan &pla
     return hipGetLastError();
 }
 
-// VS_PICK_WAVE=0 keeps the one-lane-per-point pick for register shortlists
-static bool pick_wave_enabled() {
-    const char *v = getenv("VS_PICK_WAVE");
-    return !(v && v[0] == '0');
-}
-
 hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, const float *cen,
                               int64_t K, const float *cand_v, const int32_t *cand_i,
                               const uint32_t *gthr, const ScanPlan &plan, float bound,
@@ -1454,24 +1444,11 @@ hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, 
         a.kmin_margin = plan.kmin_margin;
         a.kl = plan.cap;
         a.order = order;
-        kmeans_pick_wave_kernel<32, 16, true>
+        kmeans_pick_wave_kernel<32, 16>
             <<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(a);
         return hipGetLastError();
     }
-    if (plan.kind == 3) {
-        // per-lane register shortlists of the row-shared scan: 4 segments of
-        // m pairs per list
-        if (!plan.share_topm || !plan.share_ids || 4 * plan.share_topm != 32 ||
-            plan.cap < 4 * plan.share_topm)
-            return hipErrorInvalidValue;
-        a.kl = 4 * plan.share_topm;
-        a.seg_m = plan.share_topm;
-        if (ld % 16 == 0 && pick_wave_enabled())
-            kmeans_pick_wave_kernel<32, 16, false><<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(a);
-        else
-            kmeans_pick_seg_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(a);
-        return hipGetLastError();
-    }
+    if (plan.kind == 3) return hipErrorInvalidValue;  // row-shared lists are k-means lists only
     if (plan.kk_final == 16 && plan.kk == 16) {
         kmeans_pick_kernel<16><<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(a);
         return hipGetLastError();
@@ -1590,87 +1567,8 @@ __global__ __launch_bounds__(256) void kmeans_pick_kernel(MergeKArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// k-means pick over per-lane register shortlists (the row-shared scan): one
-// lane per point.  Each list holds 4 sorted segments of seg_m (accumulator,
-// centroid) pairs, one per scan lane, and every centroid a lane dropped has
-// an accumulator at or above the last value of its segment.  Pass 1 finds
-// the smallest accumulator and that bound; pass 2 re-scores exactly -- fp64,
-// dimensions in order -- every candidate within 2 * bound of the smallest
-// (any other is provably worse than it) and takes the argmin with the lowest
-// id among equal scores.  The pick is proven when every centroid outside the
-// segments is provably worse; unproven points go to the exhaustive kernel.
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void kmeans_pick_seg_kernel(MergeKArgs a) {
-    const int64_t qg = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (qg >= a.nq) return;
-    const int64_t qblk = qg / a.bn, q = qg % a.bn;
-    const int64_t nlists = a.nsplit * a.lw;
-    auto list_off = [&](int64_t l) {
-        const int64_t split = l / a.lw, w = l % a.lw;
-        return (((qblk * a.nsplit + split) * a.lw + w) * a.bn + q) * a.cap;
-    };
-    float vmin = VS_INF, seg_bound = VS_INF;
-    for (int64_t l = 0; l < nlists; ++l) {
-        const int64_t off = list_off(l);
-        for (int sgi = 0; sgi < 4; ++sgi) {
-            const float head = a.cand_v[off + sgi * a.seg_m];
-            const int hid = a.cand_i[off + sgi * a.seg_m];
-            if (hid >= 0) vmin = fminf(vmin, head);
-            seg_bound = fminf(seg_bound, a.cand_v[off + sgi * a.seg_m + a.seg_m - 1]);
-        }
-    }
-    const float lim = vmin + 2.0f * a.bound;
-    const float4 *xr = (const float4 *)(a.pts + qg * a.ld);
-    const float *cen = (const float *)a.xb;
-    const int64_t n4 = a.ld / 4;
-    double best = __builtin_huge_val(), xx = 0.0;
-    int bid = INT_MAX;
-    for (int64_t j4 = 0; j4 < n4; ++j4) {
-        const float4 xv = xr[j4];
-        xx = xx + (double)xv.x * (double)xv.x;
-        xx = xx + (double)xv.y * (double)xv.y;
-        xx = xx + (double)xv.z * (double)xv.z;
-        xx = xx + (double)xv.w * (double)xv.w;
-    }
-    for (int64_t l = 0; l < nlists; ++l) {
-        const int64_t off = list_off(l);
-        for (int e = 0; e < a.kl; ++e) {
-            const int id = a.cand_i[off + e];
-            if (id < 0 || a.cand_v[off + e] > lim) continue;
-            if ((int64_t)id >= a.nrows) {
-                atomicOr(a.flags, kFlagBadId);
-                continue;
-            }
-            const float4 *cr = (const float4 *)(cen + (int64_t)id * a.ld);
-            double sc = 0.0;
-            for (int64_t j4 = 0; j4 < n4; ++j4) {
-                const float4 xv = xr[j4];
-                const float4 cv = cr[j4];
-                const double d0 = (double)xv.x - (double)cv.x, d1 = (double)xv.y - (double)cv.y;
-                const double d2 = (double)xv.z - (double)cv.z, d3 = (double)xv.w - (double)cv.w;
-                sc = sc + d0 * d0;
-                sc = sc + d1 * d1;
-                sc = sc + d2 * d2;
-                sc = sc + d3 * d3;
-            }
-            if (sc < best || (sc == best && id < bid)) {
-                best = sc;
-                bid = id;
-            }
-        }
-    }
-    // accumulators are within `bound` of |c|^2 - 2 x.c = score - |x|^2
-    const bool safe = bid != INT_MAX &&
-                      (seg_bound == VS_INF ||
-                       (double)seg_bound - (double)a.bound > (best - xx) + 1e-9 * (fabs(xx) + 1.0));
-    a.assign[qg] = bid == INT_MAX ? 0 : bid;
-    a.best_sq[qg] = best;
-    if (!safe) a.fb_list[atomicAdd(a.fb_count, 1)] = (int32_t)qg;
-}
-
-// ---------------------------------------------------------------------------
-// The same pick with the exact re-scoring staged through LDS: one wave per
-// 64 points (lane = point).  Each lane gathers the ids of its candidates
+// k-means pick over the row-shared scan's k-means lists, the exact
+// re-scoring staged through LDS: one wave per 64 points (lane = point).  Each lane gathers the ids of its candidates
 // within 2 * bound of its smallest accumulator (at most E; a point with more
 // goes to the exhaustive kernel, whose exact argmin is the same answer).
 // The rows are then walked in chunks of CH dimensions: the chunk of the
@@ -1680,13 +1578,13 @@ __global__ __launch_bounds__(256) void kmeans_pick_seg_kernel(MergeKArgs a) {
 // own fp64 sums in dimension order -- the order, and so the rounding, of
 // the one-lane-per-point kernel above.
 //
-// LISTS: the scan's k-means lists instead of segments (count-terminated;
-// every lane appended what lay below its running minimum + kmin_margin, so
-// every centroid outside the lists has an accumulator at or above vmin +
-// kmin_margin, rounded as the scan rounds it; a list marked full, count cap
-// + 1, sends its point to the exhaustive kernel).
+// The lists are count-terminated: every scan lane appended what lay below
+// its running minimum + kmin_margin, so every centroid outside the lists has
+// an accumulator at or above vmin + kmin_margin, rounded as the scan rounds
+// it; a list marked full, count cap + 1, sends its point to the exhaustive
+// kernel.
 // ---------------------------------------------------------------------------
-template <int E, int CH, bool LISTS>
+template <int E, int CH>
 __global__ __launch_bounds__(256) void kmeans_pick_wave_kernel(MergeKArgs a) {
     constexpr int RS = 65;  // LDS words per staged dimension (64 rows + 1: no bank conflicts on reads)
     constexpr int PIECES = CH / 4;            // 16-byte pieces per row chunk
@@ -1713,57 +1611,42 @@ __global__ __launch_bounds__(256) void kmeans_pick_wave_kernel(MergeKArgs a) {
         const int64_t split = l / a.lw, w = l % a.lw;
         return (((qblk * a.nsplit + split) * a.lw + w) * a.bn + q) * a.cap;
     };
-    float vmin = VS_INF, seg_bound = VS_INF;
+    float vmin = VS_INF;
     bool over = false;
     auto list_len = [&](int64_t l) -> int {
-        if constexpr (LISTS) {
-            const int64_t split = l / a.lw, w = l % a.lw;
-            const int c = a.list_cnt[((qblk * a.nsplit + split) * a.lw + w) * a.bn + q];
-            return c > a.cap ? 0 : c;
-        } else {
-            return a.kl;
-        }
+        const int64_t split = l / a.lw, w = l % a.lw;
+        const int c = a.list_cnt[((qblk * a.nsplit + split) * a.lw + w) * a.bn + q];
+        return c > a.cap ? 0 : c;
     };
     for (int64_t l = 0; l < nlists; ++l) {
         const int64_t off = list_off(l);
-        if constexpr (LISTS) {
-            const int64_t split = l / a.lw, w = l % a.lw;
-            if (a.list_cnt[((qblk * a.nsplit + split) * a.lw + w) * a.bn + q] > a.cap) over = true;
-            // every appended entry has a real id; 16-byte reads (lists hold
-            // a multiple of 4 slots)
-            const int lc = list_len(l);
-            for (int e = 0; e < lc; e += 4) {
-                const float4 v4 = *(const float4 *)(a.cand_v + off + e);
-                vmin = fminf(vmin, v4.x);
-                if (e + 1 < lc) vmin = fminf(vmin, v4.y);
-                if (e + 2 < lc) vmin = fminf(vmin, v4.z);
-                if (e + 3 < lc) vmin = fminf(vmin, v4.w);
-            }
-        } else {
-            for (int sgi = 0; sgi < 4; ++sgi) {
-                const float head = a.cand_v[off + sgi * a.seg_m];
-                const int hid = a.cand_i[off + sgi * a.seg_m];
-                if (hid >= 0) vmin = fminf(vmin, head);
-                seg_bound = fminf(seg_bound, a.cand_v[off + sgi * a.seg_m + a.seg_m - 1]);
-            }
+        const int64_t split = l / a.lw, w = l % a.lw;
+        if (a.list_cnt[((qblk * a.nsplit + split) * a.lw + w) * a.bn + q] > a.cap) over = true;
+        // every appended entry has a real id; 16-byte reads (lists hold a
+        // multiple of 4 slots)
+        const int lc = list_len(l);
+        for (int e = 0; e < lc; e += 4) {
+            const float4 v4 = *(const float4 *)(a.cand_v + off + e);
+            vmin = fminf(vmin, v4.x);
+            if (e + 1 < lc) vmin = fminf(vmin, v4.y);
+            if (e + 2 < lc) vmin = fminf(vmin, v4.z);
+            if (e + 3 < lc) vmin = fminf(vmin, v4.w);
         }
     }
     // every centroid outside the lists: accumulator >= vmin + margin (the
     // scan's fp32 sum, monotone in vmin)
-    if constexpr (LISTS) seg_bound = vmin + a.kmin_margin;
+    const float seg_bound = vmin + a.kmin_margin;
     const float lim = vmin + 2.0f * a.bound;
     int ne = 0;
     for (int64_t l = 0; l < nlists; ++l) {
         const int64_t off = list_off(l);
         const int lc = list_len(l);
         for (int e = 0; e < lc; ++e) {
-            if constexpr (LISTS) {  // values four at a time; ids of the candidates only
-                if ((e & 3) == 0) {
-                    const float4 v4 = *(const float4 *)(a.cand_v + off + e);
-                    if (!(v4.x <= lim || v4.y <= lim || v4.z <= lim || v4.w <= lim)) {
-                        e += 3;
-                        continue;
-                    }
+            if ((e & 3) == 0) {  // values four at a time; ids of the candidates only
+                const float4 v4 = *(const float4 *)(a.cand_v + off + e);
+                if (!(v4.x <= lim || v4.y <= lim || v4.z <= lim || v4.w <= lim)) {
+                    e += 3;
+                    continue;
                 }
             }
             if (a.cand_v[off + e] > lim) continue;

@@ -63,18 +63,15 @@ size_t share_lds_bytes(int nks, int nqb, int rt, int cap) {
 // registers, and writes them out at the end (4 * TOPM values per query and
 // workgroup, ids 0).  The r-th smallest value of their union is the query's
 // r-th smallest over the rows whenever no lane met more than TOPM of those r,
-// and larger otherwise, never smaller.  MODE 3 (shortlists, k-means): the
-// same with the row ids; lane g's TOPM pairs fill slots [g TOPM, (g + 1)
-// TOPM) of the query's list, sorted, so every row the lane dropped is at or
-// above the last of its slots.
-constexpr int kShareTopM = 8;    // MODE 3
+// and larger otherwise, never smaller.  MODE 4 (k-means lists): each lane
+// appends what lies below its own running minimum + kmin_margin.
 constexpr int kShareTopMEst = 4; // MODE 2: the estimate needs the 16 smallest of a sample
-                                 // spread over many lanes; fewer slots, cheaper insertions
+                                 // spread over many lanes; four slots keep insertions cheap
 
 template <int ST, int NKS, int NQB, int RT, int MODE>
 __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
     using S = ShareShape<ST, NKS, NQB, RT>;
-    constexpr int TOPM = MODE == 2 ? kShareTopMEst : kShareTopM;
+    constexpr int TOPM = kShareTopMEst;
     constexpr int TR = S::TR, KP = S::KP, BNW = S::BNW;
     extern __shared__ __align__(16) char smem[];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r16 = lane & 15, g = lane >> 4;
@@ -178,16 +175,12 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
         for (int qb = 0; qb < NQB; ++qb) thr_r[qb] = fminf(thr_r[qb], dec_order(gt[qb]));
     }
 
-    constexpr bool TOPMODE = MODE == 2 || MODE == 3;
+    constexpr bool TOPMODE = MODE == 2;
     float top[TOPMODE ? NQB : 1][TOPM];
-    int topi[MODE == 3 ? NQB : 1][TOPM];
 #pragma unroll
     for (int qb = 0; qb < (TOPMODE ? NQB : 1); ++qb)
 #pragma unroll
-        for (int m = 0; m < TOPM; ++m) {
-            top[qb][m] = VS_INF;
-            if constexpr (MODE == 3) topi[qb][m] = -1;
-        }
+        for (int m = 0; m < TOPM; ++m) top[qb][m] = VS_INF;
 
     const f32x4_t zero4 = {0.f, 0.f, 0.f, 0.f};
     int par = 0;
@@ -228,8 +221,6 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
 
             if constexpr (TOPMODE) {
                 // sorted insertion of each value below the lane's TOPM-th
-                // (rows arrive in increasing order per lane: a tie keeps the
-                // lower id first)
 #pragma unroll
                 for (int qb = 0; qb < NQB; ++qb) {
                     const float m4 =
@@ -239,25 +230,11 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
                     for (int i = 0; i < 4; ++i) {
                         float v = acc[qb][i];
                         if (v < top[qb][TOPM - 1]) {
-                            if constexpr (MODE == 2) {
 #pragma unroll
-                                for (int m = 0; m < TOPM; ++m) {
-                                    const float lo = fminf(top[qb][m], v);
-                                    v = fmaxf(top[qb][m], v);
-                                    top[qb][m] = lo;
-                                }
-                            } else {
-                                int id = (int)(rbase + i);
-#pragma unroll
-                                for (int m = 0; m < TOPM; ++m) {
-                                    const bool lt = v < top[qb][m];
-                                    const float tv = lt ? top[qb][m] : v;
-                                    const int ti = lt ? topi[qb][m] : id;
-                                    top[qb][m] = lt ? v : top[qb][m];
-                                    topi[qb][m] = lt ? id : topi[qb][m];
-                                    v = tv;
-                                    id = ti;
-                                }
+                            for (int m = 0; m < TOPM; ++m) {
+                                const float lo = fminf(top[qb][m], v);
+                                v = fmaxf(top[qb][m], v);
+                                top[qb][m] = lo;
                             }
                         }
                     }
@@ -384,8 +361,8 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
     }
 
     if constexpr (TOPMODE) {
-        // lane (r16, g) writes its TOPM values (and ids) of query qw + 16 qb
-        // + r16 to slots [g * TOPM, (g + 1) * TOPM) of that query's list
+        // lane (r16, g) writes its TOPM values of query qw + 16 qb + r16 to
+        // slots [g * TOPM, (g + 1) * TOPM) of that query's list (ids 0)
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb) {
             const int q = qw + qb * 16 + r16;
@@ -394,7 +371,7 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
 #pragma unroll
             for (int m = 0; m < TOPM; ++m) {
                 cvq[m] = top[qb][m];
-                ciq[m] = MODE == 3 ? topi[qb][m] : 0;
+                ciq[m] = 0;
             }
         }
         int32_t *lc = a.list_cnt + (qblk * a.nsplit + split) * (int64_t)S::BN + qw;
@@ -453,12 +430,11 @@ static void (*share_kmin_kernel())(ScanKArgs) {
 #define VS_SHARE_SHAPES(X) \
     X(1, 4, 4, 4) X(1, 8, 2, 4) X(2, 4, 4, 2) X(2, 8, 2, 2) X(1, 8, 2, 2) X(1, 4, 4, 8)
 
-// mode: 0 lists, 2 top-m values, 3 top-m values and ids
+// mode: 0 lists, 2 top-m values, 4 k-means lists
 static void (*share_kernel(int st, int nks, int bn, int rt, int64_t ld, int mode))(ScanKArgs) {
 #define VS_SHARE_PICK(ST_, NKS_, NQB_, RT_)                                                     \
     if (st == ST_ && nks == NKS_ && bn == 64 * NQB_ && rt == RT_ && ld == 32 * NKS_)              \
         return mode == 4   ? share_kmin_kernel<ST_, NKS_, NQB_, RT_>()                             \
-               : mode == 3 ? share_scan_kernel<ST_, NKS_, NQB_, RT_, 3>                           \
                : mode == 2 ? share_scan_kernel<ST_, NKS_, NQB_, RT_, 2>                           \
                            : share_scan_kernel<ST_, NKS_, NQB_, RT_, 0>;
     VS_SHARE_SHAPES(VS_SHARE_PICK)
@@ -466,7 +442,7 @@ static void (*share_kernel(int st, int nks, int bn, int rt, int64_t ld, int mode
     return nullptr;
 }
 
-int share_topm(bool ids) { return ids ? kShareTopM : kShareTopMEst; }
+int share_topm_est() { return kShareTopMEst; }
 
 // Workgroups of the shape that one CU holds at once (registers and LDS).
 int share_blocks_per_cu(int st, int nks, int bn, int rt, int64_t ld, size_t lds, int mode) {
@@ -484,13 +460,12 @@ int share_blocks_per_cu(int st, int nks, int bn, int rt, int64_t ld, size_t lds,
 hipError_t launch_share_scan(const ScanPlan &plan, const ScanKArgs &args, hipStream_t st) {
     if (plan.kk != plan.kk_final || plan.cap < plan.kk + 16 || plan.lw != 1 || !args.list_cnt)
         return hipErrorInvalidValue;
-    if (plan.share_topm && (plan.share_topm != share_topm(plan.share_ids != 0) ||
-                            plan.cap < 4 * plan.share_topm))
+    if (plan.share_topm && (plan.share_topm != kShareTopMEst || plan.cap < 4 * plan.share_topm))
         return hipErrorInvalidValue;
     const int64_t total = plan.nqblk * plan.nsplit;
     const int64_t grid = ((total + 7) / 8) * 8;
     if (plan.share_kmin && (plan.share_topm || !(plan.kmin_margin > 0.f))) return hipErrorInvalidValue;
-    const int mode = plan.share_kmin ? 4 : !plan.share_topm ? 0 : plan.share_ids ? 3 : 2;
+    const int mode = plan.share_kmin ? 4 : plan.share_topm ? 2 : 0;
     void (*fn)(ScanKArgs) =
         share_kernel(plan.tile_st, plan.nks, plan.bn, plan.tm, args.ld, mode);
     if (!fn) return hipErrorInvalidValue;

@@ -40,7 +40,7 @@ EXPORTED = [
     "vs_dev_alloc", "vs_dev_free", "vs_dev_upload", "vs_dev_download", "vs_dev_copy", "vs_dev_probe",
     "vs_device_count",
     "vs_device_name", "vs_gen_normal", "vs_prof_enable", "vs_prof_get", "vs_prof_reset",
-    "vs_index_sync",
+    "vs_index_sync", "vs_index_set_option",
 ]
 
 
@@ -138,6 +138,7 @@ def load() -> ctypes.CDLL:
                          ctypes.POINTER(ctypes.c_double)], i32),
         "vs_prof_reset": ([p], i32),
         "vs_index_sync": ([p], i32),
+        "vs_index_set_option": ([p, ctypes.c_char_p, i64], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)

@@ -28,6 +28,12 @@ def _dtype_code(a: np.ndarray) -> tuple[np.ndarray, int]:
     return np.ascontiguousarray(a, dtype=np.float32), N.VS_DTYPE_F32
 
 
+# Planner options applied to every index this module creates or adopts
+# (vs_index_set_option; the library's defaults when empty).  Test support:
+# tests reach every kernel variant on small inputs by forcing a path here.
+DEFAULT_OPTIONS: dict[str, int] = {}
+
+
 class GpuIndexFlat(Index):
     """Exact flat index whose vectors stay resident on one GPU.
 
@@ -47,6 +53,15 @@ class GpuIndexFlat(Index):
         N.check(self._lib.vs_index_create(device, int(d), int(self.metric), self._STORAGE[storage],
                                           ctypes.byref(h)))
         self._h = h
+        self._apply_default_options()
+
+    def _apply_default_options(self) -> None:
+        for name, value in DEFAULT_OPTIONS.items():
+            self.set_option(name, value)
+
+    def set_option(self, name: str, value: int) -> None:
+        """Force a planner option of this index (vs_index_set_option)."""
+        N.check(self._lib.vs_index_set_option(self._h, name.encode(), int(value)))
 
     # --- constructors (gpu_index_flat.dart:46-57) ---
     @classmethod
@@ -66,6 +81,7 @@ class GpuIndexFlat(Index):
         g._lib = lib
         g.device = device
         g._h = handle
+        g._apply_default_options()
         return g
 
     @classmethod

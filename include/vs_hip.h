@@ -226,18 +226,38 @@ VS_API int vs_gen_normal(int device, void *dst_dev, int out_dtype, int64_t n, in
 /* Per-kernel timing on the index's stream with HIP events: when enabled,
  * every launch of the named kernel family is bracketed by events and its
  * duration accumulated.  Families: "scan", "merge", "range", "assign",
- * "update", "join".  The families "tiled" and "streamed" count, whether or
- * not timing is enabled, the distance scans that ran on the LDS-tiled kernel
- * (large batches) and on the streaming kernel (small batches); the family
- * "tile:S,P,Q,R,K,W" counts the tiled scans of one built shape (storage,
- * query planes, 32-query blocks, 32-row blocks per wave, K-chunk, waves per
- * workgroup). */
+ * "update", "join".  Whether or not timing is enabled, the families
+ * "streamed" (streaming scan, small batches; "streamed8" its eight-wave
+ * form), "shared" (row-shared scan) and "gemm" (GEMM-tiled scan) count the
+ * distance scans that ran on each kernel, and "gemm:S,P,WR,WQ,RB,QB,KC"
+ * those of one GEMM shape (storage, query planes, row waves, query waves,
+ * 32-row blocks per wave, 32-query blocks per wave, K-chunk). */
 VS_API int vs_prof_enable(vs_index *idx, int on);
 VS_API int vs_prof_get(vs_index *idx, const char *family, int64_t *launches, double *total_ms);
 VS_API int vs_prof_reset(vs_index *idx);
 
 /* Synchronise the index's stream. */
 VS_API int vs_index_sync(vs_index *idx);
+
+/* Test support, no counterpart in the reference: sets one planner option of
+ * this handle, so that tests reach every kernel variant on small inputs.
+ * The defaults are the tuned plan; every option keeps results exact.
+ *   "gemm"        -1 planner rule (rows >= 256 elements, batch >= 512), 0 off, 1 any d
+ *   "gemm_min_nq" smallest batch on the GEMM-tiled scan (0: the rule's)
+ *   "gemm_wq", "gemm_qb", "gemm_kc"  force that GEMM shape field (0: any)
+ *   "gemm_dma"    1 allows the LDS-DMA GEMM shapes where the build enables them
+ *   "share"       -1 rule (bf16 rows of 128 elements, batch >= 256), 0 off, 1 also 256
+ *   "coarse"      1: one-pass bf16 selection of fp32 rows (range, self-join, k-means)
+ *   "copy16"      1: that selection reads a bf16 copy of the rows
+ *   "guess"       1: large batches start from thresholds estimated on a row sample
+ *   "prepass"     1: small batches seed their thresholds from a pre-pass
+ *   "scan_kkw"    >0: per-list keep forced down (exercises the list verification)
+ *   "scan_nw8"    1: eight-wave streaming scan where it fits
+ *   "km16"        1: the k-means assign reads a bf16 copy of the centroids
+ *   "km16_rt"     2 or 4: 16-row blocks per tile of that scan
+ *   "pick_order"  1: the k-means pick walks the points grouped by the last step's clusters
+ * Unknown names and out-of-range values: VS_ERR_INVALID. */
+VS_API int vs_index_set_option(vs_index *idx, const char *name, int64_t value);
 
 #ifdef __cplusplus
 }

@@ -22,3 +22,16 @@ def vs():
     if vector_store.device_count() < 1:
         pytest.fail("no HIP device visible to libvs_hip.so")
     return vector_store
+
+
+@pytest.fixture
+def opts(monkeypatch):
+    """opts(name=value, ...) forces planner options (vs_index_set_option) on
+    every index the test creates from then on; restored afterwards."""
+    from vector_store import gpu_index_flat
+
+    def set_(**kw):
+        for name, value in kw.items():
+            monkeypatch.setitem(gpu_index_flat.DEFAULT_OPTIONS, name, int(value))
+
+    return set_

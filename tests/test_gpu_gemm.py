@@ -39,12 +39,10 @@ def _key(shape):
 
 
 @pytest.fixture(autouse=True)
-def _gemm(monkeypatch):
+def _gemm(opts):
     """The GEMM-tiled scan is switched on for every test here (the row-shared
     scan, planned before it, off)."""
-    monkeypatch.setenv("VS_GEMM", "1")
-    monkeypatch.setenv("VS_SHARE", "0")
-    monkeypatch.setenv("VS_GEMM_MIN_NQ", "256")
+    opts(gemm=1, share=0, gemm_min_nq=256)
 
 
 # The LDS-DMA shapes (query planes, row waves, query waves, 32-row blocks per
@@ -56,12 +54,10 @@ DMA_SHAPES = [
 ]
 
 
-def _force(monkeypatch, shape):
+def _force(opts, shape):
     """Force a register-staged shape (the LDS-DMA shapes switched off)."""
     _, _, _, wq, _, qb, kc = shape
-    monkeypatch.setenv("VS_GEMM_DMA", "0")
-    for name, v in (("WQ", wq), ("QB", qb), ("KC", kc)):
-        monkeypatch.setenv("VS_GEMM_" + name, str(v))
+    opts(gemm_dma=0, gemm_wq=wq, gemm_qb=qb, gemm_kc=kc)
 
 
 def _search(vs, xb, xq, k, metric, storage, shape=None, key=None):
@@ -94,8 +90,8 @@ def _inputs(shape, d, seed, n=9000, nq=300):
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "-".join(map(str, s)))
 @pytest.mark.parametrize("metric", [0, 1])
 @pytest.mark.parametrize("k,d", [(10, 200), (100, 768), (1, 72)])
-def test_gemm_shape_parity(vs, monkeypatch, shape, metric, k, d):
-    _force(monkeypatch, shape)
+def test_gemm_shape_parity(vs, opts, shape, metric, k, d):
+    _force(opts, shape)
     xb, xq, storage = _inputs(shape, d, 31 + metric)
     D, I, gemm = _search(vs, xb, xq, k, metric, storage, shape)
     assert gemm >= 1
@@ -113,11 +109,10 @@ DMA_OFF = ("the LDS-DMA kernel is switched off (kGemmDmaEnabled = false in vs_ap
 @pytest.mark.parametrize("shape", DMA_SHAPES, ids=lambda s: "-".join(map(str, s)))
 @pytest.mark.parametrize("metric", [0, 1])
 @pytest.mark.parametrize("k,d", [(10, 200), (100, 768), (1, 72)])
-def test_gemm_dma_shape_parity(vs, monkeypatch, shape, metric, k, d):
+def test_gemm_dma_shape_parity(vs, opts, shape, metric, k, d):
     """The LDS-DMA kernel in each built shape: bf16 rows and bf16 queries."""
     _, _, wq, _, qb, _ = shape
-    monkeypatch.setenv("VS_GEMM_WQ", str(wq))
-    monkeypatch.setenv("VS_GEMM_QB", str(qb))
+    opts(gemm_wq=wq, gemm_qb=qb)
     xb, xq, storage = _inputs((1, 1), d, 51 + metric)
     D, I, gemm = _search(vs, xb, xq, k, metric, storage,
                          key="gemmdma:" + ",".join(map(str, shape)))
@@ -128,13 +123,11 @@ def test_gemm_dma_shape_parity(vs, monkeypatch, shape, metric, k, d):
 
 @pytest.mark.parametrize("dma", [pytest.param(1, marks=pytest.mark.skip(reason=DMA_OFF)), 0])
 @pytest.mark.parametrize("wq,qb", [(4, 2), (2, 2)])
-def test_gemm_config2_exact(vs, monkeypatch, wq, qb, dma):
+def test_gemm_config2_exact(vs, opts, wq, qb, dma):
     """configs[1] arithmetic on a 100k slice with 1,000 queries: integer
     distances, bit-exact, k = 100, on the LDS-DMA and register-staged
     kernels."""
-    monkeypatch.setenv("VS_GEMM_WQ", str(wq))
-    monkeypatch.setenv("VS_GEMM_QB", str(qb))
-    monkeypatch.setenv("VS_GEMM_DMA", str(dma))
+    opts(gemm_wq=wq, gemm_qb=qb, gemm_dma=dma)
     xb = syn.int_grid(100_000, 128, 1234, 0)
     xq = syn.int_grid(1000, 128, 1234, 1)
     key = f"gemmdma:1,2,{wq},4,{qb},4" if dma else _key((1, 1, 2, wq, 4, qb, 32))
@@ -145,13 +138,13 @@ def test_gemm_config2_exact(vs, monkeypatch, wq, qb, dma):
     assert np.all(D == np.round(D))
 
 
-def test_gemm_matches_streaming(vs, monkeypatch):
+def test_gemm_matches_streaming(vs, opts):
     """Same inputs through the GEMM-tiled and streaming scans give the same
     answers (integer data: exact distances)."""
     xb = syn.int_grid(30_000, 64, 3, 0)
     xq = syn.int_grid(700, 64, 3, 1)
     D1, I1, g1 = _search(vs, xb, xq, 16, 0, "auto")
-    monkeypatch.setenv("VS_GEMM", "0")
+    opts(gemm=0)
     D0, I0, g0 = _search(vs, xb, xq, 16, 0, "auto")
     assert g1 >= 1 and g0 == 0
     assert np.array_equal(D0, D1)
@@ -159,11 +152,11 @@ def test_gemm_matches_streaming(vs, monkeypatch):
     assert_knn_parity(D1, I1, Dr, Ir, 0, rtol=0.0, atol=0.0, xb=xb, xq=xq)
 
 
-def test_gemm_verification_path(vs, monkeypatch):
-    """Lists forced down to 4 entries (VS_SCAN_KKW) with k = 60: the merge
+def test_gemm_verification_path(vs, opts):
+    """Lists forced down to 4 entries (option scan_kkw) with k = 60: the merge
     must detect queries whose lists may have dropped a winner and search
     them again; the answer stays exact."""
-    monkeypatch.setenv("VS_SCAN_KKW", "4")
+    opts(scan_kkw=4)
     xb = syn.int_grid(20_000, 64, 5, 0)
     xq = syn.int_grid(300, 64, 5, 1)
     D, I, gemm = _search(vs, xb, xq, 60, 0, "auto")
@@ -267,12 +260,11 @@ def _one_pass_runs(g):
 
 
 @pytest.mark.parametrize("coarse", [1, 0])
-def test_coarse_self_join(vs, monkeypatch, coarse):
+def test_coarse_self_join(vs, opts, coarse):
     """configs[4] shape at 4,000 rows (d = 512, 5% planted copies, cos >=
     0.95): the one-pass selection (bf16 hi planes, widened margins, exact
     fp64 re-test) and the three-pass one give the oracle's pair list."""
-    monkeypatch.setenv("VS_GEMM", "-1")  # the default planner rule
-    monkeypatch.setenv("VS_COARSE", str(coarse))
+    opts(gemm=-1, coarse=coarse)  # the default planner rule
     x = syn.dedup_set(4000, 512, 0.05, 0.01, 11)
     g = vs.GpuIndexFlat(512, vs.Metric(1), storage="f32")
     g.add(x)
@@ -288,12 +280,11 @@ def test_coarse_self_join(vs, monkeypatch, coarse):
 
 
 @pytest.mark.parametrize("coarse", [1, 0])
-def test_coarse_kmeans(vs, monkeypatch, coarse):
+def test_coarse_kmeans(vs, opts, coarse):
     """configs[3] arithmetic at 30,000 points (d = 256, 1,024 mixture
     components, 4,096 centroids): assignments, objective and centroids equal
     the oracle's with and without the one-pass selection."""
-    monkeypatch.setenv("VS_GEMM", "-1")
-    monkeypatch.setenv("VS_COARSE", str(coarse))
+    opts(gemm=-1, coarse=coarse)
     x, _ = syn.gaussian_mixture(30_000, 256, 1024, 0.1, 77)
     cen = x[syn.seeded_subset(len(x), 4096, 77)].copy()
     pts = vs.GpuIndexFlat.l2(256, storage="f32")
@@ -312,10 +303,10 @@ def test_coarse_kmeans(vs, monkeypatch, coarse):
 
 
 @pytest.mark.parametrize("metric", [0, 1])
-def test_coarse_range_search(vs, monkeypatch, metric):
+def test_coarse_range_search(vs, opts, metric):
     """Range search of 700 fp32 queries (d = 256) on the one-pass selection:
     the CSR result equals the oracle's bit for bit."""
-    monkeypatch.setenv("VS_GEMM", "-1")
+    opts(gemm=-1)
     xb = syn.normal_unit(6000, 256, 19, 0)
     xq = np.concatenate([xb[:350] + 0.01, syn.normal_unit(350, 256, 19, 1)]).astype(np.float32)
     radius = 0.05 if metric == 0 else 0.5
@@ -331,13 +322,12 @@ def test_coarse_range_search(vs, monkeypatch, metric):
 
 
 @pytest.mark.parametrize("coarse", [1, 0])
-def test_kmeans_exhaustive_fallback(vs, monkeypatch, coarse):
+def test_kmeans_exhaustive_fallback(vs, opts, coarse):
     """Twenty identical copies of one centroid fill the 16-entry shortlist
     of the points near it, so their pick cannot be proven and the exhaustive
     exact scan runs: the answer is the lowest index among the copies (the
     strict '<' scan, kmeans.dart:93-101), as the oracle gives."""
-    monkeypatch.setenv("VS_GEMM", "-1")
-    monkeypatch.setenv("VS_COARSE", str(coarse))
+    opts(gemm=-1, coarse=coarse)
     x, _ = syn.gaussian_mixture(6000, 256, 16, 0.1, 5)
     cen = x[syn.seeded_subset(len(x), 300, 5)].copy()
     cen[100:120] = cen[3]  # 20 copies of centroid 3

@@ -70,13 +70,13 @@ def test_range_empty_and_bf16(vs):
     assert rr.total_matches == 0 and rr.nq == 30
 
 
-@pytest.mark.parametrize("copy16", ["1", "0"])
-def test_self_join_dedup(vs, monkeypatch, copy16):
+@pytest.mark.parametrize("copy16", [1, 0])
+def test_self_join_dedup(vs, opts, copy16):
     """configs[4] arithmetic on 30k x 512: 5 % planted near-duplicates,
     pairs i<j with cos >= 0.95, sorted by (i, j).  The one-pass selection
     reads a bf16 copy of the fp32 rows (copy16 1, the default) or rounds
     the fp32 rows in the kernel (0)."""
-    monkeypatch.setenv("VS_COPY16", copy16)
+    opts(copy16=copy16)
     x = syn.dedup_set(30_000, 512, 0.05, 0.01, 1234)
     g = vs.GpuIndexFlat.ip(512, storage="f32")
     g.add(x)
@@ -87,12 +87,12 @@ def test_self_join_dedup(vs, monkeypatch, copy16):
     assert np.array_equal(s.view(np.uint32), rs.view(np.uint32))
 
 
-@pytest.mark.parametrize("copy16", ["1", "0"])
-def test_range_l2_one_pass_rows(vs, monkeypatch, copy16):
+@pytest.mark.parametrize("copy16", [1, 0])
+def test_range_l2_one_pass_rows(vs, opts, copy16):
     """L2 range search of 600 queries over 20k x 256 fp32 rows on the
     GEMM-tiled one-pass selection (row norms from the fp32 rows), radius at
     the 40th score of query 0: the oracle's CSR result."""
-    monkeypatch.setenv("VS_COPY16", copy16)
+    opts(copy16=copy16)
     xb = blobs(20_000, 256, seed=11)
     xq = np.concatenate([xb[:300] + 0.02, blobs(300, 256, seed=12)]).astype(np.float32)
     Dk, _ = oracle.flat_search(xb, xq[:1], 40, 0, 1)
@@ -101,7 +101,7 @@ def test_range_l2_one_pass_rows(vs, monkeypatch, copy16):
     g.add(xb)
     rr = g.range_search(xq, radius)
     # the GEMM-tiled scan ran on the copy (storage 1) or the fp32 rows (2)
-    n, _ = g.prof_get("gemm:%s,1,2,4,4,2,32" % ("1" if copy16 == "1" else "2"))
+    n, _ = g.prof_get("gemm:%s,1,2,4,4,2,32" % ("1" if copy16 == 1 else "2"))
     assert n >= 1
     lims, D, I = oracle.flat_range_search(xb, xq, radius, 0, NT)
     assert rr.total_matches > 0

@@ -98,11 +98,11 @@ def test_bf16_storage_ip(vs, nq):
     assert_knn_parity(r.distances, r.ids, Dr, Ir, 1, rtol=1e-3)
 
 
-def test_eight_wave_streaming_scan(vs, monkeypatch):
-    """Regression test of the 8-wave streaming scan (VS_SCAN_NW8=1), whose
+def test_eight_wave_streaming_scan(vs, opts):
+    """Regression test of the 8-wave streaming scan (option scan_nw8), whose
     LDS id area once started at the 4-wave offset: the batch-64 shape of
     test_bf16_storage_ip, where it runs, against the oracle."""
-    monkeypatch.setenv("VS_SCAN_NW8", "1")
+    opts(scan_nw8=1)
     xb16 = syn.to_bf16_bits(syn.normal_unit(60_000, 768, 99, 0))
     xq16 = syn.to_bf16_bits(syn.normal_unit(64, 768, 99, 1))
     idx = vs.GpuIndexFlat(768, vs.Metric.innerProduct, storage="bf16")
@@ -113,6 +113,7 @@ def test_eight_wave_streaming_scan(vs, monkeypatch):
     idx.close()
     assert n8 >= 1, "the 8-wave scan did not run"
     Dr, Ir = oracle.flat_search(syn.bf16_bits_to_f32(xb16), syn.bf16_bits_to_f32(xq16), 10, 1, NT)
+    assert_knn_parity(r.distances, r.ids, Dr, Ir, 1, rtol=1e-3)
     assert_knn_parity(r.distances, r.ids, Dr, Ir, 1, rtol=1e-3)
 
 
@@ -265,7 +266,7 @@ def test_faisdart_fixtures(vs):
 
 
 @pytest.mark.parametrize("k", [10, 50, 100])
-def test_short_lists_are_verified(vs, monkeypatch, k):
+def test_short_lists_are_verified(vs, opts, k):
     """Per-wave lists may keep fewer than the merged candidates; the merge
     proves no list dropped a winner or re-runs the query with full lists.
     Rows sorted by distance to query 0 put all its winners in one list, and a
@@ -275,7 +276,7 @@ def test_short_lists_are_verified(vs, monkeypatch, k):
     xq = g.standard_normal((3, 32)).astype(np.float32)
     xb = g.standard_normal((8000, 32)).astype(np.float32)
     xb = xb[np.argsort(((xb.astype(np.float64) - xq[0]) ** 2).sum(1), kind="stable")]
-    monkeypatch.setenv("VS_SCAN_KKW", "4")
+    opts(scan_kkw=4)
     idx = vs.GpuIndexFlat.l2(32, storage="f32")
     idx.add(xb)
     r = idx.search(xq, k)
@@ -287,19 +288,19 @@ def test_short_lists_are_verified(vs, monkeypatch, k):
 
 
 @pytest.mark.parametrize("nq,k,metric", [(1, 10, 1), (37, 10, 0), (64, 100, 0), (16, 100, 1)])
-def test_small_batch_prepass(vs, monkeypatch, nq, k, metric):
+def test_small_batch_prepass(vs, nq, k, metric):
     """Small batches over 300,000 rows plan many short lists, so a pre-pass
     over a sample of the rows seeds every query's shared threshold before
     the full scan.  Integer data (exact distances): the result equals the
     oracle's, and the distances equal those of a search without the
-    pre-pass (VS_PREPASS=0)."""
+    pre-pass (option prepass = 0)."""
     xb = syn.int_grid(300_000, 64, 8, 0)
     xq = syn.int_grid(nq, 64, 8, 1)
     idx = vs.GpuIndexFlat(64, vs.Metric(metric), storage="auto")
     idx.add(xb)
     r1 = idx.search(xq, k)
     npre, _ = idx.prof_get("prepass_scans")
-    monkeypatch.setenv("VS_PREPASS", "0")
+    idx.set_option("prepass", 0)
     r0 = idx.search(xq, k)
     npre0, _ = idx.prof_get("prepass_scans")
     idx.close()
@@ -310,12 +311,12 @@ def test_small_batch_prepass(vs, monkeypatch, nq, k, metric):
 
 
 @pytest.mark.parametrize("nq,k,metric", [(512, 100, 0), (300, 10, 1), (1024, 1, 0)])
-def test_large_batch_estimated_threshold(vs, monkeypatch, nq, k, metric):
+def test_large_batch_estimated_threshold(vs, nq, k, metric):
     """Large batches over 2^18+ rows start every query's threshold from an
     estimate taken on a sample of the rows (a rank of the sample chosen so
     that kk_final rows of the full scan very likely lie below it).  Integer
     data: the result equals the oracle's and a search without the estimate
-    (VS_GUESS=0), and no query needed the exact re-search."""
+    (option guess = 0), and no query needed the exact re-search."""
     xb = syn.int_grid(300_000, 32, 11, 0)
     xq = syn.int_grid(nq, 32, 11, 1)
     idx = vs.GpuIndexFlat(32, vs.Metric(metric), storage="auto")
@@ -324,7 +325,7 @@ def test_large_batch_estimated_threshold(vs, monkeypatch, nq, k, metric):
     r1 = idx.search(xq, k)
     ng, _ = idx.prof_get("guess_scans")
     nfb, _ = idx.prof_get("fallback")
-    monkeypatch.setenv("VS_GUESS", "0")
+    idx.set_option("guess", 0)
     r0 = idx.search(xq, k)
     ng0, _ = idx.prof_get("guess_scans")
     idx.close()
@@ -360,3 +361,20 @@ def test_estimated_threshold_too_tight_falls_back(vs):
     Dr, Ir = oracle.flat_search(xb, xq[sub], k, 0, NT)
     assert_knn_parity(r.distances[sub], r.ids[sub], Dr, Ir, 0, rtol=0.0, atol=0.0,
                       xb=xb, xq=xq[sub])
+
+
+def test_set_option_rejects_unknown_and_out_of_range(vs):
+    """vs_index_set_option takes the documented names only, each within its
+    range; a rejected call leaves the index's plan unchanged."""
+    idx = vs.GpuIndexFlat.l2(8)
+    idx.add(syn.int_grid(100, 8, 1, 0))
+    # VS_ERR_INVALID surfaces as ValueError (the reference's ArgumentError)
+    with pytest.raises(ValueError, match="unknown option"):
+        idx.set_option("no_such_option", 1)
+    for name, value in (("gemm", 2), ("km16_rt", 3), ("scan_kkw", -1)):
+        with pytest.raises(ValueError, match="outside"):
+            idx.set_option(name, value)
+    idx.set_option("guess", 0)
+    r = idx.search(syn.int_grid(3, 8, 1, 1), 5)
+    idx.close()
+    assert r.ids.shape == (3, 5)

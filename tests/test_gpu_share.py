@@ -19,9 +19,9 @@ NT = oracle.default_threads()
 
 
 @pytest.fixture(autouse=True)
-def _share(monkeypatch):
+def _share(opts):
     """The row-shared scan is on for both row lengths in every test here."""
-    monkeypatch.setenv("VS_SHARE", "1")
+    opts(share=1)
 
 
 def _search(vs, xb, xq, k, metric, storage="auto", expect_shared=True):
@@ -66,14 +66,14 @@ def test_bf16_unit_vectors(vs, metric):
     assert_knn_parity(D, I, Dr, Ir, metric, rtol=1e-5)
 
 
-def test_matches_streaming_scan_large(vs, monkeypatch):
+def test_matches_streaming_scan_large(vs, opts):
     """configs[1] shape on a 300k-row slice (estimated thresholds active):
     the row-shared scan returns the same distances as the streaming scan,
     and the oracle's on a query sample."""
     xb = syn.int_grid(300_000, 128, 4, 0)
     xq = syn.int_grid(1024, 128, 4, 1)
     D1, I1 = _search(vs, xb, xq, 100, 0)
-    monkeypatch.setenv("VS_SHARE", "0")
+    opts(share=0)
     D0, I0 = _search(vs, xb, xq, 100, 0, expect_shared=False)
     assert np.array_equal(D1, D0)
     sub = np.arange(0, 1024, 31)
@@ -111,31 +111,25 @@ def _kmeans_check(vs, x, cen, min_points=1, seed=0, expect_fallback=False):
     return a
 
 
-@pytest.mark.parametrize("kmin", ["1", "0"])
 @pytest.mark.parametrize("n,d,ncomp,K", [(30_000, 256, 1024, 4096), (9_000, 100, 64, 500),
                                          (3_000, 256, 8, 20)])
-def test_kmeans_register_shortlists(vs, monkeypatch, n, d, ncomp, K, kmin):
+def test_kmeans_register_shortlists(vs, n, d, ncomp, K):
     """k-means assign on the row-shared scan (fp32 points and centroids,
-    one-pass bf16 selection).  kmin 1 (default): each scan lane appends the
-    values below its running minimum + 2.5 bound to the point's list; the
-    pick re-scores those within 2 bound of the smallest in fp64 and the rest
-    are provably worse.  kmin 0: each lane keeps its 8 smallest (accumulator,
-    centroid) pairs in registers and the pick proves the argmin with the
-    smallest value any lane dropped.  Assignments, objective and centroids
-    equal the oracle's (K = 20: lanes see fewer than 8 centroids each)."""
-    monkeypatch.setenv("VS_KMIN", kmin)
+    one-pass bf16 selection): each scan lane appends the values below its
+    running minimum + 2.5 bound to the point's list; the pick re-scores those
+    within 2 bound of the smallest in fp64 and the rest are provably worse.
+    Assignments, objective and centroids equal the oracle's (K = 20: lanes
+    see few centroids each)."""
     x, _ = syn.gaussian_mixture(n, d, ncomp, 0.1, 41)
     cen = x[syn.seeded_subset(n, K, 41)].copy()
     _kmeans_check(vs, x, cen)
 
 
-@pytest.mark.parametrize("kmin", ["1", "0"])
-def test_kmeans_register_shortlists_fallback(vs, monkeypatch, kmin):
+def test_kmeans_register_shortlists_fallback(vs):
     """Forty copies of one centroid: more candidates within 2 bound of the
-    smallest than the pick's 32 slots (kmin 1), or every lane's 8 slots
-    full (kmin 0), so the exhaustive exact scan decides those points: the
-    lowest index among the copies loses to the original (kmeans.dart:93-101)."""
-    monkeypatch.setenv("VS_KMIN", kmin)
+    smallest than the pick's 32 slots, so the exhaustive exact scan decides
+    those points: the lowest index among the copies loses to the original
+    (kmeans.dart:93-101)."""
     x, _ = syn.gaussian_mixture(6000, 256, 16, 0.1, 5)
     cen = x[syn.seeded_subset(len(x), 300, 5)].copy()
     cen[100:140] = cen[3]
@@ -143,11 +137,10 @@ def test_kmeans_register_shortlists_fallback(vs, monkeypatch, kmin):
     assert not np.any((a >= 100) & (a < 140))
 
 
-def test_kmeans_lists_full(vs, monkeypatch):
+def test_kmeans_lists_full(vs):
     """Three hundred copies of one centroid overflow the points' k-means
     lists (more than cap - 16 appends): the lists are marked full and their
     points go to the exhaustive exact scan, whose argmin is the oracle's."""
-    monkeypatch.setenv("VS_KMIN", "1")
     x, _ = syn.gaussian_mixture(4000, 256, 8, 0.1, 6)
     cen = x[syn.seeded_subset(len(x), 700, 6)].copy()
     cen[200:500] = cen[7]
@@ -155,20 +148,18 @@ def test_kmeans_lists_full(vs, monkeypatch):
     assert not np.any((a >= 200) & (a < 500))
 
 
-@pytest.mark.parametrize("km16,rt", [("0", "4"), ("1", "2")])
-def test_kmeans_lists_fp32_rows(vs, monkeypatch, km16, rt):
+@pytest.mark.parametrize("km16,rt", [(0, 4), (1, 2)])
+def test_kmeans_lists_fp32_rows(vs, opts, km16, rt):
     """The k-means lists over the fp32 centroid rows rounded in the scan
-    (VS_KM16=0), or over their bf16 copy in 32-row tiles (VS_KM16_RT=2)
+    (option km16 = 0), or over their bf16 copy in 32-row tiles (km16_rt = 2)
     instead of 64-row ones: the oracle's assignments."""
-    monkeypatch.setenv("VS_KMIN", "1")
-    monkeypatch.setenv("VS_KM16", km16)
-    monkeypatch.setenv("VS_KM16_RT", rt)
+    opts(km16=km16, km16_rt=rt)
     x, _ = syn.gaussian_mixture(30_000, 256, 1024, 0.1, 44)
     cen = x[syn.seeded_subset(30_000, 4096, 44)].copy()
     _kmeans_check(vs, x, cen)
 
 
-def test_kmeans_second_step_grouped_order(vs, monkeypatch):
+def test_kmeans_second_step_grouped_order(vs):
     """The pick of a second step walks the points grouped by the first
     step's clusters (a permutation): the same assignments, objective and
     centroids as the oracle's, and as walking them in index order."""
@@ -179,7 +170,7 @@ def test_kmeans_second_step_grouped_order(vs, monkeypatch):
     pts.add(x)
     _, cen1, _, _ = vs.kmeans_step(pts, cen, 1, u)
     a2, c2, n2, o2 = vs.kmeans_step(pts, cen1, 1, u)
-    monkeypatch.setenv("VS_PICK_ORDER", "0")
+    pts.set_option("pick_order", 0)
     a3, c3, n3, o3 = vs.kmeans_step(pts, cen1, 1, u)
     pts.close()
     assert np.array_equal(a2, a3) and o2 == o3
