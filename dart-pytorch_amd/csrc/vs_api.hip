@@ -540,7 +540,15 @@ bool plan_gemm(const vs_index *x, int64_t nq, int64_t nrows, int planes, int sto
     p->nks = 0;
     p->lds_bytes = lds;
     p->nqblk = (nq + p->bn - 1) / p->bn;
-    p->tile_group = std::max<int64_t>(1, std::min<int64_t>(p->nqblk, 32));
+    // query blocks per XCD group: the most (up to 32, a power of two) whose
+    // query planes take <= 1.5 MiB, so that they stay in the XCD's 4 MiB L2
+    // beside the rows; a chunk of the grid (group x split run, about one
+    // XCD's resident workgroups) covers 32 / group splits
+    const int64_t qbytes = (int64_t)p->bn * x->ld * 2 * planes;
+    int64_t qg = 1;
+    while (qg < 32 && 2 * qg * qbytes <= (int64_t)3 << 19) qg *= 2;
+    p->tile_group = std::max<int64_t>(1, std::min<int64_t>(p->nqblk, qg));
+    int64_t spc = std::max<int64_t>(1, 32 / p->tile_group);
     const int64_t tile_rows = (int64_t)pick->wr * 32 * pick->rb;
     const int64_t ncu = (int64_t)std::max(1, x->num_cu);
     const int64_t max_split = std::max<int64_t>(1, nrows / (tile_rows * 4));
@@ -563,10 +571,14 @@ bool plan_gemm(const vs_index *x, int64_t nq, int64_t nrows, int planes, int sto
         }
         if (blocks >= 4 * rounds * ncu) break;
     }
+    // at least one split run per group (its workgroups then walk different
+    // splits together instead of idling the XCD)
+    best = std::max(best, std::min(spc, max_split));
     int64_t rps = round_up((nrows + best - 1) / best, tile_rows);
     if (rps <= 0) rps = tile_rows;
     p->rows_per_split = rps;
     p->nsplit = std::max<int64_t>(1, (nrows + rps - 1) / rps);
+    p->tile_spc = std::min(spc, p->nsplit);
     return true;
 }
 

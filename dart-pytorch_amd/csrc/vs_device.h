@@ -58,7 +58,8 @@ struct ScanKArgs {
     const uint16_t *qp;
     int64_t nq;
     int64_t nqblk, nsplit, rows_per_split;
-    int64_t qgroup;      // tiled scan: query blocks per XCD group
+    int64_t qgroup;      // GEMM-tiled scan: query blocks per XCD group
+    int64_t qspc;        // GEMM-tiled scan: splits per XCD chunk
     int flush_at;        // GEMM-tiled scan: a list holding more entries is cut to kk
                          // before the next append (so its threshold keeps tightening)
     int kk, cap, metric;
@@ -161,26 +162,33 @@ __device__ __forceinline__ bool map_block(int64_t nqblk, int64_t nsplit, int64_t
     return true;
 }
 
-// Grid of the tiled scan: the query blocks are cut into groups of qg
-// consecutive blocks, and the flat index space (group, split, query block in
-// group) is dealt to the 8 XCDs in contiguous ranges (workgroup i runs on XCD
-// i % 8).  The workgroups running together on one XCD thus cover a few
-// database splits for one group of query blocks: each database row they read
-// is shared by up to qg workgroups through that XCD's L2, and the group's
-// query planes stay resident in it.
-__host__ __device__ inline int64_t tile_grid_space(int64_t nqblk, int64_t nsplit, int64_t qg) {
-    return ((nqblk + qg - 1) / qg) * qg * nsplit;
+// Grid of the GEMM-tiled scan.  The query blocks are cut into groups of qg
+// consecutive blocks and the splits into runs of spc; a chunk is one group
+// times one run, qg * spc workgroups (about what one XCD holds at once).
+// Chunk c runs on XCD c % 8 (workgroup i runs on XCD i % 8), the chunks of
+// one XCD in increasing order.  The workgroups running together on an XCD
+// thus cover spc splits for qg query blocks: each database row they read is
+// shared by qg workgroups through that XCD's L2, and the group's query planes
+// stay resident in it.  Consecutive chunks -- the split runs of a group, or
+// the groups when there is one run -- go to different XCDs, which balances
+// the XCDs also when later query blocks have less work (the self-join's
+// upper triangle).
+__host__ __device__ inline int64_t tile_grid_space(int64_t nqblk, int64_t nsplit, int64_t qg,
+                                                   int64_t spc) {
+    const int64_t nch = ((nqblk + qg - 1) / qg) * ((nsplit + spc - 1) / spc);
+    return ((nch + 7) / 8) * 8 * qg * spc;
 }
 __device__ __forceinline__ bool map_block_grouped(int64_t nqblk, int64_t nsplit, int64_t qg,
-                                                  int64_t *split, int64_t *qblk) {
-    const int64_t space = tile_grid_space(nqblk, nsplit, qg);
-    const int64_t per_xcd = (space + 7) / 8;
-    const int64_t w = (int64_t)(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-    if (w >= space) return false;
-    const int64_t grp = w / (qg * nsplit), rem = w % (qg * nsplit);
-    *split = rem / qg;
-    *qblk = grp * qg + rem % qg;
-    return *qblk < nqblk;
+                                                  int64_t spc, int64_t *split, int64_t *qblk) {
+    const int64_t nsc = (nsplit + spc - 1) / spc, cs = qg * spc;
+    const int64_t nch = ((nqblk + qg - 1) / qg) * nsc;
+    const int64_t i = blockIdx.x >> 3;
+    const int64_t c = (i / cs) * 8 + (blockIdx.x & 7);
+    if (c >= nch) return false;
+    const int64_t r = i % cs;
+    *split = (c % nsc) * spc + r / qg;
+    *qblk = (c / nsc) * qg + r % qg;
+    return *split < nsplit && *qblk < nqblk;
 }
 
 // ---------------------------------------------------------------------------

@@ -63,6 +63,18 @@ size_t gemm_lds_bytes(int st, int pb, int wr, int wq, int rb, int qb, int kc, in
     return 2 * stage + (size_t)wr * bq * 8 + (size_t)wr * wq * cap * 8;  // st 2: one hi plane
 }
 
+// Bits v (0..15) of the values of a 32-row block whose row offsets
+// 8 (v / 4) + v % 4 + (the lane's 4 h + 32 rb) lie below t, given t minus
+// that lane offset: the offsets grow with v, so the bits form a prefix.  The
+// epilogues mask their hits with it instead of comparing every offset (per
+// value compares are hoisted by the compiler into 64 lane masks per tile).
+__device__ __forceinline__ uint32_t rows_below_mask(int t) {
+    int c = 0;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) c += min(max(t - 8 * g, 0), 4);
+    return c >= 16 ? 0xffffu : (1u << c) - 1u;
+}
+
 // Epilogue of one row tile (shared by both kernels).  Lane (l32, h) of wave
 // (wr, wq) holds query qw0 + 32 qb + l32 and, in register v of row block rb,
 // row wr0 + 32 rb + 8 (v / 4) + 4 h + v % 4.
@@ -208,10 +220,8 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[QB][RB], const Sca
                     mk[rb] = 0u;
 #pragma unroll
                     for (int v = 0; v < 16; ++v)
-                        mk[rb] |= (acc[qb][rb][v] < thr_r[qb] &&
-                                   rb * 32 + 8 * (v / 4) + 4 * h + v % 4 < lim)
-                                      ? (1u << v)
-                                      : 0u;
+                        mk[rb] |= acc[qb][rb][v] < thr_r[qb] ? (1u << v) : 0u;
+                    mk[rb] &= rows_below_mask(lim - rb * 32 - 4 * h);
                     c += __builtin_popcount(mk[rb]);
                 }
                 if (c > 0) {
@@ -255,10 +265,9 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[QB][RB], const Sca
             for (int rb = 0; rb < RB; ++rb) {
                 mk[rb] = 0u;
 #pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int off = rb * 32 + 8 * (v / 4) + 4 * h + v % 4;
-                    mk[rb] |= (acc[qb][rb][v] <= thr_r[qb] && off < lim && off >= omin) ? (1u << v) : 0u;
-                }
+                for (int v = 0; v < 16; ++v) mk[rb] |= acc[qb][rb][v] <= thr_r[qb] ? (1u << v) : 0u;
+                mk[rb] &= rows_below_mask(lim - rb * 32 - 4 * h) &
+                          ~rows_below_mask(omin - rb * 32 - 4 * h);
                 c += __builtin_popcount(mk[rb]);
             }
             if (c > 0) {
@@ -290,7 +299,7 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
     const int wr = wave % WR, wq = wave / WR;
 
     int64_t split, qblk;
-    if (!map_block_grouped(a.nqblk, a.nsplit, a.qgroup, &split, &qblk)) return;
+    if (!map_block_grouped(a.nqblk, a.nsplit, a.qgroup, a.qspc, &split, &qblk)) return;
     int64_t r0 = split * a.rows_per_split;
     const int64_t r1 = min(a.n, r0 + a.rows_per_split);
     const int64_t q0 = qblk * BQ;
@@ -448,6 +457,9 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
     bool seeded = (a.kk + 1) / 2 > 16 * RB;
     for (int64_t t0 = r0; t0 < r1; t0 += BR) {
         const bool last_tile = t0 + BR >= r1;
+        // the epilogue stays after the K loop: values it computes from the
+        // tile alone (row ids, offset masks) are then not hoisted into
+        // registers held across the loop
         for (int kc = 0; kc < nkc; ++kc) {
             char *cur = smem + par * S::STAGE_BYTES;
             char *nxt = smem + (par ^ 1) * S::STAGE_BYTES;
@@ -469,14 +481,10 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
             }
             if (more) lstore(nxt, kc_next);
             par ^= 1;
-            if (!last_chunk) {
-                __syncthreads();
-                continue;
-            }
-
-            gemm_epilogue<WR, BQ, RB, QB, MODE>(acc, a, ectx, t0 + wr * 32 * RB, thr_r, gt, seeded);
-            __syncthreads();
+            if (!last_chunk) __syncthreads();
         }
+        gemm_epilogue<WR, BQ, RB, QB, MODE>(acc, a, ectx, t0 + wr * 32 * RB, thr_r, gt, seeded);
+        __syncthreads();
     }
 
     if constexpr (MODE == 0) {
@@ -607,7 +615,7 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_dma_kernel(ScanKArgs a) {
     (void)NT;
 
     int64_t split, qblk;
-    if (!map_block_grouped(a.nqblk, a.nsplit, a.qgroup, &split, &qblk)) return;
+    if (!map_block_grouped(a.nqblk, a.nsplit, a.qgroup, a.qspc, &split, &qblk)) return;
     int64_t r0 = split * a.rows_per_split;
     const int64_t r1 = min(a.n, r0 + a.rows_per_split);
     const int64_t q0 = qblk * BQ;
@@ -810,9 +818,10 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_dma_kernel(ScanKArgs a) {
 template <int MODE>
 hipError_t launch_gemm_scan(int storage, int planes, const ScanPlan &plan, const ScanKArgs &args,
                             hipStream_t st) {
-    const int64_t grid = ((tile_grid_space(plan.nqblk, plan.nsplit, plan.tile_group) + 7) / 8) * 8;
+    const int64_t grid = tile_grid_space(plan.nqblk, plan.nsplit, plan.tile_group, plan.tile_spc);
     ScanKArgs ga = args;
     ga.qgroup = plan.tile_group;
+    ga.qspc = plan.tile_spc;
     ga.publish_block = plan.lw * plan.kk >= plan.kk_final;
     // cut lists at twice their keep: each cut tightens the list's threshold
     // for the price of one sort of ~2 kk entries

@@ -99,6 +99,7 @@ struct ScanPlan {
     int tile_st = 1, tile_pb = 1;  // GEMM-tiled and row-shared scans: storage and query planes
                                    // they were planned for
     int64_t tile_group = 8;        // GEMM-tiled scan: query blocks per XCD group (grid order)
+    int64_t tile_spc = 1;          // GEMM-tiled scan: splits per XCD chunk (grid order)
     int share_topm = 0;   // row-shared scan: >0 keeps per-lane register top-m values (sample
                           // estimates; lists get 4 * m values per query and workgroup, ids 0)
     int share_kmin = 0;   // row-shared scan: k-means lists (each lane appends what lies below its
