@@ -29,6 +29,10 @@ int set_err(int code, const char *fmt, ...) {
 }
 
 int hip_err(hipError_t e, const char *what) {
+    // a failed runtime call (e.g. hipMalloc) also leaves its code as the
+    // thread's last error, which the next launch check would read back as
+    // its own: clear it once it is reported
+    (void)hipGetLastError();
     if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation)
         return set_err(VS_ERR_OOM, "%s: out of device memory (%s)", what, hipGetErrorString(e));
     return set_err(VS_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
@@ -53,6 +57,20 @@ struct DeviceGuard {
     }
 };
 
+// Test support (option "fail_alloc"): when > 0, the device allocation
+// that brings it to 0 fails as out of memory, so tests reach the failure
+// paths of every caller.  Per thread, like the error text.
+thread_local int64_t g_fail_alloc = 0;
+
+// Every device allocation of an index goes through here.
+hipError_t dev_malloc(void **p, size_t bytes) {
+    if (g_fail_alloc > 0 && --g_fail_alloc == 0) {
+        *p = nullptr;
+        return hipErrorOutOfMemory;
+    }
+    return hipMalloc(p, bytes);
+}
+
 // Device buffer that only grows.
 struct DevBuf {
     void *p = nullptr;
@@ -66,7 +84,7 @@ struct DevBuf {
             bytes = 0;
         }
         size_t nb = std::max(need, (size_t)4096);
-        hipError_t e = hipMalloc(&p, nb);
+        hipError_t e = dev_malloc(&p, nb);
         if (e != hipSuccess) {
             p = nullptr;
             return e;
@@ -286,8 +304,9 @@ int ensure_capacity(vs_index *x, int64_t need) {
     float *nxn = nullptr;
     const size_t xbytes = (size_t)(nc + kRowSlack) * rb;
     const size_t nbytes = (size_t)(nc + kRowSlack) * sizeof(float);
-    VS_HIP(hipMalloc(&nxb, xbytes), "allocating vector storage");
-    if (hipMalloc((void **)&nxn, nbytes) != hipSuccess) {
+    VS_HIP(dev_malloc(&nxb, xbytes), "allocating vector storage");
+    if (dev_malloc((void **)&nxn, nbytes) != hipSuccess) {
+        (void)hipGetLastError();
         (void)hipFree(nxb);
         return set_err(VS_ERR_OOM, "allocating norm storage (%zu bytes)", nbytes);
     }
@@ -340,8 +359,9 @@ int widen_storage(vs_index *x) {
     float *nxn = nullptr;
     const size_t xbytes = (size_t)(nc + kRowSlack) * new_ld * 4;
     const size_t nbytes = (size_t)(nc + kRowSlack) * sizeof(float);
-    VS_HIP(hipMalloc(&nxb, xbytes), "allocating fp32 storage");
-    if (hipMalloc((void **)&nxn, nbytes) != hipSuccess) {
+    VS_HIP(dev_malloc(&nxb, xbytes), "allocating fp32 storage");
+    if (dev_malloc((void **)&nxn, nbytes) != hipSuccess) {
+        (void)hipGetLastError();
         (void)hipFree(nxb);
         return set_err(VS_ERR_OOM, "allocating norm storage");
     }
@@ -1325,10 +1345,14 @@ int vs_device_count(int *count) {
 }
 
 int vs_device_name(int device, char *buf, int64_t len) {
+    if (!buf || len <= 0) return set_err(VS_ERR_INVALID, "null or empty name buffer");
     hipDeviceProp_t p;
     hipError_t e = hipGetDeviceProperties(&p, device);
     if (e != hipSuccess) return hip_err(e, "hipGetDeviceProperties");
-    snprintf(buf, (size_t)len, "%s (%s, %d CUs)", p.name, p.gcnArchName, p.multiProcessorCount);
+    // the marketing name can be empty (some drivers leave it blank): the
+    // architecture, CU count and memory size name the part then
+    snprintf(buf, (size_t)len, "%s (%s, %d CUs, %.0f GiB)", p.name[0] ? p.name : "HIP device",
+             p.gcnArchName, p.multiProcessorCount, (double)p.totalGlobalMem / (1024.0 * 1024 * 1024));
     return VS_OK;
 }
 
@@ -1404,6 +1428,8 @@ void vs_index_destroy(vs_index *x) {
 int vs_index_reserve(vs_index *x, int64_t n) {
     if (int rc = check_index(x)) return rc;
     if (n < 0) return set_err(VS_ERR_INVALID, "n must be >= 0");
+    if (n > (int64_t)INT32_MAX)
+        return set_err(VS_ERR_INVALID, "n = %lld rows exceeds the int32 id range", (long long)n);
     DeviceGuard g(x->device);
     return ensure_capacity(x, n);
 }
@@ -1542,8 +1568,9 @@ int vs_index_remove_ids(vs_index *x, const int64_t *ids, int64_t n, int64_t *nre
     float *nxn = nullptr;
     const size_t xbytes = (size_t)(x->cap + kRowSlack) * rb;
     const size_t nbytes = (size_t)(x->cap + kRowSlack) * 4;
-    VS_HIP(hipMalloc(&nxb, xbytes), "removeIds storage");
-    if (hipMalloc((void **)&nxn, nbytes) != hipSuccess) {
+    VS_HIP(dev_malloc(&nxb, xbytes), "removeIds storage");
+    if (dev_malloc((void **)&nxn, nbytes) != hipSuccess) {
+        (void)hipGetLastError();
         (void)hipFree(nxb);
         return set_err(VS_ERR_OOM, "removeIds norms");
     }
@@ -2440,6 +2467,11 @@ int vs_index_set_option(vs_index *x, const char *name, int64_t value) {
         {"km16_rt", &VsOptions::km16_rt, 2, 4},
         {"pick_order", &VsOptions::pick_order, 0, 1},
     };
+    if (strcmp(name, "fail_alloc") == 0) {  // not a planner option: this thread's countdown
+        if (value < 0) return set_err(VS_ERR_INVALID, "option fail_alloc: value %lld < 0", (long long)value);
+        g_fail_alloc = value;
+        return VS_OK;
+    }
     for (const Opt &o : opts) {
         if (strcmp(o.name, name) != 0) continue;
         if (value < o.lo || value > o.hi || (o.field == &VsOptions::km16_rt && value == 3))

@@ -111,136 +111,109 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[QB][RB], const Sca
     if constexpr (MODE == 0) {
         if (!seeded && lim == 32 * RB) {
             // First tile: instead of appending every value while the
-            // lists have no threshold, each lane finds (by bisection
-            // on the order-preserving code) a value T_lane with at
-            // least ceil(kk / 2) of its values at or below it; the
-            // list of (row wave, query) -- two lanes, h = 0 and 1 --
-            // then holds >= kk values at or below the larger of the
-            // two, which becomes its threshold, and only those are
-            // appended.  Rows past the split end hold +inf and are
-            // never appended; if they leave fewer than kk finite
-            // values, the threshold is +inf and stays unset.
+            // lists have no threshold, each lane takes T_lane, the largest
+            // of the minima of G groups of its 64 values (G = 16, 32 or 64,
+            // the first >= ceil(kk / 2)): at least ceil(kk / 2) of its
+            // values lie at or below T_lane.  The list of (row wave, query)
+            // -- two lanes, h = 0 and 1 -- then holds >= kk values at or
+            // below T, the larger of the two, once the append below has
+            // taken every value < T' (T' the next value code above T);
+            // T' becomes the list's threshold.
             const int need = (a.kk + 1) / 2;
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb) {
-                float fmn = VS_INF, fmx = -VS_INF;
+                float tl = -VS_INF;
+                if (need <= 4 * RB) {
+#pragma unroll
+                    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                        for (int u = 0; u < 4; ++u)
+                            tl = fmaxf(tl, fminf(fminf(acc[qb][rb][4 * u], acc[qb][rb][4 * u + 1]),
+                                                 fminf(acc[qb][rb][4 * u + 2], acc[qb][rb][4 * u + 3])));
+                } else if (need <= 8 * RB) {
+#pragma unroll
+                    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                        for (int u = 0; u < 8; ++u)
+                            tl = fmaxf(tl, fminf(acc[qb][rb][2 * u], acc[qb][rb][2 * u + 1]));
+                } else {
+#pragma unroll
+                    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) tl = fmaxf(tl, acc[qb][rb][v]);
+                }
+                const float tv = fmaxf(tl, __shfl_xor(tl, 32));
+                const int q = qw0 + qb * 32 + l32;
+                if (q0 + q < a.nq) {
+                    const float t1 = dec_order(enc_order(tv) + 1u);
+                    if (h == 0) thr_w[q] = fminf(thr_w[q], t1);
+                    thr_r[qb] = fminf(thr_r[qb], t1);
+                }
+            }
+            seeded = true;
+        }
+        // appends first, then the cuts: every list starts the tile with at
+        // most cap - 32 RB entries (a query gains at most 32 * RB per tile
+        // from this wave), and a list past that or past its flush point is
+        // cut to its kk best after the appends, when no accumulator is live
+        // any more (a cut also tightens the list's threshold)
+        uint32_t appended = 0u;  // query blocks of this wave that appended
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+            thr_r[qb] = fminf(thr_r[qb], dec_order(gt[qb]));
+            float m = VS_INF;
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) m = fminf(m, acc[qb][rb][v]);
+            if (!__ballot(m < thr_r[qb])) continue;
+            appended |= 1u << qb;
+            const int q = qw0 + qb * 32 + l32;
+            // the passing values of each 32-row block as a bit mask in a
+            // VGPR (no lane mask per value stays live across the append)
+            uint32_t mk[RB];
+            int c = 0;
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) {
+                mk[rb] = 0u;
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+                    mk[rb] |= acc[qb][rb][v] < thr_r[qb] ? (1u << v) : 0u;
+                mk[rb] &= rows_below_mask(lim - rb * 32 - 4 * h);
+                c += __builtin_popcount(mk[rb]);
+            }
+            if (c > 0) {
+                int pos = atomicAdd(&cnt_w[q], c);
+                float *cvq = cv + (int64_t)q * a.cap;
+                int32_t *ciq = ci + (int64_t)q * a.cap;
 #pragma unroll
                 for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
                     for (int v = 0; v < 16; ++v) {
-                        fmn = fminf(fmn, acc[qb][rb][v]);
-                        fmx = fmaxf(fmx, acc[qb][rb][v]);
-                    }
-                // invariant: count(value <= dec(hi)) >= need (all 16 RB >= need)
-                uint32_t lo = enc_order(fmn), hi = enc_order(fmx);
-                for (int itb = 0; itb < 20 && lo < hi; ++itb) {
-                    const uint32_t mid = lo + ((hi - lo) >> 1);
-                    const float fm = dec_order(mid);
-                    int c = 0;
-#pragma unroll
-                    for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-                        for (int v = 0; v < 16; ++v) c += acc[qb][rb][v] <= fm ? 1 : 0;
-                    if (c >= need)
-                        hi = mid;
-                    else
-                        lo = mid + 1;
-                }
-                const uint32_t tl = max(hi, (uint32_t)__shfl_xor((int)hi, 32));
-                const float tv = dec_order(tl);
-                const int q = qw0 + qb * 32 + l32;
-                const bool valid = q0 + q < a.nq;
-                uint32_t mk[RB];
-                int c = 0;
-#pragma unroll
-                for (int rb = 0; rb < RB; ++rb) {
-                    mk[rb] = 0u;
-#pragma unroll
-                    for (int v = 0; v < 16; ++v)
-                        mk[rb] |= (valid && acc[qb][rb][v] <= tv && acc[qb][rb][v] < VS_INF) ? (1u << v)
-                                                                                           : 0u;
-                    c += __builtin_popcount(mk[rb]);
-                }
-                int pos = 0;
-                if (c > 0) pos = atomicAdd(&cnt_w[q], c);
-                if (c > 0) {
-                    float *cvq = cv + (int64_t)q * a.cap;
-                    int32_t *ciq = ci + (int64_t)q * a.cap;
-#pragma unroll
-                    for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-                        for (int v = 0; v < 16; ++v) {
-                            if (mk[rb] & (1u << v)) {
-                                cvq[pos] = acc[qb][rb][v];
-                                ciq[pos] = (int32_t)(wr0 + rb * 32 + 8 * (v / 4) + 4 * h + v % 4);
-                                ++pos;
-                            }
+                        if (mk[rb] & (1u << v)) {
+                            cvq[pos] = acc[qb][rb][v];
+                            ciq[pos] = (int32_t)(wr0 + rb * 32 + 8 * (v / 4) + 4 * h + v % 4);
+                            ++pos;
                         }
-                }
-                // the list now holds >= kk values <= tv (none if the
-                // tile has fewer than kk valid rows: then tv is +inf)
-                if (valid && h == 0) thr_w[q] = fminf(thr_w[q], tv);
-                lds_wave_sync();
-                if (valid) thr_r[qb] = fminf(thr_r[qb], thr_w[q]);
+                    }
             }
-            seeded = true;
-        } else {
+        }
+        if (appended) {
+            lds_wave_sync();  // the counts' atomics are done
+            const int room = min(a.cap - 32 * RB, a.flush_at);
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb) {
-                thr_r[qb] = fminf(thr_r[qb], dec_order(gt[qb]));
-                float m = VS_INF;
-#pragma unroll
-                for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-                    for (int v = 0; v < 16; ++v) m = fminf(m, acc[qb][rb][v]);
-                if (!__ballot(m < thr_r[qb])) continue;
+                if (!(appended & (1u << qb))) continue;
                 const int q = qw0 + qb * 32 + l32;
-                // make room: a list this tile could overflow (a query
-                // gains at most 32 * RB entries per tile from this
-                // wave), or one past its flush point, is cut to its kk
-                // best first (which also tightens its threshold)
-                const int room = min(a.cap - 32 * RB, a.flush_at);
-                if (__ballot(h == 0 && cnt_w[q] > room)) {
-                    for (int j = 0; j < 32; ++j) {
-                        const int qq = qw0 + qb * 32 + j;
-                        if (cnt_w[qq] > room)
-                            flush_list(cv + (int64_t)qq * a.cap, ci + (int64_t)qq * a.cap,
-                                       &cnt_w[qq], &thr_w[qq], &thr[qq], BQ, WR,
-                                       &a.gthr[q0 + qq], sv_w, si_w, a.cap, a.kk,
-                                       a.kk_final, a.publish_block, lane);
-                    }
-                    thr_r[qb] = fminf(thr_r[qb], thr_w[q]);
+                if (!__ballot(h == 0 && cnt_w[q] > room)) continue;
+                for (int j = 0; j < 32; ++j) {
+                    const int qq = qw0 + qb * 32 + j;
+                    if (cnt_w[qq] > room)
+                        flush_list(cv + (int64_t)qq * a.cap, ci + (int64_t)qq * a.cap, &cnt_w[qq],
+                                   &thr_w[qq], &thr[qq], BQ, WR, &a.gthr[q0 + qq], sv_w, si_w,
+                                   a.cap, a.kk, a.kk_final, a.publish_block, lane);
                 }
-                // the passing values of each 32-row block as a bit mask in a
-                // VGPR (no lane mask per value stays live across the append)
-                uint32_t mk[RB];
-                int c = 0;
-#pragma unroll
-                for (int rb = 0; rb < RB; ++rb) {
-                    mk[rb] = 0u;
-#pragma unroll
-                    for (int v = 0; v < 16; ++v)
-                        mk[rb] |= acc[qb][rb][v] < thr_r[qb] ? (1u << v) : 0u;
-                    mk[rb] &= rows_below_mask(lim - rb * 32 - 4 * h);
-                    c += __builtin_popcount(mk[rb]);
-                }
-                if (c > 0) {
-                    int pos = atomicAdd(&cnt_w[q], c);
-                    float *cvq = cv + (int64_t)q * a.cap;
-                    int32_t *ciq = ci + (int64_t)q * a.cap;
-#pragma unroll
-                    for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-                        for (int v = 0; v < 16; ++v) {
-                            if (mk[rb] & (1u << v)) {
-                                cvq[pos] = acc[qb][rb][v];
-                                ciq[pos] =
-                                    (int32_t)(wr0 + rb * 32 + 8 * (v / 4) + 4 * h + v % 4);
-                                ++pos;
-                            }
-                        }
-                }
-                lds_wave_sync();
+                thr_r[qb] = fminf(thr_r[qb], thr_w[q]);
             }
         }
     } else {

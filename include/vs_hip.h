@@ -256,6 +256,8 @@ VS_API int vs_index_sync(vs_index *idx);
  *   "km16"        1: the k-means assign reads a bf16 copy of the centroids
  *   "km16_rt"     2 or 4: 16-row blocks per tile of that scan
  *   "pick_order"  1: the k-means pick walks the points grouped by the last step's clusters
+ *   "fail_alloc"  n > 0: the n-th device allocation of any index from now on, on
+ *                 this thread, fails as VS_ERR_OOM (failure-path tests; 0 clears it)
  * Unknown names and out-of-range values: VS_ERR_INVALID. */
 VS_API int vs_index_set_option(vs_index *idx, const char *name, int64_t value);
 

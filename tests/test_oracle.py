@@ -250,3 +250,24 @@ def test_self_join_brute_force_numpy():
     i, j, sc = oracle.self_join(x, t, nthreads=2)
     assert np.array_equal(i, ii) and np.array_equal(j, jj) and len(i) > 20
     assert np.allclose(sc, s[ii, jj].astype(np.float32), rtol=2e-7)
+
+
+def test_oracle_memory_safety_under_sanitizers():
+    """oracle.c under AddressSanitizer + UndefinedBehaviorSanitizer: a driver
+    (oracle/asan_check.c) calls every entry point on edge shapes (ragged d,
+    counts not multiples of 4, k above n, empty inputs, growing range
+    buffers, self-join windows, empty k-means clusters); any invalid access
+    aborts the run with the sanitizer's report."""
+    import shutil
+    import subprocess
+
+    if shutil.which("gcc") is None:
+        pytest.skip("no gcc to build the sanitizer run")
+    odir = os.path.join(os.path.dirname(HERE), "oracle")
+    b = subprocess.run(["make", "-s", "-C", odir, "asan"], capture_output=True, text=True)
+    if b.returncode != 0 and "asan" in (b.stderr + b.stdout).lower() and "cannot find" in b.stderr:
+        pytest.skip("this gcc has no sanitizer runtime")
+    assert b.returncode == 0, b.stderr
+    r = subprocess.run([os.path.join(odir, "asan_check")], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-4000:]
+    assert "asan_check ok" in r.stdout
