@@ -42,7 +42,12 @@ struct GemmShape {
     static constexpr int NW = WR * WQ, NT = 64 * NW;
     static constexpr int BR = WR * 32 * RB, BQ = WQ * 32 * QB;
     static constexpr int AP = ST == 0 ? 2 : 1;  // row planes in LDS: bf16 hi (, lo)
-    static constexpr int KP = KC + 8;           // LDS row stride in elements
+    // K-chunk 64: unpadded 128-byte LDS rows whose eight 16-byte pieces are
+    // stored XOR-swizzled by the row's low three bits (piece c of row r at
+    // c ^ (r & 7)), so that fragment reads and row writes stay free of bank
+    // conflicts without padding; smaller chunks pad each row by 16 bytes
+    static constexpr bool SW = KC == 64;
+    static constexpr int KP = SW ? KC : KC + 8;  // LDS row stride in elements
     static constexpr int ESZ = ST == 1 ? 2 : 4;  // bytes per stored element
     static constexpr int A_CPR = KC * ESZ / 16;  // 16-byte global chunks per row and K-chunk
     static constexpr int A_LOADS = BR * A_CPR / NT;
@@ -55,10 +60,12 @@ struct GemmShape {
     static_assert(BR / 4 <= NT, "one thread per 4 row norms");
     static_assert(BR <= kRowSlack, "the last row tile reads at most kRowSlack rows past the end");
     static_assert((KP * 2) % 16 == 0, "16-byte aligned LDS rows");
+    static_assert(!SW || KC * 2 / 16 == 8, "the swizzle permutes 8 pieces per row");
 };
 
 size_t gemm_lds_bytes(int st, int pb, int wr, int wq, int rb, int qb, int kc, int cap) {
-    const size_t br = (size_t)wr * 32 * rb, bq = (size_t)wq * 32 * qb, kp = (size_t)kc + 8;
+    const size_t br = (size_t)wr * 32 * rb, bq = (size_t)wq * 32 * qb;
+    const size_t kp = kc == 64 ? (size_t)kc : (size_t)kc + 8;
     const size_t stage = ((st == 0 ? 2 : 1) * br + (size_t)pb * bq) * kp * 2 + br * 4;
     return 2 * stage + (size_t)wr * bq * 8 + (size_t)wr * wq * cap * 8;  // st 2: one hi plane
 }
@@ -262,6 +269,10 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[QB][RB], const Sca
     }
 }
 
+// The register-staged kernel writes the next chunk's tiles to LDS between
+// the MFMAs of the current chunk's last K-step.
+constexpr bool kInterleaveStores = true;
+
 template <int ST, int PB, int WR, int WQ, int RB, int QB, int KC, int MODE>
 __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
     using S = GemmShape<ST, PB, WR, WQ, RB, QB, KC>;
@@ -332,36 +343,47 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
         }
         if (kc == 0 && l2 && tid < BR / 4) rn = *(const f32x4_t *)(a.xn + trow + 4 * tid);
     };
-    auto lstore = [&](char *stage, int kc) __attribute__((always_inline)) {
+    // physical 16-byte piece of logical piece c of an LDS row r
+    auto piece = [](int c, int r) __attribute__((always_inline)) {
+        return S::SW ? (c ^ (r & 7)) : c;
+    };
+    auto lstore_ab = [&](char *stage) __attribute__((always_inline)) {
         uint16_t *As = (uint16_t *)stage;
         uint16_t *Bs = As + S::AP * BR * KP;
 #pragma unroll
         for (int j = 0; j < S::A_LOADS; ++j) {
             const int i = tid + j * NT, row = i / S::A_CPR, c = i % S::A_CPR;
             if constexpr (ST == 1) {
-                *(u32x4_t *)(As + row * KP + c * 8) = ra[j];
-            } else if constexpr (ST == 2) {  // one-pass selection: the bf16 hi plane only
-                typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
-                const bf16x4_t hi = __builtin_convertvector(__builtin_bit_cast(f32x4_t, ra[j]), bf16x4_t);
-                *(u32x2_t *)(As + row * KP + c * 4) = __builtin_bit_cast(u32x2_t, hi);
+                *(u32x4_t *)(As + row * KP + piece(c, row) * 8) = ra[j];
             } else {
+                // c counts 16-byte pieces of fp32 (4 elements): bf16 element
+                // offset 4 c, i.e. half c % 2 of 16-byte bf16 piece c / 2
+                const int e = piece(c >> 1, row) * 8 + (c & 1) * 4;
                 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
                 const f32x4_t f = __builtin_bit_cast(f32x4_t, ra[j]);
                 const bf16x4_t hi = __builtin_convertvector(f, bf16x4_t);
-                const bf16x4_t lo =
-                    __builtin_convertvector(f - __builtin_convertvector(hi, f32x4_t), bf16x4_t);
-                *(u32x2_t *)(As + row * KP + c * 4) = __builtin_bit_cast(u32x2_t, hi);
-                *(u32x2_t *)(As + BR * KP + row * KP + c * 4) = __builtin_bit_cast(u32x2_t, lo);
+                *(u32x2_t *)(As + row * KP + e) = __builtin_bit_cast(u32x2_t, hi);
+                if constexpr (ST == 0) {  // split fp32 rows: the lo plane too
+                    const bf16x4_t lo =
+                        __builtin_convertvector(f - __builtin_convertvector(hi, f32x4_t), bf16x4_t);
+                    *(u32x2_t *)(As + BR * KP + row * KP + e) = __builtin_bit_cast(u32x2_t, lo);
+                }
             }
         }
 #pragma unroll
         for (int j = 0; j < S::B_LOADS; ++j) {
             const int i = tid + j * NT, qr = i / S::B_CPR, c = i % S::B_CPR;
             const int q = qr / PB, p = qr % PB;
-            *(u32x4_t *)(Bs + (p * BQ + q) * KP + c * 8) = rq[j];
+            *(u32x4_t *)(Bs + (p * BQ + q) * KP + piece(c, q) * 8) = rq[j];
         }
+    };
+    auto lstore_norms = [&](char *stage, int kc) __attribute__((always_inline)) {
         if (kc == 0 && l2 && tid < BR / 4)
-            *(f32x4_t *)((float *)(As + S::STAGE_ELEMS) + 4 * tid) = rn;
+            *(f32x4_t *)((float *)((uint16_t *)stage + S::STAGE_ELEMS) + 4 * tid) = rn;
+    };
+    auto lstore = [&](char *stage, int kc) __attribute__((always_inline)) {
+        lstore_ab(stage);
+        lstore_norms(stage, kc);
     };
 
     f32x16_t acc[QB][RB];
@@ -370,32 +392,43 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
     // One K-chunk of MFMAs from LDS stage `stage`.  FIRST: the tile's first
     // chunk, whose first K-step takes the row norms (L2) or zero (IP) as its
     // C operand.
-    auto compute = [&](const char *stage, auto first_c) __attribute__((always_inline)) {
+    // One K-chunk of MFMAs from LDS stage `stage`; with `nstage`, the next
+    // chunk's A and B tiles (already loaded into registers) are written to
+    // that stage between the MFMAs of the last K-step, so that the LDS
+    // writes overlap the matrix pipe instead of following it.
+    auto compute = [&](const char *stage, auto first_c, char *nstage) __attribute__((always_inline)) {
         constexpr bool FIRST = decltype(first_c)::value;
         const uint16_t *As = (const uint16_t *)stage;
         const uint16_t *Bs = As + S::AP * BR * KP;
-        const uint16_t *al_ = As + (wr * 32 * RB + l32) * KP + 8 * h;
-        const uint16_t *bl_ = Bs + (qw0 + l32) * KP + 8 * h;
+        // the lane's A and B rows (rows wr 32 RB + l32 + 32 rb and
+        // qw0 + l32 + 32 qb, all with low bits l32 & 7); K-step ks reads
+        // logical piece 2 ks + h of them
+        const uint16_t *al_ = As + (wr * 32 * RB + l32) * KP;
+        const uint16_t *bl_ = Bs + (qw0 + l32) * KP;
+        auto koff = [&](int ks) __attribute__((always_inline)) { return piece(2 * ks + h, l32) * 8; };
         const float *Ns = (const float *)(As + S::STAGE_ELEMS) + wr * 32 * RB + 4 * h;
 #pragma unroll
         for (int ks = 0; ks < KC / 16; ++ks) {
+            // the last K-step and the stores form a scheduling region of
+            // their own (the group barriers below order it)
+            if (kInterleaveStores && ks + 1 == KC / 16) __builtin_amdgcn_sched_barrier(0);
             bf16x8_t b0[QB], b1[QB];
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb) {
                 b0[qb] = __builtin_bit_cast(bf16x8_t,
-                                            *(const u32x4_t *)(bl_ + qb * 32 * KP + ks * 16));
+                                            *(const u32x4_t *)(bl_ + qb * 32 * KP + koff(ks)));
                 if constexpr (PB == 2)
                     b1[qb] = __builtin_bit_cast(
-                        bf16x8_t, *(const u32x4_t *)(bl_ + BQ * KP + qb * 32 * KP + ks * 16));
+                        bf16x8_t, *(const u32x4_t *)(bl_ + BQ * KP + qb * 32 * KP + koff(ks)));
             }
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb) {
                 const bf16x8_t ah = __builtin_bit_cast(
-                    bf16x8_t, *(const u32x4_t *)(al_ + rb * 32 * KP + ks * 16));
+                    bf16x8_t, *(const u32x4_t *)(al_ + rb * 32 * KP + koff(ks)));
                 bf16x8_t alo;
                 if constexpr (ST == 0)
                     alo = __builtin_bit_cast(
-                        bf16x8_t, *(const u32x4_t *)(al_ + BR * KP + rb * 32 * KP + ks * 16));
+                        bf16x8_t, *(const u32x4_t *)(al_ + BR * KP + rb * 32 * KP + koff(ks)));
                 f32x16_t x16;
                 if (FIRST && ks == 0) {
                     if (l2) {
@@ -417,6 +450,22 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
                     if constexpr (PB == 2) acc[qb][rb] = mfma32_bf16(ah, b1[qb], acc[qb][rb]);
                 }
             }
+        }
+        if constexpr (kInterleaveStores) {
+            lstore_ab(nstage);
+            // schedule of the last K-step: its B fragment reads, then per
+            // row block its A fragment read(s), its MFMAs and one store of
+            // the next stage; the remaining stores last
+            constexpr int MPB = QB * (1 + (ST == 0) + (PB == 2));  // MFMAs per row block
+            constexpr int NST = S::A_LOADS * (ST == 0 ? 2 : 1) + S::B_LOADS;
+            __builtin_amdgcn_sched_group_barrier(0x100, QB * PB, 0);
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) {
+                __builtin_amdgcn_sched_group_barrier(0x100, ST == 0 ? 2 : 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, MPB, 0);
+                if (rb < NST) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+            }
+            if (NST > RB) __builtin_amdgcn_sched_group_barrier(0x200, NST > RB ? NST - RB : 0, 0);
         }
     };
 
@@ -448,11 +497,14 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
                         gt[qb] = __hip_atomic_load(&a.gthr[q0 + qw0 + qb * 32 + l32],
                                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
-                compute(cur, std::true_type{});
+                compute(cur, std::true_type{}, nxt);
             } else {
-                compute(cur, std::false_type{});
+                compute(cur, std::false_type{}, nxt);
             }
-            if (more) lstore(nxt, kc_next);
+            // (with interleaved stores, the last chunk stores stale registers
+            // into the free stage, which nothing reads afterwards)
+            if (!kInterleaveStores && more) lstore_ab(nxt);
+            if (more) lstore_norms(nxt, kc_next);
             par ^= 1;
             if (!last_chunk) __syncthreads();
         }

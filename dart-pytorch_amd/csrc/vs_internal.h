@@ -275,6 +275,8 @@ size_t scan_lds_bytes(int bn, int planes, int64_t ld, int cap, int nw);
 // blocks queries per tile.  Storage 2 = fp32 rows read as their bf16 hi
 // plane only (one-pass selection, kSelectCoarse below).
 #define VS_GEMM_SHAPES(X)                                                                     \
+    X(1, 1, 2, 4, 4, 2, 64)                                                                   \
+    X(1, 1, 2, 2, 4, 2, 64)                                                                   \
     X(1, 1, 2, 4, 4, 2, 32)                                                                   \
     X(2, 1, 2, 4, 4, 2, 32)                                                                   \
     X(2, 1, 2, 2, 4, 2, 32)                                                                   \

@@ -3,7 +3,8 @@ staged in LDS) against the CPU oracle (restating IndexFlat.search /
 rangeSearch, index_flat.dart:62-137, and the Kmeans assign/update steps,
 kmeans.dart:91-140).
 
-Every built shape is forced here: bf16 rows with one or two query planes,
+Every built shape is forced here: bf16 rows with one or two query planes
+(K-chunks of 64 in XOR-swizzled LDS rows, or 32 in padded ones),
 fp32 rows (split into bf16 hi/lo planes in LDS) with one or two query
 planes, 128- and 256-query blocks, 4 and 8 waves.  Row counts end inside a
 row tile, query counts inside a query block, d is ragged, both metrics, k
@@ -23,6 +24,8 @@ NT = oracle.default_threads()
 # blocks per wave, 32-query blocks per wave, K-chunk), as listed by
 # VS_GEMM_SHAPES in dart-pytorch_amd/csrc/vs_internal.h.
 SHAPES = [
+    (1, 1, 2, 4, 4, 2, 64),
+    (1, 1, 2, 2, 4, 2, 64),
     (1, 1, 2, 4, 4, 2, 32),
     (1, 1, 2, 2, 4, 2, 32),
     (1, 2, 2, 4, 4, 2, 32),
@@ -121,16 +124,17 @@ def test_gemm_dma_shape_parity(vs, opts, shape, metric, k, d):
     assert_knn_parity(D, I, Dr, Ir, metric, rtol=1e-3)
 
 
-@pytest.mark.parametrize("dma", [pytest.param(1, marks=pytest.mark.skip(reason=DMA_OFF)), 0])
+@pytest.mark.parametrize("dma,kc", [pytest.param(1, 32, marks=pytest.mark.skip(reason=DMA_OFF)),
+                                    (0, 64), (0, 32)])
 @pytest.mark.parametrize("wq,qb", [(4, 2), (2, 2)])
-def test_gemm_config2_exact(vs, opts, wq, qb, dma):
+def test_gemm_config2_exact(vs, opts, wq, qb, dma, kc):
     """configs[1] arithmetic on a 100k slice with 1,000 queries: integer
     distances, bit-exact, k = 100, on the LDS-DMA and register-staged
-    kernels."""
-    opts(gemm_wq=wq, gemm_qb=qb, gemm_dma=dma)
+    kernels (K-chunks of 64 and 32)."""
+    opts(gemm_wq=wq, gemm_qb=qb, gemm_dma=dma, gemm_kc=kc)
     xb = syn.int_grid(100_000, 128, 1234, 0)
     xq = syn.int_grid(1000, 128, 1234, 1)
-    key = f"gemmdma:1,2,{wq},4,{qb},4" if dma else _key((1, 1, 2, wq, 4, qb, 32))
+    key = f"gemmdma:1,2,{wq},4,{qb},4" if dma else _key((1, 1, 2, wq, 4, qb, kc))
     D, I, gemm = _search(vs, xb, xq, 100, 0, "auto", key=key)
     assert gemm >= 1
     Dr, Ir = oracle.flat_search(xb, xq, 100, 0, NT)
