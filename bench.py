@@ -67,8 +67,12 @@ CPU_SHARE = 16  # host cores of one GPU's share on the measurement boxes
 # (workload, n, nq, k).  The command and readings are in the named profile;
 # configurations without a measurement report traffic null.
 MEASURED_TRAFFIC = {
-    ("c2", 1_000_000, 10_000, 100): (1.09e9, "profiles/scan_c2_1Mx128_k100.md"),
-    ("c3", 20_000_000, 1, 10): (30.88e9, "profiles/scan_c3_20Mx768_b1_b64.md"),
+    ("c2", 1_000_000, 10_000, 100): (1.093e9, "profiles/scan_c2_1Mx128_k100.md"),
+    ("c3", 20_000_000, 1, 10): (30.83e9, "profiles/scan_c3_20Mx768_b1_b64.md"),
+    ("c3", 20_000_000, 64, 10): (30.78e9, "profiles/scan_c3_20Mx768_b1_b64.md"),
+    ("c3", 20_000_000, 1024, 10): (43.99e9, "profiles/gemm_c3_20Mx768_b1024_b8192.md"),
+    ("c4", 2_000_000, 4096, 256): (2.52e9, "profiles/kmeans_c4_2Mx256.md"),
+    ("c5", 500_000, 500_000, 512): (240.36e9, "profiles/selfjoin_c5_500kx512.md"),
 }
 
 
@@ -481,7 +485,8 @@ def run_kmeans(vs, NN, args, ctx):
     fam = {f: pts.prof_get(f) for f in ("assign", "pick", "exhaustive", "update")}
     nsc, scan_s = kernel_avg(pts, "assign")
     passes = mfma_passes(pts)
-    roof = roofline("mfma", 2.0 * n * K * d, scan_s, ctx["peaks"], "assign scan", nsc,
+    traffic, tsrc = MEASURED_TRAFFIC.get(("c4", n, K, d), (None, None))
+    roof = roofline("mfma", 2.0 * n * K * d, scan_s, ctx["peaks"], "assign scan", nsc, traffic, tsrc,
                     peak_div=passes,
                     extra={"peak_note": f"bf16 dense MFMA peak / {passes} pass(es) per distance"})
     out = {"metric": "k-means assign+update, points per second per iteration",
@@ -560,8 +565,9 @@ def run_join(vs, NN, args, ctx):
     pi, pj, ps = res["p"]
     nj, join_s = kernel_avg(g, "join")
     passes = mfma_passes(g)
+    traffic, tsrc = MEASURED_TRAFFIC.get(("c5", n, n, d), (None, None))
     roof = roofline("mfma", 2.0 * d * n * (n - 1) / 2, join_s, ctx["peaks"],
-                    "join scan (upper triangle)", nj, peak_div=passes,
+                    "join scan (upper triangle)", nj, traffic, tsrc, peak_div=passes,
                     extra={"peak_note": f"bf16 dense MFMA peak / {passes} pass(es) per distance",
                            "refine_avg_ms": round(kernel_avg(g, "refine")[1] * 1e3, 3)})
     out = {"metric": "cosine self-join, vectors per second", "value": round(n * args.steps / wall, 1),
