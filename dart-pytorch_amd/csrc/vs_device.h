@@ -134,6 +134,79 @@ __device__ inline void flush_list(float *cvq, int32_t *ciq, int *cnt_q, float *t
     wave_sync();
 }
 
+// The final cut of a wave's lists, one lane per list (lane q < bn handles
+// list q; bn <= 64, kk <= KM): each lane keeps its list's kk best (value, id)
+// pairs in registers by insertion, writes them back sorted and padded to kk,
+// and sets and publishes the list's threshold as flush_list does -- the
+// same lists and thresholds as flush_list on every list of more than kk
+// entries, without visiting the lists one after another.
+template <int KM>
+__device__ inline void final_cut_lanes(float *cv, int32_t *ci, int *cnt_w, float *thr_w,
+                                       const float *thr, int bn, int nl, uint32_t *gthr,
+                                       int cap, int kk, int kk_final, int publish_block, int lane) {
+    wave_sync();  // every lane's appends and counts are visible
+    const int q = lane;
+    if (q < bn) {
+        const int c = cnt_w[q];
+        const int keep = c < kk ? c : kk;
+        float *cvq = cv + (int64_t)q * cap;
+        int32_t *ciq = ci + (int64_t)q * cap;
+        if (c > kk) {
+            float bv[KM];
+            int bi[KM];
+#pragma unroll
+            for (int m = 0; m < KM; ++m) {
+                bv[m] = VS_INF;
+                bi[m] = INT_MAX;
+            }
+            for (int e = 0; e < c; ++e) {
+                float v = cvq[e];
+                int id = ciq[e];
+                // insertion by (value, id); slots past kk stay +inf
+#pragma unroll
+                for (int m = 0; m < KM; ++m) {
+                    const bool lt = m < kk && (v < bv[m] || (v == bv[m] && id < bi[m]));
+                    const float tv = lt ? bv[m] : v;
+                    const int ti = lt ? bi[m] : id;
+                    bv[m] = lt ? v : bv[m];
+                    bi[m] = lt ? id : bi[m];
+                    v = tv;
+                    id = ti;
+                }
+            }
+            float kth = VS_INF;
+#pragma unroll
+            for (int m = 0; m < KM; ++m) {
+                if (m < kk) {
+                    cvq[m] = bv[m];
+                    ciq[m] = bi[m];
+                }
+                if (m == kk - 1) kth = bv[m];
+            }
+            cnt_w[q] = keep;
+            thr_w[q] = fminf(thr_w[q], kth);
+        } else {
+            for (int j = c; j < kk; ++j) {
+                cvq[j] = VS_INF;
+                ciq[j] = -1;
+            }
+        }
+    }
+    lds_wave_sync();  // the lists' thresholds are written
+    if (q < bn && cnt_w[q] >= kk) {
+        const float kth = thr_w[q];
+        if (kk >= kk_final) {
+            atomicMin(&gthr[q], enc_order(kth));
+        } else if (publish_block) {
+            const float *t0 = thr + q;
+            float b = t0[0];
+            for (int i = 1; i < nl; ++i) b = fmaxf(b, t0[i * bn]);
+            if (b < VS_INF) atomicMin(&gthr[q], enc_order(b));
+        }
+    }
+    wave_sync();
+}
+
 __device__ __forceinline__ f32x4_t mfma_bf16(bf16x8_t a, bf16x8_t b, f32x4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }

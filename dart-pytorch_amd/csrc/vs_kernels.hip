@@ -523,18 +523,24 @@ __global__ __launch_bounds__(64 * NW) void scan_kernel(ScanKArgs a) {
     }
 
     if constexpr (MODE == 0) {
-        // final: every list holds its kk best in slots [0, kk), padded
-        wave_sync();
-        for (int q = 0; q < BN; ++q) {
-            const int c = cnt_w[q];
-            if (c > a.kk) {
-                flush_list(cv + (int64_t)q * a.cap, ci + (int64_t)q * a.cap, &cnt_w[q], &thr_w[q],
-                           &thr[q], BN, 4, &a.gthr[q0 + q], sv_w, si_w, a.cap, a.kk, a.kk_final,
-                           a.publish_block, lane);
-            } else {
-                for (int j = c + lane; j < a.kk; j += 64) {
-                    cv[(int64_t)q * a.cap + j] = VS_INF;
-                    ci[(int64_t)q * a.cap + j] = -1;
+        // final: every list holds its kk best in slots [0, kk), padded (one
+        // lane per list when the keep fits in registers)
+        if (a.kk <= 16) {
+            final_cut_lanes<16>(cv, ci, cnt_w, thr_w, thr, BN, 4, &a.gthr[q0], a.cap, a.kk,
+                                a.kk_final, a.publish_block, lane);
+        } else {
+            wave_sync();
+            for (int q = 0; q < BN; ++q) {
+                const int c = cnt_w[q];
+                if (c > a.kk) {
+                    flush_list(cv + (int64_t)q * a.cap, ci + (int64_t)q * a.cap, &cnt_w[q],
+                               &thr_w[q], &thr[q], BN, 4, &a.gthr[q0 + q], sv_w, si_w, a.cap,
+                               a.kk, a.kk_final, a.publish_block, lane);
+                } else {
+                    for (int j = c + lane; j < a.kk; j += 64) {
+                        cv[(int64_t)q * a.cap + j] = VS_INF;
+                        ci[(int64_t)q * a.cap + j] = -1;
+                    }
                 }
             }
         }
