@@ -174,6 +174,8 @@ struct VsOptions {
     int km16 = 1;          // k-means: the scan reads a bf16 copy of the centroids
     int km16_rt = 4;       // k-means on that copy: 16-row blocks per tile (2 or 4)
     int pick_order = 1;    // k-means: the pick walks points grouped by the last step's clusters
+    int merge_mu = 0;      // merge: 1024-entry chunks per workgroup pass (0: by batch size; 1, 2,
+                           // 4 or 8)
 };
 
 struct vs_index {
@@ -616,6 +618,12 @@ bool plan_gemm(const vs_index *x, int64_t nq, int64_t nrows, int planes, int sto
 int plan_scan(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t kk_final,
               int storage, vs::ScanPlan *p, bool safe = false, int64_t max_lists = 0,
               bool range = false, int min_tiles = 8, size_t list_budget = 0) {
+    // the merge runs one workgroup per query: a batch that leaves most CUs
+    // idle reads more chunks per pass (more loads in flight per workgroup)
+    int mu = x->opt.merge_mu;
+    if (!mu) mu = nq <= x->num_cu ? 8 : nq <= 4 * x->num_cu ? 4 : 1;
+    while (mu > 1 && vs::merge_lds_bytes(x->ld, mu) > x->lds_max) mu >>= 1;
+    p->merge_mu = mu;
     int64_t kk = kk_final <= 32 ? kk_final : kk_final / 4;
     const int kkw = x->opt.scan_kkw;
     if (kkw > 0) kk = std::min<int64_t>(kk_final, std::max<int64_t>(4, next_pow2(kkw)));
@@ -2466,6 +2474,7 @@ int vs_index_set_option(vs_index *x, const char *name, int64_t value) {
         {"km16", &VsOptions::km16, 0, 1},
         {"km16_rt", &VsOptions::km16_rt, 2, 4},
         {"pick_order", &VsOptions::pick_order, 0, 1},
+        {"merge_mu", &VsOptions::merge_mu, 0, 8},
     };
     if (strcmp(name, "fail_alloc") == 0) {  // not a planner option: this thread's countdown
         if (value < 0) return set_err(VS_ERR_INVALID, "option fail_alloc: value %lld < 0", (long long)value);
@@ -2474,7 +2483,9 @@ int vs_index_set_option(vs_index *x, const char *name, int64_t value) {
     }
     for (const Opt &o : opts) {
         if (strcmp(o.name, name) != 0) continue;
-        if (value < o.lo || value > o.hi || (o.field == &VsOptions::km16_rt && value == 3))
+        const bool hole = (o.field == &VsOptions::km16_rt && value == 3) ||
+                          (o.field == &VsOptions::merge_mu && value > 2 && value != 4 && value != 8);
+        if (value < o.lo || value > o.hi || hole)
             return set_err(VS_ERR_INVALID, "option %s: value %lld outside [%d, %d]", name,
                            (long long)value, o.lo, o.hi);
         x->opt.*(o.field) = (int)value;

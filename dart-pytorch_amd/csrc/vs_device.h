@@ -134,16 +134,18 @@ __device__ inline void flush_list(float *cvq, int32_t *ciq, int *cnt_q, float *t
     wave_sync();
 }
 
-// The final cut of a wave's lists, one lane per list (lane q < bn handles
-// list q; bn <= 64, kk <= KM): each lane keeps its list's kk best (value, id)
-// pairs in registers by insertion, writes them back sorted and padded to kk,
-// and sets and publishes the list's threshold as flush_list does -- the
-// same lists and thresholds as flush_list on every list of more than kk
-// entries, without visiting the lists one after another.
+// Cuts a wave's lists of more than `over` (>= kk) entries, one lane per list
+// (lane q < bn handles list q; bn <= 64, kk <= KM): each lane keeps its
+// list's kk best (value, id) pairs in registers by insertion, writes them
+// back sorted, and sets and publishes the list's threshold as flush_list
+// does -- the same lists and thresholds as flush_list on each of those
+// lists, without visiting the lists one after another.  pad: lists of fewer
+// than kk entries are padded to kk with sentinels (the final cut, over = kk).
 template <int KM>
-__device__ inline void final_cut_lanes(float *cv, int32_t *ci, int *cnt_w, float *thr_w,
+__device__ inline void cut_lists_lanes(float *cv, int32_t *ci, int *cnt_w, float *thr_w,
                                        const float *thr, int bn, int nl, uint32_t *gthr,
-                                       int cap, int kk, int kk_final, int publish_block, int lane) {
+                                       int cap, int kk, int kk_final, int publish_block,
+                                       int over, bool pad, int lane) {
     wave_sync();  // every lane's appends and counts are visible
     const int q = lane;
     if (q < bn) {
@@ -151,7 +153,7 @@ __device__ inline void final_cut_lanes(float *cv, int32_t *ci, int *cnt_w, float
         const int keep = c < kk ? c : kk;
         float *cvq = cv + (int64_t)q * cap;
         int32_t *ciq = ci + (int64_t)q * cap;
-        if (c > kk) {
+        if (c > over) {
             float bv[KM];
             int bi[KM];
 #pragma unroll
@@ -159,19 +161,32 @@ __device__ inline void final_cut_lanes(float *cv, int32_t *ci, int *cnt_w, float
                 bv[m] = VS_INF;
                 bi[m] = INT_MAX;
             }
-            for (int e = 0; e < c; ++e) {
-                float v = cvq[e];
-                int id = ciq[e];
-                // insertion by (value, id); slots past kk stay +inf
+            // 8 entries per batch, all loaded before any is inserted (cap is
+            // a multiple of 8, so a batch never leaves the list's buffer;
+            // entries past the count become sentinels, which never insert)
+            for (int e0 = 0; e0 < c; e0 += 8) {
+                float v8[8];
+                int i8[8];
 #pragma unroll
-                for (int m = 0; m < KM; ++m) {
-                    const bool lt = m < kk && (v < bv[m] || (v == bv[m] && id < bi[m]));
-                    const float tv = lt ? bv[m] : v;
-                    const int ti = lt ? bi[m] : id;
-                    bv[m] = lt ? v : bv[m];
-                    bi[m] = lt ? id : bi[m];
-                    v = tv;
-                    id = ti;
+                for (int u = 0; u < 8; ++u) {
+                    v8[u] = cvq[e0 + u];
+                    i8[u] = ciq[e0 + u];
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    float v = e0 + u < c ? v8[u] : VS_INF;
+                    int id = e0 + u < c ? i8[u] : INT_MAX;
+                    // insertion by (value, id); slots past kk stay +inf
+#pragma unroll
+                    for (int m = 0; m < KM; ++m) {
+                        const bool lt = m < kk && (v < bv[m] || (v == bv[m] && id < bi[m]));
+                        const float tv = lt ? bv[m] : v;
+                        const int ti = lt ? bi[m] : id;
+                        bv[m] = lt ? v : bv[m];
+                        bi[m] = lt ? id : bi[m];
+                        v = tv;
+                        id = ti;
+                    }
                 }
             }
             float kth = VS_INF;
@@ -185,7 +200,7 @@ __device__ inline void final_cut_lanes(float *cv, int32_t *ci, int *cnt_w, float
             }
             cnt_w[q] = keep;
             thr_w[q] = fminf(thr_w[q], kth);
-        } else {
+        } else if (pad) {
             for (int j = c; j < kk; ++j) {
                 cvq[j] = VS_INF;
                 ciq[j] = -1;

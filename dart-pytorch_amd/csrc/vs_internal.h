@@ -106,6 +106,8 @@ struct ScanPlan {
                           // running minimum + kmin_margin; a list that would fill is marked
                           // full, count cap + 1, and takes no more)
     float kmin_margin = 0.f;
+    int merge_mu = 1;     // merge: 1024-entry chunks each workgroup loads per pass (1, 2, 4, 8;
+                          // more hides load latency when few queries leave most CUs idle)
     int64_t nqblk = 0;    // query blocks
     int64_t nsplit = 0;   // database splits
     int64_t rows_per_split = 0;
@@ -268,6 +270,8 @@ hipError_t launch_gen_normal(void *dst, int out_dtype, int64_t n, int64_t d, uin
 // Shape rules shared by the host planner and the kernels.
 int64_t storage_ld(int64_t d, int storage);  // elements per stored row
 size_t scan_lds_bytes(int bn, int planes, int64_t ld, int cap, int nw);
+// LDS of the merge workgroup reading mu chunks per pass
+size_t merge_lds_bytes(int64_t ld, int mu);
 // The built shapes of the GEMM-tiled scan, in the planner's order of
 // preference: X(storage, query planes, row waves, query waves, 32-row blocks
 // per wave, 32-query blocks per wave, K-chunk).  A workgroup covers

@@ -526,8 +526,8 @@ __global__ __launch_bounds__(64 * NW) void scan_kernel(ScanKArgs a) {
         // final: every list holds its kk best in slots [0, kk), padded (one
         // lane per list when the keep fits in registers)
         if (a.kk <= 16) {
-            final_cut_lanes<16>(cv, ci, cnt_w, thr_w, thr, BN, 4, &a.gthr[q0], a.cap, a.kk,
-                                a.kk_final, a.publish_block, lane);
+            cut_lists_lanes<16>(cv, ci, cnt_w, thr_w, thr, BN, 4, &a.gthr[q0], a.cap, a.kk,
+                                a.kk_final, a.publish_block, a.kk, true, lane);
         } else {
             wave_sync();
             for (int q = 0; q < BN; ++q) {
@@ -825,12 +825,13 @@ __device__ void select_block(float *sv, int *si, int n, int kk, float *tmp_v, in
     __syncthreads();
 }
 
-template <int ST, int MODE>
+template <int ST, int MODE, int MU>
 __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
+    constexpr int MBUF = kMergeBuf * MU;
     extern __shared__ __align__(16) char smem[];
-    float *bv = (float *)smem;                  // [kMergeBuf]
-    int *bi = (int *)(bv + kMergeBuf);          // [kMergeBuf]
-    float *qsh = (float *)(bi + kMergeBuf);     // [ld]
+    float *bv = (float *)smem;                  // [MBUF]
+    int *bi = (int *)(bv + MBUF);               // [MBUF]
+    float *qsh = (float *)(bi + MBUF);          // [ld]
     float *tmp_v = qsh + a.ld;                  // [kMergeKeepMax]
     int *tmp_i = (int *)(tmp_v + kMergeKeepMax);  // [kMergeKeepMax]
     __shared__ SelScratch sel;
@@ -862,56 +863,54 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
 
     // entries above the query's final shared threshold cannot be among the
     // kk best (at least kk candidates lie at or below it); each thread reads
-    // 4 adjacent entries of one list per step (kl is a multiple of 4)
+    // 4 adjacent entries of one list per 1024-entry chunk (kl is a multiple
+    // of 4), MU chunks per pass with all their loads in flight at once, and
+    // the buffer takes a whole pass (MU * 1024 entries) before it is cut
     const float tfinal = a.gthr ? dec_order(a.gthr[qg]) : VS_INF;
-    for (int64_t base = 0; base < total; base += 1024) {
-        const int64_t e = base + 4 * tid;
-        if (e < total) {
-            const int64_t list = e / kl, j = e % kl;
-            const int64_t split = list / a.lw, w = list % a.lw;
-            const int64_t li = ((qblk * a.nsplit + split) * a.lw + w) * a.bn + q;
-            const int64_t lc = a.list_cnt ? a.list_cnt[li] : kl;  // entries past it are stale
-            if (j < lc) {
-                const int64_t off = li * a.cap + j;
-                const float4 v4 = *(const float4 *)(a.cand_v + off);
-                const int4 i4 = *(const int4 *)(a.cand_i + off);
-                const float vs4[4] = {v4.x, v4.y, v4.z, v4.w};
-                const int is4[4] = {i4.x, i4.y, i4.z, i4.w};
-                const float th = s_thr;
-                const int thi = s_thr_id;
+    for (int64_t base = 0; base < total; base += 1024 * MU) {
+        float4 v4[MU];
+        int4 i4[MU];
+        int nv[MU];  // valid entries of the thread's 4 (0 when past the end or the list's count)
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const float v = vs4[u];
-                    const int id = is4[u];
-                    if (j + u < lc && id >= 0 && v <= tfinal && (v < th || (v == th && id < thi))) {
-                        const int pos = atomicAdd(&s_cnt, 1);
-                        bv[kk + pos] = v;
-                        bi[kk + pos] = id;
-                    }
+        for (int u = 0; u < MU; ++u) {
+            const int64_t e = base + 1024 * u + 4 * tid;
+            nv[u] = 0;
+            if (e < total) {
+                const int64_t list = e / kl, j = e % kl;
+                const int64_t split = list / a.lw, w = list % a.lw;
+                const int64_t li = ((qblk * a.nsplit + split) * a.lw + w) * a.bn + q;
+                const int64_t lc = a.list_cnt ? a.list_cnt[li] : kl;  // entries past it are stale
+                if (j < lc) {
+                    const int64_t off = li * a.cap + j;
+                    v4[u] = *(const float4 *)(a.cand_v + off);
+                    i4[u] = *(const int4 *)(a.cand_i + off);
+                    nv[u] = (int)min<int64_t>(4, lc - j);
+                }
+            }
+        }
+        const float th = s_thr;
+        const int thi = s_thr_id;
+#pragma unroll
+        for (int u = 0; u < MU; ++u) {
+            const float vs4[4] = {v4[u].x, v4[u].y, v4[u].z, v4[u].w};
+            const int is4[4] = {i4[u].x, i4[u].y, i4[u].z, i4[u].w};
+#pragma unroll
+            for (int x = 0; x < 4; ++x) {
+                const float v = vs4[x];
+                const int id = is4[x];
+                if (x < nv[u] && id >= 0 && v <= tfinal && (v < th || (v == th && id < thi))) {
+                    const int pos = atomicAdd(&s_cnt, 1);
+                    bv[kk + pos] = v;
+                    bi[kk + pos] = id;
                 }
             }
         }
         __syncthreads();
         const int c = s_cnt;
-        if (c > kMergeBuf - kk - 1024 || (base + 1024 >= total && c > 0)) {
-            if constexpr (MODE == 2) {  // the r-th value is wanted: sorted
-                int sz = 1;
-                while (sz < kk + c) sz <<= 1;
-                for (int t = kk + c + tid; t < sz; t += 256) {
-                    bv[t] = VS_INF;
-                    bi[t] = INT_MAX;
-                }
-                __syncthreads();
-                bitonic_sort_block(bv, bi, sz);
-                if (tid == 0) {
-                    s_cnt = 0;
-                    s_thr = bv[kk - 1];
-                    s_thr_id = bi[kk - 1];
-                }
-            } else {  // the kk best in any order, and the kk-th
-                select_block(bv, bi, kk + c, kk, tmp_v, tmp_i, sel, &s_thr, &s_thr_id);
-                if (tid == 0) s_cnt = 0;
-            }
+        if (c > MBUF - kk - 1024 * MU || (base + 1024 * MU >= total && c > 0)) {
+            // the kk best in any order, and the kk-th
+            select_block(bv, bi, kk + c, kk, tmp_v, tmp_i, sel, &s_thr, &s_thr_id);
+            if (tid == 0) s_cnt = 0;
         }
         __syncthreads();
     }
@@ -921,6 +920,7 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
         // value (r = kk: a bound on the query's kk-th best; r < kk: an
         // estimate of a larger rank of the full scan), and its successor
         // code keeps that value itself below the threshold
+        bitonic_sort_block(bv, bi, kk);
         const int r = a.seed_rank > 0 ? a.seed_rank : kk;
         if (tid == 0 && bi[r - 1] != INT_MAX && bv[r - 1] < VS_INF)
             atomicMin(&a.gthr_w[qg], enc_order(bv[r - 1]) + 1u);
@@ -1057,8 +1057,22 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
     }
 }
 
-static size_t merge_lds(int64_t ld) {
-    return (size_t)kMergeBuf * 8 + (size_t)ld * 4 + (size_t)kMergeKeepMax * 8;
+static size_t merge_lds(int64_t ld, int mu = 1) {
+    return (size_t)kMergeBuf * mu * 8 + (size_t)ld * 4 + (size_t)kMergeKeepMax * 8;
+}
+
+size_t merge_lds_bytes(int64_t ld, int mu) { return merge_lds(ld, mu); }
+
+// merge_refine_kernel<ST, MODE, mu> for mu in {1, 2, 4, 8}, or null
+template <int ST, int MODE>
+static void (*merge_fn(int mu))(MergeKArgs) {
+    switch (mu) {
+        case 1: return merge_refine_kernel<ST, MODE, 1>;
+        case 2: return merge_refine_kernel<ST, MODE, 2>;
+        case 4: return merge_refine_kernel<ST, MODE, 4>;
+        case 8: return merge_refine_kernel<ST, MODE, 8>;
+        default: return nullptr;
+    }
 }
 
 hipError_t launch_merge_refine(const void *xb, int storage, int64_t ld, int64_t d, int metric,
@@ -1106,8 +1120,10 @@ hipError_t launch_merge_refine(const void *xb, int storage, int64_t ld, int64_t 
     a.k = k;
     a.D = D;
     a.I = I;
-    const size_t lds = merge_lds(ld);
-    void (*fn)(MergeKArgs) = storage == 1 ? merge_refine_kernel<1, 0> : merge_refine_kernel<0, 0>;
+    const size_t lds = merge_lds(ld, plan.merge_mu);
+    void (*fn)(MergeKArgs) =
+        storage == 1 ? merge_fn<1, 0>(plan.merge_mu) : merge_fn<0, 0>(plan.merge_mu);
+    if (!fn) return hipErrorInvalidValue;
     if (lds > 64 * 1024) {
         hipError_t e = hipFuncSetAttribute((const void *)fn,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -1399,8 +1415,9 @@ hipError_t launch_merge_threshold(const PreparedQueries &pq, const ScanPlan &pla
         merge_estimate_kernel<<<dim3((unsigned)((pq.nq + 3) / 4)), dim3(256), 0, st>>>(a);
         return hipGetLastError();
     }
-    const size_t lds = merge_lds(ld);
-    void (*fn)(MergeKArgs) = merge_refine_kernel<1, 2>;
+    const size_t lds = merge_lds(ld, plan.merge_mu);
+    void (*fn)(MergeKArgs) = merge_fn<1, 2>(plan.merge_mu);
+    if (!fn) return hipErrorInvalidValue;
     if (lds > 64 * 1024) {
         hipError_t e = hipFuncSetAttribute((const void *)fn,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -1460,7 +1477,7 @@ hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, 
         return hipGetLastError();
     }
     const size_t lds = merge_lds(ld);
-    void (*fn)(MergeKArgs) = merge_refine_kernel<0, 1>;
+    void (*fn)(MergeKArgs) = merge_refine_kernel<0, 1, 1>;
     if (lds > 64 * 1024) {
         hipError_t e = hipFuncSetAttribute((const void *)fn,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);

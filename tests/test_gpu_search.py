@@ -337,6 +337,29 @@ def test_large_batch_estimated_threshold(vs, nq, k, metric):
     assert np.array_equal(r1.distances, r0.distances)
 
 
+@pytest.mark.parametrize("nq,k,metric", [(5, 100, 0), (64, 10, 1), (300, 100, 1)])
+def test_merge_chunks_per_pass(vs, nq, k, metric):
+    """The merge reads 1, 2, 4 or 8 chunks of 1024 list entries per pass
+    (option merge_mu; by default more when the batch is small).  Over
+    300,000 integer rows -- a threshold pre-pass or estimate, thousands of
+    lists per query, buffer cuts -- every setting gives the oracle's result."""
+    xb = syn.int_grid(300_000, 64, 13, 0)
+    xq = syn.int_grid(nq, 64, 13, 1)
+    idx = vs.GpuIndexFlat(64, vs.Metric(metric), storage="auto")
+    idx.add(xb)
+    res = {}
+    for mu in (1, 2, 4, 8):
+        idx.set_option("merge_mu", mu)
+        res[mu] = idx.search(xq, k)
+    idx.close()
+    sub = np.arange(0, nq, 3)
+    Dr, Ir = oracle.flat_search(xb, xq[sub], k, metric, NT)
+    for mu, r in res.items():
+        assert_knn_parity(r.distances[sub], r.ids[sub], Dr, Ir, metric, rtol=0.0, atol=0.0,
+                          xb=xb, xq=xq[sub])
+        assert np.array_equal(r.distances, res[1].distances), mu
+
+
 def test_estimated_threshold_too_tight_falls_back(vs):
     """A sample that is not representative: the first 1/16 of the rows holds
     64 near copies of every query, the rest lies far away.  The estimate
@@ -371,7 +394,8 @@ def test_set_option_rejects_unknown_and_out_of_range(vs):
     # VS_ERR_INVALID surfaces as ValueError (the reference's ArgumentError)
     with pytest.raises(ValueError, match="unknown option"):
         idx.set_option("no_such_option", 1)
-    for name, value in (("gemm", 2), ("km16_rt", 3), ("scan_kkw", -1)):
+    for name, value in (("gemm", 2), ("km16_rt", 3), ("scan_kkw", -1), ("merge_mu", 3),
+                        ("merge_mu", 16)):
         with pytest.raises(ValueError, match="outside"):
             idx.set_option(name, value)
     idx.set_option("guess", 0)
