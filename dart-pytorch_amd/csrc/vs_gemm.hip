@@ -43,9 +43,13 @@ struct GemmShape {
     static constexpr int BR = WR * 32 * RB, BQ = WQ * 32 * QB;
     static constexpr int AP = ST == 0 ? 2 : 1;  // row planes in LDS: bf16 hi (, lo)
     // K-chunk 64: unpadded 128-byte LDS rows whose eight 16-byte pieces are
-    // stored XOR-swizzled by the row's low three bits (piece c of row r at
-    // c ^ (r & 7)), so that fragment reads and row writes stay free of bank
-    // conflicts without padding; smaller chunks pad each row by 16 bytes
+    // stored XOR-swizzled (piece c of row r at c ^ ((r >> 1) & 7)).  The LDS
+    // serves 256 bytes (64 banks) per cycle, so a 16-byte fragment read is
+    // conflict-free when 16 consecutive lanes -- rows r .. r + 15, the same
+    // logical piece -- hit 16 distinct 16-byte bank groups; a row's group is
+    // 8 (r & 1) + physical piece, hence the swizzle by r >> 1 (by r & 7 rows
+    // r and r + 8 collide).  Row writes (8 lanes per row) stay conflict-free
+    // too.  Smaller chunks pad each row by 16 bytes instead.
     static constexpr bool SW = KC == 64;
     static constexpr int KP = SW ? KC : KC + 8;  // LDS row stride in elements
     static constexpr int ESZ = ST == 1 ? 2 : 4;  // bytes per stored element
@@ -269,6 +273,9 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[QB][RB], const Sca
     }
 }
 
+// Word 3 of a raw buffer resource (gfx9: 32-bit data format, no swizzle).
+constexpr int kBufRsrcWord3 = 0x00020000;
+
 // The register-staged kernel writes the next chunk's tiles to LDS between
 // the MFMAs of the current chunk's last K-step.
 constexpr bool kInterleaveStores = true;
@@ -328,62 +335,87 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
     // (first chunk of a tile) the tile's row norms
     u32x4_t ra[S::A_LOADS], rq[S::B_LOADS];
     f32x4_t rn;
-    auto gload = [&](int64_t trow, int kc) __attribute__((always_inline)) {
-        const char *abase = (const char *)a.xb + trow * row_bytes + (int64_t)kc * KC * S::ESZ;
-#pragma unroll
-        for (int j = 0; j < S::A_LOADS; ++j) {
-            const int i = tid + j * NT, row = i / S::A_CPR, c = i % S::A_CPR;
-            ra[j] = *(const u32x4_t *)(abase + row * row_bytes + c * 16);
-        }
-#pragma unroll
-        for (int j = 0; j < S::B_LOADS; ++j) {
-            const int i = tid + j * NT, qr = i / S::B_CPR, c = i % S::B_CPR;
-            const int q = qr / PB, p = qr % PB;
-            rq[j] = *(const u32x4_t *)(a.qp + ((q0 + q) * 2 + p) * a.ld + kc * KC + c * 8);
-        }
-        if (kc == 0 && l2 && tid < BR / 4) rn = *(const f32x4_t *)(a.xn + trow + 4 * tid);
-    };
     // physical 16-byte piece of logical piece c of an LDS row r
     auto piece = [](int c, int r) __attribute__((always_inline)) {
-        return S::SW ? (c ^ (r & 7)) : c;
-    };
-    auto lstore_ab = [&](char *stage) __attribute__((always_inline)) {
-        uint16_t *As = (uint16_t *)stage;
-        uint16_t *Bs = As + S::AP * BR * KP;
-#pragma unroll
-        for (int j = 0; j < S::A_LOADS; ++j) {
-            const int i = tid + j * NT, row = i / S::A_CPR, c = i % S::A_CPR;
-            if constexpr (ST == 1) {
-                *(u32x4_t *)(As + row * KP + piece(c, row) * 8) = ra[j];
-            } else {
-                // c counts 16-byte pieces of fp32 (4 elements): bf16 element
-                // offset 4 c, i.e. half c % 2 of 16-byte bf16 piece c / 2
-                const int e = piece(c >> 1, row) * 8 + (c & 1) * 4;
-                typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
-                const f32x4_t f = __builtin_bit_cast(f32x4_t, ra[j]);
-                const bf16x4_t hi = __builtin_convertvector(f, bf16x4_t);
-                *(u32x2_t *)(As + row * KP + e) = __builtin_bit_cast(u32x2_t, hi);
-                if constexpr (ST == 0) {  // split fp32 rows: the lo plane too
-                    const bf16x4_t lo =
-                        __builtin_convertvector(f - __builtin_convertvector(hi, f32x4_t), bf16x4_t);
-                    *(u32x2_t *)(As + BR * KP + row * KP + e) = __builtin_bit_cast(u32x2_t, lo);
-                }
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < S::B_LOADS; ++j) {
-            const int i = tid + j * NT, qr = i / S::B_CPR, c = i % S::B_CPR;
-            const int q = qr / PB, p = qr % PB;
-            *(u32x4_t *)(Bs + (p * BQ + q) * KP + piece(c, q) * 8) = rq[j];
-        }
+        return S::SW ? (c ^ ((r >> 1) & 7)) : c;
     };
     auto lstore_norms = [&](char *stage, int kc) __attribute__((always_inline)) {
         if (kc == 0 && l2 && tid < BR / 4)
             *(f32x4_t *)((float *)((uint16_t *)stage + S::STAGE_ELEMS) + 4 * tid) = rn;
     };
-    auto lstore = [&](char *stage, int kc) __attribute__((always_inline)) {
-        lstore_ab(stage);
-        lstore_norms(stage, kc);
+    // piece p of a chunk: A load p (p < A_LOADS; piece 0 also carries a
+    // tile's row norms) or B load p - A_LOADS.  Buffer loads:
+    // a thread's pieces sit at one 32-bit offset from a per-chunk resource
+    // plus a uniform step per piece, so they need one address VGPR per
+    // operand; LDS writes likewise step by whole 16-row groups (the swizzle
+    // repeats every 16 rows), one base address per operand.
+    constexpr int NLD = S::A_LOADS + S::B_LOADS;
+    constexpr int A_STEP = NT / S::A_CPR;       // rows per A piece
+    constexpr int B_STEP = NT / S::B_CPR / PB;  // queries per B piece
+    static_assert(NT % S::A_CPR == 0 && A_STEP % 16 == 0 && NT % (S::B_CPR * PB) == 0 &&
+                      B_STEP % 16 == 0,
+                  "a thread's pieces are whole 16-row groups apart");
+    const int a_row = tid / S::A_CPR, a_c = tid % S::A_CPR;
+    const int b_row = tid / S::B_CPR, b_c = tid % S::B_CPR;  // b_row: q PB + plane
+    const int a_voff = a_row * (int)row_bytes + a_c * 16;
+    // prepared queries keep two plane rows of ld elements per query
+    const int b_voff = ((b_row / PB) * 2 + b_row % PB) * (int)a.ld * 2 + b_c * 16;
+    const __amdgpu_buffer_rsrc_t qrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(a.qp + q0 * 2 * a.ld), 0, (int)min((int64_t)INT32_MAX, (int64_t)BQ * 4 * a.ld),
+        kBufRsrcWord3);
+    // LDS element offsets of the thread's first A and B piece
+    int a_soff, b_soff;
+    if constexpr (ST == 1) {
+        a_soff = a_row * KP + piece(a_c, a_row) * 8;
+    } else {
+        a_soff = a_row * KP + piece(a_c >> 1, a_row) * 8 + (a_c & 1) * 4;
+    }
+    {
+        const int q = b_row / PB, pl = b_row % PB;
+        b_soff = (pl * BQ + q) * KP + piece(b_c, q) * 8;
+    }
+    auto load_piece = [&](int p, int64_t trow, int kc) __attribute__((always_inline)) {
+        if (p < S::A_LOADS) {
+            // the last tile reads at most BR rows past the end, inside the
+            // allocation's slack rows; the resource stops there
+            const int64_t lim = min((int64_t)INT32_MAX, (a.n - trow + BR) * row_bytes);
+            const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+                (void *)((const char *)a.xb + trow * row_bytes), 0, (int)lim, kBufRsrcWord3);
+            ra[p] = __builtin_bit_cast(
+                u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                             xrs, a_voff, p * A_STEP * (int)row_bytes + kc * KC * S::ESZ, 0));
+            if (p == 0 && kc == 0 && l2 && tid < BR / 4)
+                rn = *(const f32x4_t *)(a.xn + trow + 4 * tid);
+        } else {
+            const int j = p - S::A_LOADS;
+            rq[j] = __builtin_bit_cast(
+                u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                             qrs, b_voff, j * B_STEP * (int)a.ld * 4 + kc * KC * 2, 0));
+        }
+    };
+    auto store_piece = [&](int p, char *stage, int kc) __attribute__((always_inline)) {
+        uint16_t *As = (uint16_t *)stage;
+        uint16_t *Bs = As + S::AP * BR * KP;
+        if (p < S::A_LOADS) {
+            uint16_t *dst = As + a_soff + p * A_STEP * KP;
+            if constexpr (ST == 1) {
+                *(u32x4_t *)dst = ra[p];
+            } else {
+                typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+                const f32x4_t f = __builtin_bit_cast(f32x4_t, ra[p]);
+                const bf16x4_t hi = __builtin_convertvector(f, bf16x4_t);
+                *(u32x2_t *)dst = __builtin_bit_cast(u32x2_t, hi);
+                if constexpr (ST == 0) {
+                    const bf16x4_t lo =
+                        __builtin_convertvector(f - __builtin_convertvector(hi, f32x4_t), bf16x4_t);
+                    *(u32x2_t *)(dst + BR * KP) = __builtin_bit_cast(u32x2_t, lo);
+                }
+            }
+            if (p == 0) lstore_norms(stage, kc);
+        } else {
+            const int j = p - S::A_LOADS;
+            *(u32x4_t *)(Bs + b_soff + j * B_STEP * KP) = rq[j];
+        }
     };
 
     f32x16_t acc[QB][RB];
@@ -398,10 +430,12 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
     // writes overlap the matrix pipe instead of following it.
     auto compute = [&](const char *stage, auto first_c, char *nstage) __attribute__((always_inline)) {
         constexpr bool FIRST = decltype(first_c)::value;
+        constexpr bool IL = kInterleaveStores;
         const uint16_t *As = (const uint16_t *)stage;
         const uint16_t *Bs = As + S::AP * BR * KP;
         // the lane's A and B rows (rows wr 32 RB + l32 + 32 rb and
-        // qw0 + l32 + 32 qb, all with low bits l32 & 7); K-step ks reads
+        // qw0 + l32 + 32 qb, offsets of whole 32-row blocks from l32, so all
+        // swizzled as row l32); K-step ks reads
         // logical piece 2 ks + h of them
         const uint16_t *al_ = As + (wr * 32 * RB + l32) * KP;
         const uint16_t *bl_ = Bs + (qw0 + l32) * KP;
@@ -411,7 +445,7 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
         for (int ks = 0; ks < KC / 16; ++ks) {
             // the last K-step and the stores form a scheduling region of
             // their own (the group barriers below order it)
-            if (kInterleaveStores && ks + 1 == KC / 16) __builtin_amdgcn_sched_barrier(0);
+            if (IL && ks + 1 == KC / 16) __builtin_amdgcn_sched_barrier(0);
             bf16x8_t b0[QB], b1[QB];
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb) {
@@ -451,8 +485,9 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
                 }
             }
         }
-        if constexpr (kInterleaveStores) {
-            lstore_ab(nstage);
+        if constexpr (IL) {
+#pragma unroll
+            for (int p = 0; p < NLD; ++p) store_piece(p, nstage, -1);
             // schedule of the last K-step: its B fragment reads, then per
             // row block its A fragment read(s), its MFMAs and one store of
             // the next stage; the remaining stores last
@@ -469,8 +504,10 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
         }
     };
 
-    gload(r0, 0);
-    lstore(smem, 0);
+#pragma unroll
+    for (int p = 0; p < NLD; ++p) load_piece(p, r0, 0);
+#pragma unroll
+    for (int p = 0; p < NLD; ++p) store_piece(p, smem, 0);
     __syncthreads();
 
     int par = 0;  // stage holding the current chunk
@@ -489,7 +526,10 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
             const bool more = !(last_chunk && last_tile);
             const int kc_next = last_chunk ? 0 : kc + 1;
             const int64_t t_next = last_chunk ? t0 + BR : t0;
-            if (more) gload(t_next, kc_next);
+            if (more) {
+#pragma unroll
+                for (int p = 0; p < NLD; ++p) load_piece(p, t_next, kc_next);
+            }
             if (kc == 0) {
                 if constexpr (MODE == 0) {
 #pragma unroll
@@ -503,7 +543,10 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
             }
             // (with interleaved stores, the last chunk stores stale registers
             // into the free stage, which nothing reads afterwards)
-            if (!kInterleaveStores && more) lstore_ab(nxt);
+            if (!kInterleaveStores && more) {
+#pragma unroll
+                for (int p = 0; p < NLD; ++p) store_piece(p, nxt, -1);
+            }
             if (more) lstore_norms(nxt, kc_next);
             par ^= 1;
             if (!last_chunk) __syncthreads();

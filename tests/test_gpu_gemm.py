@@ -344,3 +344,4 @@ def test_kmeans_exhaustive_fallback(vs, opts, coarse):
     ar, _, objr = oracle.kmeans_assign(x, cen, NT)
     assert np.array_equal(a, ar) and obj == objr
     assert not np.any((a >= 100) & (a < 120))  # copies lose to centroid 3
+
