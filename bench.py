@@ -115,7 +115,8 @@ def measured_peaks(NN):
     import ctypes
 
     out = {}
-    for what, key, nbytes in ((0, "hbm_read_gbs", 8 << 30), (1, "bf16_mfma_tflops", 0)):
+    for what, key, nbytes in ((0, "hbm_read_gbs", 8 << 30), (1, "bf16_mfma_tflops", 0),
+                              (2, "bf16_mfma_random_tflops", 0)):
         v = ctypes.c_double(0.0)
         rc = NN.load().vs_dev_probe(0, what, nbytes, ctypes.byref(v))
         out[key] = round(v.value, 1) if rc == 0 else None
@@ -159,10 +160,15 @@ def roofline(kind, work, avg_s, peaks, kernel, launches, traffic=None, traffic_s
         peak = PEAK["bf16_mfma_tflops"] / peak_div
         m = peaks.get("bf16_mfma_tflops")
         meas, unit = (m / peak_div if m else None), "TFLOP/s"
+        mr = peaks.get("bf16_mfma_random_tflops")
+        mr = mr / peak_div if mr else None
     r = {"bound": kind, "achieved": round(ach, 2), "peak": round(peak, 1), "unit": unit,
          "frac": round(ach / peak, 4), "traffic": traffic,
          "measured_peak": round(meas, 1) if meas else None,
          "frac_of_measured": round(ach / meas, 4) if meas else None,
+         **({} if kind == "hbm" else {
+             "measured_peak_random": round(mr, 1) if mr else None,
+             "frac_of_measured_random": round(ach / mr, 4) if mr else None}),
          "kernel": kernel, "launches": launches, "avg_ms": round(avg_s * 1e3, 4),
          ("algorithmic_bytes_per_launch" if kind == "hbm" else "algorithmic_flops_per_launch"): work}
     if traffic_src:

@@ -2354,8 +2354,9 @@ int vs_dev_copy(int device, void *dst, const void *src, int64_t bytes) {
 }
 
 int vs_dev_probe(int device, int what, int64_t bytes, double *result) {
-    if (!result || (what != 0 && what != 1) || (what == 0 && (bytes < (1 << 20) || bytes % 16)))
-        return set_err(VS_ERR_INVALID, "vs_dev_probe: what 0 (bytes >= 1 MiB, 16-byte multiple) or 1");
+    if (!result || what < 0 || what > 2 || (what == 0 && (bytes < (1 << 20) || bytes % 16)))
+        return set_err(VS_ERR_INVALID,
+                       "vs_dev_probe: what 0 (bytes >= 1 MiB, 16-byte multiple), 1 or 2");
     DeviceGuard g(device);
     if (g.err != hipSuccess) return hip_err(g.err, "hipSetDevice");
     void *buf = nullptr;
@@ -2386,7 +2387,8 @@ int vs_dev_probe(int device, int what, int64_t bytes, double *result) {
             VS_HIP(vs::launch_read16(buf, bytes / 16, (uint32_t *)((char *)buf + bytes), nullptr),
                    "read probe");
         else
-            VS_HIP(vs::launch_mfma_peak(blocks, iters, (float *)buf, nullptr), "mfma probe");
+            VS_HIP(vs::launch_mfma_peak(blocks, iters, what == 2, (float *)buf, nullptr),
+                   "mfma probe");
         VS_HIP(hipEventRecord(b, nullptr), "event");
         VS_HIP(hipEventSynchronize(b), "probe");
         float ms = 0.f;

@@ -222,6 +222,14 @@ __device__ inline void cut_lists_lanes(float *cv, int32_t *ci, int *cnt_w, float
     wave_sync();
 }
 
+// Word 3 of a raw buffer resource (gfx9: 32-bit data format, no swizzle).
+constexpr int kBufRsrcWord3 = 0x00020000;
+
+// 16-byte buffer load at byte voff + soff of a resource (soff uniform)
+__device__ __forceinline__ u32x4_t buf_load16(__amdgpu_buffer_rsrc_t rs, int voff, int soff) {
+    return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, 0));
+}
+
 __device__ __forceinline__ f32x4_t mfma_bf16(bf16x8_t a, bf16x8_t b, f32x4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }

@@ -273,9 +273,6 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[QB][RB], const Sca
     }
 }
 
-// Word 3 of a raw buffer resource (gfx9: 32-bit data format, no swizzle).
-constexpr int kBufRsrcWord3 = 0x00020000;
-
 // The register-staged kernel writes the next chunk's tiles to LDS between
 // the MFMAs of the current chunk's last K-step.
 constexpr bool kInterleaveStores = true;

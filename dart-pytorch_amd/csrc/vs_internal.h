@@ -222,7 +222,7 @@ hipError_t launch_range_bounds(const PreparedQueries &pq, int64_t d, int metric,
 // workgroups of 4 waves each running iters rounds of 8 independent
 // 32x32x16 bf16 MFMAs (out: a word the kernels leave unwritten).
 hipError_t launch_read16(const void *src, int64_t n16, uint32_t *out, hipStream_t st);
-hipError_t launch_mfma_peak(int blocks, int iters, float *out, hipStream_t st);
+hipError_t launch_mfma_peak(int blocks, int iters, int rnd, float *out, hipStream_t st);
 
 // dst = src, n16 16-byte words (both 16-byte aligned)
 hipError_t launch_copy16(const void *src, void *dst, int64_t n16, hipStream_t st);

@@ -2074,33 +2074,49 @@ hipError_t launch_read16(const void *src, int64_t n16, uint32_t *out, hipStream_
 
 // each wave: iters rounds of 8 independent v_mfma_f32_32x32x16_bf16
 // (32 x 32 x 16 x 2 flop each) on register operands
-__global__ __launch_bounds__(256) void mfma_peak_kernel(int iters, float *out) {
+__global__ __launch_bounds__(256) void mfma_peak_kernel(int iters, int rnd, float *out) {
     const int lane = threadIdx.x & 63;
-    bf16x8_t a, b;
+    // four A and four B operands; rnd: random signs and mantissas of
+    // magnitude [0.5, 1) (xorshift32 per thread), else small integers
+    bf16x8_t av[4], bv[4];
+    uint32_t x = (blockIdx.x * 256u + threadIdx.x) * 0x9E3779B1u + 0x7F4A7C15u;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        a[i] = (__bf16)(float)((lane + i) & 7);
-        b[i] = (__bf16)(float)((lane * 3 + i) & 7);
-    }
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            if (rnd) {
+                x ^= x << 13;
+                x ^= x >> 17;
+                x ^= x << 5;
+                av[u][i] = __builtin_bit_cast(__bf16, (uint16_t)((x & 0x807Fu) | 0x3F00u));
+                bv[u][i] = __builtin_bit_cast(__bf16, (uint16_t)(((x >> 16) & 0x807Fu) | 0x3F00u));
+            } else {
+                av[u][i] = (__bf16)(float)((lane + i + u) & 7);
+                bv[u][i] = (__bf16)(float)((lane * 3 + i + u) & 7);
+            }
+        }
     f32x16_t c[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j)
 #pragma unroll
         for (int v = 0; v < 16; ++v) c[j][v] = 0.f;
-    for (int it = 0; it < iters; ++it) {
+    // the operand pair changes from one MFMA to the next (iters is even)
+    for (int it = 0; it < iters; it += 2) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) c[j] = mfma32_bf16(a, b, c[j]);
+        for (int j = 0; j < 8; ++j) c[j] = mfma32_bf16(av[j & 3], bv[j >> 2], c[j]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) c[j] = mfma32_bf16(av[j & 3], bv[2 + (j >> 2)], c[j]);
     }
     float s = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j)
 #pragma unroll
         for (int v = 0; v < 16; ++v) s += c[j][v];
-    if (s == -1.0f) out[0] = s;  // sums of non-negative products: never taken
+    if (s != s) out[0] = s;  // finite sums: never taken
 }
 
-hipError_t launch_mfma_peak(int blocks, int iters, float *out, hipStream_t st) {
-    mfma_peak_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(iters, out);
+hipError_t launch_mfma_peak(int blocks, int iters, int rnd, float *out, hipStream_t st) {
+    mfma_peak_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(iters, rnd, out);
     return hipGetLastError();
 }
 

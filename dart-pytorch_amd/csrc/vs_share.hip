@@ -112,17 +112,20 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
             bq[ks][qb] = *(const u32x4_t *)(a.qp + ((q0 + qw + qb * 16 + r16) * 2) * a.ld + ks * 32 +
                                           8 * g);
 
-    // global -> register staging of one tile of rows (and its row norms)
-    const int64_t row_bytes = (int64_t)S::LD * S::ESZ;
+    // global -> register staging of one tile of rows (and its row norms):
+    // buffer loads from a per-tile resource, the thread's j-th load NT
+    // 16-byte chunks after its first (one offset register for all)
+    constexpr int row_bytes = S::LD * S::ESZ;
     u32x4_t ra[S::LOADS];
     f32x4_t rn = {0.f, 0.f, 0.f, 0.f};
     auto gload = [&](int64_t t) __attribute__((always_inline)) {
-        const char *base = (const char *)a.xb + t * row_bytes;
+        // the last tile reads at most TR rows past the end, inside the
+        // allocation's slack rows; the resource stops there
+        const int64_t lim = min((int64_t)INT32_MAX, (a.n - t + TR) * (int64_t)row_bytes);
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)((const char *)a.xb + t * row_bytes), 0, (int)lim, kBufRsrcWord3);
 #pragma unroll
-        for (int j = 0; j < S::LOADS; ++j) {
-            const int i = tid + j * S::NT, row = i / S::CPR, c = i % S::CPR;
-            ra[j] = *(const u32x4_t *)(base + row * row_bytes + c * 16);
-        }
+        for (int j = 0; j < S::LOADS; ++j) ra[j] = buf_load16(rs, tid * 16, j * S::NT * 16);
         if (l2 && tid < TR / 4) rn = *(const f32x4_t *)(a.xn + t + 4 * tid);
     };
     auto lstore = [&](char *stage) __attribute__((always_inline)) {

@@ -209,7 +209,10 @@ VS_API int vs_dev_copy(int device, void *dst_dev, const void *src_dev, int64_t b
 /* Measured peaks for the "of measured achievable" fractions: what = 0 reads
  * `bytes` (>= 1 MiB, a multiple of 16) with 16-byte loads and returns GB/s;
  * what = 1 runs register-only bf16 MFMAs (v_mfma_f32_32x32x16_bf16) on
- * every CU and returns TFLOP/s.  Best of five timed runs after a warm-up. */
+ * every CU and returns TFLOP/s, on small-integer operands; what = 2 the same
+ * on random operands (random signs and mantissas, the bit activity of real
+ * data, which draws more power and lowers the sustained clock).  Best of
+ * five timed runs after a warm-up. */
 VS_API int vs_dev_probe(int device, int what, int64_t bytes, double *result);
 VS_API int vs_device_count(int *count);
 VS_API int vs_device_name(int device, char *buf, int64_t len);

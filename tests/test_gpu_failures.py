@@ -102,3 +102,22 @@ def test_range_and_kmeans_allocation_failures(vs):
     idx.close()
     ar, _, objr = oracle.kmeans_assign(xb, cen, NT)
     assert np.array_equal(a, ar) and obj == objr
+
+
+def test_device_probes(vs):
+    """vs_dev_probe: read bandwidth (what 0), bf16 MFMA rate on small-integer
+    (1) and random (2) operands, all positive and below the published peaks
+    (8 TB/s, 2.5 PFLOP/s); other codes are rejected."""
+    import ctypes
+    from vector_store import _native as N
+
+    lib = N.load()
+    vals = {}
+    for what, nbytes in ((0, 1 << 28), (1, 0), (2, 0)):
+        v = ctypes.c_double(0.0)
+        assert lib.vs_dev_probe(0, what, nbytes, ctypes.byref(v)) == 0
+        vals[what] = v.value
+    assert 500.0 < vals[0] < 8000.0
+    assert 100.0 < vals[1] <= 2600.0 and 100.0 < vals[2] <= 2600.0
+    v = ctypes.c_double(0.0)
+    assert lib.vs_dev_probe(0, 3, 0, ctypes.byref(v)) == N.VS_ERR_INVALID
