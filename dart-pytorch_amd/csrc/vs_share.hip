@@ -151,11 +151,6 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
     float thr_r[NQB];
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb) thr_r[qb] = thr_w[qb * 16 + r16];
-    // list counts of the lane's queries (equal in its four lanes); the LDS
-    // counters are written from them only around flushes and at the end
-    int cnt_r[NQB];
-#pragma unroll
-    for (int qb = 0; qb < NQB; ++qb) cnt_r[qb] = 0;
 
     // the shared thresholds are read at the start of a tile and applied at
     // its end, when the read has long completed
@@ -262,77 +257,63 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
                     thr_r[qb] = fminf(thr_r[qb], best_r[qb] + a.kmin_margin);
                 }
             }
+            float m4[NQB];
             bool pass = false;
 #pragma unroll
             for (int qb = 0; qb < NQB; ++qb) {
-                const float m = fminf(fminf(acc[qb][0], acc[qb][1]), fminf(acc[qb][2], acc[qb][3]));
-                pass |= m < thr_r[qb];
+                m4[qb] = fminf(fminf(acc[qb][0], acc[qb][1]), fminf(acc[qb][2], acc[qb][3]));
+                pass |= m4[qb] < thr_r[qb];
             }
             if (!__ballot(pass)) return;
-            // make room: a query gains at most 16 entries per row block
+            // make room: a list that may gain entries here (at most 16: four
+            // lanes of four rows) and holds more than cap - 16 is cut first
+            // (k-means lists are marked full instead, count cap + 1: their
+            // points go to the exhaustive search).  The counts live in LDS;
+            // only lanes with a passing value read them.
             {
                 bool need = false;
 #pragma unroll
-                for (int qb = 0; qb < NQB; ++qb) need |= cnt_r[qb] > a.cap - 16;
-                if (KMIN && __ballot(need)) {
-                    // a full list takes no more entries and is marked (count
-                    // cap + 1): its points go to the exhaustive search
+                for (int qb = 0; qb < NQB; ++qb)
+                    if (m4[qb] < thr_r[qb]) need |= cnt_w[qb * 16 + r16] > a.cap - 16;
+                if (__ballot(need)) {
+                    if constexpr (KMIN) {
 #pragma unroll
-                    for (int qb = 0; qb < NQB; ++qb)
-                        if (cnt_r[qb] > a.cap - 16) {
-                            cnt_r[qb] = a.cap + 1;
-                            thr_r[qb] = -VS_INF;
+                        for (int qb = 0; qb < NQB; ++qb) {
+                            const int q = qb * 16 + r16;
+                            if (cnt_w[q] > a.cap - 16) {
+                                thr_r[qb] = -VS_INF;
+                                if (g == 0) cnt_w[q] = a.cap + 1;
+                            }
                         }
-                } else if (__ballot(need)) {
-                    if (g == 0) {
+                    } else {
+                        lds_wave_sync();
+                        for (int q = 0; q < BNW; ++q) {
+                            if (cnt_w[q] > a.cap - 16)
+                                flush_list(cv + (int64_t)(qw + q) * a.cap,
+                                           ci + (int64_t)(qw + q) * a.cap, &cnt_w[q], &thr_w[q],
+                                           &thr_w[q], S::BN, 1, &a.gthr[q0 + qw + q], sv_w, si_w,
+                                           a.cap, a.kk, a.kk_final, 0, lane);
+                        }
+                        lds_wave_sync();
 #pragma unroll
-                        for (int qb = 0; qb < NQB; ++qb) cnt_w[qb * 16 + r16] = cnt_r[qb];
+                        for (int qb = 0; qb < NQB; ++qb)
+                            thr_r[qb] = fminf(thr_r[qb], thr_w[qb * 16 + r16]);
                     }
                     lds_wave_sync();
-                    for (int q = 0; q < BNW; ++q) {
-                        if (cnt_w[q] > a.cap - 16)
-                            flush_list(cv + (int64_t)(qw + q) * a.cap, ci + (int64_t)(qw + q) * a.cap,
-                                       &cnt_w[q], &thr_w[q], &thr_w[q], S::BN, 1,
-                                       &a.gthr[q0 + qw + q], sv_w, si_w, a.cap, a.kk, a.kk_final, 0,
-                                       lane);
-                    }
-                    lds_wave_sync();
-#pragma unroll
-                    for (int qb = 0; qb < NQB; ++qb) {
-                        cnt_r[qb] = cnt_w[qb * 16 + r16];
-                        thr_r[qb] = fminf(thr_r[qb], thr_w[qb * 16 + r16]);
-                    }
                 }
             }
-            // append positions: the four lanes of a query (rows r16, r16 +
-            // 16, r16 + 32, r16 + 48 of the wave) take consecutive slots in
-            // lane-row order.  Each lane's counts of its query blocks are
-            // packed one per byte (at most 4 each, 16 per query), and two
-            // cross-row swaps give every lane the sum of the lower rows'
-            // counts and the total.
-            uint32_t cpk = 0;
+            // appends: each lane with passing values reserves its slots with
+            // one LDS atomic on its query's count (passing values are rare:
+            // most query blocks of a row block have none)
 #pragma unroll
             for (int qb = 0; qb < NQB; ++qb) {
-                uint32_t c = 0;
+                if (!__ballot(m4[qb] < thr_r[qb])) continue;
+                int c = 0;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) c += acc[qb][i] < thr_r[qb] ? 1u : 0u;
-                cpk |= c << (8 * qb);
-            }
-            // s1: rows 2j and 2j + 1 both see row 2j's value in [0] and row
-            // 2j + 1's in [1]; s2 likewise for the halves of the wave
-            const auto s1 = __builtin_amdgcn_permlane16_swap(cpk, cpk, false, false);
-            const uint32_t pair = s1[0] + s1[1];
-            const auto s2 = __builtin_amdgcn_permlane32_swap(pair, pair, false, false);
-            const uint32_t below = ((g & 1) ? s1[0] : 0u) + ((g & 2) ? s2[0] : 0u);
-            const uint32_t total = s2[0] + s2[1];
-#pragma unroll
-            for (int qb = 0; qb < NQB; ++qb) {
-                const int c = (cpk >> (8 * qb)) & 0xff;
-                int pos = cnt_r[qb] + (int)((below >> (8 * qb)) & 0xff);
-                cnt_r[qb] += (int)((total >> (8 * qb)) & 0xff);
-                if (!__ballot(c > 0)) continue;
+                for (int i = 0; i < 4; ++i) c += acc[qb][i] < thr_r[qb] ? 1 : 0;
                 if (c > 0) {
                     const int q = qw + qb * 16 + r16;
+                    int pos = atomicAdd(&cnt_w[qb * 16 + r16], c);
                     float *cvq = cv + (int64_t)q * a.cap;
                     int32_t *ciq = ci + (int64_t)q * a.cap;
 #pragma unroll
@@ -345,6 +326,7 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
                     }
                 }
             }
+            lds_wave_sync();
         };
         f32x4_t accs[2][NQB];
         mma(0, accs[0]);
@@ -384,10 +366,6 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
     }
     // final: the lists' entry counts for the merge (which filters by the
     // final shared threshold and keeps the kk_final best itself)
-    if (g == 0) {
-#pragma unroll
-        for (int qb = 0; qb < NQB; ++qb) cnt_w[qb * 16 + r16] = cnt_r[qb];
-    }
     wave_sync();
     if (a.list_cnt) {
         // counts, and the largest one (after all lists, for the merge)
