@@ -169,6 +169,7 @@ struct VsOptions {
     int copy16 = 1;        // the one-pass selection reads a bf16 copy of the fp32 rows
     int guess = 1;         // large batches: estimated thresholds from a row sample
     int prepass = 1;       // small batches: threshold seeding pre-pass
+    int prepass_log2 = 16; // the pre-pass sample: at least 2^prepass_log2 rows
     int scan_kkw = 0;      // >0: per-list keep forced down to this (tests of the verification)
     int scan_nw8 = 0;      // streaming scan: eight waves per workgroup where it fits
     int km16 = 1;          // k-means: the scan reads a bf16 copy of the centroids
@@ -861,10 +862,17 @@ int seed_thresholds(vs_index *x, const vs::PreparedQueries &pq, int64_t S, int64
     // the estimate is larger, never smaller)
     if (pp.kind == 3 && seed_rank > 0 && seed_rank <= 4 * vs::share_topm_est())
         pp.share_topm = vs::share_topm_est();
+    // the streaming scan's lists over a short sample end full: the merge
+    // reads them uncut (cutting each list at the end costs more than the
+    // merge's extra reads), and an entry a list dropped in a cut lies above
+    // that list's kk-th value, so the merged rank-r value can only be larger
+    // (still a bound, or a larger estimate)
+    if (pp.kind == 0) pp.uncut = 1;
     if ((rc = scan_fits(pp, pq))) return rc;
     const int div = kPrepassDiv;
     if (pp.kind == 0 && pp.nsplit * pp.lw >= 512 && S >= (1 << 18)) {
-        rc = seed_thresholds(x, pq, std::max<int64_t>(1 << 16, S / div), kk_final, gthr, L,
+        rc = seed_thresholds(x, pq, std::max<int64_t>((int64_t)1 << x->opt.prepass_log2, S / div),
+                             kk_final, gthr, L,
                              need_elems, need_lists, 0, -1, list_budget);
         if (rc) return rc;
     }
@@ -1089,7 +1097,8 @@ int search_device(vs_index *x, Arena &A, const void *q_dev, int q_dtype, int64_t
     const bool verify = plan.kk < plan.kk_final;
     const bool guess = !safe && needs_guess(x, plan, nq);
     const bool seed = !guess && !safe && needs_seed(x, plan) && x->opt.prepass;
-    const int64_t seed_S = std::max<int64_t>(1 << 16, x->ntotal / kPrepassDiv);
+    const int64_t seed_S =
+        std::max<int64_t>((int64_t)1 << x->opt.prepass_log2, x->ntotal / kPrepassDiv);
     // candidate lists for the scan and its pre-passes
     size_t elems = list_elems(plan), lists = list_count(plan);
     if (guess) rc = guess_thresholds(x, pq, kk, nullptr, nullptr, &elems, &lists);
@@ -2471,6 +2480,7 @@ int vs_index_set_option(vs_index *x, const char *name, int64_t value) {
         {"copy16", &VsOptions::copy16, 0, 1},
         {"guess", &VsOptions::guess, 0, 1},
         {"prepass", &VsOptions::prepass, 0, 1},
+        {"prepass_log2", &VsOptions::prepass_log2, 10, 20},
         {"scan_kkw", &VsOptions::scan_kkw, 0, 4096},
         {"scan_nw8", &VsOptions::scan_nw8, 0, 1},
         {"km16", &VsOptions::km16, 0, 1},

@@ -106,6 +106,9 @@ struct ScanPlan {
                           // running minimum + kmin_margin; a list that would fill is marked
                           // full, count cap + 1, and takes no more)
     float kmin_margin = 0.f;
+    int uncut = 0;        // streaming scan: lists are left uncut at the end and their entry
+                          // counts written to list_cnt, as the row-shared scan's (for scans
+                          // over short samples, whose lists end full)
     int merge_mu = 1;     // merge: 1024-entry chunks each workgroup loads per pass (1, 2, 4, 8;
                           // more hides load latency when few queries leave most CUs idle)
     int64_t nqblk = 0;    // query blocks

@@ -523,6 +523,20 @@ __global__ __launch_bounds__(64 * NW) void scan_kernel(ScanKArgs a) {
     }
 
     if constexpr (MODE == 0) {
+        if (a.list_cnt) {
+            // uncut lists: their entry counts (and, after all lists, the
+            // largest) for the merge, which filters and selects itself
+            wave_sync();
+            int32_t *lc = a.list_cnt + ((qblk * a.nsplit + split) * NW + wave) * (int64_t)BN;
+            int mx = 0;
+            for (int q = lane; q < BN; q += 64) {
+                lc[q] = cnt_w[q];
+                mx = max(mx, cnt_w[q]);
+            }
+            for (int o = 32; o > 0; o >>= 1) mx = max(mx, __shfl_xor(mx, o));
+            if (lane == 0) atomicMax(a.list_cnt + a.nqblk * a.nsplit * NW * BN, mx);
+            return;
+        }
         // final: every list holds its kk best in slots [0, kk), padded (one
         // lane per list when the keep fits in registers)
         if (a.kk <= 16) {
@@ -606,8 +620,9 @@ hipError_t launch_scan_topk(const void *xb, int storage, int64_t ld, const float
                             float *cand_v, int32_t *cand_i, uint32_t *gthr, float *lbound,
                             int32_t *list_cnt, hipStream_t st) {
     ScanKArgs a{};
-    a.list_cnt = plan.kind == 3 ? list_cnt : nullptr;
-    if (plan.kind == 3 && !list_cnt) return hipErrorInvalidValue;
+    const bool counted = plan.kind == 3 || (plan.kind == 0 && plan.uncut);
+    a.list_cnt = counted ? list_cnt : nullptr;
+    if (counted && !list_cnt) return hipErrorInvalidValue;
     a.xb = xb;
     a.ld = ld;
     a.xn = xn;
@@ -867,7 +882,13 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
     // of 4), MU chunks per pass with all their loads in flight at once, and
     // the buffer takes a whole pass (MU * 1024 entries) before it is cut
     const float tfinal = a.gthr ? dec_order(a.gthr[qg]) : VS_INF;
-    for (int64_t base = 0; base < total; base += 1024 * MU) {
+    // with several chunks per pass, the first pass takes a single chunk and
+    // is cut as soon as it holds 2 kk candidates: its kk-th value then
+    // filters the passes after it (lists read without a final threshold would
+    // otherwise fill the whole buffer first)
+    for (int64_t base = 0; base < total;) {
+        const bool first = base == 0 && MU > 1;
+        const int nch = first ? 1 : MU;  // chunks of this pass
         float4 v4[MU];
         int4 i4[MU];
         int nv[MU];  // valid entries of the thread's 4 (0 when past the end or the list's count)
@@ -875,7 +896,7 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
         for (int u = 0; u < MU; ++u) {
             const int64_t e = base + 1024 * u + 4 * tid;
             nv[u] = 0;
-            if (e < total) {
+            if (u < nch && e < total) {
                 const int64_t list = e / kl, j = e % kl;
                 const int64_t split = list / a.lw, w = list % a.lw;
                 const int64_t li = ((qblk * a.nsplit + split) * a.lw + w) * a.bn + q;
@@ -907,7 +928,8 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
         }
         __syncthreads();
         const int c = s_cnt;
-        if (c > MBUF - kk - 1024 * MU || (base + 1024 * MU >= total && c > 0)) {
+        base += 1024 * nch;
+        if (c > MBUF - kk - 1024 * MU || (base >= total && c > 0) || (first && c >= 2 * kk)) {
             // the kk best in any order, and the kk-th
             select_block(bv, bi, kk + c, kk, tmp_v, tmp_i, sel, &s_thr, &s_thr_id);
             if (tid == 0) s_cnt = 0;
@@ -1093,8 +1115,9 @@ hipError_t launch_merge_refine(const void *xb, int storage, int64_t ld, int64_t 
         a.vx_count = chk->vx_count;
         a.vx_list = chk->vx_list;
     }
-    a.list_cnt = plan.kind == 3 ? list_cnt : nullptr;
-    if (plan.kind == 3 && !list_cnt) return hipErrorInvalidValue;
+    const bool counted = plan.kind == 3 || (plan.kind == 0 && plan.uncut);
+    a.list_cnt = counted ? list_cnt : nullptr;
+    if (counted && !list_cnt) return hipErrorInvalidValue;
     a.xb = xb;
     a.nrows = nrows;
     a.flags = flags;
@@ -1395,8 +1418,9 @@ hipError_t launch_merge_threshold(const PreparedQueries &pq, const ScanPlan &pla
     if (seed_rank < 0 || seed_rank > plan.kk_final) return hipErrorInvalidValue;
     MergeKArgs a{};
     a.seed_rank = seed_rank;
-    a.list_cnt = plan.kind == 3 ? list_cnt : nullptr;
-    if (plan.kind == 3 && !list_cnt) return hipErrorInvalidValue;
+    const bool counted = plan.kind == 3 || (plan.kind == 0 && plan.uncut);
+    a.list_cnt = counted ? list_cnt : nullptr;
+    if (counted && !list_cnt) return hipErrorInvalidValue;
     a.ld = ld;
     a.d = 0;
     a.qf = pq.qf;
@@ -1405,6 +1429,7 @@ hipError_t launch_merge_threshold(const PreparedQueries &pq, const ScanPlan &pla
     a.lw = plan.lw;
     a.kk = plan.kk_final;
     a.kl = a.list_cnt ? plan.cap : plan.kk;
+    a.nlists_all = plan.nqblk * plan.nsplit * plan.lw * plan.bn;  // the largest count's slot
     a.cap = plan.cap;
     a.nsplit = plan.nsplit;
     a.cand_v = cand_v;
