@@ -10,6 +10,7 @@
 #include <mutex>
 #include <numeric>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/vs_hip.h"
@@ -1888,7 +1889,14 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     DeviceGuard g(x->device);
     Arena A;
     const int64_t n = x->ntotal, d = x->d, ld = x->ld;
-    std::vector<float> cen_in(centroids_in, centroids_in + K * d);  // centroids_out may alias
+    // the input centroids are read again at the end (empty clusters); a copy
+    // only when the output may overwrite them first
+    const size_t cbytes = (size_t)K * d * 4;
+    const bool alias = (const char *)centroids_out < (const char *)centroids_in + cbytes &&
+                       (const char *)centroids_in < (const char *)centroids_out + cbytes;
+    std::vector<float> cen_copy;
+    if (alias) cen_copy.assign(centroids_in, centroids_in + K * d);
+    const float *cen_in = alias ? cen_copy.data() : centroids_in;
 
     // centroid storage: fp32 rows of ld, slack rows zero, plus norms
     VS_HIP(x->km_cen.ensure((size_t)(K + kRowSlack) * ld * 4), "centroid storage");
@@ -1896,7 +1904,7 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     VS_HIP(hipMemsetAsync(x->km_cen.p, 0, (size_t)(K + kRowSlack) * ld * 4, x->st), "clear");
     VS_HIP(hipMemsetAsync(x->km_cxn.p, 0, (size_t)(K + kRowSlack) * 4, x->st), "clear");
     VS_HIP(x->stage.ensure((size_t)K * d * 4), "centroid staging");
-    VS_HIP(hipMemcpyAsync(x->stage.p, cen_in.data(), (size_t)K * d * 4, hipMemcpyHostToDevice,
+    VS_HIP(hipMemcpyAsync(x->stage.p, cen_in, (size_t)K * d * 4, hipMemcpyHostToDevice,
                           x->st),
            "uploading centroids");
     VS_HIP(x->flags.ensure(4), "flags");
@@ -2141,27 +2149,36 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
            "reading centroids");
     VS_HIP(hipMemcpyAsync(counts, x->km_counts.p, (size_t)K * 4, hipMemcpyDeviceToHost, x->st),
            "reading counts");
-    // objective: fp64 sum in point order (kmeans.dart:104), while the update runs
+    // objective: fp64 sum in point order (kmeans.dart:104), on a helper
+    // thread while the update runs and this thread copies the results out
+    // (a sequential sum of n values is a chain of n dependent adds)
     VS_HIP(hipEventSynchronize(ev_best), "reading distances");
-    {
-        const double *best = x->km_hbest.as<double>();
-        double o = 0.0;
-        for (int64_t i = 0; i < n; ++i) o += best[i];
-        if (obj) *obj = o;
-    }
+    double o = 0.0;
+    struct Join {
+        std::thread t;
+        ~Join() {
+            if (t.joinable()) t.join();
+        }
+    } sum_thread{std::thread([&o, best = x->km_hbest.as<double>(), n] {
+        double acc = 0.0;
+        for (int64_t i = 0; i < n; ++i) acc += best[i];
+        o = acc;
+    })};
     VS_HIP(hipStreamSynchronize(x->st_copy), "reading assignments");
-    VS_HIP(hipStreamSynchronize(x->st), "update");
     memcpy(assign, x->km_hassign.p, (size_t)n * 4);
+    VS_HIP(hipStreamSynchronize(x->st), "update");
     std::vector<float> cen_new(x->km_hcen.as<float>(), x->km_hcen.as<float>() + K * d);
     // empty clusters, in centroid order, in place (kmeans.dart:127-139): the
     // largest cluster's centroid holds its new value when it precedes c, and
     // still its old one otherwise (c itself included)
+    // (the loop changes no count, so the largest cluster -- the first of the
+    // largest count -- is the same for every empty one)
+    int64_t big = 0;
+    for (int64_t cc = 1; cc < K; ++cc)
+        if (counts[cc] > counts[big]) big = cc;
     int64_t used = 0;
     for (int64_t c = 0; c < K; ++c) {
         if (counts[c] >= min_points) continue;
-        int64_t big = 0;
-        for (int64_t cc = 1; cc < K; ++cc)
-            if (counts[cc] > counts[big]) big = cc;
         const float *src = big < c ? &cen_new[(size_t)(big * d)] : &cen_in[(size_t)(big * d)];
         for (int64_t j = 0; j < d; ++j) {
             if (used >= njitter)
@@ -2173,6 +2190,8 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
         }
     }
     memcpy(centroids_out, cen_new.data(), (size_t)K * d * 4);
+    sum_thread.t.join();
+    if (obj) *obj = o;
     return VS_OK;
 }
 

@@ -97,3 +97,34 @@ def test_kmeans_prepared_points_follow_adds(vs):
     ar3, _, or3 = oracle.kmeans_assign(x[1::2], cen, NT)
     assert np.array_equal(a3, ar3) and o3 == or3
     pts.close()
+
+
+def test_kmeans_step_in_place_buffers(vs):
+    """vs_kmeans_step with centroids_out the same buffer as centroids_in (the
+    in-place update of kmeans.dart:107-140): the same centroids as with
+    separate buffers, empty clusters included (their old centroids are read
+    after the new ones are written)."""
+    import ctypes
+    from vector_store import _native as N
+
+    g = syn.rng(9, 0)
+    a_pts = (g.standard_normal((500, 16)) * 0.1).astype(np.float32)
+    b_pts = (g.standard_normal((2000, 16)) * 0.1 + 5.0).astype(np.float32)
+    x = np.concatenate([a_pts, b_pts]).astype(np.float32)
+    far = np.full((1, 16), 1e3, np.float32)
+    cen = np.concatenate([far, x[:1] + 0.3, x[600:601] + 0.3, far * 2]).astype(np.float32)
+    u = syn.rng(9, 1).random(2 * 16)
+    pts = vs.GpuIndexFlat.l2(16, storage="f32")
+    pts.add(x)
+    _, sep, cnt_sep, obj_sep = vs.kmeans_step(pts, cen, 1, u)
+    inout = cen.copy()
+    assign = np.empty(len(x), np.int32)
+    cnt = np.empty(4, np.int32)
+    obj = ctypes.c_double(0.0)
+    p = inout.ctypes.data_as(ctypes.c_void_p)
+    N.check(pts._lib.vs_kmeans_step(pts.handle, p, 4, 1, u.ctypes.data_as(ctypes.c_void_p), u.size,
+                                    assign.ctypes.data_as(ctypes.c_void_p), p,
+                                    cnt.ctypes.data_as(ctypes.c_void_p), ctypes.byref(obj)))
+    pts.close()
+    assert np.array_equal(cnt, cnt_sep) and obj.value == obj_sep and np.sum(cnt == 0) == 2
+    assert np.array_equal(inout.view(np.uint32), sep.view(np.uint32))
