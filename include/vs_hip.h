@@ -254,11 +254,14 @@ VS_API int vs_index_sync(vs_index *idx);
  *   "copy16"      1: that selection reads a bf16 copy of the rows
  *   "guess"       1: large batches start from thresholds estimated on a row sample
  *   "prepass"     1: small batches seed their thresholds from a pre-pass
+ *   "prepass_log2" 10..20: that pre-pass scans at least 2^value rows (default 16)
  *   "scan_kkw"    >0: per-list keep forced down (exercises the list verification)
  *   "scan_nw8"    1: eight-wave streaming scan where it fits
  *   "km16"        1: the k-means assign reads a bf16 copy of the centroids
  *   "km16_rt"     2 or 4: 16-row blocks per tile of that scan
  *   "pick_order"  1: the k-means pick walks the points grouped by the last step's clusters
+ *   "merge_mu"    1, 2, 4 or 8: 1,024-entry list chunks the merge reads per pass (0: by
+ *                 batch size)
  *   "fail_alloc"  n > 0: the n-th device allocation of any index from now on, on
  *                 this thread, fails as VS_ERR_OOM (failure-path tests; 0 clears it)
  * Unknown names and out-of-range values: VS_ERR_INVALID. */
