@@ -178,6 +178,7 @@ struct VsOptions {
     int pick_order = 1;    // k-means: the pick walks points grouped by the last step's clusters
     int merge_mu = 0;      // merge: 1024-entry chunks per workgroup pass (0: by batch size; 1, 2,
                            // 4 or 8)
+    int merge_g = 0;       // merge: workgroups per query (0: by batch size; 1: one; 2..64: split)
 };
 
 struct vs_index {
@@ -617,15 +618,9 @@ bool plan_gemm(const vs_index *x, int64_t nq, int64_t nrows, int planes, int sto
 // use fewer, so that their short sample still spreads over every CU)
 // list_budget > 0: the candidate lists may take at most this many bytes
 // (streaming scan only; its split count shrinks to fit).
-int plan_scan(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t kk_final,
-              int storage, vs::ScanPlan *p, bool safe = false, int64_t max_lists = 0,
-              bool range = false, int min_tiles = 8, size_t list_budget = 0) {
-    // the merge runs one workgroup per query: a batch that leaves most CUs
-    // idle reads more chunks per pass (more loads in flight per workgroup)
-    int mu = x->opt.merge_mu;
-    if (!mu) mu = nq <= x->num_cu ? 8 : nq <= 4 * x->num_cu ? 4 : 1;
-    while (mu > 1 && vs::merge_lds_bytes(x->ld, mu) > x->lds_max) mu >>= 1;
-    p->merge_mu = mu;
+int plan_scan_core(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t kk_final,
+                   int storage, vs::ScanPlan *p, bool safe, int64_t max_lists, bool range,
+                   int min_tiles, size_t list_budget) {
     int64_t kk = kk_final <= 32 ? kk_final : kk_final / 4;
     const int kkw = x->opt.scan_kkw;
     if (kkw > 0) kk = std::min<int64_t>(kk_final, std::max<int64_t>(4, next_pow2(kkw)));
@@ -687,6 +682,35 @@ int plan_scan(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t 
     p->rows_per_split = rps;
     p->nsplit = std::max<int64_t>(1, (nrows + rps - 1) / rps);
     return VS_OK;
+}
+
+// The merge's shape.  One workgroup per query reads the query's lists in
+// passes of merge_mu 1024-entry chunks: a batch that leaves most CUs idle
+// reads more chunks per pass (more loads in flight per workgroup), and, when
+// the queries are fewer than half the CUs' worth of workgroups, splits each
+// query's entries over merge_g workgroups (>= 1024 entries each, at most 64)
+// whose kk_final best pairs a second pass merges.
+void plan_merge(const vs_index *x, int64_t nq, vs::ScanPlan *p) {
+    int mu = x->opt.merge_mu;
+    if (!mu) mu = nq <= x->num_cu ? 8 : nq <= 4 * x->num_cu ? 4 : 1;
+    while (mu > 1 && vs::merge_lds_bytes(x->ld, mu) > x->lds_max) mu >>= 1;
+    p->merge_mu = mu;
+    int64_t g = x->opt.merge_g;
+    if (!g) {
+        const int64_t entries = p->nsplit * p->lw * p->kk;  // the fewest a query's lists hold
+        g = 2 * (int64_t)x->num_cu / std::max<int64_t>(1, nq);
+        g = g < 4 ? 1 : std::min<int64_t>({g, 64, entries / 1024});
+    }
+    p->merge_g = (int)std::max<int64_t>(1, g);
+}
+
+int plan_scan(const vs_index *x, int64_t nq, int64_t nrows, int planes, int64_t kk_final,
+              int storage, vs::ScanPlan *p, bool safe = false, int64_t max_lists = 0,
+              bool range = false, int min_tiles = 8, size_t list_budget = 0) {
+    const int rc = plan_scan_core(x, nq, nrows, planes, kk_final, storage, p, safe, max_lists,
+                                  range, min_tiles, list_budget);
+    if (rc == VS_OK) plan_merge(x, nq, p);
+    return rc;
 }
 
 // Device scratch of one call.  Ordinary calls use the index's grow-on-demand
@@ -757,19 +781,31 @@ int scan_fits(const vs::ScanPlan &plan, const vs::PreparedQueries &pq) {
 // (device memory, `stride` elements apart); *flags_out receives the query
 // flags (non-finite, not bf16).  The planes and copies go to qp / qf / qnorm
 // (the index's buffers) or, in a fixed arena, to fresh pieces of it.
+// defer_flags (a zeroed device word) for bf16 queries: their plane count is
+// one whatever the values, so the flags go to that word, to be read with the
+// results, and nothing waits here (a row with a non-finite value is prepared
+// as the unit vector e_0, so that the search runs on finite values).
 int prepare_queries(vs_index *x, Arena &A, const void *q_dev, int q_dtype, int64_t stride,
                     int64_t nq, vs::PreparedQueries *pq, uint32_t *flags_out, DevBuf &qp,
-                    DevBuf &qf, DevBuf &qnorm) {
+                    DevBuf &qf, DevBuf &qnorm, uint32_t *defer_flags = nullptr) {
     pq->nq = nq;
     pq->nq_pad = query_pad(nq);
     void *p_qp, *p_qf, *p_qn, *p_fl;
     VS_TAKE(A.get(qp, (size_t)pq->nq_pad * 2 * x->ld * 2, &p_qp, "query planes"));
     VS_TAKE(A.get(qf, (size_t)std::max<int64_t>(nq, 1) * x->d * 4, &p_qf, "query copy"));
     VS_TAKE(A.get(qnorm, (size_t)pq->nq_pad * 4, &p_qn, "query norms"));
-    VS_TAKE(A.get(x->flags, sizeof(uint32_t), &p_fl, "flags buffer"));
     pq->qp = (uint16_t *)p_qp;
     pq->qf = (float *)p_qf;
     pq->qnorm = (float *)p_qn;
+    if (defer_flags && q_dtype == VS_DTYPE_BF16) {
+        VS_HIP(vs::launch_prepare_queries(q_dev, q_dtype, stride, nq, x->d, x->ld, x->metric, *pq,
+                                          defer_flags, x->st),
+               "preparing queries");
+        pq->planes = 1;
+        if (flags_out) *flags_out = 0;
+        return VS_OK;
+    }
+    VS_TAKE(A.get(x->flags, sizeof(uint32_t), &p_fl, "flags buffer"));
     VS_HIP(vs::launch_fill32(p_fl, 1, 0u, x->st), "clearing flags");
     VS_HIP(vs::launch_prepare_queries(q_dev, q_dtype, stride, nq, x->d, x->ld, x->metric, *pq,
                                       (uint32_t *)p_fl, x->st),
@@ -784,9 +820,10 @@ int prepare_queries(vs_index *x, Arena &A, const void *q_dev, int q_dtype, int64
 }
 
 int prepare_queries(vs_index *x, Arena &A, const void *q_dev, int q_dtype, int64_t stride,
-                    int64_t nq, vs::PreparedQueries *pq, uint32_t *flags_out) {
+                    int64_t nq, vs::PreparedQueries *pq, uint32_t *flags_out,
+                    uint32_t *defer_flags = nullptr) {
     return prepare_queries(x, A, q_dev, q_dtype, stride, nq, pq, flags_out, x->qp, x->qf,
-                           x->qnorm);
+                           x->qnorm, defer_flags);
 }
 
 __global__ void fill_sentinels_kernel(float *D, int32_t *I, int64_t m, float v) {
@@ -807,10 +844,12 @@ struct ListBufs {
     size_t elems = 0, lists = 0;
 };
 
-size_t list_elems(const vs::ScanPlan &p) {
-    return (size_t)p.nqblk * p.nsplit * p.lw * p.bn * p.cap;
-}
 size_t list_count(const vs::ScanPlan &p) { return (size_t)p.nqblk * p.nsplit * p.lw * p.bn; }
+// the lists, then the split merge's partial area
+size_t list_elems(const vs::ScanPlan &p) {
+    const size_t part = p.merge_g > 1 ? (size_t)p.nqblk * p.bn * p.merge_g * p.kk_final : 0;
+    return list_count(p) * p.cap + part;
+}
 
 int take_lists(vs_index *x, Arena &A, size_t elems, size_t lists, ListBufs *L) {
     void *pv, *pi, *pc;
@@ -895,6 +934,8 @@ int seed_thresholds(vs_index *x, const vs::PreparedQueries &pq, int64_t S, int64
     VS_HIP(vs::launch_merge_threshold(pq, pp, L->v, L->i, gthr, x->ld, seed_rank, L->cnt, x->st),
            "seeding threshold");
     if (prof) x->prof["prepass_scans"].launches++;
+    if (prof && pp.merge_g > 1 && !(seed_rank > 0 && seed_rank <= 64))
+        x->prof["split_merges"].launches++;
     return VS_OK;
 }
 
@@ -1080,10 +1121,17 @@ int search_device(vs_index *x, Arena &A, const void *q_dev, int q_dtype, int64_t
         VS_HIP(hipStreamSynchronize(x->st), "search");
         return VS_OK;
     }
-    vs::PreparedQueries pq;
-    int rc = prepare_queries(x, A, q_dev, q_dtype, x->d, nq, &pq, nullptr);
-    if (rc) return rc;
     const int64_t kk = std::max<int64_t>(8, next_pow2(k + std::max<int64_t>(4, k / 4)));
+    // control words: merge flags, the counts of the two lists, then the
+    // query flags of bf16 queries (read with the results)
+    void *p_ctl;
+    VS_TAKE(A.get(x->ctl, 4 * sizeof(int32_t), &p_ctl, "control words"));
+    int32_t *ctl = (int32_t *)p_ctl;
+    VS_HIP(vs::launch_fill32(ctl, 4, 0u, x->st), "control words");
+    vs::PreparedQueries pq;
+    int rc = prepare_queries(x, A, q_dev, q_dtype, x->d, nq, &pq, nullptr,
+                             kk <= 512 ? (uint32_t *)(ctl + 3) : nullptr);
+    if (rc) return rc;
     if (kk > 512) {  // beyond the fused selection: the sorting path
         rc = exact_search(x, A, pq.qf, nq, k, D, I);
         if (rc) return rc;
@@ -1107,17 +1155,13 @@ int search_device(vs_index *x, Arena &A, const void *q_dev, int q_dtype, int64_t
     if (rc) return rc;
     ListBufs L;
     VS_TAKE(take_lists(x, A, elems, lists, &L));
-    void *p_gthr, *p_lb = nullptr, *p_vf, *p_vx, *p_ctl;
+    void *p_gthr, *p_lb = nullptr, *p_vf, *p_vx;
     VS_TAKE(A.get(x->gthr, (size_t)pq.nq_pad * 4, &p_gthr, "shared thresholds"));
     if (verify) VS_TAKE(A.get(x->lbound, list_count(plan) * 4, &p_lb, "list bounds"));
     VS_TAKE(A.get(x->vf, (size_t)(nq + 1) * 4, &p_vf, "verification list"));
     VS_TAKE(A.get(x->vx, (size_t)(nq + 1) * 4, &p_vx, "exactness list"));
-    // control words: flags, then the counts of the two lists
-    VS_TAKE(A.get(x->ctl, 4 * sizeof(int32_t), &p_ctl, "control words"));
-    int32_t *ctl = (int32_t *)p_ctl;
     uint32_t *gthr = (uint32_t *)p_gthr;
     VS_HIP(vs::launch_fill32(gthr, pq.nq_pad, vs::kGthrInit, x->st), "shared thresholds");
-    VS_HIP(vs::launch_fill32(ctl, 4, 0u, x->st), "control words");
     // Small batches over many rows make many short lists, each warming up on
     // its own (every list must fill kk entries before its threshold means
     // anything).  Seeding the shared thresholds from samples first (see
@@ -1148,9 +1192,12 @@ int search_device(vs_index *x, Arena &A, const void *q_dev, int q_dtype, int64_t
                                        x->st),
                "merge kernel");
     }
+    if (!x->prof_fixed && plan.merge_g > 1) x->prof["split_merges"].launches++;
     int32_t hc[4] = {0, 0, 0, 0};
     VS_HIP(hipMemcpyAsync(hc, ctl, sizeof hc, hipMemcpyDeviceToHost, x->st), "merge flags");
     VS_HIP(hipStreamSynchronize(x->st), "search");
+    if ((uint32_t)hc[3] & vs::kFlagNonFinite)
+        return set_err(VS_ERR_NONFINITE, "queries contain NaN or infinity");
     if ((uint32_t)hc[0] & vs::kFlagBadId)
         return set_err(VS_ERR_HIP, "internal error: a candidate id outside the index reached the merge");
     // queries whose shortened lists may have dropped a winner, or whose
@@ -2506,6 +2553,7 @@ int vs_index_set_option(vs_index *x, const char *name, int64_t value) {
         {"km16_rt", &VsOptions::km16_rt, 2, 4},
         {"pick_order", &VsOptions::pick_order, 0, 1},
         {"merge_mu", &VsOptions::merge_mu, 0, 8},
+        {"merge_g", &VsOptions::merge_g, 0, 64},
     };
     if (strcmp(name, "fail_alloc") == 0) {  // not a planner option: this thread's countdown
         if (value < 0) return set_err(VS_ERR_INVALID, "option fail_alloc: value %lld < 0", (long long)value);

@@ -111,6 +111,10 @@ struct ScanPlan {
                           // over short samples, whose lists end full)
     int merge_mu = 1;     // merge: 1024-entry chunks each workgroup loads per pass (1, 2, 4, 8;
                           // more hides load latency when few queries leave most CUs idle)
+    int merge_g = 1;      // merge: workgroups per query.  > 1: each reduces a slice of the
+                          // query's lists to its kk_final best pairs, written to a partial
+                          // area right after the lists ([nqblk bn][merge_g][kk_final]), and
+                          // a second pass merges those (small batches over many lists)
     int64_t nqblk = 0;    // query blocks
     int64_t nsplit = 0;   // database splits
     int64_t rows_per_split = 0;
@@ -146,10 +150,11 @@ struct TopkCheck {
 // Queries the merge cannot prove exact are appended to vf_list (count in
 // *vf_count): lists shortened below kk_final (lbound non-null) or, when
 // guess != 0, fewer than kk_final candidates found below an estimated
-// threshold.
+// threshold.  With plan.merge_g > 1 the buffers continue past the lists with
+// the partial area (nqblk bn merge_g kk_final entries), which it overwrites.
 hipError_t launch_merge_refine(const void *xb, int storage, int64_t ld, int64_t d, int metric,
                                const PreparedQueries &pq, const ScanPlan &plan,
-                               const float *cand_v, const int32_t *cand_i, const uint32_t *gthr,
+                               float *cand_v, int32_t *cand_i, const uint32_t *gthr,
                                const float *lbound, int32_t *vf_count, int32_t *vf_list,
                                int64_t k, float *D, int32_t *I, int64_t nrows, uint32_t *flags,
                                int guess, const int32_t *list_cnt, const TopkCheck *chk,
@@ -193,9 +198,10 @@ hipError_t exact_sort_topk(const void *xb, int storage, int64_t ld, int64_t d, i
 
 // Threshold seeding from a pre-pass scan: every query's shared threshold
 // (gthr) is tightened to one code above the seed_rank-th (0: kk_final-th)
-// smallest accumulator value its lists hold.
+// smallest accumulator value its lists hold (partial area as for
+// launch_merge_refine).
 hipError_t launch_merge_threshold(const PreparedQueries &pq, const ScanPlan &plan,
-                                  const float *cand_v, const int32_t *cand_i, uint32_t *gthr,
+                                  float *cand_v, int32_t *cand_i, uint32_t *gthr,
                                   int64_t ld, int seed_rank, const int32_t *list_cnt,
                                   hipStream_t st);
 

@@ -138,6 +138,17 @@ __global__ __launch_bounds__(256) void prep_queries_kernel(const TS *__restrict_
         ss += __shfl_xor(ss, o);
         f |= __shfl_xor(f, o);
     }
+    if (f & kFlagNonFinite) {
+        // the row is prepared as the unit vector e_0 instead: the call reports
+        // the flag, and the kernels after this one only ever see finite values
+        // (f is the same in every lane)
+        for (int64_t j = lane; j < ld; j += 64) {
+            if (j < d) qf[row * d + j] = j == 0 ? 1.0f : 0.0f;
+            qp[(row * 2 + 0) * ld + j] = j == 0 ? f32_to_bf16_rne(scale) : (uint16_t)0;
+            qp[(row * 2 + 1) * ld + j] = 0;
+        }
+        ss = 1.0;
+    }
     if (lane == 0) {
         if (valid) qnorm[row] = (float)sqrt(ss);
         // one atomic per new bit: rows of the same data set the same bits, and
@@ -703,6 +714,17 @@ struct MergeKArgs {
     const int32_t *list_cnt;  // per-list entry counts (kl = list capacity), or null; the
                               // largest count follows them, at list_cnt[lists in the scan]
     int64_t nlists_all;       // lists in the scan (index of the largest count)
+    // split merge, first pass: part_g workgroups per query, each reducing a
+    // slice of the query's list entries to its kk best pairs, written to
+    // part_v / part_i [nq][part_g][part_cap] (sentinels +inf, -1); null in
+    // every other pass
+    int part_g, part_cap;
+    float *part_v;
+    int32_t *part_i;
+    // layout of the lists lbound belongs to (the scan's, also when the
+    // lists read are a split merge's partial area)
+    int64_t lb_nsplit;
+    int lb_lw, lb_bn;
     int32_t *vf_count;    // queries whose lists may have dropped a winner
     int32_t *vf_list;
     int guess;            // thresholds were estimated: flag queries left short
@@ -740,12 +762,12 @@ constexpr int kMergeKeepMax = 512;  // kk_final of this build is at most 512
 // key and, in *rank_out, its rank among the entries with exactly that key.
 struct SelScratch {
     int hist[4][256];
-    int bin, below, n_lt, n_eq;
+    int bin, below, eq, n_lt, n_eq, max_id;
 };
 
 template <typename KeyF, typename PredF>
 __device__ uint32_t radix_select_block(int n, int rank, KeyF key, PredF pred, SelScratch &ss,
-                                       int *rank_out) {
+                                       int *rank_out, int *eq_out = nullptr) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     uint32_t prefix = 0, mask = 0;
     for (int shift = 24; shift >= 0; shift -= 8) {
@@ -777,6 +799,7 @@ __device__ uint32_t radix_select_block(int n, int rank, KeyF key, PredF pred, Se
                     if (cum + c[u] >= rank) {
                         ss.bin = 4 * lane + u;
                         ss.below = cum;
+                        ss.eq = c[u];  // last round: the entries with exactly the key
                         break;
                     }
                     cum += c[u];
@@ -789,6 +812,7 @@ __device__ uint32_t radix_select_block(int n, int rank, KeyF key, PredF pred, Se
         mask |= 0xFFu << shift;
     }
     *rank_out = rank;
+    if (eq_out) *eq_out = ss.eq;
     return prefix;
 }
 
@@ -800,18 +824,25 @@ __device__ uint32_t radix_select_block(int n, int rank, KeyF key, PredF pred, Se
 __device__ void select_block(float *sv, int *si, int n, int kk, float *tmp_v, int *tmp_i,
                              SelScratch &ss, float *kth_v, int *kth_i) {
     const int tid = threadIdx.x;
-    int need = 0, unused = 0;
+    int need = 0, unused = 0, eq = 0;
     const uint32_t T = radix_select_block(
-        n, kk, [&](int t) { return enc_order(sv[t]); }, [](int) { return true; }, ss, &need);
-    const uint32_t I = radix_select_block(
-        n, need, [&](int t) { return (uint32_t)si[t]; },
-        [&](int t) { return enc_order(sv[t]) == T; }, ss, &unused);
+        n, kk, [&](int t) { return enc_order(sv[t]); }, [](int) { return true; }, ss, &need, &eq);
+    // the pairs tied at the pivot code are all taken when need of them tie
+    // (the usual case): the kk-th pair is then the tied one with the largest
+    // id, found while they are copied, and the selection on ids is skipped
+    const bool all_eq = eq == need;
+    const uint32_t I =
+        all_eq ? 0xFFFFFFFFu
+               : radix_select_block(
+                     n, need, [&](int t) { return (uint32_t)si[t]; },
+                     [&](int t) { return enc_order(sv[t]) == T; }, ss, &unused);
     // kk - need pairs lie strictly below the pivot code and take slots
     // [0, kk - need); the tied ones take the rest, at most need of them (equal
     // sentinels can tie beyond need)
     if (tid == 0) {
         ss.n_lt = 0;
         ss.n_eq = 0;
+        ss.max_id = 0;
     }
     __syncthreads();
     for (int t = tid; t < n; t += 256) {
@@ -822,6 +853,7 @@ __device__ void select_block(float *sv, int *si, int n, int kk, float *tmp_v, in
         } else if (c == T && (uint32_t)si[t] <= I) {
             const int q = atomicAdd(&ss.n_eq, 1);
             if (q < need) p = kk - need + q;
+            if (all_eq) atomicMax(&ss.max_id, si[t]);
         }
         if (p >= 0) {
             tmp_v[p] = sv[t];
@@ -835,7 +867,7 @@ __device__ void select_block(float *sv, int *si, int n, int kk, float *tmp_v, in
     }
     if (tid == 0) {
         *kth_v = dec_order(T);
-        *kth_i = (int)I;
+        *kth_i = all_eq ? ss.max_id : (int)I;
     }
     __syncthreads();
 }
@@ -854,7 +886,8 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
     __shared__ float s_thr;
     __shared__ int s_thr_id;
 
-    const int64_t qg = blockIdx.x;
+    const bool part = a.part_v != nullptr;
+    const int64_t qg = part ? blockIdx.x / a.part_g : blockIdx.x;
     const int tid = threadIdx.x;
     const int kk = a.kk;
     // counted lists: only the longest list's fill (rounded up to whole
@@ -863,6 +896,15 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
     const int64_t qblk = qg / a.bn, q = qg % a.bn;
     const int64_t nlists = a.nsplit * a.lw;
     const int64_t total = nlists * kl;
+    // the entries this workgroup visits: all of them, or (split merge) one
+    // slice of whole 4-entry groups (kl is a multiple of 4, so a group never
+    // straddles two lists)
+    int64_t lo = 0, hi = total;
+    if (part) {
+        const int64_t per = ((total + a.part_g - 1) / a.part_g + 3) & ~(int64_t)3;
+        lo = min(total, (int64_t)(blockIdx.x % a.part_g) * per);
+        hi = min(total, lo + per);
+    }
 
     for (int t = tid; t < kk; t += 256) {
         bv[t] = VS_INF;
@@ -873,7 +915,8 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
         s_thr = VS_INF;
         s_thr_id = INT_MAX;
     }
-    for (int64_t j = tid; j < a.ld; j += 256) qsh[j] = j < a.d ? a.qf[qg * a.d + j] : 0.0f;
+    if (!part)
+        for (int64_t j = tid; j < a.ld; j += 256) qsh[j] = j < a.d ? a.qf[qg * a.d + j] : 0.0f;
     __syncthreads();
 
     // entries above the query's final shared threshold cannot be among the
@@ -886,8 +929,8 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
     // is cut as soon as it holds 2 kk candidates: its kk-th value then
     // filters the passes after it (lists read without a final threshold would
     // otherwise fill the whole buffer first)
-    for (int64_t base = 0; base < total;) {
-        const bool first = base == 0 && MU > 1;
+    for (int64_t base = lo; base < hi;) {
+        const bool first = base == lo && MU > 1;
         const int nch = first ? 1 : MU;  // chunks of this pass
         float4 v4[MU];
         int4 i4[MU];
@@ -896,7 +939,7 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
         for (int u = 0; u < MU; ++u) {
             const int64_t e = base + 1024 * u + 4 * tid;
             nv[u] = 0;
-            if (u < nch && e < total) {
+            if (u < nch && e < hi) {
                 const int64_t list = e / kl, j = e % kl;
                 const int64_t split = list / a.lw, w = list % a.lw;
                 const int64_t li = ((qblk * a.nsplit + split) * a.lw + w) * a.bn + q;
@@ -929,12 +972,24 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
         __syncthreads();
         const int c = s_cnt;
         base += 1024 * nch;
-        if (c > MBUF - kk - 1024 * MU || (base >= total && c > 0) || (first && c >= 2 * kk)) {
+        if (c > MBUF - kk - 1024 * MU || (base >= hi && c > 0) || (first && c >= 2 * kk)) {
             // the kk best in any order, and the kk-th
             select_block(bv, bi, kk + c, kk, tmp_v, tmp_i, sel, &s_thr, &s_thr_id);
             if (tid == 0) s_cnt = 0;
         }
         __syncthreads();
+    }
+
+    if (part) {
+        // the slice's kk best pairs (the kk best of the query are among the
+        // union of its slices'), for the second pass
+        const int64_t o = (int64_t)blockIdx.x * a.part_cap;
+        for (int t = tid; t < a.part_cap; t += 256) {
+            const bool ok = t < kk && bi[t] != INT_MAX;
+            a.part_v[o + t] = ok ? bv[t] : VS_INF;
+            a.part_i[o + t] = ok ? bi[t] : -1;
+        }
+        return;
     }
 
     if constexpr (MODE == 2) {
@@ -960,9 +1015,11 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
         __shared__ float s_lmin[4];
         float lmin = VS_INF;
         if (a.lbound) {
-            for (int64_t l = tid; l < nlists; l += 256) {
-                const int64_t split = l / a.lw, w = l % a.lw;
-                lmin = fminf(lmin, a.lbound[((qblk * a.nsplit + split) * a.lw + w) * a.bn + q]);
+            const int64_t lq = qg / a.lb_bn, lqq = qg % a.lb_bn;
+            for (int64_t l = tid; l < a.lb_nsplit * a.lb_lw; l += 256) {
+                const int64_t split = l / a.lb_lw, w = l % a.lb_lw;
+                lmin = fminf(lmin,
+                             a.lbound[((lq * a.lb_nsplit + split) * a.lb_lw + w) * a.lb_bn + lqq]);
             }
         }
         for (int o = 32; o > 0; o >>= 1) lmin = fminf(lmin, __shfl_xor(lmin, o));
@@ -987,6 +1044,36 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
     float a_last = 0.f;
     if constexpr (MODE == 1) a_last = s_thr;
     __syncthreads();
+    // When the survivors' rows fit in the buffer past slot kk, the whole
+    // workgroup first copies them there, every load in flight at once; each
+    // fp64 sum (sequential, in the reference's order) then reads LDS instead
+    // of making one HBM round trip per 64 elements.
+    const int row_bytes = (int)a.ld * (ST == 1 ? 2 : 4);
+    char *stage = (char *)(bv + kk);
+    const bool staged = kk * row_bytes <= (MBUF - kk) * 4;
+    if (staged) {
+        const int ppr = row_bytes / 16, np = kk * ppr;  // 16-byte pieces (ld: 64-element multiple)
+        for (int t0 = 0; t0 < np; t0 += 8 * 256) {
+            uint4 r[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int t = t0 + u * 256 + tid;
+                r[u] = make_uint4(0u, 0u, 0u, 0u);
+                if (t < np) {
+                    const int id = bi[t / ppr];
+                    if (id >= 0 && id != INT_MAX && (int64_t)id < a.nrows)
+                        r[u] = *(const uint4 *)((const char *)a.xb + (int64_t)id * row_bytes +
+                                                (t % ppr) * 16);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int t = t0 + u * 256 + tid;
+                if (t < np) *(uint4 *)(stage + t * 16) = r[u];
+            }
+        }
+        __syncthreads();
+    }
     for (int t = tid; t < kk; t += 256) {
         const int id = bi[t];
         float key = VS_INF;
@@ -994,7 +1081,8 @@ __global__ __launch_bounds__(256) void merge_refine_kernel(MergeKArgs a) {
             atomicOr(a.flags, kFlagBadId);
             bi[t] = INT_MAX;
         } else if (id != INT_MAX) {
-            const double ex = exact_score<ST>(qsh, a.xb, a.ld, id, a.d, a.metric);
+            const double ex = staged ? exact_score<ST>(qsh, stage, a.ld, t, a.d, a.metric)
+                                     : exact_score<ST>(qsh, a.xb, a.ld, id, a.d, a.metric);
             key = a.metric == 0 ? (float)ex : -(float)ex;
             if (MODE == 1 && (ex < best_ex || (ex == best_ex && id < best_id))) {
                 best_ex = ex;
@@ -1097,9 +1185,52 @@ static void (*merge_fn(int mu))(MergeKArgs) {
     }
 }
 
+// One merge pass over the lists, or (plan.merge_g > 1) the split merge's
+// two: the first reduces each slice of a query's list entries to its kk best
+// pairs, written to the partial area after the lists, and the second merges
+// those with the final mode.
+static hipError_t launch_merge_passes(void (*fn)(MergeKArgs), size_t lds, MergeKArgs a,
+                                      const ScanPlan &plan, int64_t nq, float *cand_v,
+                                      int32_t *cand_i, hipStream_t st) {
+    if (!fn) return hipErrorInvalidValue;
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute((const void *)fn,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    a.lb_nsplit = plan.nsplit;
+    a.lb_lw = plan.lw;
+    a.lb_bn = plan.bn;
+    const int g = plan.merge_g;
+    if (g <= 1) {
+        hipLaunchKernelGGL(fn, dim3((unsigned)nq), dim3(256), lds, st, a);
+        return hipGetLastError();
+    }
+    if (plan.kk_final % 4 || nq * g > INT32_MAX) return hipErrorInvalidValue;
+    const int64_t off = plan.nqblk * plan.nsplit * plan.lw * plan.bn * plan.cap;
+    MergeKArgs a1 = a;
+    a1.part_g = g;
+    a1.part_cap = plan.kk_final;
+    a1.part_v = cand_v + off;
+    a1.part_i = cand_i + off;
+    hipLaunchKernelGGL(fn, dim3((unsigned)(nq * g)), dim3(256), lds, st, a1);
+    if (hipError_t e = hipGetLastError()) return e;
+    MergeKArgs a2 = a;
+    a2.cand_v = a1.part_v;
+    a2.cand_i = a1.part_i;
+    a2.list_cnt = nullptr;
+    a2.bn = 1;
+    a2.lw = 1;
+    a2.nsplit = g;
+    a2.cap = plan.kk_final;
+    a2.kl = plan.kk_final;
+    hipLaunchKernelGGL(fn, dim3((unsigned)nq), dim3(256), lds, st, a2);
+    return hipGetLastError();
+}
+
 hipError_t launch_merge_refine(const void *xb, int storage, int64_t ld, int64_t d, int metric,
                                const PreparedQueries &pq, const ScanPlan &plan,
-                               const float *cand_v, const int32_t *cand_i, const uint32_t *gthr,
+                               float *cand_v, int32_t *cand_i, const uint32_t *gthr,
                                const float *lbound, int32_t *vf_count, int32_t *vf_list,
                                int64_t k, float *D, int32_t *I, int64_t nrows, uint32_t *flags,
                                int guess, const int32_t *list_cnt, const TopkCheck *chk,
@@ -1143,17 +1274,10 @@ hipError_t launch_merge_refine(const void *xb, int storage, int64_t ld, int64_t 
     a.k = k;
     a.D = D;
     a.I = I;
-    const size_t lds = merge_lds(ld, plan.merge_mu);
     void (*fn)(MergeKArgs) =
         storage == 1 ? merge_fn<1, 0>(plan.merge_mu) : merge_fn<0, 0>(plan.merge_mu);
-    if (!fn) return hipErrorInvalidValue;
-    if (lds > 64 * 1024) {
-        hipError_t e = hipFuncSetAttribute((const void *)fn,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-    }
-    hipLaunchKernelGGL(fn, dim3((unsigned)pq.nq), dim3(256), lds, st, a);
-    return hipGetLastError();
+    return launch_merge_passes(fn, merge_lds(ld, plan.merge_mu), a, plan, pq.nq, cand_v, cand_i,
+                               st);
 }
 
 // ---------------------------------------------------------------------------
@@ -1411,7 +1535,7 @@ __global__ __launch_bounds__(256) void merge_estimate_kernel(MergeKArgs a) {
 // Threshold seeding from a pre-pass: for every query, the kk_final-th
 // smallest accumulator value over its lists tightens its shared threshold.
 hipError_t launch_merge_threshold(const PreparedQueries &pq, const ScanPlan &plan,
-                                  const float *cand_v, const int32_t *cand_i, uint32_t *gthr,
+                                  float *cand_v, int32_t *cand_i, uint32_t *gthr,
                                   int64_t ld, int seed_rank, const int32_t *list_cnt,
                                   hipStream_t st) {
     if (pq.nq <= 0) return hipSuccess;
@@ -1440,16 +1564,8 @@ hipError_t launch_merge_threshold(const PreparedQueries &pq, const ScanPlan &pla
         merge_estimate_kernel<<<dim3((unsigned)((pq.nq + 3) / 4)), dim3(256), 0, st>>>(a);
         return hipGetLastError();
     }
-    const size_t lds = merge_lds(ld, plan.merge_mu);
-    void (*fn)(MergeKArgs) = merge_fn<1, 2>(plan.merge_mu);
-    if (!fn) return hipErrorInvalidValue;
-    if (lds > 64 * 1024) {
-        hipError_t e = hipFuncSetAttribute((const void *)fn,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-    }
-    hipLaunchKernelGGL(fn, dim3((unsigned)pq.nq), dim3(256), lds, st, a);
-    return hipGetLastError();
+    return launch_merge_passes(merge_fn<1, 2>(plan.merge_mu), merge_lds(ld, plan.merge_mu), a,
+                               plan, pq.nq, cand_v, cand_i, st);
 }
 
 hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, const float *cen,

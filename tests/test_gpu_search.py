@@ -193,6 +193,38 @@ def test_edge_cases(vs):
     idx.close()
 
 
+@pytest.mark.parametrize("nq,bad_bits", [(1, 0x7FC0), (64, 0x7F80), (300, 0xFF80)])
+def test_nonfinite_bf16_queries(vs, nq, bad_bits):
+    """bf16 queries take one MFMA plane whatever their values, so the search
+    reads their flags together with its results instead of waiting for them
+    first; meanwhile a row holding NaN or an infinity is searched as a unit
+    vector.  The call still fails with VS_ERR_NONFINITE, on the host and the
+    device entry points, and the next search is exact again."""
+    xb = syn.int_grid(300_000, 64, 13, 0)
+    q16 = syn.to_bf16_bits(syn.int_grid(nq, 64, 13, 3))
+    bad = q16.copy()
+    bad[nq // 2, 5] = bad_bits
+    idx = vs.GpuIndexFlat(64, vs.Metric.innerProduct, storage="auto")
+    idx.add(xb)
+    with pytest.raises(vs.VsError) as e:
+        idx.search(bad, 10)
+    assert e.value.code == vs._native.VS_ERR_NONFINITE
+    qd = vs._native.DeviceBuffer(bad.nbytes)
+    qd.upload(bad)
+    Dd = vs._native.DeviceBuffer(nq * 10 * 4)
+    Id = vs._native.DeviceBuffer(nq * 10 * 4)
+    with pytest.raises(vs.VsError) as e:
+        idx.search_device(qd, nq, 10, Dd, Id, dtype=vs._native.VS_DTYPE_BF16)
+    assert e.value.code == vs._native.VS_ERR_NONFINITE
+    r = idx.search(q16, 10)
+    idx.close()
+    for b in (qd, Dd, Id):
+        b.free()
+    xq = syn.bf16_bits_to_f32(q16)
+    Dr, Ir = oracle.flat_search(xb, xq, 10, 1, NT)
+    assert_knn_parity(r.distances, r.ids, Dr, Ir, 1, rtol=0.0, atol=0.0, xb=xb, xq=xq)
+
+
 def test_add_after_search_and_wrap(vs):
     """vector_store_test.dart:3607-3637: a vector added after a search is found
     at id old_ntotal; wrap() keeps the ranking."""
@@ -360,6 +392,34 @@ def test_merge_chunks_per_pass(vs, nq, k, metric):
         assert np.array_equal(r.distances, res[1].distances), mu
 
 
+@pytest.mark.parametrize("nq,k,metric", [(1, 10, 1), (5, 100, 0), (64, 10, 1), (40, 400, 0)])
+def test_split_merge(vs, nq, k, metric):
+    """A batch with fewer queries than half the CUs' worth of workgroups
+    splits each query's list entries over several merge workgroups (option
+    merge_g; 0 plans it), each keeping its slice's kk_final best pairs, and
+    a second pass merges those -- for the threshold seeding and for the
+    final merge.  Integer rows with many tied distances: every split count
+    gives the one-workgroup merge's result, equal to the oracle's."""
+    xb = syn.int_grid(300_000, 64, 13, 0)
+    xq = syn.int_grid(nq, 64, 13, 2)
+    idx = vs.GpuIndexFlat(64, vs.Metric(metric), storage="auto")
+    idx.add(xb)
+    res, nsplit = {}, {}
+    for g in (1, 2, 7, 64, 0):
+        idx.set_option("merge_g", g)
+        idx.prof_reset()
+        res[g] = idx.search(xq, k)
+        nsplit[g] = idx.prof_get("split_merges")[0]
+    idx.close()
+    assert nsplit[1] == 0 and nsplit[2] == 2 and nsplit[7] == 2 and nsplit[64] == 2
+    assert nsplit[0] == 2  # planned: these batches leave most CUs idle
+    Dr, Ir = oracle.flat_search(xb, xq, k, metric, NT)
+    for g, r in res.items():
+        assert_knn_parity(r.distances, r.ids, Dr, Ir, metric, rtol=0.0, atol=0.0, xb=xb, xq=xq)
+        assert np.array_equal(r.distances, res[1].distances), g
+        assert np.array_equal(r.ids, res[1].ids), g
+
+
 def test_estimated_threshold_too_tight_falls_back(vs):
     """A sample that is not representative: the first 1/16 of the rows holds
     64 near copies of every query, the rest lies far away.  The estimate
@@ -395,7 +455,8 @@ def test_set_option_rejects_unknown_and_out_of_range(vs):
     with pytest.raises(ValueError, match="unknown option"):
         idx.set_option("no_such_option", 1)
     for name, value in (("gemm", 2), ("km16_rt", 3), ("scan_kkw", -1), ("merge_mu", 3),
-                        ("merge_mu", 16), ("prepass_log2", 9), ("prepass_log2", 21)):
+                        ("merge_mu", 16), ("prepass_log2", 9), ("prepass_log2", 21),
+                        ("merge_g", -1), ("merge_g", 65)):
         with pytest.raises(ValueError, match="outside"):
             idx.set_option(name, value)
     idx.set_option("guess", 0)
