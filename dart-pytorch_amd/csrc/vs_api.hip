@@ -687,9 +687,11 @@ int plan_scan_core(const vs_index *x, int64_t nq, int64_t nrows, int planes, int
 // The merge's shape.  One workgroup per query reads the query's lists in
 // passes of merge_mu 1024-entry chunks: a batch that leaves most CUs idle
 // reads more chunks per pass (more loads in flight per workgroup), and, when
-// the queries are fewer than half the CUs' worth of workgroups, splits each
-// query's entries over merge_g workgroups (>= 1024 entries each, at most 64)
-// whose kk_final best pairs a second pass merges.
+// a quarter of the workgroups that fit on the CUs at once would still
+// outnumber the queries, splits each query's entries over merge_g workgroups
+// (all resident at once, >= 1024 entries each, at most 64) whose kk_final
+// best pairs a second pass merges.  Called again when the lists' kind
+// changes (uncut lists hold more entries).
 void plan_merge(const vs_index *x, int64_t nq, vs::ScanPlan *p) {
     int mu = x->opt.merge_mu;
     if (!mu) mu = nq <= x->num_cu ? 8 : nq <= 4 * x->num_cu ? 4 : 1;
@@ -697,8 +699,11 @@ void plan_merge(const vs_index *x, int64_t nq, vs::ScanPlan *p) {
     p->merge_mu = mu;
     int64_t g = x->opt.merge_g;
     if (!g) {
-        const int64_t entries = p->nsplit * p->lw * p->kk;  // the fewest a query's lists hold
-        g = 2 * (int64_t)x->num_cu / std::max<int64_t>(1, nq);
+        const bool counted = p->kind == 3 || (p->kind == 0 && p->uncut);
+        const int64_t entries = p->nsplit * p->lw * (counted ? p->cap : p->kk);
+        const int64_t per_cu = std::max<int64_t>(
+            1, (int64_t)(x->lds_max / std::max<size_t>(1, vs::merge_lds_bytes(x->ld, mu))));
+        g = (int64_t)x->num_cu * per_cu / std::max<int64_t>(1, nq);
         g = g < 4 ? 1 : std::min<int64_t>({g, 64, entries / 1024});
     }
     p->merge_g = (int)std::max<int64_t>(1, g);
@@ -907,7 +912,10 @@ int seed_thresholds(vs_index *x, const vs::PreparedQueries &pq, int64_t S, int64
     // merge's extra reads), and an entry a list dropped in a cut lies above
     // that list's kk-th value, so the merged rank-r value can only be larger
     // (still a bound, or a larger estimate)
-    if (pp.kind == 0) pp.uncut = 1;
+    if (pp.kind == 0) {
+        pp.uncut = 1;
+        plan_merge(x, pq.nq, &pp);
+    }
     if ((rc = scan_fits(pp, pq))) return rc;
     const int div = kPrepassDiv;
     if (pp.kind == 0 && pp.nsplit * pp.lw >= 512 && S >= (1 << 18)) {

@@ -297,48 +297,58 @@ __device__ __forceinline__ bool map_block_grouped(int64_t nqblk, int64_t nsplit,
 template <int ST>
 __device__ double exact_score(const float *qrow, const void *xb, int64_t ld, int64_t id,
                               int64_t d, int metric) {
-    // the row is read 64 elements at a time (one batch of independent 16-byte
-    // loads, so a candidate costs a few memory round trips, not one per 16
-    // bytes); ld is a multiple of 64 elements, so every load stays in the
-    // row.  Elements past d are zero in the row and in qrow: their terms are
-    // +0, and s (which starts at +0 and is never -0) is unchanged by them.
+    // The row and the query are read 16 elements at a time, each batch as
+    // independent 16-byte loads issued before any of them is used, so that a
+    // candidate costs one memory round trip per batch instead of one per
+    // element pair; ld is a multiple of 64 elements and qrow (16-byte
+    // aligned) holds ld values, so every load stays in bounds.  Elements past
+    // d are zero in the row and in qrow: their terms are +0, and s (which
+    // starts at +0 and is never -0) is unchanged by them.
+    constexpr int B = 16;
     double s = 0.0;
-    const int64_t dend = (d + 7) & ~(int64_t)7;
-    auto term = [&](double qv, double xv) __attribute__((always_inline)) {
-        if (metric == 0) {
-            const double diff = qv - xv;
-            s = s + diff * diff;
+    const int64_t dend = (d + B - 1) & ~(int64_t)(B - 1);
+    for (int64_t j0 = 0; j0 < dend; j0 += B) {
+        float q[B], x[B];
+#pragma unroll
+        for (int c = 0; c < B / 4; ++c) {
+            const float4 v = *(const float4 *)(qrow + j0 + 4 * c);
+            q[4 * c + 0] = v.x;
+            q[4 * c + 1] = v.y;
+            q[4 * c + 2] = v.z;
+            q[4 * c + 3] = v.w;
+        }
+        if constexpr (ST == 1) {
+            const uint16_t *xr = (const uint16_t *)xb + id * ld + j0;
+#pragma unroll
+            for (int c = 0; c < B / 8; ++c) {
+                const uint4 r = *(const uint4 *)(xr + 8 * c);
+                const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {  // element 2u is the low half
+                    x[8 * c + 2 * u] = __builtin_bit_cast(float, w[u] << 16);
+                    x[8 * c + 2 * u + 1] = __builtin_bit_cast(float, w[u] & 0xFFFF0000u);
+                }
+            }
         } else {
-            s = s + qv * xv;
-        }
-    };
-    if constexpr (ST == 1) {
-        const uint16_t *x = (const uint16_t *)xb + id * ld;
-        for (int64_t j0 = 0; j0 < dend; j0 += 64) {
-            uint4 raw[8];
+            const float *xr = (const float *)xb + id * ld + j0;
 #pragma unroll
-            for (int c = 0; c < 8; ++c) raw[c] = *(const uint4 *)(x + j0 + 8 * c);
-#pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                const uint16_t *h = (const uint16_t *)&raw[c];
-#pragma unroll
-                for (int u = 0; u < 8; ++u)
-                    term((double)qrow[j0 + 8 * c + u], (double)bf16_to_f32(h[u]));
+            for (int c = 0; c < B / 4; ++c) {
+                const float4 v = *(const float4 *)(xr + 4 * c);
+                x[4 * c + 0] = v.x;
+                x[4 * c + 1] = v.y;
+                x[4 * c + 2] = v.z;
+                x[4 * c + 3] = v.w;
             }
         }
-    } else {
-        const float *x = (const float *)xb + id * ld;
-        for (int64_t j0 = 0; j0 < dend; j0 += 64) {
-            float4 raw[16];
+        if (metric == 0) {
 #pragma unroll
-            for (int c = 0; c < 16; ++c) raw[c] = *(const float4 *)(x + j0 + 4 * c);
-#pragma unroll
-            for (int c = 0; c < 16; ++c) {
-                term((double)qrow[j0 + 4 * c + 0], (double)raw[c].x);
-                term((double)qrow[j0 + 4 * c + 1], (double)raw[c].y);
-                term((double)qrow[j0 + 4 * c + 2], (double)raw[c].z);
-                term((double)qrow[j0 + 4 * c + 3], (double)raw[c].w);
+            for (int u = 0; u < B; ++u) {
+                const double diff = (double)q[u] - (double)x[u];
+                s = s + diff * diff;
             }
+        } else {
+#pragma unroll
+            for (int u = 0; u < B; ++u) s = s + (double)q[u] * (double)x[u];
         }
     }
     return s;
