@@ -179,6 +179,7 @@ struct VsOptions {
     int merge_mu = 0;      // merge: 1024-entry chunks per workgroup pass (0: by batch size; 1, 2,
                            // 4 or 8)
     int merge_g = 0;       // merge: workgroups per query (0: by batch size; 1: one; 2..64: split)
+    int guess_div_log2 = 0;  // large batches: the estimate's sample is 1/2^this of the rows (0: 5)
 };
 
 struct vs_index {
@@ -962,10 +963,21 @@ bool needs_guess(const vs_index *x, const vs::ScanPlan &plan, int64_t nq) {
            x->ntotal >= (1 << 18) && plan.nsplit * plan.lw * plan.kk >= 4 * plan.kk_final;
 }
 
-int guess_thresholds(vs_index *x, const vs::PreparedQueries &pq, int64_t kk_final,
+// The sample is 1/2^div_log2 of the rows (option guess_div_log2, 1/32 by
+// default): a smaller one costs less to scan but leaves more candidates to
+// the full scan (about j 2^div_log2 rows per query lie below the estimate).
+// Measured on 20M x 768 bf16 at batch 1024 and 8192 (GEMM-tiled scan): 1/64
+// to 1/256 cut the pre-pass from 2.0 / 12.8 ms to 0.6-1.2 / 2.5-7.4 ms but
+// slowed the full scan by 2-5 %, about the same per step; 1/32 keeps the
+// full scan fastest.
+int guess_div_log2(const vs_index *x) {
+    return x->opt.guess_div_log2 ? x->opt.guess_div_log2 : 5;
+}
+
+int guess_thresholds(vs_index *x, const vs::PreparedQueries &pq, int64_t kk_final, int div_log2,
                      uint32_t *gthr, ListBufs *L, size_t *need_elems, size_t *need_lists) {
-    const int64_t div = 32;
-    const int64_t S = std::min<int64_t>(x->ntotal, std::max<int64_t>(4096, x->ntotal / div));
+    const int64_t S =
+        std::min<int64_t>(x->ntotal, std::max<int64_t>(4096, x->ntotal >> div_log2));
     const double lam = (double)kk_final * (double)S / (double)x->ntotal;
     const int j = (int)std::ceil(lam + 4.0 * std::sqrt(lam) + 4.0);
     const int64_t kkp = std::max<int64_t>(8, next_pow2(j));
@@ -1158,7 +1170,8 @@ int search_device(vs_index *x, Arena &A, const void *q_dev, int q_dtype, int64_t
         std::max<int64_t>((int64_t)1 << x->opt.prepass_log2, x->ntotal / kPrepassDiv);
     // candidate lists for the scan and its pre-passes
     size_t elems = list_elems(plan), lists = list_count(plan);
-    if (guess) rc = guess_thresholds(x, pq, kk, nullptr, nullptr, &elems, &lists);
+    const int gdl = guess_div_log2(x);
+    if (guess) rc = guess_thresholds(x, pq, kk, gdl, nullptr, nullptr, &elems, &lists);
     else if (seed) rc = seed_thresholds(x, pq, seed_S, kk, nullptr, nullptr, &elems, &lists, 0, -1, list_budget);
     if (rc) return rc;
     ListBufs L;
@@ -1176,7 +1189,7 @@ int search_device(vs_index *x, Arena &A, const void *q_dev, int q_dtype, int64_t
     // seed_thresholds) lets the full scan start tight; large batches start
     // from an estimate (guess_thresholds).
     size_t e0 = 0, l0 = 0;
-    if (guess) rc = guess_thresholds(x, pq, kk, gthr, &L, &e0, &l0);
+    if (guess) rc = guess_thresholds(x, pq, kk, gdl, gthr, &L, &e0, &l0);
     else if (seed) rc = seed_thresholds(x, pq, seed_S, kk, gthr, &L, &e0, &l0, 0, -1, list_budget);
     if (rc) return rc;
     if (!x->prof_fixed) note_scan_kind(x, plan);
@@ -2562,6 +2575,7 @@ int vs_index_set_option(vs_index *x, const char *name, int64_t value) {
         {"pick_order", &VsOptions::pick_order, 0, 1},
         {"merge_mu", &VsOptions::merge_mu, 0, 8},
         {"merge_g", &VsOptions::merge_g, 0, 64},
+        {"guess_div_log2", &VsOptions::guess_div_log2, 0, 10},
     };
     if (strcmp(name, "fail_alloc") == 0) {  // not a planner option: this thread's countdown
         if (value < 0) return set_err(VS_ERR_INVALID, "option fail_alloc: value %lld < 0", (long long)value);

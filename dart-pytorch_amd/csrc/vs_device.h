@@ -141,11 +141,13 @@ __device__ inline void flush_list(float *cvq, int32_t *ciq, int *cnt_q, float *t
 // does -- the same lists and thresholds as flush_list on each of those
 // lists, without visiting the lists one after another.  pad: lists of fewer
 // than kk entries are padded to kk with sentinels (the final cut, over = kk).
+// The block's lists of query q sit at thr[q + i tstride], i < nl (tstride 0:
+// bn).
 template <int KM>
 __device__ inline void cut_lists_lanes(float *cv, int32_t *ci, int *cnt_w, float *thr_w,
                                        const float *thr, int bn, int nl, uint32_t *gthr,
                                        int cap, int kk, int kk_final, int publish_block,
-                                       int over, bool pad, int lane) {
+                                       int over, bool pad, int lane, int tstride = 0) {
     wave_sync();  // every lane's appends and counts are visible
     const int q = lane;
     if (q < bn) {
@@ -214,8 +216,9 @@ __device__ inline void cut_lists_lanes(float *cv, int32_t *ci, int *cnt_w, float
             atomicMin(&gthr[q], enc_order(kth));
         } else if (publish_block) {
             const float *t0 = thr + q;
+            const int ts = tstride ? tstride : bn;
             float b = t0[0];
-            for (int i = 1; i < nl; ++i) b = fmaxf(b, t0[i * bn]);
+            for (int i = 1; i < nl; ++i) b = fmaxf(b, t0[i * ts]);
             if (b < VS_INF) atomicMin(&gthr[q], enc_order(b));
         }
     }

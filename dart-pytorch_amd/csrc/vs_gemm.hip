@@ -123,18 +123,37 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[QB][RB], const Sca
         if (!seeded && lim == 32 * RB) {
             // First tile: instead of appending every value while the
             // lists have no threshold, each lane takes T_lane, the largest
-            // of the minima of G groups of its 64 values (G = 16, 32 or 64,
-            // the first >= ceil(kk / 2)): at least ceil(kk / 2) of its
-            // values lie at or below T_lane.  The list of (row wave, query)
-            // -- two lanes, h = 0 and 1 -- then holds >= kk values at or
-            // below T, the larger of the two, once the append below has
-            // taken every value < T' (T' the next value code above T);
-            // T' becomes the list's threshold.
+            // of the minima of G groups of its 16 RB values (G = RB, 2 RB,
+            // 4 RB, 8 RB or 16 RB, the first >= ceil(kk / 2)): at least
+            // ceil(kk / 2) of its values lie at or below T_lane.  The list of
+            // (row wave, query) -- two lanes, h = 0 and 1 -- then holds >= kk
+            // values at or below T, the larger of the two, once the append
+            // below has taken every value < T' (T' the next value code above
+            // T); T' becomes the list's threshold.  (The fewest groups that
+            // suffice give the tightest threshold.)
             const int need = (a.kk + 1) / 2;
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb) {
                 float tl = -VS_INF;
-                if (need <= 4 * RB) {
+                if (need <= RB) {
+#pragma unroll
+                    for (int rb = 0; rb < RB; ++rb) {
+                        float m = acc[qb][rb][0];
+#pragma unroll
+                        for (int v = 1; v < 16; ++v) m = fminf(m, acc[qb][rb][v]);
+                        tl = fmaxf(tl, m);
+                    }
+                } else if (need <= 2 * RB) {
+#pragma unroll
+                    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                        for (int u = 0; u < 2; ++u) {
+                            float m = acc[qb][rb][8 * u];
+#pragma unroll
+                            for (int v = 1; v < 8; ++v) m = fminf(m, acc[qb][rb][8 * u + v]);
+                            tl = fmaxf(tl, m);
+                        }
+                } else if (need <= 4 * RB) {
 #pragma unroll
                     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
@@ -220,9 +239,10 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[QB][RB], const Sca
                 for (int j = 0; j < 32; ++j) {
                     const int qq = qw0 + qb * 32 + j;
                     if (cnt_w[qq] > room)
-                        flush_list(cv + (int64_t)qq * a.cap, ci + (int64_t)qq * a.cap, &cnt_w[qq],
-                                   &thr_w[qq], &thr[qq], BQ, WR, &a.gthr[q0 + qq], sv_w, si_w,
-                                   a.cap, a.kk, a.kk_final, a.publish_block, lane);
+                        flush_list(cv + (int64_t)qq * a.cap, ci + (int64_t)qq * a.cap,
+                                   &cnt_w[qq], &thr_w[qq], &thr[qq], BQ, WR, &a.gthr[q0 + qq],
+                                   sv_w, si_w, a.cap, a.kk, a.kk_final, a.publish_block,
+                                   lane);
                 }
                 thr_r[qb] = fminf(thr_r[qb], thr_w[q]);
             }
@@ -554,9 +574,18 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
 
     if constexpr (MODE == 0) {
         // final: every list of this wave's queries holds its kk best in
-        // slots [0, kk), padded
+        // slots [0, kk), padded -- one lane per list where kk fits in
+        // registers, else the lists one after another
         wave_sync();
-        for (int q = qw0; q < qw0 + 32 * QB; ++q) {
+        if (a.kk <= 16)
+            cut_lists_lanes<16>(cv + (int64_t)qw0 * a.cap, ci + (int64_t)qw0 * a.cap, cnt_w + qw0,
+                                thr_w + qw0, thr + qw0, 32 * QB, WR, &a.gthr[q0 + qw0], a.cap,
+                                a.kk, a.kk_final, a.publish_block, a.kk, true, lane, BQ);
+        else if (a.kk <= 32)
+            cut_lists_lanes<32>(cv + (int64_t)qw0 * a.cap, ci + (int64_t)qw0 * a.cap, cnt_w + qw0,
+                                thr_w + qw0, thr + qw0, 32 * QB, WR, &a.gthr[q0 + qw0], a.cap,
+                                a.kk, a.kk_final, a.publish_block, a.kk, true, lane, BQ);
+        else for (int q = qw0; q < qw0 + 32 * QB; ++q) {
             const int c = cnt_w[q];
             if (c > a.kk) {
                 flush_list(cv + (int64_t)q * a.cap, ci + (int64_t)q * a.cap, &cnt_w[q], &thr_w[q],

@@ -156,6 +156,34 @@ def test_gemm_matches_streaming(vs, opts):
     assert_knn_parity(D1, I1, Dr, Ir, 0, rtol=0.0, atol=0.0, xb=xb, xq=xq)
 
 
+@pytest.mark.parametrize("k,metric", [(10, 0), (100, 1)])
+def test_gemm_estimated_threshold_sample(vs, opts, k, metric):
+    """A large batch over 2^18+ rows on the GEMM-tiled scan starts from a
+    threshold estimated on the first 1/2^g of the rows (option
+    guess_div_log2; 1/32 by default): every sample size gives
+    the oracle's result, with one estimate pre-pass and no exact re-search."""
+    xb = syn.int_grid(300_000, 64, 17, 0)
+    xq = syn.int_grid(600, 64, 17, 1)
+    res = {}
+    for g in (0, 5, 7, 10):
+        opts(guess_div_log2=g)
+        idx = vs.GpuIndexFlat(64, vs.Metric(metric), storage="auto")
+        idx.add(xb)
+        r = idx.search(xq, k)
+        ng, _ = idx.prof_get("guess_scans")
+        nfb, _ = idx.prof_get("fallback")
+        ngm, _ = idx.prof_get("gemm")
+        idx.close()
+        assert ng == 1 and nfb == 0 and ngm >= 1, (g, ng, nfb, ngm)
+        res[g] = r
+    sub = np.arange(0, 600, 5)
+    Dr, Ir = oracle.flat_search(xb, xq[sub], k, metric, NT)
+    for g, r in res.items():
+        assert_knn_parity(r.distances[sub], r.ids[sub], Dr, Ir, metric, rtol=0.0, atol=0.0,
+                          xb=xb, xq=xq[sub])
+        assert np.array_equal(r.distances, res[5].distances), g
+
+
 def test_gemm_verification_path(vs, opts):
     """Lists forced down to 4 entries (option scan_kkw) with k = 60: the merge
     must detect queries whose lists may have dropped a winner and search

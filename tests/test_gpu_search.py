@@ -456,7 +456,7 @@ def test_set_option_rejects_unknown_and_out_of_range(vs):
         idx.set_option("no_such_option", 1)
     for name, value in (("gemm", 2), ("km16_rt", 3), ("scan_kkw", -1), ("merge_mu", 3),
                         ("merge_mu", 16), ("prepass_log2", 9), ("prepass_log2", 21),
-                        ("merge_g", -1), ("merge_g", 65)):
+                        ("merge_g", -1), ("merge_g", 65), ("guess_div_log2", 11)):
         with pytest.raises(ValueError, match="outside"):
             idx.set_option(name, value)
     idx.set_option("guess", 0)
