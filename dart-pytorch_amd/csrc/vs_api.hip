@@ -672,7 +672,16 @@ int plan_scan_core(const vs_index *x, int64_t nq, int64_t nrows, int planes, int
     const int64_t target = (int64_t)x->num_cu * 4;
     int64_t nsplit = std::max<int64_t>(1, (target + p->nqblk - 1) / p->nqblk);
     const int64_t min_rows = tile_rows * std::max(1, min_tiles);
-    nsplit = std::min<int64_t>(nsplit, std::max<int64_t>(1, (nrows + min_rows - 1) / min_rows));
+    int64_t by_rows = (nrows + min_rows - 1) / min_rows;
+    // a short scan that would leave most CUs idle takes splits down to one
+    // tile each (up to one workgroup per CU): each wave then works alone on
+    // its SIMD and its time is mostly memory latency, so more splits, not
+    // warmer lists, shorten it
+    if (p->nqblk * by_rows < x->num_cu)
+        by_rows = std::max<int64_t>(
+            by_rows, std::min<int64_t>((nrows + tile_rows - 1) / tile_rows,
+                                       std::max<int64_t>(1, x->num_cu / p->nqblk)));
+    nsplit = std::min<int64_t>(nsplit, std::max<int64_t>(1, by_rows));
     if (max_lists > 0) nsplit = std::min<int64_t>(nsplit, std::max<int64_t>(1, max_lists / p->lw));
     if (list_budget > 0) {
         const size_t per_split = (size_t)p->nqblk * p->lw * p->bn * p->cap * 8;

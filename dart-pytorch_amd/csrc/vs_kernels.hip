@@ -279,13 +279,27 @@ __global__ __launch_bounds__(64 * NW) void scan_kernel(ScanKArgs a) {
 
     const int64_t q0 = qblk * BN;
     if constexpr (QPL > 0) {
-        const int64_t cpr = a.ld / 8;  // 16-byte chunks per plane row
-        const int64_t nch = (int64_t)BN * QPL * cpr;
-        for (int64_t c = threadIdx.x; c < nch; c += 64 * NW) {
-            const int64_t row = c / cpr, ch = c % cpr;
-            const int64_t q = row / QPL, p = row % QPL;
-            const uint4 v = *(const uint4 *)(a.qp + ((q0 + q) * 2 + p) * a.ld + ch * 8);
-            *(uint4 *)(qs + row * ldp + ch * 8) = v;
+        // the block's query planes into LDS, eight 16-byte loads per thread
+        // in flight before their stores (one memory round trip per batch)
+        const int cpr = (int)(a.ld / 8);  // 16-byte chunks per plane row
+        const int nch = BN * QPL * cpr;
+        constexpr int U = 8;
+        for (int c0 = threadIdx.x; c0 < nch; c0 += U * 64 * NW) {
+            u32x4_t v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {  // (chunks past the end reload chunk 0)
+                const int c = c0 + u * 64 * NW < nch ? c0 + u * 64 * NW : 0;
+                const int row = c / cpr, ch = c % cpr;
+                const int q = row / QPL, p = row % QPL;
+                v[u] = *(const u32x4_t *)(a.qp + ((q0 + q) * 2 + p) * a.ld + ch * 8);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {  // (chunks past the end go to row 0's padding)
+                const int c = c0 + u * 64 * NW;
+                const bool in = c < nch;
+                const int row = in ? c / cpr : 0, ch = in ? c % cpr : cpr;
+                *(u32x4_t *)(qs + row * ldp + ch * 8) = v[u];
+            }
         }
     }
     for (int t = threadIdx.x; t < NW * BN; t += 64 * NW) {
