@@ -2142,31 +2142,59 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     // on a second stream, so that the copies overlap the grouping and update
     if (!x->st_copy)
         VS_HIP(hipStreamCreateWithFlags(&x->st_copy, hipStreamNonBlocking), "copy stream");
-    hipEvent_t ev_pick = nullptr, ev_best = nullptr;
-    VS_HIP(hipEventCreateWithFlags(&ev_pick, hipEventDisableTiming), "event");
+    // the distances come over in kSumChunks pieces, each followed by an
+    // event, so that the objective's sum starts with the first piece
+    constexpr int kSumChunks = 8;
     struct EvGuard {
-        hipEvent_t e;
+        hipEvent_t e = nullptr;
         ~EvGuard() {
             if (e) (void)hipEventDestroy(e);
         }
-    } evg0{ev_pick};
-    VS_HIP(hipEventCreateWithFlags(&ev_best, hipEventDisableTiming), "event");
-    EvGuard evg1{ev_best};
-    VS_HIP(hipEventRecord(ev_pick, x->st), "event");
-    VS_HIP(hipStreamWaitEvent(x->st_copy, ev_pick, 0), "event");
+    } ev_pick, ev_best[kSumChunks];
+    VS_HIP(hipEventCreateWithFlags(&ev_pick.e, hipEventDisableTiming), "event");
+    for (auto &e : ev_best) VS_HIP(hipEventCreateWithFlags(&e.e, hipEventDisableTiming), "event");
+    VS_HIP(hipEventRecord(ev_pick.e, x->st), "event");
+    VS_HIP(hipStreamWaitEvent(x->st_copy, ev_pick.e, 0), "event");
     // the copy stream is drained before this call returns (below, and on
     // every error path), so the next call cannot overwrite what it reads
     struct CopyDrain {
         hipStream_t s;
         ~CopyDrain() { (void)hipStreamSynchronize(s); }
     } drain{x->st_copy};
-    VS_HIP(hipMemcpyAsync(x->km_hbest.p, x->km_best.p, (size_t)n * 8, hipMemcpyDeviceToHost,
-                          x->st_copy),
-           "reading distances");
-    VS_HIP(hipEventRecord(ev_best, x->st_copy), "event");
+    for (int c = 0; c < kSumChunks; ++c) {
+        const int64_t i0 = n * c / kSumChunks, i1 = n * (c + 1) / kSumChunks;
+        if (i1 > i0)
+            VS_HIP(hipMemcpyAsync(x->km_hbest.as<double>() + i0, x->km_best.as<double>() + i0,
+                                  (size_t)(i1 - i0) * 8, hipMemcpyDeviceToHost, x->st_copy),
+                   "reading distances");
+        VS_HIP(hipEventRecord(ev_best[c].e, x->st_copy), "event");
+    }
     VS_HIP(hipMemcpyAsync(x->km_hassign.p, x->km_assign.p, (size_t)n * 4, hipMemcpyDeviceToHost,
                           x->st_copy),
            "reading assignments");
+    // objective: fp64 sum in point order (kmeans.dart:104), on a helper
+    // thread while the update runs and this thread copies the results out
+    // (a sequential sum of n values is a chain of n dependent adds)
+    double o = 0.0;
+    hipError_t sum_err = hipSuccess;
+    struct Join {
+        std::thread t;
+        ~Join() {
+            if (t.joinable()) t.join();
+        }
+    } sum_thread{std::thread([&o, &sum_err, &ev_best, best = x->km_hbest.as<double>(), n] {
+        double acc = 0.0;
+        for (int c = 0; c < kSumChunks; ++c) {
+            const hipError_t e = hipEventSynchronize(ev_best[c].e);
+            if (e != hipSuccess) {
+                sum_err = e;
+                return;
+            }
+            const int64_t i1 = n * (c + 1) / kSumChunks;
+            for (int64_t i = n * c / kSumChunks; i < i1; ++i) acc += best[i];
+        }
+        o = acc;
+    })};
 
     // update: counts, stable grouping by cluster, ordered fp32 sums
     VS_HIP(x->km_counts.ensure((size_t)K * 4), "counts");
@@ -2226,21 +2254,6 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
            "reading centroids");
     VS_HIP(hipMemcpyAsync(counts, x->km_counts.p, (size_t)K * 4, hipMemcpyDeviceToHost, x->st),
            "reading counts");
-    // objective: fp64 sum in point order (kmeans.dart:104), on a helper
-    // thread while the update runs and this thread copies the results out
-    // (a sequential sum of n values is a chain of n dependent adds)
-    VS_HIP(hipEventSynchronize(ev_best), "reading distances");
-    double o = 0.0;
-    struct Join {
-        std::thread t;
-        ~Join() {
-            if (t.joinable()) t.join();
-        }
-    } sum_thread{std::thread([&o, best = x->km_hbest.as<double>(), n] {
-        double acc = 0.0;
-        for (int64_t i = 0; i < n; ++i) acc += best[i];
-        o = acc;
-    })};
     VS_HIP(hipStreamSynchronize(x->st_copy), "reading assignments");
     memcpy(assign, x->km_hassign.p, (size_t)n * 4);
     VS_HIP(hipStreamSynchronize(x->st), "update");
@@ -2268,6 +2281,7 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     }
     memcpy(centroids_out, cen_new.data(), (size_t)K * d * 4);
     sum_thread.t.join();
+    VS_HIP(sum_err, "reading distances");
     if (obj) *obj = o;
     return VS_OK;
 }
