@@ -1495,6 +1495,9 @@ template <int KK>
 __global__ void kmeans_pick_kernel(MergeKArgs a);
 template <int E, int CH>
 __global__ void kmeans_pick_wave_kernel(MergeKArgs a);
+template <int E, int CH>
+__global__ void kmeans_pick_set_kernel(MergeKArgs a);
+constexpr int kPickSetMaxK = 16384;  // the distinct-candidate pick's largest K
 
 // Threshold estimates from a pre-pass (seed_rank <= 64): one wave per query.
 // Every lane keeps the 8 smallest values it reads from the query's lists,
@@ -1622,8 +1625,12 @@ hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, 
         a.kmin_margin = plan.kmin_margin;
         a.kl = plan.cap;
         a.order = order;
-        kmeans_pick_wave_kernel<32, 16>
-            <<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(a);
+        if (K <= kPickSetMaxK)
+            kmeans_pick_set_kernel<32, 16>
+                <<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(a);
+        else
+            kmeans_pick_wave_kernel<32, 16>
+                <<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(a);
         return hipGetLastError();
     }
     if (plan.kind == 3) return hipErrorInvalidValue;  // row-shared lists are k-means lists only
@@ -1744,6 +1751,94 @@ __global__ __launch_bounds__(256) void kmeans_pick_kernel(MergeKArgs a) {
     if (!safe) a.fb_list[atomicAdd(a.fb_count, 1)] = (int32_t)qg;
 }
 
+// The pick's first phase for one point (row qc of the scan's query blocks):
+// vmin, the smallest value of its count-terminated k-means lists, the bound
+// vmin + kmin_margin that every centroid outside them reaches, and its
+// candidates -- the ids within 2 * bound of vmin -- handed to put(slot, id)
+// in list order.  Returns their number; *over is set when a list was marked
+// full or more than E candidates were found (the point then goes to the
+// exhaustive kernel).
+template <int E, typename Put>
+__device__ __forceinline__ int pick_candidates(const MergeKArgs &a, int64_t qc, float *vmin_out,
+                                               float *seg_bound_out, bool *over_io, Put put) {
+    const int64_t qblk = qc / a.bn, q = qc % a.bn;
+    const int64_t nlists = a.nsplit * a.lw;
+    auto list_off = [&](int64_t l) {
+        const int64_t split = l / a.lw, w = l % a.lw;
+        return (((qblk * a.nsplit + split) * a.lw + w) * a.bn + q) * a.cap;
+    };
+    float vmin = VS_INF;
+    bool over = *over_io;
+    auto list_len = [&](int64_t l) -> int {
+        const int64_t split = l / a.lw, w = l % a.lw;
+        const int c = a.list_cnt[((qblk * a.nsplit + split) * a.lw + w) * a.bn + q];
+        return c > a.cap ? 0 : c;
+    };
+    // 16 entries (four 16-byte reads, all in flight) per step: a list's
+    // capacity is a power of two >= 16, so a step never leaves its buffer;
+    // entries past the count are skipped by index
+    constexpr int G = 16;
+    for (int64_t l = 0; l < nlists; ++l) {
+        const int64_t off = list_off(l);
+        const int64_t split = l / a.lw, w = l % a.lw;
+        if (a.list_cnt[((qblk * a.nsplit + split) * a.lw + w) * a.bn + q] > a.cap) over = true;
+        // every appended entry has a real id
+        const int lc = list_len(l);
+        for (int e0 = 0; e0 < lc; e0 += G) {
+            float4 v4[G / 4];
+#pragma unroll
+            for (int u = 0; u < G / 4; ++u) v4[u] = *(const float4 *)(a.cand_v + off + e0 + 4 * u);
+#pragma unroll
+            for (int u = 0; u < G / 4; ++u) {
+                const float v[4] = {v4[u].x, v4[u].y, v4[u].z, v4[u].w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    if (e0 + 4 * u + k < lc) vmin = fminf(vmin, v[k]);
+            }
+        }
+    }
+    // every centroid outside the lists: accumulator >= vmin + margin (the
+    // scan's fp32 sum, monotone in vmin)
+    const float lim = vmin + 2.0f * a.bound;
+    int ne = 0;
+    for (int64_t l = 0; l < nlists; ++l) {
+        const int64_t off = list_off(l);
+        const int lc = list_len(l);
+        for (int e0 = 0; e0 < lc; e0 += G) {
+            float4 v4[G / 4];
+            int4 i4[G / 4];
+#pragma unroll
+            for (int u = 0; u < G / 4; ++u) {
+                v4[u] = *(const float4 *)(a.cand_v + off + e0 + 4 * u);
+                i4[u] = *(const int4 *)(a.cand_i + off + e0 + 4 * u);
+            }
+#pragma unroll
+            for (int u = 0; u < G / 4; ++u) {
+                const float v[4] = {v4[u].x, v4[u].y, v4[u].z, v4[u].w};
+                const int ids[4] = {i4[u].x, i4[u].y, i4[u].z, i4[u].w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    if (e0 + 4 * u + k >= lc || v[k] > lim) continue;
+                    const int id = ids[k];
+                    if (id < 0) continue;
+                    if ((int64_t)id >= a.nrows) {
+                        atomicOr(a.flags, kFlagBadId);
+                        continue;
+                    }
+                    if (ne < E)
+                        put(ne++, id);
+                    else
+                        over = true;
+                }
+            }
+        }
+    }
+    *vmin_out = vmin;
+    *seg_bound_out = vmin + a.kmin_margin;
+    *over_io = over;
+    return ne;
+}
+
 // ---------------------------------------------------------------------------
 // k-means pick over the row-shared scan's k-means lists, the exact
 // re-scoring staged through LDS: one wave per 64 points (lane = point).  Each lane gathers the ids of its candidates
@@ -1783,63 +1878,10 @@ __global__ __launch_bounds__(256) void kmeans_pick_wave_kernel(MergeKArgs a) {
     // lanes past the end mirror the wave's first point
     const int64_t qg = point(live ? p0 + lane : p0);
     const int64_t qc = qg;
-    const int64_t qblk = qc / a.bn, q = qc % a.bn;
-    const int64_t nlists = a.nsplit * a.lw;
-    auto list_off = [&](int64_t l) {
-        const int64_t split = l / a.lw, w = l % a.lw;
-        return (((qblk * a.nsplit + split) * a.lw + w) * a.bn + q) * a.cap;
-    };
-    float vmin = VS_INF;
+    float vmin = VS_INF, seg_bound = VS_INF;
     bool over = false;
-    auto list_len = [&](int64_t l) -> int {
-        const int64_t split = l / a.lw, w = l % a.lw;
-        const int c = a.list_cnt[((qblk * a.nsplit + split) * a.lw + w) * a.bn + q];
-        return c > a.cap ? 0 : c;
-    };
-    for (int64_t l = 0; l < nlists; ++l) {
-        const int64_t off = list_off(l);
-        const int64_t split = l / a.lw, w = l % a.lw;
-        if (a.list_cnt[((qblk * a.nsplit + split) * a.lw + w) * a.bn + q] > a.cap) over = true;
-        // every appended entry has a real id; 16-byte reads (lists hold a
-        // multiple of 4 slots)
-        const int lc = list_len(l);
-        for (int e = 0; e < lc; e += 4) {
-            const float4 v4 = *(const float4 *)(a.cand_v + off + e);
-            vmin = fminf(vmin, v4.x);
-            if (e + 1 < lc) vmin = fminf(vmin, v4.y);
-            if (e + 2 < lc) vmin = fminf(vmin, v4.z);
-            if (e + 3 < lc) vmin = fminf(vmin, v4.w);
-        }
-    }
-    // every centroid outside the lists: accumulator >= vmin + margin (the
-    // scan's fp32 sum, monotone in vmin)
-    const float seg_bound = vmin + a.kmin_margin;
-    const float lim = vmin + 2.0f * a.bound;
-    int ne = 0;
-    for (int64_t l = 0; l < nlists; ++l) {
-        const int64_t off = list_off(l);
-        const int lc = list_len(l);
-        for (int e = 0; e < lc; ++e) {
-            if ((e & 3) == 0) {  // values four at a time; ids of the candidates only
-                const float4 v4 = *(const float4 *)(a.cand_v + off + e);
-                if (!(v4.x <= lim || v4.y <= lim || v4.z <= lim || v4.w <= lim)) {
-                    e += 3;
-                    continue;
-                }
-            }
-            if (a.cand_v[off + e] > lim) continue;
-            const int id = a.cand_i[off + e];
-            if (id < 0) continue;
-            if ((int64_t)id >= a.nrows) {
-                atomicOr(a.flags, kFlagBadId);
-                continue;
-            }
-            if (ne < E)
-                ids[ne++ * 64 + lane] = id;
-            else
-                over = true;
-        }
-    }
+    const int ne = pick_candidates<E>(a, qc, &vmin, &seg_bound, &over,
+                                      [&](int e, int id) { ids[e * 64 + lane] = id; });
     int emax = live && !over ? ne : 0;
     for (int o = 32; o > 0; o >>= 1) emax = max(emax, __shfl_xor(emax, o));
     for (int e = ne; e < emax; ++e) ids[e * 64 + lane] = -1;
@@ -1900,6 +1942,173 @@ __global__ __launch_bounds__(256) void kmeans_pick_wave_kernel(MergeKArgs a) {
     for (int e = 0; e < E; ++e) {
         const int id = e < ne ? ids[e * 64 + lane] : INT_MAX;
         if (e < ne && (sc[e] < best || (sc[e] == best && id < bid))) {
+            best = sc[e];
+            bid = id;
+        }
+    }
+    const bool safe = !over && bid != INT_MAX &&
+                      (seg_bound == VS_INF ||
+                       (double)seg_bound - (double)a.bound > (best - xx) + 1e-9 * (fabs(xx) + 1.0));
+    a.assign[qg] = bid == INT_MAX ? 0 : bid;
+    a.best_sq[qg] = best;
+    if (!safe) a.fb_list[atomicAdd(a.fb_count, 1)] = (int32_t)qg;
+}
+
+// ---------------------------------------------------------------------------
+// The same pick with each distinct candidate centroid read once per wave.
+// The wave's points walk in cluster order, so its 64 lanes share most of
+// their candidates: the union of their ids (a bitmap over the K <=
+// kPickSetMaxK centroids, ranked by a prefix count over its words) numbers
+// the distinct centroids 0 .. u - 1, and every lane's candidate becomes a
+// slot in that numbering.  Each CH-dimension chunk then stages the points'
+// chunk and the distinct centroids' chunks (64 slots per batch, usually one
+// batch) with all loads in flight at once, and every lane continues its
+// candidates' fp64 sums in dimension order, as the kernel above does (same
+// order, same rounding), reading the centroid values by slot.  A wave whose
+// union exceeds kPickSetMaxU sends its points to the exhaustive kernel.
+// ---------------------------------------------------------------------------
+constexpr int kPickSetMaxU = 1024;
+
+template <int E, int CH>
+__global__ __launch_bounds__(256) void kmeans_pick_set_kernel(MergeKArgs a) {
+    constexpr int RS = 65;  // LDS words per staged dimension (64 rows + 1: no bank conflicts on reads)
+    constexpr int PIECES = CH / 4;            // 16-byte pieces per row chunk
+    constexpr int ROWS_PER = 64 / PIECES;     // rows covered by one wave-wide load
+    constexpr int KW = kPickSetMaxK / 64;     // bitmap words
+    constexpr int WPL = KW / 64;              // bitmap words per lane (contiguous)
+    static_assert(CH % 4 == 0 && 64 % PIECES == 0, "whole 16-byte pieces");
+    static_assert(kPickSetMaxU <= 65536 && kPickSetMaxK <= 65536, "16-bit ids and slots");
+    __shared__ float xs_all[4][CH * RS];
+    __shared__ float cs_all[4][CH * RS];
+    __shared__ uint16_t sl_all[4][E * 64];           // [candidate][lane]: id, then slot
+    __shared__ uint16_t uid_all[4][kPickSetMaxU];    // slot -> centroid id
+    __shared__ unsigned long long bits_all[4][KW];   // the wave's candidate ids
+    __shared__ uint16_t wb_all[4][KW];               // slots before each bitmap word
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    float *xs = xs_all[wave], *cs = cs_all[wave];
+    uint16_t *sl = sl_all[wave], *uid = uid_all[wave], *wb = wb_all[wave];
+    unsigned long long *bits = bits_all[wave];
+    const int64_t p0 = ((int64_t)blockIdx.x * 4 + wave) * 64;
+    if (p0 >= a.nq) return;  // whole waves only: every lane below stays to the end
+    auto point = [&](int64_t s) -> int64_t { return a.order ? (int64_t)a.order[s] : s; };
+    const bool live = p0 + lane < a.nq;
+    const int64_t qg = point(live ? p0 + lane : p0);  // lanes past the end mirror the first point
+    const int kw = (int)((a.nrows + 63) / 64);         // bitmap words in use (<= KW)
+#pragma unroll
+    for (int i = 0; i < WPL; ++i) bits[lane * WPL + i] = 0ull;
+    lds_wave_sync();
+    float vmin = VS_INF, seg_bound = VS_INF;
+    bool over = false;
+    const int ne = pick_candidates<E>(a, qg, &vmin, &seg_bound, &over, [&](int e, int id) {
+        sl[e * 64 + lane] = (uint16_t)id;
+        atomicOr(&bits[id >> 6], 1ull << (id & 63));
+    });
+    lds_wave_sync();
+    // slots: lane l ranks words [l WPL, (l + 1) WPL) after the words of the
+    // lanes below it
+    int cnt = 0;
+#pragma unroll
+    for (int i = 0; i < WPL; ++i)
+        cnt += lane * WPL + i < kw ? __popcll(bits[lane * WPL + i]) : 0;
+    int incl = cnt;
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, o);
+        if (lane >= o) incl += y;
+    }
+    const int u = __shfl(incl, 63);  // distinct candidates of the wave
+    if (u <= kPickSetMaxU) {
+        int slot = incl - cnt;
+#pragma unroll
+        for (int i = 0; i < WPL; ++i) {
+            const int w = lane * WPL + i;
+            wb[w] = (uint16_t)slot;
+            unsigned long long m = w < kw ? bits[w] : 0ull;
+            while (m) {
+                const int b = __ffsll((long long)m) - 1;
+                m &= m - 1;
+                uid[slot++] = (uint16_t)(w * 64 + b);
+            }
+        }
+    } else {
+        over = true;  // (uniform: the whole wave goes to the exhaustive kernel)
+    }
+    lds_wave_sync();
+    int emax = live && !over ? ne : 0;
+    for (int o = 32; o > 0; o >>= 1) emax = max(emax, __shfl_xor(emax, o));
+    for (int e = 0; e < ne && e < emax; ++e) {
+        const int id = sl[e * 64 + lane];
+        const unsigned long long below = bits[id >> 6] & ((1ull << (id & 63)) - 1ull);
+        sl[e * 64 + lane] = (uint16_t)(wb[id >> 6] + __popcll(below));
+    }
+    lds_wave_sync();
+
+    const int prow = lane / PIECES, pcol = (lane % PIECES) * 4;  // this lane's load piece
+    const int nb = emax > 0 ? u : 0;  // distinct centroids to stage
+    double sc[E], xx = 0.0;
+#pragma unroll
+    for (int e = 0; e < E; ++e) sc[e] = 0.0;
+    for (int64_t c0 = 0; c0 < a.ld; c0 += CH) {
+        float xr[CH];
+        for (int b0 = 0; b0 == 0 || b0 < nb; b0 += 64) {
+            // the points' chunk (first batch) and the chunks of distinct
+            // centroids b0 .. b0 + 63 (rows past u read centroid 0), all
+            // loads issued before the first LDS write
+            float4 pv[PIECES], cv[PIECES];
+#pragma unroll
+            for (int i = 0; i < PIECES; ++i) {
+                const int r = i * ROWS_PER + prow;
+                if (b0 == 0) {
+                    const int64_t pr = point(p0 + r < a.nq ? p0 + r : p0);
+                    pv[i] = *(const float4 *)(a.pts + pr * a.ld + c0 + pcol);
+                }
+                const int id = b0 + r < nb ? uid[b0 + r] : 0;
+                cv[i] = *(const float4 *)((const float *)a.xb + (int64_t)id * a.ld + c0 + pcol);
+            }
+#pragma unroll
+            for (int i = 0; i < PIECES; ++i) {
+                const int r = i * ROWS_PER + prow;
+                if (b0 == 0) {
+                    xs[(pcol + 0) * RS + r] = pv[i].x;
+                    xs[(pcol + 1) * RS + r] = pv[i].y;
+                    xs[(pcol + 2) * RS + r] = pv[i].z;
+                    xs[(pcol + 3) * RS + r] = pv[i].w;
+                }
+                cs[(pcol + 0) * RS + r] = cv[i].x;
+                cs[(pcol + 1) * RS + r] = cv[i].y;
+                cs[(pcol + 2) * RS + r] = cv[i].z;
+                cs[(pcol + 3) * RS + r] = cv[i].w;
+            }
+            lds_wave_sync();
+            if (b0 == 0) {
+#pragma unroll
+                for (int j = 0; j < CH; ++j) {
+                    xr[j] = xs[j * RS + lane];
+                    xx = xx + (double)xr[j] * (double)xr[j];
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                if (e < emax) {  // uniform: every slot index stays a constant
+                    const int s = e < ne ? (int)sl[e * 64 + lane] - b0 : -1;
+                    if (s >= 0 && s < 64) {
+#pragma unroll
+                        for (int j = 0; j < CH; ++j) {
+                            const double dd = (double)xr[j] - (double)cs[j * RS + s];
+                            sc[e] = sc[e] + dd * dd;
+                        }
+                    }
+                }
+            }
+            lds_wave_sync();  // xs and cs are rewritten by the next batch or chunk
+        }
+    }
+    if (!live) return;
+    double best = __builtin_huge_val();
+    int bid = INT_MAX;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int id = e < ne && !over ? (int)uid[sl[e * 64 + lane]] : INT_MAX;
+        if (e < ne && !over && (sc[e] < best || (sc[e] == best && id < bid))) {
             best = sc[e];
             bid = id;
         }
