@@ -934,6 +934,16 @@ int seed_thresholds(vs_index *x, const vs::PreparedQueries &pq, int64_t S, int64
                              need_elems, need_lists, 0, -1, list_budget);
         if (rc) return rc;
     }
+    // the GEMM-tiled estimate pre-pass: its lists would warm up on their own
+    // share of the sample (most of its tiles then take the append path); a
+    // bound on the kk_final-th value of the first 1/32 of the sample lets it
+    // start tight (the sample's own kk_final smallest all lie below it, so
+    // the estimate is unchanged)
+    if (pp.kind == 2 && seed_rank > 0 && S >= (1 << 16)) {
+        rc = seed_thresholds(x, pq, S / 32, kk_final, gthr, L, need_elems, need_lists, 0, -1,
+                             list_budget);
+        if (rc) return rc;
+    }
     if (!L) {
         *need_elems = std::max(*need_elems, list_elems(pp));
         *need_lists = std::max(*need_lists, list_count(pp));

@@ -161,20 +161,25 @@ def test_gemm_estimated_threshold_sample(vs, opts, k, metric):
     """A large batch over 2^18+ rows on the GEMM-tiled scan starts from a
     threshold estimated on the first 1/2^g of the rows (option
     guess_div_log2; 1/32 by default): every sample size gives
-    the oracle's result, with one estimate pre-pass and no exact re-search."""
+    the oracle's result, with one estimate pre-pass and no exact re-search.
+    A sample of 2^16 rows or more (here 1/2) is itself seeded by a bound from
+    its first 1/32 (one more pre-pass scan)."""
     xb = syn.int_grid(300_000, 64, 17, 0)
     xq = syn.int_grid(600, 64, 17, 1)
     res = {}
-    for g in (0, 5, 7, 10):
+    for g in (0, 1, 5, 7, 10):
         opts(guess_div_log2=g)
         idx = vs.GpuIndexFlat(64, vs.Metric(metric), storage="auto")
         idx.add(xb)
+        idx.prof_enable(True)
         r = idx.search(xq, k)
         ng, _ = idx.prof_get("guess_scans")
+        npre, _ = idx.prof_get("prepass_scans")
         nfb, _ = idx.prof_get("fallback")
         ngm, _ = idx.prof_get("gemm")
         idx.close()
         assert ng == 1 and nfb == 0 and ngm >= 1, (g, ng, nfb, ngm)
+        assert npre == (2 if g == 1 else 1), (g, npre)
         res[g] = r
     sub = np.arange(0, 600, 5)
     Dr, Ir = oracle.flat_search(xb, xq[sub], k, metric, NT)

@@ -125,6 +125,15 @@ def test_kmeans_register_shortlists(vs, n, d, ncomp, K):
     _kmeans_check(vs, x, cen)
 
 
+def test_kmeans_pick_beyond_distinct_bitmap(vs):
+    """More than 16,384 centroids: the pick stages every lane's candidate
+    slot by slot instead of numbering the wave's distinct candidates through
+    its 16,384-bit map; the oracle's assignments, objective and centroids."""
+    x, _ = syn.gaussian_mixture(18_000, 100, 64, 0.1, 47)
+    cen = x[syn.seeded_subset(18_000, 17_000, 47)].copy()
+    _kmeans_check(vs, x, cen)
+
+
 def test_kmeans_register_shortlists_fallback(vs):
     """Forty copies of one centroid: more candidates within 2 bound of the
     smallest than the pick's 32 slots, so the exhaustive exact scan decides
