@@ -577,15 +577,22 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
         // slots [0, kk), padded -- one lane per list where kk fits in
         // registers, else the lists one after another
         wave_sync();
-        if (a.kk <= 16)
-            cut_lists_lanes<16>(cv + (int64_t)qw0 * a.cap, ci + (int64_t)qw0 * a.cap, cnt_w + qw0,
-                                thr_w + qw0, thr + qw0, 32 * QB, WR, &a.gthr[q0 + qw0], a.cap,
-                                a.kk, a.kk_final, a.publish_block, a.kk, true, lane, BQ);
-        else if (a.kk <= 32)
-            cut_lists_lanes<32>(cv + (int64_t)qw0 * a.cap, ci + (int64_t)qw0 * a.cap, cnt_w + qw0,
-                                thr_w + qw0, thr + qw0, 32 * QB, WR, &a.gthr[q0 + qw0], a.cap,
-                                a.kk, a.kk_final, a.publish_block, a.kk, true, lane, BQ);
-        else for (int q = qw0; q < qw0 + 32 * QB; ++q) {
+        if (a.kk <= 32) {
+            // (64 lists, one per lane, at a time)
+            for (int g0 = qw0; g0 < qw0 + 32 * QB; g0 += 64) {
+                const int nl = min(64, qw0 + 32 * QB - g0);
+                if (a.kk <= 16)
+                    cut_lists_lanes<16>(cv + (int64_t)g0 * a.cap, ci + (int64_t)g0 * a.cap,
+                                        cnt_w + g0, thr_w + g0, thr + g0, nl, WR, &a.gthr[q0 + g0],
+                                        a.cap, a.kk, a.kk_final, a.publish_block, a.kk, true, lane,
+                                        BQ);
+                else
+                    cut_lists_lanes<32>(cv + (int64_t)g0 * a.cap, ci + (int64_t)g0 * a.cap,
+                                        cnt_w + g0, thr_w + g0, thr + g0, nl, WR, &a.gthr[q0 + g0],
+                                        a.cap, a.kk, a.kk_final, a.publish_block, a.kk, true, lane,
+                                        BQ);
+            }
+        } else for (int q = qw0; q < qw0 + 32 * QB; ++q) {
             const int c = cnt_w[q];
             if (c > a.kk) {
                 flush_list(cv + (int64_t)q * a.cap, ci + (int64_t)q * a.cap, &cnt_w[q], &thr_w[q],
