@@ -577,7 +577,13 @@ bool plan_gemm(const vs_index *x, int64_t nq, int64_t nrows, int planes, int sto
     int64_t spc = std::max<int64_t>(1, 32 / p->tile_group);
     const int64_t tile_rows = (int64_t)pick->wr * 32 * pick->rb;
     const int64_t ncu = (int64_t)std::max(1, x->num_cu);
-    const int64_t max_split = std::max<int64_t>(1, nrows / (tile_rows * 4));
+    int64_t max_split = std::max<int64_t>(1, nrows / (tile_rows * 4));
+    // a short scan that would leave CUs idle (a pre-pass over a small
+    // sample) takes splits down to one tile each
+    if (p->nqblk * max_split < ncu)
+        max_split = std::max<int64_t>(
+            max_split, std::min<int64_t>((nrows + tile_rows - 1) / tile_rows,
+                                         (ncu + p->nqblk - 1) / p->nqblk));
     const int64_t rounds = 2;
     // smallest split count whose grid covers the target rounds of CUs and
     // fills >= 90% of its last round; else the best fill seen

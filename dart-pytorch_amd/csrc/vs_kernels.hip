@@ -1625,7 +1625,12 @@ hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, 
         a.kmin_margin = plan.kmin_margin;
         a.kl = plan.cap;
         a.order = order;
-        if (K <= kPickSetMaxK)
+        // points grouped by the previous step's clusters share candidates:
+        // each distinct one is staged once per wave; in index order (the
+        // first step) they share few, and slot-by-slot staging is faster
+        // (measured on C4: 1.99 against 2.70 ms grouped, 5.61 against
+        // 4.19 ms in index order)
+        if (K <= kPickSetMaxK && order)
             kmeans_pick_set_kernel<32, 16>
                 <<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(a);
         else
