@@ -180,6 +180,7 @@ struct VsOptions {
                            // 4 or 8)
     int merge_g = 0;       // merge: workgroups per query (0: by batch size; 1: one; 2..64: split)
     int guess_div_log2 = 0;  // large batches: the estimate's sample is 1/2^this of the rows (0: 5)
+    int kmin_init = 1;       // k-means: start the assign scan's running minima from the last step
 };
 
 struct vs_index {
@@ -213,6 +214,12 @@ struct vs_index {
     // these rows (version) and this many points
     uint64_t km_order_version = ~0ull;
     int64_t km_order_n = 0;
+    // k-means: km_assign / km_best / km_cen hold a whole step's assignments,
+    // squared distances and centroids for these rows (version), points and K
+    // (the next step's scan starts its running minima from them)
+    DevBuf km_shift, km_init;
+    uint64_t km_prev_version = ~0ull;
+    int64_t km_prev_n = 0, km_prev_K = 0;
     vs::PreparedQueries km_pq;
     uint32_t km_pflags = 0;
     uint64_t km_prep_version = ~0ull;
@@ -1522,7 +1529,7 @@ void vs_index_destroy(vs_index *x) {
                       &x->km_fb,   &x->km_keys,   &x->km_order, &x->km_tmp,   &x->km_counts,
                       &x->km_offsets, &x->km_out, &x->km_iota, &x->lcnt,   &x->km_qp,
                       &x->km_qf,   &x->km_qnorm,  &x->km_cen16, &x->km_c16n, &x->xb16,
-                      &x->xb16n,   &x->vx,        &x->ctl};
+                      &x->xb16n,   &x->vx,        &x->ctl,      &x->km_shift, &x->km_init};
     for (DevBuf *b : bufs) b->release();
     x->km_hbest.release();
     x->km_hassign.release();
@@ -1991,15 +1998,25 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     if (alias) cen_copy.assign(centroids_in, centroids_in + K * d);
     const float *cen_in = alias ? cen_copy.data() : centroids_in;
 
+    // the previous step's results, if they belong to these points and K:
+    // how far each centroid moved since (before its rows are replaced)
+    const bool prev = x->km_prev_version == x->version && x->km_prev_n == n && x->km_prev_K == K;
+    x->km_prev_version = ~0ull;  // set again once this step's results are whole
+    VS_HIP(x->stage.ensure((size_t)K * d * 4), "centroid staging");
+    VS_HIP(hipMemcpyAsync(x->stage.p, cen_in, (size_t)K * d * 4, hipMemcpyHostToDevice,
+                          x->st),
+           "uploading centroids");
+    if (prev) {
+        VS_HIP(x->km_shift.ensure((size_t)K * 8), "centroid shifts");
+        VS_HIP(vs::launch_kmeans_shift(x->km_cen.as<float>(), ld, (const float *)x->stage.p, d, K,
+                                       x->km_shift.as<double>(), x->st),
+               "centroid shifts");
+    }
     // centroid storage: fp32 rows of ld, slack rows zero, plus norms
     VS_HIP(x->km_cen.ensure((size_t)(K + kRowSlack) * ld * 4), "centroid storage");
     VS_HIP(x->km_cxn.ensure((size_t)(K + kRowSlack) * 4), "centroid norms");
     VS_HIP(hipMemsetAsync(x->km_cen.p, 0, (size_t)(K + kRowSlack) * ld * 4, x->st), "clear");
     VS_HIP(hipMemsetAsync(x->km_cxn.p, 0, (size_t)(K + kRowSlack) * 4, x->st), "clear");
-    VS_HIP(x->stage.ensure((size_t)K * d * 4), "centroid staging");
-    VS_HIP(hipMemcpyAsync(x->stage.p, cen_in, (size_t)K * d * 4, hipMemcpyHostToDevice,
-                          x->st),
-           "uploading centroids");
     VS_HIP(x->flags.ensure(4), "flags");
     VS_HIP(hipMemsetAsync(x->flags.p, 0, 4, x->st), "flags");
     VS_HIP(vs::launch_store_rows(x->stage.p, 0, d, K, d, x->km_cen.p, 0, ld,
@@ -2065,6 +2082,16 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     if (coarse && plan.kind == 3) {
         plan.share_kmin = 1;
         plan.kmin_margin = 2.5f * bound;
+        // the running minima start at the previous assignment's bound
+        if (prev && x->opt.kmin_init) {
+            VS_HIP(x->km_init.ensure((size_t)pq.nq_pad * 4), "running minima");
+            VS_HIP(vs::launch_kmeans_init(x->km_assign.as<int32_t>(), x->km_best.as<double>(),
+                                          x->km_shift.as<double>(), pq.qnorm, n, pq.nq_pad, K,
+                                          bound, x->km_init.as<float>(), x->st),
+                   "running minima");
+            plan.kmin_init = x->km_init.as<float>();
+            x->prof["kmin_init"].launches++;
+        }
     }
     if ((rc = scan_fits(plan, pq))) return rc;
     const size_t nlists = (size_t)plan.nqblk * plan.nsplit * plan.lw * plan.bn;
@@ -2299,6 +2326,9 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     sum_thread.t.join();
     VS_HIP(sum_err, "reading distances");
     if (obj) *obj = o;
+    x->km_prev_version = x->version;
+    x->km_prev_n = n;
+    x->km_prev_K = K;
     return VS_OK;
 }
 
@@ -2615,6 +2645,7 @@ int vs_index_set_option(vs_index *x, const char *name, int64_t value) {
         {"merge_mu", &VsOptions::merge_mu, 0, 8},
         {"merge_g", &VsOptions::merge_g, 0, 64},
         {"guess_div_log2", &VsOptions::guess_div_log2, 0, 10},
+        {"kmin_init", &VsOptions::kmin_init, 0, 1},
     };
     if (strcmp(name, "fail_alloc") == 0) {  // not a planner option: this thread's countdown
         if (value < 0) return set_err(VS_ERR_INVALID, "option fail_alloc: value %lld < 0", (long long)value);

@@ -77,6 +77,8 @@ struct ScanKArgs {
     int64_t out_cap;
     float kmin_margin;   // row-shared scan, k-means lists: each lane appends the values below
                          // its running minimum plus this margin
+    const float *kmin_init;  // k-means lists: per query, a value at or above the accumulator of
+                             // some scanned row (the running minimum starts there), or null
 };
 
 // Order-preserving map of finite floats to uint32 (a < b  <=>  enc(a) < enc(b)),

@@ -106,6 +106,8 @@ struct ScanPlan {
                           // running minimum + kmin_margin; a list that would fill is marked
                           // full, count cap + 1, and takes no more)
     float kmin_margin = 0.f;
+    const float *kmin_init = nullptr;  // k-means lists: per query (nq_pad entries), a value at or
+                                       // above the accumulator of some scanned row, or null
     int uncut = 0;        // streaming scan: lists are left uncut at the end and their entry
                           // counts written to list_cnt, as the row-shared scan's (for scans
                           // over short samples, whose lists end full)
@@ -261,6 +263,14 @@ hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, 
                               hipStream_t st);
 
 hipError_t launch_kmeans_count(const int32_t *assign, int64_t n, int32_t *counts, hipStream_t st);
+// |new_c - old_c| per centroid (upper bounds, fp64); old rows ld apart, new dense.
+hipError_t launch_kmeans_shift(const float *old_cen, int64_t ld, const float *new_cen, int64_t d,
+                               int64_t K, double *shift, hipStream_t st);
+// Starting values of the assign scan's running minima (kmin_init) from the
+// previous step's assignments and squared distances and the centroid shifts.
+hipError_t launch_kmeans_init(const int32_t *assign, const double *best_sq, const double *shift,
+                              const float *qnorm, int64_t n, int64_t n_pad, int64_t K, float bound,
+                              float *init, hipStream_t st);
 hipError_t launch_exclusive_scan_i32(const int32_t *in, int64_t n, int32_t *out, hipStream_t st);
 
 // Stable sort of (key, value) int32 pairs by key (rocPRIM radix sort).

@@ -667,6 +667,7 @@ hipError_t launch_scan_topk(const void *xb, int storage, int64_t ld, const float
     a.publish_block = 4 * plan.kk >= plan.kk_final;
     a.lbound = plan.kk < plan.kk_final ? lbound : nullptr;
     a.kmin_margin = plan.kmin_margin;
+    a.kmin_init = plan.kmin_init;
     return launch_scan_mode<0>(storage, pq, plan, a, st);
 }
 
@@ -2252,6 +2253,78 @@ hipError_t launch_kmeans_count(const int32_t *assign, int64_t n, int32_t *counts
     if (n <= 0) return hipSuccess;
     kmeans_count_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(assign, n,
                                                                                  counts);
+    return hipGetLastError();
+}
+
+// How far each centroid moved between two steps: one wave per centroid, an
+// upper bound on the Euclidean distance |new_c - old_c| (fp64 sum of the
+// squared differences, any order, times 1 + 1e-9; +inf when not finite).
+__global__ __launch_bounds__(256) void kmeans_shift_kernel(const float *__restrict__ old_cen,
+                                                           int64_t ld,
+                                                           const float *__restrict__ new_cen,
+                                                           int64_t d, int64_t K, double *shift) {
+    const int64_t c = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (c >= K) return;
+    double s = 0.0;
+    for (int64_t j = lane; j < d; j += 64) {
+        const double t = (double)new_cen[c * d + j] - (double)old_cen[c * ld + j];
+        s += t * t;
+    }
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    if (lane == 0) shift[c] = isfinite(s) ? sqrt(s) * (1.0 + 1e-9) : (double)VS_INF;
+}
+
+hipError_t launch_kmeans_shift(const float *old_cen, int64_t ld, const float *new_cen, int64_t d,
+                               int64_t K, double *shift, hipStream_t st) {
+    if (K <= 0) return hipSuccess;
+    kmeans_shift_kernel<<<dim3((unsigned)((K + 3) / 4)), dim3(256), 0, st>>>(old_cen, ld, new_cen,
+                                                                              d, K, shift);
+    return hipGetLastError();
+}
+
+// Starting values of the assign scan's running minima from the previous
+// step: point i was assigned centroid c at squared distance best_sq[i], and
+// c has since moved by at most shift[c], so (triangle inequality) its new
+// squared distance is at most (sqrt(best_sq) + shift)^2; in the scan's
+// accumulator space (|c|^2 - 2 x.c = squared distance - |x|^2, within
+// `bound` of the accumulator) that is at most
+//   (sqrt(best_sq) + shift)^2 (1 + 1e-9) - qnorm^2 (1 - 1e-6) + bound,
+// rounded up to fp32 (qnorm is |x| rounded to fp32).  Rows i >= n (query
+// padding) and anything not finite start at +inf (no bound).
+__global__ void kmeans_init_kernel(const int32_t *__restrict__ assign,
+                                   const double *__restrict__ best_sq,
+                                   const double *__restrict__ shift,
+                                   const float *__restrict__ qnorm, int64_t n, int64_t n_pad,
+                                   int64_t K, float bound, float *init) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_pad) return;
+    float f = VS_INF;
+    if (i < n) {
+        const int32_t c = assign[i];
+        const double b = best_sq[i];
+        if (c >= 0 && c < K && b >= 0.0 && isfinite(b)) {
+            const double r = sqrt(b) + shift[c];
+            const double qn = (double)qnorm[i];
+            const double v = r * r * (1.0 + 1e-9) - qn * qn * (1.0 - 1e-6) + (double)bound;
+            if (isfinite(v) && v < 1e37) {
+                f = (float)v;
+                if ((double)f < v)  // the next float up
+                    f = f == 0.f ? __uint_as_float(1u)
+                                 : __uint_as_float(f > 0.f ? __float_as_uint(f) + 1u
+                                                           : __float_as_uint(f) - 1u);
+            }
+        }
+    }
+    init[i] = f;
+}
+
+hipError_t launch_kmeans_init(const int32_t *assign, const double *best_sq, const double *shift,
+                              const float *qnorm, int64_t n, int64_t n_pad, int64_t K, float bound,
+                              float *init, hipStream_t st) {
+    if (n_pad <= 0) return hipSuccess;
+    kmeans_init_kernel<<<dim3((unsigned)((n_pad + 255) / 256)), dim3(256), 0, st>>>(
+        assign, best_sq, shift, qnorm, n, n_pad, K, bound, init);
     return hipGetLastError();
 }
 

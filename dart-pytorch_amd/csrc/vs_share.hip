@@ -64,7 +64,11 @@ size_t share_lds_bytes(int nks, int nqb, int rt, int cap) {
 // workgroup, ids 0).  The r-th smallest value of their union is the query's
 // r-th smallest over the rows whenever no lane met more than TOPM of those r,
 // and larger otherwise, never smaller.  MODE 4 (k-means lists): each lane
-// appends what lies below its own running minimum + kmin_margin.
+// appends what lies below its own running minimum + kmin_margin; with
+// kmin_init the minimum starts at the query's entry there, a value at or
+// above the accumulator of some row of the scan (so at or above the
+// smallest accumulator, which is then still appended: every list keeps what
+// lies below the smallest accumulator + kmin_margin).
 constexpr int kShareTopMEst = 4; // MODE 2: the estimate needs the 16 smallest of a sample
                                  // spread over many lanes; four slots keep insertions cheap
 
@@ -166,7 +170,8 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
     constexpr bool KMIN = MODE == 4;
     float best_r[KMIN ? NQB : 1];
 #pragma unroll
-    for (int qb = 0; qb < (KMIN ? NQB : 1); ++qb) best_r[qb] = VS_INF;
+    for (int qb = 0; qb < (KMIN ? NQB : 1); ++qb)
+        best_r[qb] = KMIN && a.kmin_init ? a.kmin_init[q0 + qw + qb * 16 + r16] : VS_INF;
     if constexpr (!KMIN) {
         gthr_load();
 #pragma unroll

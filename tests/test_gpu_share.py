@@ -168,6 +168,75 @@ def test_kmeans_lists_fp32_rows(vs, opts, km16, rt):
     _kmeans_check(vs, x, cen)
 
 
+def _kmeans_oracle_step(x, cen, u):
+    ar, _, objr = oracle.kmeans_assign(x, cen, NT)
+    cr, cntr, _ = oracle.kmeans_update(x, ar, cen, 1, u)
+    return ar, cr, cntr, objr
+
+
+def test_kmeans_running_minima_from_last_step(vs):
+    """Lloyd steps on one index: from the second step on, each point's
+    running minimum in the assign scan starts at a bound from its previous
+    centroid (previous squared distance, the centroid's shift, the
+    accumulator bound), so its list holds what lies within the margin of
+    the smallest accumulator.  Every step equals the oracle's step, and the
+    same steps with the option kmin_init = 0."""
+    x, _ = syn.gaussian_mixture(30_000, 256, 1024, 0.1, 48)
+    cen = x[syn.seeded_subset(30_000, 4096, 48)].copy()
+    u = syn.rng(49, 0).random(4096 * 256)
+    a = vs.GpuIndexFlat.l2(256, storage="f32")
+    b = vs.GpuIndexFlat.l2(256, storage="f32")
+    a.add(x)
+    b.add(x)
+    b.set_option("kmin_init", 0)
+    a.prof_enable(True)
+    c = cen
+    for step in range(3):
+        ra = vs.kmeans_step(a, c, 1, u)
+        rb = vs.kmeans_step(b, c, 1, u)
+        ar, cr, cntr, objr = _kmeans_oracle_step(x, c, u)
+        assert np.array_equal(ra[0], ar), f"step {step}: {np.sum(ra[0] != ar)} assignments differ"
+        assert ra[3] == objr and np.array_equal(ra[2], cntr)
+        assert np.array_equal(ra[1].view(np.uint32), cr.view(np.uint32))
+        assert np.array_equal(ra[0], rb[0]) and ra[3] == rb[3]
+        c = ra[1]
+    assert a.prof_get("kmin_init")[0] == 2
+    assert b.prof_get("kmin_init")[0] == 0
+    a.close()
+    b.close()
+
+
+def test_kmeans_running_minima_any_centroids(vs):
+    """The starting bound holds for whatever centroids the next call brings
+    (it only needs the previous centroid's shift): unrelated centroids,
+    the same ones permuted, and after a change of K (no bound then, as
+    after rows are added) all give the oracle's step."""
+    x, _ = syn.gaussian_mixture(20_000, 256, 256, 0.1, 50)
+    K = 1024
+    u = syn.rng(51, 0).random(2 * K * 256)
+    idx = vs.GpuIndexFlat.l2(256, storage="f32")
+    idx.add(x)
+    idx.prof_enable(True)
+    steps = [x[syn.seeded_subset(20_000, K, 50)].copy(),
+             x[syn.seeded_subset(20_000, K, 52)].copy()]  # unrelated
+    steps.append(steps[1][::-1].copy())                     # permuted
+    steps.append(x[syn.seeded_subset(20_000, K + 7, 53)].copy())  # K changes
+    for i, c in enumerate(steps):
+        r = vs.kmeans_step(idx, c, 1, u)
+        ar, cr, cntr, objr = _kmeans_oracle_step(x, c, u)
+        assert np.array_equal(r[0], ar), f"call {i}: {np.sum(r[0] != ar)} assignments differ"
+        assert r[3] == objr and np.array_equal(r[1].view(np.uint32), cr.view(np.uint32))
+    assert idx.prof_get("kmin_init")[0] == 2  # calls 1 and 2
+    idx.add(x[:5])  # new rows: the last step no longer describes these points
+    c = steps[3]
+    x2 = np.concatenate([x, x[:5]])
+    r = vs.kmeans_step(idx, c, 1, u)
+    ar, cr, _, objr = _kmeans_oracle_step(x2, c, u)
+    assert np.array_equal(r[0], ar) and r[3] == objr
+    assert idx.prof_get("kmin_init")[0] == 2
+    idx.close()
+
+
 def test_kmeans_second_step_grouped_order(vs):
     """The pick of a second step walks the points grouped by the first
     step's clusters (a permutation): the same assignments, objective and
