@@ -207,7 +207,7 @@ struct vs_index {
     // k-means: the points prepared as queries, kept while the rows are unchanged
     DevBuf km_qp, km_qf, km_qnorm;
     // k-means: pinned copies of the distances, assignments and new centroids
-    HostBuf km_hbest, km_hassign, km_hcen;
+    HostBuf km_hbest, km_hassign, km_hcen, km_hfb;
     HostBuf rstage;  // reconstruct: pinned staging of stored rows
     hipStream_t st_copy = nullptr;  // k-means: reads results back beside the update
     // k-means: km_order holds the last step's points grouped by cluster, for
@@ -217,7 +217,7 @@ struct vs_index {
     // k-means: km_assign / km_best / km_cen hold a whole step's assignments,
     // squared distances and centroids for these rows (version), points and K
     // (the next step's scan starts its running minima from them)
-    DevBuf km_shift, km_init;
+    DevBuf km_shift, km_init, km_pkeys, km_part;
     uint64_t km_prev_version = ~0ull;
     int64_t km_prev_n = 0, km_prev_K = 0;
     vs::PreparedQueries km_pq;
@@ -1529,11 +1529,13 @@ void vs_index_destroy(vs_index *x) {
                       &x->km_fb,   &x->km_keys,   &x->km_order, &x->km_tmp,   &x->km_counts,
                       &x->km_offsets, &x->km_out, &x->km_iota, &x->lcnt,   &x->km_qp,
                       &x->km_qf,   &x->km_qnorm,  &x->km_cen16, &x->km_c16n, &x->xb16,
-                      &x->xb16n,   &x->vx,        &x->ctl,      &x->km_shift, &x->km_init};
+                      &x->xb16n,   &x->vx,        &x->ctl,      &x->km_shift, &x->km_init,
+                      &x->km_pkeys, &x->km_part};
     for (DevBuf *b : bufs) b->release();
     x->km_hbest.release();
     x->km_hassign.release();
     x->km_hcen.release();
+    x->km_hfb.release();
     x->rstage.release();
     if (x->st_copy) {
         (void)hipStreamSynchronize(x->st_copy);
@@ -2147,21 +2149,129 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     int32_t *fb_count = x->km_fb.as<int32_t>();
     int32_t *fb_list = fb_count + 1;
     VS_HIP(hipMemsetAsync(x->flags.p, 0, sizeof(uint32_t), x->st), "clearing flags");
+    // distances and assignments go to pinned memory on a second stream, so
+    // that the copies overlap the GPU's later work
+    constexpr int kSumChunks = 4;
+    VS_HIP(x->km_hbest.ensure((size_t)n * 8), "pinned distances");
+    VS_HIP(x->km_hassign.ensure((size_t)n * 4), "pinned assignments");
+    VS_HIP(x->km_hcen.ensure((size_t)K * d * 4), "pinned centroids");
+    VS_HIP(x->km_hfb.ensure((size_t)kSumChunks * 4), "pinned fallback counts");
+    if (!x->st_copy)
+        VS_HIP(hipStreamCreateWithFlags(&x->st_copy, hipStreamNonBlocking), "copy stream");
+    // The objective is a sequential fp64 sum over the points in index order
+    // (kmeans.dart:104): a chain of n dependent adds on the host.  Over the
+    // row-shared scan's lists the pick runs in kSumChunks launches over
+    // consecutive point ranges (each range's points in the previous step's
+    // grouped order), and each range's distances and assignments come over
+    // with the fallback count so far as soon as its pick ends: the sum of a
+    // range, and the copy of its assignments into the caller's buffer, run
+    // while the GPU picks the next ones.  From the first range with a
+    // fallback point on, both wait for the exhaustive pass.
+    struct EvGuard {
+        hipEvent_t e = nullptr;
+        ~EvGuard() {
+            if (e) (void)hipEventDestroy(e);
+        }
+    } ev_pick[kSumChunks], ev_best[kSumChunks], ev_fix;
+    for (auto &e : ev_pick) VS_HIP(hipEventCreateWithFlags(&e.e, hipEventDisableTiming), "event");
+    for (auto &e : ev_best) VS_HIP(hipEventCreateWithFlags(&e.e, hipEventDisableTiming), "event");
+    VS_HIP(hipEventCreateWithFlags(&ev_fix.e, hipEventDisableTiming), "event");
+    // the copy stream is drained before this call returns (below, and on
+    // every error path), so the next call cannot overwrite what it reads
+    struct CopyDrain {
+        hipStream_t s;
+        ~CopyDrain() { (void)hipStreamSynchronize(s); }
+    } drain{x->st_copy};
+    const bool chunked = plan.kind == 3 && plan.share_kmin;
+    const int32_t *order = x->km_order_version == x->version && x->km_order_n == n &&
+                                   x->opt.pick_order
+                               ? x->km_order.as<int32_t>()
+                               : nullptr;
+    if (chunked && order) {
+        // each range's points in walk order at that same range: a stable
+        // partition of the order by range
+        VS_HIP(x->km_pkeys.ensure((size_t)n * 4), "range keys");
+        VS_HIP(x->km_part.ensure((size_t)n * 4), "range order");
+        VS_HIP(x->km_keys.ensure((size_t)n * 4), "sort keys");
+        VS_HIP(vs::launch_chunk_keys(order, n, kSumChunks, x->km_pkeys.as<int32_t>(), x->st),
+               "range keys");
+        size_t pbytes = 0;
+        VS_HIP(vs::sort_pairs_by_key(nullptr, pbytes, x->km_pkeys.as<int32_t>(),
+                                     x->km_keys.as<int32_t>(), order, x->km_part.as<int32_t>(), n,
+                                     2, x->st),
+               "sort size");
+        VS_HIP(x->km_tmp.ensure(pbytes + 16), "sort scratch");
+        VS_HIP(vs::sort_pairs_by_key(x->km_tmp.p, pbytes, x->km_pkeys.as<int32_t>(),
+                                     x->km_keys.as<int32_t>(), order, x->km_part.as<int32_t>(), n,
+                                     2, x->st),
+               "range order");
+        order = x->km_part.as<int32_t>();
+    }
     {
         ProfScope ps(x, "pick");
-        VS_HIP(vs::launch_kmeans_pick((const float *)x->xb, ld, d, n, x->km_cen.as<float>(), K,
-                                      x->cand_v.as<float>(), x->cand_i.as<int32_t>(),
-                                      x->gthr.as<uint32_t>(), plan, bound,
-                                      pq.qf, x->km_assign.as<int32_t>(), x->km_best.as<double>(),
-                                      fb_count, fb_list, x->flags.as<uint32_t>(),
-                                      x->lcnt.as<int32_t>(),
-                                      x->km_order_version == x->version && x->km_order_n == n &&
-                                              x->opt.pick_order
-                                          ? x->km_order.as<int32_t>()
-                                          : nullptr,
-                                      x->st),
-               "assign pick");
+        const int npick = chunked ? kSumChunks : 1;
+        for (int c = 0; c < npick; ++c) {
+            const int64_t s0 = n * c / npick, s1 = n * (c + 1) / npick;
+            VS_HIP(vs::launch_kmeans_pick((const float *)x->xb, ld, d, n, x->km_cen.as<float>(), K,
+                                          x->cand_v.as<float>(), x->cand_i.as<int32_t>(),
+                                          x->gthr.as<uint32_t>(), plan, bound, pq.qf,
+                                          x->km_assign.as<int32_t>(), x->km_best.as<double>(),
+                                          fb_count, fb_list, x->flags.as<uint32_t>(),
+                                          x->lcnt.as<int32_t>(), order ? order + s0 : nullptr,
+                                          x->st, s0, s1 - s0),
+                   "assign pick");
+            VS_HIP(hipEventRecord(ev_pick[c].e, x->st), "event");
+        }
     }
+    int32_t *hfb = x->km_hfb.as<int32_t>();
+    for (int c = 0; c < kSumChunks; ++c) {
+        const int64_t i0 = n * c / kSumChunks, i1 = n * (c + 1) / kSumChunks;
+        VS_HIP(hipStreamWaitEvent(x->st_copy, ev_pick[chunked ? c : 0].e, 0), "event");
+        if (i1 > i0) {
+            VS_HIP(hipMemcpyAsync(x->km_hbest.as<double>() + i0, x->km_best.as<double>() + i0,
+                                  (size_t)(i1 - i0) * 8, hipMemcpyDeviceToHost, x->st_copy),
+                   "reading distances");
+            VS_HIP(hipMemcpyAsync(x->km_hassign.as<int32_t>() + i0,
+                                  x->km_assign.as<int32_t>() + i0, (size_t)(i1 - i0) * 4,
+                                  hipMemcpyDeviceToHost, x->st_copy),
+                   "reading assignments");
+        }
+        VS_HIP(hipMemcpyAsync(hfb + c, fb_count, 4, hipMemcpyDeviceToHost, x->st_copy),
+               "reading fallback counts");
+        VS_HIP(hipEventRecord(ev_best[c].e, x->st_copy), "event");
+    }
+    // the sum and the assignments, on a helper thread, up to the first range
+    // with a fallback point (`dirty`; the rest follow here after the
+    // exhaustive pass)
+    double o = 0.0;
+    int dirty = kSumChunks;
+    hipError_t sum_err = hipSuccess;
+    struct Join {
+        std::thread t;
+        ~Join() {
+            if (t.joinable()) t.join();
+        }
+    } sum_thread{std::thread([&o, &dirty, &sum_err, &ev_best, hfb, assign,
+                              best = x->km_hbest.as<double>(),
+                              hassign = x->km_hassign.as<int32_t>(), n] {
+        double acc = 0.0;
+        for (int c = 0; c < kSumChunks; ++c) {
+            const hipError_t e = hipEventSynchronize(ev_best[c].e);
+            if (e != hipSuccess) {
+                sum_err = e;
+                return;
+            }
+            if (hfb[c] > 0) {
+                dirty = c;
+                break;
+            }
+            const int64_t i0 = n * c / kSumChunks, i1 = n * (c + 1) / kSumChunks;
+            for (int64_t i = i0; i < i1; ++i) acc += best[i];
+            memcpy(assign + i0, hassign + i0, (size_t)(i1 - i0) * 4);
+        }
+        o = acc;
+    })};
+
     int32_t nfb = 0;
     uint32_t pflags = 0;
     VS_HIP(hipMemcpyAsync(&nfb, fb_count, 4, hipMemcpyDeviceToHost, x->st), "fallbacks");
@@ -2170,74 +2280,35 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     if (pflags & vs::kFlagBadId)
         return set_err(VS_ERR_HIP, "internal error: a k-means candidate outside the centroids");
     x->prof["kmeans_fallback_points"].launches += nfb;
+    int64_t refetch = n;  // distances from here on are read again after the exhaustive pass
     if (nfb > 0) {
-        ProfScope ps(x, "exhaustive");
-        VS_HIP(vs::launch_kmeans_exhaustive((const float *)x->xb, ld, d, x->km_cen.as<float>(), K,
-                                            fb_list, nfb, x->km_assign.as<int32_t>(),
-                                            x->km_best.as<double>(), x->st),
-               "exhaustive assign");
+        {
+            ProfScope ps(x, "exhaustive");
+            VS_HIP(vs::launch_kmeans_exhaustive((const float *)x->xb, ld, d,
+                                                x->km_cen.as<float>(), K, fb_list, nfb,
+                                                x->km_assign.as<int32_t>(),
+                                                x->km_best.as<double>(), x->st),
+                   "exhaustive assign");
+        }
+        // the ranges' fallback counts are all in (the sum thread stops at
+        // the first nonzero one, and never reads past it)
+        VS_HIP(hipEventSynchronize(ev_best[kSumChunks - 1].e), "reading fallback counts");
+        int first = 0;
+        while (first < kSumChunks && hfb[first] == 0) ++first;
+        refetch = n * first / kSumChunks;
     }
-    // distances and assignments to pinned memory; the host sums the objective
-    // while the update runs
-    VS_HIP(x->km_hbest.ensure((size_t)n * 8), "pinned distances");
-    VS_HIP(x->km_hassign.ensure((size_t)n * 4), "pinned assignments");
-    VS_HIP(x->km_hcen.ensure((size_t)K * d * 4), "pinned centroids");
-    // on a second stream, so that the copies overlap the grouping and update
-    if (!x->st_copy)
-        VS_HIP(hipStreamCreateWithFlags(&x->st_copy, hipStreamNonBlocking), "copy stream");
-    // the distances come over in kSumChunks pieces, each followed by an
-    // event, so that the objective's sum starts with the first piece
-    constexpr int kSumChunks = 8;
-    struct EvGuard {
-        hipEvent_t e = nullptr;
-        ~EvGuard() {
-            if (e) (void)hipEventDestroy(e);
-        }
-    } ev_pick, ev_best[kSumChunks];
-    VS_HIP(hipEventCreateWithFlags(&ev_pick.e, hipEventDisableTiming), "event");
-    for (auto &e : ev_best) VS_HIP(hipEventCreateWithFlags(&e.e, hipEventDisableTiming), "event");
-    VS_HIP(hipEventRecord(ev_pick.e, x->st), "event");
-    VS_HIP(hipStreamWaitEvent(x->st_copy, ev_pick.e, 0), "event");
-    // the copy stream is drained before this call returns (below, and on
-    // every error path), so the next call cannot overwrite what it reads
-    struct CopyDrain {
-        hipStream_t s;
-        ~CopyDrain() { (void)hipStreamSynchronize(s); }
-    } drain{x->st_copy};
-    for (int c = 0; c < kSumChunks; ++c) {
-        const int64_t i0 = n * c / kSumChunks, i1 = n * (c + 1) / kSumChunks;
-        if (i1 > i0)
-            VS_HIP(hipMemcpyAsync(x->km_hbest.as<double>() + i0, x->km_best.as<double>() + i0,
-                                  (size_t)(i1 - i0) * 8, hipMemcpyDeviceToHost, x->st_copy),
-                   "reading distances");
-        VS_HIP(hipEventRecord(ev_best[c].e, x->st_copy), "event");
+    if (refetch < n) {
+        VS_HIP(hipEventRecord(ev_fix.e, x->st), "event");
+        VS_HIP(hipStreamWaitEvent(x->st_copy, ev_fix.e, 0), "event");
+        VS_HIP(hipMemcpyAsync(x->km_hbest.as<double>() + refetch,
+                              x->km_best.as<double>() + refetch, (size_t)(n - refetch) * 8,
+                              hipMemcpyDeviceToHost, x->st_copy),
+               "reading distances");
+        VS_HIP(hipMemcpyAsync(x->km_hassign.as<int32_t>() + refetch,
+                              x->km_assign.as<int32_t>() + refetch, (size_t)(n - refetch) * 4,
+                              hipMemcpyDeviceToHost, x->st_copy),
+               "reading assignments");
     }
-    VS_HIP(hipMemcpyAsync(x->km_hassign.p, x->km_assign.p, (size_t)n * 4, hipMemcpyDeviceToHost,
-                          x->st_copy),
-           "reading assignments");
-    // objective: fp64 sum in point order (kmeans.dart:104), on a helper
-    // thread while the update runs and this thread copies the results out
-    // (a sequential sum of n values is a chain of n dependent adds)
-    double o = 0.0;
-    hipError_t sum_err = hipSuccess;
-    struct Join {
-        std::thread t;
-        ~Join() {
-            if (t.joinable()) t.join();
-        }
-    } sum_thread{std::thread([&o, &sum_err, &ev_best, best = x->km_hbest.as<double>(), n] {
-        double acc = 0.0;
-        for (int c = 0; c < kSumChunks; ++c) {
-            const hipError_t e = hipEventSynchronize(ev_best[c].e);
-            if (e != hipSuccess) {
-                sum_err = e;
-                return;
-            }
-            const int64_t i1 = n * (c + 1) / kSumChunks;
-            for (int64_t i = n * c / kSumChunks; i < i1; ++i) acc += best[i];
-        }
-        o = acc;
-    })};
 
     // update: counts, stable grouping by cluster, ordered fp32 sums
     VS_HIP(x->km_counts.ensure((size_t)K * 4), "counts");
@@ -2297,34 +2368,44 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
            "reading centroids");
     VS_HIP(hipMemcpyAsync(counts, x->km_counts.p, (size_t)K * 4, hipMemcpyDeviceToHost, x->st),
            "reading counts");
-    VS_HIP(hipStreamSynchronize(x->st_copy), "reading assignments");
-    memcpy(assign, x->km_hassign.p, (size_t)n * 4);
     VS_HIP(hipStreamSynchronize(x->st), "update");
-    std::vector<float> cen_new(x->km_hcen.as<float>(), x->km_hcen.as<float>() + K * d);
+
     // empty clusters, in centroid order, in place (kmeans.dart:127-139): the
     // largest cluster's centroid holds its new value when it precedes c, and
     // still its old one otherwise (c itself included)
     // (the loop changes no count, so the largest cluster -- the first of the
     // largest count -- is the same for every empty one)
-    int64_t big = 0;
+    int64_t big = 0, nempty = 0;
     for (int64_t cc = 1; cc < K; ++cc)
         if (counts[cc] > counts[big]) big = cc;
+    for (int64_t c = 0; c < K; ++c) nempty += counts[c] < min_points ? 1 : 0;
+    if (nempty * d > njitter)
+        return set_err(VS_ERR_INVALID, "empty cluster needs more jitter values than the %lld given",
+                       (long long)njitter);
+    // the new centroids straight into the caller's buffer (an input it
+    // aliases was copied above)
+    float *cen_new = centroids_out;
+    memcpy(cen_new, x->km_hcen.p, (size_t)K * d * 4);
     int64_t used = 0;
     for (int64_t c = 0; c < K; ++c) {
         if (counts[c] >= min_points) continue;
         const float *src = big < c ? &cen_new[(size_t)(big * d)] : &cen_in[(size_t)(big * d)];
         for (int64_t j = 0; j < d; ++j) {
-            if (used >= njitter)
-                return set_err(VS_ERR_INVALID,
-                               "empty cluster needs more jitter values than the %lld given",
-                               (long long)njitter);
             const double jit = (jitter_u[used++] - 0.5) * 1e-4;
             cen_new[(size_t)(c * d + j)] = (float)((double)src[j] + jit);
         }
     }
-    memcpy(centroids_out, cen_new.data(), (size_t)K * d * 4);
     sum_thread.t.join();
     VS_HIP(sum_err, "reading distances");
+    if (dirty < kSumChunks) {  // the ranges after the exhaustive pass
+        VS_HIP(hipStreamSynchronize(x->st_copy), "reading distances");
+        const double *best = x->km_hbest.as<double>();
+        const int64_t i0 = n * dirty / kSumChunks;
+        double acc = o;
+        for (int64_t i = i0; i < n; ++i) acc += best[i];
+        o = acc;
+        memcpy(assign + i0, x->km_hassign.as<int32_t>() + i0, (size_t)(n - i0) * 4);
+    }
     if (obj) *obj = o;
     x->km_prev_version = x->version;
     x->km_prev_n = n;

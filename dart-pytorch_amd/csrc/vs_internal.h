@@ -260,7 +260,12 @@ hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, 
                               const float *qf, int32_t *assign,
                               double *best_sq, int32_t *fallback_count, int32_t *fallback_list,
                               uint32_t *flags, const int32_t *list_cnt, const int32_t *order,
-                              hipStream_t st);
+                              hipStream_t st, int64_t slot0 = 0, int64_t nslots = -1);
+// (row-shared k-means lists only) slots [slot0, slot0 + nslots) of the walk:
+// points order[0 .. nslots) when order is given (the caller passes the
+// chunk's part of it), else points slot0 .. slot0 + nslots - 1.
+hipError_t launch_chunk_keys(const int32_t *order, int64_t n, int nchunk, int32_t *key,
+                             hipStream_t st);
 
 hipError_t launch_kmeans_count(const int32_t *assign, int64_t n, int32_t *counts, hipStream_t st);
 // |new_c - old_c| per centroid (upper bounds, fp64); old rows ld apart, new dense.

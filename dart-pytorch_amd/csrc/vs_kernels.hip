@@ -745,7 +745,8 @@ struct MergeKArgs {
     int guess;            // thresholds were estimated: flag queries left short
     int seed_rank;        // MODE 2: rank whose value sets the threshold (0: kk)
     float kmin_margin;    // k-means pick over the row-shared scan's k-means lists
-    const int32_t *order; // k-means pick: points in this order (a permutation of [0, nq)), or null
+    const int32_t *order; // k-means pick: slot s is point order[s] (nq slots), or null:
+    int64_t slot0;        // point slot0 + s
     int64_t k;
     float *D;
     int32_t *I;
@@ -1592,8 +1593,13 @@ hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, 
                               const float *qf, int32_t *assign,
                               double *best_sq, int32_t *fallback_count, int32_t *fallback_list,
                               uint32_t *flags, const int32_t *list_cnt, const int32_t *order,
-                              hipStream_t st) {
+                              hipStream_t st, int64_t slot0, int64_t nslots) {
     if (n <= 0) return hipSuccess;
+    if (nslots < 0) nslots = n;
+    if (slot0 < 0 || slot0 + nslots > n ||
+        ((slot0 > 0 || nslots < n) && !(plan.kind == 3 && plan.share_kmin)))
+        return hipErrorInvalidValue;
+    if (nslots == 0) return hipSuccess;
     MergeKArgs a{};
     a.xb = cen;
     a.pts = x;
@@ -1626,6 +1632,8 @@ hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, 
         a.kmin_margin = plan.kmin_margin;
         a.kl = plan.cap;
         a.order = order;
+        a.slot0 = slot0;
+        a.nq = nslots;
         // points grouped by the previous step's clusters share candidates:
         // each distinct one is staged once per wave; in index order (the
         // first step) they share few, and slot-by-slot staging is faster
@@ -1633,10 +1641,10 @@ hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, 
         // 4.19 ms in index order)
         if (K <= kPickSetMaxK && order)
             kmeans_pick_set_kernel<32, 16>
-                <<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(a);
+                <<<dim3((unsigned)((nslots + 255) / 256)), dim3(256), 0, st>>>(a);
         else
             kmeans_pick_wave_kernel<32, 16>
-                <<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(a);
+                <<<dim3((unsigned)((nslots + 255) / 256)), dim3(256), 0, st>>>(a);
         return hipGetLastError();
     }
     if (plan.kind == 3) return hipErrorInvalidValue;  // row-shared lists are k-means lists only
@@ -1878,8 +1886,8 @@ __global__ __launch_bounds__(256) void kmeans_pick_wave_kernel(MergeKArgs a) {
     const int64_t p0 = ((int64_t)blockIdx.x * 4 + wave) * 64;
     if (p0 >= a.nq) return;  // whole waves only: every lane below stays to the end
     // slot s of the walk is point order[s] (the previous step's grouping by
-    // cluster: a wave's points then share most candidates), or s itself
-    auto point = [&](int64_t s) -> int64_t { return a.order ? (int64_t)a.order[s] : s; };
+    // cluster: a wave's points then share most candidates), or slot0 + s
+    auto point = [&](int64_t s) -> int64_t { return a.order ? (int64_t)a.order[s] : a.slot0 + s; };
     const bool live = p0 + lane < a.nq;
     // lanes past the end mirror the wave's first point
     const int64_t qg = point(live ? p0 + lane : p0);
@@ -1996,7 +2004,7 @@ __global__ __launch_bounds__(256) void kmeans_pick_set_kernel(MergeKArgs a) {
     unsigned long long *bits = bits_all[wave];
     const int64_t p0 = ((int64_t)blockIdx.x * 4 + wave) * 64;
     if (p0 >= a.nq) return;  // whole waves only: every lane below stays to the end
-    auto point = [&](int64_t s) -> int64_t { return a.order ? (int64_t)a.order[s] : s; };
+    auto point = [&](int64_t s) -> int64_t { return a.order ? (int64_t)a.order[s] : a.slot0 + s; };
     const bool live = p0 + lane < a.nq;
     const int64_t qg = point(live ? p0 + lane : p0);  // lanes past the end mirror the first point
     const int kw = (int)((a.nrows + 63) / 64);         // bitmap words in use (<= KW)
@@ -2253,6 +2261,27 @@ hipError_t launch_kmeans_count(const int32_t *assign, int64_t n, int32_t *counts
     if (n <= 0) return hipSuccess;
     kmeans_count_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(assign, n,
                                                                                  counts);
+    return hipGetLastError();
+}
+
+// Chunk of each point of a walk order: key[j] = c for order[j] in
+// [n c / nchunk, n (c + 1) / nchunk) (a stable sort by these keys puts each
+// chunk's points, in walk order, at that same range).
+__global__ void chunk_keys_kernel(const int32_t *__restrict__ order, int64_t n, int nchunk,
+                                  int32_t *key) {
+    const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= n) return;
+    const int64_t v = order[j];
+    int c = 0;
+    for (int t = 1; t < nchunk; ++t) c += v >= n * t / nchunk ? 1 : 0;
+    key[j] = c;
+}
+
+hipError_t launch_chunk_keys(const int32_t *order, int64_t n, int nchunk, int32_t *key,
+                             hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    chunk_keys_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(order, n, nchunk,
+                                                                               key);
     return hipGetLastError();
 }
 

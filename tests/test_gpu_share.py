@@ -146,6 +146,36 @@ def test_kmeans_register_shortlists_fallback(vs):
     assert not np.any((a >= 100) & (a < 140))
 
 
+def test_kmeans_fallback_in_last_range_only(vs):
+    """The pick runs over four consecutive point ranges and the objective's
+    sequential sum starts on each range as soon as its pick ends; here only
+    the last range's points have more tied candidates than the pick's 32
+    slots, so the first three ranges are summed at once and the last after
+    the exhaustive pass.  Assignments, objective (bit for bit) and centroids
+    equal the oracle's, on that step and on the next one (grouped order)."""
+    d = 256
+    x1, _ = syn.gaussian_mixture(4500, d, 16, 0.1, 54)
+    v = np.full(d, 3.0 / np.sqrt(d), np.float32) + x1.max()
+    x2 = (v + 0.01 * syn.rng(55, 0).standard_normal((1500, d))).astype(np.float32)
+    x = np.concatenate([x1, x2])
+    cen = np.concatenate([x1[syn.seeded_subset(4500, 300, 54)], np.tile(v, (40, 1))])
+    u = syn.rng(56, 0).random(len(cen) * d)
+    idx = vs.GpuIndexFlat.l2(d, storage="f32")
+    idx.add(x)
+    c = cen
+    for step in range(2):
+        before = idx.prof_get("kmeans_fallback_points")[0]
+        a, newc, cnt, obj = vs.kmeans_step(idx, c, 1, u)
+        if step == 0:
+            assert idx.prof_get("kmeans_fallback_points")[0] > before
+        ar, cr, cntr, objr = _kmeans_oracle_step(x, c, u)
+        assert np.array_equal(a, ar), f"step {step}: {np.sum(a != ar)} assignments differ"
+        assert obj == objr and np.array_equal(cnt, cntr)
+        assert np.array_equal(newc.view(np.uint32), cr.view(np.uint32))
+        c = newc
+    idx.close()
+
+
 def test_kmeans_lists_full(vs):
     """Three hundred copies of one centroid overflow the points' k-means
     lists (more than cap - 16 appends): the lists are marked full and their
