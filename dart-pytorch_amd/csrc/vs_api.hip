@@ -461,10 +461,11 @@ bool plan_share(const vs_index *x, int64_t nq, int64_t nrows, int planes, int st
     // fp32 tiles: half the rows, the same staging registers
     const int rt = storage == 1 ? (nks == 4 ? 8 : 4) : 2;
     // a list of the row-shared scan gains up to 16 entries per 16-row block
-    // and query; 256 slots at least keep cuts rare while its threshold is
+    // and query, and is cut to kk before a tile when it holds more than
+    // cap - 16 rt; 256 slots at least keep cuts rare while its threshold is
     // still loose (the list is sorted only up to its fill)
     const int kk = p->kk_final;
-    const int cap = (int)std::max<int64_t>(256, next_pow2(kk + 48));
+    const int cap = (int)std::max<int64_t>(256, next_pow2(kk + std::max(48, 16 * rt)));
     const size_t lds = vs::share_lds_bytes(nks, nqb, rt, cap);
     if (lds > x->lds_max) return false;
     p->kind = 3;

@@ -268,39 +268,24 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
                 pass |= m4[qb] < thr_r[qb];
             }
             if (!__ballot(pass)) return;
-            // make room: a list that may gain entries here (at most 16: four
-            // lanes of four rows) and holds more than cap - 16 is cut first
-            // (k-means lists are marked full instead, count cap + 1: their
-            // points go to the exhaustive search).  The counts live in LDS;
-            // only lanes with a passing value read them.
-            {
+            // k-means lists: one that may gain entries here (at most 16: four
+            // lanes of four rows) and holds more than cap - 16 is marked
+            // full, count cap + 1 (its point goes to the exhaustive search).
+            // The counts live in LDS; only lanes with a passing value read
+            // them.  (Top-k lists are cut before each tile instead.)
+            if constexpr (KMIN) {
                 bool need = false;
 #pragma unroll
                 for (int qb = 0; qb < NQB; ++qb)
                     if (m4[qb] < thr_r[qb]) need |= cnt_w[qb * 16 + r16] > a.cap - 16;
                 if (__ballot(need)) {
-                    if constexpr (KMIN) {
 #pragma unroll
-                        for (int qb = 0; qb < NQB; ++qb) {
-                            const int q = qb * 16 + r16;
-                            if (cnt_w[q] > a.cap - 16) {
-                                thr_r[qb] = -VS_INF;
-                                if (g == 0) cnt_w[q] = a.cap + 1;
-                            }
+                    for (int qb = 0; qb < NQB; ++qb) {
+                        const int q = qb * 16 + r16;
+                        if (cnt_w[q] > a.cap - 16) {
+                            thr_r[qb] = -VS_INF;
+                            if (g == 0) cnt_w[q] = a.cap + 1;
                         }
-                    } else {
-                        lds_wave_sync();
-                        for (int q = 0; q < BNW; ++q) {
-                            if (cnt_w[q] > a.cap - 16)
-                                flush_list(cv + (int64_t)(qw + q) * a.cap,
-                                           ci + (int64_t)(qw + q) * a.cap, &cnt_w[q], &thr_w[q],
-                                           &thr_w[q], S::BN, 1, &a.gthr[q0 + qw + q], sv_w, si_w,
-                                           a.cap, a.kk, a.kk_final, 0, lane);
-                        }
-                        lds_wave_sync();
-#pragma unroll
-                        for (int qb = 0; qb < NQB; ++qb)
-                            thr_r[qb] = fminf(thr_r[qb], thr_w[qb * 16 + r16]);
                     }
                     lds_wave_sync();
                 }
@@ -331,6 +316,33 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
             }
             lds_wave_sync();
         };
+        if constexpr (MODE == 0) {
+            // a list gains at most 16 entries per row block (four lanes of
+            // four rows): one holding more than cap - TR is cut to its kk
+            // best before the tile (the planner's cap >= kk + TR), so the
+            // row blocks' epilogues never check for room (measured on C2:
+            // 2.74 -> 2.49 ms against a check per row block)
+            bool need = false;
+            int cq[NQB];
+#pragma unroll
+            for (int qb = 0; qb < NQB; ++qb) cq[qb] = cnt_w[qb * 16 + r16];
+#pragma unroll
+            for (int qb = 0; qb < NQB; ++qb) need |= cq[qb] > a.cap - TR;
+            if (__ballot(need)) {
+                lds_wave_sync();
+                for (int q = 0; q < BNW; ++q) {
+                    if (cnt_w[q] > a.cap - TR)
+                        flush_list(cv + (int64_t)(qw + q) * a.cap, ci + (int64_t)(qw + q) * a.cap,
+                                   &cnt_w[q], &thr_w[q], &thr_w[q], S::BN, 1,
+                                   &a.gthr[q0 + qw + q], sv_w, si_w, a.cap, a.kk, a.kk_final, 0,
+                                   lane);
+                }
+                lds_wave_sync();
+#pragma unroll
+                for (int qb = 0; qb < NQB; ++qb) thr_r[qb] = fminf(thr_r[qb], thr_w[qb * 16 + r16]);
+                lds_wave_sync();
+            }
+        }
         f32x4_t accs[2][NQB];
         mma(0, accs[0]);
 #pragma unroll
@@ -442,7 +454,8 @@ int share_blocks_per_cu(int st, int nks, int bn, int rt, int64_t ld, size_t lds,
 }
 
 hipError_t launch_share_scan(const ScanPlan &plan, const ScanKArgs &args, hipStream_t st) {
-    if (plan.kk != plan.kk_final || plan.cap < plan.kk + 16 || plan.lw != 1 || !args.list_cnt)
+    if (plan.kk != plan.kk_final || plan.cap < plan.kk + 16 * plan.tm || plan.lw != 1 ||
+        !args.list_cnt)
         return hipErrorInvalidValue;
     if (plan.share_topm && (plan.share_topm != kShareTopMEst || plan.cap < 4 * plan.share_topm))
         return hipErrorInvalidValue;
