@@ -189,6 +189,8 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
     int par = 0;
     for (int64_t t0 = r0; t0 < r1; t0 += TR) {
         const int64_t tn = t0 + TR;
+        // rows of the tile inside the split (32-bit: scalar compares below)
+        const int rows_in = (int)min((int64_t)TR, r1 - t0);
         const bool more = tn < r1;
         if constexpr (!KMIN) gthr_load();
         if (more) gload(tn);
@@ -213,10 +215,10 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
         };
         auto epi = [&](int rb, f32x4_t (&acc)[NQB]) __attribute__((always_inline)) {
             const int64_t rbase = t0 + rb * 16 + 4 * g;  // the lane's first row
-            if (t0 + rb * 16 + 16 > r1) {  // rows past the split end never qualify
+            if (rb * 16 + 16 > rows_in) {  // rows past the split end never qualify
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    if (rbase + i >= r1) {
+                    if (rb * 16 + 4 * g + i >= rows_in) {
 #pragma unroll
                         for (int qb = 0; qb < NQB; ++qb) acc[qb][i] = VS_INF;
                     }
