@@ -225,24 +225,38 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
             }
 
             if constexpr (TOPMODE) {
-                // sorted insertion of each value below the lane's TOPM-th
+                // the four smallest of the lane's four (sorted) and its four
+                // new values, branch-free: sort the new ones (five
+                // compare-exchanges), pair the two sorted runs head to tail
+                // (the smaller of each pair: a bitonic run holding the four
+                // smallest), sort that (four compare-exchanges).  While the
+                // slots fill, nearly every wave has a lane taking each value,
+                // where a per-value insertion cost four compare-exchanges.
+                static_assert(TOPM == 4, "a merge of two sorted runs of four");
+                auto cx = [](float &x, float &y) __attribute__((always_inline)) {
+                    const float lo = fminf(x, y);
+                    y = fmaxf(x, y);
+                    x = lo;
+                };
 #pragma unroll
                 for (int qb = 0; qb < NQB; ++qb) {
-                    const float m4 =
-                        fminf(fminf(acc[qb][0], acc[qb][1]), fminf(acc[qb][2], acc[qb][3]));
-                    if (!__ballot(m4 < top[qb][TOPM - 1])) continue;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        float v = acc[qb][i];
-                        if (v < top[qb][TOPM - 1]) {
-#pragma unroll
-                            for (int m = 0; m < TOPM; ++m) {
-                                const float lo = fminf(top[qb][m], v);
-                                v = fmaxf(top[qb][m], v);
-                                top[qb][m] = lo;
-                            }
-                        }
-                    }
+                    float v0 = acc[qb][0], v1 = acc[qb][1], v2 = acc[qb][2], v3 = acc[qb][3];
+                    if (!__ballot(fminf(fminf(v0, v1), fminf(v2, v3)) < top[qb][3])) continue;
+                    cx(v0, v1);
+                    cx(v2, v3);
+                    cx(v0, v2);
+                    cx(v1, v3);
+                    cx(v1, v2);
+                    float c0 = fminf(top[qb][0], v3), c1 = fminf(top[qb][1], v2);
+                    float c2 = fminf(top[qb][2], v1), c3 = fminf(top[qb][3], v0);
+                    cx(c0, c2);
+                    cx(c1, c3);
+                    cx(c0, c1);
+                    cx(c2, c3);
+                    top[qb][0] = c0;
+                    top[qb][1] = c1;
+                    top[qb][2] = c2;
+                    top[qb][3] = c3;
                 }
                 return;
             }
