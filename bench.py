@@ -299,13 +299,22 @@ def run_search(vs, NN, workload, args, ctx, full=False):
         from vector_store.bench import (BenchOptions, bench_index, to_bench_csv,
                                         to_bench_markdown)
 
-        nb, npq = min(nq, 512), min(nq, 128)
-        Dt, It = oracle.flat_search(xb, xq[:nb], k, metric, ctx["host"]["threads_all_core"])
+        # bench_faiss.dart:55-103's four flat rows on one query set: the CPU
+        # IndexFlat (the oracle on all host threads; a single query runs on
+        # one) and GpuIndexFlat, per query and batched
+        th = ctx["host"]["threads_all_core"]
+        nb = min(nq, 32)
+        Dt, It = oracle.flat_search(xb, xq[:nb], k, metric, th)
         truth = SearchResult(Dt, It)
-        rows = [bench_index(idx, xq[:nb], k, truth, label="GpuIndexFlat [batched]",
-                            options=BenchOptions(warmup=1, repeats=3, per_query=False)),
-                bench_index(idx, xq[:npq], k, SearchResult(Dt[:npq], It[:npq]),
-                            label="GpuIndexFlat", options=BenchOptions(warmup=1, repeats=3))]
+        cpu = oracle.FlatIndex(xb, metric, th)
+        cname = "IndexFlatL2" if metric == 0 else "IndexFlatIP"
+        per, bat = BenchOptions(warmup=1, repeats=3), BenchOptions(warmup=1, repeats=3,
+                                                                   per_query=False)
+        rows = [bench_index(cpu, xq[:nb], k, truth, label=cname, options=per),
+                bench_index(idx, xq[:nb], k, truth, label="GpuIndexFlat", options=per),
+                bench_index(cpu, xq[:nb], k, truth, label=cname + " [batched]", options=bat),
+                bench_index(idx, xq[:nb], k, truth, label="GpuIndexFlat [batched]",
+                            options=bat)]
         out["bench_index"] = [r.__dict__ for r in rows]
         out["bench_csv"] = to_bench_csv(rows)
         out["bench_markdown"] = to_bench_markdown(rows)
@@ -476,15 +485,16 @@ def run_kmeans(vs, NN, args, ctx):
     pts.prof_enable(True)
     pts.prof_reset()
     cen_first = cen.copy()
-    first = None
+    hist = []  # per timed step: input centroids, assignments, new centroids, objective
     times = []
     t0 = time.perf_counter()
     for i in range(args.steps):
         t = time.perf_counter()
+        cin = cen
         a, cen, cnt, obj = vs.kmeans_step(pts, cen, 1, jits[i])
         times.append(time.perf_counter() - t)
-        if first is None:
-            first = (a, cen.copy(), obj)
+        hist.append((cin, a, cen, obj))
+    first = hist[0][1:]
     wall = time.perf_counter() - t0
     log(f"[bench] c4: {args.steps} k-means steps in {wall:.3f} s")
     pts.prof_enable(False)
@@ -535,17 +545,94 @@ def run_kmeans(vs, NN, args, ctx):
         same_assign = bool(np.array_equal(a_gpu[:ma], a_or))
         cen_or, _, _ = oracle.kmeans_update(x, a_gpu, cen_first, 1, jits[0])
         same_cen = bool(np.array_equal(cen_or.view(np.uint32), cen_gpu.view(np.uint32)))
-        out["parity"] = {"ok": same_assign and same_cen, "assign_equal_on_prefix": same_assign,
+        full = kmeans_full_parity(x, hist, jits, th)
+        out["parity"] = {"ok": same_assign and same_cen and full["ok"],
+                         "assign_equal_on_prefix": same_assign,
                          "prefix_points": int(ma), "centroids_bit_identical": same_cen,
                          "rule": "first timed step: assignments identical to the oracle's on the "
-                                 "timed prefix; new centroids bit-identical to the oracle's update"}
+                                 "timed prefix; new centroids bit-identical to the oracle's update",
+                         "full_size": full}
     pts.close()
     return out
+
+
+def kmeans_full_parity(x, hist, jits, threads, sample=32768):
+    """Steps of the timed loop checked over all n points: on the first and
+    the last timed step, the assignments of a stride sample spread over every
+    point against the oracle's (kmeans.dart:91-105, with that step's input
+    centroids), the whole update recomputed by the oracle from the GPU's
+    assignments (bit-identical, kmeans.dart:107-140), and (first step) the
+    objective: the fp64 distance of every point to its assigned centroid,
+    summed in point order."""
+    import oracle
+
+    n = len(x)
+    pts = np.arange(0, n, max(1, n // sample))
+    steps = []
+    for si in sorted({0, len(hist) - 1}):
+        cin, a_gpu, cout, obj = hist[si]
+        a_or, _, _ = oracle.kmeans_assign(x[pts], cin, threads)
+        cen_or, _, _ = oracle.kmeans_update(x, a_gpu, cin, 1, jits[si])
+        st = {"step": si, "sample_points": int(len(pts)),
+              "assign_mismatches": int(np.count_nonzero(a_gpu[pts] != a_or)),
+              "centroids_bit_identical": bool(np.array_equal(cen_or.view(np.uint32),
+                                                             cout.view(np.uint32)))}
+        if si == 0:
+            dist = np.empty(n)
+            for c in range(0, n, 1 << 16):
+                diff = x[c:c + (1 << 16)].astype(np.float64) - cin[a_gpu[c:c + (1 << 16)]]
+                dist[c:c + (1 << 16)] = np.cumsum(diff * diff, axis=1)[:, -1]
+            st["objective_equal"] = bool(np.cumsum(dist)[-1] == obj)
+        steps.append(st)
+    ok = all(s["assign_mismatches"] == 0 and s["centroids_bit_identical"] and
+             s.get("objective_equal", True) for s in steps)
+    return {"ok": ok, "steps": steps,
+            "rule": "first and last timed step: assignments of a stride sample of all points "
+                    "identical to the oracle's; update bit-identical; first step's objective "
+                    "equal to the fp64 point-order sum of its assignments' distances"}
 
 
 # --------------------------------------------------------------------------
 # C5: self-join
 # --------------------------------------------------------------------------
+def fp64_dots(x, i, j, chunk=1 << 15):
+    """fp64 dot of rows i[t], j[t] summed in dimension order (index.dart dot)."""
+    out = np.empty(len(i))
+    for c in range(0, len(i), chunk):
+        p = x[i[c:c + chunk]].astype(np.float64) * x[j[c:c + chunk]].astype(np.float64)
+        out[c:c + chunk] = np.cumsum(p, axis=1)[:, -1]
+    return out
+
+
+def join_full_parity(x, pi, pj, ps, thr, planted):
+    """The whole self-join output against what fixes it at full size: every
+    emitted pair (i < j, sorted, unique) re-scored in fp64 is >= thr and its
+    score is the fp32 of that value; every planted pair (a base vector and
+    its copies, the only pairs near thr: random pairs of unit N(0,1) vectors
+    at d = 512 sit about 21 sigma below) is emitted exactly when its fp64
+    score is >= thr."""
+    n = len(x)
+    pi, pj = pi.astype(np.int64), pj.astype(np.int64)
+    key = pi * n + pj
+    ordered = bool(np.all(pi < pj) and np.all(np.diff(key) > 0))
+    s64 = fp64_dots(x, pi, pj)
+    rescored = bool(np.all(s64 >= thr))
+    scores = bool(np.array_equal(ps.view(np.uint32), s64.astype(np.float32).view(np.uint32)))
+    qi, qj = planted
+    qs = fp64_dots(x, qi, qj)
+    emitted = np.isin(qi * n + qj, key)
+    wrong = int(np.count_nonzero(emitted != (qs >= thr)))
+    outside = int(np.count_nonzero(~np.isin(key, qi * n + qj)))
+    return {"ok": ordered and rescored and scores and wrong == 0,
+            "pairs_emitted": int(len(pi)), "sorted_unique_i_lt_j": ordered,
+            "emitted_rescored_ge_threshold": rescored, "scores_fp32_of_fp64": scores,
+            "planted_pairs_checked": int(len(qi)),
+            "planted_pairs_within_1e-3_of_threshold": int(np.count_nonzero(np.abs(qs - thr) < 1e-3)),
+            "planted_pair_failures": wrong, "emitted_outside_planted": outside,
+            "rule": "every emitted pair re-scored in fp64 (>= threshold, fp32 score of it); "
+                    "every planted pair emitted iff its fp64 score >= threshold"}
+
+
 def run_join(vs, NN, args, ctx):
     """near-duplicate cosine self-join of 500k x 512 fp32 unit
     vectors (5% planted copies), all pairs i < j with dot >= 0.95 sorted by
@@ -611,9 +698,11 @@ def run_join(vs, NN, args, ctx):
             f"{n} rows; fp64 oracle", host)
         sel = pi < ra
         agree = bool(np.array_equal(ri, pi[sel]) and np.array_equal(rj, pj[sel]))
-        out["parity"] = {"ok": agree, "rows_checked": int(ra), "pairs_checked": int(len(ri)),
+        full = join_full_parity(x, pi, pj, ps, thr, syn.dedup_planted_pairs(n, 0.05, args.seed))
+        out["parity"] = {"ok": agree and full["ok"], "rows_checked": int(ra),
+                         "pairs_checked": int(len(ri)),
                          "rule": "pair list (i, j) identical to the oracle's for every i in the "
-                                 "checked rows"}
+                                 "checked rows", "full_size": full}
     g.close()
     return out
 

@@ -58,9 +58,10 @@ struct DeviceGuard {
     }
 };
 
-// Test support (option "fail_alloc"): when > 0, the device allocation
-// that brings it to 0 fails as out of memory, so tests reach the failure
-// paths of every caller.  Per thread, like the error text.
+// Test support (option "fail_alloc"): when > 0, the device or pinned host
+// allocation that brings it to 0 fails as out of memory, so tests reach the
+// failure paths of every caller (and show that a path allocates nothing).
+// Per thread, like the error text.
 thread_local int64_t g_fail_alloc = 0;
 
 // Every device allocation of an index goes through here.
@@ -70,6 +71,15 @@ hipError_t dev_malloc(void **p, size_t bytes) {
         return hipErrorOutOfMemory;
     }
     return hipMalloc(p, bytes);
+}
+
+// Every pinned host allocation of an index goes through here.
+hipError_t host_malloc(void **p, size_t bytes) {
+    if (g_fail_alloc > 0 && --g_fail_alloc == 0) {
+        *p = nullptr;
+        return hipErrorOutOfMemory;
+    }
+    return hipHostMalloc(p, bytes, hipHostMallocDefault);
 }
 
 // Device buffer that only grows.
@@ -118,7 +128,7 @@ struct HostBuf {
             bytes = 0;
         }
         size_t nb = std::max(need, (size_t)4096);
-        hipError_t e = hipHostMalloc(&p, nb, hipHostMallocDefault);
+        hipError_t e = host_malloc(&p, nb);
         if (e != hipSuccess) {
             p = nullptr;
             return e;
@@ -164,7 +174,6 @@ struct VsOptions {
     int gemm = -1;         // GEMM-tiled scan: -1 planner rule (rows >= 256 elements), 0 off, 1 any d
     int gemm_min_nq = 0;   // smallest batch on the GEMM-tiled scan (0: 512 by rule, 256 when forced)
     int gemm_wq = 0, gemm_qb = 0, gemm_kc = 0;  // force a GEMM shape field (0: any)
-    int gemm_dma = 1;      // LDS-DMA shapes allowed (only where the build enables them)
     int share = -1;        // row-shared scan: -1 rule (rows of 128 elements), 0 off, 1 also 256
     int coarse = 1;        // one-pass bf16 selection of fp32 rows (range, self-join, k-means)
     int copy16 = 1;        // the one-pass selection reads a bf16 copy of the fp32 rows
@@ -271,14 +280,10 @@ void note_scan_kind(vs_index *x, const vs::ScanPlan &plan) {
     x->prof[plan.kind == 3 ? "shared" : plan.kind == 2 ? "gemm" : "streamed"]
         .launches++;
     if (plan.kind == 0 && plan.lw == 8) x->prof["streamed8"].launches++;
-    if (plan.kind == 2) {  // and per GEMM shape: "gemm:1,1,2,4,4,2,32" or "gemmdma:1,2,4,4,2,4"
+    if (plan.kind == 2) {  // and per GEMM shape: "gemm:1,1,2,4,4,2,32"
         char key[64];
-        if (plan.g_ns > 0)
-            snprintf(key, sizeof key, "gemmdma:%d,%d,%d,%d,%d,%d", plan.tile_pb, plan.lw,
-                     plan.g_wq, plan.tile_rb, plan.g_qb, plan.g_ns);
-        else
-            snprintf(key, sizeof key, "gemm:%d,%d,%d,%d,%d,%d,%d", plan.tile_st, plan.tile_pb,
-                     plan.lw, plan.g_wq, plan.tile_rb, plan.g_qb, plan.tile_kc);
+        snprintf(key, sizeof key, "gemm:%d,%d,%d,%d,%d,%d,%d", plan.tile_st, plan.tile_pb,
+                 plan.lw, plan.g_wq, plan.tile_rb, plan.g_qb, plan.tile_kc);
         x->prof[key].launches++;
     }
 }
@@ -438,10 +443,6 @@ int check_dtype(int dt) {
 // CU; query blocks go in groups of 32 per XCD.  The options gemm,
 // gemm_min_nq and gemm_wq / gemm_qb / gemm_kc force it on or off and pick a
 // shape.
-// The LDS-DMA kernel (gemm_dma_kernel) is switched off: its first run on an
-// MI355X (8-wave shape, d = 200, L2, k = 10) left the GPU faulted, and no
-// mistake in its indexing, waits or barriers has been shown yet.
-constexpr bool kGemmDmaEnabled = false;
 
 // Row-shared scan (top-k only): bf16 rows of 128 or 256 elements, one query
 // plane, large batches.  Every list keeps kk_final entries (one list per
@@ -515,35 +516,9 @@ bool plan_gemm(const vs_index *x, int64_t nq, int64_t nrows, int planes, int sto
 #undef VS_GSHAPE_ENTRY
     const int fwq = o.gemm_wq, fqb = o.gemm_qb, fkc = o.gemm_kc;
     const Shape *pick = nullptr;
-    int kk = p->kk, cap = 0, ns = 0;
+    int kk = p->kk, cap = 0;
     size_t lds = 0;
-    // LDS-DMA shapes first (bf16 rows; option gemm_dma = 0 disables them)
-    struct DShape {
-        int pb, wr, wq, rb, qb, ns;
-    };
-#define VS_DSHAPE_ENTRY(PB_, WR_, WQ_, RB_, QB_, NS_) {PB_, WR_, WQ_, RB_, QB_, NS_},
-    static const DShape dshapes[] = {VS_GEMM_DMA_SHAPES(VS_DSHAPE_ENTRY)};
-#undef VS_DSHAPE_ENTRY
-    static Shape dpick;
-    if (kGemmDmaEnabled && storage == 1 && o.gemm_dma && (!fkc || fkc == 32) &&
-        x->ld % 32 == 0) {
-        for (const DShape &sh : dshapes) {
-            if (sh.pb != planes) continue;
-            if (fwq && sh.wq != fwq) continue;
-            if (fqb && sh.qb != fqb) continue;
-            kk = p->kk;
-            if (!kk_forced && kk < p->kk_final) kk = std::max(kk, p->kk_final / sh.wr);
-            cap = (int)next_pow2(kk + 32 * sh.rb + 16);
-            lds = vs::gemm_dma_lds_bytes(sh.pb, sh.wr, sh.wq, sh.rb, sh.qb, sh.ns, cap);
-            if (lds > x->lds_max) continue;
-            dpick = Shape{1, sh.pb, sh.wr, sh.wq, sh.rb, sh.qb, 32};
-            pick = &dpick;
-            ns = sh.ns;
-            break;
-        }
-    }
     for (const Shape &sh : shapes) {
-        if (pick) break;
         if (sh.st != storage || sh.pb != planes) continue;
         if (fwq && sh.wq != fwq) continue;
         if (fqb && sh.qb != fqb) continue;
@@ -560,7 +535,6 @@ bool plan_gemm(const vs_index *x, int64_t nq, int64_t nrows, int planes, int sto
     }
     if (!pick) return false;
     p->kind = 2;
-    p->g_ns = ns;
     p->kk = kk;
     p->cap = cap;
     p->bn = 32 * pick->wq * pick->qb;
@@ -1046,9 +1020,18 @@ int xnorm_max(vs_index *x, Arena &A, float *out) {
 //   fp32 rows (hi + lo planes), one query plane: below 2^-18;
 //   fp32 rows, two query planes: lo * q1 and the residuals, below 3.1 * 2^-18.
 // The factors below are 2.7 to 4 times those.
+// fp32 accumulation of npass MFMA passes over d elements (bf16 rows: one
+// pass per query plane; fp32 rows: hi x plane 0, lo x plane 0 [, hi x plane
+// 1]): at most npass d + 1 terms, each rounding at most one unit of a
+// truncating fp32 accumulator, 2^-23 (round-to-nearest would be 2^-24);
+// tests/test_gpu_mfma_rounding.py holds both MFMA shapes to this on
+// adversarial operands.
+double accum_gamma(int64_t d, int npass) {
+    return ((double)npass * (double)d + 4.0) * (1.0 / 8388608.0);
+}
+
 void topk_error_model(const vs_index *x, int planes, vs::TopkCheck *chk) {
-    const double u = 1.0 / 16777216.0;
-    chk->err_g = (float)((3.0 * (double)x->d + 4.0) * u);
+    chk->err_g = (float)accum_gamma(x->d, x->storage == 1 ? planes : 1 + planes);
     if (x->storage == 1)
         chk->err_r = planes == 1 ? 0.f : (float)(1.0 / 65536.0);
     else
@@ -1423,6 +1406,7 @@ namespace {
 
 std::mutex g_scratch_mu;
 void *g_scratch_ptr[kMaxDevices] = {};
+std::mutex g_scratch_call_mu[kMaxDevices];  // serialises the calls that use one device's region
 
 // The device address of this device's scratch (the current device must be
 // `device`).
@@ -1743,12 +1727,19 @@ int vs_index_search_device_noalloc(vs_index *x, const void *q_dev, int q_dtype, 
     if (g.err != hipSuccess) return hip_err(g.err, "hipSetDevice");
     char *base = nullptr;
     if (int rc = fixed_scratch(x->device, &base)) return rc;
+    // one call at a time per GPU: the region is shared by every handle on it
+    std::lock_guard<std::mutex> lk(g_scratch_call_mu[x->device]);
     Arena A;
     A.base = base;
     A.cap = kFixedScratchBytes;
     struct FixedScope {
         vs_index *x;
-        ~FixedScope() { x->prof_fixed = false; }
+        // the region is free again only once this call's GPU work is done,
+        // also after an error part-way through
+        ~FixedScope() {
+            (void)hipStreamSynchronize(x->st);
+            x->prof_fixed = false;
+        }
     } fs{x};
     x->prof_fixed = true;
     return search_device(x, A, q_dev, q_dtype, nq, k, D_dev, I_dev, false, kFixedListBudget);
@@ -2071,12 +2062,12 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     //    of -2 x_j c_j, r = 2^-8 for the one-pass selection (both operands
     //    rounded to bf16, 2^-9 each) and 2^-15 for the split-bf16 passes (hi
     //    + lo within 2^-18 of each value, the dropped lo * q1 term);
-    //  - fp32 accumulation of at most 3 d + 1 terms: gamma = (3 d + 4) 2^-24;
+    //  - fp32 accumulation (accum_gamma) of one pass (one-pass selection) or
+    //    of three (split-bf16 points and centroids);
     // so |error| <= 2 r |x| |c| + gamma (|c|^2 + 2 |x| |c|) (Cauchy-Schwarz),
     // taken with a 25% margin.
-    const double u = 1.0 / 16777216.0;
     const double r = coarse ? 1.0 / 256.0 : 1.0 / 32768.0;
-    const double gam = (3.0 * d + 4.0) * u;
+    const double gam = accum_gamma(d, coarse ? 1 : 3);
     const double pc = (double)pmax * std::sqrt((double)cmax);
     const float bound = (float)(1.25 * (2.0 * r * pc + gam * ((double)cmax + 2.0 * pc)) + 1e-6);
     // On the row-shared scan each lane appends every value below its running
@@ -2648,6 +2639,33 @@ int vs_dev_probe(int device, int what, int64_t bytes, double *result) {
     return VS_OK;
 }
 
+int vs_dev_mfma_chain(int device, int shape, int64_t nsteps, int64_t npass, const uint16_t *A,
+                      const uint16_t *B, const float *C, float *D) {
+    if (shape < 0 || shape > 1 || nsteps < 1 || nsteps > 4096 || npass < 1 || npass > 4 || !A ||
+        !B || !C || !D)
+        return set_err(VS_ERR_INVALID,
+                       "vs_dev_mfma_chain: shape 0 or 1, 1 <= nsteps <= 4096, 1 <= npass <= 4");
+    DeviceGuard g(device);
+    if (g.err != hipSuccess) return hip_err(g.err, "hipSetDevice");
+    const size_t mn = shape == 0 ? 32 : 16, K = (size_t)nsteps * (shape == 0 ? 16 : 32);
+    const size_t ab = (size_t)npass * mn * K * 2, cb = mn * mn * 4;
+    char *buf = nullptr;
+    VS_HIP(hipMalloc((void **)&buf, 2 * ab + 2 * cb), "mfma chain buffers");
+    struct Free {
+        void *p;
+        ~Free() { (void)hipFree(p); }
+    } fr{buf};
+    uint16_t *dA = (uint16_t *)buf, *dB = (uint16_t *)(buf + ab);
+    float *dC = (float *)(buf + 2 * ab), *dD = (float *)(buf + 2 * ab + cb);
+    VS_HIP(hipMemcpy(dA, A, ab, hipMemcpyHostToDevice), "mfma chain upload");
+    VS_HIP(hipMemcpy(dB, B, ab, hipMemcpyHostToDevice), "mfma chain upload");
+    VS_HIP(hipMemcpy(dC, C, cb, hipMemcpyHostToDevice), "mfma chain upload");
+    VS_HIP(vs::launch_mfma_chain(shape, (int)nsteps, (int)npass, dA, dB, dC, dD, nullptr),
+           "mfma chain");
+    VS_HIP(hipMemcpy(D, dD, cb, hipMemcpyDeviceToHost), "mfma chain download");
+    return VS_OK;
+}
+
 int vs_dev_download(int device, void *dst, const void *src, int64_t bytes) {
     DeviceGuard g(device);
     VS_HIP(hipMemcpy(dst, src, (size_t)bytes, hipMemcpyDeviceToHost), "download");
@@ -2712,7 +2730,6 @@ int vs_index_set_option(vs_index *x, const char *name, int64_t value) {
         {"gemm_wq", &VsOptions::gemm_wq, 0, 8},
         {"gemm_qb", &VsOptions::gemm_qb, 0, 8},
         {"gemm_kc", &VsOptions::gemm_kc, 0, 64},
-        {"gemm_dma", &VsOptions::gemm_dma, 0, 1},
         {"share", &VsOptions::share, -1, 1},
         {"coarse", &VsOptions::coarse, 0, 1},
         {"copy16", &VsOptions::copy16, 0, 1},

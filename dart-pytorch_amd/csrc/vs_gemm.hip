@@ -616,306 +616,6 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
     }
 }
 
-// ---------------------------------------------------------------------------
-// LDS-DMA variant for bf16 rows.  Every operand byte goes HBM/L2 -> LDS with
-// global_load_lds_dwordx4 (lane i of a wave writes 16 bytes at M0 + 16 i; one
-// instruction fills 1 KB), so no VGPRs stage the loads and NS stages are in
-// flight: chunk c + NS - 1 is issued while chunk c is multiplied.  Rows are
-// 64 bytes per K-chunk of 32, unpadded; 16-byte chunk c of row r sits at
-// position c ^ f(r), f(r) = ((r >> 1) ^ (r >> 2)) & 3, which spreads the 32
-// rows of an MFMA fragment read over all LDS banks (32- or 64-bank layouts).
-// The DMA loads are issued from inline assembly, so the compiler does not
-// treat them as LDS writes; an explicit vmcnt wait plus a barrier per chunk
-// orders them (vector memory loads complete in issue order, so "at most N
-// outstanding" with N later loads means the chunk has landed).  The tile's
-// row norms and the queries' shared thresholds arrive the same way with the
-// tile's first chunk.
-// ---------------------------------------------------------------------------
-template <int PB, int WR, int WQ, int RB, int QB, int NS>
-struct DmaShape {
-    static constexpr int NW = WR * WQ, NT = 64 * NW;
-    static constexpr int BR = WR * 32 * RB, BQ = WQ * 32 * QB;
-    static constexpr int KC = 32;  // elements per K-chunk: 64 bytes per row
-    static constexpr int A_INS = BR * 64 / 1024, B_INS = PB * BQ * 64 / 1024;
-    static constexpr int A_PW = A_INS / NW, B_PW = B_INS / NW;
-    static constexpr int L = A_PW + B_PW;  // DMA loads per wave and chunk (norms aside)
-    static constexpr int A_BYTES = BR * 64, B_BYTES = PB * BQ * 64;
-    static constexpr int N_OFF = A_BYTES + B_BYTES;  // row norms [BR] f32
-    static constexpr int G_OFF = N_OFF + BR * 4;      // shared thresholds [BQ] u32
-    static constexpr int STAGE_BYTES = G_OFF + BQ * 4;
-    static_assert(A_INS % NW == 0 && B_INS % NW == 0, "whole DMA loads per wave");
-    static_assert(BR % 256 == 0 && BR / 256 <= NW && BQ <= 256, "norm and threshold loads");
-    static_assert(BR <= kRowSlack, "the last row tile reads at most kRowSlack rows past the end");
-    static_assert(NS >= 2, "at least two stages");
-};
-
-size_t gemm_dma_lds_bytes(int pb, int wr, int wq, int rb, int qb, int ns, int cap) {
-    const size_t br = (size_t)wr * 32 * rb, bq = (size_t)wq * 32 * qb;
-    const size_t stage = br * 64 + (size_t)pb * bq * 64 + br * 4 + bq * 4;
-    return (size_t)ns * stage + (size_t)wr * bq * 8 + (size_t)wr * wq * cap * 8;
-}
-
-__device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
-
-// One 1-KB LDS DMA: lane i's 16 bytes at base + voff go to LDS byte lds +
-// 16 i (base and lds are wave-uniform; voff is the lane's byte offset).
-__device__ __forceinline__ void dma16(const void *base, uint32_t voff, uint32_t lds) {
-    const uint64_t b = (uint64_t)(uintptr_t)base;
-    const uint64_t bu = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32) |
-                        (uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
-    uint32_t save;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %1\n\t"
-        "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %2, %3\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(save)
-        : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(bu)
-        : "memory");
-}
-
-// dma16 with voff = 16 * lane, computed inside the assembly so that it is
-// never kept live (a spilled offset would cost a reload, whose wait for
-// vmcnt(0) would also drain every LDS DMA in flight).
-__device__ __forceinline__ void dma16_lane(const void *base, uint32_t lds) {
-    const uint64_t b = (uint64_t)(uintptr_t)base;
-    const uint64_t bu = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32) |
-                        (uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
-    uint32_t save, voff;
-    asm volatile(
-        "v_mbcnt_lo_u32_b32 %1, -1, 0\n\t"
-        "v_mbcnt_hi_u32_b32 %1, -1, %1\n\t"
-        "v_lshlrev_b32 %1, 4, %1\n\t"
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %2\n\t"
-        "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %1, %3\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(save), "=&v"(voff)
-        : "s"(__builtin_amdgcn_readfirstlane(lds)), "s"(bu)
-        : "memory");
-}
-
-// s_waitcnt vmcnt(n) (gfx9 encoding: vmcnt bits 3:0 and 15:14; expcnt and
-// lgkmcnt left at their maxima, i.e. not waited on)
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
-template <int PB, int WR, int WQ, int RB, int QB, int NS, int MODE>
-__global__ __launch_bounds__(64 * WR * WQ) void gemm_dma_kernel(ScanKArgs a) {
-    using S = DmaShape<PB, WR, WQ, RB, QB, NS>;
-    constexpr int NT = S::NT, BR = S::BR, BQ = S::BQ, L = S::L;
-    extern __shared__ __align__(16) char smem[];
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
-    const int wr = wave % WR, wq = wave / WR;
-    (void)NT;
-
-    int64_t split, qblk;
-    if (!map_block_grouped(a.nqblk, a.nsplit, a.qgroup, a.qspc, &split, &qblk)) return;
-    int64_t r0 = split * a.rows_per_split;
-    const int64_t r1 = min(a.n, r0 + a.rows_per_split);
-    const int64_t q0 = qblk * BQ;
-    if (MODE == 1 && a.self_join) r0 = max(r0, q0);  // only ids > query
-    if (r0 >= r1) return;
-
-    int *cnt = (int *)(smem + NS * S::STAGE_BYTES);
-    float *thr = (float *)(cnt + WR * BQ);
-    float *sv = thr + WR * BQ;
-    int *si = (int *)(sv + S::NW * a.cap);
-    for (int t = tid; t < WR * BQ; t += S::NT) {
-        cnt[t] = 0;
-        thr[t] = q0 + (t % BQ) < a.nq ? VS_INF : -VS_INF;
-    }
-    int *cnt_w = cnt + wr * BQ;
-    float *thr_w = thr + wr * BQ;
-    float *sv_w = sv + wave * a.cap;
-    int *si_w = si + wave * a.cap;
-    const int64_t list_base = ((qblk * a.nsplit + split) * WR + wr) * (int64_t)BQ * a.cap;
-    float *cv = MODE == 0 ? a.cand_v + list_base : nullptr;
-    int32_t *ci = MODE == 0 ? a.cand_i + list_base : nullptr;
-    const int qw0 = wq * 32 * QB;
-    const EpiCtx ectx{q0, r1, qw0, l32, h, lane, cnt, cnt_w, thr, thr_w, sv_w, si_w, cv, ci};
-
-    float thr_r[QB];
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-        const int64_t qg = q0 + qw0 + qb * 32 + l32;
-        if (MODE == 0)
-            thr_r[qb] = qg < a.nq ? VS_INF : -VS_INF;
-        else
-            thr_r[qb] = qg < a.nq ? a.athr[qg] : -VS_INF;
-    }
-
-    const int nkc = (int)(a.ld / S::KC);
-    const int64_t row_bytes = a.ld * 2;
-    const bool l2 = a.metric == 0;
-    const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
-
-    // per-lane global byte offsets of this wave's DMA loads (fixed per slot)
-    int aoff[S::A_PW], boff[S::B_PW];
-#pragma unroll
-    for (int j = 0; j < S::A_PW; ++j) {
-        const int r = 16 * (wave * S::A_PW + j) + (lane >> 2);
-        aoff[j] = r * (int)row_bytes + 16 * ((lane & 3) ^ swz(r));
-    }
-#pragma unroll
-    for (int j = 0; j < S::B_PW; ++j) {
-        const int br = 16 * (wave * S::B_PW + j) + (lane >> 2);  // plane-major B row
-        const int p = br / BQ, q = br % BQ;
-        boff[j] = (2 * q + p) * (int)row_bytes + 16 * ((lane & 3) ^ swz(q));
-    }
-    const char *qbase = (const char *)a.qp + (q0 * 2) * row_bytes;
-
-    // issue the loads of chunk (tile row t, K-chunk kc) into stage st
-    auto issue = [&](int64_t t, int kc, int st) __attribute__((always_inline)) {
-        const uint32_t sb = lds0 + st * S::STAGE_BYTES;
-        const char *ab = (const char *)a.xb + t * row_bytes + kc * 64;
-#pragma unroll
-        for (int j = 0; j < S::A_PW; ++j)
-            dma16(ab, (uint32_t)aoff[j], sb + (wave * S::A_PW + j) * 1024);
-        const char *bb = qbase + kc * 64;
-#pragma unroll
-        for (int j = 0; j < S::B_PW; ++j)
-            dma16(bb, (uint32_t)boff[j], sb + S::A_BYTES + (wave * S::B_PW + j) * 1024);
-        if (kc == 0) {
-            if (l2 && wave < BR / 256)
-                dma16_lane(a.xn + t + 256 * wave, sb + S::N_OFF + 1024 * wave);
-            if (MODE == 0 && wave == S::NW - 1 && lane < BQ / 4)
-                dma16_lane(a.gthr + q0, sb + S::G_OFF);
-        }
-    };
-
-    f32x16_t acc[QB][RB];
-    uint32_t gt[QB];
-    const int xo0 = 16 * ((0 + h) ^ swz(l32)), xo1 = 16 * ((2 + h) ^ swz(l32));
-
-    auto compute = [&](const char *stage, auto first_c) __attribute__((always_inline)) {
-        constexpr bool FIRST = decltype(first_c)::value;
-        const char *Ab = stage + (wr * 32 * RB + l32) * 64;
-        const char *Bb = stage + S::A_BYTES + (qw0 + l32) * 64;
-        const float *Ns = (const float *)(stage + S::N_OFF) + wr * 32 * RB + 4 * h;
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const int xo = ks == 0 ? xo0 : xo1;
-            bf16x8_t b0[QB], b1[QB];
-#pragma unroll
-            for (int qb = 0; qb < QB; ++qb) {
-                b0[qb] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t *)(Bb + qb * 32 * 64 + xo));
-                if constexpr (PB == 2)
-                    b1[qb] = __builtin_bit_cast(
-                        bf16x8_t, *(const u32x4_t *)(Bb + BQ * 64 + qb * 32 * 64 + xo));
-            }
-#pragma unroll
-            for (int rb = 0; rb < RB; ++rb) {
-                const bf16x8_t ah =
-                    __builtin_bit_cast(bf16x8_t, *(const u32x4_t *)(Ab + rb * 32 * 64 + xo));
-                f32x16_t x16;
-                if (FIRST && ks == 0) {
-                    if (l2) {
-#pragma unroll
-                        for (int u = 0; u < 4; ++u) {
-                            const f32x4_t q4 = *(const f32x4_t *)(Ns + rb * 32 + 8 * u);
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) x16[4 * u + e] = q4[e];
-                        }
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < 16; ++e) x16[e] = 0.f;
-                    }
-                }
-#pragma unroll
-                for (int qb = 0; qb < QB; ++qb) {
-                    acc[qb][rb] = mfma32_bf16(ah, b0[qb], (FIRST && ks == 0) ? x16 : acc[qb][rb]);
-                    if constexpr (PB == 2) acc[qb][rb] = mfma32_bf16(ah, b1[qb], acc[qb][rb]);
-                }
-            }
-        }
-        if constexpr (FIRST && MODE == 0) {
-            const uint32_t *G = (const uint32_t *)(stage + S::G_OFF) + qw0 + l32;
-#pragma unroll
-            for (int qb = 0; qb < QB; ++qb) gt[qb] = G[qb * 32];
-        }
-    };
-
-    const int64_t ntiles = (r1 - r0 + BR - 1) / BR;
-    const int64_t total = ntiles * nkc;
-    // prologue: chunks 0 .. NS - 2
-    int64_t it_t = r0;  // next chunk to issue: tile row and K-chunk
-    int it_kc = 0;
-    int64_t issued = 0;
-    for (; issued < NS - 1 && issued < total; ++issued) {
-        issue(it_t, it_kc, (int)issued);
-        if (++it_kc == nkc) {
-            it_kc = 0;
-            it_t += BR;
-        }
-    }
-
-    bool seeded = (a.kk + 1) / 2 > 16 * RB;
-    int64_t it = 0;
-    for (int64_t t0 = r0; t0 < r1; t0 += BR) {
-        for (int kc = 0; kc < nkc; ++kc, ++it) {
-            // chunk `it` has landed once at most (issued - 1 - it) chunks of
-            // later loads are outstanding
-            const int64_t later = issued - 1 - it;
-            if constexpr (NS >= 4) {
-                if (later >= 2) wait_vm<2 * L>();
-                else if (later == 1) wait_vm<L>();
-                else wait_vm<0>();
-            } else if constexpr (NS == 3) {
-                if (later >= 1) wait_vm<L>();
-                else wait_vm<0>();
-            } else {
-                wait_vm<0>();
-            }
-            __syncthreads();
-            if (issued < total) {
-                issue(it_t, it_kc, (int)(issued % NS));
-                ++issued;
-                if (++it_kc == nkc) {
-                    it_kc = 0;
-                    it_t += BR;
-                }
-            }
-            const char *cur = smem + (it % NS) * S::STAGE_BYTES;
-            if (kc == 0)
-                compute(cur, std::true_type{});
-            else
-                compute(cur, std::false_type{});
-            if (kc + 1 == nkc)
-                gemm_epilogue<WR, BQ, RB, QB, MODE>(acc, a, ectx, t0 + wr * 32 * RB, thr_r, gt,
-                                                    seeded);
-        }
-    }
-
-    if constexpr (MODE == 0) {
-        wave_sync();
-        for (int q = qw0; q < qw0 + 32 * QB; ++q) {
-            const int c = cnt_w[q];
-            if (c > a.kk) {
-                flush_list(cv + (int64_t)q * a.cap, ci + (int64_t)q * a.cap, &cnt_w[q], &thr_w[q],
-                           &thr[q], BQ, WR, &a.gthr[q0 + q], sv_w, si_w, a.cap, a.kk, a.kk_final,
-                           a.publish_block, lane);
-            } else {
-                for (int j = c + lane; j < a.kk; j += 64) {
-                    cv[(int64_t)q * a.cap + j] = VS_INF;
-                    ci[(int64_t)q * a.cap + j] = -1;
-                }
-            }
-        }
-        if (a.lbound) {
-            wave_sync();
-            const int64_t lb = ((qblk * a.nsplit + split) * WR + wr) * (int64_t)BQ;
-            for (int q = qw0 + lane; q < qw0 + 32 * QB; q += 64) a.lbound[lb + q] = thr_w[q];
-        }
-    }
-}
-
 template <int MODE>
 hipError_t launch_gemm_scan(int storage, int planes, const ScanPlan &plan, const ScanKArgs &args,
                             hipStream_t st) {
@@ -928,17 +628,9 @@ hipError_t launch_gemm_scan(int storage, int planes, const ScanPlan &plan, const
     // for the price of one sort of ~2 kk entries
     ga.flush_at = std::max(2 * plan.kk, 16);
     void (*fn)(ScanKArgs) = nullptr;
-#define VS_DPICK(PB_, WR_, WQ_, RB_, QB_, NS_)                                                 \
-    if (storage == 1 && planes == PB_ && plan.lw == WR_ && plan.g_wq == WQ_ &&                  \
-        plan.tile_rb == RB_ && plan.g_qb == QB_ && plan.g_ns == NS_)                              \
-        fn = gemm_dma_kernel<PB_, WR_, WQ_, RB_, QB_, NS_, MODE>;
-    if (plan.g_ns > 0) {
-        VS_GEMM_DMA_SHAPES(VS_DPICK)
-    }
-#undef VS_DPICK
 #define VS_GPICK(ST_, PB_, WR_, WQ_, RB_, QB_, KC_)                                            \
     if (storage == ST_ && planes == PB_ && plan.lw == WR_ && plan.g_wq == WQ_ &&                 \
-        plan.tile_rb == RB_ && plan.g_qb == QB_ && plan.tile_kc == KC_ && plan.g_ns == 0)        \
+        plan.tile_rb == RB_ && plan.g_qb == QB_ && plan.tile_kc == KC_)                          \
         fn = gemm_scan_kernel<ST_, PB_, WR_, WQ_, RB_, QB_, KC_, MODE>;
     VS_GEMM_SHAPES(VS_GPICK)
 #undef VS_GPICK

@@ -90,7 +90,6 @@ struct ScanPlan {
     int kind = 0;         // 0: streaming scan (vs_kernels.hip);
                           // 2: GEMM-tiled scan (vs_gemm.hip); 3: row-shared scan (vs_share.hip:
                           // nks K-steps, bn = 64 * query blocks per wave, tm = 16-row blocks per tile)
-    int g_ns = 0;            // GEMM-tiled scan: LDS-DMA stages (0: register-staged kernel)
     int g_wq = 2, g_qb = 4;  // GEMM-tiled scan: query waves, 32-query blocks per wave
                              // (row waves = lw, 32-row blocks per wave = tile_rb,
                              // K-chunk = tile_kc)
@@ -234,6 +233,8 @@ hipError_t launch_range_bounds(const PreparedQueries &pq, int64_t d, int metric,
 // 32x32x16 bf16 MFMAs (out: a word the kernels leave unwritten).
 hipError_t launch_read16(const void *src, int64_t n16, uint32_t *out, hipStream_t st);
 hipError_t launch_mfma_peak(int blocks, int iters, int rnd, float *out, hipStream_t st);
+hipError_t launch_mfma_chain(int shape, int nsteps, int npass, const uint16_t *A,
+                             const uint16_t *B, const float *C, float *D, hipStream_t st);
 
 // dst = src, n16 16-byte words (both 16-byte aligned)
 hipError_t launch_copy16(const void *src, void *dst, int64_t n16, hipStream_t st);
@@ -316,19 +317,11 @@ size_t merge_lds_bytes(int64_t ld, int mu);
     X(0, 1, 2, 4, 4, 2, 32)                                                                   \
     X(0, 1, 2, 2, 4, 2, 32)
 
-// The LDS-DMA shapes of the GEMM-tiled scan (bf16 rows, K-chunk 32), tried
-// before the register-staged ones: X(query planes, row waves, query waves,
-// 32-row blocks per wave, 32-query blocks per wave, LDS stages).
-#define VS_GEMM_DMA_SHAPES(X)                                                                 \
-    X(1, 2, 4, 4, 2, 4)                                                                       \
-    X(1, 2, 2, 4, 2, 4)
-
 // Storage code of the one-pass selection (fp32 rows, bf16 hi plane and the
 // first query plane only): the GEMM-tiled scan's shapes with storage 2.
 constexpr int kSelectCoarse = 2;
 
 // LDS of the GEMM-tiled scans (stages plus list bookkeeping).
-size_t gemm_dma_lds_bytes(int pb, int wr, int wq, int rb, int qb, int ns, int cap);
 size_t gemm_lds_bytes(int st, int pb, int wr, int wq, int rb, int qb, int kc, int cap);
 
 // LDS of the row-shared scan (two row stages plus list bookkeeping).

@@ -2417,11 +2417,14 @@ hipError_t launch_range_bounds(const PreparedQueries &pq, int64_t d, int metric,
     if (pq.nq <= 0) return hipSuccess;
     // relative error of the split-bf16 dot product with fp32 accumulation:
     // products: each operand within 2^-16 relative of its value (hi + lo),
-    // 2^-8 when a query is rounded to one bf16 plane; accumulation gamma_d.
-    // One-pass selection rounds both operands to bf16 (2^-9 each, taken
-    // four times for margin).
-    const double u = 1.0 / 16777216.0;
-    double rel = 4.0 * (double)(d + 4) * u + 1.0 / 1048576.0;
+    // 2^-8 when a query is rounded to one bf16 plane; accumulation: npass d
+    // + 1 terms, each rounding at most one unit of a truncating fp32
+    // accumulator (2^-23), npass the MFMA passes (rows hi [, lo] x query
+    // plane 0 [, rows hi x plane 1]), taken twice for margin.  One-pass
+    // selection rounds both operands to bf16 (2^-9 each, taken four times
+    // for margin).
+    const int npass = coarse ? 1 : (exact_x ? 1 : 2) + (exact_q ? 0 : 1);
+    double rel = 2.0 * ((double)npass * (double)d + 4.0) / 8388608.0 + 1.0 / 1048576.0;
     if (!exact_x) rel += 4.0 / 65536.0;
     if (!exact_q) rel += 4.0 / 65536.0;
     if (coarse) rel += 4.0 / 256.0;
@@ -2588,6 +2591,60 @@ __global__ __launch_bounds__(256) void mfma_peak_kernel(int iters, int rnd, floa
 
 hipError_t launch_mfma_peak(int blocks, int iters, int rnd, float *out, hipStream_t st) {
     mfma_peak_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(iters, rnd, out);
+    return hipGetLastError();
+}
+
+// Chained MFMAs on given operands, one wave: the accumulation the scans
+// rely on, exposed so that a test can compare every accumulator with the
+// exact sum.  shape 0: v_mfma_f32_32x32x16_bf16 (M = N = 32, K-step 16);
+// shape 1: v_mfma_f32_16x16x32_bf16 (M = N = 16, K-step 32).  A is
+// [npass][M][K] and B [npass][N][K] bf16 bits, row-major, K = nsteps *
+// K-step; C and D are [M][N] fp32.  D = C, then for each K-step s and pass p
+// in that order, D += A_p[:, s] B_p[:, s]^T -- the order in which the scans
+// chain their plane products (rows hi x query plane 0, rows lo x plane 0,
+// rows hi x plane 1).
+__global__ __launch_bounds__(64) void mfma_chain_kernel(int shape, int nsteps, int npass,
+                                                        const uint16_t *__restrict__ A,
+                                                        const uint16_t *__restrict__ B,
+                                                        const float *__restrict__ C,
+                                                        float *__restrict__ D) {
+    const int lane = threadIdx.x;
+    if (shape == 0) {
+        const int r = lane & 31, h = lane >> 5;
+        const int64_t K = (int64_t)nsteps * 16;
+        f32x16_t acc;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[v] = C[(8 * (v / 4) + 4 * h + v % 4) * 32 + r];
+        for (int s = 0; s < nsteps; ++s)
+            for (int p = 0; p < npass; ++p) {
+                const int64_t off = ((int64_t)p * 32 + r) * K + s * 16 + 8 * h;
+                const bf16x8_t a = __builtin_bit_cast(bf16x8_t, *(const u32x4_t *)(A + off));
+                const bf16x8_t b = __builtin_bit_cast(bf16x8_t, *(const u32x4_t *)(B + off));
+                acc = mfma32_bf16(a, b, acc);
+            }
+#pragma unroll
+        for (int v = 0; v < 16; ++v) D[(8 * (v / 4) + 4 * h + v % 4) * 32 + r] = acc[v];
+    } else {
+        const int r = lane & 15, g = lane >> 4;
+        const int64_t K = (int64_t)nsteps * 32;
+        f32x4_t acc;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[v] = C[(4 * g + v) * 16 + r];
+        for (int s = 0; s < nsteps; ++s)
+            for (int p = 0; p < npass; ++p) {
+                const int64_t off = ((int64_t)p * 16 + r) * K + s * 32 + 8 * g;
+                const bf16x8_t a = __builtin_bit_cast(bf16x8_t, *(const u32x4_t *)(A + off));
+                const bf16x8_t b = __builtin_bit_cast(bf16x8_t, *(const u32x4_t *)(B + off));
+                acc = mfma_bf16(a, b, acc);
+            }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) D[(4 * g + v) * 16 + r] = acc[v];
+    }
+}
+
+hipError_t launch_mfma_chain(int shape, int nsteps, int npass, const uint16_t *A,
+                             const uint16_t *B, const float *C, float *D, hipStream_t st) {
+    mfma_chain_kernel<<<dim3(1), dim3(64), 0, st>>>(shape, nsteps, npass, A, B, C, D);
     return hipGetLastError();
 }
 

@@ -38,6 +38,7 @@ EXPORTED = [
     "vs_index_range_search", "vs_range_result_free",
     "vs_index_self_join", "vs_pairs_free", "vs_kmeans_step", "vs_last_error",
     "vs_dev_alloc", "vs_dev_free", "vs_dev_upload", "vs_dev_download", "vs_dev_copy", "vs_dev_probe",
+    "vs_dev_mfma_chain",
     "vs_device_count",
     "vs_device_name", "vs_gen_normal", "vs_prof_enable", "vs_prof_get", "vs_prof_reset",
     "vs_index_sync", "vs_index_set_option",
@@ -130,6 +131,7 @@ def load() -> ctypes.CDLL:
         "vs_dev_download": ([i32, p, p, i64], i32),
         "vs_dev_copy": ([i32, p, p, i64], i32),
         "vs_dev_probe": ([i32, i32, i64, ctypes.POINTER(ctypes.c_double)], i32),
+        "vs_dev_mfma_chain": ([i32, i32, i64, i64, p, p, p, p], i32),
         "vs_device_count": ([ctypes.POINTER(ctypes.c_int)], i32),
         "vs_device_name": ([i32, ctypes.c_char_p, i64], i32),
         "vs_gen_normal": ([i32, p, i32, i64, i64, ctypes.c_uint64, ctypes.c_uint64, i32], i32),

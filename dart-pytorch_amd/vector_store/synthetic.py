@@ -76,6 +76,35 @@ def dedup_set(n: int, d: int, dup_frac: float, noise: float, seed: int) -> np.nd
     return np.ascontiguousarray(allv[perm])
 
 
+def dedup_planted_pairs(n: int, dup_frac: float, seed: int):
+    """Every pair (i, j), i < j, of rows of dedup_set(n, ..., dup_frac, ...,
+    seed) that hold the same base vector or copies of it (the generator's
+    planted near-duplicates), as two int64 arrays sorted by (i, j)."""
+    ndup = int(round(n * dup_frac))
+    nbase = n - ndup
+    src = rng(seed, 1).integers(0, nbase, size=ndup)
+    perm = rng(seed, 3).permutation(n)
+    row = np.empty(n, np.int64)
+    row[perm] = np.arange(n)  # row of generated vector v: row[v]
+    order = np.argsort(src, kind="stable")
+    pi, pj = [], []
+    start = 0
+    while start < ndup:
+        b = src[order[start]]
+        end = start
+        while end < ndup and src[order[end]] == b:
+            end += 1
+        members = np.sort(np.concatenate(([row[b]], row[nbase + order[start:end]])))
+        for a in range(len(members)):
+            for c in range(a + 1, len(members)):
+                pi.append(members[a])
+                pj.append(members[c])
+        start = end
+    pi, pj = np.asarray(pi, np.int64), np.asarray(pj, np.int64)
+    o = np.lexsort((pj, pi))
+    return pi[o], pj[o]
+
+
 DEVICE_STREAM_BASE = 1 << 32
 
 

@@ -91,10 +91,13 @@ class IndexIDMap(Index):
         return self._ext[i]
 
     def internal_of(self, ext: int) -> int:
-        try:
-            return self._ext.index(ext)
-        except ValueError:
-            return -1
+        # the reference's reverse map is built by one pass in offset order,
+        # so a duplicated external id maps to its last offset
+        # (index_id_map.dart internalOf)
+        for i in range(len(self._ext) - 1, -1, -1):
+            if self._ext[i] == ext:
+                return i
+        return -1
 
     def _map(self, ids: np.ndarray) -> np.ndarray:
         ext = np.asarray(self._ext, np.int64)
@@ -222,7 +225,9 @@ class IndexShards(Index):
             if s.d != self.d or s.metric != self.metric:
                 raise ValueError("IndexShards: shards must share d and metric")
         self.shards = shards
-        self._ntotal = 0
+        # shards that already hold rows count from the start, as the
+        # reference's constructor folds their ntotal
+        self._ntotal = sum(int(s.ntotal) for s in shards)
         self.is_trained = all(s.is_trained for s in shards)
 
     @property

@@ -19,7 +19,10 @@
  *   - the library owns all device memory; the caller owns host buffers
  *     except the result objects, which have their own free functions;
  *   - an index handle is single-threaded (one internal HIP stream);
- *     separate handles may be used from separate threads.
+ *     separate handles may be used from separate threads.  One exception:
+ *     vs_index_search_device_noalloc shares one fixed scratch region per
+ *     GPU between all handles, so its calls on one GPU are serialised by a
+ *     per-device lock (they return only after their GPU work is done).
  */
 #ifndef VS_HIP_H
 #define VS_HIP_H
@@ -140,15 +143,18 @@ VS_API int vs_index_search_device(vs_index *idx, const void *q_dev, int q_dtype,
                                   int64_t k, float *D_dev, int32_t *I_dev);
 
 /* No counterpart in the reference.  For callers that cannot allocate device
- * memory (code under HIP graph capture, tight serving loops, harnesses that
- * forbid hipMalloc): vs_index_search_device with every scratch buffer --
- * prepared queries, candidate lists, thresholds, counters and the fallback
- * paths' lists -- carved from one fixed region per device, a 128 MiB
- * static device array the library holds from load until the process ends.
- * It calls no hipMalloc / hipFree and allocates no host memory.  Limits:
- * nq <= 64, k <= 128, d <= 4096 (VS_ERR_UNSUPPORTED beyond).  Results equal
- * those of vs_index_search_device.  All calls on one GPU share its region:
- * calls that overlap on one GPU (from several threads or handles) race. */
+ * memory (tight serving loops, harnesses that forbid hipMalloc):
+ * vs_index_search_device with every scratch buffer -- prepared queries,
+ * candidate lists, thresholds, counters and the fallback paths' lists --
+ * carved from one fixed region per device, a 128 MiB static device array
+ * the library holds from load until the process ends.  It calls no
+ * hipMalloc / hipFree / hipHostMalloc.  Limits: nq <= 64, k <= 128,
+ * d <= 4096 (VS_ERR_UNSUPPORTED beyond).  Results equal those of
+ * vs_index_search_device.  It is not for HIP graph capture: like every
+ * search it runs on the index's own stream and synchronises it before
+ * returning.  All calls on one GPU share its region, which keeps the last
+ * call's contents; calls that overlap on one GPU would race on it, so a
+ * per-device lock serialises them within the process. */
 VS_API int vs_index_search_device_noalloc(vs_index *idx, const void *q_dev, int q_dtype,
                                           int64_t nq, int64_t k, float *D_dev, int32_t *I_dev);
 
@@ -216,6 +222,15 @@ VS_API int vs_dev_copy(int device, void *dst_dev, const void *src_dev, int64_t b
  * data, which draws more power and lowers the sustained clock).  Best of
  * five timed runs after a warm-up. */
 VS_API int vs_dev_probe(int device, int what, int64_t bytes, double *result);
+/* The scans' MFMA accumulation on given operands (test support for the
+ * rounding model behind the top-k exactness check): shape 0 chains
+ * v_mfma_f32_32x32x16_bf16 (M = N = 32, K-step 16), shape 1
+ * v_mfma_f32_16x16x32_bf16 (M = N = 16, K-step 32).  Host buffers: A
+ * [npass][M][K] and B [npass][N][K] bf16 bits, K = nsteps * K-step; C and D
+ * [M][N] fp32.  D = C, then for each K-step s and each pass p in order
+ * D += A_p[:, s] B_p[:, s]^T.  1 <= nsteps <= 4096, 1 <= npass <= 4. */
+VS_API int vs_dev_mfma_chain(int device, int shape, int64_t nsteps, int64_t npass,
+                             const uint16_t *A, const uint16_t *B, const float *C, float *D);
 VS_API int vs_device_count(int *count);
 VS_API int vs_device_name(int device, char *buf, int64_t len);
 
@@ -250,7 +265,6 @@ VS_API int vs_index_sync(vs_index *idx);
  *   "gemm"        -1 planner rule (rows >= 256 elements, batch >= 512), 0 off, 1 any d
  *   "gemm_min_nq" smallest batch on the GEMM-tiled scan (0: the rule's)
  *   "gemm_wq", "gemm_qb", "gemm_kc"  force that GEMM shape field (0: any)
- *   "gemm_dma"    1 allows the LDS-DMA GEMM shapes where the build enables them
  *   "share"       -1 rule (bf16 rows of 128 elements, batch >= 256), 0 off, 1 also 256
  *   "coarse"      1: one-pass bf16 selection of fp32 rows (range, self-join, k-means)
  *   "copy16"      1: that selection reads a bf16 copy of the rows

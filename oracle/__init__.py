@@ -96,6 +96,31 @@ def flat_search(xb, xq, k: int, metric: int, nthreads: int = 1):
     return D, I
 
 
+class _Result:
+    """The fields benchIndex reads of a SearchResult (index.dart:28-35)."""
+
+    def __init__(self, D, I):
+        self.distances, self.ids = D, I
+        self.nq, self.k = D.shape
+
+
+class FlatIndex:
+    """The CPU IndexFlat (index_flat.dart:17-97) as an index object for the
+    bench harness: the rows of the `IndexFlatL2` / `IndexFlatIP` rows of
+    bench_faiss.dart:55-103, timed by the same benchIndex as the GPU index."""
+
+    def __init__(self, xb, metric: int, nthreads: int = 1):
+        self.xb = _f32(xb)
+        self.metric, self.nthreads = int(metric), int(nthreads)
+
+    @property
+    def ntotal(self) -> int:
+        return int(self.xb.shape[0])
+
+    def search(self, xq, k: int):
+        return _Result(*flat_search(self.xb, xq, k, self.metric, self.nthreads))
+
+
 def flat_range_search(xb, xq, radius: float, metric: int, nthreads: int = 1):
     """IndexFlat.rangeSearch (index_flat.dart:99-137). Returns CSR (lims int64, D, I)."""
     xb = _f32(xb)

@@ -2,7 +2,8 @@
 own harness tests (test/vector_store_test.dart:2750-2930): recall of the
 flat baseline, sweep rows, RFC-4180 CSV, GFM Markdown, Pareto frontier,
 argument checks.  The index here is a small numpy flat index (host logic
-only); tests/test_gpu_bench_harness.py runs the harness on the GPU index."""
+only); tests/test_gpu_bench_harness.py runs it on the GPU index beside the
+CPU oracle, as bench_faiss.dart's four flat rows."""
 import numpy as np
 import pytest
 

@@ -48,19 +48,10 @@ def _gemm(opts):
     opts(gemm=1, share=0, gemm_min_nq=256)
 
 
-# The LDS-DMA shapes (query planes, row waves, query waves, 32-row blocks per
-# wave, 32-query blocks per wave, LDS stages) of VS_GEMM_DMA_SHAPES; bf16 rows
-# only, tried before the register-staged shapes.
-DMA_SHAPES = [
-    (1, 2, 4, 4, 2, 4),
-    (1, 2, 2, 4, 2, 4),
-]
-
-
 def _force(opts, shape):
-    """Force a register-staged shape (the LDS-DMA shapes switched off)."""
+    """Force one GEMM shape."""
     _, _, _, wq, _, qb, kc = shape
-    opts(gemm_dma=0, gemm_wq=wq, gemm_qb=qb, gemm_kc=kc)
+    opts(gemm_wq=wq, gemm_qb=qb, gemm_kc=kc)
 
 
 def _search(vs, xb, xq, k, metric, storage, shape=None, key=None):
@@ -103,38 +94,15 @@ def test_gemm_shape_parity(vs, opts, shape, metric, k, d):
     assert_knn_parity(D, I, Dr, Ir, metric, rtol=1e-3 if storage == "bf16" else 1e-5)
 
 
-DMA_OFF = ("the LDS-DMA kernel is switched off (kGemmDmaEnabled = false in vs_api.hip): its "
-           "first GPU run (8-wave shape, d = 200, L2, k = 10) left the GPU faulted and the "
-           "cause has not been shown")
-
-
-@pytest.mark.skip(reason=DMA_OFF)
-@pytest.mark.parametrize("shape", DMA_SHAPES, ids=lambda s: "-".join(map(str, s)))
-@pytest.mark.parametrize("metric", [0, 1])
-@pytest.mark.parametrize("k,d", [(10, 200), (100, 768), (1, 72)])
-def test_gemm_dma_shape_parity(vs, opts, shape, metric, k, d):
-    """The LDS-DMA kernel in each built shape: bf16 rows and bf16 queries."""
-    _, _, wq, _, qb, _ = shape
-    opts(gemm_wq=wq, gemm_qb=qb)
-    xb, xq, storage = _inputs((1, 1), d, 51 + metric)
-    D, I, gemm = _search(vs, xb, xq, k, metric, storage,
-                         key="gemmdma:" + ",".join(map(str, shape)))
-    assert gemm >= 1
-    Dr, Ir = oracle.flat_search(syn.bf16_bits_to_f32(xb), xq, k, metric, NT)
-    assert_knn_parity(D, I, Dr, Ir, metric, rtol=1e-3)
-
-
-@pytest.mark.parametrize("dma,kc", [pytest.param(1, 32, marks=pytest.mark.skip(reason=DMA_OFF)),
-                                    (0, 64), (0, 32)])
+@pytest.mark.parametrize("kc", [64, 32])
 @pytest.mark.parametrize("wq,qb", [(4, 2), (2, 2)])
-def test_gemm_config2_exact(vs, opts, wq, qb, dma, kc):
+def test_gemm_config2_exact(vs, opts, wq, qb, kc):
     """configs[1] arithmetic on a 100k slice with 1,000 queries: integer
-    distances, bit-exact, k = 100, on the LDS-DMA and register-staged
-    kernels (K-chunks of 64 and 32)."""
-    opts(gemm_wq=wq, gemm_qb=qb, gemm_dma=dma, gemm_kc=kc)
+    distances, bit-exact, k = 100, with K-chunks of 64 and 32."""
+    opts(gemm_wq=wq, gemm_qb=qb, gemm_kc=kc)
     xb = syn.int_grid(100_000, 128, 1234, 0)
     xq = syn.int_grid(1000, 128, 1234, 1)
-    key = f"gemmdma:1,2,{wq},4,{qb},4" if dma else _key((1, 1, 2, wq, 4, qb, kc))
+    key = _key((1, 1, 2, wq, 4, qb, kc))
     D, I, gemm = _search(vs, xb, xq, 100, 0, "auto", key=key)
     assert gemm >= 1
     Dr, Ir = oracle.flat_search(xb, xq, 100, 0, NT)

@@ -90,3 +90,35 @@ def test_shards_equal_flat(vs, metric):
     assert_knn_parity(r.distances, r.ids, Dr, Ir, metric)
     for s in sh.shards:
         s.close()
+
+
+def test_shards_prepopulated(vs):
+    """Shards that already hold rows: ntotal starts at their sum (the
+    reference's constructor folds it), so later adds continue the external id
+    sequence and its round-robin dealing (index_shards.dart constructor, add)."""
+    x, q = data(n=3000)
+    a, b = (vs.GpuIndexFlat(32, vs.Metric.l2, storage="f32") for _ in range(2))
+    # external ids 0..999 dealt round-robin by hand: even ids in a, odd in b
+    a.add(x[0:1000:2])
+    b.add(x[1:1000:2])
+    sh = vs.IndexShards([a, b])
+    assert sh.ntotal == 1000
+    sh.add(x[1000:])
+    assert sh.ntotal == 3000 and a.ntotal == 1500 and b.ntotal == 1500
+    r = sh.search(q, 10)
+    Dr, Ir = oracle.flat_search(x, q, 10, 0, NT)
+    assert_knn_parity(r.distances, r.ids, Dr, Ir, 0)
+    a.close()
+    b.close()
+
+
+def test_id_map_duplicate_external_ids(vs):
+    """A duplicated external id resolves to its last internal offset, as the
+    reference's reverse map built in offset order does (index_id_map.dart
+    internalOf); ids never added give -1."""
+    x, _ = data(n=6)
+    m = vs.IndexIDMap(vs.GpuIndexFlat(32, vs.Metric.l2, storage="f32"))
+    m.add_with_ids(x, [7, 3, 7, 9, 3, 5])
+    assert [m.internal_of(e) for e in (7, 3, 9, 5, 11)] == [2, 4, 3, 5, -1]
+    assert m.id_of(0) == 7 and m.id_of(4) == 3
+    m.inner.close()

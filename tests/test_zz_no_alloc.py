@@ -3,6 +3,10 @@ called through the C ABI, against the existing vs_index_search_device on the
 same index and device buffers: two calls in a row, the second with a smaller
 input, each to the parity bar (distances bit-identical, ids equal except in
 exact ties), and against the oracle (IndexFlat.search, index_flat.dart:62-97).
+
+Every allocation-free call runs with the test-support countdown "fail_alloc"
+armed at 1, so that any device or pinned host allocation the library makes
+during the call fails it with VS_ERR_OOM.
 """
 import numpy as np
 import pytest
@@ -19,9 +23,16 @@ NT = oracle.default_threads()
 def _search(idx, entry, q, k, dtype):
     nq = q.shape[0]
     qb, Db, Ib = NN.DeviceBuffer(q.nbytes), NN.DeviceBuffer(nq * k * 4), NN.DeviceBuffer(nq * k * 4)
+    armed = entry.endswith("_noalloc")
     try:
         qb.upload(q)
-        NN.check(getattr(NN.load(), entry)(idx.handle, qb.ptr, dtype, nq, k, Db.ptr, Ib.ptr))
+        if armed:  # the next allocation of this thread fails the call
+            idx.set_option("fail_alloc", 1)
+        try:
+            NN.check(getattr(NN.load(), entry)(idx.handle, qb.ptr, dtype, nq, k, Db.ptr, Ib.ptr))
+        finally:
+            if armed:
+                idx.set_option("fail_alloc", 0)
         D = np.empty((nq, k), np.float32)
         I = np.empty((nq, k), np.int32)
         Db.download(D)
