@@ -293,6 +293,58 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[QB][RB], const Sca
     }
 }
 
+// Final cut of a top-k scan (MODE 0): every list of this wave's queries
+// holds its kk best in slots [0, kk), padded -- one lane per list where kk
+// fits in registers, else the lists one after another.  lb0: index of the
+// wave's first list bound (its lists' own final thresholds, for the merge's
+// verification when lists keep fewer than kk_final).
+template <int WR, int BQ, int QB>
+__device__ __forceinline__ void gemm_final_cut(const ScanKArgs &a, const EpiCtx &e, int64_t lb0) {
+    const int64_t q0 = e.q0;
+    const int qw0 = e.qw0, lane = e.lane;
+    int *cnt_w = e.cnt_w;
+    float *thr = e.thr, *thr_w = e.thr_w, *sv_w = e.sv_w;
+    int *si_w = e.si_w;
+    float *cv = e.cv;
+    int32_t *ci = e.ci;
+    wave_sync();
+    if (a.kk <= 32) {
+        // (64 lists, one per lane, at a time)
+        for (int g0 = qw0; g0 < qw0 + 32 * QB; g0 += 64) {
+            const int nl = min(64, qw0 + 32 * QB - g0);
+            if (a.kk <= 16)
+                cut_lists_lanes<16>(cv + (int64_t)g0 * a.cap, ci + (int64_t)g0 * a.cap, cnt_w + g0,
+                                    thr_w + g0, thr + g0, nl, WR, &a.gthr[q0 + g0], a.cap, a.kk,
+                                    a.kk_final, a.publish_block, a.kk, true, lane, BQ);
+            else
+                cut_lists_lanes<32>(cv + (int64_t)g0 * a.cap, ci + (int64_t)g0 * a.cap, cnt_w + g0,
+                                    thr_w + g0, thr + g0, nl, WR, &a.gthr[q0 + g0], a.cap, a.kk,
+                                    a.kk_final, a.publish_block, a.kk, true, lane, BQ);
+        }
+    } else {
+        for (int q = qw0; q < qw0 + 32 * QB; ++q) {
+            const int c = cnt_w[q];
+            if (c > a.kk) {
+                flush_list(cv + (int64_t)q * a.cap, ci + (int64_t)q * a.cap, &cnt_w[q], &thr_w[q],
+                           &thr[q], BQ, WR, &a.gthr[q0 + q], sv_w, si_w, a.cap, a.kk, a.kk_final,
+                           a.publish_block, lane);
+            } else {
+                for (int j = c + lane; j < a.kk; j += 64) {
+                    cv[(int64_t)q * a.cap + j] = VS_INF;
+                    ci[(int64_t)q * a.cap + j] = -1;
+                }
+            }
+        }
+    }
+    // a list cut to kk < kk_final entries may have dropped rows at or
+    // above its own final threshold: the merge checks that value against
+    // the query's final kk_final-th value
+    if (a.lbound) {
+        wave_sync();
+        for (int q = qw0 + lane; q < qw0 + 32 * QB; q += 64) a.lbound[lb0 + q] = thr_w[q];
+    }
+}
+
 // The register-staged kernel writes the next chunk's tiles to LDS between
 // the MFMAs of the current chunk's last K-step.
 constexpr bool kInterleaveStores = true;
@@ -572,48 +624,276 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
         __syncthreads();
     }
 
-    if constexpr (MODE == 0) {
-        // final: every list of this wave's queries holds its kk best in
-        // slots [0, kk), padded -- one lane per list where kk fits in
-        // registers, else the lists one after another
-        wave_sync();
-        if (a.kk <= 32) {
-            // (64 lists, one per lane, at a time)
-            for (int g0 = qw0; g0 < qw0 + 32 * QB; g0 += 64) {
-                const int nl = min(64, qw0 + 32 * QB - g0);
-                if (a.kk <= 16)
-                    cut_lists_lanes<16>(cv + (int64_t)g0 * a.cap, ci + (int64_t)g0 * a.cap,
-                                        cnt_w + g0, thr_w + g0, thr + g0, nl, WR, &a.gthr[q0 + g0],
-                                        a.cap, a.kk, a.kk_final, a.publish_block, a.kk, true, lane,
-                                        BQ);
-                else
-                    cut_lists_lanes<32>(cv + (int64_t)g0 * a.cap, ci + (int64_t)g0 * a.cap,
-                                        cnt_w + g0, thr_w + g0, thr + g0, nl, WR, &a.gthr[q0 + g0],
-                                        a.cap, a.kk, a.kk_final, a.publish_block, a.kk, true, lane,
-                                        BQ);
-            }
-        } else for (int q = qw0; q < qw0 + 32 * QB; ++q) {
-            const int c = cnt_w[q];
-            if (c > a.kk) {
-                flush_list(cv + (int64_t)q * a.cap, ci + (int64_t)q * a.cap, &cnt_w[q], &thr_w[q],
-                           &thr[q], BQ, WR, &a.gthr[q0 + q], sv_w, si_w, a.cap, a.kk, a.kk_final,
-                           a.publish_block, lane);
-            } else {
-                for (int j = c + lane; j < a.kk; j += 64) {
-                    cv[(int64_t)q * a.cap + j] = VS_INF;
-                    ci[(int64_t)q * a.cap + j] = -1;
+    if constexpr (MODE == 0)
+        gemm_final_cut<WR, BQ, QB>(a, ectx, ((qblk * a.nsplit + split) * WR + wr) * (int64_t)BQ);
+}
+
+// ---------------------------------------------------------------------------
+// Four-wave pipelined GEMM-tiled scan: bf16 rows, one query plane (configs[2]
+// at large batches; the self-join's bf16 copy of the rows).
+//
+// 256 rows x 256 queries per tile.  Wave (wr, wq) multiplies rows
+// wr*128 .. +128 by queries wq*128 .. +128 with sixteen 32 x 32 accumulator
+// blocks (256 accumulation registers), one wave per SIMD: per 16-element
+// K-step 4 row and 4 query fragment reads feed 16 MFMAs (0.5 reads per MFMA).
+//
+// K-chunks of 32 elements cycle through four LDS stages (chunk g in stage
+// g % 4; rows and query planes 64 bytes each, 16-byte pieces XOR-swizzled by
+// (row >> 2) & 3, so the 16 lanes of a fragment read hit 16 distinct 16-byte
+// bank groups of the 64-bank LDS, and so do the row writes).  During chunk g:
+//   - the global loads of chunk g + 3 are issued (into the staging set that
+//     chunk g + 1 left free);
+//   - K-step 0 multiplies from registers while K-step 1's fragments are read;
+//   - chunk g + 2 (loaded during chunk g - 1) is written to its stage, whose
+//     last reader, chunk g - 2, finished before the previous barrier;
+//   - K-step 1 multiplies while the fragments of chunk g + 1's K-step 0 --
+//     written during chunk g - 1, so visible since the previous barrier --
+//     are read;
+//   - one barrier.
+// So the matrix pipe never waits on a fragment read issued after a barrier,
+// and a global load has two chunks (about 2,000 cycles) to arrive.  A tile's
+// first chunk sits in stage 0 (ld is a multiple of 128 elements for bf16
+// rows, so a tile has a multiple of four chunks), which also carries the
+// tile's row norms (L2).  The epilogue (lists, thresholds, range appends) is
+// the shared gemm_epilogue, once per tile.
+// ---------------------------------------------------------------------------
+namespace g4 {
+constexpr int NW = 4, NT = 256, WR = 2, WQ = 2, RB = 4, QB = 4, BR = 256, BQ = 256;
+constexpr int KC = 32, NSTG = 4;
+constexpr int ROWB = KC * 2;                 // bytes per row (query) per chunk
+constexpr int A_OFF = 0, B_OFF = BR * ROWB;  // within a stage
+constexpr int N_OFF = B_OFF + BQ * ROWB;     // row norms of the tile (stage 0, L2)
+constexpr int STAGE = N_OFF + BR * 4;
+constexpr int LOADS = BR * (ROWB / 16) / NT;  // 16-byte loads per thread and operand
+static_assert(LOADS == 4 && BQ == BR, "thread layout of the loads");
+static_assert(BR <= kRowSlack, "the last row tile reads at most kRowSlack rows past the end");
+}  // namespace g4
+
+size_t gemm4_lds_bytes(int cap) {
+    return (size_t)g4::NSTG * g4::STAGE + (size_t)g4::WR * g4::BQ * 8 + (size_t)g4::NW * cap * 8;
+}
+
+template <int MODE, bool L2>
+__global__ __launch_bounds__(256) void gemm4_scan_kernel(ScanKArgs a) {
+    using namespace g4;
+    extern __shared__ __align__(16) char smem[];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
+    const int wr = wave % WR, wq = wave / WR;
+
+    int64_t split, qblk;
+    if (!map_block_grouped(a.nqblk, a.nsplit, a.qgroup, a.qspc, &split, &qblk)) return;
+    int64_t r0 = split * a.rows_per_split;
+    const int64_t r1 = min(a.n, r0 + a.rows_per_split);
+    const int64_t q0 = qblk * BQ;
+    if (MODE == 1 && a.self_join) r0 = max(r0, q0);  // only ids > query
+    if (r0 >= r1) return;
+
+    // LDS: four stages, then the lists' counters and thresholds [WR][BQ] and
+    // the per-wave sort buffers [NW][cap]
+    int *cnt = (int *)(smem + NSTG * STAGE);
+    float *thr = (float *)(cnt + WR * BQ);
+    float *sv = thr + WR * BQ;
+    int *si = (int *)(sv + NW * a.cap);
+    for (int t = tid; t < WR * BQ; t += NT) {
+        cnt[t] = 0;
+        thr[t] = q0 + (t % BQ) < a.nq ? VS_INF : -VS_INF;
+    }
+    int *cnt_w = cnt + wr * BQ;
+    float *thr_w = thr + wr * BQ;
+    const int64_t list_base = ((qblk * a.nsplit + split) * WR + wr) * (int64_t)BQ * a.cap;
+    float *cv = MODE == 0 ? a.cand_v + list_base : nullptr;
+    int32_t *ci = MODE == 0 ? a.cand_i + list_base : nullptr;
+    const int qw0 = wq * 32 * QB;
+    const EpiCtx ectx{q0, r1, qw0, l32, h, lane, cnt, cnt_w, thr, thr_w,
+                      sv + wave * a.cap, si + wave * a.cap, cv, ci};
+
+    float thr_r[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+        const int64_t qg = q0 + qw0 + qb * 32 + l32;
+        if (MODE == 0)
+            thr_r[qb] = qg < a.nq ? VS_INF : -VS_INF;
+        else
+            thr_r[qb] = qg < a.nq ? a.athr[qg] : -VS_INF;
+    }
+
+    const int nkc = (int)(a.ld / KC);  // a multiple of 4
+    const int row_bytes = (int)(a.ld * 2);
+    const int ntiles = (int)((r1 - r0 + BR - 1) / BR);
+    const int total = ntiles * nkc;  // chunks of this workgroup
+
+    // ---- global -> staging registers: thread t loads rows (queries)
+    // t / 4 + 64 i, 16-byte piece t % 4 of the chunk ----
+    const int ld_row = tid >> 2, ld_pc = tid & 3;
+    const int ld_voff_a = ld_row * row_bytes + ld_pc * 16;
+    const int ld_voff_b = ld_row * (row_bytes * 2) + ld_pc * 16;  // two planes per query
+    const __amdgpu_buffer_rsrc_t qrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(a.qp + q0 * 2 * a.ld), 0, (int)min((int64_t)INT32_MAX, (int64_t)BQ * 4 * a.ld),
+        kBufRsrcWord3);
+    // LDS byte offset (within a stage) of the thread's writes: row ld_row +
+    // 64 i, physical piece ld_pc ^ ((row >> 2) & 3) (64 i keeps the swizzle)
+    const int st_off = ld_row * ROWB + ((ld_pc ^ ((ld_row >> 2) & 3)) << 4);
+
+    u32x4_t sa[2][LOADS], sb[2][LOADS];
+    f32x4_t sn[2];
+
+    // chunk index g -> (tile row, K-chunk)
+    auto chunk_pos = [&](int g, int64_t *trow, int *kc) __attribute__((always_inline)) {
+        const int t = g / nkc;
+        *kc = g - t * nkc;
+        *trow = r0 + (int64_t)t * BR;
+    };
+    auto issue = [&](auto set_c, int g) __attribute__((always_inline)) {
+        constexpr int S = decltype(set_c)::value;
+        int64_t trow;
+        int kc;
+        chunk_pos(g, &trow, &kc);
+        // the last tile reads at most BR rows past the end, inside the
+        // allocation's slack rows; the resource stops there
+        const int64_t lim = min((int64_t)INT32_MAX, (a.n - trow + BR) * (int64_t)row_bytes);
+        const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)((const char *)a.xb + trow * row_bytes), 0, (int)lim, kBufRsrcWord3);
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) {
+            sa[S][i] = buf_load16(xrs, ld_voff_a, i * 64 * row_bytes + kc * ROWB);
+            sb[S][i] = buf_load16(qrs, ld_voff_b, i * 64 * row_bytes * 2 + kc * ROWB);
+        }
+        if (L2 && kc == 0 && tid < BR / 4) sn[S] = *(const f32x4_t *)(a.xn + trow + 4 * tid);
+    };
+    auto write = [&](auto set_c, auto stage_c, int g) __attribute__((always_inline)) {
+        constexpr int S = decltype(set_c)::value, T = decltype(stage_c)::value;
+        char *st = smem + T * STAGE;
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) {
+            *(u32x4_t *)(st + A_OFF + st_off + i * 64 * ROWB) = sa[S][i];
+            *(u32x4_t *)(st + B_OFF + st_off + i * 64 * ROWB) = sb[S][i];
+        }
+        if (L2 && T == 0 && tid < BR / 4) *(f32x4_t *)(st + N_OFF + 16 * tid) = sn[S];
+        (void)g;
+    };
+
+    // ---- fragments: lane (l32, h) reads row wr*128 + 32 rb + l32 and query
+    // qw0 + 32 qb + l32, logical piece 2 ks + h of the chunk ----
+    const int swz = (l32 >> 2) & 3;
+    const int fa0 = (wr * 128 + l32) * ROWB + (((0 + h) ^ swz) << 4);
+    const int fa1 = (wr * 128 + l32) * ROWB + (((2 + h) ^ swz) << 4);
+    const int fb0 = B_OFF + (qw0 + l32) * ROWB + (((0 + h) ^ swz) << 4);
+    const int fb1 = B_OFF + (qw0 + l32) * ROWB + (((2 + h) ^ swz) << 4);
+    bf16x8_t fa[2][RB], fb[2][QB];
+    auto read_frags = [&](auto buf_c, auto stage_c, auto ks_c) __attribute__((always_inline)) {
+        constexpr int F = decltype(buf_c)::value, T = decltype(stage_c)::value;
+        constexpr int KS = decltype(ks_c)::value;
+        const char *st = smem + T * STAGE;
+        const int oa = KS == 0 ? fa0 : fa1, ob = KS == 0 ? fb0 : fb1;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+            fa[F][rb] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t *)(st + oa + rb * 32 * ROWB));
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb)
+            fb[F][qb] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t *)(st + ob + qb * 32 * ROWB));
+    };
+
+    f32x16_t acc[QB][RB];
+    uint32_t gt[QB];
+
+    // 16 MFMAs of one K-step from fragment buffer F; FIRST: the tile's first
+    // K-step, whose C operand is the row norms (L2) or zero (IP)
+    auto mfmas = [&](auto buf_c, auto first_c) __attribute__((always_inline)) {
+        constexpr int F = decltype(buf_c)::value;
+        constexpr bool FIRST = decltype(first_c)::value;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            f32x16_t c0;
+            if constexpr (FIRST) {
+                if constexpr (L2) {
+                    const float *Ns = (const float *)(smem + N_OFF) + wr * 128 + rb * 32 + 4 * h;
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const f32x4_t q4 = *(const f32x4_t *)(Ns + 8 * u);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) c0[4 * u + e] = q4[e];
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) c0[e] = 0.f;
                 }
             }
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb)
+                acc[qb][rb] = mfma32_bf16(fa[F][rb], fb[F][qb], FIRST ? c0 : acc[qb][rb]);
         }
-        // a list cut to kk < kk_final entries may have dropped rows at or
-        // above its own final threshold: the merge checks that value against
-        // the query's final kk_final-th value
-        if (a.lbound) {
-            wave_sync();
-            const int64_t lb = ((qblk * a.nsplit + split) * WR + wr) * (int64_t)BQ;
-            for (int q = qw0 + lane; q < qw0 + 32 * QB; q += 64) a.lbound[lb + q] = thr_w[q];
+    };
+
+    // One chunk g (stage T = g % 4, staging set S = g % 2 for chunk g + 2).
+    auto chunk = [&](auto stage_c, auto first_c, int g) __attribute__((always_inline)) {
+        constexpr int T = decltype(stage_c)::value;
+        constexpr int S = T & 1;
+        constexpr bool FIRST = decltype(first_c)::value;
+        if (g + 3 < total) issue(std::integral_constant<int, S ^ 1>{}, g + 3);
+        // K-step 0 from fa/fb[0] while K-step 1's fragments are read
+        read_frags(std::integral_constant<int, 1>{}, stage_c, std::integral_constant<int, 1>{});
+        mfmas(std::integral_constant<int, 0>{}, first_c);
+        __builtin_amdgcn_sched_group_barrier(0x020, 2 * LOADS, 0);  // global loads
+        __builtin_amdgcn_sched_group_barrier(0x100, RB + QB, 0);    // fragment reads
+        __builtin_amdgcn_sched_group_barrier(0x008, RB * QB, 0);    // MFMAs
+        __builtin_amdgcn_sched_barrier(0);
+        // chunk g + 2 into its stage, then K-step 1 while the next chunk's
+        // K-step 0 fragments are read
+        if (g + 2 < total)
+            write(std::integral_constant<int, S>{}, std::integral_constant<int, (T + 2) & 3>{}, g + 2);
+        if (g + 1 < total)
+            read_frags(std::integral_constant<int, 0>{}, std::integral_constant<int, (T + 1) & 3>{},
+                       std::integral_constant<int, 0>{});
+        mfmas(std::integral_constant<int, 1>{}, std::false_type{});
+        __builtin_amdgcn_sched_group_barrier(0x200, 2 * LOADS, 0);  // LDS writes
+        __builtin_amdgcn_sched_group_barrier(0x100, RB + QB, 0);    // fragment reads
+        __builtin_amdgcn_sched_group_barrier(0x008, RB * QB, 0);    // MFMAs
+        __builtin_amdgcn_sched_barrier(0);
+        (void)FIRST;
+        __syncthreads();
+    };
+
+    // prologue: chunks 0 and 1 into stages 0 and 1 (set 0 and 1), chunk 2's
+    // loads issued into set 0, the first fragments read
+    issue(std::integral_constant<int, 0>{}, 0);
+    if (1 < total) issue(std::integral_constant<int, 1>{}, 1);
+    write(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, 0);
+    if (1 < total) write(std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{}, 1);
+    if (2 < total) issue(std::integral_constant<int, 0>{}, 2);
+    __syncthreads();
+    read_frags(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{},
+               std::integral_constant<int, 0>{});
+
+    // the first tile seeds the lists' thresholds when two lanes can hold kk
+    // values (ceil(kk / 2) <= 16 * RB)
+    bool seeded = (a.kk + 1) / 2 > 16 * RB;
+    int g = 0;
+    for (int64_t t0 = r0; t0 < r1; t0 += BR) {
+        if constexpr (MODE == 0) {
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb)
+                gt[qb] = __hip_atomic_load(&a.gthr[q0 + qw0 + qb * 32 + l32], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
         }
+        chunk(std::integral_constant<int, 0>{}, std::true_type{}, g);
+        chunk(std::integral_constant<int, 1>{}, std::false_type{}, g + 1);
+        chunk(std::integral_constant<int, 2>{}, std::false_type{}, g + 2);
+        chunk(std::integral_constant<int, 3>{}, std::false_type{}, g + 3);
+        g += 4;
+        for (int kc = 4; kc < nkc; kc += 4) {
+            chunk(std::integral_constant<int, 0>{}, std::false_type{}, g);
+            chunk(std::integral_constant<int, 1>{}, std::false_type{}, g + 1);
+            chunk(std::integral_constant<int, 2>{}, std::false_type{}, g + 2);
+            chunk(std::integral_constant<int, 3>{}, std::false_type{}, g + 3);
+            g += 4;
+        }
+        gemm_epilogue<WR, BQ, RB, QB, MODE>(acc, a, ectx, t0 + wr * 128, thr_r, gt, seeded);
+        __syncthreads();
     }
+
+    if constexpr (MODE == 0)
+        gemm_final_cut<WR, BQ, QB>(a, ectx, ((qblk * a.nsplit + split) * WR + wr) * (int64_t)BQ);
 }
 
 template <int MODE>
