@@ -188,7 +188,9 @@ def mfma_passes(idx):
     bf16 selection ran (GEMM shapes of storage code 2, or 1 on the bf16 copy
     of the rows, or the row-shared scan, which reads fp32 rows only that
     way), else 3 (hi*q0 + lo*q0 + hi*q1 of the split-bf16 planes)."""
-    coarse = sum(idx.prof_get(f"gemm:{st},1,2,{wq},4,2,32")[0] for st in (1, 2) for wq in (2, 4))
+    coarse = sum(idx.prof_get(f"gemm:{st},1,2,{wq},4,2,{kc}")[0]
+                 for st in (1, 2) for wq in (2, 4) for kc in (32, 64))
+    coarse += idx.prof_get("gemm:1,1,2,2,4,4,32")[0]  # the four-wave kernel on the bf16 copy
     coarse += idx.prof_get("shared")[0]
     return 1 if coarse else 3
 
@@ -783,6 +785,9 @@ def main():
     ap.add_argument("--no-single-core", action="store_true")
     ap.add_argument("--csv", default="", help="write the benchIndex rows as CSV (toBenchCsv)")
     ap.add_argument("--md", default="", help="write the benchIndex rows as Markdown")
+    ap.add_argument("--opt", action="append", default=[], metavar="NAME=VALUE",
+                    help="planner option set on every index (vs_index_set_option), for "
+                         "profiling runs of a kernel variant; the default run sets none")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the multi-GPU "
@@ -793,7 +798,11 @@ def main():
         return
     import vector_store as vs
     from vector_store import _native as NN
+    from vector_store import gpu_index_flat
 
+    for o in args.opt:
+        name, _, value = o.partition("=")
+        gpu_index_flat.DEFAULT_OPTIONS[name] = int(value)
     if vs.device_count() < 1:
         raise SystemExit("no HIP device visible")
     if args.workload == "copy":
@@ -831,6 +840,8 @@ def main():
         out = run_join(vs, NN, args, ctx)
     out["host"] = ctx["host"]
     out["measured_peaks"] = ctx["peaks"]
+    if args.opt:
+        out["options"] = dict(gpu_index_flat.DEFAULT_OPTIONS)
     if ctx.get("bench_rows"):
         from vector_store.bench import to_bench_csv, to_bench_markdown
 

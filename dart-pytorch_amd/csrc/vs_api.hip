@@ -174,6 +174,7 @@ struct VsOptions {
     int gemm = -1;         // GEMM-tiled scan: -1 planner rule (rows >= 256 elements), 0 off, 1 any d
     int gemm_min_nq = 0;   // smallest batch on the GEMM-tiled scan (0: 512 by rule, 256 when forced)
     int gemm_wq = 0, gemm_qb = 0, gemm_kc = 0;  // force a GEMM shape field (0: any)
+    int gemm4 = 0;         // GEMM-tiled scan: 1 = the four-wave pipelined kernel where it applies
     int share = -1;        // row-shared scan: -1 rule (rows of 128 elements), 0 off, 1 also 256
     int coarse = 1;        // one-pass bf16 selection of fp32 rows (range, self-join, k-means)
     int copy16 = 1;        // the one-pass selection reads a bf16 copy of the fp32 rows
@@ -518,7 +519,23 @@ bool plan_gemm(const vs_index *x, int64_t nq, int64_t nrows, int planes, int sto
     const Shape *pick = nullptr;
     int kk = p->kk, cap = 0;
     size_t lds = 0;
+    // the four-wave pipelined kernel: bf16 rows whose stride is whole
+    // groups of four 32-element K-chunks, one query plane
+    static const Shape pipe4 = {1, 1, 2, 2, 4, 4, 32};
+    p->g_pipe = 0;
+    if (o.gemm4 && storage == 1 && planes == 1 && x->ld % 128 == 0 && (!fwq || fwq == 2) &&
+        (!fqb || fqb == 4) && (!fkc || fkc == 32)) {
+        kk = p->kk;
+        if (!kk_forced && kk < p->kk_final) kk = std::max(kk, p->kk_final / pipe4.wr);
+        cap = (int)next_pow2(kk + 32 * pipe4.rb + 16);
+        lds = vs::gemm4_lds_bytes(cap);
+        if (lds <= x->lds_max) {
+            pick = &pipe4;
+            p->g_pipe = 1;
+        }
+    }
     for (const Shape &sh : shapes) {
+        if (pick) break;
         if (sh.st != storage || sh.pb != planes) continue;
         if (fwq && sh.wq != fwq) continue;
         if (fqb && sh.qb != fqb) continue;
@@ -1303,6 +1320,12 @@ int range_core(vs_index *x, const vs::PreparedQueries &pq, double radius, int se
             }
         }
         if (x->xb16_version == x->version) {
+            // the copy holds bf16 rows: their own plan (the four-wave
+            // pipelined kernel applies to them)
+            vs::ScanPlan p16;
+            if (plan_scan(x, pq.nq, x->ntotal, 1, 8, 1, &p16, false, 0, true) == VS_OK &&
+                p16.kind == 2 && p16.bn <= 256 && p16.nqblk * p16.bn <= pq.nq_pad)
+                plan = p16;
             plan.tile_st = 1;
             scan_rows = x->xb16.p;
             scan_storage = 1;
@@ -2730,6 +2753,7 @@ int vs_index_set_option(vs_index *x, const char *name, int64_t value) {
         {"gemm_wq", &VsOptions::gemm_wq, 0, 8},
         {"gemm_qb", &VsOptions::gemm_qb, 0, 8},
         {"gemm_kc", &VsOptions::gemm_kc, 0, 64},
+        {"gemm4", &VsOptions::gemm4, 0, 1},
         {"share", &VsOptions::share, -1, 1},
         {"coarse", &VsOptions::coarse, 0, 1},
         {"copy16", &VsOptions::copy16, 0, 1},

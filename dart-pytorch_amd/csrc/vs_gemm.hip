@@ -629,33 +629,36 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Four-wave pipelined GEMM-tiled scan: bf16 rows, one query plane (configs[2]
-// at large batches; the self-join's bf16 copy of the rows).
+// Four-wave pipelined GEMM-tiled scan (option gemm4): bf16 rows, one query
+// plane (configs[2] at large batches; the self-join's bf16 copy of the rows).
 //
 // 256 rows x 256 queries per tile.  Wave (wr, wq) multiplies rows
 // wr*128 .. +128 by queries wq*128 .. +128 with sixteen 32 x 32 accumulator
 // blocks (256 accumulation registers), one wave per SIMD: per 16-element
-// K-step 4 row and 4 query fragment reads feed 16 MFMAs (0.5 reads per MFMA).
+// K-step 4 row and 4 query fragment reads feed 16 MFMAs (0.5 reads per MFMA,
+// against 0.75 in the eight-wave kernel).
 //
 // K-chunks of 32 elements cycle through four LDS stages (chunk g in stage
 // g % 4; rows and query planes 64 bytes each, 16-byte pieces XOR-swizzled by
 // (row >> 2) & 3, so the 16 lanes of a fragment read hit 16 distinct 16-byte
 // bank groups of the 64-bank LDS, and so do the row writes).  During chunk g:
 //   - the global loads of chunk g + 3 are issued (into the staging set that
-//     chunk g + 1 left free);
-//   - K-step 0 multiplies from registers while K-step 1's fragments are read;
+//     chunk g + 1 left free), one after every second MFMA of K-step 0, while
+//     K-step 1's fragments are read, one after each other MFMA;
 //   - chunk g + 2 (loaded during chunk g - 1) is written to its stage, whose
-//     last reader, chunk g - 2, finished before the previous barrier;
-//   - K-step 1 multiplies while the fragments of chunk g + 1's K-step 0 --
-//     written during chunk g - 1, so visible since the previous barrier --
-//     are read;
+//     last reader, chunk g - 2, finished before the previous barrier, and the
+//     fragments of chunk g + 1's K-step 0 -- written during chunk g - 1, so
+//     visible since the previous barrier -- are read, both during the first
+//     half of K-step 1's MFMAs;
 //   - one barrier.
 // So the matrix pipe never waits on a fragment read issued after a barrier,
-// and a global load has two chunks (about 2,000 cycles) to arrive.  A tile's
-// first chunk sits in stage 0 (ld is a multiple of 128 elements for bf16
-// rows, so a tile has a multiple of four chunks), which also carries the
-// tile's row norms (L2).  The epilogue (lists, thresholds, range appends) is
-// the shared gemm_epilogue, once per tile.
+// and a global load has about one and a half chunks to arrive.  Loads are
+// issued unconditionally (past the end they read slack rows or nothing), so
+// the waits before the LDS writes leave the younger loads in flight.  A
+// tile's first chunk sits in stage 0 (ld is a multiple of 128 elements for
+// bf16 rows, so a tile has a multiple of four chunks), which also carries
+// the tile's row norms (L2).  The epilogue (lists, thresholds, range
+// appends) is the shared gemm_epilogue, once per tile.
 // ---------------------------------------------------------------------------
 namespace g4 {
 constexpr int NW = 4, NT = 256, WR = 2, WQ = 2, RB = 4, QB = 4, BR = 256, BQ = 256;
@@ -666,6 +669,8 @@ constexpr int N_OFF = B_OFF + BQ * ROWB;     // row norms of the tile (stage 0, 
 constexpr int STAGE = N_OFF + BR * 4;
 constexpr int LOADS = BR * (ROWB / 16) / NT;  // 16-byte loads per thread and operand
 static_assert(LOADS == 4 && BQ == BR, "thread layout of the loads");
+static_assert(2 * LOADS == RB + QB && RB * QB == 4 * LOADS,
+              "per K-step: one load (or LDS write) and one fragment read per two MFMAs");
 static_assert(BR <= kRowSlack, "the last row tile reads at most kRowSlack rows past the end");
 }  // namespace g4
 
@@ -720,8 +725,6 @@ __global__ __launch_bounds__(256) void gemm4_scan_kernel(ScanKArgs a) {
 
     const int nkc = (int)(a.ld / KC);  // a multiple of 4
     const int row_bytes = (int)(a.ld * 2);
-    const int ntiles = (int)((r1 - r0 + BR - 1) / BR);
-    const int total = ntiles * nkc;  // chunks of this workgroup
 
     // ---- global -> staging registers: thread t loads rows (queries)
     // t / 4 + 64 i, 16-byte piece t % 4 of the chunk ----
@@ -736,32 +739,39 @@ __global__ __launch_bounds__(256) void gemm4_scan_kernel(ScanKArgs a) {
     const int st_off = ld_row * ROWB + ((ld_pc ^ ((ld_row >> 2) & 3)) << 4);
 
     u32x4_t sa[2][LOADS], sb[2][LOADS];
-    f32x4_t sn[2];
+    float sn;  // one row norm per thread (row tid of a tile)
 
-    // chunk index g -> (tile row, K-chunk)
-    auto chunk_pos = [&](int g, int64_t *trow, int *kc) __attribute__((always_inline)) {
-        const int t = g / nkc;
-        *kc = g - t * nkc;
-        *trow = r0 + (int64_t)t * BR;
+    // Every chunk's loads are issued unconditionally -- past the last chunk
+    // they read rows beyond the split end (inside the allocation's slack) or
+    // nothing at all (the resource's record count is zero) -- so the waits
+    // before the LDS writes count only the loads issued since (a skipped
+    // load would make every wait a full drain).
+    // buffer resources of a tile's rows and row norms: the last tile reads
+    // at most BR rows past the end, inside the allocation's slack rows
+    auto rows_rs = [&](int64_t trow) __attribute__((always_inline)) {
+        const int64_t lim =
+            min((int64_t)INT32_MAX, max((int64_t)0, (a.n - trow + BR) * (int64_t)row_bytes));
+        return __builtin_amdgcn_make_buffer_rsrc((void *)((const char *)a.xb + trow * row_bytes), 0,
+                                                 (int)lim, kBufRsrcWord3);
     };
-    auto issue = [&](auto set_c, int g) __attribute__((always_inline)) {
+    auto norms_rs = [&](int64_t trow) __attribute__((always_inline)) {
+        const int64_t lim = min((int64_t)INT32_MAX, max((int64_t)0, (a.n - trow + BR) * 4));
+        return __builtin_amdgcn_make_buffer_rsrc((void *)(a.xn + trow), 0, (int)lim, kBufRsrcWord3);
+    };
+    auto issue = [&](auto set_c, __amdgpu_buffer_rsrc_t xrs, int kc) __attribute__((always_inline)) {
         constexpr int S = decltype(set_c)::value;
-        int64_t trow;
-        int kc;
-        chunk_pos(g, &trow, &kc);
-        // the last tile reads at most BR rows past the end, inside the
-        // allocation's slack rows; the resource stops there
-        const int64_t lim = min((int64_t)INT32_MAX, (a.n - trow + BR) * (int64_t)row_bytes);
-        const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
-            (void *)((const char *)a.xb + trow * row_bytes), 0, (int)lim, kBufRsrcWord3);
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
             sa[S][i] = buf_load16(xrs, ld_voff_a, i * 64 * row_bytes + kc * ROWB);
             sb[S][i] = buf_load16(qrs, ld_voff_b, i * 64 * row_bytes * 2 + kc * ROWB);
         }
-        if (L2 && kc == 0 && tid < BR / 4) sn[S] = *(const f32x4_t *)(a.xn + trow + 4 * tid);
     };
-    auto write = [&](auto set_c, auto stage_c, int g) __attribute__((always_inline)) {
+    // the row norms of a tile: thread t loads row t
+    auto issue_norms = [&](__amdgpu_buffer_rsrc_t nrs) __attribute__((always_inline)) {
+        if constexpr (L2)
+            sn = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(nrs, tid * 4, 0, 0));
+    };
+    auto write = [&](auto set_c, auto stage_c) __attribute__((always_inline)) {
         constexpr int S = decltype(set_c)::value, T = decltype(stage_c)::value;
         char *st = smem + T * STAGE;
 #pragma unroll
@@ -769,8 +779,9 @@ __global__ __launch_bounds__(256) void gemm4_scan_kernel(ScanKArgs a) {
             *(u32x4_t *)(st + A_OFF + st_off + i * 64 * ROWB) = sa[S][i];
             *(u32x4_t *)(st + B_OFF + st_off + i * 64 * ROWB) = sb[S][i];
         }
-        if (L2 && T == 0 && tid < BR / 4) *(f32x4_t *)(st + N_OFF + 16 * tid) = sn[S];
-        (void)g;
+    };
+    auto write_norms = [&]() __attribute__((always_inline)) {
+        if constexpr (L2) *(float *)(smem + N_OFF + 4 * tid) = sn;
     };
 
     // ---- fragments: lane (l32, h) reads row wr*128 + 32 rb + l32 and query
@@ -825,42 +836,90 @@ __global__ __launch_bounds__(256) void gemm4_scan_kernel(ScanKArgs a) {
         }
     };
 
-    // One chunk g (stage T = g % 4, staging set S = g % 2 for chunk g + 2).
-    auto chunk = [&](auto stage_c, auto first_c, int g) __attribute__((always_inline)) {
+    // Chunks go in groups of four, g0 .. g0 + 3 (a group never spans two
+    // tiles); kc_c is the current group's first K-chunk and xrs_c its tile's
+    // row resource, kc_n / xrs_n / nrs_n the next group's.  Chunk g0 + T
+    // (stage T, staging set S = T & 1 for chunk g0 + T + 2) issues the loads
+    // of chunk g0 + T + 3, and at T = 1 the norms of the next group's tile
+    // (written with that group's first chunk at T = 2: unchanged unless it
+    // starts a tile, and the current tile's were used by its first chunk).
+    // The next group's positions and resources are computed at the end of
+    // the group's last chunk, before its barrier, where the wave waits
+    // anyway (not between a barrier and the MFMAs after it).
+    int64_t trow_n = r0;
+    int kc_c = 0, kc_n = 0;
+    __amdgpu_buffer_rsrc_t xrs_c = rows_rs(r0), xrs_n, nrs_n;
+    auto advance = [&]() __attribute__((always_inline)) {
+        trow_n = kc_n + 4 == nkc ? trow_n + BR : trow_n;
+        kc_n = kc_n + 4 == nkc ? 0 : kc_n + 4;
+        xrs_n = rows_rs(trow_n);
+        nrs_n = norms_rs(trow_n);
+    };
+    advance();  // the second group's
+    auto chunk = [&](auto stage_c, auto first_c) __attribute__((always_inline)) {
         constexpr int T = decltype(stage_c)::value;
         constexpr int S = T & 1;
-        constexpr bool FIRST = decltype(first_c)::value;
-        if (g + 3 < total) issue(std::integral_constant<int, S ^ 1>{}, g + 3);
-        // K-step 0 from fa/fb[0] while K-step 1's fragments are read
+        if constexpr (T == 0)
+            issue(std::integral_constant<int, S ^ 1>{}, xrs_c, kc_c + 3);
+        else
+            issue(std::integral_constant<int, S ^ 1>{}, xrs_n, kc_n + T - 1);
+        if constexpr (T == 1) issue_norms(nrs_n);
+        // K-step 0 from fa/fb[0] while K-step 1's fragments are read; one
+        // global load and one fragment read after every second MFMA
         read_frags(std::integral_constant<int, 1>{}, stage_c, std::integral_constant<int, 1>{});
         mfmas(std::integral_constant<int, 0>{}, first_c);
-        __builtin_amdgcn_sched_group_barrier(0x020, 2 * LOADS, 0);  // global loads
-        __builtin_amdgcn_sched_group_barrier(0x100, RB + QB, 0);    // fragment reads
-        __builtin_amdgcn_sched_group_barrier(0x008, RB * QB, 0);    // MFMAs
+#pragma unroll
+        for (int i = 0; i < 2 * LOADS; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global load
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // fragment read
+        }
+        if (T == 1 && L2) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
         __builtin_amdgcn_sched_barrier(0);
-        // chunk g + 2 into its stage, then K-step 1 while the next chunk's
-        // K-step 0 fragments are read
-        if (g + 2 < total)
-            write(std::integral_constant<int, S>{}, std::integral_constant<int, (T + 2) & 3>{}, g + 2);
-        if (g + 1 < total)
-            read_frags(std::integral_constant<int, 0>{}, std::integral_constant<int, (T + 1) & 3>{},
-                       std::integral_constant<int, 0>{});
+        // chunk g0 + T + 2 into its stage and the next chunk's K-step 0
+        // fragments read: one LDS write and one read after each of the
+        // first eight MFMAs of K-step 1, so the last eight leave them time
+        // to complete before the barrier waits for them
+        write(std::integral_constant<int, S>{}, std::integral_constant<int, (T + 2) & 3>{});
+        if constexpr (T == 2) write_norms();
+        read_frags(std::integral_constant<int, 0>{}, std::integral_constant<int, (T + 1) & 3>{},
+                   std::integral_constant<int, 0>{});
         mfmas(std::integral_constant<int, 1>{}, std::false_type{});
-        __builtin_amdgcn_sched_group_barrier(0x200, 2 * LOADS, 0);  // LDS writes
-        __builtin_amdgcn_sched_group_barrier(0x100, RB + QB, 0);    // fragment reads
-        __builtin_amdgcn_sched_group_barrier(0x008, RB * QB, 0);    // MFMAs
+        if (T == 2 && L2) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+#pragma unroll
+        for (int i = 0; i < 2 * LOADS; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS write
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // fragment read
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, RB * QB - 2 * LOADS, 0);
         __builtin_amdgcn_sched_barrier(0);
-        (void)FIRST;
+        if constexpr (T == 3) {
+            xrs_c = xrs_n;
+            kc_c = kc_n;
+            advance();
+        }
         __syncthreads();
     };
+    // one group of four chunks; FIRST: the tile's first group
+    auto group = [&](auto first_c) __attribute__((always_inline)) {
+        chunk(std::integral_constant<int, 0>{}, first_c);
+        chunk(std::integral_constant<int, 1>{}, std::false_type{});
+        chunk(std::integral_constant<int, 2>{}, std::false_type{});
+        chunk(std::integral_constant<int, 3>{}, std::false_type{});
+    };
 
-    // prologue: chunks 0 and 1 into stages 0 and 1 (set 0 and 1), chunk 2's
-    // loads issued into set 0, the first fragments read
-    issue(std::integral_constant<int, 0>{}, 0);
-    if (1 < total) issue(std::integral_constant<int, 1>{}, 1);
-    write(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, 0);
-    if (1 < total) write(std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{}, 1);
-    if (2 < total) issue(std::integral_constant<int, 0>{}, 2);
+    // prologue: chunks 0 and 1 (and the first tile's norms) into stages 0
+    // and 1 from sets 0 and 1, chunk 2's loads issued into set 0, the first
+    // fragments read
+    issue(std::integral_constant<int, 0>{}, xrs_c, 0);
+    issue(std::integral_constant<int, 1>{}, xrs_c, 1);
+    issue_norms(norms_rs(r0));
+    write(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+    write(std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
+    write_norms();
+    issue(std::integral_constant<int, 0>{}, xrs_c, 2);
     __syncthreads();
     read_frags(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{},
                std::integral_constant<int, 0>{});
@@ -868,7 +927,6 @@ __global__ __launch_bounds__(256) void gemm4_scan_kernel(ScanKArgs a) {
     // the first tile seeds the lists' thresholds when two lanes can hold kk
     // values (ceil(kk / 2) <= 16 * RB)
     bool seeded = (a.kk + 1) / 2 > 16 * RB;
-    int g = 0;
     for (int64_t t0 = r0; t0 < r1; t0 += BR) {
         if constexpr (MODE == 0) {
 #pragma unroll
@@ -876,18 +934,8 @@ __global__ __launch_bounds__(256) void gemm4_scan_kernel(ScanKArgs a) {
                 gt[qb] = __hip_atomic_load(&a.gthr[q0 + qw0 + qb * 32 + l32], __ATOMIC_RELAXED,
                                            __HIP_MEMORY_SCOPE_AGENT);
         }
-        chunk(std::integral_constant<int, 0>{}, std::true_type{}, g);
-        chunk(std::integral_constant<int, 1>{}, std::false_type{}, g + 1);
-        chunk(std::integral_constant<int, 2>{}, std::false_type{}, g + 2);
-        chunk(std::integral_constant<int, 3>{}, std::false_type{}, g + 3);
-        g += 4;
-        for (int kc = 4; kc < nkc; kc += 4) {
-            chunk(std::integral_constant<int, 0>{}, std::false_type{}, g);
-            chunk(std::integral_constant<int, 1>{}, std::false_type{}, g + 1);
-            chunk(std::integral_constant<int, 2>{}, std::false_type{}, g + 2);
-            chunk(std::integral_constant<int, 3>{}, std::false_type{}, g + 3);
-            g += 4;
-        }
+        group(std::true_type{});
+        for (int kc = 4; kc < nkc; kc += 4) group(std::false_type{});
         gemm_epilogue<WR, BQ, RB, QB, MODE>(acc, a, ectx, t0 + wr * 128, thr_r, gt, seeded);
         __syncthreads();
     }
@@ -908,6 +956,20 @@ hipError_t launch_gemm_scan(int storage, int planes, const ScanPlan &plan, const
     // for the price of one sort of ~2 kk entries
     ga.flush_at = std::max(2 * plan.kk, 16);
     void (*fn)(ScanKArgs) = nullptr;
+    if (plan.g_pipe) {
+        // the four-wave pipelined kernel: bf16 rows, one query plane, rows
+        // of whole four-chunk groups
+        if (storage != 1 || planes != 1 || args.ld % (4 * g4::KC) != 0 || plan.lw != g4::WR ||
+            plan.bn != g4::BQ || plan.tile_rb != g4::RB || plan.g_qb != g4::QB)
+            return hipErrorInvalidValue;
+        fn = args.metric == 0 ? gemm4_scan_kernel<MODE, true> : gemm4_scan_kernel<MODE, false>;
+        const size_t lds = plan.lds_bytes;
+        hipError_t e = hipFuncSetAttribute((const void *)fn,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(g4::NT), lds, st, ga);
+        return hipGetLastError();
+    }
 #define VS_GPICK(ST_, PB_, WR_, WQ_, RB_, QB_, KC_)                                            \
     if (storage == ST_ && planes == PB_ && plan.lw == WR_ && plan.g_wq == WQ_ &&                 \
         plan.tile_rb == RB_ && plan.g_qb == QB_ && plan.tile_kc == KC_)                          \

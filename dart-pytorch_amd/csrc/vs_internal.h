@@ -93,6 +93,8 @@ struct ScanPlan {
     int g_wq = 2, g_qb = 4;  // GEMM-tiled scan: query waves, 32-query blocks per wave
                              // (row waves = lw, 32-row blocks per wave = tile_rb,
                              // K-chunk = tile_kc)
+    int g_pipe = 0;       // GEMM-tiled scan: 1 = the four-wave pipelined kernel (bf16 rows, one
+                          // query plane; shape 2 x 2 waves, 4 x 4 blocks, K-chunk 32)
     int tile_rb = 2;      // GEMM-tiled scan: 32-row blocks per wave
     int tile_kc = 32;     // GEMM-tiled scan: K-chunk per pipeline step (elements)
     int tile_st = 1, tile_pb = 1;  // GEMM-tiled and row-shared scans: storage and query planes
@@ -323,6 +325,9 @@ constexpr int kSelectCoarse = 2;
 
 // LDS of the GEMM-tiled scans (stages plus list bookkeeping).
 size_t gemm_lds_bytes(int st, int pb, int wr, int wq, int rb, int qb, int kc, int cap);
+// LDS of the four-wave pipelined GEMM-tiled scan (four stages plus list
+// bookkeeping).
+size_t gemm4_lds_bytes(int cap);
 
 // LDS of the row-shared scan (two row stages plus list bookkeeping).
 size_t share_lds_bytes(int nks, int nqb, int rt, int cap);

@@ -265,6 +265,8 @@ VS_API int vs_index_sync(vs_index *idx);
  *   "gemm"        -1 planner rule (rows >= 256 elements, batch >= 512), 0 off, 1 any d
  *   "gemm_min_nq" smallest batch on the GEMM-tiled scan (0: the rule's)
  *   "gemm_wq", "gemm_qb", "gemm_kc"  force that GEMM shape field (0: any)
+ *   "gemm4"       1: the four-wave pipelined GEMM-tiled kernel where it applies (bf16
+ *                 rows, one query plane; shape 2,2,4,4,32); 0 (default): the eight-wave one
  *   "share"       -1 rule (bf16 rows of 128 elements, batch >= 256), 0 off, 1 also 256
  *   "coarse"      1: one-pass bf16 selection of fp32 rows (range, self-join, k-means)
  *   "copy16"      1: that selection reads a bf16 copy of the rows

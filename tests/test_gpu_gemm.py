@@ -22,8 +22,10 @@ NT = oracle.default_threads()
 
 # The built shapes (storage, query planes, row waves, query waves, 32-row
 # blocks per wave, 32-query blocks per wave, K-chunk), as listed by
-# VS_GEMM_SHAPES in dart-pytorch_amd/csrc/vs_internal.h.
+# VS_GEMM_SHAPES in dart-pytorch_amd/csrc/vs_internal.h, and first the
+# four-wave pipelined kernel (bf16 rows, one query plane; option gemm4).
 SHAPES = [
+    (1, 1, 2, 2, 4, 4, 32),  # the four-wave pipelined kernel
     (1, 1, 2, 4, 4, 2, 64),
     (1, 1, 2, 2, 4, 2, 64),
     (1, 1, 2, 4, 4, 2, 32),
@@ -49,9 +51,10 @@ def _gemm(opts):
 
 
 def _force(opts, shape):
-    """Force one GEMM shape."""
+    """Force one GEMM shape (32-query blocks per wave = 4: the four-wave
+    kernel, option gemm4)."""
     _, _, _, wq, _, qb, kc = shape
-    opts(gemm_wq=wq, gemm_qb=qb, gemm_kc=kc)
+    opts(gemm_wq=wq, gemm_qb=qb, gemm_kc=kc, gemm4=int(qb == 4))
 
 
 def _search(vs, xb, xq, k, metric, storage, shape=None, key=None):
@@ -122,6 +125,23 @@ def test_gemm_matches_streaming(vs, opts):
     assert np.array_equal(D0, D1)
     Dr, Ir = oracle.flat_search(xb, xq, 16, 0, NT)
     assert_knn_parity(D1, I1, Dr, Ir, 0, rtol=0.0, atol=0.0, xb=xb, xq=xq)
+
+
+@pytest.mark.parametrize("metric", [0, 1])
+def test_four_wave_matches_eight_wave(vs, opts, metric):
+    """The four-wave pipelined kernel (option gemm4) and the eight-wave one
+    give the same answers on bf16 rows of integers (exact distances), k =
+    100, 50,001 rows (ending inside a 256-row tile) and 777 queries (inside
+    a 256-query block), both equal to the oracle's."""
+    xb = syn.int_grid(50_001, 128, 5, 0)
+    xq = syn.int_grid(777, 128, 5, 1)
+    opts(gemm_min_nq=256)
+    D8, I8, g8 = _search(vs, xb, xq, 100, metric, "auto", key="gemm:1,1,2,4,4,2,64")
+    opts(gemm4=1)
+    D4, I4, g4 = _search(vs, xb, xq, 100, metric, "auto", key="gemm:1,1,2,2,4,4,32")
+    assert np.array_equal(D8, D4) and np.array_equal(I8, I4)
+    Dr, Ir = oracle.flat_search(xb, xq, 100, metric, NT)
+    assert_knn_parity(D4, I4, Dr, Ir, metric, rtol=0.0, atol=0.0, xb=xb, xq=xq)
 
 
 @pytest.mark.parametrize("k,metric", [(10, 0), (100, 1)])
@@ -257,7 +277,8 @@ def test_gemm_large_k_unseeded(vs):
 
 # one-pass selection shapes: fp32 rows rounded in the kernel (storage code 2)
 # or their bf16 copy (storage code 1, range search and self-join)
-COARSE_KEYS = ("gemm:2,1,2,4,4,2,32", "gemm:1,1,2,4,4,2,32")
+COARSE_KEYS = ("gemm:2,1,2,4,4,2,32", "gemm:1,1,2,4,4,2,64", "gemm:1,1,2,4,4,2,32",
+               "gemm:1,1,2,2,4,4,32")
 
 
 def _one_pass_runs(g):

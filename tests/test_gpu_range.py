@@ -70,13 +70,14 @@ def test_range_empty_and_bf16(vs):
     assert rr.total_matches == 0 and rr.nq == 30
 
 
-@pytest.mark.parametrize("copy16", [1, 0])
-def test_self_join_dedup(vs, opts, copy16):
+@pytest.mark.parametrize("copy16,gemm4", [(1, 0), (0, 0), (1, 1)])
+def test_self_join_dedup(vs, opts, copy16, gemm4):
     """configs[4] arithmetic on 30k x 512: 5 % planted near-duplicates,
     pairs i<j with cos >= 0.95, sorted by (i, j).  The one-pass selection
     reads a bf16 copy of the fp32 rows (copy16 1, the default) or rounds
-    the fp32 rows in the kernel (0)."""
-    opts(copy16=copy16)
+    the fp32 rows in the kernel (0); on the copy, the eight-wave or the
+    four-wave GEMM-tiled kernel (gemm4)."""
+    opts(copy16=copy16, gemm4=gemm4)
     x = syn.dedup_set(30_000, 512, 0.05, 0.01, 1234)
     g = vs.GpuIndexFlat.ip(512, storage="f32")
     g.add(x)
@@ -101,7 +102,10 @@ def test_range_l2_one_pass_rows(vs, opts, copy16):
     g.add(xb)
     rr = g.range_search(xq, radius)
     # the GEMM-tiled scan ran on the copy (storage 1) or the fp32 rows (2)
-    n, _ = g.prof_get("gemm:%s,1,2,4,4,2,32" % ("1" if copy16 == 1 else "2"))
+    # (on the copy: the four-wave kernel, or the eight-wave one with it off)
+    keys = (["gemm:1,1,2,4,4,2,64", "gemm:1,1,2,2,4,4,32"] if copy16 == 1
+            else ["gemm:2,1,2,4,4,2,32"])
+    n = sum(g.prof_get(key)[0] for key in keys)
     assert n >= 1
     lims, D, I = oracle.flat_range_search(xb, xq, radius, 0, NT)
     assert rr.total_matches > 0
