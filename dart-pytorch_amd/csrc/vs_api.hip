@@ -1860,6 +1860,70 @@ int vs_index_score_all(vs_index *x, const float *q, float *out) {
     return VS_OK;
 }
 
+}  // extern "C"
+
+// Subset search beyond the list path's keep (k > 409): per query, the fp64
+// score of every row its segments name, as (fp32 key code, id) keys sorted
+// on the device (exact_sort_topk_ids); the k first are the answer, sentinel
+// padded past the subset's size.  The ids are checked on the host (the
+// list path checks them in its kernels).
+static int search_subsets_sorted(vs_index *x, Arena &A, const vs::PreparedQueries &pq, int64_t k,
+                                 const int32_t *ids, const int64_t *seg_off,
+                                 const int64_t *seg_len, int64_t nseg, float *D, int32_t *I) {
+    const int64_t nq = pq.nq;
+    int64_t mmax = 0;
+    for (int64_t qi = 0; qi < nq; ++qi) {
+        int64_t m = 0;
+        for (int64_t s = 0; s < nseg; ++s) {
+            const int64_t o = seg_off[qi * nseg + s], l = seg_len[qi * nseg + s];
+            for (int64_t j = o; j < o + l; ++j)
+                if (ids[j] < 0 || ids[j] >= x->ntotal)
+                    return set_err(VS_ERR_INVALID, "id %lld of query %lld outside [0, %lld)",
+                                   (long long)ids[j], (long long)qi, (long long)x->ntotal);
+            m += l;
+        }
+        mmax = std::max(mmax, m);
+    }
+    if (mmax > (int64_t)UINT32_MAX)
+        return set_err(VS_ERR_UNSUPPORTED, "a query's subsets hold %lld rows", (long long)mmax);
+    size_t tmp_bytes = 0;
+    VS_HIP(vs::exact_sort_topk_ids(x->xb, x->storage, x->ld, x->d, x->metric, pq.qf, nullptr, mmax,
+                                   k, nullptr, nullptr, nullptr, nullptr, tmp_bytes, x->st),
+           "sort size");
+    void *pids, *keys, *tmp, *pD, *pI;
+    VS_TAKE(A.tmp((size_t)std::max<int64_t>(mmax, 1) * 4, &pids, "subset ids"));
+    VS_TAKE(A.tmp((size_t)std::max<int64_t>(mmax, 1) * 16, &keys, "sort keys"));
+    VS_TAKE(A.tmp(tmp_bytes + 256, &tmp, "sort scratch"));
+    VS_TAKE(A.tmp((size_t)k * 4, &pD, "results"));
+    VS_TAKE(A.tmp((size_t)k * 4, &pI, "results"));
+    std::vector<int32_t> flat((size_t)std::max<int64_t>(mmax, 1));
+    for (int64_t qi = 0; qi < nq; ++qi) {
+        int64_t m = 0;
+        for (int64_t s = 0; s < nseg; ++s) {
+            const int64_t o = seg_off[qi * nseg + s], l = seg_len[qi * nseg + s];
+            std::copy(ids + o, ids + o + l, flat.begin() + m);
+            m += l;
+        }
+        // (flat is refilled only after the stream has finished with it)
+        if (m > 0)
+            VS_HIP(hipMemcpyAsync(pids, flat.data(), (size_t)m * 4, hipMemcpyHostToDevice, x->st),
+                   "ids");
+        VS_HIP(vs::exact_sort_topk_ids(x->xb, x->storage, x->ld, x->d, x->metric, pq.qf + qi * x->d,
+                                       (const int32_t *)pids, m, k, (float *)pD, (int32_t *)pI,
+                                       (uint64_t *)keys, tmp, tmp_bytes, x->st),
+               "subset sort");
+        VS_HIP(hipMemcpyAsync(D + qi * k, pD, (size_t)k * 4, hipMemcpyDeviceToHost, x->st),
+               "results");
+        VS_HIP(hipMemcpyAsync(I + qi * k, pI, (size_t)k * 4, hipMemcpyDeviceToHost, x->st),
+               "results");
+        VS_HIP(hipStreamSynchronize(x->st), "subset search");
+    }
+    if (!x->prof_fixed) x->prof["exact_sort_queries"].launches += nq;
+    return VS_OK;
+}
+
+extern "C" {
+
 int vs_index_search_subsets(vs_index *x, const void *q, int q_dtype, int64_t nq, int64_t k,
                             const int32_t *ids, int64_t nids, const int64_t *seg_off,
                             const int64_t *seg_len, int64_t nseg, float *D, int32_t *I) {
@@ -1870,8 +1934,7 @@ int vs_index_search_subsets(vs_index *x, const void *q, int q_dtype, int64_t nq,
     if (nq == 0) return VS_OK;
     if (k == 0) return set_err(VS_ERR_INVALID, "k must be >= 1");
     const int64_t kk = std::max<int64_t>(8, next_pow2(k + std::max<int64_t>(4, k / 4)));
-    if (kk > 512)
-        return set_err(VS_ERR_UNSUPPORTED, "subset search: k <= 409 (got %lld)", (long long)k);
+    if (k > INT32_MAX) return set_err(VS_ERR_INVALID, "k = %lld is too large", (long long)k);
     if (!q || !D || !I || (nq * nseg > 0 && (!seg_off || !seg_len)) || (nids > 0 && !ids))
         return set_err(VS_ERR_INVALID, "null buffer");
     for (int64_t t = 0; t < nq * nseg; ++t)
@@ -1886,6 +1949,7 @@ int vs_index_search_subsets(vs_index *x, const void *q, int q_dtype, int64_t nq,
     VS_HIP(hipMemcpyAsync(x->stage.p, q, qbytes, hipMemcpyHostToDevice, x->st), "uploading queries");
     vs::PreparedQueries pq;
     if (int rc = prepare_queries(x, A, x->stage.p, q_dtype, x->d, nq, &pq, nullptr)) return rc;
+    if (kk > 512) return search_subsets_sorted(x, A, pq, k, ids, seg_off, seg_len, nseg, D, I);
     const int64_t ns = std::max<int64_t>(1, nseg);
     void *pids, *poff, *plen, *pv, *pi, *pf, *pD, *pI;
     VS_TAKE(A.tmp((size_t)std::max<int64_t>(nids, 1) * 4, &pids, "ids"));

@@ -198,6 +198,13 @@ hipError_t exact_sort_topk(const void *xb, int storage, int64_t ld, int64_t d, i
                            const float *qf, int64_t nq, int64_t n, int64_t k, float *D, int32_t *I,
                            uint64_t *keys, int64_t qchunk, void *tmp, size_t &tmp_bytes,
                            hipStream_t st);
+// The same for one query (fp32 row qf [d]) over the rows ids[0 .. m) (ids in
+// [0, ntotal), checked by the caller): keys holds 2 m words of 64 bits, tmp
+// tmp_bytes (query with tmp == nullptr); D / I [k], sentinel-filled past m.
+hipError_t exact_sort_topk_ids(const void *xb, int storage, int64_t ld, int64_t d, int metric,
+                               const float *qf, const int32_t *ids, int64_t m, int64_t k, float *D,
+                               int32_t *I, uint64_t *keys, void *tmp, size_t &tmp_bytes,
+                               hipStream_t st);
 
 // Threshold seeding from a pre-pass scan: every query's shared threshold
 // (gthr) is tightened to one code above the seed_rank-th (0: kk_final-th)

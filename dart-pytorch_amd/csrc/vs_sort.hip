@@ -101,4 +101,56 @@ hipError_t exact_sort_topk(const void *xb, int storage, int64_t ld, int64_t d, i
     return hipSuccess;
 }
 
+// keys[p] = enc_order(key) << 32 | ids[p] for one query (fp32 row qf [d])
+// against the rows ids[0 .. m): the exact_keys_kernel arithmetic over a
+// given row subset.  One thread per candidate; the query staged in LDS,
+// zero past d.
+__global__ __launch_bounds__(256) void exact_keys_ids_kernel(const void *xb, int storage,
+                                                             int64_t ld, int64_t d, int metric,
+                                                             const float *qf, const int32_t *ids,
+                                                             int64_t m, uint64_t *keys) {
+    extern __shared__ __align__(16) char smem[];
+    float *qs = (float *)smem;  // [ld]
+    for (int64_t j = threadIdx.x; j < ld; j += 256) qs[j] = j < d ? qf[j] : 0.0f;
+    __syncthreads();
+    const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (p >= m) return;
+    const int64_t id = ids[p];
+    const double ex = storage == 1 ? exact_score<1>(qs, xb, ld, id, d, metric)
+                                   : exact_score<0>(qs, xb, ld, id, d, metric);
+    const float key = metric == 0 ? (float)ex : -(float)ex;
+    keys[p] = ((uint64_t)enc_order(key) << 32) | (uint32_t)id;
+}
+
+hipError_t exact_sort_topk_ids(const void *xb, int storage, int64_t ld, int64_t d, int metric,
+                               const float *qf, const int32_t *ids, int64_t m, int64_t k, float *D,
+                               int32_t *I, uint64_t *keys, void *tmp, size_t &tmp_bytes,
+                               hipStream_t st) {
+    if (m < 0 || m > (int64_t)UINT32_MAX) return hipErrorInvalidValue;
+    if (!tmp) {
+        return rocprim::radix_sort_keys(nullptr, tmp_bytes, (const uint64_t *)nullptr,
+                                        (uint64_t *)nullptr, (size_t)std::max<int64_t>(m, 1), 0,
+                                        64, st);
+    }
+    uint64_t *out = keys + m;
+    if (m > 0) {
+        const size_t lds = (size_t)ld * 4;
+        if (lds > 64 * 1024) {
+            hipError_t e = hipFuncSetAttribute((const void *)exact_keys_ids_kernel,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return e;
+        }
+        exact_keys_ids_kernel<<<dim3((unsigned)((m + 255) / 256)), dim3(256), lds, st>>>(
+            xb, storage, ld, d, metric, qf, ids, m, keys);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        size_t tb = tmp_bytes;
+        e = rocprim::radix_sort_keys(tmp, tb, keys, out, (size_t)m, 0, 64, st);
+        if (e != hipSuccess) return e;
+    }
+    extract_topk_kernel<<<dim3((unsigned)((k + 255) / 256)), dim3(256), 0, st>>>(out, m, k, metric,
+                                                                              D, I);
+    return hipGetLastError();
+}
+
 }  // namespace vs

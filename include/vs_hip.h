@@ -163,7 +163,8 @@ VS_API int vs_index_search_device_noalloc(vs_index *idx, const void *q_dev, int 
  * the fine scan of IndexIVFFlat.search over its probed inverted lists
  * (index_ivf_flat.dart:131-170): fp64 scores in dimension order, the k best
  * by (fp32 score, id), sentinels when fewer rows were scanned.  Host
- * buffers; k <= 409.  An id outside [0, ntotal) gives VS_ERR_INVALID. */
+ * buffers; any k (beyond 409 each query's subset rows are sorted on the
+ * device).  An id outside [0, ntotal) gives VS_ERR_INVALID. */
 VS_API int vs_index_search_subsets(vs_index *idx, const void *q, int q_dtype, int64_t nq,
                                    int64_t k, const int32_t *ids, int64_t nids,
                                    const int64_t *seg_off, const int64_t *seg_len, int64_t nseg,

@@ -138,3 +138,33 @@ def test_subset_search_edges(vs):
         g.search_subsets(q, 6, np.array([0, 9999], np.int32), off[:, :1] * 0,
                          np.array([[2], [0], [0]], np.int64))
     g.close()
+
+
+@pytest.mark.parametrize("metric", [0, 1])
+def test_subset_search_large_k(vs, metric):
+    """k beyond the list path (600 > 409): each query's subset rows scored
+    in fp64 and sorted by (fp32 score, id) -- the oracle's top-k over those
+    rows, sentinels past the subset's size (query 1 names 250 rows, query 2
+    none) -- and the list path's k = 400 answers are its first 400."""
+    x = blobs(5000, 24, seed=4)
+    g = vs.GpuIndexFlat(24, vs.Metric(metric), storage="f32")
+    g.add(x)
+    ids = syn.rng(5, 0).permutation(5000)[:3000].astype(np.int32)
+    q = (x[[7, 11, 13]] + 0.01).astype(np.float32)
+    off = np.array([[0, 2000], [100, 0], [0, 0]], np.int64)
+    ln = np.array([[1500, 800], [250, 0], [0, 0]], np.int64)
+    k = 600
+    r = g.search_subsets(q, k, ids, off, ln)
+    r4 = g.search_subsets(q, 400, ids, off, ln)
+    g.close()
+    for i in range(3):
+        rows = np.concatenate([ids[o:o + n] for o, n in zip(off[i], ln[i])]).astype(np.int64)
+        if len(rows) == 0:
+            assert np.all(r.ids[i] == -1)
+            assert np.all(np.isinf(r.distances[i]))
+            continue
+        Dr, Ir = oracle.flat_search(x[rows], q[i:i + 1], k, metric)
+        Ir = np.where(Ir >= 0, rows[np.maximum(Ir, 0)], -1).astype(np.int32)
+        assert_knn_parity(r.distances[i:i + 1], r.ids[i:i + 1], Dr, Ir, metric)
+        assert (r.ids[i] >= 0).sum() == min(k, len(rows))
+    assert np.array_equal(r.ids[:, :400], r4.ids) and np.array_equal(r.distances[:, :400], r4.distances)

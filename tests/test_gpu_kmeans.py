@@ -68,6 +68,52 @@ def test_kmeans_empty_cluster_before_largest(vs):
     assert np.abs(newc[0] - cen[2]).max() < 1e-3 and np.abs(newc[3] - cr[2]).max() < 1e-3
 
 
+def _rejitter(cen_old, newc, counts, min_points, u):
+    """The Dart drop-in's GpuKmeans update of empty clusters: after a step
+    with neutral jitter (u = 0.5, a plain copy), each cluster below
+    min_points, in centroid order, becomes the largest cluster's centroid
+    (its new value when it precedes, its old one otherwise) plus
+    (u - 0.5) * 1e-4 in fp64, rounded to fp32 -- the draws taken in order."""
+    out = newc.copy()
+    big = int(np.argmax(counts))  # the first of the largest count
+    t = 0
+    for c in range(len(counts)):
+        if counts[c] >= min_points:
+            continue
+        src = out[big] if big < c else cen_old[big]
+        for j in range(out.shape[1]):
+            out[c, j] = np.float32(np.float64(src[j]) + (u[t] - 0.5) * 1e-4)
+            t += 1
+    return out
+
+
+@pytest.mark.parametrize("min_points", [1, 600])
+def test_kmeans_neutral_jitter_then_host_jitter(vs, min_points):
+    """The GpuKmeans of the Dart drop-in draws the jitter from dart:math
+    Random itself: it runs each step with neutral jitter and re-jitters the
+    clusters below minPointsPerCentroid on the host.  That equals a step
+    given the same draws directly, bit for bit, with empty clusters before
+    and after the largest one (min_points 600 also replaces a small
+    non-empty cluster)."""
+    g = syn.rng(9, 0)
+    a_pts = (g.standard_normal((500, 16)) * 0.1).astype(np.float32)
+    b_pts = (g.standard_normal((2000, 16)) * 0.1 + 5.0).astype(np.float32)
+    x = np.concatenate([a_pts, b_pts]).astype(np.float32)
+    far = np.full((1, 16), 1e3, np.float32)
+    cen = np.concatenate([far, x[:1] + 0.3, x[600:601] + 0.3, far * 2]).astype(np.float32)
+    u = syn.rng(9, 2).random(4 * 16)
+    pts = vs.GpuIndexFlat.l2(16, storage="f32")
+    pts.add(x)
+    a1, direct, cnt1, obj1 = vs.kmeans_step(pts, cen, min_points, u)
+    a2, neutral, cnt2, obj2 = vs.kmeans_step(pts, cen, min_points, np.full(4 * 16, 0.5))
+    pts.close()
+    assert np.array_equal(a1, a2) and obj1 == obj2 and np.array_equal(cnt1, cnt2)
+    host = _rejitter(cen, neutral, cnt2, min_points, u)
+    assert np.array_equal(host.view(np.uint32), direct.view(np.uint32))
+    _, _, used = oracle.kmeans_update(x, a1, cen, min_points, u)
+    assert used == 16 * int(np.sum(cnt1 < min_points)) and used >= 32
+
+
 def test_kmeans_train_monotone(vs):
     """vector_store_test.dart:91-111: re-assignment objective <= 1.05 x training objective."""
     x, _ = syn.gaussian_mixture(400, 16, 8, 0.05, 1)
