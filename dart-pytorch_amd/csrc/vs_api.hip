@@ -185,6 +185,8 @@ struct VsOptions {
     int scan_nw8 = 0;      // streaming scan: eight waves per workgroup where it fits
     int km16 = 1;          // k-means: the scan reads a bf16 copy of the centroids
     int km16_rt = 4;       // k-means on that copy: 16-row blocks per tile (2 or 4)
+    int km16_nqb = 4;      // k-means on that copy: 16-point blocks per wave (2, or 4 with
+                           // 32-row tiles)
     int pick_order = 1;    // k-means: the pick walks points grouped by the last step's clusters
     int merge_mu = 0;      // merge: 1024-entry chunks per workgroup pass (0: by batch size; 1, 2,
                            // 4 or 8)
@@ -2163,6 +2165,19 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     if (coarse && plan.kind == 3) {
         plan.share_kmin = 1;
         plan.kmin_margin = 2.5f * bound;
+        // option km16_nqb 4: 64 points per wave on the bf16 copy of the
+        // centroids (32-row tiles keep it at two waves per SIMD); decided
+        // here, before the lists are sized
+        if (x->opt.km16_nqb == 4 && x->opt.km16 && plan.tile_st == vs::kSelectCoarse &&
+            plan.nks == 8) {
+            const size_t lds = vs::share_lds_bytes(plan.nks, 4, 2, plan.cap);
+            if (lds <= x->lds_max) {
+                plan.bn = 256;
+                plan.tm = 2;
+                plan.lds_bytes = lds;
+                plan.nqblk = (n + plan.bn - 1) / plan.bn;
+            }
+        }
         // the running minima start at the previous assignment's bound
         if (prev && x->opt.kmin_init) {
             VS_HIP(x->km_init.ensure((size_t)pq.nq_pad * 4), "running minima");
@@ -2200,7 +2215,7 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
         plan.tile_st = 1;
         // bf16 rows stage twice the rows per tile in the same registers
         const int rt = x->opt.km16_rt;
-        if (rt == 4) {
+        if (rt == 4 && plan.bn == 128) {
             const size_t lds = vs::share_lds_bytes(plan.nks, plan.bn / 64, 4, plan.cap);
             if (lds <= x->lds_max) {
                 plan.tm = 4;
@@ -2392,7 +2407,7 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     // update: counts, stable grouping by cluster, ordered fp32 sums
     VS_HIP(x->km_counts.ensure((size_t)K * 4), "counts");
     VS_HIP(hipMemsetAsync(x->km_counts.p, 0, (size_t)K * 4, x->st), "counts");
-    VS_HIP(vs::launch_kmeans_count(x->km_assign.as<int32_t>(), n, x->km_counts.as<int32_t>(),
+    VS_HIP(vs::launch_kmeans_count(x->km_assign.as<int32_t>(), n, K, x->km_counts.as<int32_t>(),
                                    x->st),
            "counts");
     {
@@ -2828,6 +2843,7 @@ int vs_index_set_option(vs_index *x, const char *name, int64_t value) {
         {"scan_nw8", &VsOptions::scan_nw8, 0, 1},
         {"km16", &VsOptions::km16, 0, 1},
         {"km16_rt", &VsOptions::km16_rt, 2, 4},
+        {"km16_nqb", &VsOptions::km16_nqb, 2, 4},
         {"pick_order", &VsOptions::pick_order, 0, 1},
         {"merge_mu", &VsOptions::merge_mu, 0, 8},
         {"merge_g", &VsOptions::merge_g, 0, 64},
@@ -2842,6 +2858,7 @@ int vs_index_set_option(vs_index *x, const char *name, int64_t value) {
     for (const Opt &o : opts) {
         if (strcmp(o.name, name) != 0) continue;
         const bool hole = (o.field == &VsOptions::km16_rt && value == 3) ||
+                          (o.field == &VsOptions::km16_nqb && value == 3) ||
                           (o.field == &VsOptions::merge_mu && value > 2 && value != 4 && value != 8);
         if (value < o.lo || value > o.hi || hole)
             return set_err(VS_ERR_INVALID, "option %s: value %lld outside [%d, %d]", name,

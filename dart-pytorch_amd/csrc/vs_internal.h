@@ -277,7 +277,8 @@ hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, 
 hipError_t launch_chunk_keys(const int32_t *order, int64_t n, int nchunk, int32_t *key,
                              hipStream_t st);
 
-hipError_t launch_kmeans_count(const int32_t *assign, int64_t n, int32_t *counts, hipStream_t st);
+hipError_t launch_kmeans_count(const int32_t *assign, int64_t n, int64_t K, int32_t *counts,
+                               hipStream_t st);
 // |new_c - old_c| per centroid (upper bounds, fp64); old rows ld apart, new dense.
 hipError_t launch_kmeans_shift(const float *old_cen, int64_t ld, const float *new_cen, int64_t d,
                                int64_t K, double *shift, hipStream_t st);

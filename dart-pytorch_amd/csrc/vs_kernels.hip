@@ -1495,10 +1495,16 @@ hipError_t launch_fill32(void *p, int64_t n, uint32_t v, hipStream_t st) {
 
 template <int KK>
 __global__ void kmeans_pick_kernel(MergeKArgs a);
+// The two LDS-staged picks: two workgroups fit a CU's LDS, so two waves per
+// SIMD, and the register budget of that occupancy (the compiler's default,
+// four waves, spilled the candidates' fp64 sums; the attribute takes effect
+// on this first declaration).
 template <int E, int CH>
-__global__ void kmeans_pick_wave_kernel(MergeKArgs a);
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void
+kmeans_pick_wave_kernel(MergeKArgs a);
 template <int E, int CH>
-__global__ void kmeans_pick_set_kernel(MergeKArgs a);
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void
+kmeans_pick_set_kernel(MergeKArgs a);
 constexpr int kPickSetMaxK = 16384;  // the distinct-candidate pick's largest K
 
 // Threshold estimates from a pre-pass (seed_rank <= 64): one wave per query.
@@ -1872,7 +1878,8 @@ __device__ __forceinline__ int pick_candidates(const MergeKArgs &a, int64_t qc, 
 // kernel.
 // ---------------------------------------------------------------------------
 template <int E, int CH>
-__global__ __launch_bounds__(256) void kmeans_pick_wave_kernel(MergeKArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void kmeans_pick_wave_kernel(
+    MergeKArgs a) {
     constexpr int RS = 65;  // LDS words per staged dimension (64 rows + 1: no bank conflicts on reads)
     constexpr int PIECES = CH / 4;            // 16-byte pieces per row chunk
     constexpr int ROWS_PER = 64 / PIECES;     // rows covered by one wave-wide load
@@ -1984,7 +1991,8 @@ __global__ __launch_bounds__(256) void kmeans_pick_wave_kernel(MergeKArgs a) {
 constexpr int kPickSetMaxU = 1024;
 
 template <int E, int CH>
-__global__ __launch_bounds__(256) void kmeans_pick_set_kernel(MergeKArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void kmeans_pick_set_kernel(
+    MergeKArgs a) {
     constexpr int RS = 65;  // LDS words per staged dimension (64 rows + 1: no bank conflicts on reads)
     constexpr int PIECES = CH / 4;            // 16-byte pieces per row chunk
     constexpr int ROWS_PER = 64 / PIECES;     // rows covered by one wave-wide load
@@ -2061,59 +2069,88 @@ __global__ __launch_bounds__(256) void kmeans_pick_set_kernel(MergeKArgs a) {
     double sc[E], xx = 0.0;
 #pragma unroll
     for (int e = 0; e < E; ++e) sc[e] = 0.0;
-    for (int64_t c0 = 0; c0 < a.ld; c0 += CH) {
-        float xr[CH];
-        for (int b0 = 0; b0 == 0 || b0 < nb; b0 += 64) {
-            // the points' chunk (first batch) and the chunks of distinct
-            // centroids b0 .. b0 + 63 (rows past u read centroid 0), all
-            // loads issued before the first LDS write
-            float4 pv[PIECES], cv[PIECES];
+    // the points' chunk c0 (with_points) and the chunks of distinct
+    // centroids b0 .. b0 + 63 (rows past u read centroid 0) into registers
+    auto load = [&](int64_t c0, int b0, bool with_points, float4 (&pv)[PIECES],
+                    float4 (&cv)[PIECES]) __attribute__((always_inline)) {
 #pragma unroll
-            for (int i = 0; i < PIECES; ++i) {
-                const int r = i * ROWS_PER + prow;
-                if (b0 == 0) {
-                    const int64_t pr = point(p0 + r < a.nq ? p0 + r : p0);
-                    pv[i] = *(const float4 *)(a.pts + pr * a.ld + c0 + pcol);
-                }
-                const int id = b0 + r < nb ? uid[b0 + r] : 0;
-                cv[i] = *(const float4 *)((const float *)a.xb + (int64_t)id * a.ld + c0 + pcol);
+        for (int i = 0; i < PIECES; ++i) {
+            const int r = i * ROWS_PER + prow;
+            if (with_points) {
+                const int64_t pr = point(p0 + r < a.nq ? p0 + r : p0);
+                pv[i] = *(const float4 *)(a.pts + pr * a.ld + c0 + pcol);
             }
+            const int id = b0 + r < nb ? uid[b0 + r] : 0;
+            cv[i] = *(const float4 *)((const float *)a.xb + (int64_t)id * a.ld + c0 + pcol);
+        }
+    };
+    // registers -> dimension-major LDS
+    auto stage = [&](bool with_points, const float4 (&pv)[PIECES], const float4 (&cv)[PIECES])
+                     __attribute__((always_inline)) {
 #pragma unroll
-            for (int i = 0; i < PIECES; ++i) {
-                const int r = i * ROWS_PER + prow;
-                if (b0 == 0) {
-                    xs[(pcol + 0) * RS + r] = pv[i].x;
-                    xs[(pcol + 1) * RS + r] = pv[i].y;
-                    xs[(pcol + 2) * RS + r] = pv[i].z;
-                    xs[(pcol + 3) * RS + r] = pv[i].w;
-                }
-                cs[(pcol + 0) * RS + r] = cv[i].x;
-                cs[(pcol + 1) * RS + r] = cv[i].y;
-                cs[(pcol + 2) * RS + r] = cv[i].z;
-                cs[(pcol + 3) * RS + r] = cv[i].w;
+        for (int i = 0; i < PIECES; ++i) {
+            const int r = i * ROWS_PER + prow;
+            if (with_points) {
+                xs[(pcol + 0) * RS + r] = pv[i].x;
+                xs[(pcol + 1) * RS + r] = pv[i].y;
+                xs[(pcol + 2) * RS + r] = pv[i].z;
+                xs[(pcol + 3) * RS + r] = pv[i].w;
             }
-            lds_wave_sync();
-            if (b0 == 0) {
+            cs[(pcol + 0) * RS + r] = cv[i].x;
+            cs[(pcol + 1) * RS + r] = cv[i].y;
+            cs[(pcol + 2) * RS + r] = cv[i].z;
+            cs[(pcol + 3) * RS + r] = cv[i].w;
+        }
+    };
+    // every lane continues its candidates' sums in dimension order over the
+    // staged chunk (centroids b0 .. b0 + 63); the first batch of a chunk
+    // also reads the lane's own point values and their squares
+    float xr[CH];
+    auto compute = [&](int b0) __attribute__((always_inline)) {
+        if (b0 == 0) {
 #pragma unroll
-                for (int j = 0; j < CH; ++j) {
-                    xr[j] = xs[j * RS + lane];
-                    xx = xx + (double)xr[j] * (double)xr[j];
-                }
+            for (int j = 0; j < CH; ++j) {
+                xr[j] = xs[j * RS + lane];
+                xx = xx + (double)xr[j] * (double)xr[j];
             }
+        }
 #pragma unroll
-            for (int e = 0; e < E; ++e) {
-                if (e < emax) {  // uniform: every slot index stays a constant
-                    const int s = e < ne ? (int)sl[e * 64 + lane] - b0 : -1;
-                    if (s >= 0 && s < 64) {
+        for (int e = 0; e < E; ++e) {
+            if (e < emax) {  // uniform: every slot index stays a constant
+                const int s = e < ne ? (int)sl[e * 64 + lane] - b0 : -1;
+                if (s >= 0 && s < 64) {
 #pragma unroll
-                        for (int j = 0; j < CH; ++j) {
-                            const double dd = (double)xr[j] - (double)cs[j * RS + s];
-                            sc[e] = sc[e] + dd * dd;
-                        }
+                    for (int j = 0; j < CH; ++j) {
+                        const double dd = (double)xr[j] - (double)cs[j * RS + s];
+                        sc[e] = sc[e] + dd * dd;
                     }
                 }
             }
-            lds_wave_sync();  // xs and cs are rewritten by the next batch or chunk
+        }
+    };
+    if (nb <= 64) {
+        // one batch per chunk (the usual case): the next chunk's loads are
+        // in flight while this one is summed
+        float4 pv[PIECES], cv[PIECES];
+        load(0, 0, true, pv, cv);
+        for (int64_t c0 = 0; c0 < a.ld; c0 += CH) {
+            stage(true, pv, cv);
+            lds_wave_sync();
+            if (c0 + CH < a.ld) load(c0 + CH, 0, true, pv, cv);
+            compute(0);
+            lds_wave_sync();  // xs and cs are rewritten by the next chunk
+        }
+    } else {
+        for (int64_t c0 = 0; c0 < a.ld; c0 += CH) {
+            for (int b0 = 0; b0 < nb; b0 += 64) {
+                // all loads issued before the first LDS write
+                float4 pv[PIECES], cv[PIECES];
+                load(c0, b0, b0 == 0, pv, cv);
+                stage(b0 == 0, pv, cv);
+                lds_wave_sync();
+                compute(b0);
+                lds_wave_sync();  // xs and cs are rewritten by the next batch or chunk
+            }
         }
     }
     if (!live) return;
@@ -2257,10 +2294,34 @@ __global__ void kmeans_count_kernel(const int32_t *__restrict__ assign, int64_t 
     if (i < n) atomicAdd(&counts[assign[i]], 1);
 }
 
-hipError_t launch_kmeans_count(const int32_t *assign, int64_t n, int32_t *counts, hipStream_t st) {
+// The same with a histogram per workgroup in LDS (K counters): each of the
+// few workgroups counts a contiguous range of the points with LDS atomics
+// and adds its nonzero counters to the global ones, so each global counter
+// takes one atomic per workgroup instead of one per point.
+__global__ __launch_bounds__(256) void kmeans_count_lds_kernel(const int32_t *__restrict__ assign,
+                                                               int64_t n, int K, int32_t *counts) {
+    extern __shared__ int hist[];
+    for (int c = threadIdx.x; c < K; c += 256) hist[c] = 0;
+    __syncthreads();
+    const int64_t per = (n + gridDim.x - 1) / gridDim.x;
+    const int64_t i0 = (int64_t)blockIdx.x * per, i1 = min(n, i0 + per);
+    for (int64_t i = i0 + threadIdx.x; i < i1; i += 256) atomicAdd(&hist[assign[i]], 1);
+    __syncthreads();
+    for (int c = threadIdx.x; c < K; c += 256)
+        if (hist[c]) atomicAdd(&counts[c], hist[c]);
+}
+
+hipError_t launch_kmeans_count(const int32_t *assign, int64_t n, int64_t K, int32_t *counts,
+                               hipStream_t st) {
     if (n <= 0) return hipSuccess;
-    kmeans_count_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(assign, n,
-                                                                                 counts);
+    if (K <= 16384) {
+        const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(256, (n + 8191) / 8192));
+        kmeans_count_lds_kernel<<<dim3((unsigned)blocks), dim3(256), (size_t)K * 4, st>>>(
+            assign, n, (int)K, counts);
+    } else {
+        kmeans_count_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(assign, n,
+                                                                                     counts);
+    }
     return hipGetLastError();
 }
 
@@ -2480,19 +2541,28 @@ hipError_t launch_range_refine(const void *xb, int storage, int64_t ld, int64_t 
     return hipGetLastError();
 }
 
-__global__ void max_reduce_kernel(const float *__restrict__ x, int64_t n, float *out) {
+__global__ __launch_bounds__(256) void max_reduce_kernel(const float *__restrict__ x, int64_t n,
+                                                         float *out) {
+    __shared__ float wm[4];
     float m = 0.0f;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x)
         m = fmaxf(m, x[i]);
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    if ((threadIdx.x & 63) == 0) atomicMax((unsigned int *)out, __float_as_uint(m));
+    if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
+    __syncthreads();
+    // one atomic per workgroup (the values are >= 0: their bits order as
+    // unsigned integers)
+    if (threadIdx.x == 0)
+        atomicMax((unsigned int *)out,
+                  __float_as_uint(fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]))));
 }
 
 hipError_t launch_max_reduce(const float *x, int64_t n, float *out, hipStream_t st) {
     hipError_t e = launch_fill32(out, 1, 0u, st);
     if (e != hipSuccess || n <= 0) return e;
-    max_reduce_kernel<<<dim3(1024), dim3(256), 0, st>>>(x, n, out);
+    const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(1024, (n + 4095) / 4096));
+    max_reduce_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(x, n, out);
     return hipGetLastError();
 }
 

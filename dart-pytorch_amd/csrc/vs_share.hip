@@ -440,7 +440,7 @@ static void (*share_kmin_kernel())(ScanKArgs) {
 // The built shapes: X(storage, K-steps, 16-query blocks per wave, 16-row
 // blocks per tile).
 #define VS_SHARE_SHAPES(X) \
-    X(1, 4, 4, 4) X(1, 8, 2, 4) X(2, 4, 4, 2) X(2, 8, 2, 2) X(1, 8, 2, 2) X(1, 4, 4, 8)
+    X(1, 4, 4, 4) X(1, 8, 2, 4) X(2, 4, 4, 2) X(2, 8, 2, 2) X(1, 8, 2, 2) X(1, 4, 4, 8) X(1, 8, 4, 2)
 
 // mode: 0 lists, 2 top-m values, 4 k-means lists
 static void (*share_kernel(int st, int nks, int bn, int rt, int64_t ld, int mode))(ScanKArgs) {

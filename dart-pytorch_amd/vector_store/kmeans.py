@@ -38,14 +38,26 @@ class KmeansResult:
 
 
 def kmeans_step(points: GpuIndexFlat, centroids: np.ndarray, min_points: int = 1,
-                jitter_u: np.ndarray | None = None):
-    """One Lloyd iteration.  Returns (assign, new_centroids, counts, objective)."""
+                jitter_u: np.ndarray | None = None, out=None):
+    """One Lloyd iteration.  Returns (assign, new_centroids, counts, objective).
+
+    out: optional (assign int32 [n], centroids float32 [K, d], counts int32
+    [K]) C-contiguous arrays the results are written to (as the reference's
+    train loop reuses its assignment buffer across iterations)."""
     cen = np.ascontiguousarray(centroids, dtype=np.float32)
     K, d = cen.shape
     n = points.ntotal
-    assign = np.empty(n, np.int32)
-    out = np.empty((K, d), np.float32)
-    counts = np.empty(K, np.int32)
+    if out is None:
+        assign = np.empty(n, np.int32)
+        out_c = np.empty((K, d), np.float32)
+        counts = np.empty(K, np.int32)
+    else:
+        assign, out_c, counts = out
+        for arr, dt, shape in ((assign, np.int32, (n,)), (out_c, np.float32, (K, d)),
+                               (counts, np.int32, (K,))):
+            if arr.dtype != dt or arr.shape != shape or not arr.flags.c_contiguous:
+                raise ValueError(f"out array {arr.dtype} {arr.shape}: need C-contiguous {dt} {shape}")
+    out = out_c
     obj = ctypes.c_double(0.0)
     ju = np.ascontiguousarray(jitter_u if jitter_u is not None else np.zeros(0), dtype=np.float64)
     N.check(points._lib.vs_kmeans_step(points.handle, cen.ctypes.data_as(ctypes.c_void_p), K,

@@ -278,6 +278,7 @@ VS_API int vs_index_sync(vs_index *idx);
  *   "scan_nw8"    1: eight-wave streaming scan where it fits
  *   "km16"        1: the k-means assign reads a bf16 copy of the centroids
  *   "km16_rt"     2 or 4: 16-row blocks per tile of that scan
+ *   "km16_nqb"    2 or 4 (default): 16-point blocks per wave of that scan (4: 32-row tiles)
  *   "pick_order"  1: the k-means pick walks the points grouped by the last step's clusters
  *   "merge_mu"    1, 2, 4 or 8: 1,024-entry list chunks the merge reads per pass (0: by
  *                 batch size)

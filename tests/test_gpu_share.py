@@ -187,12 +187,14 @@ def test_kmeans_lists_full(vs):
     assert not np.any((a >= 200) & (a < 500))
 
 
-@pytest.mark.parametrize("km16,rt", [(0, 4), (1, 2)])
-def test_kmeans_lists_fp32_rows(vs, opts, km16, rt):
+@pytest.mark.parametrize("km16,rt,nqb", [(0, 4, 2), (1, 2, 2), (1, 4, 4)])
+def test_kmeans_lists_fp32_rows(vs, opts, km16, rt, nqb):
     """The k-means lists over the fp32 centroid rows rounded in the scan
     (option km16 = 0), or over their bf16 copy in 32-row tiles (km16_rt = 2)
-    instead of 64-row ones: the oracle's assignments."""
-    opts(km16=km16, km16_rt=rt)
+    instead of 64-row ones, or with 64 points per wave (km16_nqb = 4, 32-row
+    tiles; 30,000 points end inside a 256-point block): the oracle's
+    assignments."""
+    opts(km16=km16, km16_rt=rt, km16_nqb=nqb)
     x, _ = syn.gaussian_mixture(30_000, 256, 1024, 0.1, 44)
     cen = x[syn.seeded_subset(30_000, 4096, 44)].copy()
     _kmeans_check(vs, x, cen)
@@ -204,7 +206,8 @@ def _kmeans_oracle_step(x, cen, u):
     return ar, cr, cntr, objr
 
 
-def test_kmeans_running_minima_from_last_step(vs):
+@pytest.mark.parametrize("nqb", [2, 4])
+def test_kmeans_running_minima_from_last_step(vs, nqb):
     """Lloyd steps on one index: from the second step on, each point's
     running minimum in the assign scan starts at a bound from its previous
     centroid (previous squared distance, the centroid's shift, the
@@ -219,6 +222,8 @@ def test_kmeans_running_minima_from_last_step(vs):
     a.add(x)
     b.add(x)
     b.set_option("kmin_init", 0)
+    for g in (a, b):
+        g.set_option("km16_nqb", nqb)
     a.prof_enable(True)
     c = cen
     for step in range(3):
