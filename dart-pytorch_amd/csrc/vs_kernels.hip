@@ -1495,15 +1495,15 @@ hipError_t launch_fill32(void *p, int64_t n, uint32_t v, hipStream_t st) {
 
 template <int KK>
 __global__ void kmeans_pick_kernel(MergeKArgs a);
-// The two LDS-staged picks: two workgroups fit a CU's LDS, so two waves per
-// SIMD, and the register budget of that occupancy (the compiler's default,
-// four waves, spilled the candidates' fp64 sums; the attribute takes effect
-// on this first declaration).
+// The two LDS-staged picks get the register budget of the occupancy their
+// LDS allows (two workgroups per CU with 16-dimension chunks, three with 8);
+// the compiler's default budget, four waves, spilled the candidates' fp64
+// sums.  (The attribute takes effect on this first declaration.)
 template <int E, int CH>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void
 kmeans_pick_wave_kernel(MergeKArgs a);
 template <int E, int CH>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 3))) void
 kmeans_pick_set_kernel(MergeKArgs a);
 constexpr int kPickSetMaxK = 16384;  // the distinct-candidate pick's largest K
 
@@ -1644,9 +1644,10 @@ hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, 
         // each distinct one is staged once per wave; in index order (the
         // first step) they share few, and slot-by-slot staging is faster
         // (measured on C4: 1.99 against 2.70 ms grouped, 5.61 against
-        // 4.19 ms in index order)
+        // 4.19 ms in index order).  8-dimension chunks leave LDS for three
+        // workgroups per CU (C4 pick 1.72 -> 1.56 ms against 16)
         if (K <= kPickSetMaxK && order)
-            kmeans_pick_set_kernel<32, 16>
+            kmeans_pick_set_kernel<32, 8>
                 <<<dim3((unsigned)((nslots + 255) / 256)), dim3(256), 0, st>>>(a);
         else
             kmeans_pick_wave_kernel<32, 16>
@@ -1991,7 +1992,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 constexpr int kPickSetMaxU = 1024;
 
 template <int E, int CH>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void kmeans_pick_set_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 3))) void kmeans_pick_set_kernel(
     MergeKArgs a) {
     constexpr int RS = 65;  // LDS words per staged dimension (64 rows + 1: no bank conflicts on reads)
     constexpr int PIECES = CH / 4;            // 16-byte pieces per row chunk
