@@ -193,6 +193,8 @@ struct VsOptions {
     int merge_g = 0;       // merge: workgroups per query (0: by batch size; 1: one; 2..64: split)
     int guess_div_log2 = 0;  // large batches: the estimate's sample is 1/2^this of the rows (0: 5)
     int kmin_init = 1;       // k-means: start the assign scan's running minima from the last step
+    int assign_order = 1;    // k-means: the assign scan walks the points grouped by the last
+                             // step's clusters
 };
 
 struct vs_index {
@@ -2188,6 +2190,13 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
             plan.kmin_init = x->km_init.as<float>();
             x->prof["kmin_init"].launches++;
         }
+        // the points grouped by the previous step's clusters (the order the
+        // update sorted them into): a wave's points then share their few
+        // candidate centroids, so most row blocks append nothing
+        if (x->opt.assign_order && x->km_order_version == x->version && x->km_order_n == n) {
+            plan.qorder = x->km_order.as<int32_t>();
+            x->prof["assign_order"].launches++;
+        }
     }
     if ((rc = scan_fits(plan, pq))) return rc;
     const size_t nlists = (size_t)plan.nqblk * plan.nsplit * plan.lw * plan.bn;
@@ -2849,6 +2858,7 @@ int vs_index_set_option(vs_index *x, const char *name, int64_t value) {
         {"merge_g", &VsOptions::merge_g, 0, 64},
         {"guess_div_log2", &VsOptions::guess_div_log2, 0, 10},
         {"kmin_init", &VsOptions::kmin_init, 0, 1},
+        {"assign_order", &VsOptions::assign_order, 0, 1},
     };
     if (strcmp(name, "fail_alloc") == 0) {  // not a planner option: this thread's countdown
         if (value < 0) return set_err(VS_ERR_INVALID, "option fail_alloc: value %lld < 0", (long long)value);

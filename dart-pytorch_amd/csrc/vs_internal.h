@@ -107,6 +107,8 @@ struct ScanPlan {
                           // running minimum + kmin_margin; a list that would fill is marked
                           // full, count cap + 1, and takes no more)
     float kmin_margin = 0.f;
+    const int32_t *qorder = nullptr;   // k-means lists: the points in the order the scan walks
+                                       // them (slot s: point qorder[s]), or null (index order)
     const float *kmin_init = nullptr;  // k-means lists: per query (nq_pad entries), a value at or
                                        // above the accumulator of some scanned row, or null
     int uncut = 0;        // streaming scan: lists are left uncut at the end and their entry

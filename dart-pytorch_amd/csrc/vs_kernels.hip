@@ -668,6 +668,7 @@ hipError_t launch_scan_topk(const void *xb, int storage, int64_t ld, const float
     a.lbound = plan.kk < plan.kk_final ? lbound : nullptr;
     a.kmin_margin = plan.kmin_margin;
     a.kmin_init = plan.kmin_init;
+    a.qorder = plan.qorder;
     return launch_scan_mode<0>(storage, pq, plan, a, st);
 }
 

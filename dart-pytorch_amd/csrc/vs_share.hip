@@ -107,14 +107,33 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
     int32_t *ci = a.cand_i + list_base;
     const bool l2 = a.metric == 0;
 
+    // MODE 4 with qorder: slot s of the block stands for point qorder[s]
+    // (slots past nq for themselves), whose planes, starting minimum, list
+    // and count it uses; list of point p: block p / BN, position p % BN.
+    // The block's points are kept in LDS for the appends, in the per-wave
+    // sort buffers, which k-means lists never use.
+    constexpr bool KMIN = MODE == 4;
+    int32_t *pidx = (int32_t *)sv;  // [BN] (MODE 4)
+    auto point_of = [&](int64_t s) __attribute__((always_inline)) -> int64_t {
+        return KMIN && a.qorder && s < a.nq ? (int64_t)a.qorder[s] : s;
+    };
+    if constexpr (KMIN) {
+        static_assert(S::BN <= S::NW * 256, "the points fit the sort buffers (cap >= 256)");
+        for (int t = tid; t < S::BN; t += S::NT) pidx[t] = (int32_t)point_of(q0 + t);
+    }
+    auto list_of = [&](int64_t p) __attribute__((always_inline)) {
+        return ((p / S::BN) * a.nsplit + split) * (int64_t)S::BN + p % S::BN;
+    };
+
     // the wave's queries, plane 0, for the whole kernel
     u32x4_t bq[NKS][NQB];
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
-        for (int qb = 0; qb < NQB; ++qb)
-            bq[ks][qb] = *(const u32x4_t *)(a.qp + ((q0 + qw + qb * 16 + r16) * 2) * a.ld + ks * 32 +
-                                          8 * g);
+        for (int qb = 0; qb < NQB; ++qb) {
+            const int64_t qrow = point_of(q0 + qw + qb * 16 + r16);
+            bq[ks][qb] = *(const u32x4_t *)(a.qp + (qrow * 2) * a.ld + ks * 32 + 8 * g);
+        }
 
     // global -> register staging of one tile of rows (and its row norms):
     // buffer loads from a per-tile resource, the thread's j-th load NT
@@ -167,11 +186,10 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
     };
     // MODE 4 (k-means lists) keeps its thresholds to itself: each lane
     // appends what lies below its own running minimum + kmin_margin
-    constexpr bool KMIN = MODE == 4;
     float best_r[KMIN ? NQB : 1];
 #pragma unroll
     for (int qb = 0; qb < (KMIN ? NQB : 1); ++qb)
-        best_r[qb] = KMIN && a.kmin_init ? a.kmin_init[q0 + qw + qb * 16 + r16] : VS_INF;
+        best_r[qb] = KMIN && a.kmin_init ? a.kmin_init[point_of(q0 + qw + qb * 16 + r16)] : VS_INF;
     if constexpr (!KMIN) {
         gthr_load();
 #pragma unroll
@@ -318,8 +336,10 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
                 if (c > 0) {
                     const int q = qw + qb * 16 + r16;
                     int pos = atomicAdd(&cnt_w[qb * 16 + r16], c);
-                    float *cvq = cv + (int64_t)q * a.cap;
-                    int32_t *ciq = ci + (int64_t)q * a.cap;
+                    const int64_t lq = KMIN ? list_of(pidx[q]) * a.cap
+                                            : list_base + (int64_t)q * a.cap;
+                    float *cvq = a.cand_v + lq;
+                    int32_t *ciq = a.cand_i + lq;
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         if (acc[qb][i] < thr_r[qb]) {
@@ -403,7 +423,10 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
         int32_t *lc = a.list_cnt + (qblk * a.nsplit + split) * (int64_t)S::BN + qw;
         int mx = 0;
         for (int q = lane; q < BNW; q += 64) {
-            lc[q] = cnt_w[q];
+            if (KMIN)
+                a.list_cnt[list_of(pidx[qw + q])] = cnt_w[q];
+            else
+                lc[q] = cnt_w[q];
             mx = max(mx, cnt_w[q]);
         }
         for (int o = 32; o > 0; o >>= 1) mx = max(mx, __shfl_xor(mx, o));

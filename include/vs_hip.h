@@ -280,6 +280,7 @@ VS_API int vs_index_sync(vs_index *idx);
  *   "km16_rt"     2 or 4: 16-row blocks per tile of that scan
  *   "km16_nqb"    2 or 4 (default): 16-point blocks per wave of that scan (4: 32-row tiles)
  *   "pick_order"  1: the k-means pick walks the points grouped by the last step's clusters
+ *   "assign_order" 1: so does the k-means assign scan
  *   "merge_mu"    1, 2, 4 or 8: 1,024-entry list chunks the merge reads per pass (0: by
  *                 batch size)
  *   "fail_alloc"  n > 0: the n-th device allocation of any index from now on, on

@@ -290,3 +290,33 @@ def test_kmeans_second_step_grouped_order(vs):
     assert np.array_equal(c2.view(np.uint32), c3.view(np.uint32)) and np.array_equal(n2, n3)
     ar, _, objr = oracle.kmeans_assign(x, cen1, NT)
     assert np.array_equal(a2, ar) and o2 == objr
+
+
+def test_kmeans_assign_order_matches_index_order(vs):
+    """From the second step on the assign scan walks the points grouped by
+    the last step's clusters (option assign_order, the default), their
+    lists and counts still indexed by point: three chained steps on 30,000
+    points (ending inside a 256-point block) give the same assignments,
+    objective and centroids as index order, and the oracle's."""
+    x, _ = syn.gaussian_mixture(30_000, 256, 1024, 0.1, 52)
+    cen = x[syn.seeded_subset(30_000, 4096, 52)].copy()
+    u = syn.rng(53, 0).random(4096 * 256)
+    a = vs.GpuIndexFlat.l2(256, storage="f32")
+    b = vs.GpuIndexFlat.l2(256, storage="f32")
+    a.add(x)
+    b.add(x)
+    b.set_option("assign_order", 0)
+    ca = cb = cen
+    for step in range(3):
+        ra = vs.kmeans_step(a, ca, 1, u)
+        rb = vs.kmeans_step(b, cb, 1, u)
+        ar, cr, cntr, objr = _kmeans_oracle_step(x, ca, u)
+        assert np.array_equal(ra[0], ar), f"step {step}: {np.sum(ra[0] != ar)} assignments differ"
+        assert ra[3] == objr and np.array_equal(ra[2], cntr)
+        assert np.array_equal(ra[1].view(np.uint32), cr.view(np.uint32))
+        assert np.array_equal(ra[0], rb[0]) and ra[3] == rb[3]
+        assert np.array_equal(ra[1].view(np.uint32), rb[1].view(np.uint32))
+        ca, cb = ra[1], rb[1]
+    assert a.prof_get("assign_order")[0] == 2 and b.prof_get("assign_order")[0] == 0
+    a.close()
+    b.close()
