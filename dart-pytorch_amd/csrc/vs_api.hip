@@ -2102,20 +2102,19 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     VS_HIP(x->km_cxn.ensure((size_t)(K + kRowSlack) * 4), "centroid norms");
     VS_HIP(hipMemsetAsync(x->km_cen.p, 0, (size_t)(K + kRowSlack) * ld * 4, x->st), "clear");
     VS_HIP(hipMemsetAsync(x->km_cxn.p, 0, (size_t)(K + kRowSlack) * 4, x->st), "clear");
-    VS_HIP(x->flags.ensure(4), "flags");
-    VS_HIP(hipMemsetAsync(x->flags.p, 0, 4, x->st), "flags");
+    // misc: [0] the largest centroid norm, [1] the centroids' flags, [2] the
+    // accumulator bound -- all on the device: no host round trip separates
+    // the centroids from the assign scan (the flags are read with the
+    // pick's results, before any exhaustive pass)
+    VS_HIP(x->misc.ensure(16), "misc");
+    float *kmisc = x->misc.as<float>();
+    uint32_t *cflags_dev = (uint32_t *)(kmisc + 1);
+    VS_HIP(vs::launch_fill32(cflags_dev, 1, 0u, x->st), "flags");
     VS_HIP(vs::launch_store_rows(x->stage.p, 0, d, K, d, x->km_cen.p, 0, ld,
-                                 x->km_cxn.as<float>(), x->flags.as<uint32_t>(), x->st),
+                                 x->km_cxn.as<float>(), cflags_dev, x->st),
            "storing centroids");
-    uint32_t cf = 0;
-    VS_HIP(hipMemcpyAsync(&cf, x->flags.p, 4, hipMemcpyDeviceToHost, x->st), "flags");
-    // the largest centroid norm, for the accumulator's error bound
-    float cmax = 0.f;
-    VS_HIP(x->misc.ensure(4), "misc");
-    VS_HIP(vs::launch_max_reduce(x->km_cxn.as<float>(), K, x->misc.as<float>(), x->st), "max");
-    VS_HIP(hipMemcpyAsync(&cmax, x->misc.p, 4, hipMemcpyDeviceToHost, x->st), "max");
-    VS_HIP(hipStreamSynchronize(x->st), "centroids");
-    if (cf & vs::kFlagNonFinite) return set_err(VS_ERR_NONFINITE, "centroids contain NaN or infinity");
+    VS_HIP(vs::launch_max_reduce(x->km_cxn.as<float>(), K, kmisc, x->st), "max");
+    VS_HIP(x->flags.ensure(4), "flags");
 
     // points as prepared queries against the centroid "database" (kept
     // across iterations while the stored rows are unchanged)
@@ -2159,14 +2158,16 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     // taken with a 25% margin.
     const double r = coarse ? 1.0 / 256.0 : 1.0 / 32768.0;
     const double gam = accum_gamma(d, coarse ? 1 : 3);
-    const double pc = (double)pmax * std::sqrt((double)cmax);
-    const float bound = (float)(1.25 * (2.0 * r * pc + gam * ((double)cmax + 2.0 * pc)) + 1e-6);
+    float *bound_dev = kmisc + 2;
+    VS_HIP(vs::launch_kmeans_bound(kmisc, (double)pmax, r, gam, bound_dev, x->st), "bound");
+    plan.dev_bound = bound_dev;
+    const float bound = 0.f;  // (the kernels read bound_dev)
     // On the row-shared scan each lane appends every value below its running
     // minimum + 2.5 bound to its list (the pick re-scores those within 2 bound
     // of the smallest and proves the rest worse with the other half bound).
     if (coarse && plan.kind == 3) {
         plan.share_kmin = 1;
-        plan.kmin_margin = 2.5f * bound;
+        plan.kmin_margin = 0.f;  // 2.5 * bound_dev, read by the kernels
         // option km16_nqb 4: 64 points per wave on the bf16 copy of the
         // centroids (32-row tiles keep it at two waves per SIMD); decided
         // here, before the lists are sized
@@ -2185,7 +2186,7 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
             VS_HIP(x->km_init.ensure((size_t)pq.nq_pad * 4), "running minima");
             VS_HIP(vs::launch_kmeans_init(x->km_assign.as<int32_t>(), x->km_best.as<double>(),
                                           x->km_shift.as<double>(), pq.qnorm, n, pq.nq_pad, K,
-                                          bound, x->km_init.as<float>(), x->st),
+                                          bound, bound_dev, x->km_init.as<float>(), x->st),
                    "running minima");
             plan.kmin_init = x->km_init.as<float>();
             x->prof["kmin_init"].launches++;
@@ -2376,10 +2377,12 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
     })};
 
     int32_t nfb = 0;
-    uint32_t pflags = 0;
+    uint32_t pflags = 0, cf = 0;
     VS_HIP(hipMemcpyAsync(&nfb, fb_count, 4, hipMemcpyDeviceToHost, x->st), "fallbacks");
     VS_HIP(hipMemcpyAsync(&pflags, x->flags.p, 4, hipMemcpyDeviceToHost, x->st), "pick flags");
+    VS_HIP(hipMemcpyAsync(&cf, cflags_dev, 4, hipMemcpyDeviceToHost, x->st), "centroid flags");
     VS_HIP(hipStreamSynchronize(x->st), "assign");
+    if (cf & vs::kFlagNonFinite) return set_err(VS_ERR_NONFINITE, "centroids contain NaN or infinity");
     if (pflags & vs::kFlagBadId)
         return set_err(VS_ERR_HIP, "internal error: a k-means candidate outside the centroids");
     x->prof["kmeans_fallback_points"].launches += nfb;

@@ -77,6 +77,8 @@ struct ScanKArgs {
     int64_t out_cap;
     float kmin_margin;   // row-shared scan, k-means lists: each lane appends the values below
                          // its running minimum plus this margin
+    const float *dev_bound;  // k-means lists: the bound on the device (the margin is 2.5 times
+                             // it, overriding kmin_margin), or null
     const int32_t *qorder;   // k-means lists: slot s of the scan stands for point qorder[s]
                              // (s < nq; lists, counts and kmin_init stay indexed by point), or null
     const float *kmin_init;  // k-means lists: per query, a value at or above the accumulator of

@@ -107,6 +107,9 @@ struct ScanPlan {
                           // running minimum + kmin_margin; a list that would fill is marked
                           // full, count cap + 1, and takes no more)
     float kmin_margin = 0.f;
+    const float *dev_bound = nullptr;  // k-means: the accumulator bound on the device; when set,
+                                       // the scan's and the pick's margin is 2.5 times it and
+                                       // kmin_margin is ignored
     const int32_t *qorder = nullptr;   // k-means lists: the points in the order the scan walks
                                        // them (slot s: point qorder[s]), or null (index order)
     const float *kmin_init = nullptr;  // k-means lists: per query (nq_pad entries), a value at or
@@ -288,7 +291,12 @@ hipError_t launch_kmeans_shift(const float *old_cen, int64_t ld, const float *ne
 // previous step's assignments and squared distances and the centroid shifts.
 hipError_t launch_kmeans_init(const int32_t *assign, const double *best_sq, const double *shift,
                               const float *qnorm, int64_t n, int64_t n_pad, int64_t K, float bound,
-                              float *init, hipStream_t st);
+                              const float *dev_bound, float *init, hipStream_t st);
+// *bound = the k-means accumulator bound from the largest centroid norm *cmax
+// and the largest point norm pmax (fp64 arithmetic, rounded to fp32), so
+// that no host round trip separates the centroids' norms from the scan.
+hipError_t launch_kmeans_bound(const float *cmax, double pmax, double r, double gam, float *bound,
+                               hipStream_t st);
 hipError_t launch_exclusive_scan_i32(const int32_t *in, int64_t n, int32_t *out, hipStream_t st);
 
 // Stable sort of (key, value) int32 pairs by key (rocPRIM radix sort).

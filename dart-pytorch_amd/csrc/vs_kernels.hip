@@ -669,6 +669,7 @@ hipError_t launch_scan_topk(const void *xb, int storage, int64_t ld, const float
     a.kmin_margin = plan.kmin_margin;
     a.kmin_init = plan.kmin_init;
     a.qorder = plan.qorder;
+    a.dev_bound = plan.dev_bound;
     return launch_scan_mode<0>(storage, pq, plan, a, st);
 }
 
@@ -746,6 +747,8 @@ struct MergeKArgs {
     int guess;            // thresholds were estimated: flag queries left short
     int seed_rank;        // MODE 2: rank whose value sets the threshold (0: kk)
     float kmin_margin;    // k-means pick over the row-shared scan's k-means lists
+    const float *dev_bound;  // k-means pick: the bound on the device (overrides bound; the
+                             // margin is then 2.5 times it), or null
     const int32_t *order; // k-means pick: slot s is point order[s] (nq slots), or null:
     int64_t slot0;        // point slot0 + s
     int64_t k;
@@ -1627,13 +1630,15 @@ hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, 
     a.cand_i = cand_i;
     a.gthr = gthr;
     a.bound = bound;
+    a.dev_bound = plan.dev_bound;
     a.assign = assign;
     a.best_sq = best_sq;
     a.fb_count = fallback_count;
     a.fb_list = fallback_list;
     if (plan.kind == 3 && plan.share_kmin) {
         // count-terminated k-means lists of the row-shared scan
-        if (!list_cnt || ld % 16 || plan.share_topm || !(plan.kmin_margin > 0.f))
+        if (!list_cnt || ld % 16 || plan.share_topm ||
+            !(plan.kmin_margin > 0.f || plan.dev_bound))
             return hipErrorInvalidValue;
         a.list_cnt = list_cnt;
         a.kmin_margin = plan.kmin_margin;
@@ -1684,6 +1689,7 @@ hipError_t launch_kmeans_pick(const float *x, int64_t ld, int64_t d, int64_t n, 
 // ---------------------------------------------------------------------------
 template <int KK>
 __global__ __launch_bounds__(256) void kmeans_pick_kernel(MergeKArgs a) {
+    if (a.dev_bound) a.bound = *a.dev_bound;
     const int64_t qg = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (qg >= a.nq) return;
     const int64_t qblk = qg / a.bn, q = qg % a.bn;
@@ -1882,6 +1888,10 @@ __device__ __forceinline__ int pick_candidates(const MergeKArgs &a, int64_t qc, 
 template <int E, int CH>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void kmeans_pick_wave_kernel(
     MergeKArgs a) {
+    if (a.dev_bound) {
+        a.bound = *a.dev_bound;
+        a.kmin_margin = 2.5f * a.bound;
+    }
     constexpr int RS = 65;  // LDS words per staged dimension (64 rows + 1: no bank conflicts on reads)
     constexpr int PIECES = CH / 4;            // 16-byte pieces per row chunk
     constexpr int ROWS_PER = 64 / PIECES;     // rows covered by one wave-wide load
@@ -1995,6 +2005,10 @@ constexpr int kPickSetMaxU = 1024;
 template <int E, int CH>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 3))) void kmeans_pick_set_kernel(
     MergeKArgs a) {
+    if (a.dev_bound) {
+        a.bound = *a.dev_bound;
+        a.kmin_margin = 2.5f * a.bound;
+    }
     constexpr int RS = 65;  // LDS words per staged dimension (64 rows + 1: no bank conflicts on reads)
     constexpr int PIECES = CH / 4;            // 16-byte pieces per row chunk
     constexpr int ROWS_PER = 64 / PIECES;     // rows covered by one wave-wide load
@@ -2388,9 +2402,10 @@ __global__ void kmeans_init_kernel(const int32_t *__restrict__ assign,
                                    const double *__restrict__ best_sq,
                                    const double *__restrict__ shift,
                                    const float *__restrict__ qnorm, int64_t n, int64_t n_pad,
-                                   int64_t K, float bound, float *init) {
+                                   int64_t K, float bound, const float *dev_bound, float *init) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n_pad) return;
+    if (dev_bound) bound = *dev_bound;
     float f = VS_INF;
     if (i < n) {
         const int32_t c = assign[i];
@@ -2413,10 +2428,27 @@ __global__ void kmeans_init_kernel(const int32_t *__restrict__ assign,
 
 hipError_t launch_kmeans_init(const int32_t *assign, const double *best_sq, const double *shift,
                               const float *qnorm, int64_t n, int64_t n_pad, int64_t K, float bound,
-                              float *init, hipStream_t st) {
+                              const float *dev_bound, float *init, hipStream_t st) {
     if (n_pad <= 0) return hipSuccess;
     kmeans_init_kernel<<<dim3((unsigned)((n_pad + 255) / 256)), dim3(256), 0, st>>>(
-        assign, best_sq, shift, qnorm, n, n_pad, K, bound, init);
+        assign, best_sq, shift, qnorm, n, n_pad, K, bound, dev_bound, init);
+    return hipGetLastError();
+}
+
+// The k-means accumulator bound from the largest centroid norm (cmax, on the
+// device) and the largest point norm pmax: 1.25 (2 r pmax sqrt(cmax) +
+// gam (cmax + 2 pmax sqrt(cmax))) + 1e-6, in fp64, rounded to fp32.
+__global__ void kmeans_bound_kernel(const float *cmax, double pmax, double r, double gam,
+                                    float *bound) {
+    if (threadIdx.x != 0) return;
+    const double c = (double)*cmax;
+    const double pc = pmax * sqrt(c);
+    *bound = (float)(1.25 * (2.0 * r * pc + gam * (c + 2.0 * pc)) + 1e-6);
+}
+
+hipError_t launch_kmeans_bound(const float *cmax, double pmax, double r, double gam, float *bound,
+                               hipStream_t st) {
+    kmeans_bound_kernel<<<dim3(1), dim3(64), 0, st>>>(cmax, pmax, r, gam, bound);
     return hipGetLastError();
 }
 

@@ -118,6 +118,7 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
         return KMIN && a.qorder && s < a.nq ? (int64_t)a.qorder[s] : s;
     };
     if constexpr (KMIN) {
+        if (a.dev_bound) a.kmin_margin = 2.5f * *a.dev_bound;
         static_assert(S::BN <= S::NW * 256, "the points fit the sort buffers (cap >= 256)");
         for (int t = tid; t < S::BN; t += S::NT) pidx[t] = (int32_t)point_of(q0 + t);
     }
@@ -500,7 +501,8 @@ hipError_t launch_share_scan(const ScanPlan &plan, const ScanKArgs &args, hipStr
         return hipErrorInvalidValue;
     const int64_t total = plan.nqblk * plan.nsplit;
     const int64_t grid = ((total + 7) / 8) * 8;
-    if (plan.share_kmin && (plan.share_topm || !(plan.kmin_margin > 0.f))) return hipErrorInvalidValue;
+    if (plan.share_kmin && (plan.share_topm || !(plan.kmin_margin > 0.f || plan.dev_bound)))
+        return hipErrorInvalidValue;
     const int mode = plan.share_kmin ? 4 : plan.share_topm ? 2 : 0;
     void (*fn)(ScanKArgs) =
         share_kernel(plan.tile_st, plan.nks, plan.bn, plan.tm, args.ld, mode);

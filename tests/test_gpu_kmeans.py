@@ -174,3 +174,29 @@ def test_kmeans_step_in_place_buffers(vs):
     pts.close()
     assert np.array_equal(cnt, cnt_sep) and obj.value == obj_sep and np.sum(cnt == 0) == 2
     assert np.array_equal(inout.view(np.uint32), sep.view(np.uint32))
+
+
+@pytest.mark.parametrize("bad", [np.nan, np.inf])
+def test_kmeans_nonfinite_centroids(vs, bad):
+    """Centroids holding NaN or infinity: the step reports VS_ERR_NONFINITE
+    (checked with the pick's results, before any exhaustive pass), and the
+    next step on the same points with finite centroids equals the oracle's."""
+    from vector_store import _native as N
+
+    x, _ = syn.gaussian_mixture(20_000, 256, 64, 0.1, 91)
+    cen = x[syn.seeded_subset(len(x), 256, 91)].copy()
+    pts = vs.GpuIndexFlat.l2(256, storage="f32")
+    pts.add(x)
+    u = syn.rng(92, 0).random(256 * 256)
+    a, c1, _, _ = vs.kmeans_step(pts, cen, 1, u)  # a previous step (running minima, order)
+    badc = c1.copy()
+    badc[17, 5] = bad
+    with pytest.raises(N.VsError) as ei:
+        vs.kmeans_step(pts, badc, 1, u)
+    assert ei.value.code == N.VS_ERR_NONFINITE
+    a2, c2, cnt2, obj2 = vs.kmeans_step(pts, c1, 1, u)
+    pts.close()
+    ar, _, objr = oracle.kmeans_assign(x, c1, NT)
+    cr, cntr, _ = oracle.kmeans_update(x, ar, c1, 1, u)
+    assert np.array_equal(a2, ar) and obj2 == objr and np.array_equal(cnt2, cntr)
+    assert np.array_equal(c2.view(np.uint32), cr.view(np.uint32))
