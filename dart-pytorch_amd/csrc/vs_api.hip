@@ -449,15 +449,38 @@ int check_dtype(int dt) {
 // gemm_min_nq and gemm_wq / gemm_qb / gemm_kc force it on or off and pick a
 // shape.
 
+// The row-shared scan's lists.  Top-k lists (lane): one per lane, four per
+// query and workgroup (each lane sees rows 4g .. 4g + 3 of every 16-row
+// block), each keeping kk (kk_final, or kk_final / 4 with the merge's
+// verification); a lane's list gains up to 4 entries per row block and is
+// cut before a tile when it holds more than cap - 4 rt, and cap leaves kk +
+// 4 rt slots above kk so that cuts stay rare.  Otherwise (k-means lists,
+// estimates) one list per query and workgroup keeping kk_final, cut when it
+// holds more than cap - 16 rt; 256 slots at least keep cuts rare while its
+// threshold is still loose (the list is sorted only up to its fill).
+bool share_lists(const vs_index *x, vs::ScanPlan *p, bool lane) {
+    const int rt = p->tm;
+    const int kk = lane ? p->kk : p->kk_final;
+    const int cap = lane ? (int)std::max<int64_t>(64, next_pow2(2 * kk + 4 * rt))
+                         : (int)std::max<int64_t>(256, next_pow2(kk + std::max(48, 16 * rt)));
+    const size_t lds = vs::share_lds_bytes(p->nks, p->bn / 64, rt, cap, lane ? 4 : 1);
+    if (lds > x->lds_max) return false;
+    p->kk = kk;
+    p->cap = cap;
+    p->lw = lane ? 4 : 1;
+    p->lds_bytes = lds;
+    return true;
+}
+
 // Row-shared scan (top-k only): bf16 rows of 128 or 256 elements, one query
-// plane, large batches.  Every list keeps kk_final entries (one list per
-// query and workgroup).  Option share: -1 = planner rule (rows of 128
+// plane, large batches.  Option share: -1 = planner rule (rows of 128
 // elements, batch >= 256), 0 = off, 1 = also rows of 256 elements.  The
 // one-pass selection of fp32 rows (storage kSelectCoarse, k-means) takes
 // rows of 128 and 256 elements.  The grid is four times the resident
-// workgroups.
+// workgroups.  lane: top-k lane lists (bf16 rows by default); false for
+// the estimate pre-pass (lists of each lane's smallest values, one per query).
 bool plan_share(const vs_index *x, int64_t nq, int64_t nrows, int planes, int storage,
-                vs::ScanPlan *p, int64_t max_split) {
+                vs::ScanPlan *p, int64_t max_split, int lane = -1) {
     const int mode = x->opt.share;
     if (mode == 0 || (storage != 1 && storage != vs::kSelectCoarse) || planes != 1) return false;
     if (!(x->ld == 128 || (x->ld == 256 && (mode > 0 || storage == vs::kSelectCoarse))))
@@ -466,24 +489,17 @@ bool plan_share(const vs_index *x, int64_t nq, int64_t nrows, int planes, int st
     const int nks = (int)(x->ld / 32), nqb = nks == 4 ? 4 : 2;
     // fp32 tiles: half the rows, the same staging registers
     const int rt = storage == 1 ? (nks == 4 ? 8 : 4) : 2;
-    // a list of the row-shared scan gains up to 16 entries per 16-row block
-    // and query, and is cut to kk before a tile when it holds more than
-    // cap - 16 rt; 256 slots at least keep cuts rare while its threshold is
-    // still loose (the list is sorted only up to its fill)
-    const int kk = p->kk_final;
-    const int cap = (int)std::max<int64_t>(256, next_pow2(kk + std::max(48, 16 * rt)));
-    const size_t lds = vs::share_lds_bytes(nks, nqb, rt, cap);
-    if (lds > x->lds_max) return false;
+    vs::ScanPlan sp = *p;
+    sp.nks = nks;
+    sp.bn = 64 * nqb;
+    sp.tm = rt;
+    // bf16 rows: top-k lists; the one-pass selection: k-means lists
+    if (!share_lists(x, &sp, lane < 0 ? storage == 1 : lane > 0)) return false;
+    *p = sp;
     p->kind = 3;
     p->tile_st = storage;
     p->share_topm = 0;
-    p->kk = kk;
-    p->cap = cap;
-    p->nks = nks;
-    p->bn = 64 * nqb;
-    p->tm = rt;
-    p->lw = 1;
-    p->lds_bytes = lds;
+    const size_t lds = p->lds_bytes;
     p->nqblk = (nq + p->bn - 1) / p->bn;
     const int64_t tile_rows = 16 * rt;
     // Splits: the whole grid resident at once (or whole rounds of it), so the
@@ -494,7 +510,7 @@ bool plan_share(const vs_index *x, int64_t nq, int64_t nrows, int planes, int st
     const int64_t target = resident * 4;
     int64_t nsplit = std::max<int64_t>(1, target / p->nqblk);
     nsplit = std::min<int64_t>(nsplit, std::max<int64_t>(1, nrows / (tile_rows * 8)));
-    if (max_split > 0) nsplit = std::min<int64_t>(nsplit, max_split);
+    if (max_split > 0) nsplit = std::min<int64_t>(nsplit, std::max<int64_t>(1, max_split / p->lw));
     int64_t rps = round_up((nrows + nsplit - 1) / nsplit, tile_rows);
     if (rps <= 0) rps = tile_rows;
     p->rows_per_split = rps;
@@ -924,8 +940,14 @@ int seed_thresholds(vs_index *x, const vs::PreparedQueries &pq, int64_t S, int64
     // the row-shared scan then keeps each lane's smallest in registers
     // instead of lists (exact unless one lane met more than m of them; then
     // the estimate is larger, never smaller)
-    if (pp.kind == 3 && seed_rank > 0 && seed_rank <= 4 * vs::share_topm_est())
-        pp.share_topm = vs::share_topm_est();
+    if (pp.kind == 3 && seed_rank > 0 && seed_rank <= 4 * vs::share_topm_est()) {
+        vs::ScanPlan tp = pp;
+        if (plan_share(x, pq.nq, S, pq.planes, x->storage, &tp, max_lists, 0)) {
+            pp = tp;
+            pp.share_topm = vs::share_topm_est();
+            plan_merge(x, pq.nq, &pp);
+        }
+    }
     // the streaming scan's lists over a short sample end full: the merge
     // reads them uncut (cutting each list at the end costs more than the
     // merge's extra reads), and an entry a list dropped in a cut lies above
@@ -2173,7 +2195,7 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
         // here, before the lists are sized
         if (x->opt.km16_nqb == 4 && x->opt.km16 && plan.tile_st == vs::kSelectCoarse &&
             plan.nks == 8) {
-            const size_t lds = vs::share_lds_bytes(plan.nks, 4, 2, plan.cap);
+            const size_t lds = vs::share_lds_bytes(plan.nks, 4, 2, plan.cap, 1);
             if (lds <= x->lds_max) {
                 plan.bn = 256;
                 plan.tm = 2;
@@ -2226,7 +2248,7 @@ int vs_kmeans_step(vs_index *x, const float *centroids_in, int64_t K, int64_t mi
         // bf16 rows stage twice the rows per tile in the same registers
         const int rt = x->opt.km16_rt;
         if (rt == 4 && plan.bn == 128) {
-            const size_t lds = vs::share_lds_bytes(plan.nks, plan.bn / 64, 4, plan.cap);
+            const size_t lds = vs::share_lds_bytes(plan.nks, plan.bn / 64, 4, plan.cap, 1);
             if (lds <= x->lds_max) {
                 plan.tm = 4;
                 plan.lds_bytes = lds;

@@ -348,7 +348,7 @@ size_t gemm_lds_bytes(int st, int pb, int wr, int wq, int rb, int qb, int kc, in
 size_t gemm4_lds_bytes(int cap);
 
 // LDS of the row-shared scan (two row stages plus list bookkeeping).
-size_t share_lds_bytes(int nks, int nqb, int rt, int cap);
+size_t share_lds_bytes(int nks, int nqb, int rt, int cap, int lw);
 // Row-shared scan workgroups one CU holds at once (0: no such shape; mode 0
 // lists, 2 top-m values, 4 k-means lists).
 int share_blocks_per_cu(int st, int nks, int bn, int rt, int64_t ld, size_t lds, int mode);
