@@ -8,6 +8,9 @@ database, the queries and the result buffers resident in HBM.  The other
 configurations sit under "workloads":
 
   c1  10k x 384 fp32 unit rows, IP, 100 queries, k = 10 (the CPU-runnable case);
+  c2f configs[1]'s shape on fp32 unit N(0,1) rows, which bf16 does not hold
+      exactly: the rows stay fp32 and every product takes three MFMA passes
+      over split-bf16 planes (the path of general fp32 embeddings);
   c3  20M x 768 bf16 unit rows (device-generated), IP, k = 10, batches
       1 / 64 / 1024 / 8192;
   c4  k-means step, 2M x 256 fp32 mixture points, K = 4096;
@@ -38,7 +41,7 @@ C2 also reports the PCIe-inclusive rate of the host-buffer entry point
 formats (toBenchCsv / toBenchMarkdown, bench.dart:217-312); --csv / --md write
 them to files.
 
-Single workloads (--workload c1|c2|c3|c4|c5, --batch for c3) print that
+Single workloads (--workload c1|c2|c2f|c3|c4|c5, --batch for c3) print that
 workload's line alone (profiling runs use them); --workload copy / libgemm are
 the counter yardstick and the vendor GEMM for scale.
 """
@@ -67,12 +70,13 @@ CPU_SHARE = 16  # host cores of one GPU's share on the measurement boxes
 # (workload, n, nq, k).  The command and readings are in the named profile;
 # configurations without a measurement report traffic null.
 MEASURED_TRAFFIC = {
-    ("c2", 1_000_000, 10_000, 100): (1.052e9, "profiles/scan_c2_1Mx128_k100.md"),
+    ("c2", 1_000_000, 10_000, 100): (1.194e9, "profiles/scan_c2_1Mx128_k100.md"),
     ("c3", 20_000_000, 1, 10): (30.73e9, "profiles/scan_c3_20Mx768_b1_b64.md"),
     ("c3", 20_000_000, 64, 10): (30.78e9, "profiles/scan_c3_20Mx768_b1_b64.md"),
-    ("c3", 20_000_000, 1024, 10): (32.60e9, "profiles/gemm_c3_20Mx768_b1024_b8192.md"),
-    ("c4", 2_000_000, 4096, 256): (2.19e9, "profiles/kmeans_c4_2Mx256.md"),
-    ("c5", 500_000, 500_000, 512): (233.11e9, "profiles/selfjoin_c5_500kx512.md"),
+    ("c3", 20_000_000, 1024, 10): (32.44e9, "profiles/gemm_c3_20Mx768_b1024_b8192.md"),
+    ("c3", 20_000_000, 8192, 10): (364.55e9, "profiles/gemm_c3_20Mx768_b1024_b8192.md"),
+    ("c4", 2_000_000, 4096, 256): (2.38e9, "profiles/kmeans_c4_2Mx256.md"),
+    ("c5", 500_000, 500_000, 512): (301.49e9, "profiles/selfjoin_c5_500kx512.md"),
 }
 
 
@@ -237,6 +241,14 @@ def search_setup(vs, NN, workload, args):
         xb, xq = syn.int_grid(n, d, args.seed, 0), syn.int_grid(nq, d, args.seed, 1)
         storage = "auto"
         desc = f"c2: exact L2 top-{k}, {n} x {d} fp32 integers 0..255, {nq} queries"
+    elif workload == "c2f":
+        # configs[1]'s shape on general fp32 values (not exact in bf16): the rows stay fp32
+        # and the scan multiplies their split-bf16 planes, three MFMA passes per product
+        n, d, nq, k, metric = args.n or 1_000_000, 128, args.nq or 10_000, args.k or 100, 0
+        xb, xq = syn.normal_unit(n, d, args.seed, 0), syn.normal_unit(nq, d, args.seed, 1)
+        storage = "auto"
+        desc = (f"c2 shape on fp32 data: exact L2 top-{k}, {n} x {d} fp32 unit N(0,1), "
+                f"{nq} queries (split-bf16 planes, three MFMA passes)")
     else:
         n, d, nq, k, metric = args.n or 10_000, 384, args.nq or 100, args.k or 10, 1
         xb, xq = syn.normal_unit(n, d, args.seed, 0), syn.normal_unit(nq, d, args.seed, 1)
@@ -783,7 +795,7 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="all",
-                    choices=["all", "c1", "c2", "c3", "c4", "c5", "copy", "libgemm"])
+                    choices=["all", "c1", "c2", "c2f", "c3", "c4", "c5", "copy", "libgemm"])
     ap.add_argument("--batch", type=int, default=0, help="c3 alone: one batch size")
     ap.add_argument("--c3-batches", default="1,64,1024,8192")
     ap.add_argument("--n", type=int, default=0)
@@ -827,6 +839,7 @@ def main():
         args.n = 0  # --n applies to single workloads only
         out["workloads"] = {
             "c1": guarded("c1", lambda: run_search(vs, NN, "c1", args, ctx)),
+            "c2f": guarded("c2f", lambda: run_search(vs, NN, "c2f", args, ctx)),
             "c3": guarded("c3", lambda: run_c3(vs, NN, args, ctx, batches)),
             "c4": guarded("c4", lambda: run_kmeans(vs, NN, args, ctx)),
             "c5": guarded("c5", lambda: run_join(vs, NN, args, ctx)),
@@ -839,7 +852,7 @@ def main():
             else:
                 oks.append(r.get("parity", {}).get("ok"))
         out["parity_all_ok"] = all(o is True for o in oks) if not args.no_cpu else None
-    elif args.workload in ("c1", "c2"):
+    elif args.workload in ("c1", "c2", "c2f"):
         out = run_search(vs, NN, args.workload, args, ctx, full=True)
     elif args.workload == "c3":
         batches = [args.batch] if args.batch else [int(b) for b in args.c3_batches.split(",") if b]
