@@ -150,7 +150,7 @@ __device__ inline void flush_list(float *cvq, int32_t *ciq, int *cnt_q, float *t
 // The block's lists of query q sit at thr[q + i tstride], i < nl (tstride 0:
 // bn).
 template <int KM>
-__device__ inline void cut_lists_lanes(float *cv, int32_t *ci, int *cnt_w, float *thr_w,
+__device__ __forceinline__ void cut_lists_lanes(float *cv, int32_t *ci, int *cnt_w, float *thr_w,
                                        const float *thr, int bn, int nl, uint32_t *gthr,
                                        int cap, int kk, int kk_final, int publish_block,
                                        int over, bool pad, int lane, int tstride = 0) {

@@ -79,6 +79,22 @@ size_t gemm_lds_bytes(int st, int pb, int wr, int wq, int rb, int qb, int kc, in
 // that lane offset: the offsets grow with v, so the bits form a prefix.  The
 // epilogues mask their hits with it instead of comparing every offset (per
 // value compares are hoisted by the compiler into 64 lane masks per tile).
+// Bit v (0..15) set where x[v] < t (LT) or x[v] <= t.  Each compare selects
+// an inline constant with the sign bit set or zero, and a funnel shift moves
+// that bit in below the bits of the values after it, so no per-bit constant
+// is held in a register across the epilogue.
+template <bool LT>
+__device__ __forceinline__ uint32_t value_mask16(const f32x16_t &x, float t) {
+    uint32_t m = 0u;
+#pragma unroll
+    for (int v = 15; v >= 0; --v) {
+        const float xv = x[v];
+        const bool p = LT ? xv < t : xv <= t;
+        m = __builtin_amdgcn_alignbit(m, p ? 0xbf800000u : 0u, 31);
+    }
+    return m;
+}
+
 __device__ __forceinline__ uint32_t rows_below_mask(int t) {
     int c = 0;
 #pragma unroll
@@ -205,10 +221,7 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[QB][RB], const Sca
             int c = 0;
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb) {
-                mk[rb] = 0u;
-#pragma unroll
-                for (int v = 0; v < 16; ++v)
-                    mk[rb] |= acc[qb][rb][v] < thr_r[qb] ? (1u << v) : 0u;
+                mk[rb] = value_mask16<true>(acc[qb][rb], thr_r[qb]);
                 mk[rb] &= rows_below_mask(lim - rb * 32 - 4 * h);
                 c += __builtin_popcount(mk[rb]);
             }
@@ -220,7 +233,7 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[QB][RB], const Sca
                 for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
                     for (int v = 0; v < 16; ++v) {
-                        if (mk[rb] & (1u << v)) {
+                        if ((mk[rb] >> v) & 1u) {
                             cvq[pos] = acc[qb][rb][v];
                             ciq[pos] = (int32_t)(wr0 + rb * 32 + 8 * (v / 4) + 4 * h + v % 4);
                             ++pos;
@@ -267,9 +280,7 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[QB][RB], const Sca
             int c = 0;
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb) {
-                mk[rb] = 0u;
-#pragma unroll
-                for (int v = 0; v < 16; ++v) mk[rb] |= acc[qb][rb][v] <= thr_r[qb] ? (1u << v) : 0u;
+                mk[rb] = value_mask16<false>(acc[qb][rb], thr_r[qb]);
                 mk[rb] &= rows_below_mask(lim - rb * 32 - 4 * h) &
                           ~rows_below_mask(omin - rb * 32 - 4 * h);
                 c += __builtin_popcount(mk[rb]);
@@ -280,7 +291,7 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[QB][RB], const Sca
                 for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
                     for (int v = 0; v < 16; ++v) {
-                        if (mk[rb] & (1u << v)) {
+                        if ((mk[rb] >> v) & 1u) {
                             if (pos < (unsigned long long)a.out_cap) {
                                 a.out_q[pos] = (int32_t)qg;
                                 a.out_i[pos] = (int32_t)(wr0 + rb * 32 + 8 * (v / 4) + 4 * h + v % 4);
@@ -348,6 +359,9 @@ __device__ __forceinline__ void gemm_final_cut(const ScanKArgs &a, const EpiCtx 
 // The register-staged kernel writes the next chunk's tiles to LDS between
 // the MFMAs of the current chunk's last K-step.
 constexpr bool kInterleaveStores = true;
+// Row fragments read ahead of the MFMAs that use them in the pipelined chunk
+// (two: 4 more VGPRs than one, still spill-free at 256 for top-k).
+constexpr int kPipeDist = 2;
 
 template <int ST, int PB, int WR, int WQ, int RB, int QB, int KC, int MODE>
 __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
@@ -355,7 +369,10 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
     constexpr int NT = S::NT, BR = S::BR, BQ = S::BQ, KP = S::KP;
     extern __shared__ __align__(16) char smem[];
     const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
+    // the wave index in a scalar register: every per-wave base (lists,
+    // thresholds, sort buffers) stays scalar instead of taking VGPRs
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63, l32 = lane & 31, h = lane >> 5;
     const int wr = wave % WR, wq = wave / WR;
 
     int64_t split, qblk;
@@ -490,15 +507,16 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
     f32x16_t acc[QB][RB];
     uint32_t gt[QB];
 
-    // One K-chunk of MFMAs from LDS stage `stage`.  FIRST: the tile's first
-    // chunk, whose first K-step takes the row norms (L2) or zero (IP) as its
-    // C operand.
     // One K-chunk of MFMAs from LDS stage `stage`; with `nstage`, the next
     // chunk's A and B tiles (already loaded into registers) are written to
     // that stage between the MFMAs of the last K-step, so that the LDS
-    // writes overlap the matrix pipe instead of following it.
+    // writes overlap the matrix pipe instead of following it.  first_c: 0 a
+    // later chunk; 1 a tile's first chunk, whose first K-step takes the row
+    // norms (L2) or zero (IP) as its C operand; 2 a tile's first chunk of an
+    // inner-product scan (zero C operand, no metric test inside).
     auto compute = [&](const char *stage, auto first_c, char *nstage) __attribute__((always_inline)) {
-        constexpr bool FIRST = decltype(first_c)::value;
+        constexpr int FM = decltype(first_c)::value;
+        constexpr bool FIRST = FM != 0;
         constexpr bool IL = kInterleaveStores;
         const uint16_t *As = (const uint16_t *)stage;
         const uint16_t *Bs = As + S::AP * BR * KP;
@@ -510,6 +528,58 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
         const uint16_t *bl_ = Bs + (qw0 + l32) * KP;
         auto koff = [&](int ks) __attribute__((always_inline)) { return piece(2 * ks + h, l32) * 8; };
         const float *Ns = (const float *)(As + S::STAGE_ELEMS) + wr * 32 * RB + 4 * h;
+        if constexpr (ST == 1 && PB == 1 && FM != 1 && IL) {
+            // Software-pipelined chunk (bf16 rows, one query plane): the
+            // (K-step, row block) pairs run in order; the row fragment of the
+            // pair kPipeDist ahead, and at a K-step's first row block the next
+            // K-step's query fragments, are read before this pair's MFMAs, so
+            // the matrix pipe waits on no fragment read issued just before it.
+            constexpr int NKS = KC / 16, NI = NKS * RB;
+            constexpr int NST = S::A_LOADS + S::B_LOADS;
+            constexpr int PD = kPipeDist;
+            bf16x8_t af[PD + 1], bq[2][QB];
+            auto rd_a = [&](int i) __attribute__((always_inline)) {
+                return __builtin_bit_cast(
+                    bf16x8_t, *(const u32x4_t *)(al_ + (i % RB) * 32 * KP + koff(i / RB)));
+            };
+            auto rd_b = [&](int ks, int qb) __attribute__((always_inline)) {
+                return __builtin_bit_cast(bf16x8_t,
+                                          *(const u32x4_t *)(bl_ + qb * 32 * KP + koff(ks)));
+            };
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) bq[0][qb] = rd_b(0, qb);
+#pragma unroll
+            for (int i = 0; i < PD; ++i) af[i] = rd_a(i);
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const int ks = i / RB, rb = i % RB;
+                if (i + PD < NI) af[(i + PD) % (PD + 1)] = rd_a(i + PD);
+                if (rb == 0 && ks + 1 < NKS) {
+#pragma unroll
+                    for (int qb = 0; qb < QB; ++qb) bq[(ks + 1) & 1][qb] = rd_b(ks + 1, qb);
+                }
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb)
+                    acc[qb][rb] = mfma32_bf16(af[i % (PD + 1)], bq[ks & 1][qb],
+                                              FM == 2 && ks == 0 ? f32x16_t{} : acc[qb][rb]);
+            }
+#pragma unroll
+            for (int p = 0; p < NLD; ++p) store_piece(p, nstage, -1);
+            // the order: the first reads, then per pair its look-ahead reads
+            // and its MFMAs, in the last K-step one store of the next stage
+            // after each pair's MFMAs, the remaining stores last
+            __builtin_amdgcn_sched_group_barrier(0x100, QB + PD, 0);
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const int ks = i / RB, rb = i % RB;
+                if (i + PD < NI) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                if (rb == 0 && ks + 1 < NKS) __builtin_amdgcn_sched_group_barrier(0x100, QB, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, QB, 0);
+                if (ks == NKS - 1 && rb < NST) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+            }
+            if (NST > RB) __builtin_amdgcn_sched_group_barrier(0x200, NST > RB ? NST - RB : 0, 0);
+            return;
+        }
 #pragma unroll
         for (int ks = 0; ks < KC / 16; ++ks) {
             // the last K-step and the stores form a scheduling region of
@@ -606,9 +676,12 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
                         gt[qb] = __hip_atomic_load(&a.gthr[q0 + qw0 + qb * 32 + l32],
                                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
-                compute(cur, std::true_type{}, nxt);
+                if (l2)
+                    compute(cur, std::integral_constant<int, 1>{}, nxt);
+                else
+                    compute(cur, std::integral_constant<int, 2>{}, nxt);
             } else {
-                compute(cur, std::false_type{}, nxt);
+                compute(cur, std::integral_constant<int, 0>{}, nxt);
             }
             // (with interleaved stores, the last chunk stores stale registers
             // into the free stage, which nothing reads afterwards)
@@ -667,6 +740,8 @@ constexpr int ROWB = KC * 2;                 // bytes per row (query) per chunk
 constexpr int A_OFF = 0, B_OFF = BR * ROWB;  // within a stage
 constexpr int N_OFF = B_OFF + BQ * ROWB;     // row norms of the tile (stage 0, L2)
 constexpr int STAGE = N_OFF + BR * 4;
+static_assert(NW == WR * WQ && NT == 64 * NW && BR == WR * 128 && BQ == WQ * 128,
+              "each wave multiplies 128 rows by 128 queries");
 constexpr int LOADS = BR * (ROWB / 16) / NT;  // 16-byte loads per thread and operand
 static_assert(LOADS == 4 && BQ == BR, "thread layout of the loads");
 static_assert(2 * LOADS == RB + QB && RB * QB == 4 * LOADS,
@@ -683,7 +758,10 @@ __global__ __launch_bounds__(256) void gemm4_scan_kernel(ScanKArgs a) {
     using namespace g4;
     extern __shared__ __align__(16) char smem[];
     const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
+    // the wave index in a scalar register: every per-wave base (lists,
+    // thresholds, sort buffers) stays scalar instead of taking VGPRs
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63, l32 = lane & 31, h = lane >> 5;
     const int wr = wave % WR, wq = wave / WR;
 
     int64_t split, qblk;
