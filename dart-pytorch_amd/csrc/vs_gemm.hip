@@ -460,7 +460,7 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
         const int q = b_row / PB, pl = b_row % PB;
         b_soff = (pl * BQ + q) * KP + piece(b_c, q) * 8;
     }
-    auto load_piece = [&](int p, int64_t trow, int kc) __attribute__((always_inline)) {
+    auto load_piece = [&](int p, int64_t trow, int kc, bool norms = true) __attribute__((always_inline)) {
         if (p < S::A_LOADS) {
             // the last tile reads at most BR rows past the end, inside the
             // allocation's slack rows; the resource stops there
@@ -470,7 +470,7 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
             ra[p] = __builtin_bit_cast(
                 u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
                              xrs, a_voff, p * A_STEP * (int)row_bytes + kc * KC * S::ESZ, 0));
-            if (p == 0 && kc == 0 && l2 && tid < BR / 4)
+            if (p == 0 && kc == 0 && l2 && norms && tid < BR / 4)
                 rn = *(const f32x4_t *)(a.xn + trow + 4 * tid);
         } else {
             const int j = p - S::A_LOADS;
@@ -513,8 +513,9 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
     // writes overlap the matrix pipe instead of following it.  first_c: 0 a
     // later chunk; 1 a tile's first chunk, whose first K-step takes the row
     // norms (L2) or zero (IP) as its C operand; 2 a tile's first chunk of an
-    // inner-product scan (zero C operand, no metric test inside).
-    auto compute = [&](const char *stage, auto first_c, char *nstage) __attribute__((always_inline)) {
+    // inner-product scan (zero C operand, no metric test inside).  ld(p)
+    // issues the next chunk's load p.
+    auto compute = [&](const char *stage, auto first_c, char *nstage, auto ld) __attribute__((always_inline)) {
         constexpr int FM = decltype(first_c)::value;
         constexpr bool FIRST = FM != 0;
         constexpr bool IL = kInterleaveStores;
@@ -534,9 +535,18 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
             // pair kPipeDist ahead, and at a K-step's first row block the next
             // K-step's query fragments, are read before this pair's MFMAs, so
             // the matrix pipe waits on no fragment read issued just before it.
+            // The next chunk's global loads follow the MFMAs of K-step 0's
+            // pairs, and its LDS writes (into the stage last read before the
+            // previous barrier) the MFMAs of the pairs of the last SK K-steps,
+            // spread evenly: no pair carries a burst of memory instructions,
+            // and the loads have most of the chunk to arrive.
             constexpr int NKS = KC / 16, NI = NKS * RB;
             constexpr int NST = S::A_LOADS + S::B_LOADS;
             constexpr int PD = kPipeDist;
+            constexpr int SK = MODE == 1 ? 3 : 2;  // (measured best per mode)
+            constexpr int SP = SK * RB < NI ? SK * RB : NI;  // pairs that carry the writes
+            auto ld_lo = [](int rb) __attribute__((always_inline)) { return rb * NLD / RB; };
+            auto st_lo = [](int j) __attribute__((always_inline)) { return j * NST / SP; };
             bf16x8_t af[PD + 1], bq[2][QB];
             auto rd_a = [&](int i) __attribute__((always_inline)) {
                 return __builtin_bit_cast(
@@ -562,12 +572,20 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
                 for (int qb = 0; qb < QB; ++qb)
                     acc[qb][rb] = mfma32_bf16(af[i % (PD + 1)], bq[ks & 1][qb],
                                               FM == 2 && ks == 0 ? f32x16_t{} : acc[qb][rb]);
-            }
+                if (ks == 0) {
 #pragma unroll
-            for (int p = 0; p < NLD; ++p) store_piece(p, nstage, -1);
-            // the order: the first reads, then per pair its look-ahead reads
-            // and its MFMAs, in the last K-step one store of the next stage
-            // after each pair's MFMAs, the remaining stores last
+                    for (int p = ld_lo(rb); p < ld_lo(rb + 1); ++p) ld(p);
+                }
+                // (the writes stay in program order after the fragment reads
+                // before them: the compiler cannot tell the two stages apart)
+                if (i >= NI - SP) {
+#pragma unroll
+                    for (int p = st_lo(i - (NI - SP)); p < st_lo(i - (NI - SP) + 1); ++p)
+                        store_piece(p, nstage, -1);
+                }
+            }
+            // the order: the first reads, then per pair its look-ahead reads,
+            // its MFMAs, its loads (K-step 0) and its writes (last SK K-steps)
             __builtin_amdgcn_sched_group_barrier(0x100, QB + PD, 0);
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
@@ -575,11 +593,21 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
                 if (i + PD < NI) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
                 if (rb == 0 && ks + 1 < NKS) __builtin_amdgcn_sched_group_barrier(0x100, QB, 0);
                 __builtin_amdgcn_sched_group_barrier(0x008, QB, 0);
-                if (ks == NKS - 1 && rb < NST) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+                if (ks == 0) {
+#pragma unroll
+                    for (int p = ld_lo(rb); p < ld_lo(rb + 1); ++p)
+                        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                }
+                if (i >= NI - SP) {
+#pragma unroll
+                    for (int p = st_lo(i - (NI - SP)); p < st_lo(i - (NI - SP) + 1); ++p)
+                        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+                }
             }
-            if (NST > RB) __builtin_amdgcn_sched_group_barrier(0x200, NST > RB ? NST - RB : 0, 0);
             return;
         }
+#pragma unroll
+        for (int p = 0; p < NLD; ++p) ld(p);
 #pragma unroll
         for (int ks = 0; ks < KC / 16; ++ks) {
             // the last K-step and the stores form a scheduling region of
@@ -665,10 +693,12 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
             const bool more = !(last_chunk && last_tile);
             const int kc_next = last_chunk ? 0 : kc + 1;
             const int64_t t_next = last_chunk ? t0 + BR : t0;
-            if (more) {
-#pragma unroll
-                for (int p = 0; p < NLD; ++p) load_piece(p, t_next, kc_next);
-            }
+            // the next chunk's loads, issued inside compute: unconditionally
+            // (past the last tile they read slack rows), the norms only when a
+            // next tile follows
+            auto ld = [&](int p) __attribute__((always_inline)) {
+                load_piece(p, t_next, kc_next, more);
+            };
             if (kc == 0) {
                 if constexpr (MODE == 0) {
 #pragma unroll
@@ -677,11 +707,11 @@ __global__ __launch_bounds__(64 * WR * WQ) void gemm_scan_kernel(ScanKArgs a) {
                                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
                 if (l2)
-                    compute(cur, std::integral_constant<int, 1>{}, nxt);
+                    compute(cur, std::integral_constant<int, 1>{}, nxt, ld);
                 else
-                    compute(cur, std::integral_constant<int, 2>{}, nxt);
+                    compute(cur, std::integral_constant<int, 2>{}, nxt, ld);
             } else {
-                compute(cur, std::integral_constant<int, 0>{}, nxt);
+                compute(cur, std::integral_constant<int, 0>{}, nxt, ld);
             }
             // (with interleaved stores, the last chunk stores stale registers
             // into the free stage, which nothing reads afterwards)
