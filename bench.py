@@ -73,10 +73,10 @@ MEASURED_TRAFFIC = {
     ("c2", 1_000_000, 10_000, 100): (1.194e9, "profiles/scan_c2_1Mx128_k100.md"),
     ("c3", 20_000_000, 1, 10): (30.73e9, "profiles/scan_c3_20Mx768_b1_b64.md"),
     ("c3", 20_000_000, 64, 10): (30.78e9, "profiles/scan_c3_20Mx768_b1_b64.md"),
-    ("c3", 20_000_000, 1024, 10): (32.76e9, "profiles/gemm_c3_20Mx768_b1024_b8192.md"),
-    ("c3", 20_000_000, 8192, 10): (548.9e9, "profiles/gemm_c3_20Mx768_b1024_b8192.md"),
+    ("c3", 20_000_000, 1024, 10): (31.94e9, "profiles/gemm_c3_20Mx768_b1024_b8192.md"),
+    ("c3", 20_000_000, 8192, 10): (325.3e9, "profiles/gemm_c3_20Mx768_b1024_b8192.md"),
     ("c4", 2_000_000, 4096, 256): (2.38e9, "profiles/kmeans_c4_2Mx256.md"),
-    ("c5", 500_000, 500_000, 512): (281.65e9, "profiles/selfjoin_c5_500kx512.md"),
+    ("c5", 500_000, 500_000, 512): (278.25e9, "profiles/selfjoin_c5_500kx512.md"),
 }
 
 
