@@ -824,10 +824,14 @@ int scan_fits(const vs::ScanPlan &plan, const vs::PreparedQueries &pq) {
 // defer_flags (a zeroed device word) for bf16 queries: their plane count is
 // one whatever the values, so the flags go to that word, to be read with the
 // results, and nothing waits here (a row with a non-finite value is prepared
-// as the unit vector e_0, so that the search runs on finite values).
+// as the unit vector e_0, so that the search runs on finite values).  With
+// spec_one_plane, fp32 queries take the same path with one plane on trust
+// (both planes are written): the caller reads the flags with its results and
+// searches again with two planes if any query was not bf16-exact.
 int prepare_queries(vs_index *x, Arena &A, const void *q_dev, int q_dtype, int64_t stride,
                     int64_t nq, vs::PreparedQueries *pq, uint32_t *flags_out, DevBuf &qp,
-                    DevBuf &qf, DevBuf &qnorm, uint32_t *defer_flags = nullptr) {
+                    DevBuf &qf, DevBuf &qnorm, uint32_t *defer_flags = nullptr,
+                    bool spec_one_plane = false) {
     pq->nq = nq;
     pq->nq_pad = query_pad(nq);
     void *p_qp, *p_qf, *p_qn, *p_fl;
@@ -837,7 +841,7 @@ int prepare_queries(vs_index *x, Arena &A, const void *q_dev, int q_dtype, int64
     pq->qp = (uint16_t *)p_qp;
     pq->qf = (float *)p_qf;
     pq->qnorm = (float *)p_qn;
-    if (defer_flags && q_dtype == VS_DTYPE_BF16) {
+    if (defer_flags && (q_dtype == VS_DTYPE_BF16 || spec_one_plane)) {
         VS_HIP(vs::launch_prepare_queries(q_dev, q_dtype, stride, nq, x->d, x->ld, x->metric, *pq,
                                           defer_flags, x->st),
                "preparing queries");
@@ -861,9 +865,9 @@ int prepare_queries(vs_index *x, Arena &A, const void *q_dev, int q_dtype, int64
 
 int prepare_queries(vs_index *x, Arena &A, const void *q_dev, int q_dtype, int64_t stride,
                     int64_t nq, vs::PreparedQueries *pq, uint32_t *flags_out,
-                    uint32_t *defer_flags = nullptr) {
+                    uint32_t *defer_flags = nullptr, bool spec_one_plane = false) {
     return prepare_queries(x, A, q_dev, q_dtype, stride, nq, pq, flags_out, x->qp, x->qf,
-                           x->qnorm, defer_flags);
+                           x->qnorm, defer_flags, spec_one_plane);
 }
 
 __global__ void fill_sentinels_kernel(float *D, int32_t *I, int64_t m, float v) {
@@ -1208,8 +1212,13 @@ int search_device(vs_index *x, Arena &A, const void *q_dev, int q_dtype, int64_t
     int32_t *ctl = (int32_t *)p_ctl;
     VS_HIP(vs::launch_fill32(ctl, 4, 0u, x->st), "control words");
     vs::PreparedQueries pq;
+    // fp32 queries on bf16 rows: one query plane on trust (nothing waits for
+    // the query flags, which are read with the results); the rare batch with
+    // a query that bf16 does not hold is searched again with two planes (not
+    // in a fixed arena, whose scratch holds one search)
+    const bool spec = kk <= 512 && q_dtype != VS_DTYPE_BF16 && x->storage == 1 && !A.fixed();
     int rc = prepare_queries(x, A, q_dev, q_dtype, x->d, nq, &pq, nullptr,
-                             kk <= 512 ? (uint32_t *)(ctl + 3) : nullptr);
+                             kk <= 512 ? (uint32_t *)(ctl + 3) : nullptr, spec);
     if (rc) return rc;
     if (kk > 512) {  // beyond the fused selection: the sorting path
         rc = exact_search(x, A, pq.qf, nq, k, D, I);
@@ -1217,82 +1226,90 @@ int search_device(vs_index *x, Arena &A, const void *q_dev, int q_dtype, int64_t
         VS_HIP(hipStreamSynchronize(x->st), "search");
         return VS_OK;
     }
-    vs::ScanPlan plan;
-    rc = plan_scan(x, nq, x->ntotal, pq.planes, kk, x->storage, &plan, safe, 0, false, 8,
-                   list_budget);
-    if (rc) return rc;
-    if ((rc = scan_fits(plan, pq))) return rc;
-    const bool verify = plan.kk < plan.kk_final;
-    const bool guess = !safe && needs_guess(x, plan, nq);
-    const bool seed = !guess && !safe && needs_seed(x, plan) && x->opt.prepass;
-    const int64_t seed_S =
-        std::max<int64_t>((int64_t)1 << x->opt.prepass_log2, x->ntotal / kPrepassDiv);
-    // candidate lists for the scan and its pre-passes
-    size_t elems = list_elems(plan), lists = list_count(plan);
-    const int gdl = guess_div_log2(x);
-    if (guess) rc = guess_thresholds(x, pq, kk, gdl, nullptr, nullptr, &elems, &lists);
-    else if (seed) rc = seed_thresholds(x, pq, seed_S, kk, nullptr, nullptr, &elems, &lists, 0, -1, list_budget);
-    if (rc) return rc;
-    ListBufs L;
-    VS_TAKE(take_lists(x, A, elems, lists, &L));
-    void *p_gthr, *p_lb = nullptr, *p_vf, *p_vx;
-    VS_TAKE(A.get(x->gthr, (size_t)pq.nq_pad * 4, &p_gthr, "shared thresholds"));
-    if (verify) VS_TAKE(A.get(x->lbound, list_count(plan) * 4, &p_lb, "list bounds"));
-    VS_TAKE(A.get(x->vf, (size_t)(nq + 1) * 4, &p_vf, "verification list"));
-    VS_TAKE(A.get(x->vx, (size_t)(nq + 1) * 4, &p_vx, "exactness list"));
-    uint32_t *gthr = (uint32_t *)p_gthr;
-    VS_HIP(vs::launch_fill32(gthr, pq.nq_pad, vs::kGthrInit, x->st), "shared thresholds");
-    // Small batches over many rows make many short lists, each warming up on
-    // its own (every list must fill kk entries before its threshold means
-    // anything).  Seeding the shared thresholds from samples first (see
-    // seed_thresholds) lets the full scan start tight; large batches start
-    // from an estimate (guess_thresholds).
-    size_t e0 = 0, l0 = 0;
-    if (guess) rc = guess_thresholds(x, pq, kk, gdl, gthr, &L, &e0, &l0);
-    else if (seed) rc = seed_thresholds(x, pq, seed_S, kk, gthr, &L, &e0, &l0, 0, -1, list_budget);
-    if (rc) return rc;
-    if (!x->prof_fixed) note_scan_kind(x, plan);
-    VS_HIP(vs::launch_fill32(L.cnt + list_count(plan), 1, 0u, x->st), "list counts");
-    {
-        ProfScope ps(x, "scan");
-        VS_HIP(vs::launch_scan_topk(x->xb, x->storage, x->ld, x->xn, x->ntotal, x->metric, pq, plan,
-                                    L.v, L.i, gthr, (float *)p_lb, L.cnt, x->st),
-               "scan kernel");
+    for (int attempt = 0;; ++attempt) {
+        vs::ScanPlan plan;
+        rc = plan_scan(x, nq, x->ntotal, pq.planes, kk, x->storage, &plan, safe, 0, false, 8,
+                       list_budget);
+        if (rc) return rc;
+        if ((rc = scan_fits(plan, pq))) return rc;
+        const bool verify = plan.kk < plan.kk_final;
+        const bool guess = !safe && needs_guess(x, plan, nq);
+        const bool seed = !guess && !safe && needs_seed(x, plan) && x->opt.prepass;
+        const int64_t seed_S =
+            std::max<int64_t>((int64_t)1 << x->opt.prepass_log2, x->ntotal / kPrepassDiv);
+        // candidate lists for the scan and its pre-passes
+        size_t elems = list_elems(plan), lists = list_count(plan);
+        const int gdl = guess_div_log2(x);
+        if (guess) rc = guess_thresholds(x, pq, kk, gdl, nullptr, nullptr, &elems, &lists);
+        else if (seed) rc = seed_thresholds(x, pq, seed_S, kk, nullptr, nullptr, &elems, &lists, 0, -1, list_budget);
+        if (rc) return rc;
+        ListBufs L;
+        VS_TAKE(take_lists(x, A, elems, lists, &L));
+        void *p_gthr, *p_lb = nullptr, *p_vf, *p_vx;
+        VS_TAKE(A.get(x->gthr, (size_t)pq.nq_pad * 4, &p_gthr, "shared thresholds"));
+        if (verify) VS_TAKE(A.get(x->lbound, list_count(plan) * 4, &p_lb, "list bounds"));
+        VS_TAKE(A.get(x->vf, (size_t)(nq + 1) * 4, &p_vf, "verification list"));
+        VS_TAKE(A.get(x->vx, (size_t)(nq + 1) * 4, &p_vx, "exactness list"));
+        uint32_t *gthr = (uint32_t *)p_gthr;
+        VS_HIP(vs::launch_fill32(gthr, pq.nq_pad, vs::kGthrInit, x->st), "shared thresholds");
+        // Small batches over many rows make many short lists, each warming up on
+        // its own (every list must fill kk entries before its threshold means
+        // anything).  Seeding the shared thresholds from samples first (see
+        // seed_thresholds) lets the full scan start tight; large batches start
+        // from an estimate (guess_thresholds).
+        size_t e0 = 0, l0 = 0;
+        if (guess) rc = guess_thresholds(x, pq, kk, gdl, gthr, &L, &e0, &l0);
+        else if (seed) rc = seed_thresholds(x, pq, seed_S, kk, gthr, &L, &e0, &l0, 0, -1, list_budget);
+        if (rc) return rc;
+        if (!x->prof_fixed) note_scan_kind(x, plan);
+        VS_HIP(vs::launch_fill32(L.cnt + list_count(plan), 1, 0u, x->st), "list counts");
+        {
+            ProfScope ps(x, "scan");
+            VS_HIP(vs::launch_scan_topk(x->xb, x->storage, x->ld, x->xn, x->ntotal, x->metric, pq, plan,
+                                        L.v, L.i, gthr, (float *)p_lb, L.cnt, x->st),
+                   "scan kernel");
+        }
+        vs::TopkCheck chk;
+        VS_TAKE(xnorm_max(x, A, &chk.xmax));
+        topk_error_model(x, pq.planes, &chk);
+        chk.vx_count = ctl + 2;
+        chk.vx_list = (int32_t *)p_vx;
+        {
+            ProfScope ps(x, "merge");
+            VS_HIP(vs::launch_merge_refine(x->xb, x->storage, x->ld, x->d, x->metric, pq, plan, L.v, L.i,
+                                           gthr, (float *)p_lb, ctl + 1, (int32_t *)p_vf, k, D, I,
+                                           x->ntotal, (uint32_t *)ctl, guess ? 1 : 0, L.cnt, &chk,
+                                           x->st),
+                   "merge kernel");
+        }
+        if (!x->prof_fixed && plan.merge_g > 1) x->prof["split_merges"].launches++;
+        int32_t hc[4] = {0, 0, 0, 0};
+        VS_HIP(hipMemcpyAsync(hc, ctl, sizeof hc, hipMemcpyDeviceToHost, x->st), "merge flags");
+        VS_HIP(hipStreamSynchronize(x->st), "search");
+        if (attempt == 0 && spec && ((uint32_t)hc[3] & vs::kFlagNotBf16) &&
+            !((uint32_t)hc[3] & vs::kFlagNonFinite)) {
+            pq.planes = 2;  // (both planes were prepared)
+            VS_HIP(vs::launch_fill32(ctl, 3, 0u, x->st), "control words");
+            continue;
+        }
+        if ((uint32_t)hc[3] & vs::kFlagNonFinite)
+            return set_err(VS_ERR_NONFINITE, "queries contain NaN or infinity");
+        if ((uint32_t)hc[0] & vs::kFlagBadId)
+            return set_err(VS_ERR_HIP, "internal error: a candidate id outside the index reached the merge");
+        // queries whose shortened lists may have dropped a winner, or whose
+        // estimated threshold left fewer than kk_final candidates, are searched
+        // again with full-length lists and no estimate; queries whose selection
+        // the accumulator's error could have changed go to the exact path
+        // (both rare for unordered data)
+        // (the exact path first: the re-search prepares its queries into the
+        // index's query buffers, which both gathers read)
+        rc = research_listed(x, A, pq, (const int32_t *)p_vx, hc[2], k, D, I, 1);
+        if (rc) return rc;
+        rc = research_listed(x, A, pq, (const int32_t *)p_vf, hc[1], k, D, I, 0);
+        if (rc) return rc;
+        VS_HIP(hipStreamSynchronize(x->st), "search");
+        return VS_OK;
     }
-    vs::TopkCheck chk;
-    VS_TAKE(xnorm_max(x, A, &chk.xmax));
-    topk_error_model(x, pq.planes, &chk);
-    chk.vx_count = ctl + 2;
-    chk.vx_list = (int32_t *)p_vx;
-    {
-        ProfScope ps(x, "merge");
-        VS_HIP(vs::launch_merge_refine(x->xb, x->storage, x->ld, x->d, x->metric, pq, plan, L.v, L.i,
-                                       gthr, (float *)p_lb, ctl + 1, (int32_t *)p_vf, k, D, I,
-                                       x->ntotal, (uint32_t *)ctl, guess ? 1 : 0, L.cnt, &chk,
-                                       x->st),
-               "merge kernel");
-    }
-    if (!x->prof_fixed && plan.merge_g > 1) x->prof["split_merges"].launches++;
-    int32_t hc[4] = {0, 0, 0, 0};
-    VS_HIP(hipMemcpyAsync(hc, ctl, sizeof hc, hipMemcpyDeviceToHost, x->st), "merge flags");
-    VS_HIP(hipStreamSynchronize(x->st), "search");
-    if ((uint32_t)hc[3] & vs::kFlagNonFinite)
-        return set_err(VS_ERR_NONFINITE, "queries contain NaN or infinity");
-    if ((uint32_t)hc[0] & vs::kFlagBadId)
-        return set_err(VS_ERR_HIP, "internal error: a candidate id outside the index reached the merge");
-    // queries whose shortened lists may have dropped a winner, or whose
-    // estimated threshold left fewer than kk_final candidates, are searched
-    // again with full-length lists and no estimate; queries whose selection
-    // the accumulator's error could have changed go to the exact path
-    // (both rare for unordered data)
-    // (the exact path first: the re-search prepares its queries into the
-    // index's query buffers, which both gathers read)
-    rc = research_listed(x, A, pq, (const int32_t *)p_vx, hc[2], k, D, I, 1);
-    if (rc) return rc;
-    rc = research_listed(x, A, pq, (const int32_t *)p_vf, hc[1], k, D, I, 0);
-    if (rc) return rc;
-    VS_HIP(hipStreamSynchronize(x->st), "search");
-    return VS_OK;
 }
 
 struct RangeHits {
