@@ -165,15 +165,24 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
     constexpr int row_bytes = S::LD * S::ESZ;
     u32x4_t ra[S::LOADS];
     f32x4_t rn = {0.f, 0.f, 0.f, 0.f};
-    auto gload = [&](int64_t t) __attribute__((always_inline)) {
+    auto rows_rs = [&](int64_t t) __attribute__((always_inline)) {
         // the last tile reads at most TR rows past the end, inside the
         // allocation's slack rows; the resource stops there
         const int64_t lim = min((int64_t)INT32_MAX, (a.n - t + TR) * (int64_t)row_bytes);
-        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-            (void *)((const char *)a.xb + t * row_bytes), 0, (int)lim, kBufRsrcWord3);
-#pragma unroll
-        for (int j = 0; j < S::LOADS; ++j) ra[j] = buf_load16(rs, tid * 16, j * S::NT * 16);
+        return __builtin_amdgcn_make_buffer_rsrc((void *)((const char *)a.xb + t * row_bytes), 0,
+                                                 (int)lim, kBufRsrcWord3);
+    };
+    auto gload_piece = [&](const __amdgpu_buffer_rsrc_t &rs, int j) __attribute__((always_inline)) {
+        ra[j] = buf_load16(rs, tid * 16, j * S::NT * 16);
+    };
+    auto gload_norms = [&](int64_t t) __attribute__((always_inline)) {
         if (l2 && tid < TR / 4) rn = *(const f32x4_t *)(a.xn + t + 4 * tid);
+    };
+    auto gload = [&](int64_t t) __attribute__((always_inline)) {
+        const __amdgpu_buffer_rsrc_t rs = rows_rs(t);
+#pragma unroll
+        for (int j = 0; j < S::LOADS; ++j) gload_piece(rs, j);
+        gload_norms(t);
     };
     // (t: the staged tile's first row)
     auto lstore = [&](char *stage, int64_t t) __attribute__((always_inline)) {
@@ -254,7 +263,14 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
         const int64_t tn = t0 + TR;
         const bool more = tn < r1;
         if constexpr (!KMIN) gthr_load();
-        if (more) gload(tn);
+        // the next tile's loads: all at once for short tiles, else spread
+        // over the first half of the row blocks (two per row block), so the
+        // tile's first MFMAs do not wait behind a burst of loads (C2 scan
+        // 2.25 -> 2.22 ms); they are written to LDS at the tile's end
+        constexpr bool SPL = RT >= 4;
+        const __amdgpu_buffer_rsrc_t rs_n = rows_rs(tn);
+        if (!SPL && more) gload(tn);
+        if (SPL && more) gload_norms(tn);
         const uint16_t *As = (const uint16_t *)(smem + par * S::STAGE_BYTES);
         const float *Ns = (const float *)(As + TR * KP);
         const uint16_t *al = As + r16 * KP + 8 * g;
@@ -498,6 +514,12 @@ __global__ __launch_bounds__(256) void share_scan_kernel(ScanKArgs a) {
 #pragma unroll
         for (int rb = 0; rb < RT; ++rb) {
             const int c = rb & 1, n = c ^ 1;
+            if (SPL && more) {
+                constexpr int H = RT / 2;
+#pragma unroll
+                for (int j = 0; j < S::LOADS; ++j)
+                    if (j * H / S::LOADS == rb) gload_piece(rs_n, j);
+            }
             if (!PREF && rb + 1 < RT) frag(rb + 1, afr[n], ini[n]);
             if constexpr (TOPMODE) {
                 if (rb + 1 < RT) mma(afr[n], ini[n], accs[n]);
