@@ -70,7 +70,7 @@ CPU_SHARE = 16  # host cores of one GPU's share on the measurement boxes
 # (workload, n, nq, k).  The command and readings are in the named profile;
 # configurations without a measurement report traffic null.
 MEASURED_TRAFFIC = {
-    ("c2", 1_000_000, 10_000, 100): (1.194e9, "profiles/scan_c2_1Mx128_k100.md"),
+    ("c2", 1_000_000, 10_000, 100): (1.199e9, "profiles/scan_c2_1Mx128_k100.md"),
     ("c3", 20_000_000, 1, 10): (30.73e9, "profiles/scan_c3_20Mx768_b1_b64.md"),
     ("c3", 20_000_000, 64, 10): (30.78e9, "profiles/scan_c3_20Mx768_b1_b64.md"),
     ("c3", 20_000_000, 1024, 10): (31.94e9, "profiles/gemm_c3_20Mx768_b1024_b8192.md"),
