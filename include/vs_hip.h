@@ -137,8 +137,9 @@ VS_API int vs_index_load_flat_buffer(int device, const void *buf, int64_t len, i
 VS_API int vs_index_search(vs_index *idx, const void *q, int q_dtype, int64_t nq, int64_t k,
                            float *D, int32_t *I);
 /* Same with q, D and I in device memory (inputs resident in HBM).  On
- * VS_ERR_NONFINITE from bf16 queries, D and I hold unspecified values (their
- * flags are read with the results). */
+ * VS_ERR_NONFINITE from bf16 queries, or from fp32 queries on an index of
+ * bf16 rows, D and I hold unspecified values (their flags are read with the
+ * results). */
 VS_API int vs_index_search_device(vs_index *idx, const void *q_dev, int q_dtype, int64_t nq,
                                   int64_t k, float *D_dev, int32_t *I_dev);
 
